@@ -1,0 +1,127 @@
+/*
+ * sva_hip.h -- C ABI of the MI355X (gfx950) SVA summon -> verify decode path.
+ *
+ * The reference (asystemoffields/sva) is pure Python on PyTorch and has no FFI;
+ * each entry point below replaces the torch ops of one stage of its decode
+ * path, cited as file:line.  A ctypes binding (sva_amd/_lib.py) is the host
+ * side; INTEGRATION.md shows how a reference-side caller would bind it.
+ *
+ * Conventions
+ *  - Pointers are device pointers unless stated.  Nothing here allocates,
+ *    frees or synchronizes; work is enqueued on `stream` (a hipStream_t).
+ *  - Returns sva_status; on failure sva_last_error() (thread-local) explains.
+ *  - Query items: item = (seq * H + head) * Q + token.  Per-item buffers are
+ *    laid out [n_seq, H, Q, ...] row-major.
+ *  - Key rows: key n of sequence b lives at row seq_offsets[b] + n of the
+ *    packed cache.  seq_offsets / seq_lens are device int64 arrays of length
+ *    n_seq, or both NULL for one sequence of n_keys keys at row 0.
+ *  - Element (h, row, x) of a per-head catalog lives at h * head_stride +
+ *    row * row_stride + x (strides in elements).
+ *  - Selection rule: top-k by (score desc, key index asc).
+ */
+#ifndef SVA_HIP_H
+#define SVA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  SVA_OK = 0,
+  SVA_ERR_INVALID_ARGUMENT = 1,
+  SVA_ERR_HIP = 2,
+  SVA_ERR_UNSUPPORTED = 3
+} sva_status;
+
+typedef enum { SVA_DTYPE_F32 = 0, SVA_DTYPE_BF16 = 1, SVA_DTYPE_F16 = 2 } sva_dtype;
+typedef enum { SVA_CODE_U8 = 0, SVA_CODE_I16 = 1, SVA_CODE_I32 = 2, SVA_CODE_I64 = 3 } sva_code_type;
+typedef enum {
+  SVA_MASK_NONE = 0, /* causal rule: key n allowed for token t iff n <= len - Q + t */
+  SVA_MASK_F32 = 1,  /* additive mask: allowed iff mask > -1e4                     */
+  SVA_MASK_BF16 = 2,
+  SVA_MASK_F16 = 3,
+  SVA_MASK_BOOL = 4 /* bool mask: the reference's `mask > -1e4` allows every key */
+} sva_mask_type;
+
+/* Message for the last failed call on this thread ("" if none). */
+const char *sva_last_error(void);
+/* ABI version of this library. */
+int sva_abi_version(void);
+
+/*
+ * Learned query map and per-query PQ lookup table.
+ * Replaces sva/llama.py:211 (q_low = einsum(q, q_proj) * scale) and the table
+ * of sva/ops.py:66-68.
+ *   q        (b, h, t, d) at b*q_seq_stride + h*q_head_stride + t*q_tok_stride + d
+ *   q_proj   [H, D, R] fp32, scale [H] fp32, codebooks [H, S, C, R/S] fp32
+ *   q_low    [n_seq, H, Q, R] fp32 out
+ *   lut      [n_seq, H, Q, S, C] fp32 out (unscaled dot products)
+ *   score_range [n_seq, H, Q, 2] fp32 out: bounds of any scan score.
+ */
+int sva_query_lut(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride, int64_t q_tok_stride,
+                  int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R, int64_t S, int64_t C,
+                  const float *q_proj, const float *scale, const float *codebooks, float *q_low, float *lut,
+                  float *score_range, void *stream);
+
+/*
+ * PQ scan scores for every key (sva/ops.py:50-71, product_quantized_scores):
+ * scores[item, n] = (((0 + T0[c0]) + T1[c1]) + ...) / sqrt(R).
+ *   codes    (h, row, s) at h*code_head_stride + row*S + s
+ *   scores   [n_seq, H, Q, n_keys] fp32 out (entries past a sequence's length untouched)
+ */
+int sva_pq_scores(const float *lut, const void *codes, int code_type, int64_t code_head_stride,
+                  const int64_t *seq_offsets, const int64_t *seq_lens, int64_t n_seq, int64_t H, int64_t Q,
+                  int64_t n_keys, int64_t R, int64_t S, int64_t C, float *scores, void *stream);
+
+/*
+ * Summon: PQ scan + shortlist select + exact low-rank rescore.
+ * Replaces sva/llama.py:270-292 (product_quantized_scores, masked topk(L),
+ * candidate_counts, gather of k_low and the rank-score sum).
+ *   k_low    (h, row, r) at h*k_low_head_stride + row*R + r, fp32
+ *   mask     (t, n) at t*mask_tok_stride + n (single sequence only), or NULL
+ *   sl_idx   [items, L] key indices of the shortlist (first sl_count[item] valid)
+ *   sl_rank  [items, L] their rank scores sum(k_low * q_low) / sqrt(R)
+ *   sl_count [items] = min(L, #allowed keys)
+ * workspace: sva_summon_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+size_t sva_summon_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);
+int sva_summon(const float *lut, const float *score_range, const float *q_low, const void *codes, int code_type,
+               int64_t code_head_stride, const float *k_low, int64_t k_low_head_stride, const int64_t *seq_offsets,
+               const int64_t *seq_lens, int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S,
+               int64_t C, int64_t L, const void *mask, int mask_type, int64_t mask_tok_stride, int32_t *sl_idx,
+               float *sl_rank, int32_t *sl_count, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Budget select: top-B of each shortlist by (rank desc, key index asc).
+ * Replaces sva/llama.py:293-302 (masked topk(B), gather, verified counts).
+ *   fin_idx [items, B] chosen key indices sorted ascending; fin_count[item] = min(B, sl_count[item]).
+ */
+int sva_budget_select(const int32_t *sl_idx, const float *sl_rank, const int32_t *sl_count, int64_t n_items,
+                      int64_t L, int64_t B, int32_t *fin_idx, int32_t *fin_count, void *stream);
+
+/*
+ * Exact verifier, GQA-aware: for each KV head g and token, the union of the
+ * budget lists of its H/G query heads is read once; each row is scored
+ * against every query head that selected it (fp32, times `scaling`), then a
+ * softmax and the weighted V sum per head.
+ * Replaces sva/llama.py:304-317 (scan path) and :532-553 (static path).
+ *   keys/values (g, row, d) at g*kv_head_stride + row*kv_row_stride + d
+ *   fin_idx [items, B] sorted ascending, fin_count [items]; indices are
+ *   clamped into [0, len) of their sequence so every read stays in bounds
+ *   out (b, h, t, d) at b*out_seq_stride + h*out_head_stride + t*out_tok_stride + d
+ */
+int sva_verify(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride, int64_t q_tok_stride,
+               const void *keys, const void *values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+               const int64_t *seq_offsets, const int64_t *seq_lens, int64_t n_keys, const int32_t *fin_idx,
+               const int32_t *fin_count, int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B,
+               float scaling, void *out, int out_dtype, int64_t out_seq_stride, int64_t out_head_stride,
+               int64_t out_tok_stride, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVA_HIP_H */

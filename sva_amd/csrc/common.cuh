@@ -1,0 +1,327 @@
+// Device-side building blocks shared by the SVA decode-path kernels (gfx950).
+//
+// Conventions
+//  * Wavefront = 64 lanes.  Block sizes are multiples of 64.
+//  * Scores are ranked through an order-preserving uint32 key (f2key); key 0 is
+//    reserved for "not allowed" (no finite float maps to it).
+//  * A ranked element is (key, key index); ties on key break toward the LOWER
+//    key index.  The 64-bit composite (key << 32) | (0xFFFFFFFF - index) is
+//    unique per key index and orders exactly like that rule.
+//  * Every fp32 reduction whose bits matter is written with an explicit order
+//    and with FP contraction disabled in its scope.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define SVA_DEV __device__ __forceinline__
+
+namespace sva {
+
+enum DType : int { F32 = 0, BF16 = 1, F16 = 2 };
+enum CodeType : int { CODE_U8 = 0, CODE_I16 = 1, CODE_I32 = 2, CODE_I64 = 3 };
+
+constexpr int WAVE = 64;
+
+SVA_DEV uint32_t f2key(float x) {
+  x = x + 0.0f;  // folds -0 onto +0 (not contracted or folded without nsz)
+  uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+SVA_DEV float key2f(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(u);
+}
+
+SVA_DEV uint64_t composite(uint32_t key, uint32_t index) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - index);
+}
+SVA_DEV uint32_t composite_index(uint64_t c) { return 0xFFFFFFFFu - (uint32_t)(c & 0xFFFFFFFFu); }
+SVA_DEV uint32_t composite_key(uint64_t c) { return (uint32_t)(c >> 32); }
+
+SVA_DEV float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == F32) return ((const float*)p)[i];
+  if (dtype == BF16) {
+    uint16_t b = ((const uint16_t*)p)[i];
+    return __uint_as_float((uint32_t)b << 16);
+  }
+  return __half2float(((const __half*)p)[i]);
+}
+
+SVA_DEV void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == F32) {
+    ((float*)p)[i] = v;
+  } else if (dtype == BF16) {
+    // round to nearest even (what torch's .to(bfloat16) does for finite values)
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7F800000u) == 0x7F800000u) {
+      ((uint16_t*)p)[i] = (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+    } else {
+      u += 0x7FFFu + ((u >> 16) & 1u);
+      ((uint16_t*)p)[i] = (uint16_t)(u >> 16);
+    }
+  } else {
+    ((__half*)p)[i] = __float2half_rn(v);
+  }
+}
+
+SVA_DEV int64_t load_code(const void* p, int64_t i, int ctype) {
+  switch (ctype) {
+    case CODE_U8: return ((const uint8_t*)p)[i];
+    case CODE_I16: return ((const int16_t*)p)[i];
+    case CODE_I32: return ((const int32_t*)p)[i];
+    default: return ((const int64_t*)p)[i];
+  }
+}
+
+SVA_DEV void store_code(void* p, int64_t i, int ctype, int64_t v) {
+  switch (ctype) {
+    case CODE_U8: ((uint8_t*)p)[i] = (uint8_t)v; break;
+    case CODE_I16: ((int16_t*)p)[i] = (int16_t)v; break;
+    case CODE_I32: ((int32_t*)p)[i] = (int32_t)v; break;
+    default: ((int64_t*)p)[i] = v; break;
+  }
+}
+
+// Additive / boolean attention-mask rule of the reference: allowed = mask > -1e4
+// evaluated in the mask's dtype (a bool mask is therefore always allowed).
+enum MaskType : int { MASK_NONE = 0, MASK_F32 = 1, MASK_BF16 = 2, MASK_F16 = 3, MASK_BOOL = 4 };
+
+SVA_DEV bool mask_allows(const void* mask, int64_t i, int mtype) {
+  switch (mtype) {
+    case MASK_F32: return ((const float*)mask)[i] > -1e4f;
+    case MASK_BF16: return __uint_as_float((uint32_t)((const uint16_t*)mask)[i] << 16) > -1e4f;
+    case MASK_F16: return __half2float(((const __half*)mask)[i]) > -1e4f;
+    default: return true;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wave / block collectives
+
+SVA_DEV int lane_id() { return (int)__lane_id(); }
+
+SVA_DEV float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+SVA_DEV float wave_max(float v) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
+  return v;
+}
+SVA_DEV uint32_t wave_sum_u32(uint32_t v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+// Inclusive scan within a wave (Hillis-Steele over 64 lanes).
+SVA_DEV uint32_t wave_incl_scan(uint32_t v) {
+  const int lane = lane_id();
+  for (int off = 1; off < WAVE; off <<= 1) {
+    uint32_t t = __shfl_up(v, off, WAVE);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// Exclusive block scan of one value per thread.  `scratch` holds >= BLOCK/64 + 1
+// uint32 in LDS.  Returns the exclusive prefix; *total gets the block sum.
+template <int BLOCK>
+SVA_DEV uint32_t block_excl_scan(uint32_t v, uint32_t* scratch, uint32_t* total) {
+  constexpr int NW = BLOCK / WAVE;
+  const int lane = lane_id();
+  const int wid = threadIdx.x / WAVE;
+  uint32_t incl = wave_incl_scan(v);
+  if (lane == WAVE - 1) scratch[wid] = incl;
+  __syncthreads();
+  if (wid == 0) {
+    uint32_t w = lane < NW ? scratch[lane] : 0u;
+    uint32_t wi = wave_incl_scan(w);
+    if (lane < NW) scratch[lane] = wi - w;
+    if (lane == NW - 1) scratch[NW] = wi;
+  }
+  __syncthreads();
+  uint32_t res = scratch[wid] + incl - v;
+  if (total) *total = scratch[NW];
+  __syncthreads();
+  return res;
+}
+
+// ---------------------------------------------------------------------------
+// Radix select over uint32 keys.  Finds the threshold key T and k_eq such that
+// the k largest elements are: every element with key > T plus the k_eq
+// lowest-index elements with key == T.  Elements with key 0 never count.
+// get(i) returns the key of element i in [0, n).  hist: 256 uint32 in LDS,
+// scratch: block_excl_scan scratch, shared: 4 uint32 in LDS.
+template <int BLOCK, typename Get>
+SVA_DEV void radix_select_u32(Get get, int n, int k, uint32_t* hist, uint32_t* scratch, uint32_t* shared,
+                              uint32_t* T_out, int* keq_out) {
+  uint32_t prefix = 0, pmask = 0;
+  int k_rem = k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += BLOCK) hist[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += BLOCK) {
+      const uint32_t key = get(i);
+      if (key != 0u && (key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    // cumulative count from the top digit down
+    uint32_t c = 0;
+    if (threadIdx.x < 256) c = hist[255 - threadIdx.x];
+    uint32_t tot;
+    uint32_t before = block_excl_scan<BLOCK>(threadIdx.x < 256 ? c : 0u, scratch, &tot);
+    if (threadIdx.x < 256 && before < (uint32_t)k_rem && before + c >= (uint32_t)k_rem) {
+      shared[0] = 255u - threadIdx.x;
+      shared[1] = before;
+    }
+    __syncthreads();
+    const uint32_t d = shared[0];
+    k_rem -= (int)shared[1];
+    prefix |= d << shift;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  *T_out = prefix;
+  *keq_out = k_rem;
+}
+
+// Radix select over uint64 composites (unique per index); returns the
+// k-th largest composite X: the selection is exactly {c >= X}.
+template <int BLOCK, typename Get>
+SVA_DEV uint64_t radix_select_u64(Get get, int n, int k, uint32_t* hist, uint32_t* scratch, uint32_t* shared) {
+  uint64_t prefix = 0, pmask = 0;
+  int k_rem = k;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int i = threadIdx.x; i < 256; i += BLOCK) hist[i] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += BLOCK) {
+      const uint64_t c = get(i);
+      if (c != 0ull && (c & pmask) == prefix) atomicAdd(&hist[(uint32_t)(c >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    uint32_t cnt = 0;
+    if (threadIdx.x < 256) cnt = hist[255 - threadIdx.x];
+    uint32_t tot;
+    uint32_t before = block_excl_scan<BLOCK>(threadIdx.x < 256 ? cnt : 0u, scratch, &tot);
+    if (threadIdx.x < 256 && before < (uint32_t)k_rem && before + cnt >= (uint32_t)k_rem) {
+      shared[0] = 255u - threadIdx.x;
+      shared[1] = before;
+    }
+    __syncthreads();
+    const uint64_t d = shared[0];
+    k_rem -= (int)shared[1];
+    prefix |= d << shift;
+    pmask |= 255ull << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// In-place bitonic sort of n (power of two) uint64 in LDS, descending if desc.
+template <int BLOCK>
+SVA_DEV void bitonic_sort_u64(uint64_t* a, int n, bool desc) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = threadIdx.x; t < n / 2; t += BLOCK) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = ((lo & size) == 0) != desc;  // ascending block?
+        const uint64_t x = a[lo], y = a[hi];
+        if ((x > y) == up) {
+          a[lo] = y;
+          a[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+SVA_DEV int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// torch.sum(dim=-1) order for a row of k <= 511 products (see the oracle):
+// 8-lane vectors, 4 interleaved accumulators, leftovers into accumulator 0,
+// accumulators folded in order, scalar tail first, then lanes in order.
+// Products are rounded separately (no FMA).
+SVA_DEV float torch_order_dot(const float* __restrict__ a, const float* __restrict__ b, int k) {
+#pragma clang fp contract(off)
+  const int nvec = k >> 3;
+  const int rows = nvec >> 2;
+  float acc[4][8];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[x][l] = 0.0f;
+  for (int i = 0; i < rows; ++i) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const int e = (i * 4 + x) * 8 + l;
+        const float p = a[e] * b[e];
+        acc[x][l] = acc[x][l] + p;
+      }
+  }
+  for (int v = rows * 4; v < nvec; ++v) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const float p = a[v * 8 + l] * b[v * 8 + l];
+      acc[0][l] = acc[0][l] + p;
+    }
+  }
+#pragma unroll
+  for (int x = 1; x < 4; ++x)
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[0][l] = acc[0][l] + acc[x][l];
+  float total = 0.0f;
+  for (int t = nvec * 8; t < k; ++t) {
+    const float p = a[t] * b[t];
+    total = total + p;
+  }
+#pragma unroll
+  for (int l = 0; l < 8; ++l) total = total + acc[0][l];
+  return total;
+}
+
+// Same order, specialised for k == 64 with the row read as 16 float4 from
+// global memory (16-byte aligned) and the other operand from LDS.
+SVA_DEV float torch_order_dot64(const float* __restrict__ row, const float* __restrict__ q) {
+#pragma clang fp contract(off)
+  float r[64];
+  const float4* r4 = reinterpret_cast<const float4*>(row);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float4 v = r4[i];
+    r[4 * i + 0] = v.x;
+    r[4 * i + 1] = v.y;
+    r[4 * i + 2] = v.z;
+    r[4 * i + 3] = v.w;
+  }
+  float part[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) {
+    float a0 = 0.0f + r[l] * q[l];
+    a0 = a0 + r[32 + l] * q[32 + l];
+    float a1 = 0.0f + r[8 + l] * q[8 + l];
+    a1 = a1 + r[40 + l] * q[40 + l];
+    float a2 = 0.0f + r[16 + l] * q[16 + l];
+    a2 = a2 + r[48 + l] * q[48 + l];
+    float a3 = 0.0f + r[24 + l] * q[24 + l];
+    a3 = a3 + r[56 + l] * q[56 + l];
+    part[l] = ((a0 + a1) + a2) + a3;
+  }
+  float total = 0.0f;
+#pragma unroll
+  for (int l = 0; l < 8; ++l) total = total + part[l];
+  return total;
+}
+
+}  // namespace sva

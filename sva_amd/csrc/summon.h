@@ -1,0 +1,48 @@
+// Parameters shared by the two summon strategies (per-item and wide).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sva {
+
+constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
+
+struct SummonParams {
+  const float* lut;    // [items, S*C]
+  const float* range;  // [items, 2] bounds of any scan score
+  const float* q_low;  // [items, R]
+  const void* codes;
+  int ctype;
+  int64_t code_hs;
+  const float* k_low;
+  int64_t klow_hs;
+  const int64_t* offs;
+  const int64_t* lens;
+  int H, Q;
+  int64_t N;  // keys of the single sequence, or the longest sequence
+  int R, S, C, L;
+  const void* mask;
+  int mask_type;
+  int64_t mask_ts;
+  float sqrt_r;
+  int32_t* sl_idx;
+  float* sl_rank;
+  int32_t* sl_count;
+};
+
+int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
+bool summon_wide_eligible(const SummonParams& p, int64_t items);
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
+size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);
+
+inline int next_pow2_host(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// Fills n int32 with a value on the stream (graph-capture safe, no memset node).
+int fill_i32(int32_t* ptr, int64_t n, int32_t value, hipStream_t stream);
+int fill_u32(uint32_t* ptr, int64_t n, uint32_t value, hipStream_t stream);
+
+}  // namespace sva

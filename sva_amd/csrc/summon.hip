@@ -1,0 +1,238 @@
+// Summon: PQ scan over the cached codes, exact shortlist selection and the
+// low-rank rescore of the shortlist (sva/llama.py:270-292, sva/ops.py:50-71).
+//
+// Item path (this file, summon_item_kernel): one workgroup per query item
+// (sequence, head, token).  The LUT sits in LDS; every allowed key's score is
+// turned into an order-preserving key; an LDS radix select finds the L-th
+// largest key T and how many keys equal to T to take (lowest key indices
+// first); a compaction in key-index order writes the shortlist; each
+// shortlisted key is rescored against q_low in torch's summation order.
+// Keys live in LDS when they fit, otherwise they are recomputed per pass.
+//
+// The long-context q=1 path (many workgroups per item) is in summon_wide.hip.
+#include "capi_internal.h"
+#include "common.cuh"
+#include "summon.h"
+
+using namespace sva;
+
+namespace {
+
+constexpr int ITEM_BLOCK = 1024;
+
+struct ItemLds {
+  // offsets (bytes) of the dynamic LDS regions
+  int tab, ql, hist, scratch, shared, slidx, keys, total;
+};
+
+__host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
+
+__host__ __device__ inline ItemLds item_lds_layout(int S, int C, int R, int L, int64_t N, bool keys_in_lds) {
+  ItemLds l;
+  int o = 0;
+  l.tab = o;
+  o = align16(o + 4 * S * C);
+  l.ql = o;
+  o = align16(o + 4 * R);
+  l.hist = o;
+  o = align16(o + 4 * 256);
+  l.scratch = o;
+  o = align16(o + 4 * (ITEM_BLOCK / WAVE + 1));
+  l.shared = o;
+  o = align16(o + 4 * 4);
+  l.slidx = o;
+  o = align16(o + 4 * L);
+  l.keys = o;
+  if (keys_in_lds) o = align16(o + (int)(4 * N));
+  l.total = o;
+  return l;
+}
+
+__global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p, int keys_in_lds) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int item = blockIdx.x;
+  const int t = item % p.Q;
+  const int h = (item / p.Q) % p.H;
+  const int b = item / (p.Q * p.H);
+  const int64_t len = p.lens ? p.lens[b] : p.N;
+  const int64_t off = p.offs ? p.offs[b] : 0;
+  const ItemLds L = item_lds_layout(p.S, p.C, p.R, p.L, len, keys_in_lds != 0);
+  float* tab = (float*)(lds + L.tab);
+  float* ql = (float*)(lds + L.ql);
+  uint32_t* hist = (uint32_t*)(lds + L.hist);
+  uint32_t* scratch = (uint32_t*)(lds + L.scratch);
+  uint32_t* shared = (uint32_t*)(lds + L.shared);
+  int32_t* slidx = (int32_t*)(lds + L.slidx);
+  uint32_t* keys = (uint32_t*)(lds + L.keys);
+
+  const int SC = p.S * p.C;
+  const float* lsrc = p.lut + (int64_t)item * SC;
+  for (int e = threadIdx.x; e < SC; e += ITEM_BLOCK) tab[e] = lsrc[e];
+  const float* qsrc = p.q_low + (int64_t)item * p.R;
+  for (int r = threadIdx.x; r < p.R; r += ITEM_BLOCK) ql[r] = qsrc[r];
+  __syncthreads();
+
+  const int64_t code_base = (int64_t)h * p.code_hs + off * p.S;
+  const int64_t causal_last = len - p.Q + t;  // last allowed key without a mask
+  const char* mrow = p.mask ? (const char*)p.mask : nullptr;
+  const int S = p.S, C = p.C;
+  const float sqrt_r = p.sqrt_r;
+
+  auto compute_key = [&](int64_t n) -> uint32_t {
+    const bool allowed =
+        p.mask_type == MASK_NONE ? n <= causal_last : mask_allows(mrow, (int64_t)t * p.mask_ts + n, p.mask_type);
+    if (!allowed) return 0u;
+    float acc = 0.0f;
+    const int64_t row = code_base + n * S;
+    for (int s = 0; s < S; ++s) {
+      int64_t c = load_code(p.codes, row + s, p.ctype);
+      c = c < 0 ? 0 : (c >= C ? C - 1 : c);
+      acc = acc + tab[s * C + c];
+    }
+    return f2key(acc / sqrt_r);
+  };
+
+  uint32_t cnt = 0;
+  for (int64_t n = threadIdx.x; n < len; n += ITEM_BLOCK) {
+    const uint32_t k = compute_key(n);
+    cnt += k != 0u;
+    if (keys_in_lds) keys[n] = k;
+  }
+  uint32_t allowed_total;
+  block_excl_scan<ITEM_BLOCK>(cnt, scratch, &allowed_total);
+  const int leff = (int)min((int64_t)p.L, (int64_t)allowed_total);
+  if (leff == 0) {
+    if (threadIdx.x == 0) p.sl_count[item] = 0;
+    return;
+  }
+
+  auto get_key = [&](int64_t n) -> uint32_t { return keys_in_lds ? keys[n] : compute_key(n); };
+
+  uint32_t T;
+  int keq;
+  radix_select_u32<ITEM_BLOCK>([&](int i) { return get_key(i); }, (int)len, leff, hist, scratch, shared, &T, &keq);
+
+  // compaction in key-index order over thread-contiguous segments
+  const int64_t seg = (len + ITEM_BLOCK - 1) / ITEM_BLOCK;
+  const int64_t lo = min((int64_t)threadIdx.x * seg, len);
+  const int64_t hi = min(lo + seg, len);
+  uint32_t gt = 0, eq = 0;
+  for (int64_t n = lo; n < hi; ++n) {
+    const uint32_t k = get_key(n);
+    gt += k > T;
+    eq += k == T;
+  }
+  const uint32_t eq_before = block_excl_scan<ITEM_BLOCK>(eq, scratch, nullptr);
+  const int take_eq = max(0, min((int)eq, keq - (int)eq_before));
+  uint32_t pos = block_excl_scan<ITEM_BLOCK>(gt + (uint32_t)take_eq, scratch, nullptr);
+  int taken = 0;
+  for (int64_t n = lo; n < hi; ++n) {
+    const uint32_t k = get_key(n);
+    if (k > T) {
+      slidx[pos++] = (int32_t)n;
+    } else if (k == T && taken < take_eq) {
+      slidx[pos++] = (int32_t)n;
+      ++taken;
+    }
+  }
+  __syncthreads();
+
+  // exact low-rank rescore of the shortlist (torch's sum order)
+  const float* kl = p.k_low + (int64_t)h * p.klow_hs + off * p.R;
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
+    const int64_t n = slidx[j];
+    const float* row = kl + n * p.R;
+    const float dot = p.R == 64 ? torch_order_dot64(row, ql) : torch_order_dot(row, ql, p.R);
+    out_idx[j] = (int32_t)n;
+    out_rank[j] = dot / sqrt_r;
+  }
+  if (threadIdx.x == 0) p.sl_count[item] = leff;
+}
+
+}  // namespace
+
+namespace sva {
+
+int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream) {
+  const bool keys_fit = item_lds_layout(p.S, p.C, p.R, p.L, p.N, true).total <= kMaxLds;
+  const ItemLds layout = item_lds_layout(p.S, p.C, p.R, p.L, p.N, keys_fit);
+  SVA_UNSUPPORTED(layout.total <= kMaxLds, "sva_summon: shortlist %d with %dx%d codes exceeds LDS", p.L, p.S, p.C);
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)summon_item_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      kMaxLds),
+                  "hipFuncSetAttribute(summon_item_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(summon_item_kernel, dim3((unsigned)items), dim3(ITEM_BLOCK), (size_t)layout.total, stream, p,
+                     keys_fit ? 1 : 0);
+  SVA_CHECK_LAUNCH("summon_item_kernel");
+  return SVA_OK;
+}
+
+}  // namespace sva
+
+extern "C" size_t sva_summon_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L) {
+  return sva::summon_wide_workspace_bytes(n_seq, H, Q, n_keys, L);
+}
+
+extern "C" int sva_summon(const float* lut, const float* score_range, const float* q_low, const void* codes,
+                          int code_type, int64_t code_head_stride, const float* k_low, int64_t k_low_head_stride,
+                          const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
+                          int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
+                          int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count,
+              "sva_summon: null pointer");
+  SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "sva_summon: offsets and lengths go together");
+  SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "sva_summon: bad sizes");
+  SVA_REQUIRE(n_keys < (1ll << 31), "sva_summon: at most 2^31-1 keys per sequence");
+  SVA_REQUIRE(R > 0 && R <= 511 && S > 0 && R % S == 0 && C > 0 && S * C <= 16384,
+              "sva_summon: bad rank/PQ layout R=%lld S=%lld C=%lld", (long long)R, (long long)S, (long long)C);
+  SVA_REQUIRE(L > 0 && L <= 16384, "sva_summon: shortlist %lld out of range (1..16384)", (long long)L);
+  SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_summon: bad code type");
+  SVA_REQUIRE(mask_type >= 0 && mask_type <= 4, "sva_summon: bad mask type");
+  SVA_REQUIRE(mask_type == SVA_MASK_NONE || mask_type == SVA_MASK_BOOL || mask != nullptr,
+              "sva_summon: mask type given without a mask");
+  SVA_REQUIRE(mask_type == SVA_MASK_NONE || n_seq == 1, "sva_summon: masks apply to a single sequence");
+  SVA_REQUIRE(R != 64 || (((uintptr_t)k_low & 15u) == 0 && k_low_head_stride % 4 == 0),
+              "sva_summon: k_low must be 16-byte aligned");
+  const int64_t items = n_seq * H * Q;
+  SVA_REQUIRE(items < (1ll << 31), "sva_summon: too many query items");
+  sva::SummonParams p;
+  p.lut = lut;
+  p.range = score_range;
+  p.q_low = q_low;
+  p.codes = codes;
+  p.ctype = code_type;
+  p.code_hs = code_head_stride;
+  p.k_low = k_low;
+  p.klow_hs = k_low_head_stride;
+  p.offs = seq_offsets;
+  p.lens = seq_lens;
+  p.H = (int)H;
+  p.Q = (int)Q;
+  p.N = n_keys;
+  p.R = (int)R;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.L = (int)L;
+  p.mask = mask;
+  p.mask_type = mask_type;
+  p.mask_ts = mask_tok_stride;
+  p.sqrt_r = (float)sqrt((double)R);
+  p.sl_idx = sl_idx;
+  p.sl_rank = sl_rank;
+  p.sl_count = sl_count;
+  if (n_keys == 0) {
+    return sva::fill_i32(sl_count, items, 0, (hipStream_t)stream);
+  }
+  if (sva::summon_wide_eligible(p, items)) {
+    return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream);
+  }
+  return sva::summon_item_path(p, items, (hipStream_t)stream);
+}

@@ -1,0 +1,183 @@
+"""Tensor-level wrappers of the C-ABI entry points (one function per stage).
+
+Every function takes device tensors, allocates its outputs with torch's
+caching allocator and enqueues the kernel on torch's current stream.  Shapes
+follow include/sva_hip.h: query items are [n_seq, H, Q], per-head catalogs are
+[H, rows, X] with the last dim contiguous.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import check, code_type, dtype_code, lib, ptr, require_device, stream_handle
+
+
+def _as_query(q: torch.Tensor) -> torch.Tensor:
+    if q.dim() == 3:
+        q = q.unsqueeze(0)
+    if q.dim() != 4:
+        raise ValueError(f"query must be [n_seq, H, Q, D] or [H, Q, D], got {tuple(q.shape)}")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    return q
+
+
+def _f32c(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        t = t.float().contiguous()
+    return t
+
+
+def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor):
+    """q_low [n_seq,H,Q,R], lut [n_seq,H,Q,S,C], score_range [n_seq,H,Q,2] (sva/llama.py:211, sva/ops.py:66-68)."""
+
+    q = _as_query(q)
+    q_proj, scale, codebooks = _f32c(q_proj), _f32c(scale), _f32c(codebooks)
+    device = require_device(q, q_proj, scale, codebooks)
+    n_seq, heads, q_len, head_dim = q.shape
+    rank = q_proj.shape[-1]
+    subspaces, codewords = codebooks.shape[1], codebooks.shape[2]
+    if tuple(q_proj.shape) != (heads, head_dim, rank):
+        raise ValueError(f"q_proj shape {tuple(q_proj.shape)} != {(heads, head_dim, rank)}")
+    q_low = torch.empty(n_seq, heads, q_len, rank, device=device, dtype=torch.float32)
+    lut = torch.empty(n_seq, heads, q_len, subspaces, codewords, device=device, dtype=torch.float32)
+    rng = torch.empty(n_seq, heads, q_len, 2, device=device, dtype=torch.float32)
+    check(
+        lib().sva_query_lut(
+            ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), n_seq, heads, q_len, head_dim, rank,
+            subspaces, codewords, ptr(q_proj), ptr(scale), ptr(codebooks), ptr(q_low), ptr(lut), ptr(rng),
+            stream_handle(device),
+        ),
+        "sva_query_lut",
+    )
+    return q_low, lut, rng
+
+
+def _check_catalog(name: str, t: torch.Tensor, heads: int, width: int) -> None:
+    if t.dim() != 3 or t.shape[0] != heads or t.shape[2] != width or t.stride(2) != 1 or t.stride(1) != width:
+        raise ValueError(f"{name} must be [H={heads}, rows, {width}] with contiguous rows, got {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+
+
+def pq_scores(lut: torch.Tensor, codes: torch.Tensor, n_keys: int, rank: int,
+              seq_offsets: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None) -> torch.Tensor:
+    """All scan scores [n_seq, H, Q, n_keys] (sva/ops.py:50-71)."""
+
+    n_seq, heads, q_len, subspaces, codewords = lut.shape
+    _check_catalog("codes", codes, heads, subspaces)
+    device = require_device(lut, codes, seq_offsets, seq_lens)
+    scores = torch.empty(n_seq, heads, q_len, n_keys, device=device, dtype=torch.float32)
+    check(
+        lib().sva_pq_scores(
+            ptr(lut), ptr(codes), code_type(codes), codes.stride(0), ptr(seq_offsets), ptr(seq_lens), n_seq, heads,
+            q_len, n_keys, rank, subspaces, codewords, ptr(scores), stream_handle(device),
+        ),
+        "sva_pq_scores",
+    )
+    return scores
+
+
+def mask_args(mask: torch.Tensor | None, q_len: int, n_keys: int):
+    """(tensor, mask type, token stride) for an HF attention mask [..., Q, >=N]."""
+
+    if mask is None:
+        return None, 0, 0
+    m = mask.reshape(-1, *mask.shape[-2:])[0][:q_len, :n_keys]
+    if m.dtype not in _lib.MASK_TYPES:
+        m = m.float()
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    return m, _lib.MASK_TYPES[m.dtype], m.stride(0)
+
+
+def summon(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist: int, mask: torch.Tensor | None = None,
+           seq_offsets: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None):
+    """Shortlist (idx, rank score, count) per query item (sva/llama.py:270-292)."""
+
+    n_seq, heads, q_len, subspaces, codewords = lut.shape
+    rank = q_low.shape[-1]
+    _check_catalog("codes", codes, heads, subspaces)
+    _check_catalog("k_low", k_low, heads, rank)
+    device = require_device(lut, score_range, q_low, codes, k_low, seq_offsets, seq_lens, mask)
+    items = n_seq * heads * q_len
+    sl_idx = torch.empty(items, shortlist, device=device, dtype=torch.int32)
+    sl_rank = torch.empty(items, shortlist, device=device, dtype=torch.float32)
+    sl_count = torch.empty(items, device=device, dtype=torch.int32)
+    m, mtype, mstride = mask_args(mask, q_len, n_keys)
+    ws_bytes = int(lib().sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
+    ws = torch.empty(max(ws_bytes, 256), device=device, dtype=torch.uint8)
+    check(
+        lib().sva_summon(
+            ptr(lut), ptr(score_range), ptr(q_low), ptr(codes), code_type(codes), codes.stride(0), ptr(k_low),
+            k_low.stride(0), ptr(seq_offsets), ptr(seq_lens), n_seq, heads, q_len, n_keys, rank, subspaces,
+            codewords, shortlist, ptr(m), mtype, mstride, ptr(sl_idx), ptr(sl_rank), ptr(sl_count), ptr(ws),
+            ws.numel(), stream_handle(device),
+        ),
+        "sva_summon",
+    )
+    return sl_idx, sl_rank, sl_count
+
+
+def budget_select(sl_idx: torch.Tensor, sl_rank: torch.Tensor, sl_count: torch.Tensor, budget: int):
+    """Budget lists (ascending key indices) and counts (sva/llama.py:293-302)."""
+
+    items, shortlist = sl_idx.shape
+    device = require_device(sl_idx, sl_rank, sl_count)
+    fin_idx = torch.empty(items, budget, device=device, dtype=torch.int32)
+    fin_count = torch.empty(items, device=device, dtype=torch.int32)
+    check(
+        lib().sva_budget_select(ptr(sl_idx), ptr(sl_rank), ptr(sl_count), items, shortlist, budget, ptr(fin_idx),
+                                ptr(fin_count), stream_handle(device)),
+        "sva_budget_select",
+    )
+    return fin_idx, fin_count
+
+
+def verify(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, fin_idx: torch.Tensor,
+           fin_count: torch.Tensor, n_keys: int, scaling: float, out_dtype: torch.dtype | None = None,
+           seq_offsets: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None) -> torch.Tensor:
+    """Verified attention output [n_seq, H, Q, D] (sva/llama.py:304-317)."""
+
+    q = _as_query(q)
+    n_seq, heads, q_len, head_dim = q.shape
+    if keys.dim() != 3 or keys.stride(-1) != 1 or values.stride() != keys.stride() or keys.shape != values.shape:
+        raise ValueError("keys/values must be [G, rows, D] views with identical strides and contiguous rows")
+    if keys.dtype != values.dtype:
+        raise TypeError("keys and values must share a dtype")
+    kv_heads = keys.shape[0]
+    budget = fin_idx.shape[1]
+    device = require_device(q, keys, values, fin_idx, fin_count, seq_offsets, seq_lens)
+    out = torch.empty(n_seq, heads, q_len, head_dim, device=device, dtype=out_dtype or q.dtype)
+    check(
+        lib().sva_verify(
+            ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), ptr(keys), ptr(values), dtype_code(keys),
+            keys.stride(0), keys.stride(1), ptr(seq_offsets), ptr(seq_lens), n_keys, ptr(fin_idx), ptr(fin_count),
+            n_seq, heads, kv_heads, q_len, head_dim, budget, float(scaling), ptr(out), dtype_code(out), out.stride(0),
+            out.stride(1), out.stride(2), stream_handle(device),
+        ),
+        "sva_verify",
+    )
+    return out
+
+
+def scan_decode(q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, shortlist: int, budget: int,
+                scaling: float, mask=None, seq_offsets=None, seq_lens=None, out_dtype=None):
+    """The whole scan-mode lookup for one layer call: LUT -> summon -> budget -> verify.
+
+    shortlist/budget are the reference's actual_shortlist / actual_budget.
+    Returns (out, sl_count, fin_count)."""
+
+    q = _as_query(q)
+    q_low, lut, rng = query_lut(q, q_proj, scale, codebooks)
+    sl_idx, sl_rank, sl_count = summon(lut, rng, q_low, codes, k_low, n_keys, shortlist, mask, seq_offsets, seq_lens)
+    fin_idx, fin_count = budget_select(sl_idx, sl_rank, sl_count, budget)
+    out = verify(q, keys, values, fin_idx, fin_count, n_keys, scaling, out_dtype, seq_offsets, seq_lens)
+    return out, sl_count, fin_count
+
+
+def sqrt_rank(rank: int) -> float:
+    return math.sqrt(rank)

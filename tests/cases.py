@@ -1,0 +1,66 @@
+"""Seeded synthetic inputs shared by the tests (numpy on the host)."""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass
+class Case:
+    H: int
+    G: int
+    N: int
+    D: int
+    R: int
+    S: int
+    C: int
+    q: np.ndarray          # [H, Q, D] fp32 (values representable in the kv dtype)
+    keys: np.ndarray       # [G, N, D]
+    values: np.ndarray     # [G, N, D]
+    k_low: np.ndarray      # [H, N, R] fp32
+    q_proj: np.ndarray     # [H, D, R]
+    k_proj: np.ndarray     # [H, D, R]
+    scale: np.ndarray      # [H]
+    codebooks: np.ndarray  # [H, S, C, R/S]
+    codes: np.ndarray      # [H, N, S] uint8 / int16
+    dtype: torch.dtype
+
+    def t(self, name: str, device, dtype=None):
+        a = getattr(self, name)
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        if dtype is not None:
+            t = t.to(dtype)
+        return t.to(device)
+
+
+def round_to(a: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dtype).float().numpy()
+
+
+def make_case(H=9, G=3, N=8192, D=64, R=64, S=2, C=256, Q=1, dtype=torch.float32, seed=0,
+              code_mode="random", ties=False) -> Case:
+    """Random GQA cache.  code_mode='random' draws uniform codes; 'few' draws
+    from 3 codewords per subspace (massive exact ties)."""
+
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    q = round_to(rng.standard_normal((H, Q, D)).astype(f), dtype)
+    keys = round_to(rng.standard_normal((G, N, D)).astype(f), dtype)
+    values = round_to(rng.standard_normal((G, N, D)).astype(f), dtype)
+    k_low = rng.standard_normal((H, N, R)).astype(f)
+    q_proj = (rng.standard_normal((H, D, R)) / 8.0).astype(f)
+    k_proj = (rng.standard_normal((H, D, R)) / 8.0).astype(f)
+    scale = np.exp(rng.standard_normal(H).astype(f) * 0.1).astype(f)
+    codebooks = rng.standard_normal((H, S, C, R // S)).astype(f)
+    code_dtype = np.uint8 if C <= 256 else np.int16
+    if code_mode == "few":
+        codes = rng.integers(0, min(3, C), size=(H, N, S)).astype(code_dtype)
+    else:
+        codes = rng.integers(0, C, size=(H, N, S)).astype(code_dtype)
+    if ties:
+        # duplicate k_low rows so rank scores tie exactly
+        k_low[:, 1::2] = k_low[:, 0::2][:, : k_low[:, 1::2].shape[1]]
+    return Case(H, G, N, D, R, S, C, q, keys, values, k_low, q_proj, k_proj, scale, codebooks, codes, dtype)
