@@ -95,6 +95,15 @@ int sva_summon(const float *lut, const float *score_range, const float *q_low, c
                float *sl_rank, int32_t *sl_count, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Which summon strategy a call with these shapes takes (16-byte aligned
+ * catalogs assumed): 0 = one workgroup per query item, 1 = wide cooperative
+ * path (q = 1 over a long cache: many workgroups per item, one pass over the
+ * codes).
+ */
+int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S, int64_t C,
+                        int64_t L, int code_type, int mask_type);
+
+/*
  * Budget select: top-B of each shortlist by (rank desc, key index asc).
  * Replaces sva/llama.py:293-302 (masked topk(B), gather, verified counts).
  *   fin_idx [items, B] chosen key indices sorted ascending; fin_count[item] = min(B, sl_count[item]).

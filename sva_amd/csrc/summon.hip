@@ -175,6 +175,26 @@ int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream) {
 
 }  // namespace sva
 
+extern "C" int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S,
+                                   int64_t C, int64_t L, int code_type, int mask_type) {
+  sva::SummonParams p{};
+  alignas(16) static const float dummy[4] = {0, 0, 0, 0};
+  p.codes = dummy;
+  p.ctype = code_type;
+  p.code_hs = 0;
+  p.offs = n_seq == 1 ? nullptr : (const int64_t*)dummy;
+  p.H = (int)H;
+  p.Q = (int)Q;
+  p.N = n_keys;
+  p.R = (int)R;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.L = (int)L;
+  p.mask = dummy;
+  p.mask_type = mask_type;
+  return sva::summon_wide_eligible(p, n_seq * H * Q) ? 1 : 0;
+}
+
 extern "C" size_t sva_summon_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L) {
   return sva::summon_wide_workspace_bytes(n_seq, H, Q, n_keys, L);
 }

@@ -16,6 +16,22 @@ from . import _lib
 from ._lib import check, code_type, dtype_code, lib, ptr, require_device, stream_handle
 
 
+_workspaces: dict[torch.device, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device summon workspace.  It is zero-filled when (re)allocated and
+    the kernels return it to all-zero, so one buffer serves every call made
+    on the device's current stream (calls on concurrent streams must not
+    share it)."""
+
+    ws = _workspaces.get(device)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), device=device, dtype=torch.uint8)
+        _workspaces[device] = ws
+    return ws
+
+
 def _as_query(q: torch.Tensor) -> torch.Tensor:
     if q.dim() == 3:
         q = q.unsqueeze(0)
@@ -109,7 +125,7 @@ def summon(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist: int, m
     sl_count = torch.empty(items, device=device, dtype=torch.int32)
     m, mtype, mstride = mask_args(mask, q_len, n_keys)
     ws_bytes = int(lib().sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
-    ws = torch.empty(max(ws_bytes, 256), device=device, dtype=torch.uint8)
+    ws = workspace(device, ws_bytes)
     check(
         lib().sva_summon(
             ptr(lut), ptr(score_range), ptr(q_low), ptr(codes), code_type(codes), codes.stride(0), ptr(k_low),

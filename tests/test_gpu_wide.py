@@ -1,0 +1,118 @@
+"""GPU parity of the long-context q=1 summon (wide cooperative path).
+
+Shortlists over caches of 64K..1M keys are compared as SETS, bit-exact, with
+the oracle's top-L on the same LUT (selection rule: score desc, key index
+asc); rank scores bit-exact; the wide path must also agree with the
+one-workgroup-per-item path on the same inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(device, N, S, C, H=9, R=64, seed=0, few=False):
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    codes = rng.integers(0, 3 if few else C, size=(H, N, S), dtype=np.uint8)
+    k_low = torch.randn(H, N, R, device=device, generator=gen)
+    q = rng.standard_normal((H, 1, 64)).astype(np.float32)
+    q_proj = (rng.standard_normal((H, 64, R)) / 8).astype(np.float32)
+    scale = np.ones(H, np.float32)
+    cb = rng.standard_normal((H, S, C, R // S)).astype(np.float32)
+    return codes, k_low, q, q_proj, scale, cb
+
+
+def _summon(device, codes, k_low, q, q_proj, scale, cb, L, mask=None):
+    from sva_amd import kernels
+
+    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q).to(device), torch.from_numpy(q_proj).to(device),
+                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device))
+    codes_t = torch.from_numpy(codes).to(device)
+    sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes_t, k_low, codes.shape[1], L, mask=mask)
+    torch.cuda.synchronize()
+    return q_low[0, :, 0].cpu().numpy(), lut[0, :, 0].cpu().numpy(), sl_idx.cpu().numpy(), sl_rank.cpu().numpy(), \
+        sl_count.cpu().numpy()
+
+
+def _strategy(H, N, R, S, C, L, mask_type=0):
+    from sva_amd import _lib
+
+    return _lib.lib().sva_summon_strategy(1, H, 1, N, R, S, C, L, 0, mask_type)
+
+
+def _check(codes, k_low, q_low, lut, sl_idx, sl_rank, sl_count, L, allowed=None):
+    H, N, _ = codes.shape
+    for h in range(H):
+        scores = oracle.pq_scores_from_lut(lut[h], codes[h], 64)
+        sl = oracle.topk(scores, L, allowed=allowed)
+        cnt = int(sl_count[h])
+        assert cnt == len(sl)
+        got = sl_idx[h, :cnt].astype(np.int64)
+        assert len(np.unique(got)) == cnt, "duplicate shortlist entries"
+        assert set(got.tolist()) == set(sl.tolist()), f"head {h}: shortlist set differs"
+        rows = k_low[h, torch.from_numpy(got).to(k_low.device)].cpu().numpy()
+        ref = oracle.rank_scores(rows, np.arange(cnt), q_low[h], 64)
+        np.testing.assert_array_equal(sl_rank[h, :cnt].view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,S,C", [(65536, 4, 64), (200003, 2, 256), (1048576, 4, 64), (1048576, 1, 256)])
+def test_wide_matches_oracle(device, N, S, C):
+    assert _strategy(9, N, 64, S, C, 2048) == 1, "wide path not selected"
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=N % 97)
+    res = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)
+    _check(codes, k_low, *res, 2048)
+
+
+def test_wide_massive_ties_and_repeat(device):
+    # 3 codewords: the threshold bin holds ~1/9 of all keys; exact resolution
+    N, S, C = 120000, 2, 256
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=7, few=True)
+    first = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)
+    _check(codes, k_low, *first, 2048)
+    second = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)  # workspace reused
+    for a, b in zip(first[2:], second[2:]):
+        np.testing.assert_array_equal(np.sort(a, axis=-1) if a.ndim == 2 else a, np.sort(b, axis=-1) if b.ndim == 2 else b)
+
+
+def test_wide_tight_budget_and_mask(device):
+    N, S, C = 300000, 4, 64
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=3)
+    rng = np.random.default_rng(5)
+    mask = np.where(rng.random(N) < 0.5, np.finfo(np.float32).min, 0.0).astype(np.float32)[None, None, None, :]
+    res = _summon(device, codes, k_low, q, q_proj, scale, cb, 512, mask=torch.from_numpy(mask).to(device))
+    _check(codes, k_low, *res, 512, allowed=mask[0, 0, 0] > -1e4)
+
+
+def test_wide_agrees_with_item_path(device):
+    from sva_amd import kernels
+
+    N, S, C = 40000, 4, 64
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=11)
+    wide = _summon(device, codes, k_low, q, q_proj, scale, cb, 1024)
+    # one query item per head through the per-item path: 2 tokens (q = 2) disable the wide path
+    q2 = np.concatenate([q, q], axis=1)
+    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q2).to(device), torch.from_numpy(q_proj).to(device),
+                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device))
+    sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, torch.from_numpy(codes).to(device), k_low, N, 1024,
+                                               mask=torch.zeros(1, 1, 2, N, device=device))
+    sl_idx = sl_idx.view(9, 2, -1)[:, 0].cpu().numpy()
+    for h in range(9):
+        assert set(sl_idx[h].tolist()) == set(wide[2][h].tolist())
+
+
+def test_wide_workspace_shared_across_shapes(device):
+    # Regression: calls of different cache lengths and head counts share one
+    # workspace; the per-item histograms and counters live at fixed offsets
+    # and every call leaves them zero, whatever the tie buffers held before.
+    for N, S, C, H, few in ((150000, 2, 256, 9, True), (50000, 4, 64, 3, False), (33000, 4, 64, 9, False),
+                            (150000, 2, 256, 9, True), (40000, 4, 64, 9, False)):
+        codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=N % 13, few=few)
+        res = _summon(device, codes, k_low, q, q_proj, scale, cb, 1024)
+        _check(codes, k_low, *res, 1024)
