@@ -1,0 +1,261 @@
+"""Headline benchmark: SVA summon + verify decode lookup at 1M cached keys.
+
+Workload (one step = one decode lookup of one layer for one query token):
+  1,048,576 cached keys, 9 query heads over 3 KV heads (GQA), head_dim 64,
+  rank 64, PQ codes uint8 (default 4x64), shortlist 2048 / budget 512, q = 1.
+  K/V bf16 [3, N, 64]; k_low fp32 [9, N, 64] (the production catalog);
+  codebooks and learned maps N(0, 1) / N(0, 1/64); synthetic data, seeded.
+A step runs the four HIP stages on torch's current stream:
+  query_lut -> summon (PQ scan + exact shortlist + rescore) -> budget select
+  -> GQA verifier.
+Caches of `--layers` distinct layers are rotated so that the codes touched
+per step (>256 MB over the rotation) do not stay in the 256 MB Infinity Cache.
+
+Prints ONE JSON line (value = microseconds per query per layer, lower is
+better) with a roofline object for the dominant kernel (summon) and the CPU
+oracle timed on this host on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak (AMD spec)
+LAYOUTS = {"1x256": (1, 256), "2x256": (2, 256), "4x64": (4, 64)}
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--keys", type=int, default=1_048_576)
+    ap.add_argument("--layout", default="4x64", choices=sorted(LAYOUTS))
+    ap.add_argument("--shortlist", type=int, default=2048)
+    ap.add_argument("--budget", type=int, default=512)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layer caches rotated per step")
+    ap.add_argument("--cpu-repeats", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=17)
+    return ap.parse_args()
+
+
+class Layer:
+    """One layer's synthetic decode state resident in HBM."""
+
+    def __init__(self, torch, device, n_keys, subspaces, codewords, seed):
+        heads, kv_heads, head_dim, rank = 9, 3, 64, 64
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.q = torch.randn(1, heads, 1, head_dim, device=device, generator=g).to(torch.bfloat16)
+        self.q_proj = torch.randn(heads, head_dim, rank, device=device, generator=g) / 8.0
+        self.scale = torch.ones(heads, device=device)
+        self.codebooks = torch.randn(heads, subspaces, codewords, rank // subspaces, device=device, generator=g)
+        self.keys = torch.randn(kv_heads, n_keys, head_dim, device=device, generator=g).to(torch.bfloat16)
+        self.values = torch.randn(kv_heads, n_keys, head_dim, device=device, generator=g).to(torch.bfloat16)
+        self.k_low = torch.randn(heads, n_keys, rank, device=device, generator=g)
+        self.codes = torch.randint(0, codewords, (heads, n_keys, subspaces), device=device, generator=g,
+                                   dtype=torch.int32).to(torch.uint8)
+
+
+def algorithmic_bytes(n_keys, heads, subspaces, codewords, shortlist, budget, rank=64, head_dim=64, kv_elem=2):
+    scan = heads * n_keys * subspaces
+    lut = heads * subspaces * codewords * 4
+    rescore = heads * shortlist * rank * 4
+    verify = heads * budget * head_dim * kv_elem * 2
+    return {"scan": scan, "lut": lut, "rescore": rescore, "verify": verify,
+            "summon": scan + lut + rescore, "total": scan + lut + rescore + verify}
+
+
+def cpu_baseline(torch, layer, shortlist, budget, repeats):
+    import numpy as np
+
+    import oracle
+
+    threads = os.cpu_count() or 1
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    q = layer.q[0, :, 0].float().cpu().numpy()
+    q_low = torch.einsum("hd,hdr->hr", layer.q[0, :, 0].float(), layer.q_proj).mul_(layer.scale[:, None]).cpu().numpy()
+    keys = layer.keys.float().cpu().numpy()
+    values = layer.values.float().cpu().numpy()
+    k_low = layer.k_low.cpu().numpy()
+    cb = layer.codebooks.cpu().numpy()
+    codes = layer.codes.cpu().numpy()
+    times = []
+    used = 1
+    for i in range(repeats + 1):
+        t0 = time.perf_counter()
+        _, _, _, used = oracle.decode(q, q_low, keys, values, k_low, cb, codes, shortlist, budget, 64 ** -0.5)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+    avg_us = 1e6 * sum(times) / len(times)
+    cpu_model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    flags = ""
+    try:
+        flags = next(line for line in open("/proc/cpuinfo") if line.startswith("flags"))
+    except (OSError, StopIteration):
+        pass
+    return {
+        "value": round(avg_us, 1),
+        "unit": "us/query",
+        "cores": int(used),
+        "kind": "port",
+        "sample": f"{repeats} decode lookups (after 1 warmup) of the same 1M-key workload, all 9 heads, "
+                  f"oracle/sva_oracle.c with OpenMP over heads",
+        "p50_us": round(1e6 * float(np.percentile(times, 50)), 1),
+        "p95_us": round(1e6 * float(np.percentile(times, 95)), 1),
+        "host_threads": threads,
+        "cpu_model": cpu_model,
+        "avx512": " avx512f " in f" {flags} ",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "
+                                   "sequence (see DESIGN.md) but no multi-GPU figure is produced",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from sva_amd import _lib, kernels
+
+    device = torch.device("cuda:0")
+    subspaces, codewords = LAYOUTS[args.layout]
+    n = args.keys
+    heads, kv_heads = 9, 3
+    layers = [Layer(torch, device, n, subspaces, codewords, args.seed + n * 13 + 101 + 7919 * i)
+              for i in range(args.layers)]
+    strategy = _lib.lib().sva_summon_strategy(1, heads, 1, n, 64, subspaces, codewords, args.shortlist, 0, 0)
+    shortlist = min(args.shortlist, n)
+    budget = min(args.budget, shortlist)
+    scaling = 64 ** -0.5
+    stages = ("query_lut", "summon", "budget_select", "verify")
+
+    plan = kernels.ScanDecodePlan(device, 1, heads, 1, 64, 64, subspaces, codewords, shortlist, budget)
+    outs = [torch.empty(1, heads, 1, 64, device=device, dtype=torch.bfloat16) for _ in layers]
+
+    def step(i):
+        layer = layers[i % len(layers)]
+        plan.run(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, layer.k_low, layer.keys,
+                 layer.values, n, scaling, out=outs[i % len(layers)])
+
+    def step_staged(i, ev):
+        # the same four launches with an event between stages (per-kernel times)
+        layer = layers[i % len(layers)]
+        ev[0].record()
+        q_low, lut, rng = kernels.query_lut(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, n,
+                                            shortlist)
+        ev[1].record()
+        sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, layer.codes, layer.k_low, n, shortlist)
+        ev[2].record()
+        fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, budget)
+        ev[3].record()
+        kernels.verify(layer.q, layer.keys, layer.values, fin_idx, fin_count, n, scaling)
+        ev[4].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # timed region: exactly `steps` decode lookups, synchronized on both sides
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us_per_query = 1e6 * wall / args.steps
+
+    # per-kernel durations: HIP events on the launch stream around each stage
+    n_ev = min(args.steps, 200)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n_ev)]
+    # hold the stream in a device-side spin while the host enqueues, so the
+    # events bracket kernel execution rather than host launch gaps
+    torch.cuda._sleep(int(2e8))
+    for i in range(n_ev):
+        step_staged(i, events[i])
+    torch.cuda.synchronize()
+    per_stage = {s: 0.0 for s in stages}
+    for ev in events:
+        for j, s in enumerate(stages):
+            per_stage[s] += ev[j].elapsed_time(ev[j + 1])
+    per_stage_us = {s: round(1e3 * v / n_ev, 2) for s, v in per_stage.items()}
+    gpu_us = sum(per_stage_us.values())
+
+    bytes_ = algorithmic_bytes(n, heads, subspaces, codewords, shortlist, budget)
+    summon_us = per_stage_us["summon"]
+    achieved = bytes_["summon"] / (summon_us * 1e-6) / 1e9
+    traffic = None
+    pmc = ROOT / "profiles" / f"summon_wide_{args.layout}_1m_pmc.json"
+    if pmc.exists() and n == 1_048_576:
+        try:
+            traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    result = {
+        "metric": "us/query summon+verify at 1M keys (q=1, 2048/512)",
+        "value": round(us_per_query, 2),
+        "unit": "us/query",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_query / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 scores / u8 codes / bf16 K,V",
+        "data": "synthetic (seeded N(0,1) caches, uniform codes)",
+        "config": {
+            "workload": f"million-key cached decode lookup, one layer, q=1, {args.layout} codes",
+            "keys": n, "q_heads": heads, "kv_heads": kv_heads, "head_dim": 64, "rank": 64,
+            "shortlist": shortlist, "budget": budget, "layers_rotated": args.layers,
+            "summon_strategy": "wide" if strategy == 1 else "per-item",
+        },
+        "stage_us": per_stage_us,
+        "gpu_us_per_query": round(gpu_us, 2),
+        "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "kernel": "summon_wide_kernel" if strategy == 1 else "summon_item_kernel",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": bytes_["summon"],
+        },
+        "verify_roofline": {
+            "achieved": round(bytes_["verify"] / (per_stage_us["verify"] * 1e-6) / 1e9, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bytes_["verify"] / (per_stage_us["verify"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": bytes_["verify"],
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, layers[0], shortlist, budget, args.cpu_repeats)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

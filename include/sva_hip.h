@@ -57,14 +57,21 @@ int sva_abi_version(void);
  * of sva/ops.py:66-68.
  *   q        (b, h, t, d) at b*q_seq_stride + h*q_head_stride + t*q_tok_stride + d
  *   q_proj   [H, D, R] fp32, scale [H] fp32, codebooks [H, S, C, R/S] fp32
+ *            (both 16-byte aligned)
+ *   codes    optional (may be NULL): the cache's codes (h, row, s) at
+ *            h*code_head_stride + row*S + s, n_keys rows, used for one query
+ *            token of one sequence to sample a shortlist-threshold estimate
  *   q_low    [n_seq, H, Q, R] fp32 out
  *   lut      [n_seq, H, Q, S, C] fp32 out (unscaled dot products)
- *   score_range [n_seq, H, Q, 2] fp32 out: bounds of any scan score.
+ *   score_range [n_seq, H, Q, 4] fp32 out: lower and upper bound of any scan
+ *            sum before the 1/sqrt(R) scale, the sampled estimate (or -inf),
+ *            and 0.  Only a performance hint for sva_summon, never a result.
  */
 int sva_query_lut(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride, int64_t q_tok_stride,
                   int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R, int64_t S, int64_t C,
-                  const float *q_proj, const float *scale, const float *codebooks, float *q_low, float *lut,
-                  float *score_range, void *stream);
+                  const float *q_proj, const float *scale, const float *codebooks, const void *codes,
+                  int code_type, int64_t code_head_stride, int64_t n_keys, int64_t shortlist, float *q_low,
+                  float *lut, float *score_range, void *stream);
 
 /*
  * PQ scan scores for every key (sva/ops.py:50-71, product_quantized_scores):
@@ -113,21 +120,25 @@ int sva_budget_select(const int32_t *sl_idx, const float *sl_rank, const int32_t
 
 /*
  * Exact verifier, GQA-aware: for each KV head g and token, the union of the
- * budget lists of its H/G query heads is read once; each row is scored
- * against every query head that selected it (fp32, times `scaling`), then a
- * softmax and the weighted V sum per head.
+ * budget lists of its H/G query heads is read once (each selected K and V row
+ * is fetched by exactly one workgroup); each row is scored against every query
+ * head that selected it (fp32, times `scaling`), then a softmax and the
+ * weighted V sum per head, merged across workgroups by a second kernel.
  * Replaces sva/llama.py:304-317 (scan path) and :532-553 (static path).
  *   keys/values (g, row, d) at g*kv_head_stride + row*kv_row_stride + d
  *   fin_idx [items, B] sorted ascending, fin_count [items]; indices are
  *   clamped into [0, len) of their sequence so every read stays in bounds
  *   out (b, h, t, d) at b*out_seq_stride + h*out_head_stride + t*out_tok_stride + d
+ *   head_dim must be a multiple of 16 (<= 256).
+ * workspace: sva_verify_workspace_bytes(...) bytes (no state between calls).
  */
+size_t sva_verify_workspace_bytes(int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B);
 int sva_verify(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride, int64_t q_tok_stride,
                const void *keys, const void *values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                const int64_t *seq_offsets, const int64_t *seq_lens, int64_t n_keys, const int32_t *fin_idx,
                const int32_t *fin_count, int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B,
                float scaling, void *out, int out_dtype, int64_t out_seq_stride, int64_t out_head_stride,
-               int64_t out_tok_stride, void *stream);
+               int64_t out_tok_stride, void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

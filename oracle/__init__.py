@@ -81,7 +81,7 @@ def lib() -> ctypes.CDLL:
         _lib.sva_oracle_topk.argtypes = [c_p, c_p, c_p, i64, i64, c_p]
         _lib.sva_oracle_verify.argtypes = [c_p, c_p, c_p, i64, c_p, i64, ctypes.c_double, c_p]
         _lib.sva_oracle_decode.restype = ctypes.c_int
-        _lib.sva_oracle_decode.argtypes = [i64] * 7 + [c_p] * 8 + [ctypes.c_int, i64, i64, ctypes.c_double, c_p, c_p, c_p]
+        _lib.sva_oracle_decode.argtypes = [i64] * 7 + [c_p] * 7 + [ctypes.c_int, i64, i64, ctypes.c_double, c_p, c_p, c_p]
     return _lib
 
 

@@ -29,15 +29,17 @@ _SZ = ctypes.c_size_t
 _SIGNATURES: dict[str, tuple[type, list]] = {
     "sva_abi_version": (_I, []),
     "sva_last_error": (ctypes.c_char_p, []),
-    "sva_query_lut": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "sva_query_lut": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I,
+                           _I64, _I64, _I64, _P, _P, _P, _P]),
     "sva_pq_scores": (_I, [_P, _P, _I, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "sva_summon_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "sva_summon": (_I, [_P, _P, _P, _P, _I, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                         _P, _I, _I64, _P, _P, _P, _P, _SZ, _P]),
     "sva_summon_strategy": (_I, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I]),
     "sva_budget_select": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "sva_verify_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "sva_verify": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
-                        _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P]),
+                        _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P, _SZ, _P]),
 }
 
 

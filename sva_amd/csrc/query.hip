@@ -1,5 +1,6 @@
 // Query side of the decode path: learned query map, per-query PQ lookup
-// table, score bounds, and the all-keys PQ score kernel.
+// table, score bounds and a sampled shortlist-threshold estimate, and the
+// all-keys PQ score kernel.
 //
 // q_low[r]  = (sum_d q[d] * q_proj[h][d][r], sequential fma over d) * scale[h]
 //             (sva/llama.py:211)
@@ -8,66 +9,181 @@
 // score     = (((0 + lut[0][c0]) + lut[1][c1]) + ...) / sqrt(R)   (sva/ops.py:64-71)
 #include "capi_internal.h"
 #include "common.cuh"
+#include "summon.h"
 
 using namespace sva;
 
 namespace {
 
 constexpr int PREP_BLOCK = 256;
+constexpr int SAMPLE_BLOCKS = 16;       // contiguous sample blocks spread over the cache
+constexpr int SAMPLE_KEYS = 128;        // keys per sample block
+constexpr int SAMPLE_BINS = 1024;
+constexpr int SAMPLE_TARGET = 4;        // sampled threshold aims at ~4x the shortlist above it
+constexpr int SAMPLE_MAX_S = 8;         // sampling stages the sampled uint8 codes in LDS
 
-__global__ void __launch_bounds__(PREP_BLOCK)
-    query_lut_kernel(const void* __restrict__ q, int q_dtype, int64_t q_bs, int64_t q_hs, int64_t q_ts, int H, int Q,
-                     int D, int R, int S, int C, const float* __restrict__ q_proj, const float* __restrict__ scale,
-                     const float* __restrict__ codebooks, float sqrt_r, float* __restrict__ q_low,
-                     float* __restrict__ lut, float* __restrict__ range) {
+struct LutParams {
+  const void* q;
+  int q_dtype;
+  int64_t q_bs, q_hs, q_ts;
+  int H, Q, D, R, S, C;
+  const float* q_proj;
+  const float* scale;
+  const float* codebooks;
+  float* q_low;
+  float* lut;
+  float* range;  // [items, 4]
+  const void* codes;  // optional uint8 codes: sample for the threshold estimate
+
+  int64_t code_hs;
+  int64_t n_keys;
+  int64_t shortlist;
+};
+
+__global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
 #pragma clang fp contract(off)
-  __shared__ float qf[512];
-  __shared__ float ql[512];
-  __shared__ uint32_t kmin[64];
-  __shared__ uint32_t kmax[64];
+  extern __shared__ __align__(16) unsigned char lds[];
   const int item = blockIdx.x;
-  const int t = item % Q;
-  const int h = (item / Q) % H;
-  const int b = item / (Q * H);
-  const int64_t qbase = (int64_t)b * q_bs + (int64_t)h * q_hs + (int64_t)t * q_ts;
-  for (int d = threadIdx.x; d < D; d += PREP_BLOCK) qf[d] = load_elem(q, qbase + d, q_dtype);
+  const int t = item % p.Q;
+  const int h = (item / p.Q) % p.H;
+  const int b = item / (p.Q * p.H);
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int sub = R / S;
+  float* W = (float*)lds;              // [max(D*R, S*C)] learned map of head h, then its table
+  float* cb = W + max(D * R, S * C);   // [S][C][sub] codebooks of head h
+  float* qf = cb + S * C * sub;        // [D]
+  float* ql = qf + D;                  // [R]
+  uint32_t* kmin = (uint32_t*)(ql + R);  // [S]
+  uint32_t* kmax = kmin + S;             // [S]
+  uint32_t* shist = kmax + S;            // [SAMPLE_BINS]
+  uint32_t* misc = shist + SAMPLE_BINS;  // [4 + PREP_BLOCK/64 + 1]
+  // [SAMPLE_BLOCKS * SAMPLE_KEYS * S] sampled codes, 16-byte aligned
+  uint8_t* scodes = lds + ((((unsigned char*)(misc + 8) - lds) + 15) & ~(ptrdiff_t)15);
+
+  // stage the head's weights in LDS with wide coalesced loads
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * D * R);
+    for (int i = threadIdx.x; i < D * R / 4; i += PREP_BLOCK) reinterpret_cast<float4*>(W)[i] = w4[i];
+    const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + (int64_t)h * S * C * sub);
+    for (int i = threadIdx.x; i < S * C * sub / 4; i += PREP_BLOCK) reinterpret_cast<float4*>(cb)[i] = c4[i];
+  }
+  const int64_t qbase = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs + (int64_t)t * p.q_ts;
+  for (int d = threadIdx.x; d < D; d += PREP_BLOCK) qf[d] = load_elem(p.q, qbase + d, p.q_dtype);
   for (int s = threadIdx.x; s < S; s += PREP_BLOCK) {
     kmin[s] = 0xFFFFFFFFu;
     kmax[s] = 0u;
   }
+  for (int i = threadIdx.x; i < SAMPLE_BINS; i += PREP_BLOCK) shist[i] = 0u;
   __syncthreads();
-  const float* W = q_proj + (int64_t)h * D * R;
-  const float sc = scale[h];
+  const float sc = p.scale[h];
   for (int r = threadIdx.x; r < R; r += PREP_BLOCK) {
     float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qf[d], W[(int64_t)d * R + r], acc);
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qf[d], W[d * R + r], acc);
     const float v = acc * sc;
     ql[r] = v;
-    q_low[(int64_t)item * R + r] = v;
+    p.q_low[(int64_t)item * R + r] = v;
   }
   __syncthreads();
-  const int sub = R / S;
-  const float* cb = codebooks + (int64_t)h * S * C * sub;
+  float* lut_out = p.lut + (int64_t)item * S * C;
+  float* tab = W;  // the map is no longer needed: reuse its LDS for the table
   for (int e = threadIdx.x; e < S * C; e += PREP_BLOCK) {
     const int s = e / C;
     const float* w = cb + (int64_t)e * sub;
     const float* qs = ql + s * sub;
     float acc = 0.0f;
     for (int j = 0; j < sub; ++j) acc = __builtin_fmaf(qs[j], w[j], acc);
-    lut[(int64_t)item * S * C + e] = acc;
+    lut_out[e] = acc;
+    tab[e] = acc;
     const uint32_t k = f2key(acc);
     atomicMin(&kmin[s], k);
     atomicMax(&kmax[s], k);
   }
   __syncthreads();
+  // bounds of any sum of one table entry per subspace (before the 1/sqrt(R)
+  // scale), in the scan's summation order
   if (threadIdx.x == 0) {
     float lo = 0.0f, hi = 0.0f;
     for (int s = 0; s < S; ++s) {
       lo = lo + key2f(kmin[s]);
       hi = hi + key2f(kmax[s]);
     }
-    range[(int64_t)item * 2 + 0] = lo / sqrt_r;
-    range[(int64_t)item * 2 + 1] = hi / sqrt_r;
+    misc[0] = __float_as_uint(lo);
+    misc[1] = __float_as_uint(hi);
+  }
+  __syncthreads();
+  const float lo = __uint_as_float(misc[0]);
+  const float hi = __uint_as_float(misc[1]);
+  float t_lo = -INFINITY;
+  // sampled estimate of a sum below which the shortlist threshold almost
+  // surely lies: the k-th largest of SAMPLE_BLOCKS * SAMPLE_KEYS sampled
+  // keys with k ~ SAMPLE_TARGET * L * samples / N.  Only a performance hint:
+  // the wide summon stays exact whatever it returns.  Sample blocks start at
+  // multiples of 16 keys so that each is a run of 16-byte words.
+  const int64_t N = p.n_keys;
+  constexpr int n_sample = SAMPLE_BLOCKS * SAMPLE_KEYS;
+  if (p.codes != nullptr && N >= 4 * (int64_t)n_sample) {
+    const double want = (double)SAMPLE_TARGET * (double)p.shortlist * (double)n_sample / (double)N;
+    const int k = (int)want + 1;
+    if (k < n_sample / 2 && hi > lo) {
+      const float inv_w = (float)SAMPLE_BINS / (hi - lo);
+      const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+      const int words = SAMPLE_KEYS * S / 16;  // 16-byte words per sample block
+      if (((uintptr_t)head & 15u) == 0) {
+        for (int w = threadIdx.x; w < SAMPLE_BLOCKS * words; w += PREP_BLOCK) {
+          const int blk = w / words;
+          const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+          reinterpret_cast<uint4*>(scodes)[w] = reinterpret_cast<const uint4*>(head + n0 * S)[w % words];
+        }
+      } else {
+        for (int e = threadIdx.x; e < n_sample * S; e += PREP_BLOCK) {
+          const int blk = e / (SAMPLE_KEYS * S);
+          const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+          scodes[e] = head[n0 * S + e % (SAMPLE_KEYS * S)];
+        }
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < n_sample; i += PREP_BLOCK) {
+        float acc = 0.0f;
+        for (int s = 0; s < S; ++s) {
+          const int c = min((int)scodes[i * S + s], C - 1);
+          acc = acc + tab[s * C + c];
+        }
+        int bin = (int)((acc - lo) * inv_w);
+        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
+        atomicAdd(&shist[bin], 1u);
+      }
+      __syncthreads();
+      // thread j owns bins [SAMPLE_BINS - PER*(j+1), SAMPLE_BINS - PER*j):
+      // a suffix scan from the top finds the bin holding the k-th largest
+      constexpr int PER = SAMPLE_BINS / PREP_BLOCK;
+      const int top = SAMPLE_BINS - PER * threadIdx.x;
+      uint32_t mine = 0;
+#pragma unroll
+      for (int i = 1; i <= PER; ++i) mine += shist[top - i];
+      uint32_t total;
+      const uint32_t above = block_excl_scan<PREP_BLOCK>(mine, misc + 4, &total);
+      if (threadIdx.x == 0) misc[2] = 0u;  // bin 0 when fewer than k samples exist
+      __syncthreads();
+      if (above < (uint32_t)k && above + mine >= (uint32_t)k) {
+        uint32_t run = above;
+        for (int i = 1; i <= PER; ++i) {
+          run += shist[top - i];
+          if (run >= (uint32_t)k) {
+            misc[2] = (uint32_t)(top - i);
+            break;
+          }
+        }
+      }
+      __syncthreads();
+      t_lo = lo + (float)misc[2] / inv_w;
+    }
+  }
+  if (threadIdx.x == 0) {
+    float* rg = p.range + (int64_t)item * 4;
+    rg[0] = lo;
+    rg[1] = hi;
+    rg[2] = t_lo;
+    rg[3] = 0.0f;
   }
 }
 
@@ -99,12 +215,20 @@ __global__ void __launch_bounds__(SCORE_BLOCK)
   scores[(int64_t)item * N + n] = acc / sqrt_r;
 }
 
+size_t lut_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C, bool sample) {
+  const int64_t sub = R / S;
+  return sizeof(float) * (size_t)(std::max(D * R, S * C) + S * C * sub + D + R) +
+         sizeof(uint32_t) * (size_t)(2 * S + SAMPLE_BINS + 8) +
+         (sample ? (size_t)(SAMPLE_BLOCKS * SAMPLE_KEYS * S + 16) : 0);
+}
+
 }  // namespace
 
 extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride,
                              int64_t q_tok_stride, int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R,
                              int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
-                             float* q_low, float* lut, float* score_range, void* stream) {
+                             const void* codes, int code_type, int64_t code_head_stride, int64_t n_keys,
+                             int64_t shortlist, float* q_low, float* lut, float* score_range, void* stream) {
   sva::clear_error();
   SVA_REQUIRE(q && q_proj && scale && codebooks && q_low && lut && score_range, "sva_query_lut: null pointer");
   SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0, "sva_query_lut: empty query batch");
@@ -112,14 +236,49 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
               (long long)D, (long long)R);
   SVA_REQUIRE(S > 0 && S <= 64 && R % S == 0, "sva_query_lut: rank %lld not divisible by subspaces %lld",
               (long long)R, (long long)S);
-  SVA_REQUIRE(C > 0 && S * C <= 65536, "sva_query_lut: codewords %lld out of range", (long long)C);
+  SVA_REQUIRE(C > 0, "sva_query_lut: codewords %lld out of range", (long long)C);
+  SVA_REQUIRE((D * R) % 4 == 0 && (S * C * (R / S)) % 4 == 0 && ((uintptr_t)q_proj & 15u) == 0 &&
+                  ((uintptr_t)codebooks & 15u) == 0,
+              "sva_query_lut: q_proj / codebooks must be 16-byte aligned fp32");
   SVA_REQUIRE(q_dtype >= 0 && q_dtype <= 2, "sva_query_lut: bad q dtype");
+  SVA_REQUIRE(codes == nullptr || (code_type >= 0 && code_type <= 3 && n_keys >= 0 && shortlist > 0),
+              "sva_query_lut: bad sampling arguments");
+  // the threshold estimate serves the single-query uint8 scan; otherwise skipped
+  const bool sample = codes != nullptr && n_seq == 1 && Q == 1 && code_type == 0 && S <= SAMPLE_MAX_S;
+  const size_t lds = lut_lds_bytes(D, R, S, C, sample);
+  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_query_lut: head weights of %zu bytes exceed LDS", lds);
   const int64_t items = n_seq * H * Q;
   SVA_REQUIRE(items < (1ll << 31), "sva_query_lut: too many query items");
-  const float sqrt_r = (float)sqrt((double)R);
-  hipLaunchKernelGGL(query_lut_kernel, dim3((unsigned)items), dim3(PREP_BLOCK), 0, (hipStream_t)stream, q, q_dtype,
-                     q_seq_stride, q_head_stride, q_tok_stride, (int)H, (int)Q, (int)D, (int)R, (int)S, (int)C, q_proj,
-                     scale, codebooks, sqrt_r, q_low, lut, score_range);
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)query_lut_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      sva::kMaxLds),
+                  "hipFuncSetAttribute(query_lut_kernel)");
+    attr_set = true;
+  }
+  LutParams p;
+  p.q = q;
+  p.q_dtype = q_dtype;
+  p.q_bs = q_seq_stride;
+  p.q_hs = q_head_stride;
+  p.q_ts = q_tok_stride;
+  p.H = (int)H;
+  p.Q = (int)Q;
+  p.D = (int)D;
+  p.R = (int)R;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.q_proj = q_proj;
+  p.scale = scale;
+  p.codebooks = codebooks;
+  p.q_low = q_low;
+  p.lut = lut;
+  p.range = score_range;
+  p.codes = sample ? codes : nullptr;
+  p.code_hs = code_head_stride;
+  p.n_keys = n_keys;
+  p.shortlist = shortlist;
+  hipLaunchKernelGGL(query_lut_kernel, dim3((unsigned)items), dim3(PREP_BLOCK), lds, (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("query_lut_kernel");
   return SVA_OK;
 }

@@ -9,7 +9,7 @@ constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 struct SummonParams {
   const float* lut;    // [items, S*C]
-  const float* range;  // [items, 2] bounds of any scan score
+  const float* range;  // [items, 4]: bounds of any scan sum, sampled floor, 0
   const float* q_low;  // [items, R]
   const void* codes;
   int ctype;

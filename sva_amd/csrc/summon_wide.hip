@@ -1,445 +1,479 @@
 // Long-context summon for few query items (decode, q = 1): many workgroups
-// per item, one pass over the packed uint8 codes.
+// per item, three kernels, no grid-wide synchronisation and no atomics on
+// shared global words.
 //
-// Cooperative launch (every workgroup resident); per query item the keys are
-// split into contiguous chunks, one per workgroup.
-//   Phase A  each thread loads its chunk's codes with 16-byte loads, scores its
-//            keys through the LUT (LDS) in the reference's order and keeps the
-//            order-preserving keys in registers.  A workgroup histogram over
-//            NB linear bins of [lo, hi] (monotone in the score) is built in
-//            LDS; only the bins from the workgroup's own L-th-largest bin up
-//            are published (atomics) to the item's global histogram -- the
-//            item's threshold bin can never lie below that bin.
-//   barrier
-//   Phase B  every workgroup finds the item's threshold bin t (largest bin
-//            whose suffix count reaches L); keys in bins above t are in the
-//            shortlist, keys in bin t go to a tie buffer as unique 64-bit
-//            composites.  Shortlisted keys are rescored against q_low.
-//   barrier
-//   Phase C  one workgroup per item takes the `need` largest composites of the
-//            tie buffer (radix select), rescores them, and returns the item's
-//            histogram and counters to zero for the next call.
-// Selection is exact: the result equals a full sort by (score desc, key asc).
-// The tie buffer holds one entry per key, so it cannot overflow; a heavily
-// tied threshold bin only makes phase C slower.
-#include <hip/hip_cooperative_groups.h>
-
+//   wide_scan     one workgroup per chunk of WB * 32 keys.  Streams the
+//                 chunk's packed uint8 codes (16-byte loads, all in flight
+//                 before use), scores every key through the LUT in the
+//                 reference's order, and appends each allowed key whose sum
+//                 reaches the item's sampled floor t_lo to its wave's own
+//                 candidate list as a unique 64-bit composite (score key,
+//                 key index); counts go to the wave's own counter words.
+//   wide_select   one workgroup per item.  Gathers the candidates (~4x the
+//                 shortlist for the sampled floor) into LDS and radix-selects
+//                 the L largest composites exactly, writing their key
+//                 indices.  When the floor overshot (fewer than L candidates)
+//                 it selects over every key of the item instead: slower, same
+//                 result.
+//   wide_rescore  many workgroups per item: rank score of every shortlisted
+//                 key (k_low . q_low in torch's sum order, 16 lanes per row).
+// Selection equals a full sort by (score desc, key index asc): with R = 64
+// the score is the sum / 8 exactly, so every key below the floor ranks
+// strictly below every candidate.
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
 
-namespace cg = cooperative_groups;
 using namespace sva;
 
 namespace {
 
-constexpr int WB = 256;      // threads per workgroup
-constexpr int NB = 2048;     // histogram bins
-constexpr int NW = WB / WAVE;
-constexpr int EMIT_CAP = 512;   // sure keys a workgroup rescores itself
+constexpr int WB = 256;          // threads per scan workgroup
+constexpr int NW = WB / WAVE;    // waves per scan workgroup
+constexpr int KEYS_PT = 32;      // keys per scan thread
+constexpr int CHUNK = WB * KEYS_PT;
+constexpr int WAVE_KEYS = WAVE * KEYS_PT;  // keys (and candidate capacity) per wave
+constexpr int SB = 1024;         // threads of the select kernel
+constexpr int SNW = SB / WAVE;
+constexpr int LDS_CAND = 16384;  // candidates the select kernel stages in LDS
+constexpr int RROWS = 64;        // rows per rescore workgroup
+constexpr int RB = 256;          // threads per rescore workgroup
 constexpr int64_t kWideMinKeys = 32768;
 constexpr int64_t kMaxWideItems = 64;
 
-struct WideParams {
-  SummonParams p;
-  int W;            // workgroups per item
-  int64_t chunk;    // keys per workgroup (multiple of WB * keys-per-load)
-  uint32_t* ghist;  // [items, NB]
-  uint32_t* gctr;   // [items, 4]: allowed, sure, tie, spare
-  uint64_t* ties;   // [items, tie_cap]
-  int64_t tie_cap;  // = keys per item: the threshold bin can never overflow it
-};
-
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Byte j of a 16-byte vector.
-SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
-
-SVA_DEV int score_bin(float s, float lo, float inv_w) {
-  const float f = (s - lo) * inv_w;  // monotone non-decreasing in s
-  int b = (int)f;
-  b = b < 0 ? 0 : (b >= NB ? NB - 1 : b);
-  return f != f ? 0 : b;
-}
-
-// Rank score of one 64-float k_low row in torch's sum order (the same bits
-// as torch_order_dot64), streamed one 8-float group pair at a time so that
-// only ~24 values are live.
-SVA_DEV float rank_dot64_stream(const float* __restrict__ row, const float* __restrict__ q) {
-#pragma clang fp contract(off)
-  const float4* r4 = reinterpret_cast<const float4*>(row);
-  float part[8];
-#pragma unroll 1
-  for (int x = 0; x < 4; ++x) {
-    const float4 a = r4[2 * x], b = r4[2 * x + 1], c = r4[2 * x + 8], d = r4[2 * x + 9];
-    const float* qa = q + 8 * x;
-    const float* qc = q + 32 + 8 * x;
-    float ax[8];
-    ax[0] = (0.0f + a.x * qa[0]) + c.x * qc[0];
-    ax[1] = (0.0f + a.y * qa[1]) + c.y * qc[1];
-    ax[2] = (0.0f + a.z * qa[2]) + c.z * qc[2];
-    ax[3] = (0.0f + a.w * qa[3]) + c.w * qc[3];
-    ax[4] = (0.0f + b.x * qa[4]) + d.x * qc[4];
-    ax[5] = (0.0f + b.y * qa[5]) + d.y * qc[5];
-    ax[6] = (0.0f + b.z * qa[6]) + d.z * qc[6];
-    ax[7] = (0.0f + b.w * qa[7]) + d.w * qc[7];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) part[l] = x == 0 ? ax[l] : part[l] + ax[l];
-  }
-  float total = 0.0f;
-#pragma unroll
-  for (int l = 0; l < 8; ++l) total = total + part[l];
-  return total;
-}
-
-// Wave-aggregated slot reservation: returns this lane's slot (flag set) from
-// one atomic per wave.
-SVA_DEV uint32_t wave_reserve(uint32_t* counter, bool flag) {
-  const uint64_t ballot = __ballot(flag);
-  if (ballot == 0) return 0;
-  const int lane = lane_id();
-  const uint32_t below = (uint32_t)__popcll(ballot & ((1ull << lane) - 1ull));
-  const int leader = __ffsll((long long)ballot) - 1;
-  uint32_t base = 0;
-  if (lane == leader) base = atomicAdd(counter, (uint32_t)__popcll(ballot));
-  base = __shfl(base, leader, WAVE);
-  return base + below;
-}
-
-// Exact score of key n through the LUT (codes re-read; used for the few
-// threshold-bin members).
-template <int S>
-SVA_DEV float score_at(const uint8_t* __restrict__ codes, int n, const float* tab, int C, float sqrt_r) {
-#pragma clang fp contract(off)
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    uint32_t c = codes[(int64_t)n * S + s];
-    c = c < (uint32_t)C ? c : (uint32_t)(C - 1);
-    acc = acc + tab[s * C + c];
-  }
-  return acc / sqrt_r;
-}
-
-template <int S, int RND>
-__global__ void __launch_bounds__(WB, 4) summon_wide_kernel(WideParams wp) {
-#pragma clang fp contract(off)
-  constexpr int KPT = 16 / S;  // keys per 16-byte load
-  constexpr int KEYS = RND * KPT;
-  constexpr uint32_t NOBIN = 0xFFFFu;
-  static_assert(KEYS <= 64 && KEYS % 2 == 0, "two 16-bit bins per register, 64-bit key masks");
-  __shared__ float tab[S * 256];
-  __shared__ float ql[512];
-  __shared__ uint32_t hist[NB];
-  __shared__ uint32_t scratch[NW + 1];
-  __shared__ uint32_t shared[8];
-  __shared__ int32_t emit_n[EMIT_CAP];
-  __shared__ uint32_t emit_slot[EMIT_CAP];
-
-  const SummonParams& p = wp.p;
-  const int item = blockIdx.x / wp.W;
-  const int w = blockIdx.x % wp.W;
-  const int h = item % p.H;  // q = 1, one sequence
-  const int C = p.C;
-  const int N = (int)p.N;
-  const int cs = (int)((int64_t)w * wp.chunk);
-  const int ce = (int)min((int64_t)cs + wp.chunk, (int64_t)N);
-  const float lo = p.range[2 * item];
-  const float hi = p.range[2 * item + 1];
-  const float span = hi - lo;
-  const float inv_w = (span > 0.0f && span < INFINITY) ? (float)NB / span : 0.0f;
-  const float sqrt_r = p.sqrt_r;
-
-  for (int e = threadIdx.x; e < S * C; e += WB) tab[e] = p.lut[(int64_t)item * S * C + e];
-  for (int r = threadIdx.x; r < p.R; r += WB) ql[r] = p.q_low[(int64_t)item * p.R + r];
-  for (int b = threadIdx.x; b < NB; b += WB) hist[b] = 0;
-  __syncthreads();
-
-  // ---- phase A: stream codes, score, histogram ------------------------------
-  const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
-  const bool masked = p.mask_type != MASK_NONE;
-  u32x4 raw[RND];
-#pragma unroll
-  for (int r = 0; r < RND; ++r) {
-    const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
-    if (base + KPT <= ce) {
-      raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + (int64_t)base * S));
-    } else {
-      uint32_t wv[4] = {0u, 0u, 0u, 0u};
-      for (int j = 0; j < KPT * S; ++j)
-        if (base + j / S < ce) wv[j >> 2] |= (uint32_t)codes[(int64_t)base * S + j] << (8 * (j & 3));
-      raw[r] = u32x4{wv[0], wv[1], wv[2], wv[3]};
-    }
-  }
-  uint32_t bins[KEYS / 2];  // two 16-bit bins per register, NOBIN = not allowed
-  uint32_t n_allowed = 0;
-#pragma unroll
-  for (int r = 0; r < RND; ++r) {
-    const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
-#pragma unroll
-    for (int k = 0; k < KPT; ++k) {
-      const int n = base + k;
-      bool ok = n < ce;
-      if (ok && masked) ok = mask_allows(p.mask, n, p.mask_type);
-      float acc = 0.0f;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        uint32_t c = byte_of(raw[r], k * S + s);
-        c = c < (uint32_t)C ? c : (uint32_t)(C - 1);
-        acc = acc + tab[s * C + c];
-      }
-      const int bin = score_bin(acc / sqrt_r, lo, inv_w);
-      const uint32_t bv = ok ? (uint32_t)bin : NOBIN;
-      const int i = r * KPT + k;
-      if (i & 1) bins[i >> 1] |= bv << 16;
-      else bins[i >> 1] = bv;
-      if (ok) {
-        atomicAdd(&hist[bin], 1u);
-        ++n_allowed;
-      }
-    }
-  }
-  __syncthreads();
-  {
-    constexpr int PER = NB / WB;
-    uint32_t c[PER];
-    uint32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      c[i] = hist[NB - 1 - ((int)threadIdx.x * PER + i)];
-      sum += c[i];
-    }
-    uint32_t tot;
-    const uint32_t before = block_excl_scan<WB>(sum, scratch, &tot);
-    if (threadIdx.x == 0) shared[0] = 0;  // lowest bin to publish
-    __syncthreads();
-    uint32_t run = before;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint32_t prev = run;
-      run += c[i];
-      if (prev < (uint32_t)p.L && run >= (uint32_t)p.L) shared[0] = NB - 1 - ((int)threadIdx.x * PER + i);
-    }
-    __syncthreads();
-    const int pub_lo = (int)shared[0];
-    uint32_t* gh = wp.ghist + (int64_t)item * NB;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int b = NB - 1 - ((int)threadIdx.x * PER + i);
-      if (b >= pub_lo && c[i] != 0u) atomicAdd(&gh[b], c[i]);
-    }
-    const uint32_t wave_allowed = wave_sum_u32(n_allowed);
-    if (lane_id() == 0 && wave_allowed) atomicAdd(&wp.gctr[(int64_t)item * 4 + 0], wave_allowed);
-  }
-  __threadfence();
-  cg::this_grid().sync();
-
-  // ---- phase B: threshold bin, emit sure keys and ties ----------------------
-  const uint32_t* gh = wp.ghist + (int64_t)item * NB;
-  const uint32_t allowed_total =
-      __hip_atomic_load(&wp.gctr[(int64_t)item * 4 + 0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int leff = (int)min((int64_t)p.L, (int64_t)allowed_total);
-  {
-    constexpr int PER = NB / WB;
-    uint32_t c[PER];
-    uint32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      c[i] = __hip_atomic_load(&gh[NB - 1 - ((int)threadIdx.x * PER + i)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sum += c[i];
-    }
-    uint32_t tot;
-    const uint32_t before = block_excl_scan<WB>(sum, scratch, &tot);
-    if (threadIdx.x == 0) {
-      shared[1] = 0;  // threshold bin
-      shared[2] = 0;  // count above it
-    }
-    __syncthreads();
-    uint32_t run = before;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const uint32_t prev = run;
-      run += c[i];
-      if (leff > 0 && prev < (uint32_t)leff && run >= (uint32_t)leff) {
-        shared[1] = NB - 1 - ((int)threadIdx.x * PER + i);
-        shared[2] = prev;
-      }
-    }
-    __syncthreads();
-  }
-  const uint32_t tbin = shared[1];
-  const float* klow = p.k_low + (int64_t)h * p.klow_hs;
-  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  uint32_t* ctr = wp.gctr + (int64_t)item * 4;
-  uint64_t* ties = wp.ties + (int64_t)item * wp.tie_cap;
-  uint64_t sure_mask = 0, tie_mask = 0;
-  if (leff > 0) {
-#pragma unroll
-    for (int i = 0; i < KEYS; ++i) {
-      const uint32_t bv = (bins[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-      sure_mask |= (uint64_t)(bv != NOBIN && bv > tbin) << i;
-      tie_mask |= (uint64_t)(bv == tbin) << i;
-    }
-  }
-  const uint32_t n_sure = (uint32_t)__popcll(sure_mask), n_tie = (uint32_t)__popcll(tie_mask);
-  uint32_t sure_tot, tie_tot;
-  uint32_t s_off = block_excl_scan<WB>(n_sure, scratch, &sure_tot);
-  uint32_t t_off = block_excl_scan<WB>(n_tie, scratch, &tie_tot);
-  if (threadIdx.x == 0) {
-    shared[3] = sure_tot;
-    shared[4] = sure_tot ? atomicAdd(&ctr[1], sure_tot) : 0u;
-    shared[5] = tie_tot ? atomicAdd(&ctr[2], tie_tot) : 0u;
-  }
-  __syncthreads();
-  const uint32_t sure_base = shared[4], tie_base = shared[5];
-  while (sure_mask | tie_mask) {
-    const int i = __builtin_ctzll(sure_mask | tie_mask);
-    const uint64_t bit = 1ull << i;
-    const int n = cs + ((i / KPT) * WB + (int)threadIdx.x) * KPT + (i % KPT);
-    if (sure_mask & bit) {
-      const uint32_t slot = sure_base + s_off;
-      if (slot < (uint32_t)p.L) {
-        out_idx[slot] = n;
-        if (s_off < (uint32_t)EMIT_CAP) {
-          emit_n[s_off] = n;
-          emit_slot[s_off] = slot;
-        } else {
-          out_rank[slot] = __uint_as_float(0x7FC0DEADu);  // rescored in phase C
-        }
-      }
-      ++s_off;
-    } else {
-      const int64_t ts = (int64_t)tie_base + t_off;
-      if (ts < wp.tie_cap) ties[ts] = composite(f2key(score_at<S>(codes, n, tab, C, sqrt_r)), (uint32_t)n);
-      ++t_off;
-    }
-    sure_mask &= ~bit;
-    tie_mask &= ~bit;
-  }
-  __syncthreads();
-  {
-    const int n_emit = (int)min(shared[3], (uint32_t)EMIT_CAP);
-#pragma unroll 1
-    for (int e = threadIdx.x; e < n_emit; e += WB) {
-      const float* row = klow + (int64_t)emit_n[e] * p.R;
-      out_rank[emit_slot[e]] = rank_dot64_stream(row, ql) / sqrt_r;
-    }
-  }
-  __threadfence();
-  cg::this_grid().sync();
-
-  // ---- phase C: resolve the threshold bin (one workgroup per item) ---------
-  if (w == 0) {
-    const uint32_t above = shared[2];
-    const int need = leff - (int)above;
-    const uint32_t n_ties = __hip_atomic_load(&ctr[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int nt = (int)min((int64_t)n_ties, wp.tie_cap);
-    if (leff > 0 && need > 0) {
-      uint64_t X = 0;  // take every tie when exactly `need` of them exist
-      if (nt != need) X = radix_select_u64<WB>([&](int i) { return ties[i]; }, nt, need, hist, scratch, shared + 4);
-      if (threadIdx.x == 0) shared[3] = 0;
-      __syncthreads();
-#pragma unroll 1
-      for (int i = threadIdx.x; i < nt; i += WB) {
-        const uint64_t cmp = ties[i];
-        if (cmp >= X) {
-          const uint32_t j = atomicAdd(&shared[3], 1u);
-          const uint32_t n = composite_index(cmp);
-          if (above + j < (uint32_t)p.L && n < (uint32_t)N) {
-            out_idx[above + j] = (int32_t)n;
-            out_rank[above + j] = rank_dot64_stream(klow + (int64_t)n * p.R, ql) / sqrt_r;
-          }
-        }
-      }
-    }
-    {
-      // sure entries whose workgroup list overflowed carry a sentinel rank
-      const int n_above = (int)min(above, (uint32_t)p.L);
-#pragma unroll 1
-      for (int j = threadIdx.x; j < n_above; j += WB) {
-        const int32_t n = out_idx[j];
-        if (__float_as_uint(out_rank[j]) == 0x7FC0DEADu && n >= 0 && n < N)
-          out_rank[j] = rank_dot64_stream(klow + (int64_t)n * p.R, ql) / sqrt_r;
-      }
-    }
-    if (threadIdx.x == 0) {
-      p.sl_count[item] = leff;
-      ctr[0] = 0u;
-      ctr[1] = 0u;
-      ctr[2] = 0u;
-      ctr[3] = 0u;
-    }
-    uint32_t* ghw = wp.ghist + (int64_t)item * NB;
-    for (int b = threadIdx.x; b < NB; b += WB) ghw[b] = 0u;
-  }
-}
-
-template <int S, int RND>
-const void* wide_fn() {
-  return (const void*)summon_wide_kernel<S, RND>;
-}
-
-const void* wide_kernel_for(int S, int rnd) {
-#define SVA_WIDE_CASE(SS, RR) \
-  if (S == SS && rnd == RR) return wide_fn<SS, RR>();
-  SVA_WIDE_CASE(1, 1) SVA_WIDE_CASE(1, 2) SVA_WIDE_CASE(1, 3) SVA_WIDE_CASE(1, 4)
-  SVA_WIDE_CASE(2, 2) SVA_WIDE_CASE(2, 4) SVA_WIDE_CASE(2, 6) SVA_WIDE_CASE(2, 8)
-  SVA_WIDE_CASE(4, 2) SVA_WIDE_CASE(4, 4) SVA_WIDE_CASE(4, 8) SVA_WIDE_CASE(4, 12) SVA_WIDE_CASE(4, 16)
-  SVA_WIDE_CASE(8, 4) SVA_WIDE_CASE(8, 8) SVA_WIDE_CASE(8, 16) SVA_WIDE_CASE(8, 24) SVA_WIDE_CASE(8, 32)
-#undef SVA_WIDE_CASE
-  return nullptr;
-}
-
-const int* rnd_options(int S, int* count) {
-  static const int r1[] = {1, 2, 3, 4};
-  static const int r2[] = {2, 4, 6, 8};
-  static const int r4[] = {2, 4, 8, 12, 16};
-  static const int r8[] = {4, 8, 16, 24, 32};
-  switch (S) {
-    case 1: *count = 4; return r1;
-    case 2: *count = 4; return r2;
-    case 4: *count = 5; return r4;
-    case 8: *count = 5; return r8;
-    default: *count = 0; return nullptr;
-  }
-}
-
-struct WidePlan {
-  const void* fn;
-  int W;
-  int64_t chunk;
+struct WideArgs {
+  SummonParams p;
+  uint32_t* ncand;   // [items, W * NW] candidates of each scan wave
+  uint32_t* nallow;  // [items, W * NW] allowed keys of each scan wave
+  uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
+  int W;             // scan workgroups per item
 };
 
-bool plan_wide(const SummonParams& p, int64_t items, WidePlan* plan) {
-  int nopt = 0;
-  const int* opts = rnd_options(p.S, &nopt);
-  if (!opts) return false;
-  const int kpt = 16 / p.S;
-  const int cus = device_cu_count();
-  for (int i = 0; i < nopt; ++i) {
-    const void* fn = wide_kernel_for(p.S, opts[i]);
-    if (!fn) continue;
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, WB, 0) != hipSuccess || per_cu <= 0) continue;
-    const int64_t resident = (int64_t)per_cu * cus;
-    const int64_t w_max = resident / items;
-    if (w_max < 2) continue;
-    const int64_t per_wg = (int64_t)WB * kpt * opts[i];
-    const int64_t w_need = (p.N + per_wg - 1) / per_wg;
-    if (w_need > w_max) continue;
-    // spread over as many workgroups as residency allows, keeping whole loads
-    const int64_t W = std::max<int64_t>(w_need, std::min<int64_t>(w_max, (p.N + (int64_t)WB * kpt - 1) / ((int64_t)WB * kpt)));
-    const int64_t step = (int64_t)WB * kpt;
-    int64_t chunk = (p.N + W - 1) / W;
-    chunk = (chunk + step - 1) / step * step;
-    if (chunk > per_wg) continue;
-    plan->fn = fn;
-    plan->W = (int)((p.N + chunk - 1) / chunk);
-    plan->chunk = chunk;
-    return true;
+SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
+
+// Loads a chunk's codes: every full 16-byte group with one unconditional
+// vector load (all issued before any is used); a partial last chunk falls
+// back to guarded byte loads.
+template <int S>
+SVA_DEV void load_chunk(const uint8_t* __restrict__ codes, int cs, int ce, u32x4 (&raw)[KEYS_PT * S / 16]) {
+  constexpr int KPT = 16 / S;
+  constexpr int RND = KEYS_PT / KPT;
+  if (ce - cs == CHUNK) {
+#pragma unroll
+    for (int r = 0; r < RND; ++r) {
+      const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
+      raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + (int64_t)base * S));
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RND; ++r) {
+      const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
+      if (base + KPT <= ce) {
+        raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + (int64_t)base * S));
+      } else {
+        uint32_t wv[4] = {0u, 0u, 0u, 0u};
+        for (int j = 0; j < KPT * S; ++j)
+          if (base + j / S < ce) wv[j >> 2] |= (uint32_t)codes[(int64_t)base * S + j] << (8 * (j & 3));
+        raw[r] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      }
+    }
   }
-  return false;
+}
+
+// Per-query tables for the scan.  BP: entry c of subspace s lives in lane c
+// of reg[s] and is fetched with ds_bpermute (conflict-free; needs C <= 64 and
+// all 64 lanes active).  Otherwise an LDS table of 256 entries per subspace
+// (entries past C repeat entry C-1, so any uint8 code stays in bounds).
+template <int S, bool BP>
+struct ScanTables {
+  float reg[BP ? S : 1];
+  const float* tab;
+  SVA_DEV void init(const SummonParams& p, int item, float* lds_tab) {
+    const float* src = p.lut + (int64_t)item * S * p.C;
+    if (BP) {
+      const int c = min(lane_id(), p.C - 1);
+#pragma unroll
+      for (int s = 0; s < (BP ? S : 1); ++s) reg[s] = src[s * p.C + c];
+    } else {
+      for (int e = threadIdx.x; e < S * 256; e += blockDim.x) lds_tab[e] = src[(e >> 8) * p.C + min(e & 255, p.C - 1)];
+      tab = lds_tab;
+    }
+  }
+  SVA_DEV float get(int s, uint32_t c) const {
+    if (BP) return __int_as_float(__builtin_amdgcn_ds_bpermute((int)(c << 2), __float_as_int(reg[BP ? s : 0])));
+    return tab[s * 256 + c];
+  }
+};
+
+// Scores the keys of one 16-byte round of the thread, branch-free so that
+// the round's table lookups are in flight together: acc[k] = ((T0 + T1) +
+// T2) + ... (the scan sum before the 1/8 scale; the reference's leading
+// 0 + T0 only changes the sign of a zero).  bpermute lookups need all 64
+// lanes, which this guarantees.
+template <int S, bool BP>
+SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, BP>& T, float (&acc)[16 / S]) {
+#pragma clang fp contract(off)
+  constexpr int KPT = 16 / S;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    float a = T.get(0, byte_of(raw, k * S));
+#pragma unroll
+    for (int s = 1; s < S; ++s) a = a + T.get(s, byte_of(raw, k * S + s));
+    acc[k] = a;
+  }
+}
+
+// Key index of slot i of this thread in the chunk starting at cs.
+template <int S>
+SVA_DEV int slot_key(int cs, int i) {
+  constexpr int KPT = 16 / S;
+  return cs + ((i / KPT) * WB + (int)threadIdx.x) * KPT + (i % KPT);
+}
+
+template <bool FULL, bool MASKED>
+SVA_DEV bool key_ok(const SummonParams& p, int n, int ce) {
+  bool ok = FULL || n < ce;
+  if (MASKED && ok) ok = mask_allows(p.mask, n, p.mask_type);
+  return ok;
+}
+
+// Rank score of a 64-float k_low row in torch's sum order, computed by the
+// 16-lane group of the calling lane (lane j holds float4 j of the row; the
+// pairing, lane chains and final order follow torch_order_dot64).  Every lane
+// of the group receives the result.  All 16 lanes must call it.
+SVA_DEV float rank_dot64_group16(const float* __restrict__ row, const float* __restrict__ q) {
+#pragma clang fp contract(off)
+  const int j = lane_id() & 15;
+  const float4 r = reinterpret_cast<const float4*>(row)[j];
+  const float4 qq = reinterpret_cast<const float4*>(q)[j];
+  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
+  // element e (< 32) pairs with e + 32, held by lane j + 8
+  const float a0 = (0.0f + p0) + __shfl_down(p0, 8, 16);
+  const float a1 = (0.0f + p1) + __shfl_down(p1, 8, 16);
+  const float a2 = (0.0f + p2) + __shfl_down(p2, 8, 16);
+  const float a3 = (0.0f + p3) + __shfl_down(p3, 8, 16);
+  // lanes g, g+2, g+4, g+6 hold accumulators 0..3 of lane-group g
+  const float v0 = ((a0 + __shfl_down(a0, 2, 16)) + __shfl_down(a0, 4, 16)) + __shfl_down(a0, 6, 16);
+  const float v1 = ((a1 + __shfl_down(a1, 2, 16)) + __shfl_down(a1, 4, 16)) + __shfl_down(a1, 6, 16);
+  const float v2 = ((a2 + __shfl_down(a2, 2, 16)) + __shfl_down(a2, 4, 16)) + __shfl_down(a2, 6, 16);
+  const float v3 = ((a3 + __shfl_down(a3, 2, 16)) + __shfl_down(a3, 4, 16)) + __shfl_down(a3, 6, 16);
+  const float w0 = __shfl_down(v0, 1, 16), w1 = __shfl_down(v1, 1, 16);
+  const float w2 = __shfl_down(v2, 1, 16), w3 = __shfl_down(v3, 1, 16);
+  const float t = (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
+  return __shfl(t, 0, 16);
+}
+
+// Exact score of key n from the global table (the reference's order, with the
+// leading 0 + T0 and the division).  Used by the all-keys fallback only.
+SVA_DEV float score_at(const SummonParams& p, const uint8_t* __restrict__ codes, int item, int n) {
+#pragma clang fp contract(off)
+  const float* lut = p.lut + (int64_t)item * p.S * p.C;
+  float acc = 0.0f;
+  for (int s = 0; s < p.S; ++s) {
+    uint32_t c = codes[(int64_t)n * p.S + s];
+    c = c < (uint32_t)p.C ? c : (uint32_t)(p.C - 1);
+    acc = acc + lut[s * p.C + c];
+  }
+  return acc / p.sqrt_r;
+}
+
+
+// Candidate floor of an item: the sampled estimate, or the table minimum
+// (every allowed key is a candidate) when there is none.
+SVA_DEV float item_floor(const SummonParams& p, int item) {
+  const float lo = p.range[4 * item + 0];
+  const float est = p.range[4 * item + 2];
+  return est > lo ? est : lo;
+}
+
+template <int S, bool BP, bool MASKED>
+__global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float tab_lds[BP ? 1 : S * 256];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x / a.W;
+  const int w = blockIdx.x % a.W;
+  const int h = item % p.H;
+  const int cs = w * CHUNK;
+  const int ce = (int)min((int64_t)cs + CHUNK, p.N);
+  const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+  u32x4 raw[KEYS_PT * S / 16];
+  load_chunk<S>(codes, cs, ce, raw);
+  ScanTables<S, BP> T;
+  T.init(p, item, tab_lds);
+  const float t_lo = item_floor(p, item);
+  if (!BP) __syncthreads();
+  const int wid = threadIdx.x / WAVE;
+  const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
+  uint64_t* out = a.cand + sub * WAVE_KEYS;
+  constexpr int KPT = 16 / S;
+  const bool full = ce - cs == CHUNK;
+  uint32_t n_allowed = 0;
+  uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
+#pragma unroll
+  for (int r = 0; r < KEYS_PT / KPT; ++r) {
+    float acc[KPT];
+    score_round<S, BP>(raw[r], T, acc);
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      const int n = slot_key<S>(cs, r * KPT + k);
+      const bool ok = full ? key_ok<true, MASKED>(p, n, ce) : key_ok<false, MASKED>(p, n, ce);
+      n_allowed += ok;
+      const bool c = ok && acc[k] >= t_lo;
+      const uint64_t m = __ballot(c);
+      if (m != 0ull) {  // rare: the shortlist and the keys near it
+        if (c) {
+          const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+          out[wc + below] = composite(f2key(acc[k] / p.sqrt_r), (uint32_t)n);
+        }
+        wc += (uint32_t)__popcll(m);
+      }
+    }
+  }
+  const uint32_t wa = wave_sum_u32(n_allowed);
+  if (lane_id() == 0) {
+    a.ncand[sub] = wc;
+    a.nallow[sub] = wa;
+  }
+}
+
+// Exact selection of the k largest nonzero composites among the elements a
+// visitor yields (each element exactly once per call, unique values): radix
+// passes of up to 8 bits from the highest bit where elements differ, with
+// one LDS histogram per wave.  Returns X such that the selected elements are
+// exactly those >= X.  Every thread of the block must call it.
+template <typename Visit>
+SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint32_t* scratch, uint64_t* shared64,
+                                uint32_t* shared) {
+  const int wid = threadIdx.x / WAVE;
+  // bits above the highest differing bit are common to every element
+  uint64_t vor = 0ull, vand = ~0ull;
+  visit([&](uint64_t x) {
+    vor |= x;
+    vand &= x;
+  });
+  for (int off = 1; off < WAVE; off <<= 1) {
+    vor |= __shfl_xor(vor, off, WAVE);
+    vand &= __shfl_xor(vand, off, WAVE);
+  }
+  if (threadIdx.x == 0) {
+    shared64[0] = 0ull;
+    shared64[1] = ~0ull;
+  }
+  __syncthreads();
+  if (lane_id() == 0) {
+    atomicOr((unsigned long long*)&shared64[0], (unsigned long long)vor);
+    atomicAnd((unsigned long long*)&shared64[1], (unsigned long long)vand);
+  }
+  __syncthreads();
+  const uint64_t diff = shared64[0] ^ shared64[1];
+  if (diff == 0ull) return shared64[0];  // a single element
+  int top = 63 - __clzll((long long)diff);
+  uint64_t pmask = top == 63 ? 0ull : ~0ull << (top + 1);
+  uint64_t prefix = shared64[1] & pmask;
+  int need = k;
+  while (true) {
+    const int shift = max(top - 7, 0);
+    const uint32_t dmask = (1u << (top - shift + 1)) - 1u;
+    for (int i = threadIdx.x; i < SNW * 256; i += SB) whist[i >> 8][i & 255] = 0u;
+    __syncthreads();
+    visit([&](uint64_t x) {
+      if ((x & pmask) == prefix) atomicAdd(&whist[wid][(uint32_t)(x >> shift) & dmask], 1u);
+    });
+    __syncthreads();
+    uint32_t tot = 0;
+    if (threadIdx.x < 256) {
+      const int b = 255 - (int)threadIdx.x;  // bins from the top
+      for (int v = 0; v < SNW; ++v) tot += whist[v][b];
+    }
+    uint32_t total;
+    const uint32_t above = block_excl_scan<SB>(tot, scratch, &total);
+    if (threadIdx.x < 256 && above < (uint32_t)need && above + tot >= (uint32_t)need) {
+      shared[0] = 255u - threadIdx.x;
+      shared[1] = above;
+      shared[2] = tot;
+    }
+    __syncthreads();
+    const uint32_t b = shared[0];
+    need -= (int)shared[1];
+    prefix |= (uint64_t)b << shift;
+    pmask |= (uint64_t)dmask << shift;
+    const bool done = shared[2] == (uint32_t)need || shift == 0;
+    __syncthreads();
+    if (done) return prefix;
+    top = shift - 1;
+  }
+}
+
+__global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  uint64_t* cl = (uint64_t*)lds;                                   // [LDS_CAND]
+  uint32_t(*whist)[256] = (uint32_t(*)[256])(cl + LDS_CAND);       // [SNW][256]
+  uint64_t* shared64 = (uint64_t*)(whist + SNW);                   // [2]
+  uint32_t* scratch = (uint32_t*)(shared64 + 2);                   // [SNW + 1]
+  uint32_t* shared = scratch + SNW + 1;                            // [4]
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x;
+  const int nsub = a.W * NW;
+  const uint32_t* ncand = a.ncand + (int64_t)item * nsub;
+  const uint32_t* nallow = a.nallow + (int64_t)item * nsub;
+  const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  // totals: candidates M and allowed keys A
+  uint32_t m = 0, al = 0;
+  for (int s = threadIdx.x; s < nsub; s += SB) {
+    m += ncand[s];
+    al += nallow[s];
+  }
+  uint32_t M, A;
+  block_excl_scan<SB>(m, scratch, &M);
+  block_excl_scan<SB>(al, scratch, &A);
+  const int leff = (int)min((uint32_t)p.L, A);
+  if (threadIdx.x == 0) {
+    p.sl_count[item] = leff;
+    shared[3] = 0u;  // output carry of the list-by-list path
+  }
+  if (leff == 0) return;
+  if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND) {
+    // common case: stage the candidates contiguously in LDS
+    uint32_t carry = 0;
+    for (int g = 0; g < nsub; g += SB) {
+      const int s = g + (int)threadIdx.x;
+      const uint32_t c = s < nsub ? ncand[s] : 0u;
+      uint32_t tot;
+      const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
+      const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+#pragma unroll 8
+      for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
+      carry += tot;
+    }
+    __syncthreads();
+    const int Mi = (int)M;
+    auto visit = [&](auto&& f) {
+      for (int j = threadIdx.x; j < Mi; j += SB) f(cl[j]);
+    };
+    const uint64_t X = (uint32_t)leff == M ? 1ull : select_largest(visit, leff, whist, scratch, shared64, shared);
+    // write the selected in staging order: contiguous ranges per thread
+    const int per = (Mi + SB - 1) / SB;
+    const int j0 = min(Mi, (int)threadIdx.x * per), j1 = min(Mi, j0 + per);
+    uint32_t cnt = 0;
+    for (int j = j0; j < j1; ++j) cnt += cl[j] >= X;
+    uint32_t tot;
+    uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
+    for (int j = j0; j < j1; ++j) {
+      const uint64_t x = cl[j];
+      if (x >= X && o < (uint32_t)leff) out_idx[o++] = (int32_t)composite_index(x);
+    }
+  } else if (M >= (uint32_t)leff) {
+    // many candidates: select straight from the per-wave lists
+    auto visit = [&](auto&& f) {
+      for (int s = threadIdx.x; s < nsub; s += SB) {
+        const uint32_t c = ncand[s];
+        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+        for (uint32_t j = 0; j < c; ++j) f(src[j]);
+      }
+    };
+    const uint64_t X = (uint32_t)leff == M ? 1ull : select_largest(visit, leff, whist, scratch, shared64, shared);
+    for (int g = 0; g < nsub; g += SB) {
+      const int s = g + (int)threadIdx.x;
+      const uint32_t c = s < nsub ? ncand[s] : 0u;
+      const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+      uint32_t cnt = 0;
+      for (uint32_t j = 0; j < c; ++j) cnt += src[j] >= X;
+      uint32_t tot;
+      uint32_t o = shared[3] + block_excl_scan<SB>(cnt, scratch, &tot);
+      for (uint32_t j = 0; j < c; ++j)
+        if (src[j] >= X && o < (uint32_t)leff) out_idx[o++] = (int32_t)composite_index(src[j]);
+      __syncthreads();
+      if (threadIdx.x == 0) shared[3] += tot;
+      __syncthreads();
+    }
+  } else {
+    // the sampled floor overshot: exact selection over every key of the item
+    const int h = item % p.H;
+    const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+    const int N = (int)p.N;
+    auto key_at = [&](int n) -> uint64_t {
+      if (!mask_allows(p.mask, n, p.mask_type)) return 0ull;
+      return composite(f2key(score_at(p, codes, item, n)), (uint32_t)n);
+    };
+    auto visit = [&](auto&& f) {
+      for (int n = threadIdx.x; n < N; n += SB) {
+        const uint64_t x = key_at(n);
+        if (x != 0ull) f(x);
+      }
+    };
+    const uint64_t X = (uint32_t)leff == A ? 1ull : select_largest(visit, leff, whist, scratch, shared64, shared);
+    const int per = (N + SB - 1) / SB;
+    const int n0 = min(N, (int)threadIdx.x * per), n1 = min(N, n0 + per);
+    uint32_t cnt = 0;
+    for (int n = n0; n < n1; ++n) cnt += key_at(n) >= X;
+    uint32_t tot;
+    uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
+    for (int n = n0; n < n1; ++n)
+      if (key_at(n) >= X && o < (uint32_t)leff) out_idx[o++] = n;
+  }
+}
+
+constexpr size_t kSelectLds = sizeof(uint64_t) * (LDS_CAND + 2) + sizeof(uint32_t) * (SNW * 256 + SNW + 1 + 4);
+
+// Rank scores of the shortlist: RROWS rows per workgroup, 16 lanes per row.
+__global__ void __launch_bounds__(RB) wide_rescore_kernel(WideArgs a) {
+  const SummonParams& p = a.p;
+  const int item = blockIdx.y;
+  const int h = item % p.H;
+  const int count = p.sl_count[item];
+  const int row0 = blockIdx.x * RROWS;
+  if (row0 >= count) return;
+  const float* ql = p.q_low + (int64_t)item * p.R;
+  const float* klow = p.k_low + (int64_t)h * p.klow_hs;
+  const int32_t* idx = p.sl_idx + (int64_t)item * p.L;
+  float* rank = p.sl_rank + (int64_t)item * p.L;
+  const int g = threadIdx.x >> 4;  // 16-lane group
+  for (int r = row0 + g; r < row0 + RROWS; r += RB / 16) {
+    if (r - g >= count) break;  // uniform per wave: every group of the wave passes the same r - g
+    const bool valid = r < count;
+    int32_t key = idx[valid ? r : row0];
+    key = key < 0 ? 0 : (key >= (int32_t)p.N ? (int32_t)p.N - 1 : key);
+    const float dot = rank_dot64_group16(klow + (int64_t)key * p.R, ql);
+    if (valid && (lane_id() & 15) == 0) rank[r] = dot / p.sqrt_r;
+  }
+}
+
+template <int S, bool BP, bool MASKED>
+int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
+  hipLaunchKernelGGL((wide_scan_kernel<S, BP, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  SVA_CHECK_LAUNCH("wide_scan_kernel");
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)wide_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)kSelectLds),
+                  "hipFuncSetAttribute(wide_select_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(wide_select_kernel, dim3((unsigned)items), dim3(SB), kSelectLds, stream, a);
+  SVA_CHECK_LAUNCH("wide_select_kernel");
+  const dim3 rgrid((unsigned)((a.p.L + RROWS - 1) / RROWS), (unsigned)items);
+  hipLaunchKernelGGL(wide_rescore_kernel, rgrid, dim3(RB), 0, stream, a);
+  SVA_CHECK_LAUNCH("wide_rescore_kernel");
+  return SVA_OK;
+}
+
+template <int S>
+int launch_wide_s(const WideArgs& a, int64_t items, bool masked, hipStream_t stream) {
+  const bool bp = a.p.C <= 64;
+  if (bp) return masked ? launch_wide<S, true, true>(a, items, stream) : launch_wide<S, true, false>(a, items, stream);
+  return masked ? launch_wide<S, false, true>(a, items, stream) : launch_wide<S, false, false>(a, items, stream);
+}
+
+// Workspace: per-wave counters, then per-wave candidate lists.  Every word a
+// call reads was written earlier in the same call, so no state is carried
+// between calls and calls of any shape can share one buffer.
+size_t counters_bytes(int64_t items, int64_t W) {
+  return ((size_t)(2 * items * W * NW) * sizeof(uint32_t) + 255) & ~(size_t)255;
 }
 
 }  // namespace
@@ -451,48 +485,38 @@ bool summon_wide_eligible(const SummonParams& p, int64_t items) {
   if (p.S != 1 && p.S != 2 && p.S != 4 && p.S != 8) return false;
   if (p.R != 64 || p.N < kWideMinKeys || p.N >= (1ll << 30) || items > kMaxWideItems) return false;
   if (((uintptr_t)p.codes & 15u) != 0 || p.code_hs % 16 != 0) return false;
-  if (p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16) {
-    if (p.mask == nullptr) return false;
-  }
-  WidePlan plan;
-  return plan_wide(p, items, &plan);
+  if (((uintptr_t)p.k_low & 15u) != 0 || p.klow_hs % 4 != 0 || ((uintptr_t)p.q_low & 15u) != 0) return false;
+  if (p.mask_type != MASK_NONE && p.mask_type != MASK_BOOL && p.mask == nullptr) return false;
+  return true;
 }
-
-// Workspace layout: a fixed header of per-item histograms and counters for
-// up to kMaxWideItems items (kept all-zero between calls: each call returns
-// the entries it used to zero), then the tie buffers (one entry per key per
-// item; no state carried across calls).  The header's offsets never depend
-// on the cache length, so calls of different shapes can share one buffer.
-constexpr size_t kWideHeader = (size_t)kMaxWideItems * (NB * sizeof(uint32_t) + 4 * sizeof(uint32_t));
 
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t) {
   const int64_t items = n_seq * H * Q;
   if (n_seq != 1 || Q != 1 || n_keys < kWideMinKeys || items > kMaxWideItems) return 256;
-  return kWideHeader + (size_t)items * (size_t)n_keys * sizeof(uint64_t) + 256;
+  const int64_t W = (n_keys + CHUNK - 1) / CHUNK;
+  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * sizeof(uint64_t);
 }
 
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
-  WidePlan plan;
-  SVA_UNSUPPORTED(plan_wide(p, items, &plan), "sva_summon: no resident wide plan");
   const size_t need = summon_wide_workspace_bytes(1, p.H, 1, p.N, p.L);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
-              "sva_summon: workspace of %zu bytes (256-byte aligned, zero-filled) required, got %zu", need,
-              workspace_bytes);
-  WideParams wp;
-  wp.p = p;
-  wp.W = plan.W;
-  wp.chunk = plan.chunk;
+              "sva_summon: workspace of %zu bytes (256-byte aligned) required, got %zu", need, workspace_bytes);
+  WideArgs a;
+  a.p = p;
+  a.W = (int)((p.N + CHUNK - 1) / CHUNK);
   char* ws = (char*)workspace;
-  wp.ghist = (uint32_t*)ws;                         // [kMaxWideItems, NB]
-  wp.gctr = wp.ghist + kMaxWideItems * NB;          // [kMaxWideItems, 4]
-  wp.ties = (uint64_t*)(ws + kWideHeader);          // [items, N]
-  wp.tie_cap = p.N;
-  void* args[] = {&wp};
-  const dim3 grid((unsigned)(items * plan.W));
-  SVA_CHECK_HIP(hipLaunchCooperativeKernel(plan.fn, grid, dim3(WB), args, 0, stream), "summon_wide_kernel launch");
-  SVA_CHECK_LAUNCH("summon_wide_kernel");
-  return SVA_OK;
+  a.ncand = (uint32_t*)ws;
+  a.nallow = a.ncand + items * a.W * NW;
+  a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
+  // a bool mask allows every key (the reference's `mask > -1e4` rule)
+  const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
+  switch (p.S) {
+    case 1: return launch_wide_s<1>(a, items, masked, stream);
+    case 2: return launch_wide_s<2>(a, items, masked, stream);
+    case 4: return launch_wide_s<4>(a, items, masked, stream);
+    default: return launch_wide_s<8>(a, items, masked, stream);
+  }
 }
 
 }  // namespace sva

@@ -16,19 +16,20 @@ from . import _lib
 from ._lib import check, code_type, dtype_code, lib, ptr, require_device, stream_handle
 
 
-_workspaces: dict[torch.device, torch.Tensor] = {}
+_workspaces: dict[tuple[torch.device, str], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device summon workspace.  It is zero-filled when (re)allocated and
-    the kernels return it to all-zero, so one buffer serves every call made
-    on the device's current stream (calls on concurrent streams must not
-    share it)."""
+def workspace(device: torch.device, nbytes: int, kind: str = "summon") -> torch.Tensor:
+    """Per-device scratch buffers, one per kind, grown on demand.  The kernels
+    carry no state in them between calls, so one buffer serves every call made
+    on the device's current stream (calls on concurrent streams must not share
+    it)."""
 
-    ws = _workspaces.get(device)
+    key = (device, kind)
+    ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), device=device, dtype=torch.uint8)
-        _workspaces[device] = ws
+        _workspaces[key] = ws
     return ws
 
 
@@ -48,8 +49,11 @@ def _f32c(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor):
-    """q_low [n_seq,H,Q,R], lut [n_seq,H,Q,S,C], score_range [n_seq,H,Q,2] (sva/llama.py:211, sva/ops.py:66-68)."""
+def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor,
+              codes: torch.Tensor | None = None, n_keys: int = 0, shortlist: int = 0):
+    """q_low [n_seq,H,Q,R], lut [n_seq,H,Q,S,C], score_range [n_seq,H,Q,4] (sva/llama.py:211, sva/ops.py:66-68).
+
+    With `codes`, the summon threshold estimate is sampled from the cache."""
 
     q = _as_query(q)
     q_proj, scale, codebooks = _f32c(q_proj), _f32c(scale), _f32c(codebooks)
@@ -61,12 +65,14 @@ def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebo
         raise ValueError(f"q_proj shape {tuple(q_proj.shape)} != {(heads, head_dim, rank)}")
     q_low = torch.empty(n_seq, heads, q_len, rank, device=device, dtype=torch.float32)
     lut = torch.empty(n_seq, heads, q_len, subspaces, codewords, device=device, dtype=torch.float32)
-    rng = torch.empty(n_seq, heads, q_len, 2, device=device, dtype=torch.float32)
+    rng = torch.empty(n_seq, heads, q_len, 4, device=device, dtype=torch.float32)
+    ctype = code_type(codes) if codes is not None else 0
+    chs = codes.stride(0) if codes is not None else 0
     check(
         lib().sva_query_lut(
             ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), n_seq, heads, q_len, head_dim, rank,
-            subspaces, codewords, ptr(q_proj), ptr(scale), ptr(codebooks), ptr(q_low), ptr(lut), ptr(rng),
-            stream_handle(device),
+            subspaces, codewords, ptr(q_proj), ptr(scale), ptr(codebooks), ptr(codes), ctype, chs, n_keys,
+            max(shortlist, 1), ptr(q_low), ptr(lut), ptr(rng), stream_handle(device),
         ),
         "sva_query_lut",
     )
@@ -168,12 +174,14 @@ def verify(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, fin_idx: t
     budget = fin_idx.shape[1]
     device = require_device(q, keys, values, fin_idx, fin_count, seq_offsets, seq_lens)
     out = torch.empty(n_seq, heads, q_len, head_dim, device=device, dtype=out_dtype or q.dtype)
+    ws = workspace(device, int(lib().sva_verify_workspace_bytes(n_seq, heads, kv_heads, q_len, head_dim, budget)),
+                   "verify")
     check(
         lib().sva_verify(
             ptr(q), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), ptr(keys), ptr(values), dtype_code(keys),
             keys.stride(0), keys.stride(1), ptr(seq_offsets), ptr(seq_lens), n_keys, ptr(fin_idx), ptr(fin_count),
             n_seq, heads, kv_heads, q_len, head_dim, budget, float(scaling), ptr(out), dtype_code(out), out.stride(0),
-            out.stride(1), out.stride(2), stream_handle(device),
+            out.stride(1), out.stride(2), ptr(ws), ws.numel(), stream_handle(device),
         ),
         "sva_verify",
     )
@@ -188,7 +196,7 @@ def scan_decode(q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys:
     Returns (out, sl_count, fin_count)."""
 
     q = _as_query(q)
-    q_low, lut, rng = query_lut(q, q_proj, scale, codebooks)
+    q_low, lut, rng = query_lut(q, q_proj, scale, codebooks, codes, n_keys, shortlist)
     sl_idx, sl_rank, sl_count = summon(lut, rng, q_low, codes, k_low, n_keys, shortlist, mask, seq_offsets, seq_lens)
     fin_idx, fin_count = budget_select(sl_idx, sl_rank, sl_count, budget)
     out = verify(q, keys, values, fin_idx, fin_count, n_keys, scaling, out_dtype, seq_offsets, seq_lens)
@@ -197,3 +205,60 @@ def scan_decode(q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys:
 
 def sqrt_rank(rank: int) -> float:
     return math.sqrt(rank)
+
+
+class ScanDecodePlan:
+    """Preallocated scan-mode decode lookup for a fixed query shape.
+
+    Holds every intermediate buffer (q_low, LUT, shortlist, budget lists) so a
+    decode step issues its four launches (query_lut, summon, budget select,
+    verify) with no allocation and one ctypes call each."""
+
+    def __init__(self, device, n_seq: int, heads: int, q_len: int, head_dim: int, rank: int, subspaces: int,
+                 codewords: int, shortlist: int, budget: int):
+        self.device = torch.device(device)
+        self.shape = (n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget)
+        items = n_seq * heads * q_len
+        f32, i32 = torch.float32, torch.int32
+        self.q_low = torch.empty(n_seq, heads, q_len, rank, device=self.device, dtype=f32)
+        self.lut = torch.empty(n_seq, heads, q_len, subspaces, codewords, device=self.device, dtype=f32)
+        self.rng = torch.empty(n_seq, heads, q_len, 4, device=self.device, dtype=f32)
+        self.sl_idx = torch.empty(items, shortlist, device=self.device, dtype=i32)
+        self.sl_rank = torch.empty(items, shortlist, device=self.device, dtype=f32)
+        self.sl_count = torch.empty(items, device=self.device, dtype=i32)
+        self.fin_idx = torch.empty(items, budget, device=self.device, dtype=i32)
+        self.fin_count = torch.empty(items, device=self.device, dtype=i32)
+        self._lib = lib()
+
+    def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,
+            mask=None):
+        n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
+        q = _as_query(q)
+        L = self._lib
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        check(L.sva_query_lut(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), n_seq, heads, q_len,
+                              head_dim, rank, subspaces, codewords, q_proj.data_ptr(), scale.data_ptr(),
+                              codebooks.data_ptr(), codes.data_ptr(), code_type(codes), codes.stride(0), n_keys,
+                              shortlist, self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), stream),
+              "sva_query_lut")
+        m, mtype, mstride = mask_args(mask, q_len, n_keys)
+        ws_bytes = int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
+        ws = workspace(self.device, ws_bytes)
+        check(L.sva_summon(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(), codes.data_ptr(),
+                           code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), None, None, n_seq,
+                           heads, q_len, n_keys, rank, subspaces, codewords, shortlist, ptr(m), mtype, mstride,
+                           self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(), ws.data_ptr(),
+                           ws.numel(), stream), "sva_summon")
+        check(L.sva_budget_select(self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(),
+                                  n_seq * heads * q_len, shortlist, budget, self.fin_idx.data_ptr(),
+                                  self.fin_count.data_ptr(), stream), "sva_budget_select")
+        if out is None:
+            out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
+        vws = workspace(self.device, int(L.sva_verify_workspace_bytes(n_seq, heads, keys.shape[0], q_len, head_dim,
+                                                                        budget)), "verify")
+        check(L.sva_verify(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), keys.data_ptr(),
+                           values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1), None, None, n_keys,
+                           self.fin_idx.data_ptr(), self.fin_count.data_ptr(), n_seq, heads, keys.shape[0], q_len,
+                           head_dim, budget, float(scaling), out.data_ptr(), dtype_code(out), out.stride(0),
+                           out.stride(1), out.stride(2), vws.data_ptr(), vws.numel(), stream), "sva_verify")
+        return out

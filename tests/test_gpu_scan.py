@@ -56,9 +56,10 @@ def _check_case(case, res, shortlist, budget, allowed=None, tol=1e-5):
             table = oracle.lut(q_low[h, t], case.codebooks[h])
             np.testing.assert_array_equal(res["lut"][h, t].view(np.uint32), table.view(np.uint32))
             scores = oracle.pq_scores_from_lut(table, case.codes[h], case.R)
-            lo, hi = res["range"][h, t]
+            sums = oracle.pq_scores_from_lut(table, case.codes[h], 1)  # before the 1/sqrt(R) scale
+            lo, hi = res["range"][h, t, :2]
             al = np.ones(case.N, bool) if allowed is None else allowed[t]
-            assert scores[al].min() >= lo and scores[al].max() <= hi
+            assert sums.min() >= lo and sums.max() <= hi
             sl = oracle.topk(scores, shortlist, allowed=al)
             count = int(res["sl_count"][item])
             assert count == len(sl)

@@ -1,4 +1,4 @@
-"""GPU parity of the long-context q=1 summon (wide cooperative path).
+"""GPU parity of the long-context q=1 summon (many workgroups per query item).
 
 Shortlists over caches of 64K..1M keys are compared as SETS, bit-exact, with
 the oracle's top-L on the same LUT (selection rule: score desc, key index
@@ -32,9 +32,10 @@ def _setup(device, N, S, C, H=9, R=64, seed=0, few=False):
 def _summon(device, codes, k_low, q, q_proj, scale, cb, L, mask=None):
     from sva_amd import kernels
 
-    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q).to(device), torch.from_numpy(q_proj).to(device),
-                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device))
     codes_t = torch.from_numpy(codes).to(device)
+    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q).to(device), torch.from_numpy(q_proj).to(device),
+                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device),
+                                        codes_t, codes.shape[1], L)
     sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes_t, k_low, codes.shape[1], L, mask=mask)
     torch.cuda.synchronize()
     return q_low[0, :, 0].cpu().numpy(), lut[0, :, 0].cpu().numpy(), sl_idx.cpu().numpy(), sl_rank.cpu().numpy(), \
@@ -109,10 +110,40 @@ def test_wide_agrees_with_item_path(device):
 
 def test_wide_workspace_shared_across_shapes(device):
     # Regression: calls of different cache lengths and head counts share one
-    # workspace; the per-item histograms and counters live at fixed offsets
-    # and every call leaves them zero, whatever the tie buffers held before.
+    # workspace, whatever earlier calls left in it.
     for N, S, C, H, few in ((150000, 2, 256, 9, True), (50000, 4, 64, 3, False), (33000, 4, 64, 9, False),
                             (150000, 2, 256, 9, True), (40000, 4, 64, 9, False)):
         codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=N % 13, few=few)
         res = _summon(device, codes, k_low, q, q_proj, scale, cb, 1024)
         _check(codes, k_low, *res, 1024)
+
+
+def test_wide_sampled_floor_overshoot(device):
+    # The threshold estimate samples 16 blocks of 128 keys spread evenly over
+    # the cache (block starts rounded down to 16 keys).  Giving exactly those
+    # keys the best code of every subspace puts the estimate at the top of
+    # the score range, so fewer than L keys reach it and the exact all-keys
+    # selection must take over; with L equal to the sample size the rigged
+    # keys alone fill the shortlist.
+    N, S, C, H = 100000, 4, 64, 3
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=19)
+    ql = oracle.query_low(q, q_proj, scale)[:, 0]
+    for h in range(H):
+        best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
+        for blk in range(16):
+            n0 = (blk * (N - 128) // 15) & ~15
+            codes[h, n0:n0 + 128] = best
+    for L in (3000, 2048):
+        res = _summon(device, codes, k_low, q, q_proj, scale, cb, L)
+        _check(codes, k_low, *res, L)
+
+
+def test_wide_candidates_beyond_lds_stage(device):
+    # 3 codewords over 2 subspaces at 1M keys: the top score class holds
+    # ~1/9 of the keys, far more candidates than the select kernel stages in
+    # LDS; the selection runs over the per-wave lists and ties resolve by
+    # key index.
+    N, S, C, H = 1048576, 2, 256, 3
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=23, few=True)
+    res = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)
+    _check(codes, k_low, *res, 2048)
