@@ -47,6 +47,10 @@ def parse_args():
     ap.add_argument("--cpu-repeats", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=17)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
+    ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
+                    help="summarize rocprofv3 outputs of this benchmark into profiles/ and exit")
     return ap.parse_args()
 
 
@@ -127,8 +131,93 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
     }
 
 
+# kernels of one decode lookup, by entry point
+SUMMON_KERNELS = ("wide_scan_kernel", "wide_select_kernel", "wide_rescore_kernel")
+PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_partial_kernel",
+                                                         "verify_combine_kernel")
+PROFILE_STEM = "sva_summon_decode_1m_{layout}"
+
+
+def _kernel_key(name):
+    for k in PATH_KERNELS + ("__amd_rocclr_copyBuffer",):
+        if k in name:
+            return k
+    return None
+
+
+def write_profiles(args):
+    """Summarize a --kernel-trace --stats run and two --pmc runs (FETCH_SIZE,
+    WRITE_SIZE) of this benchmark into profiles/: per-kernel durations, HBM
+    bytes per dispatch scaled by the same counters' reading of a device copy
+    of known size, and the traffic figure the roofline reports."""
+
+    import csv
+
+    stats_csv, fetch_csv, write_csv = args.write_profiles
+    stem = PROFILE_STEM.format(layout=args.layout)
+    out_dir = ROOT / "profiles"
+    out_dir.mkdir(exist_ok=True)
+    rows = {}
+    with open(stats_csv) as f:
+        for r in csv.DictReader(f):
+            k = _kernel_key(r["Name"])
+            if k in PATH_KERNELS:
+                rows[k] = (int(r["Calls"]), float(r["AverageNs"]), float(r["MinNs"]), float(r["MaxNs"]))
+    counters = {}
+    for path in (fetch_csv, write_csv):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                k = _kernel_key(r["Kernel_Name"])
+                if k is not None:
+                    counters.setdefault((k, r["Counter_Name"]), []).append(float(r["Counter_Value"]))
+    avg = {key: sum(v) / len(v) for key, v in counters.items()}
+    copy_kib = float(args.calibrate_copy << 10)
+    fetch_scale = copy_kib / avg[("__amd_rocclr_copyBuffer", "FETCH_SIZE")]
+    write_scale = copy_kib / avg[("__amd_rocclr_copyBuffer", "WRITE_SIZE")]
+    cmd_trace = (f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o ks -- python bench.py --steps 300 "
+                 f"--warmup 50 --no-cpu-baseline --calibrate-copy {args.calibrate_copy} --layout {args.layout}")
+    cmd_pmc = (f"rocprofv3 --pmc {{FETCH_SIZE|WRITE_SIZE}} --output-format csv -d OUT -o pf -- python bench.py "
+               f"--steps 20 --warmup 5 --no-cpu-baseline --calibrate-copy {args.calibrate_copy} --layout {args.layout}")
+    lines = [f"# Kernel durations: decode lookup at 1M keys, {args.layout} codes, L/B 2048/512, q=1, 9 q-heads / 3 KV heads",
+             "", f"Command: `{cmd_trace}` (file `ks_kernel_stats.csv`).", "",
+             "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    total = 0.0
+    for k in PATH_KERNELS:
+        if k in rows:
+            c, a, mn, mx = rows[k]
+            total += a
+            lines.append(f"| {k} | {c} | {a / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |")
+    lines += [f"| **sum per lookup** | | {total / 1e3:.2f} | | |", ""]
+    (out_dir / f"{stem}_kernel_trace.md").write_text("\n".join(lines))
+    summon_bytes = 0.0
+    lines = [f"# HBM traffic per dispatch: decode lookup at 1M keys, {args.layout} codes", "",
+             f"Commands: `{cmd_pmc}`, one run per counter.", "",
+             f"Calibration: the {args.calibrate_copy} MiB device copy (`__amd_rocclr_copyBuffer`) reads "
+             f"FETCH_SIZE {avg[('__amd_rocclr_copyBuffer', 'FETCH_SIZE')]:.0f} KiB and WRITE_SIZE "
+             f"{avg[('__amd_rocclr_copyBuffer', 'WRITE_SIZE')]:.0f} KiB for {copy_kib:.0f} KiB moved each way: "
+             f"scale factors {fetch_scale:.3f} (fetch) and {write_scale:.3f} (write).", "",
+             "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) |", "|---|---:|---:|---:|"]
+    for k in PATH_KERNELS:
+        fk, wk = avg.get((k, "FETCH_SIZE")), avg.get((k, "WRITE_SIZE"))
+        if fk is None or wk is None:
+            continue
+        b = 1024.0 * (fk * fetch_scale + wk * write_scale)
+        if k in SUMMON_KERNELS:
+            summon_bytes += b
+        lines.append(f"| {k} | {fk:.1f} | {wk:.1f} | {b:,.0f} |")
+    lines += ["", f"sva_summon (the three wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
+    (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
+    (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
+        {"entry_point": "sva_summon", "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
+         "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}) + "\n")
+    print(f"wrote profiles/{stem}_*.md/json")
+
+
 def main():
     args = parse_args()
+    if args.write_profiles:
+        write_profiles(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "
                                    "sequence (see DESIGN.md) but no multi-GPU figure is produced",
@@ -172,6 +261,14 @@ def main():
         kernels.verify(layer.q, layer.keys, layer.values, fin_idx, fin_count, n, scaling)
         ev[4].record()
 
+    if args.calibrate_copy:
+        src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -205,7 +302,7 @@ def main():
     summon_us = per_stage_us["summon"]
     achieved = bytes_["summon"] / (summon_us * 1e-6) / 1e9
     traffic = None
-    pmc = ROOT / "profiles" / f"summon_wide_{args.layout}_1m_pmc.json"
+    pmc = ROOT / "profiles" / (PROFILE_STEM.format(layout=args.layout) + "_traffic.json")
     if pmc.exists() and n == 1_048_576:
         try:
             traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
@@ -235,7 +332,8 @@ def main():
         "gpu_us_per_query": round(gpu_us, 2),
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "summon_wide_kernel" if strategy == 1 else "summon_item_kernel",
+            "kernel": ("sva_summon: wide_scan + wide_select + wide_rescore" if strategy == 1
+                       else "sva_summon: summon_item_kernel"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
