@@ -150,6 +150,77 @@ SVA_DEV uint32_t block_excl_scan(uint32_t v, uint32_t* scratch, uint32_t* total)
 }
 
 // ---------------------------------------------------------------------------
+// Exact selection of the k largest nonzero composites among the elements a
+// visitor yields (each element exactly once per call, unique values): radix
+// passes of up to 8 bits from the highest bit where elements differ, with
+// one LDS histogram per wave.  Returns X such that the selected elements are
+// exactly those >= X.  Every thread of the block must call it.  whist: BLOCK/64
+// rows of 256 uint32; scratch: block_excl_scan scratch; shared64: 2 uint64;
+// shared: 3 uint32 (all LDS).  BLOCK >= 256.
+template <int BLOCK, typename Visit>
+SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint32_t* scratch, uint64_t* shared64,
+                                uint32_t* shared) {
+  const int wid = threadIdx.x / WAVE;
+  // bits above the highest differing bit are common to every element
+  uint64_t vor = 0ull, vand = ~0ull;
+  visit([&](uint64_t x) {
+    vor |= x;
+    vand &= x;
+  });
+  for (int off = 1; off < WAVE; off <<= 1) {
+    vor |= __shfl_xor(vor, off, WAVE);
+    vand &= __shfl_xor(vand, off, WAVE);
+  }
+  if (threadIdx.x == 0) {
+    shared64[0] = 0ull;
+    shared64[1] = ~0ull;
+  }
+  __syncthreads();
+  if (lane_id() == 0) {
+    atomicOr((unsigned long long*)&shared64[0], (unsigned long long)vor);
+    atomicAnd((unsigned long long*)&shared64[1], (unsigned long long)vand);
+  }
+  __syncthreads();
+  const uint64_t diff = shared64[0] ^ shared64[1];
+  if (diff == 0ull) return shared64[0];  // a single element
+  int top = 63 - __clzll((long long)diff);
+  uint64_t pmask = top == 63 ? 0ull : ~0ull << (top + 1);
+  uint64_t prefix = shared64[1] & pmask;
+  int need = k;
+  while (true) {
+    const int shift = max(top - 7, 0);
+    const uint32_t dmask = (1u << (top - shift + 1)) - 1u;
+    for (int i = threadIdx.x; i < (BLOCK / WAVE) * 256; i += BLOCK) whist[i >> 8][i & 255] = 0u;
+    __syncthreads();
+    visit([&](uint64_t x) {
+      if ((x & pmask) == prefix) atomicAdd(&whist[wid][(uint32_t)(x >> shift) & dmask], 1u);
+    });
+    __syncthreads();
+    uint32_t tot = 0;
+    if (threadIdx.x < 256) {
+      const int b = 255 - (int)threadIdx.x;  // bins from the top
+      for (int v = 0; v < BLOCK / WAVE; ++v) tot += whist[v][b];
+    }
+    uint32_t total;
+    const uint32_t above = block_excl_scan<BLOCK>(tot, scratch, &total);
+    if (threadIdx.x < 256 && above < (uint32_t)need && above + tot >= (uint32_t)need) {
+      shared[0] = 255u - threadIdx.x;
+      shared[1] = above;
+      shared[2] = tot;
+    }
+    __syncthreads();
+    const uint32_t b = shared[0];
+    need -= (int)shared[1];
+    prefix |= (uint64_t)b << shift;
+    pmask |= (uint64_t)dmask << shift;
+    const bool done = shared[2] == (uint32_t)need || shift == 0;
+    __syncthreads();
+    if (done) return prefix;
+    top = shift - 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Radix select over uint32 keys.  Finds the threshold key T and k_eq such that
 // the k largest elements are: every element with key > T plus the k_eq
 // lowest-index elements with key == T.  Elements with key 0 never count.

@@ -1,10 +1,13 @@
 // Budget select: the exact top-B of each shortlist by (rank score desc, key
 // index asc), written as ascending key indices (sva/llama.py:293-302).
 //
-// One workgroup per query item.  The shortlist is loaded into LDS as unique
-// 64-bit composites, a radix select finds the B-th largest composite X, the
-// entries >= X are compacted and sorted by key index (bitonic, LDS) so that
-// the output does not depend on the shortlist's order.
+// One workgroup per query item.  All L shortlist slots are loaded at once
+// (slots past the count are ignored) as unique 64-bit composites (rank key,
+// key index) into LDS; a radix select with per-wave histograms finds the
+// B-th largest composite X; the entries >= X are compacted in shortlist order
+// and each is stored at its rank among the selected key indices, so the
+// output is ascending whatever the shortlist's order.  Shortlist key indices
+// are unique (every summon path guarantees it).
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -13,46 +16,62 @@ using namespace sva;
 
 namespace {
 
-constexpr int SEL_BLOCK = 512;
+constexpr int SEL_BLOCK = 1024;
+constexpr int SEL_NW = SEL_BLOCK / WAVE;
 
 __global__ void __launch_bounds__(SEL_BLOCK)
     budget_select_kernel(const int32_t* __restrict__ sl_idx, const float* __restrict__ sl_rank,
-                         const int32_t* __restrict__ sl_count, int L, int B, int P, int32_t* __restrict__ fin_idx,
+                         const int32_t* __restrict__ sl_count, int L, int B, int32_t* __restrict__ fin_idx,
                          int32_t* __restrict__ fin_count) {
   extern __shared__ __align__(16) unsigned char lds[];
-  uint64_t* comp = (uint64_t*)lds;       // [L]
-  uint64_t* sel = comp + L;              // [P] (P = next pow2 of B)
-  uint32_t* hist = (uint32_t*)(sel + P);  // [256]
-  uint32_t* scratch = hist + 256;         // [SEL_BLOCK/64 + 1]
-  uint32_t* shared = scratch + SEL_BLOCK / WAVE + 1;  // [4]
+  uint64_t* comp = (uint64_t*)lds;                             // [L]
+  uint32_t* sel = (uint32_t*)(comp + ((L + 1) & ~1));          // [B] selected key indices, 16-byte aligned
+  uint32_t(*whist)[256] = (uint32_t(*)[256])(sel + ((B + 3) & ~3));  // [SEL_NW][256]
+  uint64_t* shared64 = (uint64_t*)(whist + SEL_NW);            // [2]
+  uint32_t* scratch = (uint32_t*)(shared64 + 2);               // [SEL_NW + 1]
+  uint32_t* shared = scratch + SEL_NW + 1;                     // [4]
   const int item = blockIdx.x;
-  const int n = min(sl_count[item], L);
-  const int beff = min(B, n);
-  if (beff <= 0) {
-    if (threadIdx.x == 0) fin_count[item] = 0;
-    return;
-  }
   const int32_t* idx = sl_idx + (int64_t)item * L;
   const float* rank = sl_rank + (int64_t)item * L;
-  for (int i = threadIdx.x; i < n; i += SEL_BLOCK) comp[i] = composite(f2key(rank[i]), (uint32_t)idx[i]);
-  if (threadIdx.x == 0) shared[2] = 0;
+  const int n = max(0, min(sl_count[item], L));
+  for (int i = threadIdx.x; i < L; i += SEL_BLOCK) {
+    const float r = rank[i];
+    const int32_t x = idx[i];
+    comp[i] = composite(f2key(r), (uint32_t)x);
+  }
+  const int beff = min(B, n);
+  if (threadIdx.x == 0) fin_count[item] = beff;
+  if (beff <= 0) return;
   __syncthreads();
-  uint64_t X = 0;
-  if (beff < n) X = radix_select_u64<SEL_BLOCK>([&](int i) { return comp[i]; }, n, beff, hist, scratch, shared);
-  for (int i = threadIdx.x; i < n; i += SEL_BLOCK) {
+  auto visit = [&](auto&& f) {
+    for (int i = threadIdx.x; i < n; i += SEL_BLOCK) f(comp[i]);
+  };
+  const uint64_t X = beff == n ? 0ull : select_largest<SEL_BLOCK>(visit, beff, whist, scratch, shared64, shared);
+  // compact the selected in shortlist order: contiguous ranges per thread
+  const int per = (n + SEL_BLOCK - 1) / SEL_BLOCK;
+  const int i0 = min(n, (int)threadIdx.x * per), i1 = min(n, i0 + per);
+  uint32_t cnt = 0;
+  for (int i = i0; i < i1; ++i) cnt += comp[i] >= X;
+  uint32_t tot;
+  uint32_t o = block_excl_scan<SEL_BLOCK>(cnt, scratch, &tot);
+  for (int i = i0; i < i1; ++i) {
     const uint64_t c = comp[i];
-    if (c >= X) {
-      const uint32_t j = atomicAdd(&shared[2], 1u);
-      if (j < (uint32_t)P) sel[j] = ((uint64_t)composite_index(c) << 32) | (uint64_t)composite_key(c);
-    }
+    if (c >= X && o < (uint32_t)beff) sel[o++] = composite_index(c);
   }
   __syncthreads();
-  for (int i = beff + threadIdx.x; i < P; i += SEL_BLOCK) sel[i] = ~0ull;
-  __syncthreads();
-  bitonic_sort_u64<SEL_BLOCK>(sel, P, false);
+  // ascending order: each selected index goes to its rank among the selected
   int32_t* out = fin_idx + (int64_t)item * B;
-  for (int i = threadIdx.x; i < beff; i += SEL_BLOCK) out[i] = (int32_t)(sel[i] >> 32);
-  if (threadIdx.x == 0) fin_count[item] = beff;
+  for (int i = threadIdx.x; i < beff; i += SEL_BLOCK) {
+    const uint32_t v = sel[i];
+    int r = 0;
+    int j = 0;
+    for (; j + 4 <= beff; j += 4) {
+      const uint4 u = *reinterpret_cast<const uint4*>(sel + j);
+      r += (u.x < v) + (u.y < v) + (u.z < v) + (u.w < v);
+    }
+    for (; j < beff; ++j) r += sel[j] < v;
+    out[r] = (int32_t)v;
+  }
 }
 
 }  // namespace
@@ -65,8 +84,8 @@ extern "C" int sva_budget_select(const int32_t* sl_idx, const float* sl_rank, co
   SVA_REQUIRE(n_items > 0 && n_items < (1ll << 31), "sva_budget_select: bad item count");
   SVA_REQUIRE(L > 0 && L <= 16384 && B > 0 && B <= 8192, "sva_budget_select: shortlist %lld / budget %lld out of range",
               (long long)L, (long long)B);
-  const int P = sva::next_pow2_host((int)B);
-  const size_t lds = sizeof(uint64_t) * ((size_t)L + (size_t)P) + sizeof(uint32_t) * (256 + SEL_BLOCK / 64 + 1 + 4);
+  const size_t lds = sizeof(uint64_t) * ((size_t)((L + 1) & ~1) + 2) + sizeof(uint32_t) * ((size_t)((B + 3) & ~3) + SEL_NW * 256 +
+                                                                              SEL_NW + 1 + 4);
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_budget_select: shortlist %lld + budget %lld exceed LDS",
                   (long long)L, (long long)B);
   static bool attr_set = false;
@@ -77,7 +96,7 @@ extern "C" int sva_budget_select(const int32_t* sl_idx, const float* sl_rank, co
     attr_set = true;
   }
   hipLaunchKernelGGL(budget_select_kernel, dim3((unsigned)n_items), dim3(SEL_BLOCK), lds, (hipStream_t)stream, sl_idx,
-                     sl_rank, sl_count, (int)L, (int)B, P, fin_idx, fin_count);
+                     sl_rank, sl_count, (int)L, (int)B, fin_idx, fin_count);
   SVA_CHECK_LAUNCH("budget_select_kernel");
   return SVA_OK;
 }

@@ -1,16 +1,18 @@
 // Exact verifier, GQA-aware (sva/llama.py:304-317 and :532-553).
 //
-// verify_partial: one workgroup per (sequence, KV head g, token, split).  The
+// verify_part: one workgroup per (sequence, KV head g, token, slice).  The
 // budget lists of the H/G query heads sharing g (ascending key indices) are
-// read into LDS and concatenated in (head, position) order; split s takes an
-// equal slice of that concatenation.  An entry is processed only by the slice
-// holding its first occurrence (the lowest head whose list contains the key),
-// so every selected K row and V row is read from HBM once per group and is
-// scored against every query head whose list holds it.  Scores are fp32
-// dot(K[n], q_h) * scaling; each split keeps, per head, the running maximum
-// m, the sum z of exp(score - m) and the exp-weighted V sum.
-// verify_combine: one workgroup per query item merges the splits
-// (max-rescaled sums) and stores acc / z in the output dtype.
+// staged in LDS; their concatenation in (head, position) order is cut into
+// slices of at most EPW entries.  An entry is processed only by the slice
+// holding its first occurrence (the lowest head whose list contains the key,
+// found by binary search), so every selected K row and V row is read from HBM
+// once per group and scored against every query head whose list holds it.
+// Every global load of a phase is issued before any is used: the lists, the
+// query rows and the counts together, then every K and V row of the slice.
+// Scores are fp32 dot(K[n], q_h) * scaling; per head the slice keeps the
+// maximum m, the sum z of exp(score - m) and the exp-weighted V sum.
+// verify_combine: one workgroup per query item merges the slices (all loaded
+// at once, max-rescaled sums) and stores acc / z in the output dtype.
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -19,10 +21,11 @@ using namespace sva;
 
 namespace {
 
-constexpr int VB = 256;            // threads per partial workgroup
-constexpr int ROWS_PER_WG = 32;    // union entries per split (2 passes of 16 rows)
+constexpr int VB = 256;   // threads per part workgroup: 4 lanes per entry
+constexpr int EPW = VB / 4;  // union entries per slice
 constexpr int MAX_GRP = 8;
 constexpr int MAX_D = 256;
+constexpr int CB = 256;   // threads per combine workgroup
 
 SVA_DEV int bsearch_i32(const int32_t* a, int n, int32_t x) {
   int lo = 0, hi = n;
@@ -42,6 +45,7 @@ struct VerifyParams {
   const void* values;
   int kv_dtype;
   int64_t kv_hs, kv_rs;
+  bool kv_vec;  // rows start 8-byte (half types) / 16-byte (fp32) aligned: 4-element vector loads
   const int64_t* offs;
   const int64_t* lens;
   int64_t N;
@@ -55,143 +59,168 @@ struct VerifyParams {
   int64_t o_bs, o_hs, o_ts;
 };
 
-__global__ void __launch_bounds__(VB) verify_partial_kernel(VerifyParams p) {
+// Four consecutive elements of a K/V row as floats.
+SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[4]) {
+  if (vec) {
+    if (dtype == F32) {
+      const float4 x = *reinterpret_cast<const float4*>((const float*)base + e);
+      v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+      return;
+    }
+    const uint2 x = *reinterpret_cast<const uint2*>((const uint16_t*)base + e);
+    if (dtype == BF16) {
+      v[0] = __uint_as_float(x.x << 16), v[1] = __uint_as_float(x.x & 0xFFFF0000u);
+      v[2] = __uint_as_float(x.y << 16), v[3] = __uint_as_float(x.y & 0xFFFF0000u);
+    } else {
+      v[0] = __half2float(__ushort_as_half((unsigned short)(x.x & 0xFFFFu)));
+      v[1] = __half2float(__ushort_as_half((unsigned short)(x.x >> 16)));
+      v[2] = __half2float(__ushort_as_half((unsigned short)(x.y & 0xFFFFu)));
+      v[3] = __half2float(__ushort_as_half((unsigned short)(x.y >> 16)));
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = load_elem(base, e + k, dtype);
+}
+
+// DT: compile-time head_dim (0: runtime p.D).  Each of the 4 lanes of an
+// entry holds D/4 consecutive dimensions of its K and V rows.
+template <int DT>
+__global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
+#pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
+  const int D = DT > 0 ? DT : p.D;
   const int grp = p.H / p.G;
-  const int s = blockIdx.x % p.split;
-  const int gi = blockIdx.x / p.split;
+  const int s = blockIdx.x;
+  const int gi = blockIdx.y;
   const int t = gi % p.Q;
   const int g = (gi / p.Q) % p.G;
   const int b = gi / (p.Q * p.G);
-  const int B = p.B, D = p.D;
-  int32_t* lists = (int32_t*)lds;                    // [grp][B]
-  float* qv = (float*)(lists + grp * B);             // [grp][D]
-  float* vrow = qv + grp * D;                        // [ROWS_PER_WG][D]
-  float* sc = vrow + ROWS_PER_WG * D;                // [ROWS_PER_WG][grp]
-  int32_t* rkey = (int32_t*)(sc + ROWS_PER_WG * grp);  // [ROWS_PER_WG]
-  int32_t* rpos = rkey + ROWS_PER_WG;                // [ROWS_PER_WG][grp]
-  int* cnt = rpos + ROWS_PER_WG * grp;               // [MAX_GRP + 1] (prefix)
-  float* stat = (float*)(cnt + MAX_GRP + 1);         // [grp][2]
-  int* nrows = (int*)(stat + 2 * MAX_GRP);
+  const int B = p.B;
+  int32_t* lists = (int32_t*)lds;                     // [grp][B]
+  float* qv = (float*)(lists + grp * B);              // [grp][D]
+  float* vrow = qv + grp * D;                         // [EPW][D]
+  float* wt = vrow + EPW * D;                         // [EPW][MAX_GRP] scores, then weights
+  int32_t* ekey = (int32_t*)(wt + EPW * MAX_GRP);     // [EPW]
+  uint32_t* emem = (uint32_t*)(ekey + EPW);           // [EPW] heads whose list holds the entry
+  int* cnt = (int*)(emem + EPW);                      // [MAX_GRP + 1] prefix of list lengths
+  float* stat = (float*)(cnt + MAX_GRP + 1);          // [MAX_GRP][2]
 
   const int64_t len = p.lens ? p.lens[b] : p.N;
   const int64_t off = p.offs ? p.offs[b] : 0;
+  const int64_t item0 = ((int64_t)b * p.H + (int64_t)g * grp) * p.Q + t;  // head j: item0 + j * Q
+  // phase 1: counts, lists (all B slots) and query rows in one round of loads
+  if ((int)threadIdx.x < grp) cnt[threadIdx.x + 1] = max(0, min(p.fin_count[item0 + threadIdx.x * p.Q], B));
+  for (int e = threadIdx.x; e < grp * B; e += VB) {
+    const int j = e / B;
+    lists[e] = p.fin_idx[(item0 + (int64_t)j * p.Q) * B + (e - j * B)];
+  }
+  for (int e = threadIdx.x; e < grp * D; e += VB) {
+    const int j = e / D;
+    const int64_t qb = (int64_t)b * p.q_bs + (int64_t)(g * grp + j) * p.q_hs + (int64_t)t * p.q_ts;
+    qv[e] = load_elem(p.q, qb + (e - j * D), p.q_dtype);
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int j = 0; j < grp; ++j) {
-      const int64_t item = ((int64_t)b * p.H + g * grp + j) * p.Q + t;
-      cnt[j] = acc;
-      acc += max(0, min(p.fin_count[item], B));
-    }
-    cnt[grp] = acc;
+    cnt[0] = 0;
+    for (int j = 0; j < grp; ++j) cnt[j + 1] += cnt[j];
   }
   __syncthreads();
-  for (int j = 0; j < grp; ++j) {
-    const int h = g * grp + j;
-    const int64_t item = ((int64_t)b * p.H + h) * p.Q + t;
-    const int c = cnt[j + 1] - cnt[j];
-    const int32_t* src = p.fin_idx + item * B;
-    for (int i = threadIdx.x; i < c; i += VB) {
-      int32_t x = src[i];
-      x = x < 0 ? 0 : (x >= len ? (int32_t)(len - 1) : x);
-      lists[j * B + i] = x;
-    }
-    const int64_t qb = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs + (int64_t)t * p.q_ts;
-    for (int d = threadIdx.x; d < D; d += VB) qv[j * D + d] = load_elem(p.q, qb + d, p.q_dtype);
-  }
-  __syncthreads();
-
-  // this split's slice of the concatenated lists; keep first occurrences
   const int M = cnt[grp];
   const int e0 = (int)((int64_t)s * M / p.split);
-  const int e1 = (int)((int64_t)(s + 1) * M / p.split);
-  if (threadIdx.x < WAVE) {
-    const int e = e0 + (int)threadIdx.x;
-    bool own = false;
-    int j = 0, i = 0;
+  const int n = (int)((int64_t)(s + 1) * M / p.split) - e0;  // <= EPW
+  // phase 2: first occurrences of the slice and the heads holding each
+  if ((int)threadIdx.x < EPW) {
+    const int r = threadIdx.x;
+    uint32_t mem = 0u;
     int32_t x = 0;
-    if (e < e1) {
+    if (r < n) {
+      const int e = e0 + r;
+      int j = 0;
       while (j + 1 < grp && e >= cnt[j + 1]) ++j;
-      i = e - cnt[j];
-      x = lists[j * B + i];
-      own = true;
-      for (int jj = 0; jj < j && own; ++jj)
-        if (bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) >= 0) own = false;
-    }
-    const uint64_t bal = __ballot(own);
-    const int r = (int)__popcll(bal & ((1ull << lane_id()) - 1ull));
-    if (own && r < ROWS_PER_WG) {
-      rkey[r] = x;
-      for (int jj = 0; jj < grp; ++jj)
-        rpos[r * grp + jj] = jj < j ? -1 : (jj == j ? i : bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x));
-    }
-    if (threadIdx.x == 0) *nrows = min((int)__popcll(bal), ROWS_PER_WG);
-  }
-  __syncthreads();
-  const int n = *nrows;
-
-  // scores: 16 lanes per row, each lane a D/16 slice; V slice kept in LDS
-  const int grp16 = threadIdx.x >> 4;  // 16 row slots per pass
-  const int l16 = threadIdx.x & 15;
-  const int per = D / 16;
-  const char* kb = (const char*)p.keys;
-  const char* vb = (const char*)p.values;
-  const int64_t kv_head = (int64_t)g * p.kv_hs;
-  for (int r0 = 0; r0 < n; r0 += VB / 16) {
-    const int r = r0 + grp16;
-    const bool valid = r < n;
-    const int64_t row = off + (valid ? rkey[r] : rkey[0]);
-    float kr[MAX_D / 16], vr[MAX_D / 16];
-#pragma unroll
-    for (int k = 0; k < MAX_D / 16; ++k) {
-      if (k < per) {
-        const int64_t e = kv_head + row * p.kv_rs + l16 * per + k;
-        kr[k] = load_elem(kb, e, p.kv_dtype);
-        vr[k] = load_elem(vb, e, p.kv_dtype);
+      x = lists[j * B + (e - cnt[j])];
+      if (x >= 0 && (int64_t)x < len) {
+        bool own = true;
+        for (int jj = 0; jj < j && own; ++jj) own = bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) < 0;
+        if (own) {
+          mem = 1u << j;
+          for (int jj = j + 1; jj < grp; ++jj)
+            if (bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) >= 0) mem |= 1u << jj;
+        }
       }
     }
-    for (int j = 0; j < grp; ++j) {
-      float part = 0.0f;
-#pragma unroll
-      for (int k = 0; k < MAX_D / 16; ++k)
-        if (k < per) part += kr[k] * qv[j * D + l16 * per + k];
-      for (int o = 8; o > 0; o >>= 1) part += __shfl_xor(part, o, 16);
-      if (valid && l16 == 0) sc[r * grp + j] = part * p.scaling;
-    }
-    if (valid) {
-#pragma unroll
-      for (int k = 0; k < MAX_D / 16; ++k)
-        if (k < per) vrow[r * D + l16 * per + k] = vr[k];
-    }
+    ekey[r] = x;
+    emem[r] = mem;
   }
   __syncthreads();
-
-  // per-head max and exp-sum over this split's rows (fixed order)
-  if ((int)threadIdx.x < grp) {
-    const int j = threadIdx.x;
-    float m = -INFINITY;
-    for (int r = 0; r < n; ++r)
-      if (rpos[r * grp + j] >= 0) m = fmaxf(m, sc[r * grp + j]);
-    float z = 0.0f;
-    for (int r = 0; r < n; ++r) {
-      if (rpos[r * grp + j] >= 0) {
-        const float w = expf(sc[r * grp + j] - m);
-        sc[r * grp + j] = w;
-        z += w;
-      } else {
-        sc[r * grp + j] = 0.0f;
+  // phase 3: every K and V row of the slice, 4 lanes per row
+  {
+    const int r = threadIdx.x >> 2;
+    const int qt = threadIdx.x & 3;
+    const uint32_t mem = emem[r];
+    const int dq = D / 4;
+    float dot[MAX_GRP];
+#pragma unroll
+    for (int j = 0; j < MAX_GRP; ++j) dot[j] = 0.0f;
+    if (mem != 0u) {
+      const int64_t rowe = (int64_t)g * p.kv_hs + (off + ekey[r]) * p.kv_rs + qt * dq;
+      constexpr int NCH = (DT > 0 ? DT : MAX_D) / 16;  // 4-element chunks per lane
+      float kv[NCH][4], vv[NCH][4];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (DT > 0 || 4 * c < dq) {
+          load4(p.keys, rowe + 4 * c, p.kv_dtype, p.kv_vec, kv[c]);
+          load4(p.values, rowe + 4 * c, p.kv_dtype, p.kv_vec, vv[c]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (DT > 0 || 4 * c < dq) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const int d = qt * dq + 4 * c + k;
+            vrow[r * D + d] = vv[c][k];
+#pragma unroll
+            for (int j = 0; j < MAX_GRP; ++j)
+              if (j < grp) dot[j] = __builtin_fmaf(kv[c][k], qv[j * D + d], dot[j]);
+          }
+        }
+      }
+    } else if (r < n) {
+      for (int d = qt * dq; d < (qt + 1) * dq; ++d) vrow[r * D + d] = 0.0f;  // weight 0 must not meet NaN
+    }
+#pragma unroll
+    for (int j = 0; j < MAX_GRP; ++j) {
+      if (j < grp) {
+        float v = dot[j];
+        v += __shfl_xor(v, 1, 4);
+        v += __shfl_xor(v, 2, 4);
+        if (qt == 0) wt[r * MAX_GRP + j] = ((mem >> j) & 1u) ? v * p.scaling : -INFINITY;
       }
     }
-    stat[2 * j] = m;
-    stat[2 * j + 1] = z;
   }
   __syncthreads();
+  // phase 4: per head, max and exp-sum over the slice (one wave per head)
+  const int wid = threadIdx.x / WAVE;
+  for (int j = wid; j < grp; j += VB / WAVE) {
+    const int r = lane_id();
+    const float sc = r < n ? wt[r * MAX_GRP + j] : -INFINITY;
+    const float m = wave_max(sc);
+    const float e = (m == -INFINITY || sc == -INFINITY) ? 0.0f : expf(sc - m);
+    wt[r * MAX_GRP + j] = e;
+    const float z = wave_sum(e);
+    if (r == 0) {
+      stat[2 * j] = m;
+      stat[2 * j + 1] = z;
+    }
+  }
+  __syncthreads();
+  // phase 5: exp-weighted V sums, one (head, dim) per thread
   for (int e = threadIdx.x; e < grp * D; e += VB) {
-    const int j = e / D, d = e % D;
+    const int j = e / D, d = e - j * D;
     float acc = 0.0f;
-    for (int r = 0; r < n; ++r) acc += sc[r * grp + j] * vrow[r * D + d];
-    const int64_t item = ((int64_t)b * p.H + g * grp + j) * p.Q + t;
-    float* dst = p.part + (item * p.split + s) * (D + 2);
+    for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * D + d];
+    float* dst = p.part + ((item0 + (int64_t)j * p.Q) * p.split + s) * (D + 2);
     dst[2 + d] = acc;
     if (d == 0) {
       dst[0] = stat[2 * j];
@@ -200,27 +229,52 @@ __global__ void __launch_bounds__(VB) verify_partial_kernel(VerifyParams p) {
   }
 }
 
-__global__ void __launch_bounds__(MAX_D) verify_combine_kernel(VerifyParams p) {
+__global__ void __launch_bounds__(CB) verify_combine_kernel(VerifyParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  float* fs = (float*)lds;  // [split] rescale factor of each slice
+  __shared__ float red[CB / WAVE];
   const int item = blockIdx.x;
   const int t = item % p.Q;
   const int h = (item / p.Q) % p.H;
   const int b = item / (p.Q * p.H);
   const int D = p.D;
-  const float* src = p.part + (int64_t)item * p.split * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < p.split; ++s) M = fmaxf(M, src[s * (D + 2)]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float z = 0.0f, acc = 0.0f;
-    if (M > -INFINITY) {
-      for (int s = 0; s < p.split; ++s) {
-        const float m = src[s * (D + 2)];
-        if (m == -INFINITY) continue;
-        const float f = expf(m - M);
-        z += src[s * (D + 2) + 1] * f;
-        acc += src[s * (D + 2) + 2 + d] * f;
-      }
+  const int split = p.split;
+  const float* src = p.part + (int64_t)item * split * (D + 2);
+  // maximum over slices
+  float m = -INFINITY;
+  for (int s = threadIdx.x; s < split; s += CB) m = fmaxf(m, src[(int64_t)s * (D + 2)]);
+  m = wave_max(m);
+  if (lane_id() == 0) red[threadIdx.x / WAVE] = m;
+  __syncthreads();
+  float M = red[0];
+  for (int w = 1; w < CB / WAVE; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  // per-slice factors and the total exp-sum
+  float z = 0.0f;
+  for (int s = threadIdx.x; s < split; s += CB) {
+    const float ms = src[(int64_t)s * (D + 2)];
+    const float f = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+    fs[s] = f;
+    z = z + f * src[(int64_t)s * (D + 2) + 1];
+  }
+  z = wave_sum(z);
+  if (lane_id() == 0) red[threadIdx.x / WAVE] = z;
+  __syncthreads();
+  float Z = 0.0f;
+  for (int w = 0; w < CB / WAVE; ++w) Z = Z + red[w];
+  for (int d = threadIdx.x; d < D; d += CB) {
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 8 <= split; s += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = src[(int64_t)(s + k) * (D + 2) + 2 + d];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc = acc + fs[s + k] * v[k];
     }
-    const float v = z > 0.0f ? acc / z : 0.0f;
+    for (; s < split; ++s) acc = acc + fs[s] * src[(int64_t)s * (D + 2) + 2 + d];
+    const float v = (M > -INFINITY && Z > 0.0f) ? acc / Z : 0.0f;
     const int64_t o = (int64_t)b * p.o_bs + (int64_t)h * p.o_hs + (int64_t)t * p.o_ts + d;
     store_elem(p.out, o, p.out_dtype, v);
   }
@@ -228,13 +282,27 @@ __global__ void __launch_bounds__(MAX_D) verify_combine_kernel(VerifyParams p) {
 
 int verify_split(int64_t grp, int64_t B) {
   const int64_t m = grp * B;
-  return (int)std::max<int64_t>(1, (m + ROWS_PER_WG - 1) / ROWS_PER_WG);
+  return (int)std::max<int64_t>(1, (m + EPW - 1) / EPW);
 }
 
 size_t verify_lds_bytes(int64_t grp, int64_t B, int64_t D) {
-  return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * ROWS_PER_WG * D +
-         sizeof(float) * ROWS_PER_WG * grp + sizeof(int32_t) * ROWS_PER_WG + sizeof(int32_t) * ROWS_PER_WG * grp +
-         sizeof(int) * (MAX_GRP + 1) + sizeof(float) * 2 * MAX_GRP + sizeof(int) + 16;
+  return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * EPW * D +
+         sizeof(float) * EPW * MAX_GRP + 2 * sizeof(int32_t) * EPW + sizeof(int) * (MAX_GRP + 1) +
+         sizeof(float) * 2 * MAX_GRP + 16;
+}
+
+template <int DT>
+int launch_part(const VerifyParams& p, dim3 grid, size_t lds, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)verify_part_kernel<DT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      sva::kMaxLds),
+                  "hipFuncSetAttribute(verify_part_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(verify_part_kernel<DT>, grid, dim3(VB), lds, stream, p);
+  SVA_CHECK_LAUNCH("verify_part_kernel");
+  return SVA_OK;
 }
 
 }  // namespace
@@ -268,15 +336,7 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   const size_t need = sva_verify_workspace_bytes(n_seq, H, G, Q, D, B);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need, "sva_verify: workspace of %zu bytes required", need);
   const int split = verify_split(grp, B);
-  const int64_t blocks = n_seq * G * Q * split;
-  SVA_REQUIRE(blocks < (1ll << 31), "sva_verify: too many items");
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)verify_partial_kernel,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
-                  "hipFuncSetAttribute(verify_partial_kernel)");
-    attr_set = true;
-  }
+  SVA_REQUIRE(n_seq * G * Q < (1ll << 31) && n_seq * H * Q < (1ll << 31), "sva_verify: too many items");
   VerifyParams p;
   p.q = q;
   p.q_dtype = q_dtype;
@@ -288,6 +348,9 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.kv_dtype = kv_dtype;
   p.kv_hs = kv_head_stride;
   p.kv_rs = kv_row_stride;
+  const uintptr_t kv_align = kv_dtype == 0 ? 15u : 7u;
+  p.kv_vec = (((uintptr_t)keys | (uintptr_t)values) & kv_align) == 0 && kv_head_stride % 4 == 0 &&
+             kv_row_stride % 4 == 0;
   p.offs = seq_offsets;
   p.lens = seq_lens;
   p.N = n_keys;
@@ -306,9 +369,14 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.o_bs = out_seq_stride;
   p.o_hs = out_head_stride;
   p.o_ts = out_tok_stride;
-  hipLaunchKernelGGL(verify_partial_kernel, dim3((unsigned)blocks), dim3(VB), lds, (hipStream_t)stream, p);
-  SVA_CHECK_LAUNCH("verify_partial_kernel");
-  hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(MAX_D), 0, (hipStream_t)stream, p);
+  const dim3 grid((unsigned)split, (unsigned)(n_seq * G * Q));
+  int rc = SVA_OK;
+  if (D == 64) rc = launch_part<64>(p, grid, lds, (hipStream_t)stream);
+  else if (D == 128) rc = launch_part<128>(p, grid, lds, (hipStream_t)stream);
+  else rc = launch_part<0>(p, grid, lds, (hipStream_t)stream);
+  if (rc != SVA_OK) return rc;
+  hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,
+                     (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("verify_combine_kernel");
   return SVA_OK;
 }
