@@ -133,7 +133,7 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 
 # kernels of one decode lookup, by entry point
 SUMMON_KERNELS = ("wide_scan_kernel", "wide_select_kernel", "wide_rescore_kernel")
-PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_partial_kernel",
+PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel",
                                                          "verify_combine_kernel")
 PROFILE_STEM = "sva_summon_decode_1m_{layout}"
 

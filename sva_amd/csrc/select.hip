@@ -59,18 +59,26 @@ __global__ void __launch_bounds__(SEL_BLOCK)
     if (c >= X && o < (uint32_t)beff) sel[o++] = composite_index(c);
   }
   __syncthreads();
-  // ascending order: each selected index goes to its rank among the selected
+  // ascending order: each selected index goes to its rank among the selected,
+  // counted by two lanes per element over halves of the list (16-byte
+  // broadcast reads, eight in flight)
   int32_t* out = fin_idx + (int64_t)item * B;
-  for (int i = threadIdx.x; i < beff; i += SEL_BLOCK) {
-    const uint32_t v = sel[i];
+  const int hb = (((beff + 1) >> 1) + 3) & ~3;  // first half, a multiple of 4
+  for (int i = threadIdx.x; i < 2 * beff; i += SEL_BLOCK) {
+    const int e = i >> 1;
+    const uint32_t v = sel[e];
+    const int j0 = (i & 1) ? hb : 0;
+    const int j1 = (i & 1) ? beff : min(hb, beff);
     int r = 0;
-    int j = 0;
-    for (; j + 4 <= beff; j += 4) {
+    int j = j0;
+#pragma unroll 8
+    for (; j + 4 <= j1; j += 4) {
       const uint4 u = *reinterpret_cast<const uint4*>(sel + j);
-      r += (u.x < v) + (u.y < v) + (u.z < v) + (u.w < v);
+      r += (int)(u.x < v) + (int)(u.y < v) + (int)(u.z < v) + (int)(u.w < v);
     }
-    for (; j < beff; ++j) r += sel[j] < v;
-    out[r] = (int32_t)v;
+    for (; j < j1; ++j) r += (int)(sel[j] < v);
+    r += __shfl_xor(r, 1);
+    if ((i & 1) == 0) out[r] = (int32_t)v;
   }
 }
 

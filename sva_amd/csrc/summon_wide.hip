@@ -111,16 +111,30 @@ struct ScanTables {
 // the round's table lookups are in flight together: acc[k] = ((T0 + T1) +
 // T2) + ... (the scan sum before the 1/8 scale; the reference's leading
 // 0 + T0 only changes the sign of a zero).  bpermute lookups need all 64
-// lanes, which this guarantees.
+// lanes, which this guarantees.  ds_bpermute reads only bits [7:2] of its
+// address, so byte j of a word becomes a lane address with one shift (codes
+// are below C <= 64 on that path).
 template <int S, bool BP>
 SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, BP>& T, float (&acc)[16 / S]) {
 #pragma clang fp contract(off)
   constexpr int KPT = 16 / S;
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    float a = T.get(0, byte_of(raw, k * S));
+    float a = 0.0f;
 #pragma unroll
-    for (int s = 1; s < S; ++s) a = a + T.get(s, byte_of(raw, k * S + s));
+    for (int s = 0; s < S; ++s) {
+      const int j = k * S + s;  // byte of the round
+      float v;
+      if (BP) {
+        const uint32_t word = raw[j >> 2];
+        const int sh = 8 * (j & 3);
+        const uint32_t addr = sh == 0 ? word << 2 : word >> (sh - 2);
+        v = __int_as_float(__builtin_amdgcn_ds_bpermute((int)addr, __float_as_int(T.reg[BP ? s : 0])));
+      } else {
+        v = T.get(s, byte_of(raw, j));
+      }
+      a = s == 0 ? v : a + v;
+    }
     acc[k] = a;
   }
 }
@@ -188,6 +202,58 @@ SVA_DEV float item_floor(const SummonParams& p, int item) {
   return est > lo ? est : lo;
 }
 
+// Appends the keys of slot i whose flag c is set to the wave's candidate
+// list (in lane order), as composites of the exact score acc / sqrt(R).
+SVA_DEV void append_candidate(const SummonParams& p, bool c, float acc, int n, uint64_t* out, uint32_t& wc) {
+#pragma clang fp contract(off)
+  const uint64_t m = __builtin_amdgcn_ballot_w64(c);
+  if (c) {
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    out[wc + below] = composite(f2key(acc / p.sqrt_r), (uint32_t)n);
+  }
+  wc += (uint32_t)__popcll(m);
+}
+
+// The scan of one thread's slots.  CHECK: the chunk is partial or masked, so
+// every key is tested for being allowed; otherwise every key is, and a round
+// (one 16-byte word of codes) is examined key by key only when its largest
+// sum reaches the floor.
+template <int S, bool BP, bool CHECK, bool MASKED>
+SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, BP>& T,
+                         float t_lo, int cs, int ce, uint64_t* out, uint32_t& wc, uint32_t& n_allowed) {
+  constexpr int KPT = 16 / S;
+#pragma unroll
+  for (int r = 0; r < KEYS_PT / KPT; ++r) {
+    float acc[KPT];
+    score_round<S, BP>(raw[r], T, acc);
+    if (CHECK) {
+      bool c[KPT];
+      bool any = false;
+#pragma unroll
+      for (int k = 0; k < KPT; ++k) {
+        const bool ok = key_ok<false, MASKED>(p, slot_key<S>(cs, r * KPT + k), ce);
+        n_allowed += ok;
+        c[k] = ok && acc[k] >= t_lo;
+        any = any || c[k];
+      }
+      if (__builtin_amdgcn_ballot_w64(any) != 0ull) {
+#pragma unroll
+        for (int k = 0; k < KPT; ++k) append_candidate(p, c[k], acc[k], slot_key<S>(cs, r * KPT + k), out, wc);
+      }
+    } else {
+      float mx = acc[0];
+#pragma unroll
+      for (int k = 1; k < KPT; ++k) mx = fmaxf(mx, acc[k]);
+      if (__builtin_amdgcn_ballot_w64(mx >= t_lo) != 0ull) {  // rare: the shortlist and the keys near it
+#pragma unroll
+        for (int k = 0; k < KPT; ++k)
+          append_candidate(p, acc[k] >= t_lo, acc[k], slot_key<S>(cs, r * KPT + k), out, wc);
+      }
+    }
+  }
+  if (!CHECK) n_allowed = KEYS_PT;
+}
+
 template <int S, bool BP, bool MASKED>
 __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
 #pragma clang fp contract(off)
@@ -208,30 +274,12 @@ __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
   const int wid = threadIdx.x / WAVE;
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
-  constexpr int KPT = 16 / S;
-  const bool full = ce - cs == CHUNK;
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
-#pragma unroll
-  for (int r = 0; r < KEYS_PT / KPT; ++r) {
-    float acc[KPT];
-    score_round<S, BP>(raw[r], T, acc);
-#pragma unroll
-    for (int k = 0; k < KPT; ++k) {
-      const int n = slot_key<S>(cs, r * KPT + k);
-      const bool ok = full ? key_ok<true, MASKED>(p, n, ce) : key_ok<false, MASKED>(p, n, ce);
-      n_allowed += ok;
-      const bool c = ok && acc[k] >= t_lo;
-      const uint64_t m = __ballot(c);
-      if (m != 0ull) {  // rare: the shortlist and the keys near it
-        if (c) {
-          const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-          out[wc + below] = composite(f2key(acc[k] / p.sqrt_r), (uint32_t)n);
-        }
-        wc += (uint32_t)__popcll(m);
-      }
-    }
+  if (!MASKED && ce - cs == CHUNK) {
+    scan_rounds<S, BP, false, false>(p, raw, T, t_lo, cs, ce, out, wc, n_allowed);
+  } else {
+    scan_rounds<S, BP, true, MASKED>(p, raw, T, t_lo, cs, ce, out, wc, n_allowed);
   }
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane_id() == 0) {

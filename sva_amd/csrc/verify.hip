@@ -99,8 +99,8 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   const int B = p.B;
   int32_t* lists = (int32_t*)lds;                     // [grp][B]
   float* qv = (float*)(lists + grp * B);              // [grp][D]
-  float* vrow = qv + grp * D;                         // [EPW][D]
-  float* wt = vrow + EPW * D;                         // [EPW][MAX_GRP] scores, then weights
+  float* vrow = qv + grp * D;                         // [EPW][D + 1] (padded: no bank conflicts)
+  float* wt = vrow + EPW * (D + 1);                   // [EPW][MAX_GRP] scores, then weights
   int32_t* ekey = (int32_t*)(wt + EPW * MAX_GRP);     // [EPW]
   uint32_t* emem = (uint32_t*)(ekey + EPW);           // [EPW] heads whose list holds the entry
   int* cnt = (int*)(emem + EPW);                      // [MAX_GRP + 1] prefix of list lengths
@@ -129,28 +129,31 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   const int M = cnt[grp];
   const int e0 = (int)((int64_t)s * M / p.split);
   const int n = (int)((int64_t)(s + 1) * M / p.split) - e0;  // <= EPW
-  // phase 2: first occurrences of the slice and the heads holding each
-  if ((int)threadIdx.x < EPW) {
-    const int r = threadIdx.x;
-    uint32_t mem = 0u;
-    int32_t x = 0;
+  // phase 2: first occurrences of the slice and the heads holding each; the
+  // 4 lanes of an entry search lists qt and qt + 4
+  {
+    const int r = threadIdx.x >> 2;
+    const int qt = threadIdx.x & 3;
+    int j = 0;
+    int32_t x = -1;
     if (r < n) {
       const int e = e0 + r;
-      int j = 0;
       while (j + 1 < grp && e >= cnt[j + 1]) ++j;
       x = lists[j * B + (e - cnt[j])];
-      if (x >= 0 && (int64_t)x < len) {
-        bool own = true;
-        for (int jj = 0; jj < j && own; ++jj) own = bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) < 0;
-        if (own) {
-          mem = 1u << j;
-          for (int jj = j + 1; jj < grp; ++jj)
-            if (bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) >= 0) mem |= 1u << jj;
-        }
-      }
     }
-    ekey[r] = x;
-    emem[r] = mem;
+    const bool valid = r < n && x >= 0 && (int64_t)x < len;
+    uint32_t found = 0u;
+    if (valid) {
+      for (int jj = qt; jj < grp; jj += 4)
+        if (jj == j || bsearch_i32(lists + jj * B, cnt[jj + 1] - cnt[jj], x) >= 0) found |= 1u << jj;
+    }
+    found |= __shfl_xor(found, 1, 4);
+    found |= __shfl_xor(found, 2, 4);
+    if (qt == 0) {
+      const bool own = valid && (found & ((1u << j) - 1u)) == 0u;  // no lower head holds the key
+      ekey[r] = x;
+      emem[r] = own ? found : 0u;
+    }
   }
   __syncthreads();
   // phase 3: every K and V row of the slice, 4 lanes per row
@@ -179,7 +182,7 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const int d = qt * dq + 4 * c + k;
-            vrow[r * D + d] = vv[c][k];
+            vrow[r * (D + 1) + d] = vv[c][k];
 #pragma unroll
             for (int j = 0; j < MAX_GRP; ++j)
               if (j < grp) dot[j] = __builtin_fmaf(kv[c][k], qv[j * D + d], dot[j]);
@@ -187,7 +190,7 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
         }
       }
     } else if (r < n) {
-      for (int d = qt * dq; d < (qt + 1) * dq; ++d) vrow[r * D + d] = 0.0f;  // weight 0 must not meet NaN
+      for (int d = qt * dq; d < (qt + 1) * dq; ++d) vrow[r * (D + 1) + d] = 0.0f;  // weight 0 must not meet NaN
     }
 #pragma unroll
     for (int j = 0; j < MAX_GRP; ++j) {
@@ -219,7 +222,7 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   for (int e = threadIdx.x; e < grp * D; e += VB) {
     const int j = e / D, d = e - j * D;
     float acc = 0.0f;
-    for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * D + d];
+    for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * (D + 1) + d];
     float* dst = p.part + ((item0 + (int64_t)j * p.Q) * p.split + s) * (D + 2);
     dst[2 + d] = acc;
     if (d == 0) {
@@ -286,7 +289,7 @@ int verify_split(int64_t grp, int64_t B) {
 }
 
 size_t verify_lds_bytes(int64_t grp, int64_t B, int64_t D) {
-  return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * EPW * D +
+  return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * EPW * (D + 1) +
          sizeof(float) * EPW * MAX_GRP + 2 * sizeof(int32_t) * EPW + sizeof(int) * (MAX_GRP + 1) +
          sizeof(float) * 2 * MAX_GRP + 16;
 }
