@@ -52,6 +52,26 @@ const char *sva_last_error(void);
 int sva_abi_version(void);
 
 /*
+ * Write path: low-rank keys and PQ codes of cache rows [row_begin,
+ * row_begin + n_rows) for every query head (fresh catalog: all rows; append:
+ * the new rows only).
+ * Replaces sva/llama.py:597-616 (k_low = einsum(K, k_proj) on the repeat_kv
+ * expanded keys; encode_product_keys) and sva/ops.py:10-47
+ * (assign_to_centroids: argmin of |x|^2 - 2 x.c + |c|^2, first index on ties).
+ *   keys      (g, row, d) at g*kv_head_stride + row*kv_row_stride + d; query
+ *             head h reads KV head h / (H / G)
+ *   k_proj    [H, D, R] fp32; codebooks [H, S, C, R/S] fp32 (16-byte aligned)
+ *   k_low     (h, row, r) at h*k_low_head_stride + row*R + r, fp32 out
+ *   codes     (h, row, s) at h*code_head_stride + row*S + s, code_type out
+ *   R/S must be a multiple of 4; D, R <= 256.  Rows keep no state: writing a
+ *   row twice gives the same result.
+ */
+int sva_write_encode(const void *keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                     int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R, int64_t S,
+                     int64_t C, const float *k_proj, const float *codebooks, float *k_low, int64_t k_low_head_stride,
+                     void *codes, int code_type, int64_t code_head_stride, void *stream);
+
+/*
  * Learned query map and per-query PQ lookup table.
  * Replaces sva/llama.py:211 (q_low = einsum(q, q_proj) * scale) and the table
  * of sva/ops.py:66-68.
@@ -103,9 +123,8 @@ int sva_summon(const float *lut, const float *score_range, const float *q_low, c
 
 /*
  * Which summon strategy a call with these shapes takes (16-byte aligned
- * catalogs assumed): 0 = one workgroup per query item, 1 = wide cooperative
- * path (q = 1 over a long cache: many workgroups per item, one pass over the
- * codes).
+ * catalogs assumed): 0 = one workgroup per query item, 1 = wide path (q = 1
+ * over a long cache: many workgroups per item, one pass over the codes).
  */
 int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S, int64_t C,
                         int64_t L, int code_type, int mask_type);
@@ -126,8 +145,9 @@ int sva_budget_select(const int32_t *sl_idx, const float *sl_rank, const int32_t
  * weighted V sum per head, merged across workgroups by a second kernel.
  * Replaces sva/llama.py:304-317 (scan path) and :532-553 (static path).
  *   keys/values (g, row, d) at g*kv_head_stride + row*kv_row_stride + d
- *   fin_idx [items, B] sorted ascending, fin_count [items]; indices are
- *   clamped into [0, len) of their sequence so every read stays in bounds
+ *   fin_idx [items, B] sorted ascending (as sva_budget_select writes them),
+ *   fin_count [items]; indices outside [0, len) of their sequence are
+ *   skipped, so every read stays in bounds
  *   out (b, h, t, d) at b*out_seq_stride + h*out_head_stride + t*out_tok_stride + d
  *   head_dim must be a multiple of 16 (<= 256).
  * workspace: sva_verify_workspace_bytes(...) bytes (no state between calls).

@@ -1,0 +1,233 @@
+// Write path: low-rank keys and product-quantized codes of cache rows
+// (sva/llama.py:578-624, the catalog; sva/ops.py:10-47, assignment).
+//
+//   k_low[h][n][r] = sum_d K[g(h)][n][d] * k_proj[h][d][r]      (sva/llama.py:615)
+//       a sequential fma chain over d, as torch's many-row einsum rounds it;
+//       g(h) = h / (H / G) (the reference's repeat_kv expansion).
+//   codes[h][n][s] = argmin_c (|x|^2 - 2 x.c + |c|^2), first index on ties,
+//       x = k_low[h][n][s*sub:(s+1)*sub]                         (sva/ops.py:19-20)
+//       |x|^2 and |c|^2 in torch's sum order, x.c a sequential fma chain.
+//
+// One workgroup per (64 rows, head).  The head's map and the rows are staged
+// in LDS; each thread accumulates a 4 x 4 block of k_low.  For each subspace
+// the codebook is staged (rows padded against bank conflicts) and the 4 lanes
+// of a row split the centroids, then merge (distance, index) pairs keeping
+// the lower index on equal distances.  NaN distances never win (the CPU
+// oracle's rule).
+#include "capi_internal.h"
+#include "common.cuh"
+#include "summon.h"
+
+using namespace sva;
+
+namespace {
+
+constexpr int WT = 256;  // threads per workgroup
+constexpr int KT = 64;   // rows per workgroup
+constexpr int CB_PAD = 4;
+
+struct WriteParams {
+  const void* keys;
+  int kv_dtype;
+  int64_t kv_hs, kv_rs;
+  int64_t row0, n_rows;
+  int H, G, D, R, S, C;
+  const float* k_proj;     // [H, D, R]
+  const float* codebooks;  // [H, S, C, sub]
+  float* k_low;            // [H, rows, R] (head stride klow_hs)
+  int64_t klow_hs;
+  void* codes;             // [H, rows, S] (head stride code_hs)
+  int ctype;
+  int64_t code_hs;
+};
+
+// SUB: compile-time subspace width (0: runtime, x read from LDS).
+template <int SUB>
+__global__ void __launch_bounds__(WT) write_encode_kernel(WriteParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int sub = SUB > 0 ? SUB : R / S;
+  const int h = blockIdx.y;
+  const int g = h / (p.H / p.G);
+  const int64_t n0 = p.row0 + (int64_t)blockIdx.x * KT;
+  const int nk = (int)min((int64_t)KT, p.row0 + p.n_rows - n0);
+  float* W = (float*)lds;                  // [D][R]
+  float* Kt = W + D * R;                   // [KT][D + 1]
+  float* Xl = Kt + KT * (D + 1);           // [KT][R + 1] k_low of the tile
+  float* cb = Xl + KT * (R + 1);           // [C][sub + CB_PAD], 16-byte aligned rows
+  float* cn = cb + C * (sub + CB_PAD);     // [C]
+  float* xx = cn + C;                      // [KT]
+
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(p.k_proj + (int64_t)h * D * R);
+    for (int i = threadIdx.x; i < D * R / 4; i += WT) reinterpret_cast<float4*>(W)[i] = w4[i];
+    const int64_t kb = (int64_t)g * p.kv_hs;
+    for (int i = threadIdx.x; i < KT * D; i += WT) {
+      const int k = i / D, d = i - k * D;
+      Kt[k * (D + 1) + d] = k < nk ? load_elem(p.keys, kb + (n0 + k) * p.kv_rs + d, p.kv_dtype) : 0.0f;
+    }
+  }
+  __syncthreads();
+  // projection: 4 rows x 4 ranks per thread, fma chain over d
+  float* klow = p.k_low + (int64_t)h * p.klow_hs;
+  for (int blk = threadIdx.x; blk < (KT / 4) * (R / 4); blk += WT) {
+    const int kb = blk / (R / 4), rb = blk - kb * (R / 4);
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int d = 0; d < D; ++d) {
+      const float4 w = *reinterpret_cast<const float4*>(W + d * R + rb * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float kv = Kt[(kb * 4 + i) * (D + 1) + d];
+        acc[i][0] = __builtin_fmaf(kv, w.x, acc[i][0]);
+        acc[i][1] = __builtin_fmaf(kv, w.y, acc[i][1]);
+        acc[i][2] = __builtin_fmaf(kv, w.z, acc[i][2]);
+        acc[i][3] = __builtin_fmaf(kv, w.w, acc[i][3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = kb * 4 + i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Xl[k * (R + 1) + rb * 4 + j] = acc[i][j];
+      if (k < nk)
+        *reinterpret_cast<float4*>(klow + (n0 + k) * R + rb * 4) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    }
+  }
+  // assignment, one subspace at a time
+  const int k = threadIdx.x >> 2;  // row of this lane group
+  const int qt = threadIdx.x & 3;
+  for (int s = 0; s < S; ++s) {
+    __syncthreads();  // Xl complete / previous subspace done with cb
+    const float* src = p.codebooks + ((int64_t)h * S + s) * C * sub;
+    for (int i = threadIdx.x; i < C * sub / 4; i += WT) {
+      const int c = (4 * i) / sub, j = 4 * i - c * sub;
+      *reinterpret_cast<float4*>(cb + c * (sub + CB_PAD) + j) = reinterpret_cast<const float4*>(src)[i];
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += WT) cn[c] = torch_order_dot(cb + c * (sub + CB_PAD), cb + c * (sub + CB_PAD), sub);
+    for (int r = threadIdx.x; r < KT; r += WT) xx[r] = torch_order_dot(Xl + r * (R + 1) + s * sub, Xl + r * (R + 1) + s * sub, sub);
+    __syncthreads();
+    const float* xr = Xl + k * (R + 1) + s * sub;
+    float xv[SUB > 0 ? SUB : 1];
+    if (SUB > 0) {
+#pragma unroll
+      for (int j = 0; j < (SUB > 0 ? SUB : 1); ++j) xv[j] = xr[j];
+    }
+    const float xxk = xx[k];
+    float best = INFINITY;
+    int arg = 0;
+    for (int c = qt; c < C; c += 4) {
+      const float* cr = cb + c * (sub + CB_PAD);
+      float xc = 0.0f;
+      if (SUB > 0) {
+#pragma unroll
+        for (int j = 0; j < (SUB > 0 ? SUB : 1); j += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(cr + j);
+          xc = __builtin_fmaf(xv[j], v.x, xc);
+          xc = __builtin_fmaf(xv[j + 1], v.y, xc);
+          xc = __builtin_fmaf(xv[j + 2], v.z, xc);
+          xc = __builtin_fmaf(xv[j + 3], v.w, xc);
+        }
+      } else {
+        for (int j = 0; j < sub; ++j) xc = __builtin_fmaf(xr[j], cr[j], xc);
+      }
+      const float dist = (xxk - 2.0f * xc) + cn[c];
+      if (dist < best) {
+        best = dist;
+        arg = c;
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {
+      const float ob = __shfl_xor(best, o, 4);
+      const int oa = __shfl_xor(arg, o, 4);
+      if (ob < best || (ob == best && oa < arg)) {
+        best = ob;
+        arg = oa;
+      }
+    }
+    if (qt == 0 && k < nk) store_code(p.codes, (int64_t)h * p.code_hs + (n0 + k) * S + s, p.ctype, arg);
+  }
+}
+
+size_t write_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C) {
+  const int64_t sub = R / S;
+  return sizeof(float) * (size_t)(D * R + KT * (D + 1) + KT * (R + 1) + C * (sub + CB_PAD) + C + KT) + 16;
+}
+
+template <int SUB>
+int launch_write(const WriteParams& p, dim3 grid, size_t lds, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)write_encode_kernel<SUB>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
+                  "hipFuncSetAttribute(write_encode_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(write_encode_kernel<SUB>, grid, dim3(WT), lds, stream, p);
+  SVA_CHECK_LAUNCH("write_encode_kernel");
+  return SVA_OK;
+}
+
+}  // namespace
+
+extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                                int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R,
+                                int64_t S, int64_t C, const float* k_proj, const float* codebooks, float* k_low,
+                                int64_t k_low_head_stride, void* codes, int code_type, int64_t code_head_stride,
+                                void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(keys && k_proj && codebooks && k_low && codes, "sva_write_encode: null pointer");
+  SVA_REQUIRE(row_begin >= 0 && n_rows >= 0, "sva_write_encode: bad row range");
+  SVA_REQUIRE(H > 0 && G > 0 && H % G == 0, "sva_write_encode: %lld query heads over %lld KV heads", (long long)H,
+              (long long)G);
+  SVA_REQUIRE(D > 0 && D <= 256 && R > 0 && R <= 256 && R % 4 == 0 && (D * R) % 4 == 0,
+              "sva_write_encode: head_dim %lld / rank %lld unsupported", (long long)D, (long long)R);
+  SVA_REQUIRE(S > 0 && R % S == 0 && (R / S) % 4 == 0,
+              "sva_write_encode: rank_dim=%lld must be divisible by subspaces=%lld into multiples of 4", (long long)R,
+              (long long)S);
+  SVA_REQUIRE(C > 0, "sva_write_encode: codewords %lld", (long long)C);
+  SVA_REQUIRE(kv_dtype >= 0 && kv_dtype <= 2 && code_type >= 0 && code_type <= 3, "sva_write_encode: bad dtype");
+  const int64_t code_max = code_type == 0 ? 256 : code_type == 1 ? 32768 : (1ll << 31);
+  SVA_REQUIRE(C <= code_max, "sva_write_encode: %lld codewords do not fit the code type", (long long)C);
+  SVA_REQUIRE((((uintptr_t)k_proj | (uintptr_t)codebooks | (uintptr_t)k_low) & 15u) == 0 && k_low_head_stride % 4 == 0,
+              "sva_write_encode: k_proj / codebooks / k_low must be 16-byte aligned fp32");
+  const size_t lds = write_lds_bytes(D, R, S, C);
+  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_write_encode: %zu bytes of LDS needed", lds);
+  if (n_rows == 0) return SVA_OK;
+  const int64_t tiles = (n_rows + KT - 1) / KT;
+  SVA_REQUIRE(tiles < (1ll << 31) && H <= 65535, "sva_write_encode: too many rows or heads");
+  WriteParams p;
+  p.keys = keys;
+  p.kv_dtype = kv_dtype;
+  p.kv_hs = kv_head_stride;
+  p.kv_rs = kv_row_stride;
+  p.row0 = row_begin;
+  p.n_rows = n_rows;
+  p.H = (int)H;
+  p.G = (int)G;
+  p.D = (int)D;
+  p.R = (int)R;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.k_proj = k_proj;
+  p.codebooks = codebooks;
+  p.k_low = k_low;
+  p.klow_hs = k_low_head_stride;
+  p.codes = codes;
+  p.ctype = code_type;
+  p.code_hs = code_head_stride;
+  const dim3 grid((unsigned)tiles, (unsigned)H);
+  switch (R / S) {
+    case 8: return launch_write<8>(p, grid, lds, (hipStream_t)stream);
+    case 16: return launch_write<16>(p, grid, lds, (hipStream_t)stream);
+    case 32: return launch_write<32>(p, grid, lds, (hipStream_t)stream);
+    case 64: return launch_write<64>(p, grid, lds, (hipStream_t)stream);
+    default: return launch_write<0>(p, grid, lds, (hipStream_t)stream);
+  }
+}

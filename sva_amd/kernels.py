@@ -49,6 +49,41 @@ def _f32c(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def write_encode(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tensor, k_low: torch.Tensor,
+                 codes: torch.Tensor, row_begin: int = 0, n_rows: int | None = None) -> None:
+    """Fill k_low [H, rows, R] and codes [H, rows, S] for cache rows
+    [row_begin, row_begin + n_rows) from keys [G, rows, D] (sva/llama.py:597-616,
+    sva/ops.py:10-47).  k_low and codes are written in place."""
+
+    if keys.dim() != 3 or keys.stride(-1) != 1:
+        raise ValueError("keys must be [G, rows, D] with contiguous rows")
+    heads, dim, rank = k_proj.shape
+    subspaces, codewords = codebooks.shape[1], codebooks.shape[2]
+    if rank % subspaces != 0:
+        raise ValueError(f"rank_dim={rank} must be divisible by subspaces={subspaces}.")
+    if k_low.dim() != 3 or k_low.shape[0] != heads or k_low.shape[2] != rank or k_low.stride(1) != rank \
+            or k_low.stride(2) != 1 or k_low.dtype != torch.float32:
+        raise ValueError("k_low must be fp32 [H, rows, R] with contiguous rows")
+    if codes.dim() != 3 or codes.shape[0] != heads or codes.shape[2] != subspaces or codes.stride(1) != subspaces \
+            or codes.stride(2) != 1:
+        raise ValueError("codes must be [H, rows, S] with contiguous rows")
+    rows = keys.shape[1]
+    n_rows = rows - row_begin if n_rows is None else n_rows
+    if row_begin < 0 or n_rows < 0 or row_begin + n_rows > min(rows, k_low.shape[1], codes.shape[1]):
+        raise ValueError("row range outside the catalog")
+    device = require_device(keys, k_proj, codebooks, k_low, codes)
+    k_proj = _f32c(k_proj)
+    codebooks = _f32c(codebooks)
+    check(
+        lib().sva_write_encode(
+            ptr(keys), dtype_code(keys), keys.stride(0), keys.stride(1), row_begin, n_rows, heads, keys.shape[0], dim,
+            rank, subspaces, codewords, ptr(k_proj), ptr(codebooks), ptr(k_low), k_low.stride(0), ptr(codes),
+            code_type(codes), codes.stride(0), stream_handle(device),
+        ),
+        "sva_write_encode",
+    )
+
+
 def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor,
               codes: torch.Tensor | None = None, n_keys: int = 0, shortlist: int = 0):
     """q_low [n_seq,H,Q,R], lut [n_seq,H,Q,S,C], score_range [n_seq,H,Q,4] (sva/llama.py:211, sva/ops.py:66-68).
