@@ -62,7 +62,8 @@ int sva_abi_version(void);
  *             head h reads KV head h / (H / G)
  *   k_proj    [H, D, R] fp32; codebooks [H, S, C, R/S] fp32 (16-byte aligned)
  *   k_low     (h, row, r) at h*k_low_head_stride + row*R + r, fp32 out
- *   codes     (h, row, s) at h*code_head_stride + row*S + s, code_type out
+ *   codes     (h, row, s) at h*code_head_stride + row*S + s, code_type out;
+ *             NULL: k_low only (the reference's lazy static tail, :604-610)
  *   R/S must be a multiple of 4; D, R <= 256.  Rows keep no state: writing a
  *   row twice gives the same result.
  */
@@ -159,6 +160,88 @@ int sva_verify(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_
                const int32_t *fin_count, int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B,
                float scaling, void *out, int out_dtype, int64_t out_seq_stride, int64_t out_head_stride,
                int64_t out_tok_stride, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Inverted-index summon for q = 1 decode (summon_mode "inverted" and
+ * "inverted_static").
+ */
+
+/*
+ * CSR postings of the first n_rows rows: for every (head h, subspace s) and
+ * cell c, the key ids with code c, ascending.
+ * Replaces sva/llama.py:626-657 (_rebuild_postings; the dense table
+ * [H, S, C, max_bucket] becomes offsets + ids).
+ *   codes      (h, row, s) at h*code_head_stride + row*S + s
+ *   offsets    [H, S, C + 1] int32 out; ids [H, S, n_rows] int32 out
+ *   max_count  [H, S] int32 out: the largest cell of each (h, s)
+ * C <= 1024.
+ */
+int sva_postings_build(const void *codes, int code_type, int64_t code_head_stride, int64_t H, int64_t n_rows,
+                       int64_t S, int64_t C, int32_t *offsets, int32_t *ids, int32_t *max_count, void *stream);
+
+/* Candidate slots per head of sva_inverted_candidates. */
+int64_t sva_inverted_slots(int64_t S, int64_t postings_len, int64_t k_len, int64_t tail_start);
+
+/*
+ * Candidates of one decode token per head: the top `cells` cells of every
+ * subspace by LUT / sqrt(R) (ties: lower cell index), the postings of those
+ * cells (rows < postings_len, one entry per list holding a key), the rows
+ * [tail_start, k_len) (static: every row; adaptive: rows whose code is in a
+ * chosen cell), and one extra slot (static without a tail: the current row
+ * k_len - 1; adaptive: the current row if allowed, else the last allowed row
+ * as a fallback).  Each entry gets its rank score (k_low . q_low) / sqrt(R)
+ * in torch's order.
+ * Replaces sva/llama.py:359-392 (adaptive) and :451-495 (static).
+ *   lut [H, S, C] (sva_query_lut, one token), q_low [H, R], R = 64
+ *   mask: NULL / SVA_MASK_NONE / SVA_MASK_BOOL (every row allowed) or the
+ *         token's additive mask row [k_len] (allowed iff > -1e4)
+ *   comp [H, slots] uint64 out: (order-preserving key of the masked score
+ *         << 32) | (0xFFFFFFFF - key), 0 for an empty slot
+ *   flag [H, slots] uint8 out: bit 0 allowed, bit 1 fallback entry
+ *   slots = sva_inverted_slots(S, postings_len, k_len, tail_start)
+ */
+int sva_inverted_candidates(const float *lut, const float *q_low, const float *k_low, int64_t k_low_head_stride,
+                            const void *codes, int code_type, int64_t code_head_stride, const int32_t *offsets,
+                            const int32_t *ids, int64_t postings_len, int64_t tail_start, int64_t k_len, int64_t H,
+                            int64_t S, int64_t C, int64_t R, int64_t cells, const void *mask, int mask_type,
+                            int adaptive, uint64_t *comp, uint8_t *flag, int64_t slots, void *stream);
+
+/*
+ * Selection over the candidates of each head, the reference's rules:
+ *   mode 0 (static, sva/llama.py:83-116 and :497-526): refill window of the
+ *     best min(width, max(B, refill_factor * B)) entries counted with
+ *     multiplicity, width = S * cells * max(max_count) + (tail_len or 1) as
+ *     in the dense layout; first occurrence per key; margin-adaptive budget
+ *     over the min(B, refill) selected slots (fp32 comparisons);
+ *   mode 1 (adaptive, sva/llama.py:383-404): distinct allowed candidates,
+ *     rank_count = min(B, their number), margin-adaptive budget (the margin
+ *     compared as a double), the fallback entry when no candidate is allowed.
+ *   fin_idx [H, B] chosen keys ascending (for sva_verify), fin_count [H]
+ *   stats [H, 4] float out: summoned, refill pool, verified, selected slots
+ * workspace: sva_unique_select_workspace_bytes(H, B, refill_factor, slots).
+ */
+size_t sva_unique_select_workspace_bytes(int64_t H, int64_t B, int64_t refill_factor, int64_t slots);
+int sva_unique_refill_select(const uint64_t *comp, const uint8_t *flag, int64_t slots, int64_t H, int mode, int64_t B,
+                             int64_t min_budget, int64_t mid_budget, double low_margin, double high_margin,
+                             int64_t refill_factor, const int32_t *max_count, int64_t S, int64_t cells,
+                             int64_t tail_len, int32_t *fin_idx, int32_t *fin_count, float *stats, void *workspace,
+                             size_t workspace_bytes, void *stream);
+
+/*
+ * Unique refill selection over arbitrary rows of candidates
+ * (SVALlamaAttention._top_unique_candidates, sva/llama.py:83-116): per row,
+ * the best min(W, max(budget, refill_factor * budget)) entries by masked
+ * score, the best-scored occurrence of each key, then the best
+ * min(budget, refill) of those by (score desc, key asc); slots past the valid
+ * ones are invalid (score -FLT_MAX).
+ *   idx [H, W] int64, scores [H, W] fp32, valid [H, W] uint8
+ *   sel_idx [H, cap] int32, sel_scores [H, cap] fp32, sel_valid [H, cap] uint8
+ *   out, cap = min(budget, refill)
+ */
+size_t sva_top_unique_workspace_bytes(int64_t H, int64_t W, int64_t budget, int64_t refill_factor);
+int sva_top_unique(const int64_t *idx, const float *scores, const uint8_t *valid, int64_t H, int64_t W, int64_t budget,
+                   int64_t refill_factor, int32_t *sel_idx, float *sel_scores, uint8_t *sel_valid, void *workspace,
+                   size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

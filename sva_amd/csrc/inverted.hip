@@ -1,0 +1,848 @@
+// Inverted-index summon (q = 1 decode): postings, candidates, unique refill
+// selection with margin-adaptive budgets (sva/llama.py:330-425, :427-576,
+// :626-693, :83-116).
+//
+// sva_postings_build   CSR postings per (head, subspace): offsets [C + 1] and
+//                      key ids ascending within each cell (a stable counting
+//                      sort; the reference's dense [.., max_bucket] table holds
+//                      the same ids per cell, sva/llama.py:626-657).
+// sva_inverted_candidates
+//                      per head: the top `cells` cells of every subspace by
+//                      LUT / sqrt(R) (ties: lower cell index), the posting
+//                      lists of those cells (a key listed in several chosen
+//                      cells appears once per list, as in the reference), the
+//                      tail rows past the postings (static: all of them;
+//                      adaptive: those whose code falls in a chosen cell) and
+//                      one extra slot (static: the current row when there is
+//                      no tail; adaptive: the current row, or the last allowed
+//                      row as a fallback).  Every entry is rank-scored,
+//                      (k_low . q_low) / sqrt(R) in torch's sum order, masked
+//                      by the attention mask, and stored as a 64-bit composite
+//                      (score key, key index).
+// sva_unique_refill_select
+//                      per head: refill window of the best min(width,
+//                      max(B, factor B)) entries counted with multiplicity,
+//                      first occurrence of each key, the margin-adaptive budget
+//                      and the chosen keys (ascending) for sva_verify.
+#include <cfloat>
+#include <cmath>
+
+#include "capi_internal.h"
+#include "common.cuh"
+#include "summon.h"
+
+using namespace sva;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// postings
+
+constexpr int PB = 1024;
+constexpr int PNW = PB / WAVE;
+constexpr int kMaxPostingCells = 1024;
+
+__global__ void __launch_bounds__(PB)
+    postings_build_kernel(const void* __restrict__ codes, int ctype, int64_t code_hs, int S, int n_rows, int C,
+                          int32_t* __restrict__ offsets, int32_t* __restrict__ ids, int32_t* __restrict__ max_count) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  uint32_t* hist = (uint32_t*)lds;        // [C]
+  uint32_t* cursor = hist + C;            // [C]
+  uint32_t* wcnt = cursor + C;            // [PNW][C]
+  uint32_t* scratch = wcnt + PNW * C;     // [PNW + 2]
+  const int h = blockIdx.x / S, s = blockIdx.x % S;
+  const int64_t cbase = (int64_t)h * code_hs + s;
+  auto code_at = [&](int n) {
+    int64_t c = load_code(codes, cbase + (int64_t)n * S, ctype);
+    return (int)(c < 0 ? 0 : (c >= C ? C - 1 : c));
+  };
+  for (int c = threadIdx.x; c < C; c += PB) hist[c] = 0u;
+  __syncthreads();
+  for (int n = threadIdx.x; n < n_rows; n += PB) atomicAdd(&hist[code_at(n)], 1u);
+  __syncthreads();
+  int32_t* off = offsets + (int64_t)blockIdx.x * (C + 1);
+  {
+    uint32_t carry = 0, mx = 0;
+    for (int c0 = 0; c0 < C; c0 += PB) {
+      const int c = c0 + (int)threadIdx.x;
+      const uint32_t v = c < C ? hist[c] : 0u;
+      uint32_t tot;
+      const uint32_t ex = block_excl_scan<PB>(v, scratch, &tot);
+      if (c < C) {
+        off[c] = (int32_t)(carry + ex);
+        cursor[c] = carry + ex;
+        mx = max(mx, v);
+      }
+      carry += tot;
+    }
+    if (threadIdx.x == 0) {
+      off[C] = n_rows;
+      scratch[PNW] = 0u;
+    }
+    __syncthreads();
+    atomicMax(&scratch[PNW], mx);
+    __syncthreads();
+    if (threadIdx.x == 0) max_count[blockIdx.x] = (int32_t)scratch[PNW];
+    __syncthreads();
+  }
+  int bits = 0;
+  while ((1 << bits) < C) ++bits;
+  const int wid = threadIdx.x / WAVE;
+  int32_t* out = ids + (int64_t)blockIdx.x * n_rows;
+  for (int base = 0; base < n_rows; base += PB) {
+    for (int i = threadIdx.x; i < PNW * C; i += PB) wcnt[i] = 0u;
+    __syncthreads();
+    const int n = base + (int)threadIdx.x;
+    const bool valid = n < n_rows;
+    const int c = valid ? code_at(n) : 0;
+    // lanes of this wave holding the same code
+    uint64_t same = __builtin_amdgcn_ballot_w64(valid);
+    for (int b = 0; b < bits; ++b) {
+      const bool bit = (c >> b) & 1;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(bit);
+      same &= bit ? m : ~m;
+    }
+    const uint64_t below = same & ((1ull << lane_id()) - 1ull);
+    if (valid && below == 0ull) wcnt[wid * C + c] = (uint32_t)__popcll(same);  // the first lane of its code
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < C; cc += PB) {
+      uint32_t run = 0;
+      for (int w = 0; w < PNW; ++w) {
+        const uint32_t v = wcnt[w * C + cc];
+        wcnt[w * C + cc] = run;
+        run += v;
+      }
+      hist[cc] = run;  // this chunk's count of code cc
+    }
+    __syncthreads();
+    if (valid) out[cursor[c] + wcnt[wid * C + c] + (uint32_t)__popcll(below)] = n;
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < C; cc += PB) cursor[cc] += hist[cc];
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// candidates
+
+constexpr int CT = 256;          // threads per candidate workgroup
+constexpr int TAIL_ROWS = 256;   // tail rows per workgroup
+constexpr int kMaxCells = 64;
+constexpr int kMaxSub = 16;
+
+struct CandParams {
+  const float* lut;  // [H, S, C]
+  const float* q_low;  // [H, R]
+  const float* k_low;
+  int64_t klow_hs;
+  const void* codes;
+  int ctype;
+  int64_t code_hs;
+  const int32_t* offsets;  // [H, S, C + 1]
+  const int32_t* ids;      // [H, S, postings_len]
+  int postings_len;
+  int tail_start;
+  int k_len;
+  int H, S, C, R, cells;
+  float sqrt_r;
+  const void* mask;  // allowed iff mask[n] > -1e4 (MASK_* types), or NULL: every row
+  int mask_type;
+  int adaptive;
+  int W;                     // slots per head
+  uint64_t* comp;            // [H, W]; 0 = empty slot
+  uint8_t* flag;             // [H, W]: bit 0 valid, bit 1 fallback entry
+};
+
+SVA_DEV bool row_allowed(const CandParams& p, int n) {
+  return p.mask == nullptr || mask_allows(p.mask, n, p.mask_type);
+}
+
+// Rank score of key n (16 lanes), torch's order, then / sqrt(R).  R == 64.
+SVA_DEV float rank_score16(const CandParams& p, int h, int n) {
+#pragma clang fp contract(off)
+  const float* row = p.k_low + (int64_t)h * p.klow_hs + (int64_t)n * 64;
+  const float* q = p.q_low + (int64_t)h * 64;
+  const int j = lane_id() & 15;
+  const float4 r = reinterpret_cast<const float4*>(row)[j];
+  const float4 qq = reinterpret_cast<const float4*>(q)[j];
+  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
+  const float a0 = (0.0f + p0) + __shfl_down(p0, 8, 16);
+  const float a1 = (0.0f + p1) + __shfl_down(p1, 8, 16);
+  const float a2 = (0.0f + p2) + __shfl_down(p2, 8, 16);
+  const float a3 = (0.0f + p3) + __shfl_down(p3, 8, 16);
+  const float v0 = ((a0 + __shfl_down(a0, 2, 16)) + __shfl_down(a0, 4, 16)) + __shfl_down(a0, 6, 16);
+  const float v1 = ((a1 + __shfl_down(a1, 2, 16)) + __shfl_down(a1, 4, 16)) + __shfl_down(a1, 6, 16);
+  const float v2 = ((a2 + __shfl_down(a2, 2, 16)) + __shfl_down(a2, 4, 16)) + __shfl_down(a2, 6, 16);
+  const float v3 = ((a3 + __shfl_down(a3, 2, 16)) + __shfl_down(a3, 4, 16)) + __shfl_down(a3, 6, 16);
+  const float w0 = __shfl_down(v0, 1, 16), w1 = __shfl_down(v1, 1, 16);
+  const float w2 = __shfl_down(v2, 1, 16), w3 = __shfl_down(v3, 1, 16);
+  const float t = (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
+  return __shfl(t, 0, 16) / p.sqrt_r;
+}
+
+SVA_DEV uint64_t entry_comp(bool valid, float score, int n) {
+  return composite(f2key(valid ? score : -FLT_MAX), (uint32_t)n);
+}
+
+// Scores up to 16 keys per pass (16 lanes each) and stores their entries.
+template <typename KeyAt>
+SVA_DEV void score_entries(const CandParams& p, int h, int count, KeyAt key_at, uint64_t* comp, uint8_t* flag,
+                           uint8_t extra_flag) {
+  const int g = threadIdx.x >> 4;
+  for (int b = 0; b < count; b += CT / 16) {
+    const int i = b + g;
+    const bool live = i < count;
+    int n = live ? key_at(i) : -1;
+    const bool keep = n >= 0;  // key_at returns -1 for a slot left empty
+    const int nn = keep ? n : 0;
+    const float sc = rank_score16(p, h, nn);
+    if (live && (lane_id() & 15) == 0) {
+      if (keep) {
+        const bool ok = row_allowed(p, nn);
+        comp[i] = entry_comp(ok, sc, nn);
+        flag[i] = (uint8_t)((ok ? 1 : 0) | extra_flag);
+      } else {
+        comp[i] = 0ull;
+        flag[i] = 0;
+      }
+    }
+  }
+}
+
+// Whether row n's code falls in a chosen cell of one of the subspaces [0, s_end).
+SVA_DEV bool in_chosen_cells(const CandParams& p, const uint32_t* member, int64_t code_base, int n, int s_end) {
+  for (int s = 0; s < s_end; ++s) {
+    int64_t c = load_code(p.codes, code_base + (int64_t)n * p.S + s, p.ctype);
+    c = c < 0 ? 0 : (c >= p.C ? p.C - 1 : c);
+    if ((member[s * 8 + (c >> 5)] >> (c & 31)) & 1u) return true;
+  }
+  return false;
+}
+
+__global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
+#pragma clang fp contract(off)
+  __shared__ float score[kMaxSub * 256];
+  __shared__ int topc[kMaxSub * kMaxCells];
+  __shared__ uint32_t member[kMaxSub * 8];  // bit c of subspace s: cell c chosen (C <= 256)
+  __shared__ int lbase[kMaxSub * kMaxCells + 1];
+  const int h = blockIdx.y;
+  const int S = p.S, C = p.C, cells = p.cells;
+  // top cells of every subspace: rank of each cell among its subspace
+  for (int e = threadIdx.x; e < S * C; e += CT) score[e] = p.lut[(int64_t)h * S * C + e] / p.sqrt_r;
+  for (int e = threadIdx.x; e < S * 8; e += CT) member[e] = 0u;
+  for (int e = threadIdx.x; e < S * cells; e += CT) topc[e] = 0;  // NaN scores may leave ranks unfilled
+  __syncthreads();
+  for (int e = threadIdx.x; e < S * C; e += CT) {
+    const int s = e / C, c = e - s * C;
+    const float v = score[e];
+    int rank = 0;
+    for (int o = 0; o < C; ++o) {
+      const float u = score[s * C + o];
+      rank += (u > v) || (u == v && o < c);
+    }
+    if (rank < cells) {
+      topc[s * cells + rank] = c;
+      if (c < 256) atomicOr(&member[s * 8 + (c >> 5)], 1u << (c & 31));
+    }
+  }
+  __syncthreads();
+  const int nlists = S * cells;
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int j = 0; j < nlists; ++j) {
+      const int s = j / cells;
+      const int32_t* off = p.offsets + ((int64_t)h * S + s) * (C + 1);
+      const int c = min(max(topc[j], 0), C - 1);
+      lbase[j] = acc;
+      acc += off[c + 1] - off[c];
+    }
+    lbase[nlists] = acc;
+  }
+  __syncthreads();
+  uint64_t* comp = p.comp + (int64_t)h * p.W;
+  uint8_t* flag = p.flag + (int64_t)h * p.W;
+  const int tail_len = max(0, p.k_len - p.tail_start);
+  const int tail_wgs = (tail_len + TAIL_ROWS - 1) / TAIL_ROWS;
+  const int j = blockIdx.x;
+  // slots: [lists (S*postings_len at most)] [tail] [extra]
+  const int tail_slot0 = S * p.postings_len;
+  const int extra_slot = tail_slot0 + tail_len;
+  if (j < nlists) {
+    const int s = j / cells;
+    const int32_t* off = p.offsets + ((int64_t)h * S + s) * (C + 1);
+    const int c = min(max(topc[j], 0), C - 1);
+    const int o0 = off[c];
+    const int count = off[c + 1] - o0;
+    const int32_t* lst = p.ids + ((int64_t)h * S + s) * p.postings_len + o0;
+    const int64_t cb = (int64_t)h * p.code_hs;
+    score_entries(
+        p, h, count,
+        [&](int i) {
+          const int n = (int)lst[i];
+          // adaptive: distinct keys, each kept by its lowest chosen subspace
+          if (p.adaptive && in_chosen_cells(p, member, cb, n, s)) return -1;
+          return n;
+        },
+        comp + lbase[j], flag + lbase[j], 0);
+  } else if (j < nlists + tail_wgs) {
+    const int t0 = (j - nlists) * TAIL_ROWS;
+    const int count = min(TAIL_ROWS, tail_len - t0);
+    const int64_t cb = (int64_t)h * p.code_hs;
+    score_entries(
+        p, h, count,
+        [&](int i) {
+          const int n = p.tail_start + t0 + i;
+          if (!p.adaptive) return n;
+          return in_chosen_cells(p, member, cb, n, S) ? n : -1;
+        },
+        comp + tail_slot0 + t0, flag + tail_slot0 + t0, 0);
+  } else {
+    // the extra slot, and clearing of list slots past the lists' total
+    for (int i = lbase[nlists] + (int)threadIdx.x; i < tail_slot0; i += CT) comp[i] = 0ull, flag[i] = 0;
+    int n = -1;
+    uint8_t extra = 0;
+    if (!p.adaptive) {
+      if (tail_len == 0) n = p.k_len - 1;
+    } else {
+      n = p.k_len - 1;
+      if (row_allowed(p, n)) {
+        // the current row joins the candidates unless it is one already
+        if (in_chosen_cells(p, member, (int64_t)h * p.code_hs, n, S)) n = -1;
+      } else {
+        // fallback: the last allowed row, used only when nothing else is
+        for (n = p.k_len - 1; n >= 0 && !row_allowed(p, n); --n) {
+        }
+        extra = 2;
+      }
+    }
+    score_entries(p, h, 1, [&](int) { return n; }, comp + extra_slot, flag + extra_slot, extra);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// unique refill select
+
+constexpr int UB = 1024;
+constexpr int UNW = UB / WAVE;
+constexpr uint32_t EMPTY = 0xFFFFFFFFu;
+
+struct SelParams {
+  const uint64_t* comp;
+  const uint8_t* flag;
+  int W;
+  int mode;  // 0 static decode, 1 adaptive decode, 2 plain top-unique
+  int B, min_budget, mid_budget;
+  float low_f, high_f;     // fp32 thresholds (static: tensor comparison)
+  double low_d, high_d;    // fp64 thresholds (adaptive: Python float comparison)
+  int64_t width;           // plain mode: candidate width
+  const int32_t* max_count;  // static: per (head, subspace) largest cell of the postings
+  int n_max;
+  int64_t lists;           // static: S * cells
+  int64_t tail_extra;      // static: tail rows, or 1 (the current row) without a tail
+  int refill_factor;
+  int win_cap;
+  int hash;                // key table slots: a power of 2 >= 2 * win_cap
+  uint64_t* win;           // [H, win_cap] workspace
+  int32_t* fin_idx;        // [H, B] ascending (modes 0, 1)
+  int32_t* fin_count;      // [H]
+  float* stats;            // [H, 4]: summoned, refill_pool, verified, rank_count
+  int32_t* sel_idx;        // mode 2: [H, sel_cap] by score desc
+  float* sel_score;
+  uint8_t* sel_valid;
+  int sel_cap;
+};
+
+SVA_DEV uint32_t hash_key(uint32_t n, int hash) { return (n * 2654435761u) & (uint32_t)(hash - 1); }
+
+__global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int HASH = p.hash;
+  uint64_t* hcomp = (uint64_t*)lds;                        // [HASH] best composite per key
+  uint64_t* sel = hcomp + HASH;                            // [max(B, sel_cap)] chosen composites
+  uint64_t* shared64 = sel + max(p.B, p.sel_cap);          // [4]
+  uint32_t(*whist)[256] = (uint32_t(*)[256])(shared64 + 4);  // [UNW][256]
+  uint32_t* hkey = (uint32_t*)(whist + UNW);               // [HASH]
+  uint32_t* hpos = hkey + HASH;                            // [HASH] first window position of the best
+  uint32_t* scratch = hpos + HASH;                         // [UNW + 1]
+  uint32_t* shared = scratch + UNW + 1;                    // [8]
+  const int h = blockIdx.x;
+  const uint64_t* comp = p.comp + (int64_t)h * p.W;
+  const uint8_t* flag = p.flag + (int64_t)h * p.W;
+  uint64_t* win = p.win + (int64_t)h * p.win_cap;
+  const int W = p.W;
+  // counts: real entries, valid entries
+  uint32_t real = 0, nvalid = 0;
+  for (int i = threadIdx.x; i < W; i += UB) {
+    const uint64_t c = comp[i];
+    real += c != 0ull && !(flag[i] & 2);
+    nvalid += c != 0ull && (flag[i] & 1) && !(flag[i] & 2);
+  }
+  uint32_t Real, Valid;
+  block_excl_scan<UB>(real, scratch, &Real);
+  block_excl_scan<UB>(nvalid, scratch, &Valid);
+  // refill window
+  int64_t width = p.width;
+  if (p.mode == 0) {
+    // the reference's padded layout: S * cells lists of the largest cell's
+    // length, then the tail (or the current row)
+    int mb = 0;
+    for (int i = 0; i < p.n_max; ++i) mb = max(mb, (int)p.max_count[i]);
+    width = p.lists * (int64_t)max(1, mb) + p.tail_extra;
+  }
+  int64_t refill;
+  if (p.mode == 1) refill = Real;
+  else refill = min(width, (int64_t)max(p.B, p.B * p.refill_factor));
+  auto visit_real = [&](auto&& f) {
+    for (int i = threadIdx.x; i < W; i += UB) {
+      const uint64_t c = comp[i];
+      if (c != 0ull && !(flag[i] & 2)) f(c);
+    }
+  };
+  // adaptive mode: the candidates are distinct keys already, so U is read
+  // straight from them; otherwise a refill window and a key table in LDS
+  const bool direct = p.mode == 1;
+  if (threadIdx.x == 0) shared[4] = 0u;
+  if (!direct) {
+    uint64_t X1 = 1ull;
+    if (refill > 0 && (int64_t)Real > refill)
+      X1 = select_largest<UB>(visit_real, (int)refill, whist, scratch, shared64, shared);
+    if (refill <= 0) X1 = ~0ull;
+    // window entries in slot order, with their valid flag in bit 0 of the stored word
+    for (int i = threadIdx.x; i < HASH; i += UB) {
+      hkey[i] = EMPTY;
+      hcomp[i] = 0ull;
+      hpos[i] = EMPTY;
+    }
+    __syncthreads();
+    {
+      const int per = (W + UB - 1) / UB;
+      const int i0 = min(W, (int)threadIdx.x * per), i1 = min(W, i0 + per);
+      uint32_t cnt = 0;
+      for (int i = i0; i < i1; ++i) {
+        const uint64_t c = comp[i];
+        cnt += c != 0ull && !(flag[i] & 2) && c >= X1;
+      }
+      uint32_t tot;
+      uint32_t o = block_excl_scan<UB>(cnt, scratch, &tot);
+      for (int i = i0; i < i1; ++i) {
+        const uint64_t c = comp[i];
+        if (c != 0ull && !(flag[i] & 2) && c >= X1) {
+          if (o < (uint32_t)p.win_cap) {
+            win[o] = c;
+            // key table: best composite per key, then first window position of it
+            const uint32_t n = composite_index(c);
+            uint32_t slot = hash_key(n, HASH);
+            while (true) {
+              const uint32_t prev = atomicCAS(&hkey[slot], EMPTY, n);
+              if (prev == EMPTY || prev == n) break;
+              slot = (slot + 1) & (HASH - 1);
+            }
+            atomicMax((unsigned long long*)&hcomp[slot], (unsigned long long)c);
+          }
+          ++o;
+        }
+      }
+      if (threadIdx.x == 0) shared[4] = min(tot, (uint32_t)p.win_cap);
+    }
+    __syncthreads();
+    // first window position of each key's best copy (copies of a key carry
+    // the same mask value, so the masked score tells validity)
+    const int wn = (int)shared[4];
+    for (int i = threadIdx.x; i < wn; i += UB) {
+      const uint64_t c = win[i];
+      uint32_t slot = hash_key(composite_index(c), HASH);
+      while (hkey[slot] != composite_index(c)) slot = (slot + 1) & (HASH - 1);
+      if (hcomp[slot] == c) atomicMin(&hpos[slot], (uint32_t)i);
+    }
+  }
+  __syncthreads();
+  const int nwin = (int)shared[4];
+  const int ndom = direct ? W : nwin;
+  auto dom = [&](int i) -> uint64_t { return direct ? comp[i] : win[i]; };
+  auto slot_of = [&](uint32_t n) {
+    uint32_t slot = hash_key(n, HASH);
+    while (hkey[slot] != n) slot = (slot + 1) & (HASH - 1);
+    return slot;
+  };
+  // U: allowed distinct keys (the first window position of a key's best copy)
+  auto in_u = [&](int i, uint64_t c) -> bool {
+    if (direct) return c != 0ull && (flag[i] & 3) == 1;
+    const uint32_t slot = slot_of(composite_index(c));
+    return hcomp[slot] == c && hpos[slot] == (uint32_t)i && composite_key(c) != f2key(-FLT_MAX);
+  };
+  uint32_t ucount = 0;
+  for (int i = threadIdx.x; i < ndom; i += UB) ucount += in_u(i, dom(i));
+  uint32_t U;
+  block_excl_scan<UB>(ucount, scratch, &U);
+  // rank count (selected slots) and the budget
+  const int64_t rank_count = p.mode == 1 ? min((int64_t)p.B, (int64_t)U) : min((int64_t)p.B, refill);
+  auto visit_u = [&](auto&& f) {
+    for (int i = threadIdx.x; i < ndom; i += UB) {
+      const uint64_t c = dom(i);
+      if (in_u(i, c)) f(c);
+    }
+  };
+  int budget = (int)rank_count;
+  if (p.mode != 2 && rank_count > 1) {
+    // best and (min_budget)-th best scores of the selected slots; slots past
+    // U hold the masked minimum
+    const int mref = (int)min((int64_t)p.min_budget, rank_count) - 1;
+    uint64_t best = 0ull;
+    visit_u([&](uint64_t c) { best = c > best ? c : best; });
+    for (int off = 1; off < WAVE; off <<= 1) {
+      const uint64_t o = __shfl_xor(best, off, WAVE);
+      best = o > best ? o : best;
+    }
+    if (threadIdx.x == 0) {
+      shared64[2] = 0ull;
+      shared64[3] = ~0ull;
+    }
+    __syncthreads();
+    if (lane_id() == 0) atomicMax((unsigned long long*)&shared64[2], (unsigned long long)best);
+    __syncthreads();
+    const float s0 = U > 0 ? key2f(composite_key(shared64[2])) : -FLT_MAX;
+    float sref = -FLT_MAX;
+    if ((int64_t)U > mref) {
+      const uint64_t Xr = select_largest<UB>(visit_u, mref + 1, whist, scratch, shared64, shared);
+      // the (mref+1)-th largest element is the smallest one >= Xr
+      uint64_t mn = ~0ull;
+      visit_u([&](uint64_t c) { mn = (c >= Xr && c < mn) ? c : mn; });
+      for (int off = 1; off < WAVE; off <<= 1) {
+        const uint64_t o = __shfl_xor(mn, off, WAVE);
+        mn = o < mn ? o : mn;
+      }
+      if (lane_id() == 0) atomicMin((unsigned long long*)&shared64[3], (unsigned long long)mn);
+      __syncthreads();
+      sref = key2f(composite_key(shared64[3]));
+    }
+    const float margin = s0 - sref;
+    if (p.mode == 1) {
+      const double md = (double)margin;
+      budget = md >= p.high_d ? (int)min((int64_t)p.min_budget, rank_count)
+                              : (md >= p.low_d ? (int)min((int64_t)p.mid_budget, rank_count) : (int)rank_count);
+    } else {
+      budget = margin >= p.high_f ? p.min_budget : (margin >= p.low_f ? p.mid_budget : p.B);
+      budget = (int)min((int64_t)budget, rank_count);
+    }
+  } else if (p.mode == 0) {
+    budget = 1;
+  }
+  const int k3 = (int)min((int64_t)budget, (int64_t)U);
+  uint64_t X3 = 1ull;
+  if (k3 > 0 && (int)U > k3) X3 = select_largest<UB>(visit_u, k3, whist, scratch, shared64, shared);
+  // chosen keys (composites) in window order
+  if (k3 > 0) {
+    const int per = (ndom + UB - 1) / UB;
+    const int i0 = min(ndom, (int)threadIdx.x * per), i1 = min(ndom, i0 + per);
+    uint32_t cnt = 0;
+    for (int i = i0; i < i1; ++i) cnt += in_u(i, dom(i)) && dom(i) >= X3;
+    uint32_t tot;
+    uint32_t o = block_excl_scan<UB>(cnt, scratch, &tot);
+    for (int i = i0; i < i1; ++i) {
+      const uint64_t c = dom(i);
+      if (in_u(i, c) && c >= X3 && o < (uint32_t)k3) sel[o++] = c;
+    }
+  }
+  __syncthreads();
+  if (p.mode == 2) {
+    // the selected slots by score desc (key asc on ties), then invalid slots
+    const int slots = (int)min((int64_t)p.sel_cap, rank_count);
+    int32_t* oi = p.sel_idx + (int64_t)h * p.sel_cap;
+    float* os = p.sel_score + (int64_t)h * p.sel_cap;
+    uint8_t* ov = p.sel_valid + (int64_t)h * p.sel_cap;
+    for (int i = threadIdx.x; i < k3; i += UB) {
+      const uint64_t v = sel[i];
+      int r = 0;
+      for (int j = 0; j < k3; ++j) r += sel[j] > v;
+      oi[r] = (int32_t)composite_index(v);
+      os[r] = key2f(composite_key(v));
+      ov[r] = 1;
+    }
+    for (int r = k3 + (int)threadIdx.x; r < slots; r += UB) {
+      oi[r] = 0;
+      os[r] = -FLT_MAX;
+      ov[r] = 0;
+    }
+    if (threadIdx.x == 0) {
+      p.fin_count[h] = slots;
+      p.stats[(int64_t)h * 4 + 1] = (float)refill;
+    }
+    return;
+  }
+  int32_t* out = p.fin_idx + (int64_t)h * p.B;
+  int kfin = k3;
+  if (p.mode == 1 && U == 0) {
+    // no allowed candidate: the last allowed row, when there is one
+    if (threadIdx.x == 0) shared[6] = EMPTY;
+    __syncthreads();
+    for (int i = threadIdx.x; i < W; i += UB)
+      if ((flag[i] & 2) && comp[i] != 0ull) shared[6] = composite_index(comp[i]);
+    __syncthreads();
+    kfin = shared[6] == EMPTY ? 0 : 1;
+    if (threadIdx.x == 0 && kfin) out[0] = (int32_t)shared[6];
+  } else {
+    for (int i = threadIdx.x; i < k3; i += UB) {
+      const uint32_t v = composite_index(sel[i]);
+      int r = 0;
+      for (int j = 0; j < k3; ++j) r += composite_index(sel[j]) < v;
+      out[r] = (int32_t)v;
+    }
+  }
+  if (threadIdx.x == 0) {
+    p.fin_count[h] = kfin;
+    float* st = p.stats + (int64_t)h * 4;
+    st[0] = p.mode == 1 ? (float)max((uint32_t)kfin, U) : (float)Valid;
+    st[1] = p.mode == 1 ? 0.0f : (float)refill;
+    st[2] = (float)kfin;
+    st[3] = (float)rank_count;
+  }
+}
+
+// Generic entries (key, score, valid) -> composites for the plain top-unique
+// selection; the masked score of an invalid entry is -FLT_MAX (finfo.min).
+__global__ void pack_entries_kernel(const int64_t* __restrict__ idx, const float* __restrict__ score,
+                                    const uint8_t* __restrict__ valid, int64_t total, uint64_t* __restrict__ comp,
+                                    uint8_t* __restrict__ flag) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const bool ok = valid[i] != 0;
+  comp[i] = composite(f2key(ok ? score[i] : -FLT_MAX), (uint32_t)idx[i]);
+  flag[i] = ok ? 1 : 0;
+}
+
+size_t select_lds_bytes(int64_t B, int64_t hash) {
+  return sizeof(uint64_t) * (size_t)(hash + B + 4) + sizeof(uint32_t) * (size_t)(UNW * 256 + 2 * hash + UNW + 1 + 8);
+}
+
+int hash_slots(int win_cap) {
+  int h = 256;
+  while (h < 2 * win_cap) h <<= 1;
+  return h;
+}
+
+int win_cap_for(int64_t B, int refill_factor, int64_t W) {
+  // the window holds the best `refill` entries plus the copies of the
+  // boundary key (at most one per list and the tail)
+  return (int)std::min<int64_t>(W, std::max<int64_t>(B, B * refill_factor) + 64);
+}
+
+int launch_select(const SelParams& p, int64_t H, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)unique_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      sva::kMaxLds),
+                  "hipFuncSetAttribute(unique_select_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(unique_select_kernel, dim3((unsigned)H), dim3(UB),
+                     select_lds_bytes(std::max(p.B, p.sel_cap), p.hash), stream, p);
+  SVA_CHECK_LAUNCH("unique_select_kernel");
+  return SVA_OK;
+}
+
+}  // namespace
+
+namespace {
+
+int launch_attr_once(const void* fn, bool& done, const char* name) {
+  if (!done) {
+    SVA_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds), name);
+    done = true;
+  }
+  return SVA_OK;
+}
+
+}  // namespace
+
+extern "C" int sva_postings_build(const void* codes, int code_type, int64_t code_head_stride, int64_t H,
+                                  int64_t n_rows, int64_t S, int64_t C, int32_t* offsets, int32_t* ids,
+                                  int32_t* max_count, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(codes && offsets && ids && max_count, "sva_postings_build: null pointer");
+  SVA_REQUIRE(H > 0 && S > 0 && n_rows >= 0 && n_rows < (1ll << 31) && H * S < (1ll << 31),
+              "sva_postings_build: bad sizes");
+  SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_postings_build: bad code type");
+  SVA_UNSUPPORTED(C > 0 && C <= kMaxPostingCells, "sva_postings_build: %lld codewords (at most %d)", (long long)C,
+                  kMaxPostingCells);
+  static bool attr = false;
+  if (int rc = launch_attr_once((const void*)postings_build_kernel, attr, "hipFuncSetAttribute(postings_build)"))
+    return rc;
+  const size_t lds = sizeof(uint32_t) * (size_t)(2 * C + PNW * C + PNW + 2);
+  hipLaunchKernelGGL(postings_build_kernel, dim3((unsigned)(H * S)), dim3(PB), lds, (hipStream_t)stream, codes,
+                     code_type, code_head_stride, (int)S, (int)n_rows, (int)C, offsets, ids, max_count);
+  SVA_CHECK_LAUNCH("postings_build_kernel");
+  return SVA_OK;
+}
+
+extern "C" int64_t sva_inverted_slots(int64_t S, int64_t postings_len, int64_t k_len, int64_t tail_start) {
+  return S * postings_len + std::max<int64_t>(0, k_len - tail_start) + 1;
+}
+
+extern "C" int sva_inverted_candidates(const float* lut, const float* q_low, const float* k_low,
+                                       int64_t k_low_head_stride, const void* codes, int code_type,
+                                       int64_t code_head_stride, const int32_t* offsets, const int32_t* ids,
+                                       int64_t postings_len, int64_t tail_start, int64_t k_len, int64_t H, int64_t S,
+                                       int64_t C, int64_t R, int64_t cells, const void* mask, int mask_type,
+                                       int adaptive, uint64_t* comp, uint8_t* flag, int64_t slots, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(lut && q_low && k_low && codes && offsets && ids && comp && flag, "sva_inverted_candidates: null pointer");
+  SVA_REQUIRE(H > 0 && H <= 65535 && k_len > 0 && k_len < (1ll << 31) && postings_len >= 0 &&
+                  postings_len <= k_len && tail_start >= 0 && tail_start <= k_len,
+              "sva_inverted_candidates: bad sizes");
+  SVA_UNSUPPORTED(R == 64, "sva_inverted_candidates: rank %lld (64 supported)", (long long)R);
+  SVA_UNSUPPORTED(S > 0 && S <= kMaxSub && C > 0 && C <= 256 && cells > 0 && cells <= std::min<int64_t>(C, kMaxCells),
+                  "sva_inverted_candidates: layout %lldx%lld with %lld cells unsupported", (long long)S, (long long)C,
+                  (long long)cells);
+  SVA_REQUIRE((((uintptr_t)k_low | (uintptr_t)q_low) & 15u) == 0 && k_low_head_stride % 4 == 0,
+              "sva_inverted_candidates: k_low / q_low must be 16-byte aligned");
+  SVA_REQUIRE(slots == sva_inverted_slots(S, postings_len, k_len, tail_start),
+              "sva_inverted_candidates: slots must be sva_inverted_slots(...)");
+  SVA_REQUIRE(mask_type >= 0 && mask_type <= 4 && (mask_type == 0 || mask_type == 4 || mask != nullptr),
+              "sva_inverted_candidates: bad mask");
+  CandParams p;
+  p.lut = lut;
+  p.q_low = q_low;
+  p.k_low = k_low;
+  p.klow_hs = k_low_head_stride;
+  p.codes = codes;
+  p.ctype = code_type;
+  p.code_hs = code_head_stride;
+  p.offsets = offsets;
+  p.ids = ids;
+  p.postings_len = (int)postings_len;
+  p.tail_start = (int)tail_start;
+  p.k_len = (int)k_len;
+  p.H = (int)H;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.R = (int)R;
+  p.cells = (int)cells;
+  p.sqrt_r = (float)std::sqrt((double)R);
+  p.mask = (mask_type == 1 || mask_type == 2 || mask_type == 3) ? mask : nullptr;
+  p.mask_type = mask_type;
+  p.adaptive = adaptive ? 1 : 0;
+  p.W = (int)slots;
+  p.comp = comp;
+  p.flag = flag;
+  const int64_t tail_len = k_len - tail_start;
+  const int64_t wgs = S * cells + (tail_len + TAIL_ROWS - 1) / TAIL_ROWS + 1;
+  SVA_REQUIRE(wgs < (1ll << 31) && slots < (1ll << 31), "sva_inverted_candidates: too many rows");
+  hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)H), dim3(CT), 0, (hipStream_t)stream,
+                     p);
+  SVA_CHECK_LAUNCH("inverted_candidates_kernel");
+  return SVA_OK;
+}
+
+extern "C" size_t sva_unique_select_workspace_bytes(int64_t H, int64_t B, int64_t refill_factor, int64_t slots) {
+  if (H <= 0 || B <= 0 || slots <= 0) return 256;
+  return sizeof(uint64_t) * (size_t)H * (size_t)win_cap_for(B, (int)std::max<int64_t>(1, refill_factor), slots) + 256;
+}
+
+extern "C" int sva_unique_refill_select(const uint64_t* comp, const uint8_t* flag, int64_t slots, int64_t H, int mode,
+                                        int64_t B, int64_t min_budget, int64_t mid_budget, double low_margin,
+                                        double high_margin, int64_t refill_factor, const int32_t* max_count,
+                                        int64_t S, int64_t cells, int64_t tail_len, int32_t* fin_idx,
+                                        int32_t* fin_count, float* stats, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(comp && flag && fin_idx && fin_count && stats && workspace, "sva_unique_refill_select: null pointer");
+  SVA_REQUIRE(mode == 0 || mode == 1, "sva_unique_refill_select: mode 0 (static) or 1 (adaptive)");
+  SVA_REQUIRE(mode == 1 || max_count != nullptr, "sva_unique_refill_select: static mode needs the postings maxima");
+  SVA_REQUIRE(H > 0 && H < (1ll << 31) && slots > 0 && slots < (1ll << 31) && B > 0 && min_budget > 0 &&
+                  mid_budget > 0 && min_budget <= B && mid_budget <= B && refill_factor >= 1,
+              "sva_unique_refill_select: bad sizes");
+  const int win_cap = win_cap_for(B, (int)refill_factor, slots);
+  const int hash = hash_slots(win_cap);
+  const size_t lds = select_lds_bytes(B, hash);
+  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_unique_refill_select: budget %lld needs %zu bytes of LDS",
+                  (long long)B, lds);
+  SVA_REQUIRE(workspace_bytes >= sva_unique_select_workspace_bytes(H, B, refill_factor, slots),
+              "sva_unique_refill_select: workspace too small");
+  SelParams p{};
+  p.comp = comp;
+  p.flag = flag;
+  p.W = (int)slots;
+  p.mode = mode;
+  p.B = (int)B;
+  p.min_budget = (int)min_budget;
+  p.mid_budget = (int)mid_budget;
+  p.low_f = (float)low_margin;
+  p.high_f = (float)high_margin;
+  p.low_d = low_margin;
+  p.high_d = high_margin;
+  p.width = slots;
+  p.max_count = max_count;
+  p.n_max = (int)(H * S);
+  p.lists = S * cells;
+  p.tail_extra = tail_len > 0 ? tail_len : 1;
+  p.refill_factor = (int)refill_factor;
+  p.win_cap = win_cap;
+  p.hash = hash;
+  p.win = (uint64_t*)workspace;
+  p.fin_idx = fin_idx;
+  p.fin_count = fin_count;
+  p.stats = stats;
+  p.sel_cap = 0;
+  return launch_select(p, H, (hipStream_t)stream);
+}
+
+extern "C" size_t sva_top_unique_workspace_bytes(int64_t H, int64_t W, int64_t budget, int64_t refill_factor) {
+  if (H <= 0 || W <= 0 || budget <= 0) return 256;
+  const size_t n = (size_t)H * (size_t)W;
+  return 2 * ((sizeof(uint64_t) * n + 255) & ~(size_t)255) + ((n + 255) & ~(size_t)255) +
+         sizeof(float) * 4 * (size_t)H + sizeof(int32_t) * (size_t)H + 512;
+}
+
+extern "C" int sva_top_unique(const int64_t* idx, const float* scores, const uint8_t* valid, int64_t H, int64_t W,
+                              int64_t budget, int64_t refill_factor, int32_t* sel_idx, float* sel_scores,
+                              uint8_t* sel_valid, void* workspace, size_t workspace_bytes, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(idx && scores && valid && sel_idx && sel_scores && sel_valid && workspace, "sva_top_unique: null pointer");
+  SVA_REQUIRE(H > 0 && H < (1ll << 31) && W > 0 && W < (1ll << 31) && budget > 0 && refill_factor >= 1,
+              "sva_top_unique: bad sizes");
+  SVA_REQUIRE(workspace_bytes >= sva_top_unique_workspace_bytes(H, W, budget, refill_factor),
+              "sva_top_unique: workspace too small");
+  const int64_t refill = std::min<int64_t>(W, std::max<int64_t>(budget, budget * refill_factor));
+  const int64_t cap = std::min<int64_t>(budget, refill);
+  // arbitrary entries may repeat one key any number of times: the window
+  // holds every entry at or above the refill threshold
+  const int win_cap = (int)W;
+  const int hash = hash_slots(win_cap);
+  SVA_UNSUPPORTED(select_lds_bytes(std::max<int64_t>(budget, cap), hash) <= (size_t)sva::kMaxLds,
+                  "sva_top_unique: %lld entries per row too many", (long long)W);
+  char* ws = (char*)workspace;
+  const size_t n = (size_t)H * (size_t)W;
+  uint64_t* comp = (uint64_t*)ws;
+  ws += (sizeof(uint64_t) * n + 255) & ~(size_t)255;
+  uint8_t* flag = (uint8_t*)ws;
+  ws += (n + 255) & ~(size_t)255;
+  uint64_t* win = (uint64_t*)ws;
+  ws += (sizeof(uint64_t) * n + 255) & ~(size_t)255;
+  float* stats = (float*)ws;
+  int32_t* counts = (int32_t*)(stats + 4 * H);
+  const int64_t blocks = ((int64_t)n + 255) / 256;
+  hipLaunchKernelGGL(pack_entries_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, idx, scores, valid,
+                     (int64_t)n, comp, flag);
+  SVA_CHECK_LAUNCH("pack_entries_kernel");
+  SelParams p{};
+  p.comp = comp;
+  p.flag = flag;
+  p.W = (int)W;
+  p.mode = 2;
+  p.B = (int)budget;
+  p.min_budget = (int)budget;
+  p.mid_budget = (int)budget;
+  p.width = W;
+  p.refill_factor = (int)refill_factor;
+  p.win_cap = win_cap;
+  p.hash = hash;
+  p.win = win;
+  p.fin_idx = sel_idx;
+  p.fin_count = counts;
+  p.stats = stats;
+  p.sel_idx = sel_idx;
+  p.sel_score = sel_scores;
+  p.sel_valid = sel_valid;
+  p.sel_cap = (int)cap;
+  return launch_select(p, H, (hipStream_t)stream);
+}

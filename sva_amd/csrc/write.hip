@@ -98,6 +98,7 @@ __global__ void __launch_bounds__(WT) write_encode_kernel(WriteParams p) {
         *reinterpret_cast<float4*>(klow + (n0 + k) * R + rb * 4) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
     }
   }
+  if (p.codes == nullptr) return;  // projection only
   // assignment, one subspace at a time
   const int k = threadIdx.x >> 2;  // row of this lane group
   const int qt = threadIdx.x & 3;
@@ -182,7 +183,7 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
                                 int64_t k_low_head_stride, void* codes, int code_type, int64_t code_head_stride,
                                 void* stream) {
   sva::clear_error();
-  SVA_REQUIRE(keys && k_proj && codebooks && k_low && codes, "sva_write_encode: null pointer");
+  SVA_REQUIRE(keys && k_proj && codebooks && k_low, "sva_write_encode: null pointer");
   SVA_REQUIRE(row_begin >= 0 && n_rows >= 0, "sva_write_encode: bad row range");
   SVA_REQUIRE(H > 0 && G > 0 && H % G == 0, "sva_write_encode: %lld query heads over %lld KV heads", (long long)H,
               (long long)G);

@@ -50,10 +50,11 @@ def _f32c(t: torch.Tensor) -> torch.Tensor:
 
 
 def write_encode(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tensor, k_low: torch.Tensor,
-                 codes: torch.Tensor, row_begin: int = 0, n_rows: int | None = None) -> None:
+                 codes: torch.Tensor | None, row_begin: int = 0, n_rows: int | None = None) -> None:
     """Fill k_low [H, rows, R] and codes [H, rows, S] for cache rows
     [row_begin, row_begin + n_rows) from keys [G, rows, D] (sva/llama.py:597-616,
-    sva/ops.py:10-47).  k_low and codes are written in place."""
+    sva/ops.py:10-47).  k_low and codes are written in place; codes=None
+    projects only."""
 
     if keys.dim() != 3 or keys.stride(-1) != 1:
         raise ValueError("keys must be [G, rows, D] with contiguous rows")
@@ -64,12 +65,13 @@ def write_encode(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tens
     if k_low.dim() != 3 or k_low.shape[0] != heads or k_low.shape[2] != rank or k_low.stride(1) != rank \
             or k_low.stride(2) != 1 or k_low.dtype != torch.float32:
         raise ValueError("k_low must be fp32 [H, rows, R] with contiguous rows")
-    if codes.dim() != 3 or codes.shape[0] != heads or codes.shape[2] != subspaces or codes.stride(1) != subspaces \
-            or codes.stride(2) != 1:
+    if codes is not None and (codes.dim() != 3 or codes.shape[0] != heads or codes.shape[2] != subspaces
+                              or codes.stride(1) != subspaces or codes.stride(2) != 1):
         raise ValueError("codes must be [H, rows, S] with contiguous rows")
     rows = keys.shape[1]
     n_rows = rows - row_begin if n_rows is None else n_rows
-    if row_begin < 0 or n_rows < 0 or row_begin + n_rows > min(rows, k_low.shape[1], codes.shape[1]):
+    limit = min(rows, k_low.shape[1], codes.shape[1] if codes is not None else rows)
+    if row_begin < 0 or n_rows < 0 or row_begin + n_rows > limit:
         raise ValueError("row range outside the catalog")
     device = require_device(keys, k_proj, codebooks, k_low, codes)
     k_proj = _f32c(k_proj)
@@ -78,7 +80,8 @@ def write_encode(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tens
         lib().sva_write_encode(
             ptr(keys), dtype_code(keys), keys.stride(0), keys.stride(1), row_begin, n_rows, heads, keys.shape[0], dim,
             rank, subspaces, codewords, ptr(k_proj), ptr(codebooks), ptr(k_low), k_low.stride(0), ptr(codes),
-            code_type(codes), codes.stride(0), stream_handle(device),
+            code_type(codes) if codes is not None else 0, codes.stride(0) if codes is not None else 0,
+            stream_handle(device),
         ),
         "sva_write_encode",
     )

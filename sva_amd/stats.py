@@ -1,0 +1,91 @@
+"""Runtime accounting of patched attention layers (sva/stats.py:13-54).
+
+Same interface as the reference (``totals``, ``by_layer``, ``reset``, ``add``,
+``ratio``, ``summary``).  Counts that live on the GPU (shortlist and budget
+sizes of a decode step) are recorded with ``add_device`` and summed there;
+they are brought to the host only when the statistics are read, so a decode
+step never waits on a device-to-host copy for its bookkeeping.
+"""
+
+from __future__ import annotations
+
+from collections import defaultdict
+
+import torch
+
+
+def _float_stats() -> defaultdict[str, float]:
+    return defaultdict(float)
+
+
+class SVAStats:
+    """Aggregate statistics recorded by patched attention layers."""
+
+    def __init__(self) -> None:
+        self._totals: defaultdict[str, float] = _float_stats()
+        self._by_layer: defaultdict[int, defaultdict[str, float]] = defaultdict(_float_stats)
+        # (layer, name) -> float64 device accumulator not yet folded in
+        self._pending: dict[tuple[int, str], torch.Tensor] = {}
+
+    # -- recording --------------------------------------------------------
+    def add(self, layer_idx: int, values: dict[str, float]) -> None:
+        layer = self._by_layer[layer_idx]
+        for key, value in values.items():
+            self._totals[key] += float(value)
+            layer[key] += float(value)
+
+    def add_device(self, layer_idx: int, values: dict[str, torch.Tensor | float]) -> None:
+        """Accumulate device tensors (summed) or host floats without a sync."""
+
+        host = {}
+        for key, value in values.items():
+            if isinstance(value, torch.Tensor):
+                total = value.sum(dtype=torch.float64)
+                slot = self._pending.get((layer_idx, key))
+                self._pending[(layer_idx, key)] = total if slot is None else slot + total
+            else:
+                host[key] = value
+        if host:
+            self.add(layer_idx, host)
+
+    def _flush(self) -> None:
+        if not self._pending:
+            return
+        pending, self._pending = self._pending, {}
+        for (layer_idx, key), value in pending.items():
+            v = float(value.item())
+            self._totals[key] += v
+            self._by_layer[layer_idx][key] += v
+
+    # -- reading ----------------------------------------------------------
+    @property
+    def totals(self) -> defaultdict[str, float]:
+        self._flush()
+        return self._totals
+
+    @property
+    def by_layer(self) -> defaultdict[int, defaultdict[str, float]]:
+        self._flush()
+        return self._by_layer
+
+    def reset(self) -> None:
+        self._pending.clear()
+        self._totals.clear()
+        self._by_layer.clear()
+
+    def ratio(self, numerator: str, denominator: str = "queries") -> float:
+        totals = self.totals
+        den = totals.get(denominator, 0.0)
+        if den <= 0:
+            return float("nan")
+        return totals.get(numerator, 0.0) / den
+
+    def summary(self) -> dict[str, float]:
+        per_query = ("summoned", "refill_pool", "exact_scored", "verified", "cell_visits")
+        out = {"queries": self.totals.get("queries", 0.0)}
+        out.update({f"avg_{k}": self.ratio(k) for k in per_query})
+        for k in ("catalog", "refill", "budget", "gather", "exact_score", "aggregate", "total"):
+            out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_calls")
+        for k in ("projection", "key_catalog", "outer_total"):
+            out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_outer_calls")
+        return out

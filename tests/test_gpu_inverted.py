@@ -1,0 +1,195 @@
+"""GPU parity of the inverted-index decode paths against the oracle.
+
+Postings (CSR) equal the oracle's exactly; the unique refill selection
+reproduces the reference's known-answer test and brute force; static and
+adaptive decode give the oracle's chosen key sets per head (bit-exact index
+sets: same LUT, same rank scores, rule score desc / key asc), its
+statistics, and outputs within 1e-5 of its float64 verifier.  Catalog inputs
+(k_low, codes) come from sva_write_encode, whose parity is tested on its own.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _catalog(device, H=9, G=3, N=6000, D=64, R=64, S=2, C=256, seed=0):
+    from sva_amd import kernels
+
+    rng = np.random.default_rng(seed)
+    keys = rng.standard_normal((G, N, D)).astype(np.float32)
+    values = rng.standard_normal((G, N, D)).astype(np.float32)
+    q = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    k_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    q_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    scale = np.ones(H, np.float32)
+    cb = rng.standard_normal((H, S, C, R // S)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    k_low = torch.empty(H, N, R, device=device)
+    codes = torch.empty(H, N, S, device=device, dtype=torch.uint8)
+    kernels.write_encode(t(keys), t(k_proj), t(cb), k_low, codes)
+    torch.cuda.synchronize()
+    return SimpleNamespace(keys=keys, values=values, q=q, q_proj=q_proj, scale=scale, cb=cb, k_low_t=k_low,
+                           codes_t=codes, k_low=k_low.cpu().numpy(), codes=codes.cpu().numpy(), t=t, H=H, N=N, S=S,
+                           C=C, D=D)
+
+
+def _module(cat, device, mode, budget, cells, amin=None, amid=None, postings=None):
+    from sva_amd.llama import SVALlamaAttention, SVALlamaServingConfig
+    from sva_amd.stats import SVAStats
+
+    serving = SVALlamaServingConfig(rank_dim=64, coarse_shortlist=4 * budget, budget=budget, summon_mode=mode,
+                                    inverted_cells_per_subspace=cells, adaptive_min_budget=amin,
+                                    adaptive_mid_budget=amid)
+    return SimpleNamespace(serving=serving, sva_coarse_codebooks=cat.t(cat.cb), sva_q_proj=cat.t(cat.q_proj),
+                           sva_scale=cat.t(cat.scale), _postings=postings, scaling=cat.D ** -0.5, stats=SVAStats(),
+                           layer_idx=0, _profile_now=SVALlamaAttention._profile_now,
+                           _profile_elapsed_ms=SVALlamaAttention._profile_elapsed_ms)
+
+
+def test_postings_match_oracle(device):
+    from sva_amd import inverted
+
+    for C, n, skew in ((256, 5000, False), (16, 3001, True), (1024, 777, False), (64, 0, False)):
+        rng = np.random.default_rng(C + n)
+        codes = rng.integers(0, C, (3, max(n, 1), 2)).astype(np.int32)
+        if skew:
+            codes[:, : n // 2, 1] = 5
+        ct = torch.from_numpy(codes.astype(np.int16 if C > 256 else np.uint8)).to(device)
+        p = inverted.build_postings(ct, n, C)
+        torch.cuda.synchronize()
+        counts, offsets, ids = oracle.rebuild_postings(codes[:, :n], C)
+        np.testing.assert_array_equal(p.offsets.cpu().numpy(), offsets)
+        if n:
+            np.testing.assert_array_equal(p.ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(p.max_count.cpu().numpy(), counts.max(-1))
+
+
+def test_top_unique_known_answer(device):
+    # tests/test_sva_llama_adapter.py:58-73 of the reference
+    from sva_amd.llama import SVALlamaAttention
+
+    idx = torch.tensor([[4, 4, 3, 3, 2, 1]], device=device)
+    scores = torch.tensor([[9.0, 8.5, 8.0, 7.5, 7.0, 6.0]], device=device)
+    valid = torch.ones_like(idx, dtype=torch.bool)
+    sel, sc, ok, refill = SVALlamaAttention._top_unique_candidates(idx, scores, valid, budget=3, refill_factor=2)
+    assert refill == 6
+    assert sel[ok].tolist() == [4, 3, 2]
+    assert sc[ok].tolist() == [9.0, 8.0, 7.0]
+
+
+def test_top_unique_brute_force(device):
+    from sva_amd import inverted
+
+    rng = np.random.default_rng(7)
+    for trial in range(40):
+        rows, w = int(rng.integers(1, 5)), int(rng.integers(1, 60))
+        budget = int(rng.integers(1, 14))
+        ids = rng.integers(0, 20, (rows, w))
+        scores = (rng.integers(0, 7, (rows, w)) / 2).astype(np.float32)
+        valid = rng.random((rows, w)) < 0.8
+        t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+        sel, sc, ok, refill = inverted.top_unique_candidates(t(ids), t(scores), t(valid), budget)
+        sel, sc, ok = sel.cpu().numpy(), sc.cpu().numpy(), ok.cpu().numpy()
+        for r in range(rows):
+            e_ids, e_sc, e_ok, e_refill = oracle.top_unique_candidates(ids[r], scores[r], valid[r], budget)
+            assert refill == e_refill
+            assert sel.shape[1] == len(e_ids)
+            np.testing.assert_array_equal(ok[r], e_ok)
+            np.testing.assert_array_equal(sel[r][ok[r]], e_ids[e_ok])
+            np.testing.assert_array_equal(sc[r][ok[r]], e_sc[e_ok])
+
+
+def _check_decode(cat, res, ref, rtol=1e-5):
+    out, fin_idx, fin_count, stats = res
+    out = out[0, :, 0].float().cpu().numpy()
+    fin_idx, fin_count, stats = fin_idx.cpu().numpy(), fin_count.cpu().numpy(), stats.cpu().numpy()
+    for h in range(cat.H):
+        want = np.sort(ref["heads"][h]["final"])
+        got = fin_idx[h, : fin_count[h]]
+        np.testing.assert_array_equal(got, want, err_msg=f"head {h}")
+        err = np.abs(out[h] - ref["out"][h]).max() / max(np.abs(ref["out"][h]).max(), 1e-30)
+        assert err <= rtol, f"head {h}: rel err {err}"
+    assert float(stats[:, 0].sum()) == ref["stats"]["summoned"]
+    assert float(fin_count.sum()) == ref["stats"]["verified"]
+    if "refill_pool" in ref["stats"]:
+        assert float(stats[:, 1].sum()) == ref["stats"]["refill_pool"]
+
+
+@pytest.mark.parametrize("tail,amin,amid,masked", [(10, None, None, False), (0, 32, 64, False), (37, 16, 48, True),
+                                                   (1, 1, 2, False)])
+def test_static_decode_matches_oracle(device, tail, amin, amid, masked):
+    from sva_amd import inverted
+
+    cat = _catalog(device, seed=tail + 3)
+    N, budget, cells = cat.N, 128, 8
+    plen = N - tail
+    post = inverted.build_postings(cat.codes_t, plen, cat.C)
+    mod = _module(cat, device, "inverted_static", budget, cells, amin, amid, post)
+    allowed = np.ones(N, bool)
+    mask = None
+    if masked:
+        rng = np.random.default_rng(1)
+        allowed = rng.random(N) < 0.7
+        m = np.where(allowed, 0.0, np.finfo(np.float32).min).astype(np.float32)[None, None, None, :]
+        mask = torch.from_numpy(m).to(device)
+    res = inverted.static_decode(mod, cat.t(cat.q), cat.t(cat.keys), cat.t(cat.values), cat.k_low_t, cat.codes_t, N,
+                                 mask, budget, return_selection=True)
+    ql = oracle.query_low(cat.q[0], cat.q_proj, cat.scale)
+    ref = oracle.static_decode(cat.q[0], cat.keys, cat.values, ql, cat.k_low, cat.cb,
+                               oracle.rebuild_postings(cat.codes[:, :plen], cat.C), plen, budget, cells, cat.D ** -0.5,
+                               adaptive_min=amin, adaptive_mid=amid, allowed=allowed)
+    _check_decode(cat, res, ref)
+
+
+@pytest.mark.parametrize("appended,amin,amid,masked", [(0, None, None, False), (300, 16, 48, False),
+                                                       (50, 32, 64, True)])
+def test_adaptive_decode_matches_oracle(device, appended, amin, amid, masked):
+    from sva_amd import inverted
+
+    cat = _catalog(device, seed=appended + 11)
+    N, budget, cells = cat.N, 128, 8
+    post = inverted.build_postings(cat.codes_t, N - appended, cat.C)  # rows past it: found by their codes
+    mod = _module(cat, device, "inverted", budget, cells, amin, amid, post)
+    allowed = np.ones(N, bool)
+    mask = None
+    if masked:
+        rng = np.random.default_rng(2)
+        allowed = rng.random(N) < 0.6
+        allowed[-1] = False  # the current row disallowed: not a candidate
+        m = np.where(allowed, 0.0, np.finfo(np.float32).min).astype(np.float32)[None, None, None, :]
+        mask = torch.from_numpy(m).to(device)
+    res = inverted.adaptive_decode(mod, cat.t(cat.q), cat.t(cat.keys), cat.t(cat.values), cat.k_low_t, cat.codes_t, N,
+                                   mask, budget, return_selection=True)
+    ql = oracle.query_low(cat.q[0], cat.q_proj, cat.scale)
+    ref = oracle.inverted_decode(cat.q[0], cat.keys, cat.values, ql, cat.k_low, cat.cb, cat.codes, budget, cells,
+                                 cat.D ** -0.5, adaptive_min=amin, adaptive_mid=amid, allowed=allowed)
+    _check_decode(cat, res, ref)
+
+
+def test_adaptive_decode_fallback_to_last_allowed_row(device):
+    # no allowed key in the chosen cells and the current row masked: the last
+    # allowed row is the only candidate (sva/llama.py:380-381)
+    from sva_amd import inverted
+
+    cat = _catalog(device, N=500, seed=5)
+    N = cat.N
+    post = inverted.build_postings(cat.codes_t, N, cat.C)
+    mod = _module(cat, device, "inverted", 16, 2, None, None, post)
+    allowed = np.zeros(N, bool)
+    allowed[123] = True
+    ql = oracle.query_low(cat.q[0], cat.q_proj, cat.scale)
+    m = np.where(allowed, 0.0, np.finfo(np.float32).min).astype(np.float32)[None, None, None, :]
+    res = inverted.adaptive_decode(mod, cat.t(cat.q), cat.t(cat.keys), cat.t(cat.values), cat.k_low_t, cat.codes_t,
+                                   N, torch.from_numpy(m).to(device), 16, return_selection=True)
+    ref = oracle.inverted_decode(cat.q[0], cat.keys, cat.values, ql, cat.k_low, cat.cb, cat.codes, 16, 2,
+                                 cat.D ** -0.5, allowed=allowed)
+    _check_decode(cat, res, ref)
