@@ -64,8 +64,9 @@ int sva_abi_version(void);
  *   k_low     (h, row, r) at h*k_low_head_stride + row*R + r, fp32 out
  *   codes     (h, row, s) at h*code_head_stride + row*S + s, code_type out;
  *             NULL: k_low only (the reference's lazy static tail, :604-610)
- *   R/S must be a multiple of 4; D, R <= 256.  Rows keep no state: writing a
- *   row twice gives the same result.
+ *   D, R <= 256.  Rows keep no state: writing a row twice gives the same
+ *   result.  (R, R/S multiples of 4 and 16-byte aligned fp32 buffers take the
+ *   tiled path; other shapes an elementwise one with the same arithmetic.)
  */
 int sva_write_encode(const void *keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                      int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R, int64_t S,
@@ -150,7 +151,7 @@ int sva_budget_select(const int32_t *sl_idx, const float *sl_rank, const int32_t
  *   fin_count [items]; indices outside [0, len) of their sequence are
  *   skipped, so every read stays in bounds
  *   out (b, h, t, d) at b*out_seq_stride + h*out_head_stride + t*out_tok_stride + d
- *   head_dim must be a multiple of 16 (<= 256).
+ *   head_dim <= 256 (multiples of 16 take the vectorized path).
  * workspace: sva_verify_workspace_bytes(...) bytes (no state between calls).
  */
 size_t sva_verify_workspace_bytes(int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B);
@@ -192,7 +193,7 @@ int64_t sva_inverted_slots(int64_t S, int64_t postings_len, int64_t k_len, int64
  * as a fallback).  Each entry gets its rank score (k_low . q_low) / sqrt(R)
  * in torch's order.
  * Replaces sva/llama.py:359-392 (adaptive) and :451-495 (static).
- *   lut [H, S, C] (sva_query_lut, one token), q_low [H, R], R = 64
+ *   lut [H, S, C] (sva_query_lut, one token), q_low [H, R]
  *   mask: NULL / SVA_MASK_NONE / SVA_MASK_BOOL (every row allowed) or the
  *         token's additive mask row [k_len] (allowed iff > -1e4)
  *   comp [H, slots] uint64 out: (order-preserving key of the masked score

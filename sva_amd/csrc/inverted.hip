@@ -157,11 +157,18 @@ SVA_DEV bool row_allowed(const CandParams& p, int n) {
   return p.mask == nullptr || mask_allows(p.mask, n, p.mask_type);
 }
 
-// Rank score of key n (16 lanes), torch's order, then / sqrt(R).  R == 64.
+// Rank score of key n (16 lanes), torch's order, then / sqrt(R).  R == 64
+// splits the row over the 16 lanes; other ranks are summed by the group's
+// first lane.
 SVA_DEV float rank_score16(const CandParams& p, int h, int n) {
 #pragma clang fp contract(off)
-  const float* row = p.k_low + (int64_t)h * p.klow_hs + (int64_t)n * 64;
-  const float* q = p.q_low + (int64_t)h * 64;
+  const float* row = p.k_low + (int64_t)h * p.klow_hs + (int64_t)n * p.R;
+  const float* q = p.q_low + (int64_t)h * p.R;
+  if (p.R != 64) {
+    float t = 0.0f;
+    if ((lane_id() & 15) == 0) t = torch_order_dot(row, q, p.R);
+    return __shfl(t, 0, 16) / p.sqrt_r;
+  }
   const int j = lane_id() & 15;
   const float4 r = reinterpret_cast<const float4*>(row)[j];
   const float4 qq = reinterpret_cast<const float4*>(q)[j];
@@ -689,11 +696,11 @@ extern "C" int sva_inverted_candidates(const float* lut, const float* q_low, con
   SVA_REQUIRE(H > 0 && H <= 65535 && k_len > 0 && k_len < (1ll << 31) && postings_len >= 0 &&
                   postings_len <= k_len && tail_start >= 0 && tail_start <= k_len,
               "sva_inverted_candidates: bad sizes");
-  SVA_UNSUPPORTED(R == 64, "sva_inverted_candidates: rank %lld (64 supported)", (long long)R);
+  SVA_UNSUPPORTED(R > 0 && R <= 511, "sva_inverted_candidates: rank %lld unsupported", (long long)R);
   SVA_UNSUPPORTED(S > 0 && S <= kMaxSub && C > 0 && C <= 256 && cells > 0 && cells <= std::min<int64_t>(C, kMaxCells),
                   "sva_inverted_candidates: layout %lldx%lld with %lld cells unsupported", (long long)S, (long long)C,
                   (long long)cells);
-  SVA_REQUIRE((((uintptr_t)k_low | (uintptr_t)q_low) & 15u) == 0 && k_low_head_stride % 4 == 0,
+  SVA_REQUIRE(R != 64 || ((((uintptr_t)k_low | (uintptr_t)q_low) & 15u) == 0 && k_low_head_stride % 4 == 0),
               "sva_inverted_candidates: k_low / q_low must be 16-byte aligned");
   SVA_REQUIRE(slots == sva_inverted_slots(S, postings_len, k_len, tail_start),
               "sva_inverted_candidates: slots must be sva_inverted_slots(...)");

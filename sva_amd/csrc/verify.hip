@@ -83,8 +83,9 @@ SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[
   for (int k = 0; k < 4; ++k) v[k] = load_elem(base, e + k, dtype);
 }
 
-// DT: compile-time head_dim (0: runtime p.D).  Each of the 4 lanes of an
-// entry holds D/4 consecutive dimensions of its K and V rows.
+// DT: compile-time head_dim (0: runtime p.D, a multiple of 16; -1: any
+// head_dim, elementwise).  Each of the 4 lanes of an entry holds D/4
+// consecutive dimensions of its K and V rows (every 4th one for DT = -1).
 template <int DT>
 __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
 #pragma clang fp contract(off)
@@ -165,9 +166,23 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
     float dot[MAX_GRP];
 #pragma unroll
     for (int j = 0; j < MAX_GRP; ++j) dot[j] = 0.0f;
-    if (mem != 0u) {
+    if (DT < 0) {
+      // any head_dim: lane qt takes dimensions qt, qt + 4, ...
+      if (mem != 0u) {
+        const int64_t rowb = (int64_t)g * p.kv_hs + (off + ekey[r]) * p.kv_rs;
+        for (int d = qt; d < D; d += 4) {
+          const float kk = load_elem(p.keys, rowb + d, p.kv_dtype);
+          vrow[r * (D + 1) + d] = load_elem(p.values, rowb + d, p.kv_dtype);
+#pragma unroll
+          for (int j = 0; j < MAX_GRP; ++j)
+            if (j < grp) dot[j] = __builtin_fmaf(kk, qv[j * D + d], dot[j]);
+        }
+      } else if (r < n) {
+        for (int d = qt; d < D; d += 4) vrow[r * (D + 1) + d] = 0.0f;  // weight 0 must not meet NaN
+      }
+    } else if (mem != 0u) {
       const int64_t rowe = (int64_t)g * p.kv_hs + (off + ekey[r]) * p.kv_rs + qt * dq;
-      constexpr int NCH = (DT > 0 ? DT : MAX_D) / 16;  // 4-element chunks per lane
+      constexpr int NCH = (DT > 0 ? DT : MAX_D) / 16;  // 4-element chunks per lane (DT >= 0)
       float kv[NCH][4], vv[NCH][4];
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
@@ -328,8 +343,7 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   SVA_REQUIRE(n_seq > 0 && H > 0 && G > 0 && Q > 0 && B > 0 && n_keys > 0, "sva_verify: bad sizes");
   SVA_REQUIRE(H % G == 0 && H / G <= MAX_GRP, "sva_verify: %lld query heads over %lld KV heads unsupported",
               (long long)H, (long long)G);
-  SVA_REQUIRE(D > 0 && D <= MAX_D && D % 16 == 0, "sva_verify: head_dim %lld must be a multiple of 16 up to %d",
-              (long long)D, MAX_D);
+  SVA_REQUIRE(D > 0 && D <= MAX_D, "sva_verify: head_dim %lld out of range (at most %d)", (long long)D, MAX_D);
   SVA_REQUIRE(q_dtype >= 0 && q_dtype <= 2 && kv_dtype >= 0 && kv_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
               "sva_verify: bad dtype");
   const int64_t grp = H / G;
@@ -376,7 +390,8 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   int rc = SVA_OK;
   if (D == 64) rc = launch_part<64>(p, grid, lds, (hipStream_t)stream);
   else if (D == 128) rc = launch_part<128>(p, grid, lds, (hipStream_t)stream);
-  else rc = launch_part<0>(p, grid, lds, (hipStream_t)stream);
+  else if (D % 16 == 0) rc = launch_part<0>(p, grid, lds, (hipStream_t)stream);
+  else rc = launch_part<-1>(p, grid, lds, (hipStream_t)stream);
   if (rc != SVA_OK) return rc;
   hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,
                      (hipStream_t)stream, p);

@@ -156,6 +156,44 @@ __global__ void __launch_bounds__(WT) write_encode_kernel(WriteParams p) {
   }
 }
 
+// Any shape: one thread per row, the same arithmetic as the tiled kernel.
+__global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p) {
+#pragma clang fp contract(off)
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int sub = R / S;
+  const int h = blockIdx.y;
+  const int g = h / (p.H / p.G);
+  const int64_t n = p.row0 + (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (n >= p.row0 + p.n_rows) return;
+  const int64_t kb = (int64_t)g * p.kv_hs + n * p.kv_rs;
+  const float* W = p.k_proj + (int64_t)h * D * R;
+  float* x = p.k_low + (int64_t)h * p.klow_hs + n * R;
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(load_elem(p.keys, kb + d, p.kv_dtype), W[d * R + r], acc);
+    x[r] = acc;
+  }
+  if (p.codes == nullptr) return;
+  for (int s = 0; s < S; ++s) {
+    const float* xs = x + s * sub;
+    const float xx = torch_order_dot(xs, xs, sub);
+    const float* cbs = p.codebooks + ((int64_t)h * S + s) * C * sub;
+    float best = INFINITY;
+    int arg = 0;
+    for (int c = 0; c < C; ++c) {
+      const float* cr = cbs + (int64_t)c * sub;
+      float xc = 0.0f;
+      for (int j = 0; j < sub; ++j) xc = __builtin_fmaf(xs[j], cr[j], xc);
+      const float dist = (xx - 2.0f * xc) + torch_order_dot(cr, cr, sub);
+      if (dist < best) {
+        best = dist;
+        arg = c;
+      }
+    }
+    store_code(p.codes, (int64_t)h * p.code_hs + n * S + s, p.ctype, arg);
+  }
+}
+
 size_t write_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C) {
   const int64_t sub = R / S;
   return sizeof(float) * (size_t)(D * R + KT * (D + 1) + KT * (R + 1) + C * (sub + CB_PAD) + C + KT) + 16;
@@ -187,19 +225,18 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   SVA_REQUIRE(row_begin >= 0 && n_rows >= 0, "sva_write_encode: bad row range");
   SVA_REQUIRE(H > 0 && G > 0 && H % G == 0, "sva_write_encode: %lld query heads over %lld KV heads", (long long)H,
               (long long)G);
-  SVA_REQUIRE(D > 0 && D <= 256 && R > 0 && R <= 256 && R % 4 == 0 && (D * R) % 4 == 0,
-              "sva_write_encode: head_dim %lld / rank %lld unsupported", (long long)D, (long long)R);
-  SVA_REQUIRE(S > 0 && R % S == 0 && (R / S) % 4 == 0,
-              "sva_write_encode: rank_dim=%lld must be divisible by subspaces=%lld into multiples of 4", (long long)R,
-              (long long)S);
+  SVA_REQUIRE(D > 0 && D <= 256 && R > 0 && R <= 256, "sva_write_encode: head_dim %lld / rank %lld unsupported",
+              (long long)D, (long long)R);
+  SVA_REQUIRE(S > 0 && R % S == 0, "sva_write_encode: rank_dim=%lld must be divisible by subspaces=%lld",
+              (long long)R, (long long)S);
   SVA_REQUIRE(C > 0, "sva_write_encode: codewords %lld", (long long)C);
   SVA_REQUIRE(kv_dtype >= 0 && kv_dtype <= 2 && code_type >= 0 && code_type <= 3, "sva_write_encode: bad dtype");
   const int64_t code_max = code_type == 0 ? 256 : code_type == 1 ? 32768 : (1ll << 31);
   SVA_REQUIRE(C <= code_max, "sva_write_encode: %lld codewords do not fit the code type", (long long)C);
-  SVA_REQUIRE((((uintptr_t)k_proj | (uintptr_t)codebooks | (uintptr_t)k_low) & 15u) == 0 && k_low_head_stride % 4 == 0,
-              "sva_write_encode: k_proj / codebooks / k_low must be 16-byte aligned fp32");
   const size_t lds = write_lds_bytes(D, R, S, C);
-  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_write_encode: %zu bytes of LDS needed", lds);
+  const bool tiled = R % 4 == 0 && (R / S) % 4 == 0 && k_low_head_stride % 4 == 0 &&
+                     (((uintptr_t)k_proj | (uintptr_t)codebooks | (uintptr_t)k_low) & 15u) == 0 &&
+                     lds <= (size_t)sva::kMaxLds;
   if (n_rows == 0) return SVA_OK;
   const int64_t tiles = (n_rows + KT - 1) / KT;
   SVA_REQUIRE(tiles < (1ll << 31) && H <= 65535, "sva_write_encode: too many rows or heads");
@@ -224,6 +261,11 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   p.ctype = code_type;
   p.code_hs = code_head_stride;
   const dim3 grid((unsigned)tiles, (unsigned)H);
+  if (!tiled) {
+    hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, (hipStream_t)stream, p);
+    SVA_CHECK_LAUNCH("write_encode_rowwise_kernel");
+    return SVA_OK;
+  }
   switch (R / S) {
     case 8: return launch_write<8>(p, grid, lds, (hipStream_t)stream);
     case 16: return launch_write<16>(p, grid, lds, (hipStream_t)stream);

@@ -1,0 +1,177 @@
+"""The drop-in adapter on the GPU: the reference's adapter tests
+(tests/test_sva_llama_adapter.py of the reference) run against sva_amd with
+the model on cuda:0, plus end-to-end equivalence: with a shortlist and a
+budget that cover every key, SVA attention is exact attention, so the patched
+model's logits equal the unpatched model's (eager attention, fp32) for
+prefill and cached decode in every summon mode.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+from transformers import LlamaConfig, LlamaForCausalLM
+
+from sva_amd import SVAArtifactBundle, SVALayerArtifacts, SVALlamaAttention, patch_llama_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def make_tiny_model(device, hidden=16, heads=2, kv_heads=2, layers=2, attn="sdpa", seed=0):
+    torch.manual_seed(seed)
+    config = LlamaConfig(vocab_size=64, hidden_size=hidden, intermediate_size=2 * hidden, num_hidden_layers=layers,
+                         num_attention_heads=heads, num_key_value_heads=kv_heads, max_position_embeddings=256,
+                         rope_theta=10000.0, tie_word_embeddings=False, attn_implementation=attn)
+    model = LlamaForCausalLM(config)
+    model.eval()
+    return model.to(device)
+
+
+def make_tiny_bundle(heads=2, head_dim=8, rank=4, subspaces=2, codewords=8, layers=2, shortlist=4, budget=2):
+    generator = torch.Generator().manual_seed(11)
+    arts = {}
+    for i in range(layers):
+        arts[i] = SVALayerArtifacts(
+            q_proj=torch.randn(heads, head_dim, rank, generator=generator),
+            k_proj=torch.randn(heads, head_dim, rank, generator=generator),
+            logit_scale=torch.zeros(heads),
+            coarse_codebooks=torch.randn(heads, subspaces, codewords, rank // subspaces, generator=generator),
+            train_loss=0.0, hard_loss=0.0, route_source="qk")
+    manifest = {"schema_version": 1, "artifact_type": "summon_verify_attention", "rank_dim": rank,
+                "coarse_subspaces": subspaces, "coarse_codewords": codewords, "default_shortlist": shortlist,
+                "default_budget": budget, "layer_count": layers, "layers": list(range(layers))}
+    return SVAArtifactBundle(manifest=manifest, layers=arts)
+
+
+def ids(device, *tokens):
+    return torch.tensor([list(tokens)], device=device)
+
+
+def test_patch_prefill_unpatch(device):
+    model = make_tiny_model(device)
+    bundle = make_tiny_bundle()
+    original = model.model.layers[0].self_attn
+    handle = patch_llama_attention(model, bundle)
+    assert isinstance(model.model.layers[0].self_attn, SVALlamaAttention)
+    with torch.no_grad():
+        output = model(input_ids=ids(device, 1, 2, 3, 4, 5, 6), use_cache=False)
+    assert tuple(output.logits.shape) == (1, 6, 64)
+    summary = handle.stats.summary()
+    assert summary["queries"] > 0
+    assert summary["avg_verified"] <= 2.0
+    handle.unpatch()
+    assert model.model.layers[0].self_attn is original
+
+
+def test_context_manager_restores_after_cached_decode(device):
+    model = make_tiny_model(device)
+    original = model.model.layers[1].self_attn
+    with patch_llama_attention(model, make_tiny_bundle(), shortlist=4, budget=2, summon_mode="inverted",
+                               inverted_cells_per_subspace=2, adaptive_min_budget=1, adaptive_mid_budget=2) as handle:
+        with torch.no_grad():
+            first = model(input_ids=ids(device, 1, 2, 3, 4), use_cache=True)
+            second = model(input_ids=ids(device, 5), use_cache=True, past_key_values=first.past_key_values)
+        assert tuple(second.logits.shape) == (1, 1, 64)
+        assert handle.stats.summary()["queries"] > 0
+        assert handle.stats.summary()["avg_cell_visits"] > 0
+    assert model.model.layers[1].self_attn is original
+
+
+def test_static_inverted_cached_decode(device):
+    model = make_tiny_model(device)
+    original = model.model.layers[1].self_attn
+    with patch_llama_attention(model, make_tiny_bundle(), shortlist=4, budget=2, summon_mode="inverted_static",
+                               inverted_cells_per_subspace=2, profile_components=True) as handle:
+        with torch.no_grad():
+            first = model(input_ids=ids(device, 1, 2, 3, 4), use_cache=True)
+            second = model(input_ids=ids(device, 5), use_cache=True, past_key_values=first.past_key_values)
+            third = model(input_ids=ids(device, 6), use_cache=True, past_key_values=second.past_key_values)
+        assert tuple(second.logits.shape) == (1, 1, 64)
+        assert tuple(third.logits.shape) == (1, 1, 64)
+        summary = handle.stats.summary()
+        assert summary["queries"] > 0
+        assert summary["avg_refill_pool"] > 0
+        assert summary["avg_static_total_ms"] >= 0
+        assert summary["avg_static_outer_total_ms"] >= summary["avg_static_total_ms"]
+        attention = model.model.layers[1].self_attn
+        assert isinstance(attention, SVALlamaAttention)
+        assert attention._cached_key_len == 6
+        assert attention._cached_postings_key_len == 4
+        assert tuple(attention._cached_coarse_codes.shape) == (2, 4, 2)
+    assert model.model.layers[1].self_attn is original
+
+
+def test_static_inverted_rebuilds_after_tail_interval(device):
+    model = make_tiny_model(device)
+    original = model.model.layers[1].self_attn
+    with patch_llama_attention(model, make_tiny_bundle(), shortlist=4, budget=2, summon_mode="inverted_static",
+                               inverted_cells_per_subspace=2, static_tail_rebuild_interval=2):
+        with torch.no_grad():
+            first = model(input_ids=ids(device, 1, 2, 3, 4), use_cache=True)
+            second = model(input_ids=ids(device, 5), use_cache=True, past_key_values=first.past_key_values)
+            model(input_ids=ids(device, 6), use_cache=True, past_key_values=second.past_key_values)
+        attention = model.model.layers[1].self_attn
+        assert attention._cached_key_len == 6
+        assert attention._cached_postings_key_len == 6
+        assert tuple(attention._cached_coarse_codes.shape) == (2, 6, 2)
+    assert model.model.layers[1].self_attn is original
+
+
+def test_static_inverted_multitoken_cache_keeps_full_codes(device):
+    model = make_tiny_model(device)
+    original = model.model.layers[1].self_attn
+    with patch_llama_attention(model, make_tiny_bundle(), shortlist=4, budget=2, summon_mode="inverted_static",
+                               inverted_cells_per_subspace=2):
+        with torch.no_grad():
+            first = model(input_ids=ids(device, 1, 2, 3, 4), use_cache=True)
+            second = model(input_ids=ids(device, 5, 6), use_cache=True, past_key_values=first.past_key_values)
+        assert tuple(second.logits.shape) == (1, 2, 64)
+        attention = model.model.layers[1].self_attn
+        assert attention._cached_key_len == 6
+        assert tuple(attention._cached_coarse_codes.shape) == (2, 6, 2)
+    assert model.model.layers[1].self_attn is original
+
+
+def test_patch_selected_layers_only(device):
+    model = make_tiny_model(device)
+    layer0, layer1 = model.model.layers[0].self_attn, model.model.layers[1].self_attn
+    handle = patch_llama_attention(model, make_tiny_bundle(), layers=[1])
+    assert model.model.layers[0].self_attn is layer0
+    assert isinstance(model.model.layers[1].self_attn, SVALlamaAttention)
+    with torch.no_grad():
+        output = model(input_ids=ids(device, 1, 2, 3, 4), use_cache=False)
+    assert tuple(output.logits.shape) == (1, 4, 64)
+    assert handle.stats.summary()["queries"] > 0
+    handle.unpatch()
+    assert model.model.layers[0].self_attn is layer0
+    assert model.model.layers[1].self_attn is layer1
+
+
+@pytest.mark.parametrize("mode", ["scan", "inverted", "inverted_static"])
+def test_full_budget_equals_dense_attention(device, mode):
+    # GQA (4 query heads over 2 KV heads), head_dim 64, rank 64 with 2x16 codes
+    heads, kv_heads, head_dim, n_tok = 4, 2, 64, 40
+    model = make_tiny_model(device, hidden=heads * head_dim, heads=heads, kv_heads=kv_heads, attn="eager", seed=3)
+    bundle = make_tiny_bundle(heads=heads, head_dim=head_dim, rank=64, subspaces=2, codewords=16,
+                              shortlist=4096, budget=4096)
+    prompt = torch.randint(0, 64, (1, n_tok), generator=torch.Generator().manual_seed(5)).to(device)
+    steps = [7, 19, 33]
+    with torch.no_grad():
+        ref = model(input_ids=prompt, use_cache=True)
+        ref_logits = [ref.logits]
+        past = ref.past_key_values
+        for t in steps:
+            o = model(input_ids=ids(device, t), use_cache=True, past_key_values=past)
+            ref_logits.append(o.logits)
+            past = o.past_key_values
+        with patch_llama_attention(model, bundle, summon_mode=mode, inverted_cells_per_subspace=16):
+            got = model(input_ids=prompt, use_cache=True)
+            got_logits = [got.logits]
+            past = got.past_key_values
+            for t in steps:
+                o = model(input_ids=ids(device, t), use_cache=True, past_key_values=past)
+                got_logits.append(o.logits)
+                past = o.past_key_values
+    for r, g in zip(ref_logits, got_logits):
+        err = (r - g).abs().max().item() / r.abs().max().item()
+        assert err < 2e-4, f"{mode}: logits differ by {err}"

@@ -41,7 +41,8 @@ def _lists(rng, heads, groups, n, budget, counts, overlap):
 
 @pytest.mark.parametrize("D,H,G,dtype", [(64, 9, 3, torch.float32), (64, 9, 3, torch.bfloat16),
                                          (128, 8, 1, torch.float16), (48, 8, 8, torch.float32),
-                                         (128, 16, 2, torch.bfloat16)])
+                                         (128, 16, 2, torch.bfloat16), (8, 4, 2, torch.float32),
+                                         (40, 6, 3, torch.bfloat16)])
 def test_verify_matches_oracle(device, D, H, G, dtype):
     from sva_amd import kernels
 

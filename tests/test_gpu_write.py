@@ -59,6 +59,19 @@ def test_write_encode_matches_oracle(device, S, C, kv_dtype, code_dtype):
     assert diff.sum() <= max(3, diff.size // 100000)
 
 
+@pytest.mark.parametrize("D,R,S,C", [(8, 4, 2, 8), (16, 6, 3, 5), (48, 20, 5, 33)])
+def test_write_encode_any_shape(device, D, R, S, C):
+    # shapes off the tiled path (rank or sub-dimension not a multiple of 4)
+    N = 300
+    kt, k_proj, cb, keys = _case(device, N, S, C, torch.float32, seed=D + R, H=4, G=2, D=D, R=R)
+    k_low, codes = _encode(device, kt, k_proj, cb, torch.uint8, [(0, 100), (100, N)])
+    ref_low = np.stack([oracle.project(keys[h // 2], k_proj[h]) for h in range(4)])
+    np.testing.assert_array_equal(k_low.view(np.uint32), ref_low.view(np.uint32))
+    ref_codes, gaps = oracle.encode_product_keys(ref_low, cb, return_gap=True)
+    diff = codes != ref_codes
+    assert np.all(gaps[diff] <= 1e-4)
+
+
 def test_write_append_equals_fresh(device):
     N, S, C = 3000, 2, 256
     kt, k_proj, cb, _ = _case(device, N, S, C, torch.bfloat16, seed=5)
