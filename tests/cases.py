@@ -64,3 +64,26 @@ def make_case(H=9, G=3, N=8192, D=64, R=64, S=2, C=256, Q=1, dtype=torch.float32
         # duplicate k_low rows so rank scores tie exactly
         k_low[:, 1::2] = k_low[:, 0::2][:, : k_low[:, 1::2].shape[1]]
     return Case(H, G, N, D, R, S, C, q, keys, values, k_low, q_proj, k_proj, scale, codebooks, codes, dtype)
+
+
+def config1_inputs(seed: int = 20260514):
+    """The single-layer decode lookup of the reference's CPU-runnable case:
+    8192 cached keys, head_dim 64, 9 query heads over 3 KV heads, K/V/q iid
+    N(0, 1) fp32, learned maps N(0, 1/64) of rank 64, 2 x 256 PQ codebooks of
+    width 32 drawn N(0, 1), logit scale field 0 (multiplier 1.0), shortlist
+    2048, budget 512, one query token.  numpy only, so the GPU tests and the
+    fixture writer draw identical inputs."""
+
+    rng = np.random.default_rng(seed)
+    H, G, N, D, R, S, C = 9, 3, 8192, 64, 64, 2, 256
+    return {
+        "q": rng.standard_normal((H, 1, D)).astype(np.float32),
+        "keys": rng.standard_normal((G, N, D)).astype(np.float32),
+        "values": rng.standard_normal((G, N, D)).astype(np.float32),
+        "q_proj": (rng.standard_normal((H, D, R)) / 8).astype(np.float32),
+        "k_proj": (rng.standard_normal((H, D, R)) / 8).astype(np.float32),
+        "logit_scale": np.zeros(H, np.float32),
+        "codebooks": rng.standard_normal((H, S, C, R // S)).astype(np.float32),
+        "shortlist": 2048,
+        "budget": 512,
+    }

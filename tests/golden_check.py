@@ -1,0 +1,49 @@
+"""Comparison of a full decode lookup against the reference's own outputs on
+config 1 (tests/golden/config1_reference.npz, written by
+tests/golden/make_golden.py).  Shared by the oracle test (CPU) and the GPU
+test: each passes the pieces it computed."""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+
+import oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "config1_reference.npz"
+
+
+def load():
+    return dict(np.load(GOLDEN, allow_pickle=False))
+
+
+def check(ref, inp, k_low, codes, q_low, lut, shortlist_sets, budget_sets, out, rtol=1e-5):
+    """shortlist_sets / budget_sets: per head, 1-D arrays of key indices."""
+
+    H = q_low.shape[0]
+    # k_low: the many-row einsum, bit-exact
+    np.testing.assert_array_equal(k_low[:, :16].view(np.uint32), ref["k_low_rows"].view(np.uint32))
+    np.testing.assert_array_equal(k_low.astype(np.float64).sum(axis=(1, 2)), ref["k_low_head_sums"])
+    # codes: equal except where two centroids tie within rounding
+    _, gaps = oracle.encode_product_keys(k_low, inp["codebooks"], return_gap=True)
+    diff = codes.astype(np.int64) != ref["codes"]
+    assert np.all(gaps[diff] <= 1e-4) and diff.sum() <= 2
+    # q_low / LUT: MKL's single-row kernel rounds in its own order; within the
+    # float64 bound of the contraction
+    d = inp["q"].shape[-1]
+    assert np.allclose(q_low, ref["q_low"], rtol=0, atol=4 * d * np.finfo(np.float32).eps * np.abs(ref["q_low"]).max())
+    assert np.allclose(lut, ref["lut"], rtol=0, atol=1e-5 * np.abs(ref["lut"]).max())
+    # shortlist and budget sets: equal, unless the reference's boundary gap is
+    # within rounding of its scores (then the boundary key may legitimately swap)
+    for h in range(H):
+        got, want = set(np.asarray(shortlist_sets[h]).tolist()), set(ref["shortlist"][h].tolist())
+        if ref["shortlist_gap"][h] > 1e-5:
+            assert got == want, f"head {h}: shortlist differs from the reference"
+        else:
+            assert len(got ^ want) <= 2
+        got, want = set(np.asarray(budget_sets[h]).tolist()), set(ref["budget"][h].tolist())
+        if ref["budget_gap"][h] > 1e-5 and ref["shortlist_gap"][h] > 1e-5:
+            assert got == want, f"head {h}: budget set differs from the reference"
+            err = np.abs(out[h] - ref["out"][h]).max() / np.abs(ref["out"][h]).max()
+            assert err <= rtol, f"head {h}: verifier rel err {err}"
