@@ -156,6 +156,123 @@ __global__ void __launch_bounds__(WT) write_encode_kernel(WriteParams p) {
   }
 }
 
+// MFMA variant (R, C multiples of 16; D, sub multiples of 4): the projection
+// and the x.c distance products on v_mfma_f32_16x16x4f32, which accumulates
+// its four k products per step into the running sum in k order, the same
+// rounding as the fma chain above.  Operand layout of the 16x16x4 form: lane
+// l supplies A[l % 16][k0 + l / 16] and B[k0 + l / 16][l % 16] and receives
+// D[4 * (l / 16) + i][l % 16] in element i.  Wave w owns rows 16w..16w+15 of
+// the tile.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(WT) write_encode_mfma_kernel(WriteParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int sub = R / S;
+  const int h = blockIdx.y;
+  const int g = h / (p.H / p.G);
+  const int64_t n0 = p.row0 + (int64_t)blockIdx.x * KT;
+  const int nk = (int)min((int64_t)KT, p.row0 + p.n_rows - n0);
+  float* W = (float*)lds;                  // [D][R]
+  float* Kt = W + D * R;                   // [KT][D + 1]
+  float* Xl = Kt + KT * (D + 1);           // [KT][R + 1]
+  float* cb = Xl + KT * (R + 1);           // [C][sub + CB_PAD]
+  float* cn = cb + C * (sub + CB_PAD);     // [C]
+  float* xx = cn + C;                      // [KT]
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(p.k_proj + (int64_t)h * D * R);
+    for (int i = threadIdx.x; i < D * R / 4; i += WT) reinterpret_cast<float4*>(W)[i] = w4[i];
+    const int64_t kb = (int64_t)g * p.kv_hs;
+    for (int i = threadIdx.x; i < KT * D; i += WT) {
+      const int k = i / D, d = i - k * D;
+      Kt[k * (D + 1) + d] = k < nk ? load_elem(p.keys, kb + (n0 + k) * p.kv_rs + d, p.kv_dtype) : 0.0f;
+    }
+  }
+  __syncthreads();
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lr = l & 15, lk = l >> 4;
+  const int row0 = 16 * wid;
+  float* klow = p.k_low + (int64_t)h * p.klow_hs;
+  // projection: R / 16 output blocks per wave
+  for (int cb0 = 0; cb0 < R; cb0 += 64) {
+    f32x4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nblk = min(4, (R - cb0) / 16);
+    for (int k0 = 0; k0 < D; k0 += 4) {
+      const float a = Kt[(row0 + lr) * (D + 1) + k0 + lk];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (c < nblk) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, W[(k0 + lk) * R + cb0 + 16 * c + lr], acc[c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c < nblk) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + 4 * lk + i, col = cb0 + 16 * c + lr;
+          Xl[row * (R + 1) + col] = acc[c][i];
+          if (row < nk) klow[(n0 + row) * R + col] = acc[c][i];
+        }
+      }
+    }
+  }
+  if (p.codes == nullptr) return;
+  for (int s = 0; s < S; ++s) {
+    __syncthreads();
+    const float* src = p.codebooks + ((int64_t)h * S + s) * C * sub;
+    for (int i = threadIdx.x; i < C * sub / 4; i += WT) {
+      const int c = (4 * i) / sub, j = 4 * i - c * sub;
+      *reinterpret_cast<float4*>(cb + c * (sub + CB_PAD) + j) = reinterpret_cast<const float4*>(src)[i];
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += WT) cn[c] = torch_order_dot(cb + c * (sub + CB_PAD), cb + c * (sub + CB_PAD), sub);
+    for (int r = threadIdx.x; r < KT; r += WT) xx[r] = torch_order_dot(Xl + r * (R + 1) + s * sub, Xl + r * (R + 1) + s * sub, sub);
+    __syncthreads();
+    // this lane's 4 rows: running best over its centroids (l % 16 of each block)
+    float best[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+    int arg[4] = {0, 0, 0, 0};
+    float xxr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xxr[i] = xx[row0 + 4 * lk + i];
+    for (int c0 = 0; c0 < C; c0 += 16) {
+      f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int k0 = 0; k0 < sub; k0 += 4) {
+        const float a = Xl[(row0 + lr) * (R + 1) + s * sub + k0 + lk];
+        const float b = cb[(c0 + lr) * (sub + CB_PAD) + k0 + lk];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+      }
+      const int c = c0 + lr;
+      const float cnc = cn[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dist = (xxr[i] - 2.0f * acc[i]) + cnc;
+        if (dist < best[i]) {
+          best[i] = dist;
+          arg[i] = c;
+        }
+      }
+    }
+    // merge the 16 lanes of each row group: smaller distance, then lower index
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float ob = __shfl_xor(best[i], o, 16);
+        const int oa = __shfl_xor(arg[i], o, 16);
+        if (ob < best[i] || (ob == best[i] && oa < arg[i])) {
+          best[i] = ob;
+          arg[i] = oa;
+        }
+      }
+      const int row = row0 + 4 * lk + i;
+      if (lr == 0 && row < nk) store_code(p.codes, (int64_t)h * p.code_hs + (n0 + row) * S + s, p.ctype, arg[i]);
+    }
+  }
+}
+
 // Any shape: one thread per row, the same arithmetic as the tiled kernel.
 __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p) {
 #pragma clang fp contract(off)
@@ -264,6 +381,18 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   if (!tiled) {
     hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, (hipStream_t)stream, p);
     SVA_CHECK_LAUNCH("write_encode_rowwise_kernel");
+    return SVA_OK;
+  }
+  if (R % 16 == 0 && C % 16 == 0 && D % 4 == 0) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      SVA_CHECK_HIP(hipFuncSetAttribute((const void*)write_encode_mfma_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
+                    "hipFuncSetAttribute(write_encode_mfma_kernel)");
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(write_encode_mfma_kernel, grid, dim3(WT), lds, (hipStream_t)stream, p);
+    SVA_CHECK_LAUNCH("write_encode_mfma_kernel");
     return SVA_OK;
   }
   switch (R / S) {
