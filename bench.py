@@ -49,6 +49,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
+    ap.add_argument("--suite", default="decode", choices=("decode", "write"),
+                    help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA")
     ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
                     help="summarize rocprofv3 outputs of this benchmark into profiles/ and exit")
     return ap.parse_args()
@@ -213,10 +215,60 @@ def write_profiles(args):
     print(f"wrote profiles/{stem}_*.md/json")
 
 
+MFMA_F32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak (AMD spec)
+
+
+def write_suite(args):
+    """Catalog build of a fresh cache: k_low = K . k_proj and PQ codes for
+    every key of every query head (sva/llama.py:615-616), timed with HIP
+    events on the launch stream."""
+
+    import torch
+
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    subspaces, codewords = LAYOUTS[args.layout]
+    n, heads, kv_heads, d, r = args.keys, 9, 3, 64, 64
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    keys = torch.randn(kv_heads, n, d, device=device, generator=g).to(torch.bfloat16)
+    k_proj = torch.randn(heads, d, r, device=device, generator=g) / 8.0
+    cb = torch.randn(heads, subspaces, codewords, r // subspaces, device=device, generator=g)
+    k_low = torch.empty(heads, n, r, device=device)
+    codes = torch.empty(heads, n, subspaces, device=device, dtype=torch.uint8)
+    for _ in range(max(1, args.warmup // 50)):
+        kernels.write_encode(keys, k_proj, cb, k_low, codes)
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 200)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        kernels.write_encode(keys, k_proj, cb, k_low, codes)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flop = 2.0 * heads * n * (d * r + r * codewords)  # projection + x.c products of every subspace
+    tflops = flop / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "catalog build (k_low projection + PQ assignment)", "value": round(n / (ms * 1e-3) / 1e6, 2),
+        "unit": "Mkeys/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "dtype": "fp32 (bf16 K in)", "data": "synthetic", "config": {"workload": f"{n}-key catalog, 9 heads, "
+                                                                                   f"{args.layout} codes"},
+        "roofline": {"kernel": "write_encode_mfma_kernel", "bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
+                     "flop_per_launch": flop, "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.write_profiles:
         write_profiles(args)
+        return
+    if args.suite == "write":
+        if args.gpus != 1:
+            sys.exit(2)
+        write_suite(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "
