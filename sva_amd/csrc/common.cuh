@@ -153,20 +153,16 @@ SVA_DEV uint32_t block_excl_scan(uint32_t v, uint32_t* scratch, uint32_t* total)
 // Exact selection of the k largest nonzero composites among the elements a
 // visitor yields (each element exactly once per call, unique values): radix
 // passes of up to 8 bits from the highest bit where elements differ, with
-// one LDS histogram per wave.  Returns X such that the selected elements are
-// exactly those >= X.  Every thread of the block must call it.  whist: BLOCK/64
-// rows of 256 uint32; scratch: block_excl_scan scratch; shared64: 2 uint64;
-// shared: 3 uint32 (all LDS).  BLOCK >= 256.
+// one LDS histogram per wave.  vor / vand are this thread's OR and AND of the
+// elements it visits (0 and ~0 when it visits none).  Returns X such that the
+// selected elements are exactly those >= X.  Every thread of the block must
+// call it.  whist: BLOCK/64 rows of 256 uint32; scratch: block_excl_scan
+// scratch; shared64: 2 uint64; shared: 3 uint32 (all LDS).  BLOCK >= 256.
 template <int BLOCK, typename Visit>
-SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint32_t* scratch, uint64_t* shared64,
-                                uint32_t* shared) {
+SVA_DEV uint64_t select_largest_with_bounds(Visit visit, int k, uint64_t vor, uint64_t vand, uint32_t (*whist)[256],
+                                            uint32_t* scratch, uint64_t* shared64, uint32_t* shared) {
   const int wid = threadIdx.x / WAVE;
   // bits above the highest differing bit are common to every element
-  uint64_t vor = 0ull, vand = ~0ull;
-  visit([&](uint64_t x) {
-    vor |= x;
-    vand &= x;
-  });
   for (int off = 1; off < WAVE; off <<= 1) {
     vor |= __shfl_xor(vor, off, WAVE);
     vand &= __shfl_xor(vand, off, WAVE);
@@ -218,6 +214,18 @@ SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint
     if (done) return prefix;
     top = shift - 1;
   }
+}
+
+// select_largest with the OR / AND of the elements taken in an extra pass.
+template <int BLOCK, typename Visit>
+SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint32_t* scratch, uint64_t* shared64,
+                                uint32_t* shared) {
+  uint64_t vor = 0ull, vand = ~0ull;
+  visit([&](uint64_t x) {
+    vor |= x;
+    vand &= x;
+  });
+  return select_largest_with_bounds<BLOCK>(visit, k, vor, vand, whist, scratch, shared64, shared);
 }
 
 // ---------------------------------------------------------------------------

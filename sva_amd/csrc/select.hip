@@ -25,8 +25,8 @@ __global__ void __launch_bounds__(SEL_BLOCK)
                          int32_t* __restrict__ fin_count) {
   extern __shared__ __align__(16) unsigned char lds[];
   uint64_t* comp = (uint64_t*)lds;                             // [L]
-  uint32_t* sel = (uint32_t*)(comp + ((L + 1) & ~1));          // [B] selected key indices, 16-byte aligned
-  uint32_t(*whist)[256] = (uint32_t(*)[256])(sel + ((B + 3) & ~3));  // [SEL_NW][256]
+  uint32_t* sel = (uint32_t*)(comp + ((L + 1) & ~1));          // [B rounded up to 64] selected keys, 16-byte aligned
+  uint32_t(*whist)[256] = (uint32_t(*)[256])(sel + ((B + 63) & ~63));  // [SEL_NW][256]
   uint64_t* shared64 = (uint64_t*)(whist + SEL_NW);            // [2]
   uint32_t* scratch = (uint32_t*)(shared64 + 2);               // [SEL_NW + 1]
   uint32_t* shared = scratch + SEL_NW + 1;                     // [4]
@@ -34,10 +34,16 @@ __global__ void __launch_bounds__(SEL_BLOCK)
   const int32_t* idx = sl_idx + (int64_t)item * L;
   const float* rank = sl_rank + (int64_t)item * L;
   const int n = max(0, min(sl_count[item], L));
+  uint64_t vor = 0ull, vand = ~0ull;  // over this thread's entries below n
   for (int i = threadIdx.x; i < L; i += SEL_BLOCK) {
     const float r = rank[i];
     const int32_t x = idx[i];
-    comp[i] = composite(f2key(r), (uint32_t)x);
+    const uint64_t c = composite(f2key(r), (uint32_t)x);
+    comp[i] = c;
+    if (i < n) {
+      vor |= c;
+      vand &= c;
+    }
   }
   const int beff = min(B, n);
   if (threadIdx.x == 0) fin_count[item] = beff;
@@ -46,7 +52,8 @@ __global__ void __launch_bounds__(SEL_BLOCK)
   auto visit = [&](auto&& f) {
     for (int i = threadIdx.x; i < n; i += SEL_BLOCK) f(comp[i]);
   };
-  const uint64_t X = beff == n ? 0ull : select_largest<SEL_BLOCK>(visit, beff, whist, scratch, shared64, shared);
+  const uint64_t X =
+      beff == n ? 0ull : select_largest_with_bounds<SEL_BLOCK>(visit, beff, vor, vand, whist, scratch, shared64, shared);
   // compact the selected in shortlist order: contiguous ranges per thread
   const int per = (n + SEL_BLOCK - 1) / SEL_BLOCK;
   const int i0 = min(n, (int)threadIdx.x * per), i1 = min(n, i0 + per);
@@ -59,26 +66,63 @@ __global__ void __launch_bounds__(SEL_BLOCK)
     if (c >= X && o < (uint32_t)beff) sel[o++] = composite_index(c);
   }
   __syncthreads();
-  // ascending order: each selected index goes to its rank among the selected,
-  // counted by two lanes per element over halves of the list (16-byte
-  // broadcast reads, eight in flight)
+  // ascending order.  Up to SEL_BLOCK entries: each wave sorts a run of 64
+  // in registers (bitonic), then every entry's rank is its place in its run
+  // plus, for every other run, the number of smaller entries (binary search).
   int32_t* out = fin_idx + (int64_t)item * B;
-  const int hb = (((beff + 1) >> 1) + 3) & ~3;  // first half, a multiple of 4
-  for (int i = threadIdx.x; i < 2 * beff; i += SEL_BLOCK) {
-    const int e = i >> 1;
-    const uint32_t v = sel[e];
-    const int j0 = (i & 1) ? hb : 0;
-    const int j1 = (i & 1) ? beff : min(hb, beff);
-    int r = 0;
-    int j = j0;
-#pragma unroll 8
-    for (; j + 4 <= j1; j += 4) {
-      const uint4 u = *reinterpret_cast<const uint4*>(sel + j);
-      r += (int)(u.x < v) + (int)(u.y < v) + (int)(u.z < v) + (int)(u.w < v);
+  if (beff <= SEL_BLOCK) {
+    const int runs = (beff + WAVE - 1) / WAVE;
+    const int t = threadIdx.x;
+    uint32_t v = t < beff ? sel[t] : 0xFFFFFFFFu;
+    if (t < runs * WAVE) {
+      const int lane = lane_id();
+      for (int k = 2; k <= WAVE; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          const uint32_t o = (uint32_t)__shfl_xor((int)v, j, WAVE);
+          const bool up = (lane & k) == 0;
+          const bool low = (lane & j) == 0;
+          v = (low == up) ? min(v, o) : max(v, o);
+        }
+      }
     }
-    for (; j < j1; ++j) r += (int)(sel[j] < v);
-    r += __shfl_xor(r, 1);
-    if ((i & 1) == 0) out[r] = (int32_t)v;
+    __syncthreads();
+    if (t < runs * WAVE) sel[t] = v;  // sorted runs, padded with 0xFFFFFFFF
+    __syncthreads();
+    if (t < runs * WAVE && v != 0xFFFFFFFFu) {
+      const int run = t / WAVE;
+      int r = t - run * WAVE;
+      for (int q = 0; q < runs; ++q) {
+        if (q == run) continue;
+        const uint32_t* a = sel + q * WAVE;
+        int lo = 0, hi = WAVE;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (a[mid] < v) lo = mid + 1;
+          else hi = mid;
+        }
+        r += lo;
+      }
+      out[r] = (int32_t)v;
+    }
+  } else {
+    // large budgets: two lanes per entry count the smaller ones
+    const int hb = (((beff + 1) >> 1) + 3) & ~3;
+    for (int i = threadIdx.x; i < 2 * beff; i += SEL_BLOCK) {
+      const int e = i >> 1;
+      const uint32_t v = sel[e];
+      const int j0 = (i & 1) ? hb : 0;
+      const int j1 = (i & 1) ? beff : min(hb, beff);
+      int r = 0;
+      int j = j0;
+#pragma unroll 8
+      for (; j + 4 <= j1; j += 4) {
+        const uint4 u = *reinterpret_cast<const uint4*>(sel + j);
+        r += (int)(u.x < v) + (int)(u.y < v) + (int)(u.z < v) + (int)(u.w < v);
+      }
+      for (; j < j1; ++j) r += (int)(sel[j] < v);
+      r += __shfl_xor(r, 1);
+      if ((i & 1) == 0) out[r] = (int32_t)v;
+    }
   }
 }
 
@@ -92,7 +136,7 @@ extern "C" int sva_budget_select(const int32_t* sl_idx, const float* sl_rank, co
   SVA_REQUIRE(n_items > 0 && n_items < (1ll << 31), "sva_budget_select: bad item count");
   SVA_REQUIRE(L > 0 && L <= 16384 && B > 0 && B <= 8192, "sva_budget_select: shortlist %lld / budget %lld out of range",
               (long long)L, (long long)B);
-  const size_t lds = sizeof(uint64_t) * ((size_t)((L + 1) & ~1) + 2) + sizeof(uint32_t) * ((size_t)((B + 3) & ~3) + SEL_NW * 256 +
+  const size_t lds = sizeof(uint64_t) * ((size_t)((L + 1) & ~1) + 2) + sizeof(uint32_t) * ((size_t)((B + 63) & ~63) + SEL_NW * 256 +
                                                                               SEL_NW + 1 + 4);
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_budget_select: shortlist %lld + budget %lld exceed LDS",
                   (long long)L, (long long)B);

@@ -302,14 +302,17 @@ __global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
   const uint32_t* nallow = a.nallow + (int64_t)item * nsub;
   const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  // totals: candidates M and allowed keys A
+  // totals: candidates M and allowed keys A.  With at most SB lists (every
+  // cache up to 2M keys) one pass also yields each list's staging offset.
+  const bool one_pass = nsub <= SB;
   uint32_t m = 0, al = 0;
   for (int s = threadIdx.x; s < nsub; s += SB) {
     m += ncand[s];
     al += nallow[s];
   }
-  uint32_t M, A;
-  block_excl_scan<SB>(m, scratch, &M);
+  uint32_t M;
+  const uint32_t my_base = block_excl_scan<SB>(m, scratch, &M);
+  uint32_t A;
   block_excl_scan<SB>(al, scratch, &A);
   const int leff = (int)min((uint32_t)p.L, A);
   if (threadIdx.x == 0) {
@@ -318,24 +321,47 @@ __global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
   }
   if (leff == 0) return;
   if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND) {
-    // common case: stage the candidates contiguously in LDS
-    uint32_t carry = 0;
-    for (int g = 0; g < nsub; g += SB) {
-      const int s = g + (int)threadIdx.x;
-      const uint32_t c = s < nsub ? ncand[s] : 0u;
-      uint32_t tot;
-      const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
-      const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+    // common case: stage the candidates contiguously in LDS, taking the
+    // OR / AND bounds of the radix select on the way
+    uint64_t vor = 0ull, vand = ~0ull;
+    if (one_pass) {
+      const int s = threadIdx.x;
+      if (s < nsub) {
+        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
 #pragma unroll 8
-      for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
-      carry += tot;
+        for (uint32_t j = 0; j < m; ++j) {
+          const uint64_t x = src[j];
+          cl[my_base + j] = x;
+          vor |= x;
+          vand &= x;
+        }
+      }
+    } else {
+      uint32_t carry = 0;
+      for (int g = 0; g < nsub; g += SB) {
+        const int s = g + (int)threadIdx.x;
+        const uint32_t c = s < nsub ? ncand[s] : 0u;
+        uint32_t tot;
+        const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
+        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+#pragma unroll 8
+        for (uint32_t j = 0; j < c; ++j) {
+          const uint64_t x = src[j];
+          cl[base + j] = x;
+          vor |= x;
+          vand &= x;
+        }
+        carry += tot;
+      }
     }
     __syncthreads();
     const int Mi = (int)M;
     auto visit = [&](auto&& f) {
       for (int j = threadIdx.x; j < Mi; j += SB) f(cl[j]);
     };
-    const uint64_t X = (uint32_t)leff == M ? 1ull : select_largest<SB>(visit, leff, whist, scratch, shared64, shared);
+    const uint64_t X = (uint32_t)leff == M
+                           ? 1ull
+                           : select_largest_with_bounds<SB>(visit, leff, vor, vand, whist, scratch, shared64, shared);
     // write the selected in staging order: contiguous ranges per thread
     const int per = (Mi + SB - 1) / SB;
     const int j0 = min(Mi, (int)threadIdx.x * per), j1 = min(Mi, j0 + per);
