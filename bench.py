@@ -5,9 +5,9 @@ Workload (one step = one decode lookup of one layer for one query token):
   rank 64, PQ codes uint8 (default 4x64), shortlist 2048 / budget 512, q = 1.
   K/V bf16 [3, N, 64]; k_low fp32 [9, N, 64] (the production catalog);
   codebooks and learned maps N(0, 1) / N(0, 1/64); synthetic data, seeded.
-A step runs the four HIP stages on torch's current stream:
-  query_lut -> summon (PQ scan + exact shortlist + rescore) -> budget select
-  -> GQA verifier.
+A step runs three HIP calls on torch's current stream:
+  query_lut -> summon_select (PQ scan, exact shortlist, rescore and budget
+  select) -> GQA verifier.
 Caches of `--layers` distinct layers are rotated so that the codes touched
 per step (>256 MB over the rotation) do not stay in the 256 MB Infinity Cache.
 
@@ -134,7 +134,7 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 
 
 # kernels of one decode lookup, by entry point
-SUMMON_KERNELS = ("wide_scan_kernel", "wide_select_kernel", "wide_rescore_kernel")
+SUMMON_KERNELS = ("wide_scan_kernel", "wide_finish_kernel")
 PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel",
                                                          "verify_combine_kernel")
 PROFILE_STEM = "sva_summon_decode_1m_{layout}"
@@ -207,10 +207,10 @@ def write_profiles(args):
         if k in SUMMON_KERNELS:
             summon_bytes += b
         lines.append(f"| {k} | {fk:.1f} | {wk:.1f} | {b:,.0f} |")
-    lines += ["", f"sva_summon (the three wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
+    lines += ["", f"sva_summon_select (the wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
     (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
     (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
-        {"entry_point": "sva_summon", "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
+        {"entry_point": "sva_summon_select", "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
          "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}) + "\n")
     print(f"wrote profiles/{stem}_*.md/json")
 
@@ -289,7 +289,7 @@ def main():
     shortlist = min(args.shortlist, n)
     budget = min(args.budget, shortlist)
     scaling = 64 ** -0.5
-    stages = ("query_lut", "summon", "budget_select", "verify")
+    stages = ("query_lut", "summon", "verify")
 
     plan = kernels.ScanDecodePlan(device, 1, heads, 1, 64, 64, subspaces, codewords, shortlist, budget)
     outs = [torch.empty(1, heads, 1, 64, device=device, dtype=torch.bfloat16) for _ in layers]
@@ -300,18 +300,17 @@ def main():
                  layer.values, n, scaling, out=outs[i % len(layers)])
 
     def step_staged(i, ev):
-        # the same four launches with an event between stages (per-kernel times)
+        # the same three calls with an event between stages (per-stage times)
         layer = layers[i % len(layers)]
         ev[0].record()
         q_low, lut, rng = kernels.query_lut(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, n,
                                             shortlist)
         ev[1].record()
-        sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, layer.codes, layer.k_low, n, shortlist)
+        _, _, _, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, layer.codes, layer.k_low, n, shortlist,
+                                                            budget)
         ev[2].record()
-        fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, budget)
-        ev[3].record()
         kernels.verify(layer.q, layer.keys, layer.values, fin_idx, fin_count, n, scaling)
-        ev[4].record()
+        ev[3].record()
 
     if args.calibrate_copy:
         src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=device).fill_(1)
@@ -336,7 +335,7 @@ def main():
 
     # per-kernel durations: HIP events on the launch stream around each stage
     n_ev = min(args.steps, 200)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n_ev)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(n_ev)]
     # hold the stream in a device-side spin while the host enqueues, so the
     # events bracket kernel execution rather than host launch gaps
     torch.cuda._sleep(int(2e8))
@@ -384,8 +383,8 @@ def main():
         "gpu_us_per_query": round(gpu_us, 2),
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": ("sva_summon: wide_scan + wide_select + wide_rescore" if strategy == 1
-                       else "sva_summon: summon_item_kernel"),
+            "kernel": ("sva_summon_select: wide_scan + wide_finish" if strategy == 1
+                       else "sva_summon_select: summon_item_kernel + budget_select_kernel"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

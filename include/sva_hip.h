@@ -124,6 +124,22 @@ int sva_summon(const float *lut, const float *score_range, const float *q_low, c
                float *sl_rank, int32_t *sl_count, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Summon followed by the budget select, in one call: sva_summon's outputs,
+ * plus fin_idx / fin_count exactly as sva_budget_select writes them.
+ * Replaces sva/llama.py:262-302 (scan, masked topk(L), rescore, topk(B),
+ * counts).  On the wide path (q = 1 over a long cache) the shortlist and
+ * budget selects and the rescore run in one kernel per query item.
+ *   fin_idx [items, B] chosen key indices sorted ascending; fin_count[item] = min(B, sl_count[item]).
+ * workspace: sva_summon_workspace_bytes(...) bytes, 256-byte aligned.
+ */
+int sva_summon_select(const float *lut, const float *score_range, const float *q_low, const void *codes,
+                      int code_type, int64_t code_head_stride, const float *k_low, int64_t k_low_head_stride,
+                      const int64_t *seq_offsets, const int64_t *seq_lens, int64_t n_seq, int64_t H, int64_t Q,
+                      int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void *mask, int mask_type,
+                      int64_t mask_tok_stride, int32_t *sl_idx, float *sl_rank, int32_t *sl_count, int64_t B,
+                      int32_t *fin_idx, int32_t *fin_count, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Which summon strategy a call with these shapes takes (16-byte aligned
  * catalogs assumed): 0 = one workgroup per query item, 1 = wide path (q = 1
  * over a long cache: many workgroups per item, one pass over the codes).

@@ -229,6 +229,213 @@ SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint
 }
 
 // ---------------------------------------------------------------------------
+// Selection over elements held in registers: each thread of the block holds
+// NPT nonzero composites (0 = empty slot).  Radix passes of up to TOP_BITS
+// bits from the highest bit where the elements differ, counted in one shared
+// LDS histogram; as soon as the bucket holding the k-th largest has at most
+// TOP_SMALL elements they are gathered and ranked directly.  Returns X such
+// that the selected elements are exactly those >= X (with repeated values,
+// more than k elements may reach X and the caller caps its output at k).
+constexpr int TOP_BITS = 12;
+constexpr int TOP_BINS = 1 << TOP_BITS;
+constexpr int TOP_SMALL = 256;
+
+struct TopLds {
+  uint32_t* hist;      // [TOP_BINS]
+  uint64_t* small;     // [TOP_SMALL]
+  uint32_t* scratch;   // [BLOCK / 64 + 1]
+  uint32_t* shared;    // [4]
+  uint64_t* shared64;  // [2]
+};
+
+template <int BLOCK, int NPT>
+SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s) {
+  static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
+  const int lane = lane_id();
+  for (int off = 1; off < WAVE; off <<= 1) {
+    vor |= __shfl_xor(vor, off, WAVE);
+    vand &= __shfl_xor(vand, off, WAVE);
+  }
+  if (threadIdx.x == 0) {
+    s.shared64[0] = 0ull;
+    s.shared64[1] = ~0ull;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    atomicOr((unsigned long long*)&s.shared64[0], (unsigned long long)vor);
+    atomicAnd((unsigned long long*)&s.shared64[1], (unsigned long long)vand);
+  }
+  __syncthreads();
+  const uint64_t all_or = s.shared64[0], all_and = s.shared64[1];
+  const uint64_t diff = all_or ^ all_and;
+  __syncthreads();
+  if (diff == 0ull) return all_or;  // one distinct value
+  int top = 63 - __clzll((long long)diff);
+  uint64_t pmask = top == 63 ? 0ull : ~0ull << (top + 1);
+  uint64_t prefix = all_and & pmask;
+  int need = k;
+  while (true) {
+    const int shift = max(top - (TOP_BITS - 1), 0);
+    const uint32_t dmask = (1u << (top - shift + 1)) - 1u;
+    reinterpret_cast<uint4*>(s.hist)[threadIdx.x] = uint4{0u, 0u, 0u, 0u};
+    if (threadIdx.x == 0) s.shared[3] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const uint64_t x = e[i];
+      if (x != 0ull && (x & pmask) == prefix) atomicAdd(&s.hist[(uint32_t)(x >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    // thread t owns bins 4t .. 4t+3 counted from the top
+    const uint4 h = reinterpret_cast<const uint4*>(s.hist)[BLOCK - 1 - threadIdx.x];
+    uint32_t total;
+    const uint32_t above = block_excl_scan<BLOCK>(h.x + h.y + h.z + h.w, s.scratch, &total);
+    {
+      const uint32_t c[4] = {h.w, h.z, h.y, h.x};
+      uint32_t a = above;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (a < (uint32_t)need && a + c[j] >= (uint32_t)need) {
+          s.shared[0] = (uint32_t)(TOP_BINS - 1 - 4 * (int)threadIdx.x - j);
+          s.shared[1] = a;
+          s.shared[2] = c[j];
+        }
+        a += c[j];
+      }
+    }
+    __syncthreads();
+    const uint32_t b = s.shared[0];
+    const uint32_t cb = s.shared[2];
+    need -= (int)s.shared[1];
+    prefix |= (uint64_t)b << shift;
+    pmask |= (uint64_t)dmask << shift;
+    if (cb == (uint32_t)need || shift == 0) {
+      __syncthreads();
+      return prefix;
+    }
+    if (cb <= (uint32_t)TOP_SMALL) {
+      // gather the bucket and rank its elements directly
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        const uint64_t x = e[i];
+        const bool match = x != 0ull && (x & pmask) == prefix;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(match);
+        if (m != 0ull) {
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(&s.shared[3], (uint32_t)__popcll(m));
+          base = __shfl(base, 0, WAVE);
+          if (match) {
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            s.small[base + below] = x;
+          }
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < cb) {
+        const uint64_t v = s.small[threadIdx.x];
+        uint32_t gt = 0, ge = 0;
+        for (uint32_t j = 0; j < cb; ++j) {
+          const uint64_t y = s.small[j];
+          gt += y > v;
+          ge += y >= v;
+        }
+        if (gt < (uint32_t)need && ge >= (uint32_t)need) s.shared64[0] = v;
+      }
+      __syncthreads();
+      const uint64_t X = s.shared64[0];
+      __syncthreads();
+      return X;
+    }
+    top = shift - 1;
+  }
+}
+
+// Writes the beff indices of sel (LDS, capacity rounded up to 64) to out in
+// ascending order.  Up to BLOCK entries: each wave sorts a run of 64 in
+// registers (bitonic), then an entry's place is its place in its run plus,
+// for every other run, the number of smaller entries (binary search).
+// Larger counts: two lanes per entry count the smaller entries.  Entries are
+// distinct.  sel is overwritten.  Every thread of the block must call it.
+template <int BLOCK>
+SVA_DEV void write_ascending(uint32_t* sel, int beff, int32_t* out) {
+  if (beff <= BLOCK) {
+    const int runs = (beff + WAVE - 1) / WAVE;
+    const int t = threadIdx.x;
+    uint32_t v = t < beff ? sel[t] : 0xFFFFFFFFu;
+    if (t < runs * WAVE) {
+      const int lane = lane_id();
+      for (int k = 2; k <= WAVE; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+          const uint32_t o = (uint32_t)__shfl_xor((int)v, j, WAVE);
+          const bool up = (lane & k) == 0;
+          const bool low = (lane & j) == 0;
+          v = (low == up) ? min(v, o) : max(v, o);
+        }
+      }
+    }
+    __syncthreads();
+    if (t < runs * WAVE) sel[t] = v;  // sorted runs, padded with 0xFFFFFFFF
+    __syncthreads();
+    if (t < runs * WAVE && v != 0xFFFFFFFFu) {
+      const int run = t / WAVE;
+      int r = t - run * WAVE;
+      for (int q = 0; q < runs; ++q) {
+        if (q == run) continue;
+        const uint32_t* a = sel + q * WAVE;
+        int lo = 0, hi = WAVE;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (a[mid] < v) lo = mid + 1;
+          else hi = mid;
+        }
+        r += lo;
+      }
+      out[r] = (int32_t)v;
+    }
+  } else {
+    const int hb = (((beff + 1) >> 1) + 3) & ~3;
+    for (int i = threadIdx.x; i < 2 * beff; i += BLOCK) {
+      const int e = i >> 1;
+      const uint32_t v = sel[e];
+      const int j0 = (i & 1) ? hb : 0;
+      const int j1 = (i & 1) ? beff : min(hb, beff);
+      int r = 0;
+      int j = j0;
+#pragma unroll 8
+      for (; j + 4 <= j1; j += 4) {
+        const uint4 u = *reinterpret_cast<const uint4*>(sel + j);
+        r += (int)(u.x < v) + (int)(u.y < v) + (int)(u.z < v) + (int)(u.w < v);
+      }
+      for (; j < j1; ++j) r += (int)(sel[j] < v);
+      r += __shfl_xor(r, 1);
+      if ((i & 1) == 0) out[r] = (int32_t)v;
+    }
+  }
+}
+
+// Appends this thread's elements e[i] >= X (nonzero) to dst in any order,
+// at most cap of them; `counter` (LDS, zeroed and synchronised by the caller)
+// receives the count.  Every lane of a wave must call it.
+template <int NPT>
+SVA_DEV void append_selected(const uint64_t (&e)[NPT], uint64_t X, uint32_t* dst, int cap, uint32_t* counter) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const uint64_t x = e[i];
+    const bool sel = x != 0ull && x >= X;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(sel);
+    if (m != 0ull) {
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(counter, (uint32_t)__popcll(m));
+      base = __shfl(base, 0, WAVE);
+      const uint32_t o = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (sel && o < (uint32_t)cap) dst[o] = composite_index(x);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Radix select over uint32 keys.  Finds the threshold key T and k_eq such that
 // the k largest elements are: every element with key > T plus the k_eq
 // lowest-index elements with key == T.  Elements with key 0 never count.

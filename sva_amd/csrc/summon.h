@@ -28,9 +28,15 @@ struct SummonParams {
   int32_t* sl_idx;
   float* sl_rank;
   int32_t* sl_count;
+  // optional budget select fused into the summon (B = 0: none)
+  int B;
+  int32_t* fin_idx;
+  int32_t* fin_count;
 };
 
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
+int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
+                         int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);

@@ -199,30 +199,30 @@ extern "C" size_t sva_summon_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q
   return sva::summon_wide_workspace_bytes(n_seq, H, Q, n_keys, L);
 }
 
-extern "C" int sva_summon(const float* lut, const float* score_range, const float* q_low, const void* codes,
-                          int code_type, int64_t code_head_stride, const float* k_low, int64_t k_low_head_stride,
-                          const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
-                          int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
-                          int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count,
-                          void* workspace, size_t workspace_bytes, void* stream) {
-  sva::clear_error();
-  SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count,
-              "sva_summon: null pointer");
-  SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "sva_summon: offsets and lengths go together");
-  SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "sva_summon: bad sizes");
-  SVA_REQUIRE(n_keys < (1ll << 31), "sva_summon: at most 2^31-1 keys per sequence");
+namespace {
+
+int summon_impl(const char* fn, const float* lut, const float* score_range, const float* q_low, const void* codes,
+                int code_type, int64_t code_head_stride, const float* k_low, int64_t k_low_head_stride,
+                const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
+                int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
+                int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
+                int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream) {
+  SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
+  SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
+  SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "%s: bad sizes", fn);
+  SVA_REQUIRE(n_keys < (1ll << 31), "%s: at most 2^31-1 keys per sequence", fn);
   SVA_REQUIRE(R > 0 && R <= 511 && S > 0 && R % S == 0 && C > 0 && S * C <= 16384,
-              "sva_summon: bad rank/PQ layout R=%lld S=%lld C=%lld", (long long)R, (long long)S, (long long)C);
-  SVA_REQUIRE(L > 0 && L <= 16384, "sva_summon: shortlist %lld out of range (1..16384)", (long long)L);
-  SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_summon: bad code type");
-  SVA_REQUIRE(mask_type >= 0 && mask_type <= 4, "sva_summon: bad mask type");
+              "%s: bad rank/PQ layout R=%lld S=%lld C=%lld", fn, (long long)R, (long long)S, (long long)C);
+  SVA_REQUIRE(L > 0 && L <= 16384, "%s: shortlist %lld out of range (1..16384)", fn, (long long)L);
+  SVA_REQUIRE(code_type >= 0 && code_type <= 3, "%s: bad code type", fn);
+  SVA_REQUIRE(mask_type >= 0 && mask_type <= 4, "%s: bad mask type", fn);
   SVA_REQUIRE(mask_type == SVA_MASK_NONE || mask_type == SVA_MASK_BOOL || mask != nullptr,
-              "sva_summon: mask type given without a mask");
-  SVA_REQUIRE(mask_type == SVA_MASK_NONE || n_seq == 1, "sva_summon: masks apply to a single sequence");
+              "%s: mask type given without a mask", fn);
+  SVA_REQUIRE(mask_type == SVA_MASK_NONE || n_seq == 1, "%s: masks apply to a single sequence", fn);
   SVA_REQUIRE(R != 64 || (((uintptr_t)k_low & 15u) == 0 && k_low_head_stride % 4 == 0),
-              "sva_summon: k_low must be 16-byte aligned");
+              "%s: k_low must be 16-byte aligned", fn);
   const int64_t items = n_seq * H * Q;
-  SVA_REQUIRE(items < (1ll << 31), "sva_summon: too many query items");
+  SVA_REQUIRE(items < (1ll << 31), "%s: too many query items", fn);
   sva::SummonParams p;
   p.lut = lut;
   p.range = score_range;
@@ -248,11 +248,50 @@ extern "C" int sva_summon(const float* lut, const float* score_range, const floa
   p.sl_idx = sl_idx;
   p.sl_rank = sl_rank;
   p.sl_count = sl_count;
+  p.B = (int)B;
+  p.fin_idx = fin_idx;
+  p.fin_count = fin_count;
   if (n_keys == 0) {
-    return sva::fill_i32(sl_count, items, 0, (hipStream_t)stream);
+    int rc = sva::fill_i32(sl_count, items, 0, (hipStream_t)stream);
+    if (rc == SVA_OK && B > 0) rc = sva::fill_i32(fin_count, items, 0, (hipStream_t)stream);
+    return rc;
   }
   if (sva::summon_wide_eligible(p, items)) {
     return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream);
   }
-  return sva::summon_item_path(p, items, (hipStream_t)stream);
+  int rc = sva::summon_item_path(p, items, (hipStream_t)stream);
+  if (rc == SVA_OK && B > 0)
+    rc = sva::budget_select_launch(sl_idx, sl_rank, sl_count, items, L, B, fin_idx, fin_count, (hipStream_t)stream);
+  return rc;
+}
+
+}  // namespace
+
+extern "C" int sva_summon(const float* lut, const float* score_range, const float* q_low, const void* codes,
+                          int code_type, int64_t code_head_stride, const float* k_low, int64_t k_low_head_stride,
+                          const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
+                          int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
+                          int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  sva::clear_error();
+  return summon_impl("sva_summon", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
+                     k_low_head_stride, seq_offsets, seq_lens, n_seq, H, Q, n_keys, R, S, C, L, mask, mask_type,
+                     mask_tok_stride, sl_idx, sl_rank, sl_count, 0, nullptr, nullptr, workspace, workspace_bytes,
+                     stream);
+}
+
+extern "C" int sva_summon_select(const float* lut, const float* score_range, const float* q_low, const void* codes,
+                                 int code_type, int64_t code_head_stride, const float* k_low,
+                                 int64_t k_low_head_stride, const int64_t* seq_offsets, const int64_t* seq_lens,
+                                 int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S, int64_t C,
+                                 int64_t L, const void* mask, int mask_type, int64_t mask_tok_stride, int32_t* sl_idx,
+                                 float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx, int32_t* fin_count,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(fin_idx && fin_count, "sva_summon_select: null pointer");
+  SVA_REQUIRE(B > 0 && B <= 8192, "sva_summon_select: budget %lld out of range (1..8192)", (long long)B);
+  return summon_impl("sva_summon_select", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
+                     k_low_head_stride, seq_offsets, seq_lens, n_seq, H, Q, n_keys, R, S, C, L, mask, mask_type,
+                     mask_tok_stride, sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes,
+                     stream);
 }

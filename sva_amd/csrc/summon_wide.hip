@@ -1,6 +1,6 @@
 // Long-context summon for few query items (decode, q = 1): many workgroups
-// per item, three kernels, no grid-wide synchronisation and no atomics on
-// shared global words.
+// per item for the scan, one per item for the rest; two kernels, no
+// grid-wide synchronisation and no atomics on shared global words.
 //
 //   wide_scan     one workgroup per chunk of WB * 32 keys.  Streams the
 //                 chunk's packed uint8 codes (16-byte loads, all in flight
@@ -9,14 +9,14 @@
 //                 reaches the item's sampled floor t_lo to its wave's own
 //                 candidate list as a unique 64-bit composite (score key,
 //                 key index); counts go to the wave's own counter words.
-//   wide_select   one workgroup per item.  Gathers the candidates (~4x the
-//                 shortlist for the sampled floor) into LDS and radix-selects
-//                 the L largest composites exactly, writing their key
-//                 indices.  When the floor overshot (fewer than L candidates)
-//                 it selects over every key of the item instead: slower, same
-//                 result.
-//   wide_rescore  many workgroups per item: rank score of every shortlisted
-//                 key (k_low . q_low in torch's sum order, 16 lanes per row).
+//   wide_finish   one workgroup per item.  Gathers the candidates (~4x the
+//                 shortlist for the sampled floor) into LDS, selects the L
+//                 largest composites exactly (shortlist), scores them with
+//                 k_low . q_low in torch's sum order (rank), and, when a
+//                 budget is asked for, selects the B best ranks and writes
+//                 them in ascending key order.  When the floor overshot
+//                 (fewer than L candidates) the shortlist is selected over
+//                 every key of the item instead: slower, same result.
 // Selection equals a full sort by (score desc, key index asc): with R = 64
 // the score is the sum / 8 exactly, so every key below the floor ranks
 // strictly below every candidate.
@@ -36,8 +36,7 @@ constexpr int WAVE_KEYS = WAVE * KEYS_PT;  // keys (and candidate capacity) per 
 constexpr int SB = 1024;         // threads of the select kernel
 constexpr int SNW = SB / WAVE;
 constexpr int LDS_CAND = 16384;  // candidates the select kernel stages in LDS
-constexpr int RROWS = 64;        // rows per rescore workgroup
-constexpr int RB = 256;          // threads per rescore workgroup
+constexpr int KL_CAP = 256;      // candidate keys per scan wave kept in LDS for the rank scores
 constexpr int64_t kWideMinKeys = 32768;
 constexpr int64_t kMaxWideItems = 64;
 
@@ -48,10 +47,20 @@ struct WideArgs {
   uint32_t* ncand;   // [items, W * NW] candidates of each scan wave
   uint32_t* nallow;  // [items, W * NW] allowed keys of each scan wave
   uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
+  float* rank;       // [items, N] rank score of every candidate, by key index
   int W;             // scan workgroups per item
 };
 
 SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
+
+// First key of round r of the calling lane: wave w of the workgroup owns keys
+// [cs + w * WAVE_KEYS, cs + (w + 1) * WAVE_KEYS), and in round r its lanes
+// take consecutive groups of 16 / S keys (one 16-byte word of codes each).
+template <int S>
+SVA_DEV int round_key(int cs, int r) {
+  constexpr int KPT = 16 / S;
+  return cs + (int)(threadIdx.x / WAVE) * WAVE_KEYS + (r * WAVE + lane_id()) * KPT;
+}
 
 // Loads a chunk's codes: every full 16-byte group with one unconditional
 // vector load (all issued before any is used); a partial last chunk falls
@@ -63,13 +72,13 @@ SVA_DEV void load_chunk(const uint8_t* __restrict__ codes, int cs, int ce, u32x4
   if (ce - cs == CHUNK) {
 #pragma unroll
     for (int r = 0; r < RND; ++r) {
-      const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
+      const int base = round_key<S>(cs, r);
       raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + (int64_t)base * S));
     }
   } else {
 #pragma unroll
     for (int r = 0; r < RND; ++r) {
-      const int base = cs + (r * WB + (int)threadIdx.x) * KPT;
+      const int base = round_key<S>(cs, r);
       if (base + KPT <= ce) {
         raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + (int64_t)base * S));
       } else {
@@ -143,7 +152,7 @@ SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, BP>& T, float (&a
 template <int S>
 SVA_DEV int slot_key(int cs, int i) {
   constexpr int KPT = 16 / S;
-  return cs + ((i / KPT) * WB + (int)threadIdx.x) * KPT + (i % KPT);
+  return round_key<S>(cs, i / KPT) + (i % KPT);
 }
 
 template <bool FULL, bool MASKED>
@@ -151,32 +160,6 @@ SVA_DEV bool key_ok(const SummonParams& p, int n, int ce) {
   bool ok = FULL || n < ce;
   if (MASKED && ok) ok = mask_allows(p.mask, n, p.mask_type);
   return ok;
-}
-
-// Rank score of a 64-float k_low row in torch's sum order, computed by the
-// 16-lane group of the calling lane (lane j holds float4 j of the row; the
-// pairing, lane chains and final order follow torch_order_dot64).  Every lane
-// of the group receives the result.  All 16 lanes must call it.
-SVA_DEV float rank_dot64_group16(const float* __restrict__ row, const float* __restrict__ q) {
-#pragma clang fp contract(off)
-  const int j = lane_id() & 15;
-  const float4 r = reinterpret_cast<const float4*>(row)[j];
-  const float4 qq = reinterpret_cast<const float4*>(q)[j];
-  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
-  // element e (< 32) pairs with e + 32, held by lane j + 8
-  const float a0 = (0.0f + p0) + __shfl_down(p0, 8, 16);
-  const float a1 = (0.0f + p1) + __shfl_down(p1, 8, 16);
-  const float a2 = (0.0f + p2) + __shfl_down(p2, 8, 16);
-  const float a3 = (0.0f + p3) + __shfl_down(p3, 8, 16);
-  // lanes g, g+2, g+4, g+6 hold accumulators 0..3 of lane-group g
-  const float v0 = ((a0 + __shfl_down(a0, 2, 16)) + __shfl_down(a0, 4, 16)) + __shfl_down(a0, 6, 16);
-  const float v1 = ((a1 + __shfl_down(a1, 2, 16)) + __shfl_down(a1, 4, 16)) + __shfl_down(a1, 6, 16);
-  const float v2 = ((a2 + __shfl_down(a2, 2, 16)) + __shfl_down(a2, 4, 16)) + __shfl_down(a2, 6, 16);
-  const float v3 = ((a3 + __shfl_down(a3, 2, 16)) + __shfl_down(a3, 4, 16)) + __shfl_down(a3, 6, 16);
-  const float w0 = __shfl_down(v0, 1, 16), w1 = __shfl_down(v1, 1, 16);
-  const float w2 = __shfl_down(v2, 1, 16), w3 = __shfl_down(v3, 1, 16);
-  const float t = (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
-  return __shfl(t, 0, 16);
 }
 
 // Exact score of key n from the global table (the reference's order, with the
@@ -202,16 +185,31 @@ SVA_DEV float item_floor(const SummonParams& p, int item) {
   return est > lo ? est : lo;
 }
 
-// Appends the keys of slot i whose flag c is set to the wave's candidate
-// list (in lane order), as composites of the exact score acc / sqrt(R).
-SVA_DEV void append_candidate(const SummonParams& p, bool c, float acc, int n, uint64_t* out, uint32_t& wc) {
+// Appends the flagged keys of one round (key n0 + k for flag c[k]) to the
+// wave's candidate list in ascending key order (lanes in order, each lane's
+// keys in order), as composites of the exact score acc / sqrt(R); the first
+// KL_CAP key indices also go to the wave's LDS list `keys`.
+template <int KPT>
+SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const float (&acc)[KPT], int n0, uint64_t* out,
+                          uint32_t* keys, uint32_t& wc) {
 #pragma clang fp contract(off)
-  const uint64_t m = __builtin_amdgcn_ballot_w64(c);
-  if (c) {
-    const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-    out[wc + below] = composite(f2key(acc / p.sqrt_r), (uint32_t)n);
+  uint32_t below = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(c[k]);
+    below += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    tot += (uint32_t)__popcll(m);
   }
-  wc += (uint32_t)__popcll(m);
+  uint32_t o = wc + below;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    if (c[k]) {
+      out[o] = composite(f2key(acc[k] / p.sqrt_r), (uint32_t)(n0 + k));
+      if (o < (uint32_t)KL_CAP) keys[o] = (uint32_t)(n0 + k);
+      ++o;
+    }
+  }
+  wc += tot;
 }
 
 // The scan of one thread's slots.  CHECK: the chunk is partial or masked, so
@@ -220,7 +218,8 @@ SVA_DEV void append_candidate(const SummonParams& p, bool c, float acc, int n, u
 // sum reaches the floor.
 template <int S, bool BP, bool CHECK, bool MASKED>
 SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, BP>& T,
-                         float t_lo, int cs, int ce, uint64_t* out, uint32_t& wc, uint32_t& n_allowed) {
+                         float t_lo, int cs, int ce, uint64_t* out, uint32_t* keys, uint32_t& wc,
+                         uint32_t& n_allowed) {
   constexpr int KPT = 16 / S;
 #pragma unroll
   for (int r = 0; r < KEYS_PT / KPT; ++r) {
@@ -236,28 +235,85 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
         c[k] = ok && acc[k] >= t_lo;
         any = any || c[k];
       }
-      if (__builtin_amdgcn_ballot_w64(any) != 0ull) {
-#pragma unroll
-        for (int k = 0; k < KPT; ++k) append_candidate(p, c[k], acc[k], slot_key<S>(cs, r * KPT + k), out, wc);
-      }
+      if (__builtin_amdgcn_ballot_w64(any) != 0ull) append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, keys, wc);
     } else {
       float mx = acc[0];
 #pragma unroll
       for (int k = 1; k < KPT; ++k) mx = fmaxf(mx, acc[k]);
       if (__builtin_amdgcn_ballot_w64(mx >= t_lo) != 0ull) {  // rare: the shortlist and the keys near it
+        bool c[KPT];
 #pragma unroll
-        for (int k = 0; k < KPT; ++k)
-          append_candidate(p, acc[k] >= t_lo, acc[k], slot_key<S>(cs, r * KPT + k), out, wc);
+        for (int k = 0; k < KPT; ++k) c[k] = acc[k] >= t_lo;
+        append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, keys, wc);
       }
     }
   }
   if (!CHECK) n_allowed = KEYS_PT;
 }
 
+// Row shift within each 16-lane DPP row: lane j receives lane j + N of its
+// row (lanes past the row end receive 0).
+template <int N>
+SVA_DEV float row_down(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
+}
+
+// Rank score of a 64-float k_low row in torch's sum order, computed by the
+// 16 lanes of one DPP row (lane j holds float4 j of the row in r and of the
+// query in qq): element e < 32 pairs with e + 32, the lane chains g, g+2,
+// g+4, g+6 form accumulator lane 4g + c, then the eight in order, as in
+// torch_order_dot64.  The result is valid in the row's first lane.
+SVA_DEV float rank_dot64_row16(const float4 r, const float4 qq) {
+#pragma clang fp contract(off)
+  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
+  const float a0 = (0.0f + p0) + row_down<8>(p0);
+  const float a1 = (0.0f + p1) + row_down<8>(p1);
+  const float a2 = (0.0f + p2) + row_down<8>(p2);
+  const float a3 = (0.0f + p3) + row_down<8>(p3);
+  const float v0 = ((a0 + row_down<2>(a0)) + row_down<4>(a0)) + row_down<6>(a0);
+  const float v1 = ((a1 + row_down<2>(a1)) + row_down<4>(a1)) + row_down<6>(a1);
+  const float v2 = ((a2 + row_down<2>(a2)) + row_down<4>(a2)) + row_down<6>(a2);
+  const float v3 = ((a3 + row_down<2>(a3)) + row_down<4>(a3)) + row_down<6>(a3);
+  const float w0 = row_down<1>(v0), w1 = row_down<1>(v1), w2 = row_down<1>(v2), w3 = row_down<1>(v3);
+  return (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
+}
+
+// Rank scores of a scan wave's nc candidates (keys in the LDS list while
+// they fit, else from the wave's candidate list): one 16-lane DPP row per
+// candidate, 16 candidates in flight per wave; written by key index.
+SVA_DEV void rank_candidates(const SummonParams& p, const WideArgs& a, int item, const uint32_t* keys,
+                             const uint64_t* out, uint32_t nc) {
+#pragma clang fp contract(off)
+  const int j = lane_id() & 15;
+  const int row = lane_id() >> 4;
+  const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
+  const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
+  float* rank = a.rank + (int64_t)item * p.N;
+  if (nc > (uint32_t)KL_CAP) __threadfence();  // keys past the LDS list are read back from `out`
+  constexpr int RU = 4;
+  for (uint32_t c0 = 0; c0 < nc; c0 += 4 * RU) {
+    float4 rv[RU];
+    uint32_t key[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const uint32_t c = c0 + 4 * u + row;
+      key[u] = 0u;
+      if (c < nc) key[u] = c < (uint32_t)KL_CAP ? keys[c] : composite_index(out[c]);
+      rv[u] = c < nc ? reinterpret_cast<const float4*>(klow + (int64_t)key[u] * p.R)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const float dot = rank_dot64_row16(rv[u], qq);
+      if (c0 + 4 * u + row < nc && j == 0) rank[key[u]] = dot / p.sqrt_r;
+    }
+  }
+}
+
 template <int S, bool BP, bool MASKED>
 __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
 #pragma clang fp contract(off)
   __shared__ float tab_lds[BP ? 1 : S * 256];
+  __shared__ uint32_t klist[NW][KL_CAP];
   const SummonParams& p = a.p;
   const int item = blockIdx.x / a.W;
   const int w = blockIdx.x % a.W;
@@ -277,10 +333,11 @@ __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
   if (!MASKED && ce - cs == CHUNK) {
-    scan_rounds<S, BP, false, false>(p, raw, T, t_lo, cs, ce, out, wc, n_allowed);
+    scan_rounds<S, BP, false, false>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
   } else {
-    scan_rounds<S, BP, true, MASKED>(p, raw, T, t_lo, cs, ce, out, wc, n_allowed);
+    scan_rounds<S, BP, true, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
   }
+  rank_candidates(p, a, item, klist[wid], out, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane_id() == 0) {
     a.ncand[sub] = wc;
@@ -288,93 +345,140 @@ __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
   }
 }
 
-__global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
+// LDS of the finish kernel.  The staging area holds the gathered candidates;
+// once they sit in registers it is reused for the selection histogram, the
+// shortlist, its rank composites and the budget gather.
+constexpr int FIN_MAX_L = 8192;
+constexpr size_t kFinStage = sizeof(uint64_t) * LDS_CAND;                       // 128 KB
+constexpr size_t kFinHist = 0;                                                  // uint32[TOP_BINS]
+constexpr size_t kFinSl = kFinHist + sizeof(uint32_t) * TOP_BINS;               // uint32[FIN_MAX_L]
+constexpr size_t kFinRk = kFinSl + sizeof(uint32_t) * FIN_MAX_L;                // uint64[FIN_MAX_L]
+constexpr size_t kFinSmall = kFinRk + sizeof(uint64_t) * FIN_MAX_L;             // uint64[TOP_SMALL]
+static_assert(kFinSmall + sizeof(uint64_t) * TOP_SMALL <= kFinStage, "finish LDS overlay");
+constexpr size_t kFinMisc = sizeof(uint32_t) * (SNW * SNW + SNW + 1 + 7) + sizeof(uint64_t) * 2;
+constexpr size_t kFinLds = kFinStage + kFinMisc;
+
+// Order-preserving compaction of register-held elements: element i of
+// thread t stands at position t + i * BLOCK of the source order; the
+// elements >= X (nonzero) get their rank in that order, at most cap of
+// them.  wcnt: NPT * BLOCK / 64 uint32 in LDS.  Every thread must call it.
+template <int BLOCK, int NPT, typename Emit>
+SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint32_t* wcnt, uint32_t* scratch,
+                             Emit emit) {
+  constexpr int NWV = BLOCK / WAVE;
+  const int wid = threadIdx.x / WAVE;
+  const int lane = lane_id();
+  uint64_t bal[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    bal[i] = __builtin_amdgcn_ballot_w64(e[i] != 0ull && e[i] >= X);
+    if (lane == 0) wcnt[i * NWV + wid] = (uint32_t)__popcll(bal[i]);
+  }
+  __syncthreads();
+  {
+    const uint32_t c = threadIdx.x < NPT * NWV ? wcnt[threadIdx.x] : 0u;
+    uint32_t tot;
+    const uint32_t off = block_excl_scan<BLOCK>(c, scratch, &tot);
+    if (threadIdx.x < NPT * NWV) wcnt[threadIdx.x] = off;
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    if (e[i] != 0ull && e[i] >= X) {
+      const uint32_t o = wcnt[i * NWV + wid] +
+                         __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[i], 0u));
+      if (o < (uint32_t)cap) emit(o, e[i]);
+    }
+  }
+}
+
+// Finish of an item: shortlist select, rank rescore and (B > 0) budget
+// select, one workgroup per item.
+//   1. counts of the scan's per-wave lists; the lists are copied into LDS
+//      in list order, which is ascending key order;
+//   2. every thread takes 16 staged candidates into registers and the L
+//      largest are found by select_top_regs; the selected are compacted in
+//      staging order into the shortlist (LDS and sl_idx, ascending);
+//   3. rank scores k_low . q_low of the shortlist, one 16-lane DPP row per
+//      shortlist row, 16 rows in flight per lane (sl_rank, and composites in
+//      LDS);
+//   4. budget: the B largest rank composites, compacted in shortlist order,
+//      hence ascending.
+// When the sampled floor let more than LDS_CAND keys through, the shortlist
+// is selected straight from the lists in global memory; when it let fewer
+// than L through, from every key of the item.  Both give the same set.
+__global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
+#pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
-  uint64_t* cl = (uint64_t*)lds;                                   // [LDS_CAND]
-  uint32_t(*whist)[256] = (uint32_t(*)[256])(cl + LDS_CAND);       // [SNW][256]
-  uint64_t* shared64 = (uint64_t*)(whist + SNW);                   // [2]
-  uint32_t* scratch = (uint32_t*)(shared64 + 2);                   // [SNW + 1]
+  uint64_t* cl = (uint64_t*)lds;                                   // staging [LDS_CAND]
+  uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // after staging
+  uint32_t* sl = (uint32_t*)(lds + kFinSl);
+  uint64_t* rk = (uint64_t*)(lds + kFinRk);
+  uint64_t* small = (uint64_t*)(lds + kFinSmall);
+  uint32_t* wcnt = (uint32_t*)(lds + kFinStage);                   // [SNW * SNW] compaction counts
+  uint32_t* scratch = wcnt + SNW * SNW;                            // [SNW + 1]
   uint32_t* shared = scratch + SNW + 1;                            // [4]
+  uint64_t* shared64 = (uint64_t*)(((uintptr_t)(shared + 4) + 7) & ~(uintptr_t)7);  // [2]
+  const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
   const int item = blockIdx.x;
+  const int wid = threadIdx.x / WAVE;
+  const int lane = lane_id();
   const int nsub = a.W * NW;
   const uint32_t* ncand = a.ncand + (int64_t)item * nsub;
   const uint32_t* nallow = a.nallow + (int64_t)item * nsub;
   const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
-  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  // totals: candidates M and allowed keys A.  With at most SB lists (every
-  // cache up to 2M keys) one pass also yields each list's staging offset.
-  const bool one_pass = nsub <= SB;
+  // 1. totals: candidates M and allowed keys A
   uint32_t m = 0, al = 0;
   for (int s = threadIdx.x; s < nsub; s += SB) {
     m += ncand[s];
     al += nallow[s];
   }
-  uint32_t M;
-  const uint32_t my_base = block_excl_scan<SB>(m, scratch, &M);
-  uint32_t A;
+  uint32_t M, A;
+  block_excl_scan<SB>(m, scratch, &M);
   block_excl_scan<SB>(al, scratch, &A);
   const int leff = (int)min((uint32_t)p.L, A);
+  const int beff = min(p.B, leff);
   if (threadIdx.x == 0) {
     p.sl_count[item] = leff;
-    shared[3] = 0u;  // output carry of the list-by-list path
+    if (p.B > 0) p.fin_count[item] = beff;
+    shared[3] = 0u;
   }
   if (leff == 0) return;
   if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND) {
-    // common case: stage the candidates contiguously in LDS, taking the
-    // OR / AND bounds of the radix select on the way
-    uint64_t vor = 0ull, vand = ~0ull;
-    if (one_pass) {
-      const int s = threadIdx.x;
+    // stage the lists in order, one list per thread
+    uint32_t carry = 0;
+    for (int g = 0; g < nsub; g += SB) {
+      const int s = g + (int)threadIdx.x;
+      const uint32_t c = s < nsub ? ncand[s] : 0u;
+      uint32_t tot;
+      const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
       if (s < nsub) {
         const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
 #pragma unroll 8
-        for (uint32_t j = 0; j < m; ++j) {
-          const uint64_t x = src[j];
-          cl[my_base + j] = x;
-          vor |= x;
-          vand &= x;
-        }
+        for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
       }
-    } else {
-      uint32_t carry = 0;
-      for (int g = 0; g < nsub; g += SB) {
-        const int s = g + (int)threadIdx.x;
-        const uint32_t c = s < nsub ? ncand[s] : 0u;
-        uint32_t tot;
-        const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
-        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
-#pragma unroll 8
-        for (uint32_t j = 0; j < c; ++j) {
-          const uint64_t x = src[j];
-          cl[base + j] = x;
-          vor |= x;
-          vand &= x;
-        }
-        carry += tot;
-      }
+      carry += tot;
+      __syncthreads();
     }
-    __syncthreads();
-    const int Mi = (int)M;
-    auto visit = [&](auto&& f) {
-      for (int j = threadIdx.x; j < Mi; j += SB) f(cl[j]);
-    };
-    const uint64_t X = (uint32_t)leff == M
-                           ? 1ull
-                           : select_largest_with_bounds<SB>(visit, leff, vor, vand, whist, scratch, shared64, shared);
-    // write the selected in staging order: contiguous ranges per thread
-    const int per = (Mi + SB - 1) / SB;
-    const int j0 = min(Mi, (int)threadIdx.x * per), j1 = min(Mi, j0 + per);
-    uint32_t cnt = 0;
-    for (int j = j0; j < j1; ++j) cnt += cl[j] >= X;
-    uint32_t tot;
-    uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
-    for (int j = j0; j < j1; ++j) {
-      const uint64_t x = cl[j];
-      if (x >= X && o < (uint32_t)leff) out_idx[o++] = (int32_t)composite_index(x);
+    // 2. candidates into registers, shortlist select
+    constexpr int NPT = LDS_CAND / SB;
+    uint64_t e[NPT];
+    uint64_t vor = 0ull, vand = ~0ull;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const int j = (int)threadIdx.x + i * SB;
+      e[i] = j < (int)M ? cl[j] : 0ull;
+      vor |= j < (int)M ? e[i] : 0ull;
+      vand &= j < (int)M ? e[i] : ~0ull;
     }
+    __syncthreads();  // staging area free
+    const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, vor, vand, tl);
+    // shortlist in staging order (ascending key index)
+    compact_ordered<SB, NPT>(e, X, leff, wcnt, scratch, [&](uint32_t o, uint64_t x) { sl[o] = composite_index(x); });
   } else if (M >= (uint32_t)leff) {
     // many candidates: select straight from the per-wave lists
+    uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
     auto visit = [&](auto&& f) {
       for (int s = threadIdx.x; s < nsub; s += SB) {
         const uint32_t c = ncand[s];
@@ -383,6 +487,8 @@ __global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
       }
     };
     const uint64_t X = (uint32_t)leff == M ? 1ull : select_largest<SB>(visit, leff, whist, scratch, shared64, shared);
+    if (threadIdx.x == 0) shared[3] = 0u;
+    __syncthreads();
     for (int g = 0; g < nsub; g += SB) {
       const int s = g + (int)threadIdx.x;
       const uint32_t c = s < nsub ? ncand[s] : 0u;
@@ -392,13 +498,14 @@ __global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
       uint32_t tot;
       uint32_t o = shared[3] + block_excl_scan<SB>(cnt, scratch, &tot);
       for (uint32_t j = 0; j < c; ++j)
-        if (src[j] >= X && o < (uint32_t)leff) out_idx[o++] = (int32_t)composite_index(src[j]);
+        if (src[j] >= X && o < (uint32_t)leff) sl[o++] = composite_index(src[j]);
       __syncthreads();
       if (threadIdx.x == 0) shared[3] += tot;
       __syncthreads();
     }
   } else {
     // the sampled floor overshot: exact selection over every key of the item
+    uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
     const int h = item % p.H;
     const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
     const int N = (int)p.N;
@@ -420,33 +527,51 @@ __global__ void __launch_bounds__(SB) wide_select_kernel(WideArgs a) {
     uint32_t tot;
     uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
     for (int n = n0; n < n1; ++n)
-      if (key_at(n) >= X && o < (uint32_t)leff) out_idx[o++] = n;
+      if (key_at(n) >= X && o < (uint32_t)leff) sl[o++] = (uint32_t)n;
   }
-}
-
-constexpr size_t kSelectLds = sizeof(uint64_t) * (LDS_CAND + 2) + sizeof(uint32_t) * (SNW * 256 + SNW + 1 + 4);
-
-// Rank scores of the shortlist: RROWS rows per workgroup, 16 lanes per row.
-__global__ void __launch_bounds__(RB) wide_rescore_kernel(WideArgs a) {
-  const SummonParams& p = a.p;
-  const int item = blockIdx.y;
-  const int h = item % p.H;
-  const int count = p.sl_count[item];
-  const int row0 = blockIdx.x * RROWS;
-  if (row0 >= count) return;
-  const float* ql = p.q_low + (int64_t)item * p.R;
-  const float* klow = p.k_low + (int64_t)h * p.klow_hs;
-  const int32_t* idx = p.sl_idx + (int64_t)item * p.L;
-  float* rank = p.sl_rank + (int64_t)item * p.L;
-  const int g = threadIdx.x >> 4;  // 16-lane group
-  for (int r = row0 + g; r < row0 + RROWS; r += RB / 16) {
-    if (r - g >= count) break;  // uniform per wave: every group of the wave passes the same r - g
-    const bool valid = r < count;
-    int32_t key = idx[valid ? r : row0];
-    key = key < 0 ? 0 : (key >= (int32_t)p.N ? (int32_t)p.N - 1 : key);
-    const float dot = rank_dot64_group16(klow + (int64_t)key * p.R, ql);
-    if (valid && (lane_id() & 15) == 0) rank[r] = dot / p.sqrt_r;
+  __syncthreads();
+  // 3. shortlist out with its rank scores: computed by the scan for every
+  // candidate; the all-keys path scores its shortlist here
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  float* rkf = (float*)rk;  // [leff] ranks of the all-keys path
+  const bool ranks_here = M < (uint32_t)leff;
+  if (ranks_here) {
+    const int j = lane & 15;
+    const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
+    const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
+    for (int r = threadIdx.x >> 4; r < leff; r += SB / 16) {
+      const uint32_t key = sl[r];
+      const float dot = rank_dot64_row16(reinterpret_cast<const float4*>(klow + (int64_t)key * p.R)[j], qq);
+      if (j == 0) rkf[r] = dot / p.sqrt_r;
+    }
+    __syncthreads();
   }
+  constexpr int NPB = FIN_MAX_L / SB;
+  const float* rank_of = a.rank + (int64_t)item * p.N;
+  uint64_t e2[NPB];
+  uint64_t vor = 0ull, vand = ~0ull;
+#pragma unroll
+  for (int i = 0; i < NPB; ++i) {
+    const int r = (int)threadIdx.x + i * SB;
+    e2[i] = 0ull;
+    if (r < leff) {
+      const uint32_t key = sl[r];
+      const float rank = ranks_here ? rkf[r] : rank_of[key];
+      out_idx[r] = (int32_t)key;
+      out_rank[r] = rank;
+      e2[i] = composite(f2key(rank), key);
+      vor |= e2[i];
+      vand &= e2[i];
+    }
+  }
+  if (p.B <= 0) return;
+  // 4. budget select over the rank composites
+  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPB>(e2, beff, vor, vand, tl);
+  // the shortlist is in ascending key order, so is an ordered compaction
+  int32_t* fin = p.fin_idx + (int64_t)item * p.B;
+  compact_ordered<SB, NPB>(e2, X2, beff, wcnt, scratch,
+                           [&](uint32_t o, uint64_t x) { fin[o] = (int32_t)composite_index(x); });
 }
 
 template <int S, bool BP, bool MASKED>
@@ -455,16 +580,13 @@ int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
   SVA_CHECK_LAUNCH("wide_scan_kernel");
   static bool attr_set = false;
   if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)wide_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)kSelectLds),
-                  "hipFuncSetAttribute(wide_select_kernel)");
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)wide_finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)kFinLds),
+                  "hipFuncSetAttribute(wide_finish_kernel)");
     attr_set = true;
   }
-  hipLaunchKernelGGL(wide_select_kernel, dim3((unsigned)items), dim3(SB), kSelectLds, stream, a);
-  SVA_CHECK_LAUNCH("wide_select_kernel");
-  const dim3 rgrid((unsigned)((a.p.L + RROWS - 1) / RROWS), (unsigned)items);
-  hipLaunchKernelGGL(wide_rescore_kernel, rgrid, dim3(RB), 0, stream, a);
-  SVA_CHECK_LAUNCH("wide_rescore_kernel");
+  hipLaunchKernelGGL(wide_finish_kernel, dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
+  SVA_CHECK_LAUNCH("wide_finish_kernel");
   return SVA_OK;
 }
 
@@ -490,6 +612,7 @@ bool summon_wide_eligible(const SummonParams& p, int64_t items) {
   if (p.Q != 1 || p.offs != nullptr || p.ctype != CODE_U8 || p.C > 256) return false;
   if (p.S != 1 && p.S != 2 && p.S != 4 && p.S != 8) return false;
   if (p.R != 64 || p.N < kWideMinKeys || p.N >= (1ll << 30) || items > kMaxWideItems) return false;
+  if (p.L > FIN_MAX_L) return false;
   if (((uintptr_t)p.codes & 15u) != 0 || p.code_hs % 16 != 0) return false;
   if (((uintptr_t)p.k_low & 15u) != 0 || p.klow_hs % 4 != 0 || ((uintptr_t)p.q_low & 15u) != 0) return false;
   if (p.mask_type != MASK_NONE && p.mask_type != MASK_BOOL && p.mask == nullptr) return false;
@@ -500,7 +623,8 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   const int64_t items = n_seq * H * Q;
   if (n_seq != 1 || Q != 1 || n_keys < kWideMinKeys || items > kMaxWideItems) return 256;
   const int64_t W = (n_keys + CHUNK - 1) / CHUNK;
-  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * sizeof(uint64_t);
+  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * sizeof(uint64_t) +
+         (((size_t)items * (size_t)n_keys * sizeof(float) + 255) & ~(size_t)255);
 }
 
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -515,6 +639,7 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   a.ncand = (uint32_t*)ws;
   a.nallow = a.ncand + items * a.W * NW;
   a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
+  a.rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
   // a bool mask allows every key (the reference's `mask > -1e4` rule)
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
   switch (p.S) {

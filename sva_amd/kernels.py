@@ -197,6 +197,38 @@ def budget_select(sl_idx: torch.Tensor, sl_rank: torch.Tensor, sl_count: torch.T
     return fin_idx, fin_count
 
 
+def summon_select(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist: int, budget: int,
+                  mask: torch.Tensor | None = None, seq_offsets: torch.Tensor | None = None,
+                  seq_lens: torch.Tensor | None = None):
+    """Shortlist and budget in one call (sva/llama.py:262-302):
+    (sl_idx, sl_rank, sl_count, fin_idx, fin_count)."""
+
+    n_seq, heads, q_len, subspaces, codewords = lut.shape
+    rank = q_low.shape[-1]
+    _check_catalog("codes", codes, heads, subspaces)
+    _check_catalog("k_low", k_low, heads, rank)
+    device = require_device(lut, score_range, q_low, codes, k_low, seq_offsets, seq_lens, mask)
+    items = n_seq * heads * q_len
+    sl_idx = torch.empty(items, shortlist, device=device, dtype=torch.int32)
+    sl_rank = torch.empty(items, shortlist, device=device, dtype=torch.float32)
+    sl_count = torch.empty(items, device=device, dtype=torch.int32)
+    fin_idx = torch.empty(items, budget, device=device, dtype=torch.int32)
+    fin_count = torch.empty(items, device=device, dtype=torch.int32)
+    m, mtype, mstride = mask_args(mask, q_len, n_keys)
+    ws_bytes = int(lib().sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
+    ws = workspace(device, ws_bytes)
+    check(
+        lib().sva_summon_select(
+            ptr(lut), ptr(score_range), ptr(q_low), ptr(codes), code_type(codes), codes.stride(0), ptr(k_low),
+            k_low.stride(0), ptr(seq_offsets), ptr(seq_lens), n_seq, heads, q_len, n_keys, rank, subspaces,
+            codewords, shortlist, ptr(m), mtype, mstride, ptr(sl_idx), ptr(sl_rank), ptr(sl_count), budget,
+            ptr(fin_idx), ptr(fin_count), ptr(ws), ws.numel(), stream_handle(device),
+        ),
+        "sva_summon_select",
+    )
+    return sl_idx, sl_rank, sl_count, fin_idx, fin_count
+
+
 def verify(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, fin_idx: torch.Tensor,
            fin_count: torch.Tensor, n_keys: int, scaling: float, out_dtype: torch.dtype | None = None,
            seq_offsets: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None) -> torch.Tensor:
@@ -235,8 +267,8 @@ def scan_decode(q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys:
 
     q = _as_query(q)
     q_low, lut, rng = query_lut(q, q_proj, scale, codebooks, codes, n_keys, shortlist)
-    sl_idx, sl_rank, sl_count = summon(lut, rng, q_low, codes, k_low, n_keys, shortlist, mask, seq_offsets, seq_lens)
-    fin_idx, fin_count = budget_select(sl_idx, sl_rank, sl_count, budget)
+    _, _, sl_count, fin_idx, fin_count = summon_select(lut, rng, q_low, codes, k_low, n_keys, shortlist, budget, mask,
+                                                       seq_offsets, seq_lens)
     out = verify(q, keys, values, fin_idx, fin_count, n_keys, scaling, out_dtype, seq_offsets, seq_lens)
     return out, sl_count, fin_count
 
@@ -249,8 +281,8 @@ class ScanDecodePlan:
     """Preallocated scan-mode decode lookup for a fixed query shape.
 
     Holds every intermediate buffer (q_low, LUT, shortlist, budget lists) so a
-    decode step issues its four launches (query_lut, summon, budget select,
-    verify) with no allocation and one ctypes call each."""
+    decode step issues its three calls (query_lut, summon with the budget
+    select, verify) with no allocation and one ctypes call each."""
 
     def __init__(self, device, n_seq: int, heads: int, q_len: int, head_dim: int, rank: int, subspaces: int,
                  codewords: int, shortlist: int, budget: int):
@@ -282,14 +314,12 @@ class ScanDecodePlan:
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
         ws_bytes = int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
         ws = workspace(self.device, ws_bytes)
-        check(L.sva_summon(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(), codes.data_ptr(),
-                           code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), None, None, n_seq,
-                           heads, q_len, n_keys, rank, subspaces, codewords, shortlist, ptr(m), mtype, mstride,
-                           self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(), ws.data_ptr(),
-                           ws.numel(), stream), "sva_summon")
-        check(L.sva_budget_select(self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(),
-                                  n_seq * heads * q_len, shortlist, budget, self.fin_idx.data_ptr(),
-                                  self.fin_count.data_ptr(), stream), "sva_budget_select")
+        check(L.sva_summon_select(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(), codes.data_ptr(),
+                                  code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), None, None,
+                                  n_seq, heads, q_len, n_keys, rank, subspaces, codewords, shortlist, ptr(m), mtype,
+                                  mstride, self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(),
+                                  budget, self.fin_idx.data_ptr(), self.fin_count.data_ptr(), ws.data_ptr(),
+                                  ws.numel(), stream), "sva_summon_select")
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
         vws = workspace(self.device, int(L.sva_verify_workspace_bytes(n_seq, heads, keys.shape[0], q_len, head_dim,

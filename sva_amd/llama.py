@@ -206,8 +206,8 @@ class SVALlamaAttention(nn.Module):
             qc = query[:, :, qs:qe, :]
             q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks,
                                                 codes, k_len, shortlist)
-            sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes, k_low, k_len, shortlist, mask=m)
-            fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, budget)
+            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, k_len, shortlist,
+                                                                       budget, mask=m)
             outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, k_len, self.scaling,
                                        out_dtype=query.dtype))
             if self.stats is not None:

@@ -57,7 +57,7 @@ def test_summon_strategy_selection():
     assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 4, 64, 2048, 3, 0) == 0  # int64 codes
 
 
-@pytest.mark.parametrize("call", ["query_lut", "summon", "budget", "verify"])
+@pytest.mark.parametrize("call", ["query_lut", "summon", "summon_select", "budget", "verify"])
 def test_null_pointers_are_rejected_with_a_message(call):
     lib = _lib()
     if call == "query_lut":
@@ -66,6 +66,9 @@ def test_null_pointers_are_rejected_with_a_message(call):
     elif call == "summon":
         rc = lib.sva_summon(None, None, None, None, 0, 0, None, 0, None, None, 1, 9, 1, 100, 64, 2, 256, 16, None, 0,
                             0, None, None, None, None, 0, None)
+    elif call == "summon_select":
+        rc = lib.sva_summon_select(None, None, None, None, 0, 0, None, 0, None, None, 1, 9, 1, 100, 64, 2, 256, 16,
+                                   None, 0, 0, None, None, None, 4, None, None, None, 0, None)
     elif call == "budget":
         rc = lib.sva_budget_select(None, None, None, 9, 16, 4, None, None, None)
     else:
@@ -74,6 +77,16 @@ def test_null_pointers_are_rejected_with_a_message(call):
     assert rc == 1  # SVA_INVALID_ARGUMENT
     msg = lib.sva_last_error().decode()
     assert "null" in msg or "pointer" in msg, msg
+
+
+def test_summon_select_rejects_bad_budget():
+    lib = _lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: the arguments are refused first
+    for B in (0, 8193):
+        rc = lib.sva_summon_select(p, p, p, p, 0, 0, p, 0, None, None, 1, 9, 1, 100, 64, 2, 256, 16, None, 0, 0, p, p,
+                                   p, B, p, p, p, 1 << 20, None)
+        assert rc == 1
+        assert "budget" in lib.sva_last_error().decode()
 
 
 def test_device_tensors_are_required():

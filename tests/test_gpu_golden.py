@@ -39,3 +39,13 @@ def test_gpu_path_matches_reference_outputs(device):
     golden_check.check(ref, inp, k_low.cpu().numpy(), codes.cpu().numpy(), q_low[0, :, 0].cpu().numpy(),
                        lut[0, :, 0].cpu().numpy(), [sl[h, : sl_count[h]] for h in range(H)],
                        [fin[h, : fin_count[h]] for h in range(H)], out[0, :, 0].cpu().numpy())
+    # the fused summon + budget call gives the same lists
+    fused = kernels.summon_select(lut, rng, q_low, codes, k_low, N, L, B)
+    torch.cuda.synchronize()
+    f_sl, f_cnt, f_fin, f_fcnt = (fused[0].cpu().numpy(), fused[2].cpu().numpy(), fused[3].cpu().numpy(),
+                                  fused[4].cpu().numpy())
+    np.testing.assert_array_equal(f_cnt, sl_count)
+    np.testing.assert_array_equal(f_fcnt, fin_count)
+    for h in range(H):
+        np.testing.assert_array_equal(f_sl[h, : sl_count[h]], sl[h, : sl_count[h]])
+        np.testing.assert_array_equal(f_fin[h, : fin_count[h]], fin[h, : fin_count[h]])

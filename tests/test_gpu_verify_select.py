@@ -112,7 +112,8 @@ def test_verify_ragged_sequences(device):
 
 
 @pytest.mark.parametrize("L,B,distinct", [(2048, 512, 1 << 30), (2048, 512, 40), (700, 97, 3), (300, 512, 1 << 30),
-                                          (4096, 1, 5)])
+                                          (4096, 1, 5), (8192, 2048, 1 << 30), (16384, 8192, 1000),
+                                          (16384, 1000, 1 << 30)])
 def test_budget_select_matches_oracle(device, L, B, distinct):
     from sva_amd import kernels
 

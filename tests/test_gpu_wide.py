@@ -147,3 +147,91 @@ def test_wide_candidates_beyond_lds_stage(device):
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=23, few=True)
     res = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)
     _check(codes, k_low, *res, 2048)
+
+
+def _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B, mask=None):
+    from sva_amd import kernels
+
+    codes_t = torch.from_numpy(codes).to(device)
+    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q).to(device), torch.from_numpy(q_proj).to(device),
+                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device),
+                                        codes_t, codes.shape[1], L)
+    fused = kernels.summon_select(lut, rng, q_low, codes_t, k_low, codes.shape[1], L, B, mask=mask)
+    sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes_t, k_low, codes.shape[1], L, mask=mask)
+    fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, B)
+    torch.cuda.synchronize()
+    return ([t.cpu().numpy() for t in fused], [t.cpu().numpy() for t in (sl_idx, sl_rank, sl_count, fin_idx, fin_count)],
+            q_low[0, :, 0].cpu().numpy(), lut[0, :, 0].cpu().numpy())
+
+
+def _check_fused(codes, k_low, fused, split, q_low, lut, L, B, allowed=None):
+    sl_idx, sl_rank, sl_count, fin_idx, fin_count = fused
+    # the shortlist and its ranks are the summon's, slot for slot
+    np.testing.assert_array_equal(sl_count, split[2])
+    for h in range(codes.shape[0]):
+        c = int(sl_count[h])
+        np.testing.assert_array_equal(sl_idx[h, :c], split[0][h, :c])
+        np.testing.assert_array_equal(sl_rank[h, :c].view(np.uint32), split[1][h, :c].view(np.uint32))
+    _check(codes, k_low, q_low, lut, sl_idx, sl_rank, sl_count, L, allowed=allowed)
+    # the budget lists are the standalone select's, and the oracle's
+    np.testing.assert_array_equal(fin_count, split[4])
+    for h in range(codes.shape[0]):
+        c, b = int(sl_count[h]), int(fin_count[h])
+        assert b == min(B, c)
+        np.testing.assert_array_equal(fin_idx[h, :b], split[3][h, :b])
+        keep = oracle.topk(sl_rank[h, :c], b, key_index=sl_idx[h, :c])
+        np.testing.assert_array_equal(fin_idx[h, :b], np.sort(sl_idx[h, :c][keep]))
+
+
+@pytest.mark.parametrize("N,S,C,L,B,few", [(1048576, 4, 64, 2048, 512, False), (200003, 2, 256, 8192, 2048, False),
+                                           (65536, 1, 256, 2048, 3000, False), (120000, 2, 256, 2048, 512, True),
+                                           (1048576, 2, 256, 512, 128, False)])
+def test_wide_summon_select_fused(device, N, S, C, L, B, few):
+    assert _strategy(9, N, 64, S, C, L) == 1, "wide path not selected"
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=(N + L) % 89, few=few)
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B)
+    _check_fused(codes, k_low, fused, split, q_low, lut, L, B)
+
+
+def test_summon_select_fallbacks_and_mask(device):
+    # overshot floor (all-keys selection), candidates beyond the LDS stage,
+    # and a float mask, each through the fused call
+    N, S, C, H = 100000, 4, 64, 3
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=19)
+    ql = oracle.query_low(q, q_proj, scale)[:, 0]
+    for h in range(H):
+        best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
+        for blk in range(16):
+            n0 = (blk * (N - 128) // 15) & ~15
+            codes[h, n0:n0 + 128] = best
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, 3000, 700)
+    _check_fused(codes, k_low, fused, split, q_low, lut, 3000, 700)
+    N, S, C = 1048576, 2, 256
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=23, few=True)
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, 2048, 512)
+    _check_fused(codes, k_low, fused, split, q_low, lut, 2048, 512)
+    N, S, C = 300000, 4, 64
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=3)
+    rng = np.random.default_rng(5)
+    mask = np.where(rng.random(N) < 0.5, np.finfo(np.float32).min, 0.0).astype(np.float32)[None, None, None, :]
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, 1024, 256,
+                                              mask=torch.from_numpy(mask).to(device))
+    _check_fused(codes, k_low, fused, split, q_low, lut, 1024, 256, allowed=mask[0, 0, 0] > -1e4)
+
+
+def test_summon_select_per_item_path(device):
+    # q = 2 takes the one-workgroup-per-item summon, then the budget kernel
+    from sva_amd import kernels
+
+    N, S, C, L, B = 40000, 4, 64, 1024, 300
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=11)
+    q2 = np.concatenate([q, q[:, :, ::-1].copy()], axis=1)
+    codes_t = torch.from_numpy(codes).to(device)
+    q_low, lut, rng = kernels.query_lut(torch.from_numpy(q2).to(device), torch.from_numpy(q_proj).to(device),
+                                        torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device))
+    mask = torch.zeros(1, 1, 2, N, device=device)
+    fused = kernels.summon_select(lut, rng, q_low, codes_t, k_low, N, L, B, mask=mask)
+    sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes_t, k_low, N, L, mask=mask)
+    fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, B)
+    for a, b in zip(fused, (sl_idx, sl_rank, sl_count, fin_idx, fin_count)):
+        assert torch.equal(a, b)
