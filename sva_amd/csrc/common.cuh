@@ -116,37 +116,77 @@ SVA_DEV uint32_t wave_sum_u32(uint32_t v) {
   return v;
 }
 
-// Inclusive scan within a wave (Hillis-Steele over 64 lanes).
+// DPP row shifts (a DPP row is 16 lanes): lane j receives lane j - N of its
+// row.  Lanes with no source lane receive 0 (row_shr0) or keep their own
+// value (row_shr_keep: the identity for OR / AND folds).
+template <int N>
+SVA_DEV uint32_t row_shr0(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x110 + N, 0xF, 0xF, true);
+}
+template <int N>
+SVA_DEV uint32_t row_shr_keep(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x110 + N, 0xF, 0xF, false);
+}
+
+// Inclusive scan within a wave: Hillis-Steele inside each DPP row, then the
+// row totals (read from lanes 15, 31, 47) added to the later rows.  All 64
+// lanes must be active.
 SVA_DEV uint32_t wave_incl_scan(uint32_t v) {
-  const int lane = lane_id();
-  for (int off = 1; off < WAVE; off <<= 1) {
-    uint32_t t = __shfl_up(v, off, WAVE);
-    if (lane >= off) v += t;
+  v += row_shr0<1>(v);
+  v += row_shr0<2>(v);
+  v += row_shr0<4>(v);
+  v += row_shr0<8>(v);
+  const uint32_t t0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t t1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t t2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  const int row = lane_id() >> 4;
+  return v + (row == 0 ? 0u : (row == 1 ? t0 : (row == 2 ? t0 + t1 : t0 + t1 + t2)));
+}
+
+// OR and AND of a 64-bit value over the wave (all 64 lanes active), wave-uniform.
+SVA_DEV void wave_or_and_u64(uint64_t& vor, uint64_t& vand) {
+  uint32_t o[2] = {(uint32_t)vor, (uint32_t)(vor >> 32)};
+  uint32_t n[2] = {(uint32_t)vand, (uint32_t)(vand >> 32)};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    o[h] |= row_shr_keep<1>(o[h]);
+    n[h] &= row_shr_keep<1>(n[h]);
+    o[h] |= row_shr_keep<2>(o[h]);
+    n[h] &= row_shr_keep<2>(n[h]);
+    o[h] |= row_shr_keep<4>(o[h]);
+    n[h] &= row_shr_keep<4>(n[h]);
+    o[h] |= row_shr_keep<8>(o[h]);
+    n[h] &= row_shr_keep<8>(n[h]);
+    o[h] = (uint32_t)__builtin_amdgcn_readlane((int)o[h], 15) | (uint32_t)__builtin_amdgcn_readlane((int)o[h], 31) |
+           (uint32_t)__builtin_amdgcn_readlane((int)o[h], 47) | (uint32_t)__builtin_amdgcn_readlane((int)o[h], 63);
+    n[h] = (uint32_t)__builtin_amdgcn_readlane((int)n[h], 15) & (uint32_t)__builtin_amdgcn_readlane((int)n[h], 31) &
+           (uint32_t)__builtin_amdgcn_readlane((int)n[h], 47) & (uint32_t)__builtin_amdgcn_readlane((int)n[h], 63);
   }
-  return v;
+  vor = ((uint64_t)o[1] << 32) | o[0];
+  vand = ((uint64_t)n[1] << 32) | n[0];
 }
 
 // Exclusive block scan of one value per thread.  `scratch` holds >= BLOCK/64 + 1
 // uint32 in LDS.  Returns the exclusive prefix; *total gets the block sum.
+// Every wave reads all wave totals itself (no second-level scan).
 template <int BLOCK>
 SVA_DEV uint32_t block_excl_scan(uint32_t v, uint32_t* scratch, uint32_t* total) {
   constexpr int NW = BLOCK / WAVE;
   const int lane = lane_id();
   const int wid = threadIdx.x / WAVE;
-  uint32_t incl = wave_incl_scan(v);
+  const uint32_t incl = wave_incl_scan(v);
   if (lane == WAVE - 1) scratch[wid] = incl;
   __syncthreads();
-  if (wid == 0) {
-    uint32_t w = lane < NW ? scratch[lane] : 0u;
-    uint32_t wi = wave_incl_scan(w);
-    if (lane < NW) scratch[lane] = wi - w;
-    if (lane == NW - 1) scratch[NW] = wi;
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    const uint32_t t = scratch[q];
+    before += q < wid ? t : 0u;
+    all += t;
   }
+  if (total) *total = all;
   __syncthreads();
-  uint32_t res = scratch[wid] + incl - v;
-  if (total) *total = scratch[NW];
-  __syncthreads();
-  return res;
+  return before + incl - v;
 }
 
 // ---------------------------------------------------------------------------
@@ -252,10 +292,7 @@ template <int BLOCK, int NPT>
 SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s) {
   static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
   const int lane = lane_id();
-  for (int off = 1; off < WAVE; off <<= 1) {
-    vor |= __shfl_xor(vor, off, WAVE);
-    vand &= __shfl_xor(vand, off, WAVE);
-  }
+  wave_or_and_u64(vor, vand);
   if (threadIdx.x == 0) {
     s.shared64[0] = 0ull;
     s.shared64[1] = ~0ull;

@@ -36,6 +36,9 @@ constexpr int WAVE_KEYS = WAVE * KEYS_PT;  // keys (and candidate capacity) per 
 constexpr int SB = 1024;         // threads of the select kernel
 constexpr int SNW = SB / WAVE;
 constexpr int LDS_CAND = 16384;  // candidates the select kernel stages in LDS
+// The wide path has R = 64: dividing by sqrt(R) = 8 equals multiplying by
+// 0.125 exactly (both are the correctly rounded value of x / 8).
+constexpr float kInvSqrtR = 0.125f;
 constexpr int KL_CAP = 256;      // candidate keys per scan wave kept in LDS for the rank scores
 constexpr int64_t kWideMinKeys = 32768;
 constexpr int64_t kMaxWideItems = 64;
@@ -62,14 +65,14 @@ SVA_DEV int round_key(int cs, int r) {
   return cs + (int)(threadIdx.x / WAVE) * WAVE_KEYS + (r * WAVE + lane_id()) * KPT;
 }
 
-// Loads a chunk's codes: every full 16-byte group with one unconditional
-// vector load (all issued before any is used); a partial last chunk falls
-// back to guarded byte loads.
-template <int S>
+// Loads a chunk's codes: a full chunk (FULL) with one unconditional vector
+// load per 16-byte group, straight-line so that each round waits only for
+// its own load; a partial last chunk falls back to guarded byte loads.
+template <int S, bool FULL>
 SVA_DEV void load_chunk(const uint8_t* __restrict__ codes, int cs, int ce, u32x4 (&raw)[KEYS_PT * S / 16]) {
   constexpr int KPT = 16 / S;
   constexpr int RND = KEYS_PT / KPT;
-  if (ce - cs == CHUNK) {
+  if (FULL) {
 #pragma unroll
     for (int r = 0; r < RND; ++r) {
       const int base = round_key<S>(cs, r);
@@ -91,58 +94,91 @@ SVA_DEV void load_chunk(const uint8_t* __restrict__ codes, int cs, int ce, u32x4
   }
 }
 
-// Per-query tables for the scan.  BP: entry c of subspace s lives in lane c
-// of reg[s] and is fetched with ds_bpermute (conflict-free; needs C <= 64 and
-// all 64 lanes active).  Otherwise an LDS table of 256 entries per subspace
-// (entries past C repeat entry C-1, so any uint8 code stays in bounds).
-template <int S, bool BP>
+// Per-query tables for the scan, in LDS.  SMALLC (C <= 64): a pair table of
+// subspaces 0 and 1, entry c0 + 64 c1 = T0[c0] + T1[c1], and 64-entry tables
+// of the other subspaces; the pair sum equals the reference's (0 + T0) + T1
+// up to the sign of a zero, which f2key folds.  Otherwise 256-entry tables.
+// Entries past C repeat entry C - 1, so every code stays in bounds.
+template <int S, bool SMALLC>
 struct ScanTables {
-  float reg[BP ? S : 1];
+  static constexpr int PAIR = (SMALLC && S >= 2) ? 4096 : 0;
+  static constexpr int SINGLE = SMALLC ? (S >= 2 ? S - 2 : 1) * 64 : S * 256;  // entries of the single tables
+  static constexpr int LDS_FLOATS = PAIR + SINGLE;
+  static constexpr int NP = PAIR / WB;                 // pair entries per thread
+  static constexpr int NS = (SINGLE + WB - 1) / WB;    // single entries per thread
+  float t0, t1[NP ? NP : 1], ts[NS];
   const float* tab;
-  SVA_DEV void init(const SummonParams& p, int item, float* lds_tab) {
+  // Table values into registers: every load issued, none waited for, so
+  // the caller can issue its code loads behind them.
+  SVA_DEV void load(const SummonParams& p, int item) {
     const float* src = p.lut + (int64_t)item * S * p.C;
-    if (BP) {
-      const int c = min(lane_id(), p.C - 1);
+    const int t = threadIdx.x;
+    const int cm = p.C - 1;
+    if (NP) {
+      t0 = src[min(t & 63, cm)];  // (t + k * WB) & 63 == t & 63
 #pragma unroll
-      for (int s = 0; s < (BP ? S : 1); ++s) reg[s] = src[s * p.C + c];
-    } else {
-      for (int e = threadIdx.x; e < S * 256; e += blockDim.x) lds_tab[e] = src[(e >> 8) * p.C + min(e & 255, p.C - 1)];
-      tab = lds_tab;
+      for (int k = 0; k < NP; ++k) t1[k] = src[p.C + min((t + k * WB) >> 6, cm)];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+      const int e = t + k * WB;
+      ts[k] = 0.0f;
+      if (e < SINGLE) {
+        if (SMALLC) ts[k] = src[((S >= 2 ? 2 : 0) + (e >> 6)) * p.C + min(e & 63, cm)];
+        else ts[k] = src[(e >> 8) * p.C + min(e & 255, cm)];
+      }
     }
   }
-  SVA_DEV float get(int s, uint32_t c) const {
-    if (BP) return __int_as_float(__builtin_amdgcn_ds_bpermute((int)(c << 2), __float_as_int(reg[BP ? s : 0])));
-    return tab[s * 256 + c];
+  // Writes the tables to LDS (the caller synchronizes before use).
+  SVA_DEV void store(float* lds_tab) {
+#pragma clang fp contract(off)
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) lds_tab[t + k * WB] = t0 + t1[k];
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      if (t + k * WB < SINGLE) lds_tab[PAIR + t + k * WB] = ts[k];
+    tab = lds_tab;
+  }
+  SVA_DEV float at_byte(uint32_t byte_offset) const {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + byte_offset);
   }
 };
 
 // Scores the keys of one 16-byte round of the thread, branch-free so that
 // the round's table lookups are in flight together: acc[k] = ((T0 + T1) +
 // T2) + ... (the scan sum before the 1/8 scale; the reference's leading
-// 0 + T0 only changes the sign of a zero).  bpermute lookups need all 64
-// lanes, which this guarantees.  ds_bpermute reads only bits [7:2] of its
-// address, so byte j of a word becomes a lane address with one shift (codes
-// are below C <= 64 on that path).
-template <int S, bool BP>
-SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, BP>& T, float (&acc)[16 / S]) {
+// 0 + T0 only changes the sign of a zero).  On the SMALLC path a code byte
+// becomes a table byte offset with a shift and a mask (codes below 64).
+template <int S, bool SMALLC>
+SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, SMALLC>& T, float (&acc)[16 / S]) {
 #pragma clang fp contract(off)
   constexpr int KPT = 16 / S;
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
     float a = 0.0f;
+    if (SMALLC) {
+      const int j0 = k * S;
+      if (S >= 2) {
+        const uint32_t x = raw[j0 >> 2] >> (8 * (j0 & 3));
+        a = T.at_byte(((x << 2) & 0xFCu) | (x & 0x3F00u));  // 4 (c0 + 64 c1)
+      }
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const int j = k * S + s;  // byte of the round
-      float v;
-      if (BP) {
+      for (int s = (S >= 2 ? 2 : 0); s < S; ++s) {
+        const int j = j0 + s;
         const uint32_t word = raw[j >> 2];
         const int sh = 8 * (j & 3);
-        const uint32_t addr = sh == 0 ? word << 2 : word >> (sh - 2);
-        v = __int_as_float(__builtin_amdgcn_ds_bpermute((int)addr, __float_as_int(T.reg[BP ? s : 0])));
-      } else {
-        v = T.get(s, byte_of(raw, j));
+        const uint32_t off = ((sh == 0 ? word << 2 : word >> (sh - 2)) & 0xFCu) +
+                             (uint32_t)(4 * (ScanTables<S, SMALLC>::PAIR + (S >= 2 ? s - 2 : 0) * 64));
+        const float v = T.at_byte(off);
+        a = (S >= 2 || s > 0) ? a + v : v;
       }
-      a = s == 0 ? v : a + v;
+    } else {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const float v = T.tab[s * 256 + byte_of(raw, k * S + s)];  // SINGLE = S * 256 here
+        a = s == 0 ? v : a + v;
+      }
     }
     acc[k] = a;
   }
@@ -204,7 +240,7 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
     if (c[k]) {
-      out[o] = composite(f2key(acc[k] / p.sqrt_r), (uint32_t)(n0 + k));
+      out[o] = composite(f2key(acc[k] * kInvSqrtR), (uint32_t)(n0 + k));
       if (o < (uint32_t)KL_CAP) keys[o] = (uint32_t)(n0 + k);
       ++o;
     }
@@ -216,15 +252,15 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 // every key is tested for being allowed; otherwise every key is, and a round
 // (one 16-byte word of codes) is examined key by key only when its largest
 // sum reaches the floor.
-template <int S, bool BP, bool CHECK, bool MASKED>
-SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, BP>& T,
+template <int S, bool SMALLC, bool CHECK, bool MASKED>
+SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, SMALLC>& T,
                          float t_lo, int cs, int ce, uint64_t* out, uint32_t* keys, uint32_t& wc,
                          uint32_t& n_allowed) {
   constexpr int KPT = 16 / S;
 #pragma unroll
   for (int r = 0; r < KEYS_PT / KPT; ++r) {
     float acc[KPT];
-    score_round<S, BP>(raw[r], T, acc);
+    score_round<S, SMALLC>(raw[r], T, acc);
     if (CHECK) {
       bool c[KPT];
       bool any = false;
@@ -304,44 +340,55 @@ SVA_DEV void rank_candidates(const SummonParams& p, const WideArgs& a, int item,
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const float dot = rank_dot64_row16(rv[u], qq);
-      if (c0 + 4 * u + row < nc && j == 0) rank[key[u]] = dot / p.sqrt_r;
+      if (c0 + 4 * u + row < nc && j == 0) rank[key[u]] = dot * kInvSqrtR;
     }
   }
 }
 
-template <int S, bool BP, bool MASKED>
-__global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
+// One scan workgroup's chunk.  CHECK: a partial or masked chunk (every key
+// tested for being allowed, guarded loads).
+template <int S, bool SMALLC, bool CHECK, bool MASKED>
+SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint32_t (*klist)[KL_CAP]) {
 #pragma clang fp contract(off)
-  __shared__ float tab_lds[BP ? 1 : S * 256];
-  __shared__ uint32_t klist[NW][KL_CAP];
   const SummonParams& p = a.p;
-  const int item = blockIdx.x / a.W;
-  const int w = blockIdx.x % a.W;
   const int h = item % p.H;
   const int cs = w * CHUNK;
   const int ce = (int)min((int64_t)cs + CHUNK, p.N);
   const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+  // table loads first, then the codes: loads complete in order, so the
+  // tables are stored while the codes stream and each round of codes is
+  // scored as soon as its own load lands
+  ScanTables<S, SMALLC> T;
+  T.load(p, item);
   u32x4 raw[KEYS_PT * S / 16];
-  load_chunk<S>(codes, cs, ce, raw);
-  ScanTables<S, BP> T;
-  T.init(p, item, tab_lds);
+  load_chunk<S, !CHECK>(codes, cs, ce, raw);
+  T.store(tab_lds);
   const float t_lo = item_floor(p, item);
-  if (!BP) __syncthreads();
+  __syncthreads();  // tables in LDS
   const int wid = threadIdx.x / WAVE;
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
-  if (!MASKED && ce - cs == CHUNK) {
-    scan_rounds<S, BP, false, false>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
-  } else {
-    scan_rounds<S, BP, true, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
-  }
+  scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
   rank_candidates(p, a, item, klist[wid], out, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane_id() == 0) {
     a.ncand[sub] = wc;
     a.nallow[sub] = wa;
+  }
+}
+
+template <int S, bool SMALLC, bool MASKED>
+__global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
+  __shared__ __align__(16) float tab_lds[ScanTables<S, SMALLC>::LDS_FLOATS];
+  __shared__ uint32_t klist[NW][KL_CAP];
+  const int item = blockIdx.x / a.W;
+  const int w = blockIdx.x % a.W;
+  if (!MASKED && (int64_t)(w + 1) * CHUNK <= a.p.N) {
+    scan_chunk<S, SMALLC, false, false>(a, item, w, tab_lds, klist);
+  } else {
+    scan_chunk<S, SMALLC, true, MASKED>(a, item, w, tab_lds, klist);
   }
 }
 
@@ -355,13 +402,21 @@ constexpr size_t kFinSl = kFinHist + sizeof(uint32_t) * TOP_BINS;               
 constexpr size_t kFinRk = kFinSl + sizeof(uint32_t) * FIN_MAX_L;                // uint64[FIN_MAX_L]
 constexpr size_t kFinSmall = kFinRk + sizeof(uint64_t) * FIN_MAX_L;             // uint64[TOP_SMALL]
 static_assert(kFinSmall + sizeof(uint64_t) * TOP_SMALL <= kFinStage, "finish LDS overlay");
-constexpr size_t kFinMisc = sizeof(uint32_t) * (SNW * SNW + SNW + 1 + 7) + sizeof(uint64_t) * 2;
-constexpr size_t kFinLds = kFinStage + kFinMisc;
+// small arrays after the staging area (offsets keep every pointer in LDS)
+constexpr size_t kFinWcnt = kFinStage;                                          // uint32[SNW * SNW]
+constexpr size_t kFinScratch = kFinWcnt + sizeof(uint32_t) * SNW * SNW;         // uint32[SNW + 1]
+constexpr size_t kFinShared = kFinScratch + sizeof(uint32_t) * (SNW + 2);       // uint32[4], 8-byte aligned
+constexpr size_t kFinShared64 = kFinShared + sizeof(uint32_t) * 4;              // uint64[2]
+constexpr size_t kFinLcnt = kFinShared64 + sizeof(uint64_t) * 2;                // uint32[SB]
+constexpr size_t kFinLoff = kFinLcnt + sizeof(uint32_t) * SB;                   // uint32[SB]
+constexpr size_t kFinLds = kFinLoff + sizeof(uint32_t) * SB;
+static_assert(kFinShared64 % 8 == 0, "8-byte LDS words");
 
 // Order-preserving compaction of register-held elements: element i of
 // thread t stands at position t + i * BLOCK of the source order; the
-// elements >= X (nonzero) get their rank in that order, at most cap of
-// them.  wcnt: NPT * BLOCK / 64 uint32 in LDS.  Every thread must call it.
+// elements >= X (nonzero) get their rank o in that order, at most cap of
+// them, passed as emit(o, element, i).  wcnt: NPT * BLOCK / 64 uint32 in LDS.
+// Every thread must call it.
 template <int BLOCK, int NPT, typename Emit>
 SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint32_t* wcnt, uint32_t* scratch,
                              Emit emit) {
@@ -387,9 +442,20 @@ SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint
     if (e[i] != 0ull && e[i] >= X) {
       const uint32_t o = wcnt[i * NWV + wid] +
                          __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[i], 0u));
-      if (o < (uint32_t)cap) emit(o, e[i]);
+      if (o < (uint32_t)cap) emit(o, e[i], i);
     }
   }
+}
+
+// Budget of an item: the beff largest rank composites among the nonzero
+// e2 (leff of them), compacted in slot order (ascending key order) to fin.
+template <int NPT>
+SVA_DEV void finish_budget(const SummonParams& p, int item, int leff, int beff, const uint64_t (&e2)[NPT], uint64_t vor,
+                           uint64_t vand, const TopLds& tl, uint32_t* wcnt, uint32_t* scratch) {
+  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPT>(e2, beff, vor, vand, tl);
+  int32_t* fin = p.fin_idx + (int64_t)item * p.B;
+  compact_ordered<SB, NPT>(e2, X2, beff, wcnt, scratch,
+                           [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
 }
 
 // Finish of an item: shortlist select, rank rescore and (B > 0) budget
@@ -415,10 +481,10 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   uint32_t* sl = (uint32_t*)(lds + kFinSl);
   uint64_t* rk = (uint64_t*)(lds + kFinRk);
   uint64_t* small = (uint64_t*)(lds + kFinSmall);
-  uint32_t* wcnt = (uint32_t*)(lds + kFinStage);                   // [SNW * SNW] compaction counts
-  uint32_t* scratch = wcnt + SNW * SNW;                            // [SNW + 1]
-  uint32_t* shared = scratch + SNW + 1;                            // [4]
-  uint64_t* shared64 = (uint64_t*)(((uintptr_t)(shared + 4) + 7) & ~(uintptr_t)7);  // [2]
+  uint32_t* wcnt = (uint32_t*)(lds + kFinWcnt);                    // compaction counts
+  uint32_t* scratch = (uint32_t*)(lds + kFinScratch);
+  uint32_t* shared = (uint32_t*)(lds + kFinShared);
+  uint64_t* shared64 = (uint64_t*)(lds + kFinShared64);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
   const int item = blockIdx.x;
@@ -435,7 +501,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     al += nallow[s];
   }
   uint32_t M, A;
-  block_excl_scan<SB>(m, scratch, &M);
+  const uint32_t my_base = block_excl_scan<SB>(m, scratch, &M);  // list offset when nsub <= SB
   block_excl_scan<SB>(al, scratch, &A);
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
@@ -445,22 +511,54 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     shared[3] = 0u;
   }
   if (leff == 0) return;
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  const float* rank_of = a.rank + (int64_t)item * p.N;
   if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND) {
-    // stage the lists in order, one list per thread
-    uint32_t carry = 0;
-    for (int g = 0; g < nsub; g += SB) {
-      const int s = g + (int)threadIdx.x;
-      const uint32_t c = s < nsub ? ncand[s] : 0u;
-      uint32_t tot;
-      const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
-      if (s < nsub) {
-        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
-#pragma unroll 8
-        for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
-      }
-      carry += tot;
+    // stage the lists in list order (ascending key order)
+    if (nsub <= SB) {
+      // 16 lanes per list, two loads each (entries l and l + 16), the
+      // lists of all rounds in flight together
+      uint32_t* lcnt = (uint32_t*)(lds + kFinLcnt);
+      uint32_t* loff = (uint32_t*)(lds + kFinLoff);
+      lcnt[threadIdx.x] = m;
+      loff[threadIdx.x] = my_base;
       __syncthreads();
+      constexpr int NQ = SB / 16;            // list groups of 16 lanes
+      constexpr int KQ = SB / NQ;            // lists per group at most
+      const int q = threadIdx.x >> 4, l = threadIdx.x & 15;
+      uint64_t v0[KQ], v1[KQ];
+#pragma unroll
+      for (int k = 0; k < KQ; ++k) {
+        const int sidx = k * NQ + q;
+        const uint32_t c = sidx < nsub ? lcnt[sidx] : 0u;
+        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
+        v0[k] = (uint32_t)l < c ? src[l] : 0ull;
+        v1[k] = (uint32_t)(l + 16) < c ? src[l + 16] : 0ull;
+      }
+#pragma unroll
+      for (int k = 0; k < KQ; ++k) {
+        const int sidx = k * NQ + q;
+        const uint32_t c = sidx < nsub ? lcnt[sidx] : 0u;
+        const uint32_t base = sidx < nsub ? loff[sidx] : 0u;
+        if ((uint32_t)l < c) cl[base + l] = v0[k];
+        if ((uint32_t)(l + 16) < c) cl[base + 16 + l] = v1[k];
+        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
+        for (uint32_t j = 32 + l; j < c; j += 16) cl[base + j] = src[j];  // long lists (rare)
+      }
+    } else {
+      uint32_t carry = 0;
+      for (int g = 0; g < nsub; g += SB) {
+        const int sidx = g + (int)threadIdx.x;
+        const uint32_t c = sidx < nsub ? ncand[sidx] : 0u;
+        uint32_t tot;
+        const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
+        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
+        for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
+        carry += tot;
+      }
     }
+    __syncthreads();
     // 2. candidates into registers, shortlist select
     constexpr int NPT = LDS_CAND / SB;
     uint64_t e[NPT];
@@ -474,8 +572,29 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     }
     __syncthreads();  // staging area free
     const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, vor, vand, tl);
-    // shortlist in staging order (ascending key index)
-    compact_ordered<SB, NPT>(e, X, leff, wcnt, scratch, [&](uint32_t o, uint64_t x) { sl[o] = composite_index(x); });
+    // 3. ranks of the selected (computed by the scan), fetched while the
+    // shortlist is compacted in staging order (ascending key index)
+    float rnk[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) rnk[i] = (e[i] != 0ull && e[i] >= X) ? rank_of[composite_index(e[i])] : 0.0f;
+    compact_ordered<SB, NPT>(e, X, leff, wcnt, scratch, [&](uint32_t o, uint64_t x, int i) {
+      out_idx[o] = (int32_t)composite_index(x);
+      out_rank[o] = rnk[i];
+    });
+    if (p.B <= 0) return;
+    // 4. budget over the shortlist's rank composites, in the same slots
+    uint64_t e2[NPT];
+    vor = 0ull;
+    vand = ~0ull;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const bool in = e[i] != 0ull && e[i] >= X;
+      e2[i] = in ? composite(f2key(rnk[i]), composite_index(e[i])) : 0ull;
+      vor |= e2[i];
+      vand &= in ? e2[i] : ~0ull;
+    }
+    finish_budget<NPT>(p, item, leff, beff, e2, vor, vand, tl, wcnt, scratch);
+    return;
   } else if (M >= (uint32_t)leff) {
     // many candidates: select straight from the per-wave lists
     uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
@@ -532,8 +651,6 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   __syncthreads();
   // 3. shortlist out with its rank scores: computed by the scan for every
   // candidate; the all-keys path scores its shortlist here
-  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  float* out_rank = p.sl_rank + (int64_t)item * p.L;
   float* rkf = (float*)rk;  // [leff] ranks of the all-keys path
   const bool ranks_here = M < (uint32_t)leff;
   if (ranks_here) {
@@ -543,12 +660,11 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     for (int r = threadIdx.x >> 4; r < leff; r += SB / 16) {
       const uint32_t key = sl[r];
       const float dot = rank_dot64_row16(reinterpret_cast<const float4*>(klow + (int64_t)key * p.R)[j], qq);
-      if (j == 0) rkf[r] = dot / p.sqrt_r;
+      if (j == 0) rkf[r] = dot * kInvSqrtR;
     }
     __syncthreads();
   }
   constexpr int NPB = FIN_MAX_L / SB;
-  const float* rank_of = a.rank + (int64_t)item * p.N;
   uint64_t e2[NPB];
   uint64_t vor = 0ull, vand = ~0ull;
 #pragma unroll
@@ -557,7 +673,8 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     e2[i] = 0ull;
     if (r < leff) {
       const uint32_t key = sl[r];
-      const float rank = ranks_here ? rkf[r] : rank_of[key];
+      const float scanned = rank_of[key];  // in bounds; a stale value in the all-keys path
+      const float rank = ranks_here ? rkf[r] : scanned;
       out_idx[r] = (int32_t)key;
       out_rank[r] = rank;
       e2[i] = composite(f2key(rank), key);
@@ -566,17 +683,13 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     }
   }
   if (p.B <= 0) return;
-  // 4. budget select over the rank composites
-  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPB>(e2, beff, vor, vand, tl);
-  // the shortlist is in ascending key order, so is an ordered compaction
-  int32_t* fin = p.fin_idx + (int64_t)item * p.B;
-  compact_ordered<SB, NPB>(e2, X2, beff, wcnt, scratch,
-                           [&](uint32_t o, uint64_t x) { fin[o] = (int32_t)composite_index(x); });
+  // 4. budget over the shortlist's rank composites
+  finish_budget<NPB>(p, item, leff, beff, e2, vor, vand, tl, wcnt, scratch);
 }
 
-template <int S, bool BP, bool MASKED>
+template <int S, bool SMALLC, bool MASKED>
 int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_scan_kernel<S, BP, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
   SVA_CHECK_LAUNCH("wide_scan_kernel");
   static bool attr_set = false;
   if (!attr_set) {
@@ -592,8 +705,8 @@ int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
 
 template <int S>
 int launch_wide_s(const WideArgs& a, int64_t items, bool masked, hipStream_t stream) {
-  const bool bp = a.p.C <= 64;
-  if (bp) return masked ? launch_wide<S, true, true>(a, items, stream) : launch_wide<S, true, false>(a, items, stream);
+  const bool small_c = a.p.C <= 64;
+  if (small_c) return masked ? launch_wide<S, true, true>(a, items, stream) : launch_wide<S, true, false>(a, items, stream);
   return masked ? launch_wide<S, false, true>(a, items, stream) : launch_wide<S, false, false>(a, items, stream);
 }
 
