@@ -270,15 +270,16 @@ SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint
 
 // ---------------------------------------------------------------------------
 // Selection over elements held in registers: each thread of the block holds
-// NPT nonzero composites (0 = empty slot).  Radix passes of up to TOP_BITS
+// NPT nonzero composites (0 = empty slot); slots from `slots` on are empty in
+// every thread and skipped.  Radix passes of up to TOP_BITS
 // bits from the highest bit where the elements differ, counted in one shared
 // LDS histogram; as soon as the bucket holding the k-th largest has at most
-// TOP_SMALL elements they are gathered and ranked directly.  Returns X such
+// TOP_SMALL elements they are gathered and sorted by one wave.  Returns X such
 // that the selected elements are exactly those >= X (with repeated values,
 // more than k elements may reach X and the caller caps its output at k).
 constexpr int TOP_BITS = 12;
 constexpr int TOP_BINS = 1 << TOP_BITS;
-constexpr int TOP_SMALL = 256;
+constexpr int TOP_SMALL = 64;  // one wave sorts the last bucket
 
 struct TopLds {
   uint32_t* hist;      // [TOP_BINS]
@@ -289,7 +290,8 @@ struct TopLds {
 };
 
 template <int BLOCK, int NPT>
-SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s) {
+SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s,
+                                 int slots = NPT) {
   static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
   const int lane = lane_id();
   wave_or_and_u64(vor, vand);
@@ -320,7 +322,7 @@ SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, 
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       const uint64_t x = e[i];
-      if (x != 0ull && (x & pmask) == prefix) atomicAdd(&s.hist[(uint32_t)(x >> shift) & dmask], 1u);
+      if (i < slots && x != 0ull && (x & pmask) == prefix) atomicAdd(&s.hist[(uint32_t)(x >> shift) & dmask], 1u);
     }
     __syncthreads();
     // thread t owns bins 4t .. 4t+3 counted from the top
@@ -354,30 +356,35 @@ SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, 
       // gather the bucket and rank its elements directly
 #pragma unroll
       for (int i = 0; i < NPT; ++i) {
-        const uint64_t x = e[i];
-        const bool match = x != 0ull && (x & pmask) == prefix;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(match);
-        if (m != 0ull) {
-          uint32_t base = 0;
-          if (lane == 0) base = atomicAdd(&s.shared[3], (uint32_t)__popcll(m));
-          base = __shfl(base, 0, WAVE);
-          if (match) {
-            const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            s.small[base + below] = x;
+        if (i < slots) {  // uniform
+          const uint64_t x = e[i];
+          const bool match = x != 0ull && (x & pmask) == prefix;
+          const uint64_t m = __builtin_amdgcn_ballot_w64(match);
+          if (m != 0ull) {
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&s.shared[3], (uint32_t)__popcll(m));
+            base = __shfl(base, 0, WAVE);
+            if (match) {
+              const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+              s.small[base + below] = x;
+            }
           }
         }
       }
       __syncthreads();
-      if (threadIdx.x < cb) {
-        const uint64_t v = s.small[threadIdx.x];
-        uint32_t gt = 0, ge = 0;
-        for (uint32_t j = 0; j < cb; ++j) {
-          const uint64_t y = s.small[j];
-          gt += y > v;
-          ge += y >= v;
+      if (threadIdx.x < WAVE) {
+        // bitonic sort of the bucket, descending, in the lanes of wave 0
+        uint64_t v = (uint32_t)lane < cb ? s.small[lane] : 0ull;
+        for (int kk = 2; kk <= WAVE; kk <<= 1) {
+          for (int j = kk >> 1; j > 0; j >>= 1) {
+            const uint64_t o = __shfl_xor(v, j, WAVE);
+            const bool up = (lane & kk) == 0;
+            const bool low = (lane & j) == 0;
+            v = (low == up) ? (v > o ? v : o) : (v < o ? v : o);
+          }
         }
-        if (gt < (uint32_t)need && ge >= (uint32_t)need) s.shared64[0] = v;
+        if (lane == need - 1) s.shared64[0] = v;
       }
       __syncthreads();
       const uint64_t X = s.shared64[0];

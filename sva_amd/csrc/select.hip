@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(SEL_BLOCK)
   }
   if (beff == 0) return;
   const TopLds tl{hist, small, scratch, shared, shared64};
-  const uint64_t X = beff == n ? 1ull : select_top_regs<SEL_BLOCK, NPT>(e, beff, vor, vand, tl);
+  const uint64_t X = beff == n ? 1ull : select_top_regs<SEL_BLOCK, NPT>(e, beff, vor, vand, tl, (n + SEL_BLOCK - 1) / SEL_BLOCK);
   if (threadIdx.x == 0) shared[3] = 0u;
   __syncthreads();
   append_selected<NPT>(e, X, sel, beff, &shared[3]);

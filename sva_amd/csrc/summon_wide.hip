@@ -35,7 +35,8 @@ constexpr int CHUNK = WB * KEYS_PT;
 constexpr int WAVE_KEYS = WAVE * KEYS_PT;  // keys (and candidate capacity) per wave
 constexpr int SB = 1024;         // threads of the select kernel
 constexpr int SNW = SB / WAVE;
-constexpr int LDS_CAND = 16384;  // candidates the select kernel stages in LDS
+constexpr int LDS_CAND = 16384;  // candidates the finish kernel stages in LDS
+constexpr int STAGE_LISTS = 4096;  // lists whose staging offsets the finish kernel keeps in LDS
 // The wide path has R = 64: dividing by sqrt(R) = 8 equals multiplying by
 // 0.125 exactly (both are the correctly rounded value of x / 8).
 constexpr float kInvSqrtR = 0.125f;
@@ -50,7 +51,7 @@ struct WideArgs {
   uint32_t* ncand;   // [items, W * NW] candidates of each scan wave
   uint32_t* nallow;  // [items, W * NW] allowed keys of each scan wave
   uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
-  float* rank;       // [items, N] rank score of every candidate, by key index
+  float* cand_rank;  // [items, W * NW, WAVE_KEYS] rank score of each listed candidate
   int W;             // scan workgroups per item
 };
 
@@ -316,15 +317,14 @@ SVA_DEV float rank_dot64_row16(const float4 r, const float4 qq) {
 
 // Rank scores of a scan wave's nc candidates (keys in the LDS list while
 // they fit, else from the wave's candidate list): one 16-lane DPP row per
-// candidate, 16 candidates in flight per wave; written by key index.
-SVA_DEV void rank_candidates(const SummonParams& p, const WideArgs& a, int item, const uint32_t* keys,
-                             const uint64_t* out, uint32_t nc) {
+// candidate, 16 candidates in flight per wave; written beside the list.
+SVA_DEV void rank_candidates(const SummonParams& p, int item, const uint32_t* keys, const uint64_t* out,
+                             float* rank, uint32_t nc) {
 #pragma clang fp contract(off)
   const int j = lane_id() & 15;
   const int row = lane_id() >> 4;
   const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
   const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
-  float* rank = a.rank + (int64_t)item * p.N;
   if (nc > (uint32_t)KL_CAP) __threadfence();  // keys past the LDS list are read back from `out`
   constexpr int RU = 4;
   for (uint32_t c0 = 0; c0 < nc; c0 += 4 * RU) {
@@ -340,7 +340,7 @@ SVA_DEV void rank_candidates(const SummonParams& p, const WideArgs& a, int item,
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const float dot = rank_dot64_row16(rv[u], qq);
-      if (c0 + 4 * u + row < nc && j == 0) rank[key[u]] = dot * kInvSqrtR;
+      if (c0 + 4 * u + row < nc && j == 0) rank[c0 + 4 * u + row] = dot * kInvSqrtR;
     }
   }
 }
@@ -371,7 +371,7 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
   scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
-  rank_candidates(p, a, item, klist[wid], out, wc);
+  rank_candidates(p, item, klist[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane_id() == 0) {
     a.ncand[sub] = wc;
@@ -392,9 +392,10 @@ __global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
   }
 }
 
-// LDS of the finish kernel.  The staging area holds the gathered candidates;
-// once they sit in registers it is reused for the selection histogram, the
-// shortlist, its rank composites and the budget gather.
+// LDS of the finish kernel.  The staging area holds gathered candidates (one
+// of the paths); once the candidates sit in registers it is reused for the
+// selection histogram, the shortlist, its rank composites and the last bucket
+// of a selection.
 constexpr int FIN_MAX_L = 8192;
 constexpr size_t kFinStage = sizeof(uint64_t) * LDS_CAND;                       // 128 KB
 constexpr size_t kFinHist = 0;                                                  // uint32[TOP_BINS]
@@ -408,25 +409,48 @@ constexpr size_t kFinScratch = kFinWcnt + sizeof(uint32_t) * SNW * SNW;         
 constexpr size_t kFinShared = kFinScratch + sizeof(uint32_t) * (SNW + 2);       // uint32[4], 8-byte aligned
 constexpr size_t kFinShared64 = kFinShared + sizeof(uint32_t) * 4;              // uint64[2]
 constexpr size_t kFinLcnt = kFinShared64 + sizeof(uint64_t) * 2;                // uint32[SB]
-constexpr size_t kFinLoff = kFinLcnt + sizeof(uint32_t) * SB;                   // uint32[SB]
-constexpr size_t kFinLds = kFinLoff + sizeof(uint32_t) * SB;
+constexpr size_t kFinLoff = kFinLcnt + sizeof(uint32_t) * SB;                   // uint32[STAGE_LISTS]
+constexpr size_t kFinLds = kFinLoff + sizeof(uint32_t) * STAGE_LISTS;
 static_assert(kFinShared64 % 8 == 0, "8-byte LDS words");
+static_assert(kFinLds <= (size_t)kMaxLds, "finish LDS");
+
+// Direct path of the finish: lists gathered straight into registers when
+// every list holds at most DCAP candidates and there are at most DL_LISTS
+// lists (16 lanes per list, entries l + 16 h of lists k * 64 + q).
+constexpr int DQ = SB / 16;          // list groups of 16 lanes
+constexpr int DK = 8;                // lists per group
+constexpr int DCAP = 48;             // entries per list (up to 3 per lane)
+constexpr int DL_LISTS = DQ * DK;    // 512 lists: caches up to 1M keys
+
+// Rank score of a 64-float k_low row in torch's sum order, computed here
+// for the all-keys path: rows r of sl, one 16-lane DPP row each.
+SVA_DEV void rank_rows(const SummonParams& p, int item, const uint32_t* sl, int n, float* out) {
+#pragma clang fp contract(off)
+  const int j = lane_id() & 15;
+  const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
+  const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
+  for (int r = threadIdx.x >> 4; r < n; r += SB / 16) {
+    const float dot = rank_dot64_row16(reinterpret_cast<const float4*>(klow + (int64_t)sl[r] * p.R)[j], qq);
+    if (j == 0) out[r] = dot * kInvSqrtR;
+  }
+}
 
 // Order-preserving compaction of register-held elements: element i of
 // thread t stands at position t + i * BLOCK of the source order; the
 // elements >= X (nonzero) get their rank o in that order, at most cap of
-// them, passed as emit(o, element, i).  wcnt: NPT * BLOCK / 64 uint32 in LDS.
-// Every thread must call it.
+// them, passed as emit(o, element, i).  Slots from `slots` on are empty.
+// wcnt: NPT * BLOCK / 64 uint32 in LDS.  Every thread must call it.
 template <int BLOCK, int NPT, typename Emit>
 SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint32_t* wcnt, uint32_t* scratch,
-                             Emit emit) {
+                             int slots, Emit emit) {
   constexpr int NWV = BLOCK / WAVE;
   const int wid = threadIdx.x / WAVE;
   const int lane = lane_id();
   uint64_t bal[NPT];
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
-    bal[i] = __builtin_amdgcn_ballot_w64(e[i] != 0ull && e[i] >= X);
+    bal[i] = 0ull;
+    if (i < slots) bal[i] = __builtin_amdgcn_ballot_w64(e[i] != 0ull && e[i] >= X);
     if (lane == 0) wcnt[i * NWV + wid] = (uint32_t)__popcll(bal[i]);
   }
   __syncthreads();
@@ -439,7 +463,7 @@ SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint
   }
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
-    if (e[i] != 0ull && e[i] >= X) {
+    if (i < slots && e[i] != 0ull && e[i] >= X) {
       const uint32_t o = wcnt[i * NWV + wid] +
                          __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[i], 0u));
       if (o < (uint32_t)cap) emit(o, e[i], i);
@@ -448,182 +472,287 @@ SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint
 }
 
 // Budget of an item: the beff largest rank composites among the nonzero
-// e2 (leff of them), compacted in slot order (ascending key order) to fin.
+// e2 (leff of them, dense), compacted in slot order (ascending key order) to fin.
 template <int NPT>
 SVA_DEV void finish_budget(const SummonParams& p, int item, int leff, int beff, const uint64_t (&e2)[NPT], uint64_t vor,
                            uint64_t vand, const TopLds& tl, uint32_t* wcnt, uint32_t* scratch) {
-  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPT>(e2, beff, vor, vand, tl);
+  const int slots = (leff + SB - 1) / SB;
+  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPT>(e2, beff, vor, vand, tl, slots);
   int32_t* fin = p.fin_idx + (int64_t)item * p.B;
-  compact_ordered<SB, NPT>(e2, X2, beff, wcnt, scratch,
+  compact_ordered<SB, NPT>(e2, X2, beff, wcnt, scratch, slots,
                            [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
 }
 
-// Finish of an item: shortlist select, rank rescore and (B > 0) budget
-// select, one workgroup per item.
-//   1. counts of the scan's per-wave lists; the lists are copied into LDS
-//      in list order, which is ascending key order;
-//   2. every thread takes 16 staged candidates into registers and the L
-//      largest are found by select_top_regs; the selected are compacted in
-//      staging order into the shortlist (LDS and sl_idx, ascending);
-//   3. rank scores k_low . q_low of the shortlist, one 16-lane DPP row per
-//      shortlist row, 16 rows in flight per lane (sl_rank, and composites in
-//      LDS);
-//   4. budget: the B largest rank composites, compacted in shortlist order,
-//      hence ascending.
-// When the sampled floor let more than LDS_CAND keys through, the shortlist
-// is selected straight from the lists in global memory; when it let fewer
-// than L through, from every key of the item.  Both give the same set.
+// Direct path of the finish (see wide_finish_kernel): DH entries per lane
+// and list, slot DH * k + h = list k * DQ + q, entry l + 16 h.
+template <int DH, typename Emit>
+SVA_DEV void finish_direct(const WideArgs& a, int item, int nsub, int leff, uint32_t M, const uint32_t* lcnt,
+                           uint32_t* loff, const TopLds& tl, uint32_t* scratch, Emit emit) {
+  const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
+  const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
+  const int t = threadIdx.x;
+  const int q = t >> 4, l = t & 15;
+  const int kq = (nsub + DQ - 1) / DQ;
+  constexpr int NS = DH * DK;
+  uint64_t e[NS];
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+#pragma unroll
+    for (int h = 0; h < DH; ++h) e[DH * k + h] = 0ull;
+    if (k < kq) {  // uniform; entries < DCAP are inside every list's capacity
+      const int64_t off = (int64_t)min(k * DQ + q, nsub - 1) * WAVE_KEYS;
+#pragma unroll
+      for (int h = 0; h < DH; ++h) e[DH * k + h] = cand[off + l + 16 * h];
+    }
+  }
+  uint64_t vor = 0ull, vand = ~0ull;
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    const int sidx = k * DQ + q;
+    const uint32_t c = (k < kq && sidx < nsub) ? lcnt[sidx] : 0u;
+#pragma unroll
+    for (int h = 0; h < DH; ++h) {
+      if ((uint32_t)(l + 16 * h) >= c) e[DH * k + h] = 0ull;
+      vor |= e[DH * k + h];
+      vand &= e[DH * k + h] != 0ull ? e[DH * k + h] : ~0ull;
+    }
+  }
+  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NS>(e, leff, vor, vand, tl, DH * kq);
+  // the selected load their ranks (written beside the lists by the scan)
+  float rnk[NS];
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    const int64_t off = (int64_t)min(k * DQ + q, nsub - 1) * WAVE_KEYS;
+#pragma unroll
+    for (int h = 0; h < DH; ++h) {
+      const uint64_t x = e[DH * k + h];
+      rnk[DH * k + h] = (k < kq && x != 0ull && x >= X) ? crank[off + l + 16 * h] : 0.0f;
+    }
+  }
+  // list-ordered compaction: per-list counts of the selected (ballot
+  // bits of the list's 16 lanes), their scan over the lists, then each
+  // entry at its list's base plus the selected before it in the list
+  uint32_t mk[NS];
+  const int qs = 16 * (q & 3);
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int h = 0; h < DH; ++h) {
+      mk[DH * k + h] = 0u;
+      if (k < kq) {
+        const uint64_t x = e[DH * k + h];
+        const uint64_t b = __builtin_amdgcn_ballot_w64(x != 0ull && x >= X);
+        mk[DH * k + h] = (uint32_t)(b >> qs) & 0xFFFFu;
+        cnt += (uint32_t)__popc(mk[DH * k + h]);
+      }
+    }
+    const int sidx = k * DQ + q;
+    if (k < kq && l == 0 && sidx < nsub) loff[sidx] = cnt;
+  }
+  __syncthreads();
+  {
+    const uint32_t c = t < nsub ? loff[t] : 0u;
+    uint32_t tot;
+    const uint32_t o = block_excl_scan<SB>(c, scratch, &tot);
+    if (t < nsub) loff[t] = o;
+    __syncthreads();
+  }
+  const uint32_t below = (1u << l) - 1u;
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    if (k < kq) {
+      const int sidx = k * DQ + q;
+      uint32_t o = sidx < nsub ? loff[sidx] : 0u;
+#pragma unroll
+      for (int h = 0; h < DH; ++h) {
+        const uint32_t mm = mk[DH * k + h];
+        if ((mm >> l) & 1u) emit(o + (uint32_t)__popc(mm & below), e[DH * k + h], rnk[DH * k + h]);
+        o += (uint32_t)__popc(mm);
+      }
+    }
+  }
+}
+
+// Finish of an item: shortlist select, its outputs with the ranks the scan
+// computed, and (B > 0) the budget select, one workgroup per item.  The
+// candidate lists are in ascending key order, and so is every output.
+//   direct  (every list <= DCAP entries, <= 512 lists): lists gathered into
+//           registers, 16 lanes per list; the selected load their ranks;
+//           list-ordered compaction by per-list ballots and a scan over the
+//           lists;
+//   staged  (M <= LDS_CAND, <= STAGE_LISTS lists): lists staged in LDS in
+//           list order, then into registers; the selected find their list
+//           (binary search over the staging offsets) for their ranks;
+//           slot-ordered compaction;
+//   lists   (more candidates): selection straight from the global lists;
+//   all keys (the sampled floor let fewer than L keys through): selection
+//           over every key of the item, ranks computed here.
+// The last two are slower and give the same result.  The shortlist's rank
+// composites go to LDS in shortlist order for the budget.
 __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
-  uint64_t* cl = (uint64_t*)lds;                                   // staging [LDS_CAND]
-  uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // after staging
+  uint64_t* cl = (uint64_t*)lds;                                   // staged candidates [LDS_CAND]
+  uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // overlays, once staging is done
   uint32_t* sl = (uint32_t*)(lds + kFinSl);
   uint64_t* rk = (uint64_t*)(lds + kFinRk);
   uint64_t* small = (uint64_t*)(lds + kFinSmall);
-  uint32_t* wcnt = (uint32_t*)(lds + kFinWcnt);                    // compaction counts
+  uint32_t* wcnt = (uint32_t*)(lds + kFinWcnt);
   uint32_t* scratch = (uint32_t*)(lds + kFinScratch);
   uint32_t* shared = (uint32_t*)(lds + kFinShared);
   uint64_t* shared64 = (uint64_t*)(lds + kFinShared64);
+  uint32_t* lcnt = (uint32_t*)(lds + kFinLcnt);
+  uint32_t* loff = (uint32_t*)(lds + kFinLoff);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
   const int item = blockIdx.x;
-  const int wid = threadIdx.x / WAVE;
+  const int t = threadIdx.x;
+  const int wid = t / WAVE;
   const int lane = lane_id();
   const int nsub = a.W * NW;
   const uint32_t* ncand = a.ncand + (int64_t)item * nsub;
   const uint32_t* nallow = a.nallow + (int64_t)item * nsub;
   const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
-  // 1. totals: candidates M and allowed keys A
+  const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  // 1. totals: candidates M, allowed keys A; list counts and offsets
+  if (t == 0) {
+    shared[2] = 0u;  // some list longer than DCAP
+    shared[1] = 0u;  // longest list (when nsub <= SB)
+  }
   uint32_t m = 0, al = 0;
-  for (int s = threadIdx.x; s < nsub; s += SB) {
-    m += ncand[s];
-    al += nallow[s];
+  for (int sidx = t; sidx < nsub; sidx += SB) {
+    m += ncand[sidx];
+    al += nallow[sidx];
   }
   uint32_t M, A;
   const uint32_t my_base = block_excl_scan<SB>(m, scratch, &M);  // list offset when nsub <= SB
+  if (m > (uint32_t)DCAP) atomicOr(&shared[2], 1u);
+  if (m > 32u) atomicMax(&shared[1], m);
+  if (nsub <= SB) {
+    lcnt[t] = m;
+    loff[t] = my_base;
+  }
   block_excl_scan<SB>(al, scratch, &A);
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
-  if (threadIdx.x == 0) {
+  if (t == 0) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
-    shared[3] = 0u;
   }
   if (leff == 0) return;
-  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  const float* rank_of = a.rank + (int64_t)item * p.N;
-  if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND) {
-    // stage the lists in list order (ascending key order)
+  const bool long_lists = shared[2] != 0u;
+  auto emit = [&](uint32_t o, uint64_t x, float rank) {
+    const uint32_t key = composite_index(x);
+    out_idx[o] = (int32_t)key;
+    out_rank[o] = rank;
+    rk[o] = composite(f2key(rank), key);
+  };
+  bool dense = true;  // rank composites in rk (else sl + ranks in LDS)
+  if (M >= (uint32_t)leff && nsub <= DL_LISTS && !long_lists) {
+    if (shared[1] > 32u) finish_direct<3>(a, item, nsub, leff, M, lcnt, loff, tl, scratch, emit);
+    else finish_direct<2>(a, item, nsub, leff, M, lcnt, loff, tl, scratch, emit);
+  } else if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND && nsub <= STAGE_LISTS) {
+    // staged: lists into LDS in list order
     if (nsub <= SB) {
-      // 16 lanes per list, two loads each (entries l and l + 16), the
-      // lists of all rounds in flight together
-      uint32_t* lcnt = (uint32_t*)(lds + kFinLcnt);
-      uint32_t* loff = (uint32_t*)(lds + kFinLoff);
-      lcnt[threadIdx.x] = m;
-      loff[threadIdx.x] = my_base;
-      __syncthreads();
-      constexpr int NQ = SB / 16;            // list groups of 16 lanes
-      constexpr int KQ = SB / NQ;            // lists per group at most
-      const int q = threadIdx.x >> 4, l = threadIdx.x & 15;
-      uint64_t v0[KQ], v1[KQ];
-#pragma unroll
+      __syncthreads();  // lcnt / loff
+      constexpr int KQ = SB / DQ;
+      const int kq = (nsub + DQ - 1) / DQ;
+      const int q = t >> 4, l = t & 15;
       for (int k = 0; k < KQ; ++k) {
-        const int sidx = k * NQ + q;
-        const uint32_t c = sidx < nsub ? lcnt[sidx] : 0u;
-        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
-        v0[k] = (uint32_t)l < c ? src[l] : 0ull;
-        v1[k] = (uint32_t)(l + 16) < c ? src[l + 16] : 0ull;
-      }
-#pragma unroll
-      for (int k = 0; k < KQ; ++k) {
-        const int sidx = k * NQ + q;
+        if (k >= kq) break;  // uniform
+        const int sidx = k * DQ + q;
         const uint32_t c = sidx < nsub ? lcnt[sidx] : 0u;
         const uint32_t base = sidx < nsub ? loff[sidx] : 0u;
-        if ((uint32_t)l < c) cl[base + l] = v0[k];
-        if ((uint32_t)(l + 16) < c) cl[base + 16 + l] = v1[k];
-        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
-        for (uint32_t j = 32 + l; j < c; j += 16) cl[base + j] = src[j];  // long lists (rare)
+        const int64_t off = (int64_t)sidx * WAVE_KEYS;
+        for (uint32_t j = l; j < c; j += 16) cl[base + j] = cand[off + j];
       }
     } else {
       uint32_t carry = 0;
       for (int g = 0; g < nsub; g += SB) {
-        const int sidx = g + (int)threadIdx.x;
+        const int sidx = g + t;
         const uint32_t c = sidx < nsub ? ncand[sidx] : 0u;
         uint32_t tot;
         const uint32_t base = carry + block_excl_scan<SB>(c, scratch, &tot);
-        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
-        for (uint32_t j = 0; j < c; ++j) cl[base + j] = src[j];
+        if (sidx < nsub) loff[sidx] = base;
+        const int64_t off = (int64_t)sidx * WAVE_KEYS;
+        for (uint32_t j = 0; j < c; ++j) cl[base + j] = cand[off + j];
         carry += tot;
       }
     }
     __syncthreads();
-    // 2. candidates into registers, shortlist select
     constexpr int NPT = LDS_CAND / SB;
+    const int slots = ((int)M + SB - 1) / SB;
     uint64_t e[NPT];
     uint64_t vor = 0ull, vand = ~0ull;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      const int j = (int)threadIdx.x + i * SB;
+      const int j = t + i * SB;
       e[i] = j < (int)M ? cl[j] : 0ull;
       vor |= j < (int)M ? e[i] : 0ull;
       vand &= j < (int)M ? e[i] : ~0ull;
     }
     __syncthreads();  // staging area free
-    const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, vor, vand, tl);
-    // 3. ranks of the selected (computed by the scan), fetched while the
-    // shortlist is compacted in staging order (ascending key index)
+    const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, vor, vand, tl, slots);
+    // ranks of the selected: staging position -> list (last offset <= it)
     float rnk[NPT];
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) rnk[i] = (e[i] != 0ull && e[i] >= X) ? rank_of[composite_index(e[i])] : 0.0f;
-    compact_ordered<SB, NPT>(e, X, leff, wcnt, scratch, [&](uint32_t o, uint64_t x, int i) {
-      out_idx[o] = (int32_t)composite_index(x);
-      out_rank[o] = rnk[i];
-    });
-    if (p.B <= 0) return;
-    // 4. budget over the shortlist's rank composites, in the same slots
-    uint64_t e2[NPT];
-    vor = 0ull;
-    vand = ~0ull;
-#pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      const bool in = e[i] != 0ull && e[i] >= X;
-      e2[i] = in ? composite(f2key(rnk[i]), composite_index(e[i])) : 0ull;
-      vor |= e2[i];
-      vand &= in ? e2[i] : ~0ull;
+      rnk[i] = 0.0f;
+      if (i < slots && e[i] != 0ull && e[i] >= X) {
+        const uint32_t j = (uint32_t)(t + i * SB);
+        int lo = 0, hi = nsub;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (loff[mid] <= j) lo = mid + 1;
+          else hi = mid;
+        }
+        const int sidx = lo - 1;
+        rnk[i] = crank[(int64_t)sidx * WAVE_KEYS + (j - loff[sidx])];
+      }
     }
-    finish_budget<NPT>(p, item, leff, beff, e2, vor, vand, tl, wcnt, scratch);
-    return;
+    compact_ordered<SB, NPT>(e, X, leff, wcnt, scratch, slots,
+                             [&](uint32_t o, uint64_t x, int i) { emit(o, x, rnk[i]); });
   } else if (M >= (uint32_t)leff) {
-    // many candidates: select straight from the per-wave lists
+    // lists: select straight from the per-wave lists in global memory
+    dense = false;
+    float* rkf = (float*)rk;
     uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
     auto visit = [&](auto&& f) {
-      for (int s = threadIdx.x; s < nsub; s += SB) {
-        const uint32_t c = ncand[s];
-        const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+      for (int sidx = t; sidx < nsub; sidx += SB) {
+        const uint32_t c = ncand[sidx];
+        const uint64_t* src = cand + (int64_t)sidx * WAVE_KEYS;
         for (uint32_t j = 0; j < c; ++j) f(src[j]);
       }
     };
     const uint64_t X = (uint32_t)leff == M ? 1ull : select_largest<SB>(visit, leff, whist, scratch, shared64, shared);
-    if (threadIdx.x == 0) shared[3] = 0u;
+    if (t == 0) shared[3] = 0u;
     __syncthreads();
     for (int g = 0; g < nsub; g += SB) {
-      const int s = g + (int)threadIdx.x;
-      const uint32_t c = s < nsub ? ncand[s] : 0u;
-      const uint64_t* src = cand + (int64_t)s * WAVE_KEYS;
+      const int sidx = g + t;
+      const uint32_t c = sidx < nsub ? ncand[sidx] : 0u;
+      const int64_t off = (int64_t)sidx * WAVE_KEYS;
       uint32_t cnt = 0;
-      for (uint32_t j = 0; j < c; ++j) cnt += src[j] >= X;
+      for (uint32_t j = 0; j < c; ++j) cnt += cand[off + j] >= X;
       uint32_t tot;
       uint32_t o = shared[3] + block_excl_scan<SB>(cnt, scratch, &tot);
-      for (uint32_t j = 0; j < c; ++j)
-        if (src[j] >= X && o < (uint32_t)leff) sl[o++] = composite_index(src[j]);
+      for (uint32_t j = 0; j < c; ++j) {
+        const uint64_t x = cand[off + j];
+        if (x >= X && o < (uint32_t)leff) {
+          sl[o] = composite_index(x);
+          rkf[o] = crank[off + j];
+          ++o;
+        }
+      }
       __syncthreads();
-      if (threadIdx.x == 0) shared[3] += tot;
+      if (t == 0) shared[3] += tot;
       __syncthreads();
     }
   } else {
-    // the sampled floor overshot: exact selection over every key of the item
+    // all keys: the sampled floor overshot
+    dense = false;
     uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
     const int h = item % p.H;
     const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
@@ -633,57 +762,47 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
       return composite(f2key(score_at(p, codes, item, n)), (uint32_t)n);
     };
     auto visit = [&](auto&& f) {
-      for (int n = threadIdx.x; n < N; n += SB) {
+      for (int n = t; n < N; n += SB) {
         const uint64_t x = key_at(n);
         if (x != 0ull) f(x);
       }
     };
     const uint64_t X = (uint32_t)leff == A ? 1ull : select_largest<SB>(visit, leff, whist, scratch, shared64, shared);
     const int per = (N + SB - 1) / SB;
-    const int n0 = min(N, (int)threadIdx.x * per), n1 = min(N, n0 + per);
+    const int n0 = min(N, t * per), n1 = min(N, n0 + per);
     uint32_t cnt = 0;
     for (int n = n0; n < n1; ++n) cnt += key_at(n) >= X;
     uint32_t tot;
     uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
     for (int n = n0; n < n1; ++n)
       if (key_at(n) >= X && o < (uint32_t)leff) sl[o++] = (uint32_t)n;
+    __syncthreads();
+    rank_rows(p, item, sl, leff, (float*)rk);
   }
   __syncthreads();
-  // 3. shortlist out with its rank scores: computed by the scan for every
-  // candidate; the all-keys path scores its shortlist here
-  float* rkf = (float*)rk;  // [leff] ranks of the all-keys path
-  const bool ranks_here = M < (uint32_t)leff;
-  if (ranks_here) {
-    const int j = lane & 15;
-    const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
-    const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
-    for (int r = threadIdx.x >> 4; r < leff; r += SB / 16) {
-      const uint32_t key = sl[r];
-      const float dot = rank_dot64_row16(reinterpret_cast<const float4*>(klow + (int64_t)key * p.R)[j], qq);
-      if (j == 0) rkf[r] = dot * kInvSqrtR;
-    }
-    __syncthreads();
-  }
+  // shortlist outputs of the list and all-keys paths; budget input
   constexpr int NPB = FIN_MAX_L / SB;
   uint64_t e2[NPB];
   uint64_t vor = 0ull, vand = ~0ull;
 #pragma unroll
   for (int i = 0; i < NPB; ++i) {
-    const int r = (int)threadIdx.x + i * SB;
+    const int r = t + i * SB;
     e2[i] = 0ull;
     if (r < leff) {
-      const uint32_t key = sl[r];
-      const float scanned = rank_of[key];  // in bounds; a stale value in the all-keys path
-      const float rank = ranks_here ? rkf[r] : scanned;
-      out_idx[r] = (int32_t)key;
-      out_rank[r] = rank;
-      e2[i] = composite(f2key(rank), key);
+      if (dense) {
+        e2[i] = rk[r];
+      } else {
+        const uint32_t key = sl[r];
+        const float rank = ((const float*)rk)[r];
+        out_idx[r] = (int32_t)key;
+        out_rank[r] = rank;
+        e2[i] = composite(f2key(rank), key);
+      }
       vor |= e2[i];
       vand &= e2[i];
     }
   }
   if (p.B <= 0) return;
-  // 4. budget over the shortlist's rank composites
   finish_budget<NPB>(p, item, leff, beff, e2, vor, vand, tl, wcnt, scratch);
 }
 
@@ -736,8 +855,7 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   const int64_t items = n_seq * H * Q;
   if (n_seq != 1 || Q != 1 || n_keys < kWideMinKeys || items > kMaxWideItems) return 256;
   const int64_t W = (n_keys + CHUNK - 1) / CHUNK;
-  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * sizeof(uint64_t) +
-         (((size_t)items * (size_t)n_keys * sizeof(float) + 255) & ~(size_t)255);
+  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
 }
 
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -752,7 +870,7 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   a.ncand = (uint32_t*)ws;
   a.nallow = a.ncand + items * a.W * NW;
   a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
-  a.rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
+  a.cand_rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
   // a bool mask allows every key (the reference's `mask > -1e4` rule)
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
   switch (p.S) {

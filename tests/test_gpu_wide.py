@@ -235,3 +235,21 @@ def test_summon_select_per_item_path(device):
     fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, B)
     for a, b in zip(fused, (sl_idx, sl_rank, sl_count, fin_idx, fin_count)):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case", ["many_lists", "more_lists_than_threads", "long_lists"])
+def test_summon_select_staged_paths(device, case):
+    # More than 512 scan lists (1.5M keys; 2.5M keys: more lists than the
+    # finish kernel has threads), or lists longer than 32 candidates (a run
+    # of keys with the best codes): the finish kernel stages the lists in LDS
+    # instead of gathering them into registers.
+    H, S, C = (1 if case == "more_lists_than_threads" else 3), 4, 64
+    N = {"many_lists": 1536000, "more_lists_than_threads": 2500000, "long_lists": 300000}[case]
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=29)
+    if case == "long_lists":
+        ql = oracle.query_low(q, q_proj, scale)[:, 0]
+        for h in range(H):
+            best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
+            codes[h, 50000:51000] = best
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, 2048, 512)
+    _check_fused(codes, k_low, fused, split, q_low, lut, 2048, 512)
