@@ -15,12 +15,15 @@ using namespace sva;
 
 namespace {
 
-constexpr int PREP_BLOCK = 256;
+constexpr int PREP_BLOCK = 1024;
 constexpr int SAMPLE_BLOCKS = 16;       // contiguous sample blocks spread over the cache
 constexpr int SAMPLE_KEYS = 128;        // keys per sample block
-constexpr int SAMPLE_BINS = 1024;
+constexpr int SAMPLE_BINS = 1024;       // one per thread
 constexpr int SAMPLE_TARGET = 4;        // sampled threshold aims at ~4x the shortlist above it
-constexpr int SAMPLE_MAX_S = 8;         // sampling stages the sampled uint8 codes in LDS
+constexpr int SAMPLE_MAX_S = 8;         // subspaces of the sampled scan
+constexpr int N_SAMPLE = SAMPLE_BLOCKS * SAMPLE_KEYS;
+constexpr int SPT = N_SAMPLE / PREP_BLOCK;  // samples per thread
+static_assert(SAMPLE_BINS == PREP_BLOCK && SPT * PREP_BLOCK == N_SAMPLE, "sampling layout");
 
 struct LutParams {
   const void* q;
@@ -40,43 +43,89 @@ struct LutParams {
   int64_t shortlist;
 };
 
+// One workgroup per query item.  The sampled codes and the head's weights
+// are staged in LDS in one round of loads; then q_low (one thread per
+// output, a sequential fma chain over d), the
+// table (one thread per entry, codebook rows padded for conflict-free reads),
+// per-subspace key bounds folded per wave, and the sampled threshold: a
+// histogram of the sampled sums and a scan from the top bin.
 __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
   const int item = blockIdx.x;
-  const int t = item % p.Q;
+  const int t = threadIdx.x;
+  const int tq = item % p.Q;
   const int h = (item / p.Q) % p.H;
   const int b = item / (p.Q * p.H);
   const int D = p.D, R = p.R, S = p.S, C = p.C;
   const int sub = R / S;
-  float* W = (float*)lds;              // [max(D*R, S*C)] learned map of head h, then its table
-  float* cb = W + max(D * R, S * C);   // [S][C][sub] codebooks of head h
-  float* qf = cb + S * C * sub;        // [D]
-  float* ql = qf + D;                  // [R]
-  uint32_t* kmin = (uint32_t*)(ql + R);  // [S]
-  uint32_t* kmax = kmin + S;             // [S]
-  uint32_t* shist = kmax + S;            // [SAMPLE_BINS]
-  uint32_t* misc = shist + SAMPLE_BINS;  // [4 + PREP_BLOCK/64 + 1]
-  // [SAMPLE_BLOCKS * SAMPLE_KEYS * S] sampled codes, 16-byte aligned
-  uint8_t* scodes = lds + ((((unsigned char*)(misc + 8) - lds) + 15) & ~(ptrdiff_t)15);
+  const int cbs = sub + 1;                       // padded codebook row: conflict-free column reads
+  float* W = (float*)lds;                        // [D * R] learned map of head h
+  float* cb = W + D * R;                         // [S * C][cbs] its codebooks
+  float* qf = cb + S * C * cbs;                  // [D]
+  float* ql = qf + D;                            // [R]
+  float* tab = ql + R;                           // [S * C]
+  uint32_t* kmin = (uint32_t*)(tab + S * C);     // [S]
+  uint32_t* kmax = kmin + S;                     // [S]
+  uint32_t* shist = kmax + S;                    // [SAMPLE_BINS]
+  uint32_t* misc = shist + SAMPLE_BINS;          // [4]
+  uint32_t* scratch = misc + 4;                  // [PREP_BLOCK / 64 + 1]
+  uint8_t* scodes = (uint8_t*)(scratch + PREP_BLOCK / 64 + 1);  // [N_SAMPLE * S] sampled codes
 
-  // stage the head's weights in LDS with wide coalesced loads
+  // 0. sampled codes (k-th largest of the samples, k ~ SAMPLE_TARGET * L *
+  // samples / N; sample blocks start at multiples of 16 keys)
+  const int64_t N = p.n_keys;
+  int k = 0;
+  bool sample = false;
+  if (p.codes != nullptr && N >= 4 * (int64_t)N_SAMPLE) {
+    const double want = (double)SAMPLE_TARGET * (double)p.shortlist * (double)N_SAMPLE / (double)N;
+    k = (int)want + 1;
+    sample = k < N_SAMPLE / 2;
+  }
+  if (sample) {
+    // staged in LDS with the weights: the loads complete by the first barrier
+    const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+    const int wpb = SAMPLE_KEYS * S / 4;  // 32-bit words per sample block (block starts are 16-byte multiples)
+    if (((uintptr_t)head & 3u) == 0) {
+      for (int w = t; w < SAMPLE_BLOCKS * wpb; w += PREP_BLOCK) {
+        const int blk = w / wpb;
+        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+        reinterpret_cast<uint32_t*>(scodes)[w] = reinterpret_cast<const uint32_t*>(head + n0 * S)[w - blk * wpb];
+      }
+    } else {
+      for (int e = t; e < N_SAMPLE * S; e += PREP_BLOCK) {
+        const int blk = e / (SAMPLE_KEYS * S);
+        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+        scodes[e] = head[n0 * S + e % (SAMPLE_KEYS * S)];
+      }
+    }
+  }
+  // the head's weights into LDS with wide coalesced loads (one round)
   {
     const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * D * R);
-    for (int i = threadIdx.x; i < D * R / 4; i += PREP_BLOCK) reinterpret_cast<float4*>(W)[i] = w4[i];
+    for (int i = t; i < D * R / 4; i += PREP_BLOCK) reinterpret_cast<float4*>(W)[i] = w4[i];
     const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + (int64_t)h * S * C * sub);
-    for (int i = threadIdx.x; i < S * C * sub / 4; i += PREP_BLOCK) reinterpret_cast<float4*>(cb)[i] = c4[i];
+    for (int i = t; i < S * C * sub / 4; i += PREP_BLOCK) {
+      const float4 v = c4[i];
+      float* row = cb + (4 * i / sub) * cbs + (4 * i) % sub;  // sub % 4 == 0: a float4 stays in its row
+      row[0] = v.x;
+      row[1] = v.y;
+      row[2] = v.z;
+      row[3] = v.w;
+    }
   }
-  const int64_t qbase = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs + (int64_t)t * p.q_ts;
-  for (int d = threadIdx.x; d < D; d += PREP_BLOCK) qf[d] = load_elem(p.q, qbase + d, p.q_dtype);
-  for (int s = threadIdx.x; s < S; s += PREP_BLOCK) {
-    kmin[s] = 0xFFFFFFFFu;
-    kmax[s] = 0u;
+  const int64_t qbase = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs + (int64_t)tq * p.q_ts;
+  for (int d = t; d < D; d += PREP_BLOCK) qf[d] = load_elem(p.q, qbase + d, p.q_dtype);
+  shist[t] = 0u;
+  if (t < S) {
+    kmin[t] = 0xFFFFFFFFu;
+    kmax[t] = 0u;
   }
-  for (int i = threadIdx.x; i < SAMPLE_BINS; i += PREP_BLOCK) shist[i] = 0u;
+  if (t == 0) misc[2] = 0u;  // threshold bin 0 when fewer than k samples exist
   __syncthreads();
+  // 1. q_low
   const float sc = p.scale[h];
-  for (int r = threadIdx.x; r < R; r += PREP_BLOCK) {
+  for (int r = t; r < R; r += PREP_BLOCK) {
     float acc = 0.0f;
     for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qf[d], W[d * R + r], acc);
     const float v = acc * sc;
@@ -84,101 +133,70 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
     p.q_low[(int64_t)item * R + r] = v;
   }
   __syncthreads();
+  // 2. table and per-subspace key bounds
   float* lut_out = p.lut + (int64_t)item * S * C;
-  float* tab = W;  // the map is no longer needed: reuse its LDS for the table
-  for (int e = threadIdx.x; e < S * C; e += PREP_BLOCK) {
+  const bool wave_subspace = C % WAVE == 0;  // every wave's entries share a subspace
+  for (int e = t; e < S * C; e += PREP_BLOCK) {
     const int s = e / C;
-    const float* w = cb + (int64_t)e * sub;
+    const float* w = cb + e * cbs;
     const float* qs = ql + s * sub;
     float acc = 0.0f;
+#pragma unroll 16
     for (int j = 0; j < sub; ++j) acc = __builtin_fmaf(qs[j], w[j], acc);
     lut_out[e] = acc;
     tab[e] = acc;
-    const uint32_t k = f2key(acc);
-    atomicMin(&kmin[s], k);
-    atomicMax(&kmax[s], k);
-  }
-  __syncthreads();
-  // bounds of any sum of one table entry per subspace (before the 1/sqrt(R)
-  // scale), in the scan's summation order
-  if (threadIdx.x == 0) {
-    float lo = 0.0f, hi = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      lo = lo + key2f(kmin[s]);
-      hi = hi + key2f(kmax[s]);
+    uint32_t kn = f2key(acc), kx = kn;
+    if (wave_subspace) {
+      for (int off = 32; off > 0; off >>= 1) {
+        kn = min(kn, (uint32_t)__shfl_xor((int)kn, off, WAVE));
+        kx = max(kx, (uint32_t)__shfl_xor((int)kx, off, WAVE));
+      }
+      if (lane_id() == 0) {
+        atomicMin(&kmin[s], kn);
+        atomicMax(&kmax[s], kx);
+      }
+    } else {
+      atomicMin(&kmin[s], kn);
+      atomicMax(&kmax[s], kx);
     }
-    misc[0] = __float_as_uint(lo);
-    misc[1] = __float_as_uint(hi);
   }
   __syncthreads();
-  const float lo = __uint_as_float(misc[0]);
-  const float hi = __uint_as_float(misc[1]);
+  // 3. bounds of any sum of one table entry per subspace (before the 1/sqrt(R)
+  // scale), in the scan's summation order; every thread folds them itself
+  float lo = 0.0f, hi = 0.0f;
+  for (int s = 0; s < S; ++s) {
+    lo = lo + key2f(kmin[s]);
+    hi = hi + key2f(kmax[s]);
+  }
   float t_lo = -INFINITY;
-  // sampled estimate of a sum below which the shortlist threshold almost
-  // surely lies: the k-th largest of SAMPLE_BLOCKS * SAMPLE_KEYS sampled
-  // keys with k ~ SAMPLE_TARGET * L * samples / N.  Only a performance hint:
-  // the wide summon stays exact whatever it returns.  Sample blocks start at
-  // multiples of 16 keys so that each is a run of 16-byte words.
-  const int64_t N = p.n_keys;
-  constexpr int n_sample = SAMPLE_BLOCKS * SAMPLE_KEYS;
-  if (p.codes != nullptr && N >= 4 * (int64_t)n_sample) {
-    const double want = (double)SAMPLE_TARGET * (double)p.shortlist * (double)n_sample / (double)N;
-    const int k = (int)want + 1;
-    if (k < n_sample / 2 && hi > lo) {
-      const float inv_w = (float)SAMPLE_BINS / (hi - lo);
-      const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
-      const int words = SAMPLE_KEYS * S / 16;  // 16-byte words per sample block
-      if (((uintptr_t)head & 15u) == 0) {
-        for (int w = threadIdx.x; w < SAMPLE_BLOCKS * words; w += PREP_BLOCK) {
-          const int blk = w / words;
-          const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
-          reinterpret_cast<uint4*>(scodes)[w] = reinterpret_cast<const uint4*>(head + n0 * S)[w % words];
-        }
-      } else {
-        for (int e = threadIdx.x; e < n_sample * S; e += PREP_BLOCK) {
-          const int blk = e / (SAMPLE_KEYS * S);
-          const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
-          scodes[e] = head[n0 * S + e % (SAMPLE_KEYS * S)];
-        }
-      }
-      __syncthreads();
-      for (int i = threadIdx.x; i < n_sample; i += PREP_BLOCK) {
-        float acc = 0.0f;
-        for (int s = 0; s < S; ++s) {
-          const int c = min((int)scodes[i * S + s], C - 1);
-          acc = acc + tab[s * C + c];
-        }
-        int bin = (int)((acc - lo) * inv_w);
-        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
-        atomicAdd(&shist[bin], 1u);
-      }
-      __syncthreads();
-      // thread j owns bins [SAMPLE_BINS - PER*(j+1), SAMPLE_BINS - PER*j):
-      // a suffix scan from the top finds the bin holding the k-th largest
-      constexpr int PER = SAMPLE_BINS / PREP_BLOCK;
-      const int top = SAMPLE_BINS - PER * threadIdx.x;
-      uint32_t mine = 0;
+  // 4. sampled estimate of a sum below which the shortlist threshold almost
+  // surely lies.  Only a performance hint: the wide summon stays exact
+  // whatever it returns.
+  if (sample && hi > lo) {
+    const float inv_w = (float)SAMPLE_BINS / (hi - lo);
 #pragma unroll
-      for (int i = 1; i <= PER; ++i) mine += shist[top - i];
-      uint32_t total;
-      const uint32_t above = block_excl_scan<PREP_BLOCK>(mine, misc + 4, &total);
-      if (threadIdx.x == 0) misc[2] = 0u;  // bin 0 when fewer than k samples exist
-      __syncthreads();
-      if (above < (uint32_t)k && above + mine >= (uint32_t)k) {
-        uint32_t run = above;
-        for (int i = 1; i <= PER; ++i) {
-          run += shist[top - i];
-          if (run >= (uint32_t)k) {
-            misc[2] = (uint32_t)(top - i);
-            break;
-          }
-        }
+    for (int u = 0; u < SPT; ++u) {
+      const int i = t + u * PREP_BLOCK;
+      float acc = 0.0f;
+      for (int s = 0; s < S; ++s) {
+        const int c = min((int)scodes[i * S + s], C - 1);
+        acc = acc + tab[s * C + c];
       }
-      __syncthreads();
-      t_lo = lo + (float)misc[2] / inv_w;
+      int bin = (int)((acc - lo) * inv_w);
+      bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
+      atomicAdd(&shist[bin], 1u);
     }
+    __syncthreads();
+    // thread j owns bin SAMPLE_BINS - 1 - j: a scan from the top finds the
+    // bin holding the k-th largest
+    const uint32_t mine = shist[SAMPLE_BINS - 1 - t];
+    uint32_t total;
+    const uint32_t above = block_excl_scan<PREP_BLOCK>(mine, scratch, &total);
+    if (above < (uint32_t)k && above + mine >= (uint32_t)k) misc[2] = (uint32_t)(SAMPLE_BINS - 1 - t);
+    __syncthreads();
+    t_lo = lo + (float)misc[2] / inv_w;
   }
-  if (threadIdx.x == 0) {
+  if (t == 0) {
     float* rg = p.range + (int64_t)item * 4;
     rg[0] = lo;
     rg[1] = hi;
@@ -216,10 +234,9 @@ __global__ void __launch_bounds__(SCORE_BLOCK)
 }
 
 size_t lut_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C, bool sample) {
-  const int64_t sub = R / S;
-  return sizeof(float) * (size_t)(std::max(D * R, S * C) + S * C * sub + D + R) +
-         sizeof(uint32_t) * (size_t)(2 * S + SAMPLE_BINS + 8) +
-         (sample ? (size_t)(SAMPLE_BLOCKS * SAMPLE_KEYS * S + 16) : 0);
+  return sizeof(float) * (size_t)(D * R + S * C * (R / S + 1) + D + R + S * C) +
+         sizeof(uint32_t) * (size_t)(2 * S + SAMPLE_BINS + 4 + PREP_BLOCK / 64 + 1) +
+         (sample ? (size_t)(N_SAMPLE * S) : 0);
 }
 
 }  // namespace
