@@ -137,7 +137,7 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 SUMMON_KERNELS = ("wide_scan_kernel", "wide_finish_kernel")
 PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel",
                                                          "verify_combine_kernel")
-PROFILE_STEM = "sva_summon_decode_1m_{layout}"
+PROFILE_STEM = "summon_select_decode_1m_{layout}"
 
 
 def _kernel_key(name):
