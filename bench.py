@@ -49,8 +49,11 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
-    ap.add_argument("--suite", default="decode", choices=("decode", "write"),
-                    help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA")
+    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model"),
+                    help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA; "
+                         "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched")
+    ap.add_argument("--prefill", type=int, default=8192, help="model suite: prompt tokens")
+    ap.add_argument("--decode-steps", type=int, default=256, help="model suite: timed greedy decode steps")
     ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
                     help="summarize rocprofv3 outputs of this benchmark into profiles/ and exit")
     return ap.parse_args()
@@ -260,15 +263,89 @@ def write_suite(args):
     }), flush=True)
 
 
+def model_suite(args):
+    """Decode tokens/s of a SmolLM2-135M-architecture decoder (random init,
+    bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64, RoPE theta 1e5)
+    with every attention layer SVA-patched (synthetic 2x256 artifacts, rank
+    64, shortlist 2048 / budget 512): a prefill of uniform random token ids,
+    8 untimed greedy decode steps, then `--decode-steps` timed greedy steps
+    (torch.cuda.synchronize on both sides).  The same model unpatched (torch
+    sdpa attention, bf16) is timed the same way for reference."""
+
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from sva_amd import SVAArtifactBundle, SVALayerArtifacts, patch_llama_attention
+
+    device = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    n_layers, heads, kv_heads, head_dim, rank, subspaces, codewords = 30, 9, 3, 64, 64, 2, 256
+    config = LlamaConfig(vocab_size=49152, hidden_size=576, intermediate_size=1536, num_hidden_layers=n_layers,
+                         num_attention_heads=heads, num_key_value_heads=kv_heads, head_dim=head_dim,
+                         max_position_embeddings=args.prefill + args.decode_steps + 64, rope_theta=100000.0,
+                         tie_word_embeddings=True, attn_implementation="sdpa")
+    model = LlamaForCausalLM(config).to(device=device, dtype=torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(args.seed + 1)
+    arts = {i: SVALayerArtifacts(q_proj=torch.randn(heads, head_dim, rank, generator=g) / 8.0,
+                                 k_proj=torch.randn(heads, head_dim, rank, generator=g) / 8.0,
+                                 logit_scale=torch.zeros(heads),
+                                 coarse_codebooks=torch.randn(heads, subspaces, codewords, rank // subspaces,
+                                                              generator=g),
+                                 train_loss=0.0, hard_loss=0.0)
+            for i in range(n_layers)}
+    manifest = {"schema_version": 1, "artifact_type": "summon_verify_attention", "rank_dim": rank,
+                "coarse_subspaces": subspaces, "coarse_codewords": codewords, "default_shortlist": 2048,
+                "default_budget": 512, "layer_count": n_layers, "layers": list(range(n_layers))}
+    bundle = SVAArtifactBundle(manifest=manifest, layers=arts)
+    prompt = torch.randint(0, config.vocab_size, (1, args.prefill), generator=g).to(device)
+
+    def run(patched):
+        with torch.no_grad():
+            t0 = time.perf_counter()
+            out = model(input_ids=prompt, use_cache=True)
+            past = out.past_key_values
+            tok = out.logits[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+            prefill_s = time.perf_counter() - t0
+            for _ in range(8):
+                out = model(input_ids=tok, past_key_values=past, use_cache=True)
+                past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.decode_steps):
+                out = model(input_ids=tok, past_key_values=past, use_cache=True)
+                past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+            return prefill_s, time.perf_counter() - t0
+
+    dense_prefill, dense_decode = run(False)
+    with patch_llama_attention(model, bundle, shortlist=2048, budget=512, summon_mode="scan") as handle:
+        sva_prefill, sva_decode = run(True)
+        summary = handle.stats.summary()
+    tok_s = args.decode_steps / sva_decode
+    print(json.dumps({
+        "metric": "decode tok/s", "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.decode_steps, "warmup": 8, "ms_per_step": round(1e3 * sva_decode / args.decode_steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 (fp32 scores)",
+        "data": "synthetic (random-init weights, uniform random prompt, synthetic 2x256 artifacts)",
+        "config": {"workload": "SmolLM2-135M-shape decoder, 30 SVA layers, batch 1", "prefill": args.prefill,
+                   "shortlist": 2048, "budget": 512, "summon_mode": "scan", "intermediate_size": 1536},
+        "prefill_s": round(sva_prefill, 3),
+        "dense_attention": {"tok_s": round(args.decode_steps / dense_decode, 1), "prefill_s": round(dense_prefill, 3),
+                            "attention": "torch sdpa, bf16"},
+        "sva_stats": {k: round(v, 3) for k, v in summary.items() if isinstance(v, float) and v == v},
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.write_profiles:
         write_profiles(args)
         return
-    if args.suite == "write":
+    if args.suite in ("write", "model"):
         if args.gpus != 1:
             sys.exit(2)
-        write_suite(args)
+        (write_suite if args.suite == "write" else model_suite)(args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "

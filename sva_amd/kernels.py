@@ -295,9 +295,10 @@ class ScanDecodePlan:
         self.rng = torch.empty(n_seq, heads, q_len, 4, device=self.device, dtype=f32)
         self.sl_idx = torch.empty(items, shortlist, device=self.device, dtype=i32)
         self.sl_rank = torch.empty(items, shortlist, device=self.device, dtype=f32)
-        self.sl_count = torch.empty(items, device=self.device, dtype=i32)
+        self.counts = torch.empty(2, items, device=self.device, dtype=i32)  # shortlist and budget sizes
+        self.sl_count = self.counts[0]
         self.fin_idx = torch.empty(items, budget, device=self.device, dtype=i32)
-        self.fin_count = torch.empty(items, device=self.device, dtype=i32)
+        self.fin_count = self.counts[1]
         self._lib = lib()
 
     def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,

@@ -120,6 +120,7 @@ class SVALlamaAttention(nn.Module):
         self._codes_len = 0                          # rows with codes
         self._signature: tuple | None = None
         self._postings: inverted.Postings | None = None
+        self._decode_plan: kernels.ScanDecodePlan | None = None  # q = 1 buffers, kept across steps
 
     # ------------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
@@ -188,6 +189,8 @@ class SVALlamaAttention(nn.Module):
         """sva/llama.py:226-328 on the HIP path, chunked over query tokens."""
 
         q_len = query.shape[2]
+        if q_len == 1 and mask is None and query.shape[0] == 1:
+            return self._scan_decode(query, keys, values, k_low, codes, k_len, shortlist, budget)
         chunk = self.serving.query_chunk_size
         if chunk is None:
             chunk = 128 if (q_len >= 4096 or shortlist >= 2048) else q_len
@@ -215,6 +218,24 @@ class SVALlamaAttention(nn.Module):
                     "summoned": sl_count, "exact_scored": fin_count, "verified": fin_count,
                     "queries": float(sl_count.numel())})
         return outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)
+
+    def _scan_decode(self, query, keys, values, k_low, codes, k_len, shortlist, budget):
+        """One decode token (q = 1, causal): the same three calls through a
+        plan that keeps its buffers across steps."""
+
+        heads, head_dim = query.shape[1], query.shape[3]
+        rank, subspaces, codewords = self.sva_q_proj.shape[2], self.sva_coarse_codebooks.shape[1], \
+            self.sva_coarse_codebooks.shape[2]
+        shape = (1, heads, 1, head_dim, rank, subspaces, codewords, shortlist, budget)
+        plan = self._decode_plan
+        if plan is None or plan.shape != shape or plan.device != query.device:
+            plan = self._decode_plan = kernels.ScanDecodePlan(query.device, *shape)
+        out = plan.run(query, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks, codes, k_low, keys, values,
+                       k_len, self.scaling)
+        if self.stats is not None:
+            self.stats.add_device_rows(int(self.layer_idx or 0), (("summoned",), ("exact_scored", "verified")),
+                                       plan.counts, {"queries": float(heads)})
+        return out
 
     # ------------------------------------------------------------------
     def _ensure_capacity(self, rows: int, device: torch.device) -> None:

@@ -26,6 +26,8 @@ class SVAStats:
         self._by_layer: defaultdict[int, defaultdict[str, float]] = defaultdict(_float_stats)
         # (layer, name) -> float64 device accumulator not yet folded in
         self._pending: dict[tuple[int, str], torch.Tensor] = {}
+        # (layer, row names) -> float64 device vector of row sums not yet folded in
+        self._pending_rows: dict[tuple[int, tuple[tuple[str, ...], ...]], torch.Tensor] = {}
 
     # -- recording --------------------------------------------------------
     def add(self, layer_idx: int, values: dict[str, float]) -> None:
@@ -48,7 +50,30 @@ class SVAStats:
         if host:
             self.add(layer_idx, host)
 
+    def add_device_rows(self, layer_idx: int, names: tuple[tuple[str, ...], ...], counts: torch.Tensor,
+                        host: dict[str, float] | None = None) -> None:
+        """Accumulate the row sums of a device count matrix `counts` [rows,
+        n]: row i adds to every statistic named in names[i].  Two small
+        device kernels per call, no sync."""
+
+        total = counts.sum(dim=1, dtype=torch.float64)
+        key = (layer_idx, names)
+        slot = self._pending_rows.get(key)
+        if slot is None:
+            self._pending_rows[key] = total
+        else:
+            slot.add_(total)
+        if host:
+            self.add(layer_idx, host)
+
     def _flush(self) -> None:
+        if self._pending_rows:
+            rows, self._pending_rows = self._pending_rows, {}
+            for (layer_idx, names), vec in rows.items():
+                for row_names, v in zip(names, vec.tolist()):
+                    for key in row_names:
+                        self._totals[key] += v
+                        self._by_layer[layer_idx][key] += v
         if not self._pending:
             return
         pending, self._pending = self._pending, {}
@@ -70,6 +95,7 @@ class SVAStats:
 
     def reset(self) -> None:
         self._pending.clear()
+        self._pending_rows.clear()
         self._totals.clear()
         self._by_layer.clear()
 
