@@ -143,6 +143,16 @@ SVA_DEV uint32_t wave_incl_scan(uint32_t v) {
   return v + (row == 0 ? 0u : (row == 1 ? t0 : (row == 2 ? t0 + t1 : t0 + t1 + t2)));
 }
 
+// Sum over the wave (all 64 lanes active), wave-uniform.
+SVA_DEV uint32_t wave_sum_dpp(uint32_t v) {
+  v += row_shr0<1>(v);
+  v += row_shr0<2>(v);
+  v += row_shr0<4>(v);
+  v += row_shr0<8>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 15) + (uint32_t)__builtin_amdgcn_readlane((int)v, 31) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 47) + (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // OR and AND of a 64-bit value over the wave (all 64 lanes active), wave-uniform.
 SVA_DEV void wave_or_and_u64(uint64_t& vor, uint64_t& vand) {
   uint32_t o[2] = {(uint32_t)vor, (uint32_t)(vor >> 32)};
@@ -271,7 +281,9 @@ SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint
 // ---------------------------------------------------------------------------
 // Selection over elements held in registers: each thread of the block holds
 // NPT nonzero composites (0 = empty slot); slots from `slots` on are empty in
-// every thread and skipped.  Radix passes of up to TOP_BITS
+// every thread and skipped.  vor / vand: this thread's OR and AND of its
+// elements, or (bounds_given) block-uniform bounds hi >= every element >= lo,
+// whose common high bits every element shares.  Radix passes of up to TOP_BITS
 // bits from the highest bit where the elements differ, counted in one shared
 // LDS histogram; as soon as the bucket holding the k-th largest has at most
 // TOP_SMALL elements they are gathered and sorted by one wave.  Returns X such
@@ -291,23 +303,27 @@ struct TopLds {
 
 template <int BLOCK, int NPT>
 SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s,
-                                 int slots = NPT) {
+                                 int slots = NPT, bool bounds_given = false) {
   static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
   const int lane = lane_id();
-  wave_or_and_u64(vor, vand);
-  if (threadIdx.x == 0) {
-    s.shared64[0] = 0ull;
-    s.shared64[1] = ~0ull;
+  uint64_t all_or = vor, all_and = vand;  // bounds_given: block-uniform hi and lo with lo <= every element <= hi
+  if (!bounds_given) {
+    wave_or_and_u64(vor, vand);
+    if (threadIdx.x == 0) {
+      s.shared64[0] = 0ull;
+      s.shared64[1] = ~0ull;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      atomicOr((unsigned long long*)&s.shared64[0], (unsigned long long)vor);
+      atomicAnd((unsigned long long*)&s.shared64[1], (unsigned long long)vand);
+    }
+    __syncthreads();
+    all_or = s.shared64[0];
+    all_and = s.shared64[1];
+    __syncthreads();
   }
-  __syncthreads();
-  if (lane == 0) {
-    atomicOr((unsigned long long*)&s.shared64[0], (unsigned long long)vor);
-    atomicAnd((unsigned long long*)&s.shared64[1], (unsigned long long)vand);
-  }
-  __syncthreads();
-  const uint64_t all_or = s.shared64[0], all_and = s.shared64[1];
   const uint64_t diff = all_or ^ all_and;
-  __syncthreads();
   if (diff == 0ull) return all_or;  // one distinct value
   int top = 63 - __clzll((long long)diff);
   uint64_t pmask = top == 63 ? 0ull : ~0ull << (top + 1);

@@ -486,8 +486,8 @@ SVA_DEV void finish_budget(const SummonParams& p, int item, int leff, int beff, 
 // Direct path of the finish (see wide_finish_kernel): DH entries per lane
 // and list, slot DH * k + h = list k * DQ + q, entry l + 16 h.
 template <int DH, typename Emit>
-SVA_DEV void finish_direct(const WideArgs& a, int item, int nsub, int leff, uint32_t M, const uint32_t* lcnt,
-                           uint32_t* loff, const TopLds& tl, uint32_t* scratch, Emit emit) {
+SVA_DEV void finish_direct(const WideArgs& a, int item, int nsub, int leff, uint32_t M, uint64_t c_lo, uint64_t c_hi,
+                           const uint32_t* lcnt, uint32_t* loff, const TopLds& tl, uint32_t* scratch, Emit emit) {
   const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
   const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
   const int t = threadIdx.x;
@@ -505,19 +505,15 @@ SVA_DEV void finish_direct(const WideArgs& a, int item, int nsub, int leff, uint
       for (int h = 0; h < DH; ++h) e[DH * k + h] = cand[off + l + 16 * h];
     }
   }
-  uint64_t vor = 0ull, vand = ~0ull;
 #pragma unroll
   for (int k = 0; k < DK; ++k) {
     const int sidx = k * DQ + q;
     const uint32_t c = (k < kq && sidx < nsub) ? lcnt[sidx] : 0u;
 #pragma unroll
-    for (int h = 0; h < DH; ++h) {
+    for (int h = 0; h < DH; ++h)
       if ((uint32_t)(l + 16 * h) >= c) e[DH * k + h] = 0ull;
-      vor |= e[DH * k + h];
-      vand &= e[DH * k + h] != 0ull ? e[DH * k + h] : ~0ull;
-    }
   }
-  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NS>(e, leff, vor, vand, tl, DH * kq);
+  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NS>(e, leff, c_hi, c_lo, tl, DH * kq, true);
   // the selected load their ranks (written beside the lists by the scan)
   float rnk[NS];
 #pragma unroll
@@ -617,25 +613,29 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
   float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  // 1. totals: candidates M, allowed keys A; list counts and offsets
+  // 1. totals: candidates M, allowed keys A, longest list; list counts
   if (t == 0) {
+    shared[0] = 0u;  // M
+    shared[1] = 0u;  // longest list (when nsub <= SB), if over 32
     shared[2] = 0u;  // some list longer than DCAP
-    shared[1] = 0u;  // longest list (when nsub <= SB)
+    shared[3] = 0u;  // A
   }
   uint32_t m = 0, al = 0;
   for (int sidx = t; sidx < nsub; sidx += SB) {
     m += ncand[sidx];
     al += nallow[sidx];
   }
-  uint32_t M, A;
-  const uint32_t my_base = block_excl_scan<SB>(m, scratch, &M);  // list offset when nsub <= SB
+  if (nsub <= SB) lcnt[t] = m;
+  const uint32_t wm = wave_sum_dpp(m), wa = wave_sum_dpp(al);
+  __syncthreads();
+  if (lane == 0) {
+    atomicAdd(&shared[0], wm);
+    atomicAdd(&shared[3], wa);
+  }
   if (m > (uint32_t)DCAP) atomicOr(&shared[2], 1u);
   if (m > 32u) atomicMax(&shared[1], m);
-  if (nsub <= SB) {
-    lcnt[t] = m;
-    loff[t] = my_base;
-  }
-  block_excl_scan<SB>(al, scratch, &A);
+  __syncthreads();
+  const uint32_t M = shared[0], A = shared[3];
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
   if (t == 0) {
@@ -644,6 +644,10 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   }
   if (leff == 0) return;
   const bool long_lists = shared[2] != 0u;
+  const uint32_t longest = shared[1];
+  // bounds of every candidate composite: sums in [floor, upper bound of any sum]
+  const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
+  const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
   auto emit = [&](uint32_t o, uint64_t x, float rank) {
     const uint32_t key = composite_index(x);
     out_idx[o] = (int32_t)key;
@@ -652,11 +656,12 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   };
   bool dense = true;  // rank composites in rk (else sl + ranks in LDS)
   if (M >= (uint32_t)leff && nsub <= DL_LISTS && !long_lists) {
-    if (shared[1] > 32u) finish_direct<3>(a, item, nsub, leff, M, lcnt, loff, tl, scratch, emit);
-    else finish_direct<2>(a, item, nsub, leff, M, lcnt, loff, tl, scratch, emit);
+    if (longest > 32u) finish_direct<3>(a, item, nsub, leff, M, c_lo, c_hi, lcnt, loff, tl, scratch, emit);
+    else finish_direct<2>(a, item, nsub, leff, M, c_lo, c_hi, lcnt, loff, tl, scratch, emit);
   } else if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND && nsub <= STAGE_LISTS) {
     // staged: lists into LDS in list order
     if (nsub <= SB) {
+      loff[t] = block_excl_scan<SB>(m, scratch, nullptr);
       __syncthreads();  // lcnt / loff
       constexpr int KQ = SB / DQ;
       const int kq = (nsub + DQ - 1) / DQ;
@@ -686,16 +691,13 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     constexpr int NPT = LDS_CAND / SB;
     const int slots = ((int)M + SB - 1) / SB;
     uint64_t e[NPT];
-    uint64_t vor = 0ull, vand = ~0ull;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       const int j = t + i * SB;
       e[i] = j < (int)M ? cl[j] : 0ull;
-      vor |= j < (int)M ? e[i] : 0ull;
-      vand &= j < (int)M ? e[i] : ~0ull;
     }
     __syncthreads();  // staging area free
-    const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, vor, vand, tl, slots);
+    const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPT>(e, leff, c_hi, c_lo, tl, slots, true);
     // ranks of the selected: staging position -> list (last offset <= it)
     float rnk[NPT];
 #pragma unroll
