@@ -257,7 +257,7 @@ def write_suite(args):
         "unit": "Mkeys/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "dtype": "fp32 (bf16 K in)", "data": "synthetic", "config": {"workload": f"{n}-key catalog, 9 heads, "
                                                                                    f"{args.layout} codes"},
-        "roofline": {"kernel": "write_encode_mfma_kernel", "bound": "mfma", "achieved": round(tflops, 2),
+        "roofline": {"kernel": "write_encode_persistent_kernel", "bound": "mfma", "achieved": round(tflops, 2),
                      "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_F32_PEAK_TFLOPS, 4),
                      "flop_per_launch": flop, "traffic": None},
     }), flush=True)

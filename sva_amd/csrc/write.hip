@@ -273,6 +273,251 @@ __global__ void __launch_bounds__(WT) write_encode_mfma_kernel(WriteParams p) {
   }
 }
 
+// Persistent MFMA variant for the common shapes (D in {64, 128}, R = 64 with
+// 2 x 256 or 4 x 64 codes, keys rows 16-byte aligned).  Each workgroup serves
+// one head and walks that head's 64-row tiles with stride gridDim.x, so the
+// head's map, codebooks and centroid norms are loaded once, into registers.
+// The map / codebook is the MFMA A operand and the rows the B operand, so a
+// lane's four accumulator elements are four columns (centroids) of one row:
+//   projection: wave w owns columns 16(w + 4m) .. +15 of k_low;
+//   distances:  wave w owns centroids 16(w + 4m) .. +15 of every subspace.
+// Products are commutative, so the k-order rounding equals the kernel above.
+// The next tile's key rows are loaded into registers while this tile computes.
+template <int D, int S, int SUB, int C>
+__global__ void __launch_bounds__(WT, 2) write_encode_persistent_kernel(WriteParams p) {
+#pragma clang fp contract(off)
+  constexpr int R = S * SUB;
+  constexpr int NCOLW = R / 64;  // projection column blocks per wave
+  constexpr int NCBW = C / 64;   // centroid blocks per wave and subspace
+  constexpr int KS = D + 4;      // Kt row stride (floats; 16-byte rows, no bank conflicts)
+  constexpr int XS = R + 4;      // Xl row stride
+  constexpr int KJ = D / 4, XJ = SUB / 4;
+  constexpr int MAXCH = D / 16;  // 16-byte key chunks per thread and tile (fp32 keys)
+  static_assert(R % 64 == 0 && C % 64 == 0 && SUB % 4 == 0 && D % 16 == 0 && (D & (D - 1)) == 0, "shape");
+  static_assert(KT * S <= WT && S * C <= KT * XS, "tile");
+  __shared__ __align__(16) float Kt[KT * KS];
+  __shared__ __align__(16) float Xl[KT * XS];
+  __shared__ float xxl[S * KT];
+  __shared__ __align__(8) float2 mb[S * KT * 4];
+  const int h = blockIdx.y;
+  const int g = h / (p.H / p.G);
+  const int wid = threadIdx.x / WAVE;
+  const int l = lane_id();
+  const int lr = l & 15, lk = l >> 4;
+  const int64_t row_end = p.row0 + p.n_rows;
+  const int64_t n_tiles = (p.n_rows + KT - 1) / KT;
+  const bool want_codes = p.codes != nullptr;
+
+  float wreg[NCOLW][KJ];
+  {
+    const float* W = p.k_proj + (int64_t)h * D * R;
+#pragma unroll
+    for (int m = 0; m < NCOLW; ++m)
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) wreg[m][j] = W[(4 * j + lk) * R + 16 * (wid + 4 * m) + lr];
+  }
+  float cbreg[S][NCBW][XJ];
+  float cnreg[S][NCBW][4];
+  const float* CB = p.codebooks + (int64_t)h * S * C * SUB;
+  if (want_codes) {
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int m = 0; m < NCBW; ++m)
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) cbreg[s][m][j] = CB[((int64_t)s * C + 16 * (wid + 4 * m) + lr) * SUB + 4 * j + lk];
+    for (int i = threadIdx.x; i < S * C; i += WT) Xl[i] = torch_order_dot(CB + (int64_t)i * SUB, CB + (int64_t)i * SUB, SUB);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int m = 0; m < NCBW; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cnreg[s][m][i] = Xl[s * C + 16 * (wid + 4 * m) + 4 * lk + i];
+    __syncthreads();
+  }
+
+  // key rows: 16-byte chunks, chunk q of a tile = row q >> cpr_shift
+  const bool f32 = p.kv_dtype == F32;
+  const int es = f32 ? 4 : 2;
+  const int cpr_shift = __builtin_ctz(D) - (f32 ? 2 : 3);
+  const int nch = (KT << cpr_shift) / WT;
+  const unsigned char* kbytes = (const unsigned char*)p.keys;
+  uint4 pre[MAXCH];
+  auto load_tile = [&](int64_t t) {
+    const int64_t n0 = p.row0 + t * KT;
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) {
+      if (c < nch) {
+        const int q = (int)threadIdx.x + c * WT;
+        const int row = q >> cpr_shift, ch = q & ((1 << cpr_shift) - 1);
+        pre[c] = make_uint4(0u, 0u, 0u, 0u);
+        if (n0 + row < row_end)
+          pre[c] = *reinterpret_cast<const uint4*>(kbytes + ((int64_t)g * p.kv_hs + (n0 + row) * p.kv_rs) * es + 16 * ch);
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) {
+      if (c < nch) {
+        const int q = (int)threadIdx.x + c * WT;
+        const int row = q >> cpr_shift, ch = q & ((1 << cpr_shift) - 1);
+        const uint4 v = pre[c];
+        if (f32) {
+          *reinterpret_cast<uint4*>(Kt + row * KS + 4 * ch) = v;
+        } else {
+          float4 lo, hi;
+          if (p.kv_dtype == BF16) {
+            lo = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                             __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+            hi = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                             __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+          } else {
+            const __half* hv = reinterpret_cast<const __half*>(&v);
+            lo = make_float4(__half2float(hv[0]), __half2float(hv[1]), __half2float(hv[2]), __half2float(hv[3]));
+            hi = make_float4(__half2float(hv[4]), __half2float(hv[5]), __half2float(hv[6]), __half2float(hv[7]));
+          }
+          *reinterpret_cast<float4*>(Kt + row * KS + 8 * ch) = lo;
+          *reinterpret_cast<float4*>(Kt + row * KS + 8 * ch + 4) = hi;
+        }
+      }
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t < n_tiles) load_tile(t);
+  for (; t < n_tiles; t += gridDim.x) {
+    const int64_t n0 = p.row0 + t * KT;
+    const int nk = (int)min((int64_t)KT, row_end - n0);
+    store_tile();
+    if (t + gridDim.x < n_tiles) load_tile(t + gridDim.x);
+    __syncthreads();
+    // projection: Xl[row][col] = sum_d K[row][d] * W[d][col]
+    {
+      f32x4 acc[NCOLW][4];
+#pragma unroll
+      for (int m = 0; m < NCOLW; ++m)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) acc[m][rb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        float b[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) b[rb] = Kt[(16 * rb + lr) * KS + 4 * j + lk];
+#pragma unroll
+        for (int m = 0; m < NCOLW; ++m)
+#pragma unroll
+          for (int rb = 0; rb < 4; ++rb)
+            acc[m][rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wreg[m][j], b[rb], acc[m][rb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int m = 0; m < NCOLW; ++m)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+          *reinterpret_cast<f32x4*>(Xl + (16 * rb + lr) * XS + 16 * (wid + 4 * m) + 4 * lk) = acc[m][rb];
+    }
+    __syncthreads();
+    {
+      float* klow = p.k_low + (int64_t)h * p.klow_hs + n0 * R;
+      for (int q = threadIdx.x; q < KT * R / 4; q += WT) {
+        const int row = q / (R / 4), c4 = q - row * (R / 4);
+        if (row < nk)
+          *reinterpret_cast<float4*>(klow + (int64_t)row * R + 4 * c4) = *reinterpret_cast<const float4*>(Xl + row * XS + 4 * c4);
+      }
+      if (want_codes && threadIdx.x < KT * S) {
+        const int row = threadIdx.x / S, s = threadIdx.x - row * S;
+        const float* x = Xl + row * XS + s * SUB;
+        xxl[s * KT + row] = torch_order_dot(x, x, SUB);
+      }
+    }
+    if (!want_codes) continue;
+    __syncthreads();
+    // distances of this wave's centroids to the 16 rows of each row block
+#pragma unroll 1
+    for (int rb = 0; rb < 4; ++rb) {
+      float xb[S][XJ];
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int j = 0; j < XJ; ++j) xb[s][j] = Xl[(16 * rb + lr) * XS + s * SUB + 4 * j + lk];
+      f32x4 acc[S][NCBW];
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int m = 0; m < NCBW; ++m) acc[s][m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < XJ; ++j)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int m = 0; m < NCBW; ++m)
+            acc[s][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(cbreg[s][m][j], xb[s][j], acc[s][m], 0, 0, 0);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const float xx = xxl[s * KT + 16 * rb + lr];
+        float best = INFINITY;
+        int kb = 0;
+        // (xx - 2 x.c) + |c|^2; 2 x.c is exact, so the fma rounds like the subtraction
+#pragma unroll
+        for (int m = 0; m < NCBW; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float dist = __builtin_fmaf(-2.0f, acc[s][m][i], xx) + cnreg[s][m][i];
+            if (dist < best) {
+              best = dist;
+              kb = 4 * m + i;
+            }
+          }
+        int arg = 16 * wid + 64 * (kb >> 2) + 4 * lk + (kb & 3);
+#pragma unroll
+        for (int o = 16; o < WAVE; o <<= 1) {
+          const float ob = __shfl_xor(best, o);
+          const int oa = __shfl_xor(arg, o);
+          if (ob < best || (ob == best && oa < arg)) {
+            best = ob;
+            arg = oa;
+          }
+        }
+        if (lk == 0) mb[(s * KT + 16 * rb + lr) * 4 + wid] = make_float2(best, __int_as_float(arg));
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < KT * S) {
+      const int row = threadIdx.x / S, s = threadIdx.x - row * S;
+      float best = INFINITY;
+      int arg = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float2 v = mb[(s * KT + row) * 4 + w];
+        const int oa = __float_as_int(v.y);
+        if (v.x < best || (v.x == best && oa < arg)) {
+          best = v.x;
+          arg = oa;
+        }
+      }
+      if (row < nk) store_code(p.codes, (int64_t)h * p.code_hs + (n0 + row) * S + s, p.ctype, arg);
+    }
+  }
+}
+
+template <int D, int S, int SUB, int C>
+int launch_persistent(const WriteParams& p, int64_t tiles, hipStream_t stream) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    SVA_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, write_encode_persistent_kernel<D, S, SUB, C>, WT, 0),
+                  "hipOccupancyMaxActiveBlocksPerMultiprocessor(write_encode_persistent_kernel)");
+    per_cu = n > 0 ? n : 1;
+  }
+  const int64_t slots = (int64_t)per_cu * device_cu_count();
+  const int64_t per_head = std::max<int64_t>(1, std::min<int64_t>(tiles, slots / p.H));
+  hipLaunchKernelGGL((write_encode_persistent_kernel<D, S, SUB, C>), dim3((unsigned)per_head, (unsigned)p.H), dim3(WT),
+                     0, stream, p);
+  SVA_CHECK_LAUNCH("write_encode_persistent_kernel");
+  return SVA_OK;
+}
+
 // Any shape: one thread per row, the same arithmetic as the tiled kernel.
 __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p) {
 #pragma clang fp contract(off)
@@ -382,6 +627,16 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
     hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, (hipStream_t)stream, p);
     SVA_CHECK_LAUNCH("write_encode_rowwise_kernel");
     return SVA_OK;
+  }
+  const int64_t es = kv_dtype == 0 ? 4 : 2;
+  const bool rows_aligned = ((uintptr_t)keys & 15u) == 0 && (kv_head_stride * es) % 16 == 0 &&
+                            (kv_row_stride * es) % 16 == 0;
+  if (rows_aligned && R == 64 && (D == 64 || D == 128)) {
+    const hipStream_t st = (hipStream_t)stream;
+    if (S == 2 && C == 256)
+      return D == 64 ? launch_persistent<64, 2, 32, 256>(p, tiles, st) : launch_persistent<128, 2, 32, 256>(p, tiles, st);
+    if (S == 4 && C == 64)
+      return D == 64 ? launch_persistent<64, 4, 16, 64>(p, tiles, st) : launch_persistent<128, 4, 16, 64>(p, tiles, st);
   }
   if (R % 16 == 0 && C % 16 == 0 && D % 4 == 0) {
     static bool attr_set = false;
