@@ -153,6 +153,21 @@ SVA_DEV uint32_t wave_sum_dpp(uint32_t v) {
          (uint32_t)__builtin_amdgcn_readlane((int)v, 47) + (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Minimum and maximum of a uint32 over the wave (all 64 lanes active), wave-uniform.
+SVA_DEV void wave_min_max_u32(uint32_t& mn, uint32_t& mx) {
+  mn = min(mn, row_shr_keep<1>(mn));
+  mx = max(mx, row_shr_keep<1>(mx));
+  mn = min(mn, row_shr_keep<2>(mn));
+  mx = max(mx, row_shr_keep<2>(mx));
+  mn = min(mn, row_shr_keep<4>(mn));
+  mx = max(mx, row_shr_keep<4>(mx));
+  mn = min(mn, row_shr_keep<8>(mn));
+  mx = max(mx, row_shr_keep<8>(mx));
+  const auto rl = [](uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); };
+  mn = min(min(rl(mn, 15), rl(mn, 31)), min(rl(mn, 47), rl(mn, 63)));
+  mx = max(max(rl(mx, 15), rl(mx, 31)), max(rl(mx, 47), rl(mx, 63)));
+}
+
 // OR and AND of a 64-bit value over the wave (all 64 lanes active), wave-uniform.
 SVA_DEV void wave_or_and_u64(uint64_t& vor, uint64_t& vand) {
   uint32_t o[2] = {(uint32_t)vor, (uint32_t)(vor >> 32)};
@@ -286,12 +301,12 @@ SVA_DEV uint64_t select_largest(Visit visit, int k, uint32_t (*whist)[256], uint
 // whose common high bits every element shares.  Radix passes of up to TOP_BITS
 // bits from the highest bit where the elements differ, counted in one shared
 // LDS histogram; as soon as the bucket holding the k-th largest has at most
-// TOP_SMALL elements they are gathered and sorted by one wave.  Returns X such
+// TOP_SMALL elements they are gathered and ranked directly.  Returns X such
 // that the selected elements are exactly those >= X (with repeated values,
 // more than k elements may reach X and the caller caps its output at k).
 constexpr int TOP_BITS = 12;
 constexpr int TOP_BINS = 1 << TOP_BITS;
-constexpr int TOP_SMALL = 64;  // one wave sorts the last bucket
+constexpr int TOP_SMALL = 64;  // last bucket ranked directly, 16 lanes per element
 
 struct TopLds {
   uint32_t* hist;      // [TOP_BINS]
@@ -305,6 +320,7 @@ template <int BLOCK, int NPT>
 SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, uint64_t vand, const TopLds& s,
                                  int slots = NPT, bool bounds_given = false) {
   static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
+  static_assert(TOP_SMALL * 16 == BLOCK, "16 lanes per element of the last bucket");
   const int lane = lane_id();
   uint64_t all_or = vor, all_and = vand;  // bounds_given: block-uniform hi and lo with lo <= every element <= hi
   if (!bounds_given) {
@@ -389,18 +405,29 @@ SVA_DEV uint64_t select_top_regs(const uint64_t (&e)[NPT], int k, uint64_t vor, 
         }
       }
       __syncthreads();
-      if (threadIdx.x < WAVE) {
-        // bitonic sort of the bucket, descending, in the lanes of wave 0
-        uint64_t v = (uint32_t)lane < cb ? s.small[lane] : 0ull;
-        for (int kk = 2; kk <= WAVE; kk <<= 1) {
-          for (int j = kk >> 1; j > 0; j >>= 1) {
-            const uint64_t o = __shfl_xor(v, j, WAVE);
-            const bool up = (lane & kk) == 0;
-            const bool low = (lane & j) == 0;
-            v = (low == up) ? (v > o ? v : o) : (v < o ? v : o);
+      {
+        // rank of each bucket element within the bucket: one DPP row of 16
+        // lanes per element, 4 comparisons per lane counting the elements
+        // above it (low half) and at or above it (high half); the need-th
+        // largest has fewer than need above and at least need at or above
+        // (equal elements write the same value)
+        const int i = (int)threadIdx.x >> 4, g = (int)threadIdx.x & 15;
+        const uint64_t v = i < (int)cb ? s.small[i] : 0ull;
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int o = 4 * g + j;
+          if (o < (int)cb) {
+            const uint64_t y = s.small[o];
+            c += (y > v ? 1u : 0u) + (y >= v ? 0x10000u : 0u);
           }
         }
-        if (lane == need - 1) s.shared64[0] = v;
+        c += row_shr0<1>(c);
+        c += row_shr0<2>(c);
+        c += row_shr0<4>(c);
+        c += row_shr0<8>(c);
+        if (g == 15 && i < (int)cb && (c & 0xFFFFu) < (uint32_t)need && (c >> 16) >= (uint32_t)need)
+          s.shared64[0] = v;
       }
       __syncthreads();
       const uint64_t X = s.shared64[0];

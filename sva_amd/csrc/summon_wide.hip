@@ -408,7 +408,8 @@ constexpr size_t kFinWcnt = kFinStage;                                          
 constexpr size_t kFinScratch = kFinWcnt + sizeof(uint32_t) * SNW * SNW;         // uint32[SNW + 1]
 constexpr size_t kFinShared = kFinScratch + sizeof(uint32_t) * (SNW + 2);       // uint32[4], 8-byte aligned
 constexpr size_t kFinShared64 = kFinShared + sizeof(uint32_t) * 4;              // uint64[2]
-constexpr size_t kFinLcnt = kFinShared64 + sizeof(uint64_t) * 2;                // uint32[SB]
+constexpr size_t kFinRkb = kFinShared64 + sizeof(uint64_t) * 2;                 // uint32[2] rank key bounds
+constexpr size_t kFinLcnt = kFinRkb + sizeof(uint32_t) * 2;                     // uint32[SB]
 constexpr size_t kFinLoff = kFinLcnt + sizeof(uint32_t) * SB;                   // uint32[STAGE_LISTS]
 constexpr size_t kFinLds = kFinLoff + sizeof(uint32_t) * STAGE_LISTS;
 static_assert(kFinShared64 % 8 == 0, "8-byte LDS words");
@@ -475,9 +476,9 @@ SVA_DEV void compact_ordered(const uint64_t (&e)[NPT], uint64_t X, int cap, uint
 // e2 (leff of them, dense), compacted in slot order (ascending key order) to fin.
 template <int NPT>
 SVA_DEV void finish_budget(const SummonParams& p, int item, int leff, int beff, const uint64_t (&e2)[NPT], uint64_t vor,
-                           uint64_t vand, const TopLds& tl, uint32_t* wcnt, uint32_t* scratch) {
+                           uint64_t vand, bool bounds_given, const TopLds& tl, uint32_t* wcnt, uint32_t* scratch) {
   const int slots = (leff + SB - 1) / SB;
-  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPT>(e2, beff, vor, vand, tl, slots);
+  const uint64_t X2 = beff == leff ? 1ull : select_top_regs<SB, NPT>(e2, beff, vor, vand, tl, slots, bounds_given);
   int32_t* fin = p.fin_idx + (int64_t)item * p.B;
   compact_ordered<SB, NPT>(e2, X2, beff, wcnt, scratch, slots,
                            [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
@@ -598,13 +599,13 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   uint32_t* scratch = (uint32_t*)(lds + kFinScratch);
   uint32_t* shared = (uint32_t*)(lds + kFinShared);
   uint64_t* shared64 = (uint64_t*)(lds + kFinShared64);
+  uint32_t* rkb = (uint32_t*)(lds + kFinRkb);
   uint32_t* lcnt = (uint32_t*)(lds + kFinLcnt);
   uint32_t* loff = (uint32_t*)(lds + kFinLoff);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
   const int item = blockIdx.x;
   const int t = threadIdx.x;
-  const int wid = t / WAVE;
   const int lane = lane_id();
   const int nsub = a.W * NW;
   const uint32_t* ncand = a.ncand + (int64_t)item * nsub;
@@ -619,6 +620,8 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     shared[1] = 0u;  // longest list (when nsub <= SB), if over 32
     shared[2] = 0u;  // some list longer than DCAP
     shared[3] = 0u;  // A
+    rkb[0] = 0xFFFFFFFFu;  // smallest and largest rank key of the shortlist
+    rkb[1] = 0u;
   }
   uint32_t m = 0, al = 0;
   for (int sidx = t; sidx < nsub; sidx += SB) {
@@ -648,11 +651,15 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   // bounds of every candidate composite: sums in [floor, upper bound of any sum]
   const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
   const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;  // rank keys this thread emitted
   auto emit = [&](uint32_t o, uint64_t x, float rank) {
     const uint32_t key = composite_index(x);
+    const uint32_t rkey = f2key(rank);
     out_idx[o] = (int32_t)key;
     out_rank[o] = rank;
-    rk[o] = composite(f2key(rank), key);
+    rk[o] = composite(rkey, key);
+    kmin = min(kmin, rkey);
+    kmax = max(kmax, rkey);
   };
   bool dense = true;  // rank composites in rk (else sl + ranks in LDS)
   if (M >= (uint32_t)leff && nsub <= DL_LISTS && !long_lists) {
@@ -781,6 +788,12 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     __syncthreads();
     rank_rows(p, item, sl, leff, (float*)rk);
   }
+  // bounds of the emitted rank keys (direct and staged paths) for the budget select
+  wave_min_max_u32(kmin, kmax);
+  if (lane == 0 && kmin <= kmax) {
+    atomicMin(&rkb[0], kmin);
+    atomicMax(&rkb[1], kmax);
+  }
   __syncthreads();
   // shortlist outputs of the list and all-keys paths; budget input
   constexpr int NPB = FIN_MAX_L / SB;
@@ -805,7 +818,9 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     }
   }
   if (p.B <= 0) return;
-  finish_budget<NPB>(p, item, leff, beff, e2, vor, vand, tl, wcnt, scratch);
+  const bool rb = dense && rkb[0] <= rkb[1];
+  const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
+  finish_budget<NPB>(p, item, leff, beff, e2, rb ? b_hi : vor, rb ? b_lo : vand, rb, tl, wcnt, scratch);
 }
 
 template <int S, bool SMALLC, bool MASKED>
