@@ -102,9 +102,7 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   float* qv = (float*)(lists + grp * B);              // [grp][D]
   float* vrow = qv + grp * D;                         // [EPW][D + 1] (padded: no bank conflicts)
   float* wt = vrow + EPW * (D + 1);                   // [EPW][MAX_GRP] scores, then weights
-  int32_t* ekey = (int32_t*)(wt + EPW * MAX_GRP);     // [EPW]
-  uint32_t* emem = (uint32_t*)(ekey + EPW);           // [EPW] heads whose list holds the entry
-  int* cnt = (int*)(emem + EPW);                      // [MAX_GRP + 1] prefix of list lengths
+  int* cnt = (int*)(wt + EPW * MAX_GRP);              // [MAX_GRP + 1] prefix of list lengths
   float* stat = (float*)(cnt + MAX_GRP + 1);          // [MAX_GRP][2]
 
   const int64_t len = p.lens ? p.lens[b] : p.N;
@@ -131,10 +129,12 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   const int e0 = (int)((int64_t)s * M / p.split);
   const int n = (int)((int64_t)(s + 1) * M / p.split) - e0;  // <= EPW
   // phase 2: first occurrences of the slice and the heads holding each; the
-  // 4 lanes of an entry search lists qt and qt + 4
+  // 4 lanes of an entry search lists qt and qt + 4.  The 4 lanes of an entry
+  // share a wave, so the entry state stays in registers.
   {
     const int r = threadIdx.x >> 2;
     const int qt = threadIdx.x & 3;
+    const int dq = D / 4;
     int j = 0;
     int32_t x = -1;
     if (r < n) {
@@ -150,38 +150,28 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
     }
     found |= __shfl_xor(found, 1, 4);
     found |= __shfl_xor(found, 2, 4);
-    if (qt == 0) {
-      const bool own = valid && (found & ((1u << j) - 1u)) == 0u;  // no lower head holds the key
-      ekey[r] = x;
-      emem[r] = own ? found : 0u;
-    }
-  }
-  __syncthreads();
-  // phase 3: every K and V row of the slice, 4 lanes per row
-  {
-    const int r = threadIdx.x >> 2;
-    const int qt = threadIdx.x & 3;
-    const uint32_t mem = emem[r];
-    const int dq = D / 4;
+    const bool own = valid && (found & ((1u << j) - 1u)) == 0u;  // no lower head holds the key
+    const uint32_t mem = own ? found : 0u;
+    // phase 3: every owned K and V row of the slice, 4 lanes per row
     float dot[MAX_GRP];
 #pragma unroll
-    for (int j = 0; j < MAX_GRP; ++j) dot[j] = 0.0f;
+    for (int jj = 0; jj < MAX_GRP; ++jj) dot[jj] = 0.0f;
     if (DT < 0) {
       // any head_dim: lane qt takes dimensions qt, qt + 4, ...
       if (mem != 0u) {
-        const int64_t rowb = (int64_t)g * p.kv_hs + (off + ekey[r]) * p.kv_rs;
+        const int64_t rowb = (int64_t)g * p.kv_hs + (off + x) * p.kv_rs;
         for (int d = qt; d < D; d += 4) {
           const float kk = load_elem(p.keys, rowb + d, p.kv_dtype);
           vrow[r * (D + 1) + d] = load_elem(p.values, rowb + d, p.kv_dtype);
 #pragma unroll
-          for (int j = 0; j < MAX_GRP; ++j)
-            if (j < grp) dot[j] = __builtin_fmaf(kk, qv[j * D + d], dot[j]);
+          for (int jj = 0; jj < MAX_GRP; ++jj)
+            if (jj < grp) dot[jj] = __builtin_fmaf(kk, qv[jj * D + d], dot[jj]);
         }
       } else if (r < n) {
         for (int d = qt; d < D; d += 4) vrow[r * (D + 1) + d] = 0.0f;  // weight 0 must not meet NaN
       }
     } else if (mem != 0u) {
-      const int64_t rowe = (int64_t)g * p.kv_hs + (off + ekey[r]) * p.kv_rs + qt * dq;
+      const int64_t rowe = (int64_t)g * p.kv_hs + (off + x) * p.kv_rs + qt * dq;
       constexpr int NCH = (DT > 0 ? DT : MAX_D) / 16;  // 4-element chunks per lane (DT >= 0)
       float kv[NCH][4], vv[NCH][4];
 #pragma unroll
@@ -199,8 +189,8 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
             const int d = qt * dq + 4 * c + k;
             vrow[r * (D + 1) + d] = vv[c][k];
 #pragma unroll
-            for (int j = 0; j < MAX_GRP; ++j)
-              if (j < grp) dot[j] = __builtin_fmaf(kv[c][k], qv[j * D + d], dot[j]);
+            for (int jj = 0; jj < MAX_GRP; ++jj)
+              if (jj < grp) dot[jj] = __builtin_fmaf(kv[c][k], qv[jj * D + d], dot[jj]);
           }
         }
       }
@@ -208,12 +198,12 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
       for (int d = qt * dq; d < (qt + 1) * dq; ++d) vrow[r * (D + 1) + d] = 0.0f;  // weight 0 must not meet NaN
     }
 #pragma unroll
-    for (int j = 0; j < MAX_GRP; ++j) {
-      if (j < grp) {
-        float v = dot[j];
+    for (int jj = 0; jj < MAX_GRP; ++jj) {
+      if (jj < grp) {
+        float v = dot[jj];
         v += __shfl_xor(v, 1, 4);
         v += __shfl_xor(v, 2, 4);
-        if (qt == 0) wt[r * MAX_GRP + j] = ((mem >> j) & 1u) ? v * p.scaling : -INFINITY;
+        if (qt == 0) wt[r * MAX_GRP + jj] = ((mem >> jj) & 1u) ? v * p.scaling : -INFINITY;
       }
     }
   }
@@ -305,7 +295,7 @@ int verify_split(int64_t grp, int64_t B) {
 
 size_t verify_lds_bytes(int64_t grp, int64_t B, int64_t D) {
   return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * EPW * (D + 1) +
-         sizeof(float) * EPW * MAX_GRP + 2 * sizeof(int32_t) * EPW + sizeof(int) * (MAX_GRP + 1) +
+         sizeof(float) * EPW * MAX_GRP + sizeof(int) * (MAX_GRP + 1) +
          sizeof(float) * 2 * MAX_GRP + 16;
 }
 
