@@ -244,6 +244,59 @@ int sva_unique_refill_select(const uint64_t *comp, const uint8_t *flag, int64_t 
                              int64_t tail_len, int32_t *fin_idx, int32_t *fin_count, float *stats, void *workspace,
                              size_t workspace_bytes, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Ragged static inverted decode: the static mode above for a packed batch of
+ * n_seq sequences, one launch per stage (the reference decodes batch 1 only,
+ * sva/llama.py:182-183; each sequence gets sva/llama.py:427-576).  Sequence b
+ * owns packed rows [seq_offsets[b], seq_offsets[b] + k_lens[b]) of codes,
+ * k_low, K and V; its postings cover its first postings_lens[b] rows and its
+ * tail is [postings_lens[b], k_lens[b]).  Key indices are sequence-local.
+ * Items are b * H + h.  No attention mask (every row allowed).
+ */
+
+/*
+ * Postings of every sequence: offsets [n_seq, H, S, C + 1], max_count
+ * [n_seq, H, S], ids [H, S, rows] with sequence b's ids (local, ascending
+ * within a cell) at its packed rows.  C <= 1024.
+ */
+int sva_postings_build_ragged(const void *codes, int code_type, int64_t code_head_stride, const int64_t *seq_offsets,
+                              const int64_t *postings_lens, int64_t n_seq, int64_t H, int64_t rows, int64_t S,
+                              int64_t C, int32_t *offsets, int32_t *ids, int32_t *max_count, void *stream);
+
+/* Candidate slots per item: lists of the longest postings, the longest tail, one extra slot. */
+int64_t sva_inverted_slots_ragged(int64_t S, int64_t max_postings_len, int64_t max_tail);
+
+/*
+ * Candidates of every item (sva_inverted_candidates, static mode, per
+ * sequence): lut [n_seq, H, S, C] and q_low [n_seq, H, R] from sva_query_lut
+ * (one token per sequence); comp / flag [n_seq * H, slots].
+ * max_postings_len >= every postings_lens[b], max_tail >= every
+ * k_lens[b] - postings_lens[b] (larger lists or tails are cut at the slots).
+ */
+int sva_inverted_candidates_ragged(const float *lut, const float *q_low, const float *k_low,
+                                   int64_t k_low_head_stride, const void *codes, int code_type,
+                                   int64_t code_head_stride, const int32_t *offsets, const int32_t *ids, int64_t rows,
+                                   const int64_t *seq_offsets, const int64_t *postings_lens, const int64_t *k_lens,
+                                   int64_t n_seq, int64_t max_postings_len, int64_t max_tail, int64_t H, int64_t S,
+                                   int64_t C, int64_t R, int64_t cells, uint64_t *comp, uint8_t *flag, int64_t slots,
+                                   void *stream);
+
+/*
+ * Static-mode selection of every item (sva_unique_refill_select, mode 0):
+ * sequence b's budgets are min(budget, k_lens[b]) and the adaptive minimum
+ * and middle budgets derived from it as in sva/llama.py:443-445 (0: the
+ * reference's defaults); its refill width uses its own largest cell and tail.
+ *   fin_idx [n_seq * H, budget] ascending local keys, fin_count, stats [.., 4]
+ * workspace: sva_unique_select_workspace_bytes(n_seq * H, budget, refill_factor, slots).
+ */
+int sva_unique_refill_select_ragged(const uint64_t *comp, const uint8_t *flag, int64_t slots, int64_t n_seq,
+                                    int64_t H, int64_t budget, int64_t adaptive_min_budget,
+                                    int64_t adaptive_mid_budget, double low_margin, double high_margin,
+                                    int64_t refill_factor, const int32_t *max_count, int64_t S, int64_t cells,
+                                    const int64_t *postings_lens, const int64_t *k_lens, int32_t *fin_idx,
+                                    int32_t *fin_count, float *stats, void *workspace, size_t workspace_bytes,
+                                    void *stream);
+
 /*
  * Unique refill selection over arbitrary rows of candidates
  * (SVALlamaAttention._top_unique_candidates, sva/llama.py:83-116): per row,

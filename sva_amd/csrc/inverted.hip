@@ -42,16 +42,25 @@ constexpr int PB = 1024;
 constexpr int PNW = PB / WAVE;
 constexpr int kMaxPostingCells = 1024;
 
+// One workgroup per (sequence b, head h, subspace s): the first n_rows rows of
+// the sequence (rows_of[b] of a ragged batch), which start at packed row
+// row0[b] (0 without one); ids hold sequence-local key indices at the
+// sequence's own packed rows of the [H, S, ids_rows] table.
 __global__ void __launch_bounds__(PB)
-    postings_build_kernel(const void* __restrict__ codes, int ctype, int64_t code_hs, int S, int n_rows, int C,
+    postings_build_kernel(const void* __restrict__ codes, int ctype, int64_t code_hs, int H, int S, int n_rows, int C,
+                          const int64_t* __restrict__ row0, const int64_t* __restrict__ rows_of, int64_t ids_rows,
                           int32_t* __restrict__ offsets, int32_t* __restrict__ ids, int32_t* __restrict__ max_count) {
   extern __shared__ __align__(16) unsigned char lds[];
   uint32_t* hist = (uint32_t*)lds;        // [C]
   uint32_t* cursor = hist + C;            // [C]
   uint32_t* wcnt = cursor + C;            // [PNW][C]
   uint32_t* scratch = wcnt + PNW * C;     // [PNW + 2]
-  const int h = blockIdx.x / S, s = blockIdx.x % S;
-  const int64_t cbase = (int64_t)h * code_hs + s;
+  const int b = blockIdx.x / (H * S);
+  const int hs = blockIdx.x - b * (H * S);
+  const int h = hs / S, s = hs - h * S;
+  const int64_t r0 = row0 ? row0[b] : 0;
+  if (rows_of) n_rows = (int)rows_of[b];
+  const int64_t cbase = (int64_t)h * code_hs + r0 * S + s;
   auto code_at = [&](int n) {
     int64_t c = load_code(codes, cbase + (int64_t)n * S, ctype);
     return (int)(c < 0 ? 0 : (c >= C ? C - 1 : c));
@@ -88,7 +97,7 @@ __global__ void __launch_bounds__(PB)
   int bits = 0;
   while ((1 << bits) < C) ++bits;
   const int wid = threadIdx.x / WAVE;
-  int32_t* out = ids + (int64_t)blockIdx.x * n_rows;
+  int32_t* out = ids + (int64_t)hs * ids_rows + r0;
   for (int base = 0; base < n_rows; base += PB) {
     for (int i = threadIdx.x; i < PNW * C; i += PB) wcnt[i] = 0u;
     __syncthreads();
@@ -148,22 +157,44 @@ struct CandParams {
   const void* mask;  // allowed iff mask[n] > -1e4 (MASK_* types), or NULL: every row
   int mask_type;
   int adaptive;
-  int W;                     // slots per head
-  uint64_t* comp;            // [H, W]; 0 = empty slot
-  uint8_t* flag;             // [H, W]: bit 0 valid, bit 1 fallback entry
+  int W;                     // slots per item
+  uint64_t* comp;            // [items, W]; 0 = empty slot
+  uint8_t* flag;             // [items, W]: bit 0 valid, bit 1 fallback entry
+  // ragged batches (static mode): item b * H + h; sequence b starts at
+  // packed row seq_offs[b], its postings cover its first plens[b] rows, its
+  // tail is [plens[b], klens[b]); lists take S * postings_len slots and the
+  // tail tail_cap slots.  NULL for one sequence (the scalars above).
+  const int64_t* seq_offs;
+  const int64_t* plens;
+  const int64_t* klens;
+  int tail_cap;
+  int64_t ids_rows;  // row dimension of ids: [H, S, ids_rows]
 };
 
 SVA_DEV bool row_allowed(const CandParams& p, int n) {
   return p.mask == nullptr || mask_allows(p.mask, n, p.mask_type);
 }
 
+// Item geometry: the packed row of key 0, the postings length, the tail start
+// and the key count of the item's sequence.
+struct ItemRows {
+  int64_t r0;
+  int plen, tail_start, k_len;
+};
+
+SVA_DEV ItemRows item_rows(const CandParams& p, int b) {
+  if (p.seq_offs == nullptr) return ItemRows{0, p.postings_len, p.tail_start, p.k_len};
+  const int plen = (int)p.plens[b];
+  return ItemRows{p.seq_offs[b], plen, plen, (int)p.klens[b]};
+}
+
 // Rank score of key n (16 lanes), torch's order, then / sqrt(R).  R == 64
 // splits the row over the 16 lanes; other ranks are summed by the group's
 // first lane.
-SVA_DEV float rank_score16(const CandParams& p, int h, int n) {
+SVA_DEV float rank_score16(const CandParams& p, int h, int item, int64_t r0, int n) {
 #pragma clang fp contract(off)
-  const float* row = p.k_low + (int64_t)h * p.klow_hs + (int64_t)n * p.R;
-  const float* q = p.q_low + (int64_t)h * p.R;
+  const float* row = p.k_low + (int64_t)h * p.klow_hs + (r0 + n) * p.R;
+  const float* q = p.q_low + (int64_t)item * p.R;
   if (p.R != 64) {
     float t = 0.0f;
     if ((lane_id() & 15) == 0) t = torch_order_dot(row, q, p.R);
@@ -193,8 +224,8 @@ SVA_DEV uint64_t entry_comp(bool valid, float score, int n) {
 
 // Scores up to 16 keys per pass (16 lanes each) and stores their entries.
 template <typename KeyAt>
-SVA_DEV void score_entries(const CandParams& p, int h, int count, KeyAt key_at, uint64_t* comp, uint8_t* flag,
-                           uint8_t extra_flag) {
+SVA_DEV void score_entries(const CandParams& p, int h, int item, int64_t r0, int count, KeyAt key_at, uint64_t* comp,
+                           uint8_t* flag, uint8_t extra_flag) {
   const int g = threadIdx.x >> 4;
   for (int b = 0; b < count; b += CT / 16) {
     const int i = b + g;
@@ -202,7 +233,7 @@ SVA_DEV void score_entries(const CandParams& p, int h, int count, KeyAt key_at, 
     int n = live ? key_at(i) : -1;
     const bool keep = n >= 0;  // key_at returns -1 for a slot left empty
     const int nn = keep ? n : 0;
-    const float sc = rank_score16(p, h, nn);
+    const float sc = rank_score16(p, h, item, r0, nn);
     if (live && (lane_id() & 15) == 0) {
       if (keep) {
         const bool ok = row_allowed(p, nn);
@@ -216,7 +247,8 @@ SVA_DEV void score_entries(const CandParams& p, int h, int count, KeyAt key_at, 
   }
 }
 
-// Whether row n's code falls in a chosen cell of one of the subspaces [0, s_end).
+// Whether key n's code falls in a chosen cell of one of the subspaces [0, s_end)
+// (code_base: the head's codes at the sequence's first row).
 SVA_DEV bool in_chosen_cells(const CandParams& p, const uint32_t* member, int64_t code_base, int n, int s_end) {
   for (int s = 0; s < s_end; ++s) {
     int64_t c = load_code(p.codes, code_base + (int64_t)n * p.S + s, p.ctype);
@@ -232,10 +264,12 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
   __shared__ int topc[kMaxSub * kMaxCells];
   __shared__ uint32_t member[kMaxSub * 8];  // bit c of subspace s: cell c chosen (C <= 256)
   __shared__ int lbase[kMaxSub * kMaxCells + 1];
-  const int h = blockIdx.y;
+  const int item = blockIdx.y;
+  const int h = item % p.H;
+  const ItemRows ir = item_rows(p, item / p.H);
   const int S = p.S, C = p.C, cells = p.cells;
   // top cells of every subspace: rank of each cell among its subspace
-  for (int e = threadIdx.x; e < S * C; e += CT) score[e] = p.lut[(int64_t)h * S * C + e] / p.sqrt_r;
+  for (int e = threadIdx.x; e < S * C; e += CT) score[e] = p.lut[(int64_t)item * S * C + e] / p.sqrt_r;
   for (int e = threadIdx.x; e < S * 8; e += CT) member[e] = 0u;
   for (int e = threadIdx.x; e < S * cells; e += CT) topc[e] = 0;  // NaN scores may leave ranks unfilled
   __syncthreads();
@@ -254,11 +288,12 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
   }
   __syncthreads();
   const int nlists = S * cells;
+  const int32_t* item_off = p.offsets + (int64_t)item * S * (C + 1);  // [S, C + 1] of this item
   if (threadIdx.x == 0) {
     int acc = 0;
     for (int j = 0; j < nlists; ++j) {
       const int s = j / cells;
-      const int32_t* off = p.offsets + ((int64_t)h * S + s) * (C + 1);
+      const int32_t* off = item_off + s * (C + 1);
       const int c = min(max(topc[j], 0), C - 1);
       lbase[j] = acc;
       acc += off[c + 1] - off[c];
@@ -266,24 +301,26 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
     lbase[nlists] = acc;
   }
   __syncthreads();
-  uint64_t* comp = p.comp + (int64_t)h * p.W;
-  uint8_t* flag = p.flag + (int64_t)h * p.W;
-  const int tail_len = max(0, p.k_len - p.tail_start);
-  const int tail_wgs = (tail_len + TAIL_ROWS - 1) / TAIL_ROWS;
+  uint64_t* comp = p.comp + (int64_t)item * p.W;
+  uint8_t* flag = p.flag + (int64_t)item * p.W;
+  const int tail_len = max(0, ir.k_len - ir.tail_start);
+  const int tail_wgs = (p.tail_cap + TAIL_ROWS - 1) / TAIL_ROWS;
   const int j = blockIdx.x;
-  // slots: [lists (S*postings_len at most)] [tail] [extra]
+  const int64_t cb = (int64_t)h * p.code_hs + ir.r0 * S;  // the head's codes at the sequence's first row
+  // slots: [lists (S * postings_len at most)] [tail (tail_cap)] [extra]
   const int tail_slot0 = S * p.postings_len;
-  const int extra_slot = tail_slot0 + tail_len;
+  const int extra_slot = p.W - 1;
   if (j < nlists) {
     const int s = j / cells;
-    const int32_t* off = p.offsets + ((int64_t)h * S + s) * (C + 1);
+    const int32_t* off = item_off + s * (C + 1);
     const int c = min(max(topc[j], 0), C - 1);
     const int o0 = off[c];
-    const int count = off[c + 1] - o0;
-    const int32_t* lst = p.ids + ((int64_t)h * S + s) * p.postings_len + o0;
-    const int64_t cb = (int64_t)h * p.code_hs;
+    // lists fill at most S * postings_len slots; the clamp keeps a batch whose
+    // lengths exceed the stated maxima inside its row of slots
+    const int count = max(0, min(off[c + 1] - o0, tail_slot0 - lbase[j]));
+    const int32_t* lst = p.ids + ((int64_t)h * S + s) * p.ids_rows + ir.r0 + o0;
     score_entries(
-        p, h, count,
+        p, h, item, ir.r0, count,
         [&](int i) {
           const int n = (int)lst[i];
           // adaptive: distinct keys, each kept by its lowest chosen subspace
@@ -293,36 +330,36 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
         comp + lbase[j], flag + lbase[j], 0);
   } else if (j < nlists + tail_wgs) {
     const int t0 = (j - nlists) * TAIL_ROWS;
-    const int count = min(TAIL_ROWS, tail_len - t0);
-    const int64_t cb = (int64_t)h * p.code_hs;
+    const int count = min(TAIL_ROWS, p.tail_cap - t0);  // slots past this item's tail are cleared
     score_entries(
-        p, h, count,
+        p, h, item, ir.r0, count,
         [&](int i) {
-          const int n = p.tail_start + t0 + i;
+          if (t0 + i >= tail_len) return -1;
+          const int n = ir.tail_start + t0 + i;
           if (!p.adaptive) return n;
           return in_chosen_cells(p, member, cb, n, S) ? n : -1;
         },
         comp + tail_slot0 + t0, flag + tail_slot0 + t0, 0);
   } else {
     // the extra slot, and clearing of list slots past the lists' total
-    for (int i = lbase[nlists] + (int)threadIdx.x; i < tail_slot0; i += CT) comp[i] = 0ull, flag[i] = 0;
+    for (int i = min(lbase[nlists], tail_slot0) + (int)threadIdx.x; i < tail_slot0; i += CT) comp[i] = 0ull, flag[i] = 0;
     int n = -1;
     uint8_t extra = 0;
     if (!p.adaptive) {
-      if (tail_len == 0) n = p.k_len - 1;
+      if (tail_len == 0) n = ir.k_len - 1;
     } else {
-      n = p.k_len - 1;
+      n = ir.k_len - 1;
       if (row_allowed(p, n)) {
         // the current row joins the candidates unless it is one already
-        if (in_chosen_cells(p, member, (int64_t)h * p.code_hs, n, S)) n = -1;
+        if (in_chosen_cells(p, member, cb, n, S)) n = -1;
       } else {
         // fallback: the last allowed row, used only when nothing else is
-        for (n = p.k_len - 1; n >= 0 && !row_allowed(p, n); --n) {
+        for (n = ir.k_len - 1; n >= 0 && !row_allowed(p, n); --n) {
         }
         extra = 2;
       }
     }
-    score_entries(p, h, 1, [&](int) { return n; }, comp + extra_slot, flag + extra_slot, extra);
+    score_entries(p, h, item, ir.r0, 1, [&](int) { return n; }, comp + extra_slot, flag + extra_slot, extra);
   }
 }
 
@@ -357,6 +394,14 @@ struct SelParams {
   float* sel_score;
   uint8_t* sel_valid;
   int sel_cap;
+  // ragged static batches: row b * H + h of sequence b; its budgets follow
+  // from B (the largest), amin / amid (0: the defaults) and klens[b] as in
+  // sva/llama.py:443-445, its tail is [plens[b], klens[b]), its postings
+  // maxima are max_count[b * n_max, (b + 1) * n_max).  NULL: the scalars.
+  const int64_t* plens;
+  const int64_t* klens;
+  int H;
+  int amin, amid;
 };
 
 SVA_DEV uint32_t hash_key(uint32_t n, int hash) { return (n * 2654435761u) & (uint32_t)(hash - 1); }
@@ -377,6 +422,19 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   const uint8_t* flag = p.flag + (int64_t)h * p.W;
   uint64_t* win = p.win + (int64_t)h * p.win_cap;
   const int W = p.W;
+  int Bi = p.B, min_b = p.min_budget, mid_b = p.mid_budget;
+  int64_t tail_extra = p.tail_extra;
+  const int32_t* mc = p.max_count;
+  if (p.klens != nullptr) {
+    const int b = h / p.H;
+    const int64_t kl = p.klens[b], pl = p.plens[b];
+    const int64_t cap = std::min<int64_t>(p.B, kl);
+    Bi = (int)cap;
+    min_b = (int)std::min<int64_t>(p.amin > 0 ? p.amin : p.B, cap);
+    mid_b = (int)std::min<int64_t>(p.amid > 0 ? p.amid : std::max<int64_t>(min_b, p.B / 2), cap);
+    tail_extra = kl - pl > 0 ? kl - pl : 1;
+    mc = p.max_count + (int64_t)b * p.n_max;
+  }
   // counts: real entries, valid entries
   uint32_t real = 0, nvalid = 0;
   for (int i = threadIdx.x; i < W; i += UB) {
@@ -393,12 +451,12 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
     // the reference's padded layout: S * cells lists of the largest cell's
     // length, then the tail (or the current row)
     int mb = 0;
-    for (int i = 0; i < p.n_max; ++i) mb = max(mb, (int)p.max_count[i]);
-    width = p.lists * (int64_t)max(1, mb) + p.tail_extra;
+    for (int i = 0; i < p.n_max; ++i) mb = max(mb, (int)mc[i]);
+    width = p.lists * (int64_t)max(1, mb) + tail_extra;
   }
   int64_t refill;
   if (p.mode == 1) refill = Real;
-  else refill = min(width, (int64_t)max(p.B, p.B * p.refill_factor));
+  else refill = min(width, (int64_t)max(Bi, Bi * p.refill_factor));
   auto visit_real = [&](auto&& f) {
     for (int i = threadIdx.x; i < W; i += UB) {
       const uint64_t c = comp[i];
@@ -482,7 +540,7 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   uint32_t U;
   block_excl_scan<UB>(ucount, scratch, &U);
   // rank count (selected slots) and the budget
-  const int64_t rank_count = p.mode == 1 ? min((int64_t)p.B, (int64_t)U) : min((int64_t)p.B, refill);
+  const int64_t rank_count = p.mode == 1 ? min((int64_t)Bi, (int64_t)U) : min((int64_t)Bi, refill);
   auto visit_u = [&](auto&& f) {
     for (int i = threadIdx.x; i < ndom; i += UB) {
       const uint64_t c = dom(i);
@@ -493,7 +551,7 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   if (p.mode != 2 && rank_count > 1) {
     // best and (min_budget)-th best scores of the selected slots; slots past
     // U hold the masked minimum
-    const int mref = (int)min((int64_t)p.min_budget, rank_count) - 1;
+    const int mref = (int)min((int64_t)min_b, rank_count) - 1;
     uint64_t best = 0ull;
     visit_u([&](uint64_t c) { best = c > best ? c : best; });
     for (int off = 1; off < WAVE; off <<= 1) {
@@ -525,10 +583,10 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
     const float margin = s0 - sref;
     if (p.mode == 1) {
       const double md = (double)margin;
-      budget = md >= p.high_d ? (int)min((int64_t)p.min_budget, rank_count)
-                              : (md >= p.low_d ? (int)min((int64_t)p.mid_budget, rank_count) : (int)rank_count);
+      budget = md >= p.high_d ? (int)min((int64_t)min_b, rank_count)
+                              : (md >= p.low_d ? (int)min((int64_t)mid_b, rank_count) : (int)rank_count);
     } else {
-      budget = margin >= p.high_f ? p.min_budget : (margin >= p.low_f ? p.mid_budget : p.B);
+      budget = margin >= p.high_f ? min_b : (margin >= p.low_f ? mid_b : Bi);
       budget = (int)min((int64_t)budget, rank_count);
     }
   } else if (p.mode == 0) {
@@ -676,7 +734,31 @@ extern "C" int sva_postings_build(const void* codes, int code_type, int64_t code
     return rc;
   const size_t lds = sizeof(uint32_t) * (size_t)(2 * C + PNW * C + PNW + 2);
   hipLaunchKernelGGL(postings_build_kernel, dim3((unsigned)(H * S)), dim3(PB), lds, (hipStream_t)stream, codes,
-                     code_type, code_head_stride, (int)S, (int)n_rows, (int)C, offsets, ids, max_count);
+                     code_type, code_head_stride, (int)H, (int)S, (int)n_rows, (int)C, nullptr, nullptr, n_rows,
+                     offsets, ids, max_count);
+  SVA_CHECK_LAUNCH("postings_build_kernel");
+  return SVA_OK;
+}
+
+extern "C" int sva_postings_build_ragged(const void* codes, int code_type, int64_t code_head_stride,
+                                         const int64_t* seq_offsets, const int64_t* postings_lens, int64_t n_seq,
+                                         int64_t H, int64_t rows, int64_t S, int64_t C, int32_t* offsets, int32_t* ids,
+                                         int32_t* max_count, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(codes && seq_offsets && postings_lens && offsets && ids && max_count,
+              "sva_postings_build_ragged: null pointer");
+  SVA_REQUIRE(n_seq > 0 && H > 0 && S > 0 && rows > 0 && rows < (1ll << 31) && n_seq * H * S < (1ll << 31),
+              "sva_postings_build_ragged: bad sizes");
+  SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_postings_build_ragged: bad code type");
+  SVA_UNSUPPORTED(C > 0 && C <= kMaxPostingCells, "sva_postings_build_ragged: %lld codewords (at most %d)",
+                  (long long)C, kMaxPostingCells);
+  static bool attr = false;
+  if (int rc = launch_attr_once((const void*)postings_build_kernel, attr, "hipFuncSetAttribute(postings_build)"))
+    return rc;
+  const size_t lds = sizeof(uint32_t) * (size_t)(2 * C + PNW * C + PNW + 2);
+  hipLaunchKernelGGL(postings_build_kernel, dim3((unsigned)(n_seq * H * S)), dim3(PB), lds, (hipStream_t)stream, codes,
+                     code_type, code_head_stride, (int)H, (int)S, 0, (int)C, seq_offsets, postings_lens, rows,
+                     offsets, ids, max_count);
   SVA_CHECK_LAUNCH("postings_build_kernel");
   return SVA_OK;
 }
@@ -732,10 +814,80 @@ extern "C" int sva_inverted_candidates(const float* lut, const float* q_low, con
   p.comp = comp;
   p.flag = flag;
   const int64_t tail_len = k_len - tail_start;
+  p.seq_offs = nullptr;
+  p.plens = nullptr;
+  p.klens = nullptr;
+  p.tail_cap = (int)tail_len;
+  p.ids_rows = postings_len;
   const int64_t wgs = S * cells + (tail_len + TAIL_ROWS - 1) / TAIL_ROWS + 1;
   SVA_REQUIRE(wgs < (1ll << 31) && slots < (1ll << 31), "sva_inverted_candidates: too many rows");
   hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)H), dim3(CT), 0, (hipStream_t)stream,
                      p);
+  SVA_CHECK_LAUNCH("inverted_candidates_kernel");
+  return SVA_OK;
+}
+
+extern "C" int64_t sva_inverted_slots_ragged(int64_t S, int64_t max_postings_len, int64_t max_tail) {
+  return S * max_postings_len + std::max<int64_t>(0, max_tail) + 1;
+}
+
+extern "C" int sva_inverted_candidates_ragged(const float* lut, const float* q_low, const float* k_low,
+                                              int64_t k_low_head_stride, const void* codes, int code_type,
+                                              int64_t code_head_stride, const int32_t* offsets, const int32_t* ids,
+                                              int64_t rows, const int64_t* seq_offsets, const int64_t* postings_lens,
+                                              const int64_t* k_lens, int64_t n_seq, int64_t max_postings_len,
+                                              int64_t max_tail, int64_t H, int64_t S, int64_t C, int64_t R,
+                                              int64_t cells, uint64_t* comp, uint8_t* flag, int64_t slots,
+                                              void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(lut && q_low && k_low && codes && offsets && ids && seq_offsets && postings_lens && k_lens && comp &&
+                  flag,
+              "sva_inverted_candidates_ragged: null pointer");
+  SVA_REQUIRE(n_seq > 0 && H > 0 && n_seq * H <= 65535 && rows > 0 && rows < (1ll << 31) && max_postings_len >= 0 &&
+                  max_postings_len <= rows && max_tail >= 0 && max_tail <= rows,
+              "sva_inverted_candidates_ragged: bad sizes");
+  SVA_UNSUPPORTED(R > 0 && R <= 511, "sva_inverted_candidates_ragged: rank %lld unsupported", (long long)R);
+  SVA_UNSUPPORTED(S > 0 && S <= kMaxSub && C > 0 && C <= 256 && cells > 0 && cells <= std::min<int64_t>(C, kMaxCells),
+                  "sva_inverted_candidates_ragged: layout %lldx%lld with %lld cells unsupported", (long long)S,
+                  (long long)C, (long long)cells);
+  SVA_REQUIRE(R != 64 || ((((uintptr_t)k_low | (uintptr_t)q_low) & 15u) == 0 && k_low_head_stride % 4 == 0),
+              "sva_inverted_candidates_ragged: k_low / q_low must be 16-byte aligned");
+  SVA_REQUIRE(slots == sva_inverted_slots_ragged(S, max_postings_len, max_tail),
+              "sva_inverted_candidates_ragged: slots must be sva_inverted_slots_ragged(...)");
+  CandParams p;
+  p.lut = lut;
+  p.q_low = q_low;
+  p.k_low = k_low;
+  p.klow_hs = k_low_head_stride;
+  p.codes = codes;
+  p.ctype = code_type;
+  p.code_hs = code_head_stride;
+  p.offsets = offsets;
+  p.ids = ids;
+  p.postings_len = (int)max_postings_len;
+  p.tail_start = 0;
+  p.k_len = 0;
+  p.H = (int)H;
+  p.S = (int)S;
+  p.C = (int)C;
+  p.R = (int)R;
+  p.cells = (int)cells;
+  p.sqrt_r = (float)std::sqrt((double)R);
+  p.mask = nullptr;
+  p.mask_type = 0;
+  p.adaptive = 0;
+  p.W = (int)slots;
+  p.comp = comp;
+  p.flag = flag;
+  p.seq_offs = seq_offsets;
+  p.plens = postings_lens;
+  p.klens = k_lens;
+  p.tail_cap = (int)max_tail;
+  p.ids_rows = rows;
+  const int64_t wgs = S * cells + (max_tail + TAIL_ROWS - 1) / TAIL_ROWS + 1;
+  SVA_REQUIRE(wgs < (1ll << 31) && slots < (1ll << 31), "sva_inverted_candidates_ragged: too many rows");
+  hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)(n_seq * H)), dim3(CT), 0,
+                     (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("inverted_candidates_kernel");
   return SVA_OK;
 }
@@ -791,6 +943,59 @@ extern "C" int sva_unique_refill_select(const uint64_t* comp, const uint8_t* fla
   p.stats = stats;
   p.sel_cap = 0;
   return launch_select(p, H, (hipStream_t)stream);
+}
+
+extern "C" int sva_unique_refill_select_ragged(const uint64_t* comp, const uint8_t* flag, int64_t slots, int64_t n_seq,
+                                               int64_t H, int64_t budget, int64_t adaptive_min_budget,
+                                               int64_t adaptive_mid_budget, double low_margin, double high_margin,
+                                               int64_t refill_factor, const int32_t* max_count, int64_t S,
+                                               int64_t cells, const int64_t* postings_lens, const int64_t* k_lens,
+                                               int32_t* fin_idx, int32_t* fin_count, float* stats, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(comp && flag && max_count && postings_lens && k_lens && fin_idx && fin_count && stats && workspace,
+              "sva_unique_refill_select_ragged: null pointer");
+  SVA_REQUIRE(n_seq > 0 && H > 0 && n_seq * H < (1ll << 31) && slots > 0 && slots < (1ll << 31) && budget > 0 &&
+                  adaptive_min_budget >= 0 && adaptive_mid_budget >= 0 && refill_factor >= 1 && S > 0 && cells > 0,
+              "sva_unique_refill_select_ragged: bad sizes");
+  const int win_cap = win_cap_for(budget, (int)refill_factor, slots);
+  const int hash = hash_slots(win_cap);
+  const size_t lds = select_lds_bytes(budget, hash);
+  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_unique_refill_select_ragged: budget %lld needs %zu bytes of LDS",
+                  (long long)budget, lds);
+  SVA_REQUIRE(workspace_bytes >= sva_unique_select_workspace_bytes(n_seq * H, budget, refill_factor, slots),
+              "sva_unique_refill_select_ragged: workspace too small");
+  SelParams p{};
+  p.comp = comp;
+  p.flag = flag;
+  p.W = (int)slots;
+  p.mode = 0;
+  p.B = (int)budget;
+  p.min_budget = (int)budget;
+  p.mid_budget = (int)budget;
+  p.low_f = (float)low_margin;
+  p.high_f = (float)high_margin;
+  p.low_d = low_margin;
+  p.high_d = high_margin;
+  p.width = slots;
+  p.max_count = max_count;
+  p.n_max = (int)(H * S);
+  p.lists = S * cells;
+  p.tail_extra = 1;
+  p.refill_factor = (int)refill_factor;
+  p.win_cap = win_cap;
+  p.hash = hash;
+  p.win = (uint64_t*)workspace;
+  p.fin_idx = fin_idx;
+  p.fin_count = fin_count;
+  p.stats = stats;
+  p.sel_cap = 0;
+  p.plens = postings_lens;
+  p.klens = k_lens;
+  p.H = (int)H;
+  p.amin = (int)std::min<int64_t>(adaptive_min_budget, budget);
+  p.amid = (int)std::min<int64_t>(adaptive_mid_budget, budget);
+  return launch_select(p, n_seq * H, (hipStream_t)stream);
 }
 
 extern "C" size_t sva_top_unique_workspace_bytes(int64_t H, int64_t W, int64_t budget, int64_t refill_factor) {

@@ -173,3 +173,84 @@ def adaptive_decode(module, query, keys, values, k_low, codes, k_len: int, mask,
 
     return _decode(module, query, keys, values, k_low, codes, k_len, mask, budget, True, return_selection)
 
+
+
+@dataclass
+class RaggedPostings:
+    """CSR postings of every sequence of a packed batch: sequence b's first
+    ``postings_lens[b]`` keys."""
+
+    offsets: torch.Tensor        # [n_seq, H, S, C + 1] int32
+    ids: torch.Tensor            # [H, S, rows] int32: sequence b's local ids at its packed rows
+    max_count: torch.Tensor      # [n_seq, H, S] int32
+    postings_lens: torch.Tensor  # [n_seq] int64
+    max_len: int                 # the largest postings length
+
+
+def build_postings_ragged(codes: torch.Tensor, seq_offsets: torch.Tensor, postings_lens: torch.Tensor,
+                          max_len: int, codewords: int) -> RaggedPostings:
+    """sva/llama.py:626-657 for every sequence of a packed batch at once:
+    codes [H, rows, S] packed; seq_offsets / postings_lens int64 [n_seq] on
+    the device; max_len the largest of postings_lens."""
+
+    heads, rows, subspaces = codes.shape
+    n_seq = int(seq_offsets.numel())
+    device = require_device(codes, seq_offsets, postings_lens)
+    offsets = torch.empty(n_seq, heads, subspaces, codewords + 1, device=device, dtype=torch.int32)
+    ids = torch.empty(heads, subspaces, rows, device=device, dtype=torch.int32)
+    max_count = torch.empty(n_seq, heads, subspaces, device=device, dtype=torch.int32)
+    check(lib().sva_postings_build_ragged(ptr(codes), code_type(codes), codes.stride(0), ptr(seq_offsets),
+                                          ptr(postings_lens), n_seq, heads, rows, subspaces, codewords, ptr(offsets),
+                                          ptr(ids), ptr(max_count), stream_handle(device)),
+          "sva_postings_build_ragged")
+    return RaggedPostings(offsets, ids, max_count, postings_lens, int(max_len))
+
+
+def ragged_static_decode(query, q_proj, scale, codebooks, keys, values, k_low, codes, seq_offsets, k_lens,
+                         postings: RaggedPostings, max_tail: int, budget: int, cells: int, scaling: float,
+                         adaptive_min: int | None = None, adaptive_mid: int | None = None, low_margin: float = 0.35,
+                         high_margin: float = 0.70, return_selection: bool = False):
+    """_inverted_static_decode_attention (sva/llama.py:427-576) for one decode
+    token of every sequence of a packed batch, in four launches (query LUT,
+    candidates, selection, verifier) whatever the batch size.
+
+    query [n_seq, H, 1, D]; keys / values [G, rows, D], k_low [H, rows, R] and
+    codes [H, rows, S] packed, sequence b at rows [seq_offsets[b],
+    seq_offsets[b] + k_lens[b]); max_tail >= every k_lens[b] -
+    postings_lens[b].  Returns out [n_seq, H, 1, D] (and, with
+    return_selection, fin_idx / fin_count / stats per item b * H + h, keys
+    local to their sequence)."""
+
+    n_seq, heads, q_len, head_dim = query.shape
+    if q_len != 1:
+        raise ValueError("ragged static decode takes one token per sequence")
+    subspaces, codewords = int(codebooks.shape[1]), int(codebooks.shape[2])
+    rank = int(q_proj.shape[-1])
+    rows = int(codes.shape[1])
+    device = require_device(query, keys, values, k_low, codes, seq_offsets, k_lens)
+    cells = min(cells, codewords)
+    q_low, lut, _ = kernels.query_lut(query, q_proj, scale, codebooks)
+    L = lib()
+    slots = int(L.sva_inverted_slots_ragged(subspaces, postings.max_len, max_tail))
+    items = n_seq * heads
+    comp = torch.empty(items, slots, device=device, dtype=torch.int64)
+    flag = torch.empty(items, slots, device=device, dtype=torch.uint8)
+    stream = stream_handle(device)
+    check(L.sva_inverted_candidates_ragged(
+        ptr(lut), ptr(q_low), ptr(k_low), k_low.stride(0), ptr(codes), code_type(codes), codes.stride(0),
+        ptr(postings.offsets), ptr(postings.ids), rows, ptr(seq_offsets), ptr(postings.postings_lens), ptr(k_lens),
+        n_seq, postings.max_len, max_tail, heads, subspaces, codewords, rank, cells, ptr(comp), ptr(flag), slots,
+        stream), "sva_inverted_candidates_ragged")
+    fin_idx = torch.empty(items, budget, device=device, dtype=torch.int32)
+    fin_count = torch.empty(items, device=device, dtype=torch.int32)
+    stats = torch.empty(items, 4, device=device, dtype=torch.float32)
+    ws = kernels.workspace(device, int(L.sva_unique_select_workspace_bytes(items, budget, 2, slots)), "inverted")
+    check(L.sva_unique_refill_select_ragged(
+        ptr(comp), ptr(flag), slots, n_seq, heads, budget, adaptive_min or 0, adaptive_mid or 0, float(low_margin),
+        float(high_margin), 2, ptr(postings.max_count), subspaces, cells, ptr(postings.postings_lens), ptr(k_lens),
+        ptr(fin_idx), ptr(fin_count), ptr(stats), ptr(ws), ws.numel(), stream), "sva_unique_refill_select_ragged")
+    out = kernels.verify(query, keys, values, fin_idx, fin_count, rows, scaling, out_dtype=query.dtype,
+                         seq_offsets=seq_offsets, seq_lens=k_lens)
+    if return_selection:
+        return out, fin_idx, fin_count, stats
+    return out

@@ -4,8 +4,11 @@ Postings (CSR) equal the oracle's exactly; the unique refill selection
 reproduces the reference's known-answer test and brute force; static and
 adaptive decode give the oracle's chosen key sets per head (bit-exact index
 sets: same LUT, same rank scores, rule score desc / key asc), its
-statistics, and outputs within 1e-5 of its float64 verifier.  Catalog inputs
-(k_low, codes) come from sva_write_encode, whose parity is tested on its own.
+statistics, and outputs within 1e-5 of its float64 verifier.  A ragged
+batch of packed sequences (static mode, one launch per stage) gives, for
+each sequence, what the oracle gives on that sequence's rows alone.  Catalog
+inputs (k_low, codes) come from sva_write_encode, whose parity is tested on
+its own.
 """
 
 from __future__ import annotations
@@ -193,3 +196,81 @@ def test_adaptive_decode_fallback_to_last_allowed_row(device):
     ref = oracle.inverted_decode(cat.q[0], cat.keys, cat.values, ql, cat.k_low, cat.cb, cat.codes, 16, 2,
                                  cat.D ** -0.5, allowed=allowed)
     _check_decode(cat, res, ref)
+
+
+# ---------------------------------------------------------------------------
+# ragged static decode: packed sequences, one launch per stage, each sequence
+# against the batch-1 oracle on its own rows
+
+def _ragged_catalog(device, lens, H=9, G=3, D=64, R=64, S=2, C=256, seed=0):
+    from sva_amd import kernels
+
+    rng = np.random.default_rng(seed)
+    rows = int(sum(lens))
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    keys = rng.standard_normal((G, rows, D)).astype(np.float32)
+    values = rng.standard_normal((G, rows, D)).astype(np.float32)
+    q = rng.standard_normal((len(lens), H, 1, D)).astype(np.float32)
+    k_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    q_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    scale = np.ones(H, np.float32)
+    cb = rng.standard_normal((H, S, C, R // S)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    k_low = torch.empty(H, rows, R, device=device)
+    codes = torch.empty(H, rows, S, device=device, dtype=torch.uint8)
+    kernels.write_encode(t(keys), t(k_proj), t(cb), k_low, codes)
+    torch.cuda.synchronize()
+    return SimpleNamespace(keys=keys, values=values, q=q, q_proj=q_proj, scale=scale, cb=cb, k_low_t=k_low,
+                           codes_t=codes, k_low=k_low.cpu().numpy(), codes=codes.cpu().numpy(), t=t, H=H, S=S, C=C,
+                           D=D, offs=offs, lens=np.asarray(lens, np.int64), rows=rows)
+
+
+RAGGED_LENS = [3000, 700, 5200, 1500, 130]
+RAGGED_TAILS = [0, 10, 37, 1, 64]
+
+
+def test_ragged_postings_match_oracle(device):
+    from sva_amd import inverted
+
+    cat = _ragged_catalog(device, RAGGED_LENS, seed=21)
+    plens = cat.lens - np.asarray(RAGGED_TAILS)
+    post = inverted.build_postings_ragged(cat.codes_t, cat.t(cat.offs), cat.t(plens), int(plens.max()), cat.C)
+    offsets, ids, mc = post.offsets.cpu().numpy(), post.ids.cpu().numpy(), post.max_count.cpu().numpy()
+    for b, (r0, pl) in enumerate(zip(cat.offs, plens)):
+        counts, e_off, e_ids = oracle.rebuild_postings(cat.codes[:, r0:r0 + pl], cat.C)
+        np.testing.assert_array_equal(offsets[b], e_off, err_msg=f"sequence {b}")
+        np.testing.assert_array_equal(ids[:, :, r0:r0 + pl], e_ids, err_msg=f"sequence {b}")
+        np.testing.assert_array_equal(mc[b], counts.max(-1), err_msg=f"sequence {b}")
+
+
+@pytest.mark.parametrize("amin,amid,budget", [(None, None, 128), (16, 48, 128), (None, None, 1000)])
+def test_ragged_static_decode_matches_oracle(device, amin, amid, budget):
+    # budget 1000 exceeds the 130-key sequence: its budgets clamp to its length
+    from sva_amd import inverted
+
+    cat = _ragged_catalog(device, RAGGED_LENS, seed=budget + (amin or 0))
+    cells = 8
+    plens = cat.lens - np.asarray(RAGGED_TAILS)
+    post = inverted.build_postings_ragged(cat.codes_t, cat.t(cat.offs), cat.t(plens), int(plens.max()), cat.C)
+    out, fin_idx, fin_count, stats = inverted.ragged_static_decode(
+        cat.t(cat.q), cat.t(cat.q_proj), cat.t(cat.scale), cat.t(cat.cb), cat.t(cat.keys), cat.t(cat.values),
+        cat.k_low_t, cat.codes_t, cat.t(cat.offs), cat.t(cat.lens), post, int(max(RAGGED_TAILS)), budget, cells,
+        cat.D ** -0.5, adaptive_min=amin, adaptive_mid=amid, return_selection=True)
+    out = out[:, :, 0].float().cpu().numpy()
+    fin_idx, fin_count, stats = fin_idx.cpu().numpy(), fin_count.cpu().numpy(), stats.cpu().numpy()
+    for b, (r0, n, pl) in enumerate(zip(cat.offs, cat.lens, plens)):
+        sl = slice(r0, r0 + n)
+        ql = oracle.query_low(cat.q[b], cat.q_proj, cat.scale)
+        ref = oracle.static_decode(cat.q[b], cat.keys[:, sl], cat.values[:, sl], ql, cat.k_low[:, sl], cat.cb,
+                                   oracle.rebuild_postings(cat.codes[:, r0:r0 + pl], cat.C), int(pl), budget, cells,
+                                   cat.D ** -0.5, adaptive_min=amin, adaptive_mid=amid)
+        items = slice(b * cat.H, (b + 1) * cat.H)
+        for h in range(cat.H):
+            it = b * cat.H + h
+            want = np.sort(ref["heads"][h]["final"])
+            np.testing.assert_array_equal(fin_idx[it, : fin_count[it]], want, err_msg=f"sequence {b} head {h}")
+            err = np.abs(out[b, h] - ref["out"][h]).max() / max(np.abs(ref["out"][h]).max(), 1e-30)
+            assert err <= 1e-5, f"sequence {b} head {h}: rel err {err}"
+        assert float(stats[items, 0].sum()) == ref["stats"]["summoned"], f"sequence {b}"
+        assert float(fin_count[items].sum()) == ref["stats"]["verified"], f"sequence {b}"
+        assert float(stats[items, 1].sum()) == ref["stats"]["refill_pool"], f"sequence {b}"
