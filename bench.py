@@ -49,9 +49,13 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
-    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model"),
+    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged"),
                     help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA; "
-                         "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched")
+                         "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched; "
+                         "ragged: continuous-batch static inverted decode over packed sequences")
+    ap.add_argument("--batch", type=int, default=32, help="ragged suite: sequences per batch")
+    ap.add_argument("--pool", type=int, default=48, help="ragged suite: resident sequences batches are drawn from")
+    ap.add_argument("--reshuffle", type=int, default=16, help="ragged suite: steps between batch reshuffles")
     ap.add_argument("--prefill", type=int, default=8192, help="model suite: prompt tokens")
     ap.add_argument("--decode-steps", type=int, default=256, help="model suite: timed greedy decode steps")
     ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
@@ -263,6 +267,102 @@ def write_suite(args):
     }), flush=True)
 
 
+def ragged_suite(args):
+    """Continuous-batch decode over packed sequences: a pool of --pool resident
+    sequences (cache lengths log-uniform in [4096, 131072], 9 q-heads / 3 KV
+    heads, head_dim 64, rank 64, 2x256 codes from sva_write_encode, static
+    postings over all but a tail of up to 63 rows); every --reshuffle steps a
+    new batch of --batch sequences is drawn and its offsets / lengths /
+    postings gathered on the device; each step is one decode lookup of every
+    sequence of the batch (query LUT, inverted candidates, unique refill
+    selection with budget 128 and 8 cells, GQA verifier), four launches
+    whatever the batch size."""
+
+    import numpy as np
+    import torch
+
+    from sva_amd import inverted, kernels
+
+    device = torch.device("cuda:0")
+    heads, kv_heads, d, r, subspaces, codewords = 9, 3, 64, 64, 2, 256
+    budget, cells = 128, 8
+    rng = np.random.default_rng(args.seed)
+    lens = np.exp(rng.uniform(np.log(4096), np.log(131072), args.pool)).astype(np.int64)
+    tails = rng.integers(0, 64, args.pool).astype(np.int64)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    rows = int(lens.sum())
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    keys = torch.randn(kv_heads, rows, d, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(kv_heads, rows, d, device=device, generator=g).to(torch.bfloat16)
+    k_proj = torch.randn(heads, d, r, device=device, generator=g) / 8.0
+    q_proj = torch.randn(heads, d, r, device=device, generator=g) / 8.0
+    scale = torch.ones(heads, device=device)
+    cb = torch.randn(heads, subspaces, codewords, r // subspaces, device=device, generator=g)
+    k_low = torch.empty(heads, rows, r, device=device)
+    codes = torch.empty(heads, rows, subspaces, device=device, dtype=torch.uint8)
+    kernels.write_encode(keys, k_proj, cb, k_low, codes)
+    q_pool = torch.randn(args.pool, heads, 1, d, device=device, generator=g).to(torch.bfloat16)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    offs_t, lens_t, plens_t = t(offs), t(lens), t(lens - tails)
+    pool_post = inverted.build_postings_ragged(codes, offs_t, plens_t, int((lens - tails).max()), codewords)
+    torch.cuda.synchronize()
+
+    def draw(step):
+        pick = np.sort(np.random.default_rng(args.seed + 1 + step).choice(args.pool, args.batch, replace=False))
+        idx = t(pick)
+        post = inverted.RaggedPostings(pool_post.offsets.index_select(0, idx), pool_post.ids,
+                                       pool_post.max_count.index_select(0, idx), plens_t.index_select(0, idx),
+                                       int((lens - tails)[pick].max()))
+        return (q_pool.index_select(0, idx), offs_t.index_select(0, idx), lens_t.index_select(0, idx), post,
+                int(tails[pick].max()), pick)
+
+    def run(step, batch):
+        q, so, kl, post, max_tail, _ = batch
+        return inverted.ragged_static_decode(q, q_proj, scale, cb, keys, values, k_low, codes, so, kl, post, max_tail,
+                                             budget, cells, d ** -0.5)
+
+    batch = draw(0)
+    for i in range(args.warmup):
+        if i % args.reshuffle == 0:
+            batch = draw(i)
+        run(i, batch)
+    torch.cuda.synchronize()
+    steps = args.steps
+    keys_seen = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if i % args.reshuffle == 0:
+            batch = draw(args.warmup + i)
+            keys_seen += int(lens[batch[5]].sum()) * args.reshuffle
+        run(i, batch)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us_step = 1e6 * wall / steps
+    # GPU time of one step (events around the four launches of a fixed batch)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_ev = min(steps, 100)
+    torch.cuda._sleep(int(2e8))
+    e0.record()
+    for i in range(n_ev):
+        run(i, batch)
+    e1.record()
+    torch.cuda.synchronize()
+    gpu_us = 1e3 * e0.elapsed_time(e1) / n_ev
+    print(json.dumps({
+        "metric": "ragged continuous-batch decode step (static inverted, 512/128 class budget 128)",
+        "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1e3, 4), "higher_is_better": False, "dtype": "fp32 scores / bf16 K,V",
+        "data": "synthetic (seeded N(0,1) caches, codes from sva_write_encode)",
+        "config": {"workload": f"{args.batch} of {args.pool} packed sequences, cache lengths log-uniform in "
+                               f"[4096, 131072], 2x256 codes, cells 8, budget 128, reshuffled every "
+                               f"{args.reshuffle} steps", "q_heads": heads, "kv_heads": kv_heads, "head_dim": d},
+        "sequences_per_s": round(args.batch / (us_step * 1e-6), 1),
+        "gpu_us_per_step": round(gpu_us, 2),
+        "mean_keys_per_sequence": round(keys_seen / (steps * args.batch), 1),
+    }), flush=True)
+
+
 def model_suite(args):
     """Decode tokens/s of a SmolLM2-135M-architecture decoder (random init,
     bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64, RoPE theta 1e5)
@@ -342,10 +442,10 @@ def main():
     if args.write_profiles:
         write_profiles(args)
         return
-    if args.suite in ("write", "model"):
+    if args.suite in ("write", "model", "ragged"):
         if args.gpus != 1:
             sys.exit(2)
-        (write_suite if args.suite == "write" else model_suite)(args)
+        {"write": write_suite, "model": model_suite, "ragged": ragged_suite}[args.suite](args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "

@@ -269,23 +269,28 @@ int64_t sva_inverted_slots_ragged(int64_t S, int64_t max_postings_len, int64_t m
 /*
  * Candidates of every item (sva_inverted_candidates, static mode, per
  * sequence): lut [n_seq, H, S, C] and q_low [n_seq, H, R] from sva_query_lut
- * (one token per sequence); comp / flag [n_seq * H, slots].
+ * (one token per sequence); comp / flag [n_seq * H, slots]: the item's list
+ * entries in slots [0, list_counts[item]) (later list slots are not
+ * written), its tail from slot S * max_postings_len, the extra slot last.
  * max_postings_len >= every postings_lens[b], max_tail >= every
  * k_lens[b] - postings_lens[b] (larger lists or tails are cut at the slots).
+ * R = 64, n_seq * H <= 8192.  Two launches: lists per item, then the
+ * scoring of every item's live slots spread evenly over the CUs.
  */
 int sva_inverted_candidates_ragged(const float *lut, const float *q_low, const float *k_low,
                                    int64_t k_low_head_stride, const void *codes, int code_type,
                                    int64_t code_head_stride, const int32_t *offsets, const int32_t *ids, int64_t rows,
                                    const int64_t *seq_offsets, const int64_t *postings_lens, const int64_t *k_lens,
                                    int64_t n_seq, int64_t max_postings_len, int64_t max_tail, int64_t H, int64_t S,
-                                   int64_t C, int64_t R, int64_t cells, uint64_t *comp, uint8_t *flag, int64_t slots,
-                                   void *stream);
+                                   int64_t C, int64_t R, int64_t cells, uint64_t *comp, uint8_t *flag,
+                                   int32_t *list_counts, int64_t slots, void *stream);
 
 /*
  * Static-mode selection of every item (sva_unique_refill_select, mode 0):
  * sequence b's budgets are min(budget, k_lens[b]) and the adaptive minimum
  * and middle budgets derived from it as in sva/llama.py:443-445 (0: the
  * reference's defaults); its refill width uses its own largest cell and tail.
+ * Only the slots sva_inverted_candidates_ragged wrote are read (list_counts).
  *   fin_idx [n_seq * H, budget] ascending local keys, fin_count, stats [.., 4]
  * workspace: sva_unique_select_workspace_bytes(n_seq * H, budget, refill_factor, slots).
  */
@@ -293,9 +298,9 @@ int sva_unique_refill_select_ragged(const uint64_t *comp, const uint8_t *flag, i
                                     int64_t H, int64_t budget, int64_t adaptive_min_budget,
                                     int64_t adaptive_mid_budget, double low_margin, double high_margin,
                                     int64_t refill_factor, const int32_t *max_count, int64_t S, int64_t cells,
-                                    const int64_t *postings_lens, const int64_t *k_lens, int32_t *fin_idx,
-                                    int32_t *fin_count, float *stats, void *workspace, size_t workspace_bytes,
-                                    void *stream);
+                                    const int64_t *postings_lens, const int64_t *k_lens, const int32_t *list_counts,
+                                    int64_t max_postings_len, int32_t *fin_idx, int32_t *fin_count, float *stats,
+                                    void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Unique refill selection over arbitrary rows of candidates

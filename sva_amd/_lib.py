@@ -52,10 +52,10 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
     "sva_postings_build_ragged": (_I, [_P, _I, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "sva_inverted_slots_ragged": (_I64, [_I64, _I64, _I64]),
     "sva_inverted_candidates_ragged": (_I, [_P, _P, _P, _I64, _P, _I, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64,
-                                            _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
+                                            _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "sva_unique_refill_select_ragged": (_I, [_P, _P, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_double,
-                                             ctypes.c_double, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _SZ,
-                                             _P]),
+                                             ctypes.c_double, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P,
+                                             _P, _SZ, _P]),
     "sva_top_unique_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "sva_top_unique": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "sva_verify": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,

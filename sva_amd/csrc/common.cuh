@@ -153,6 +153,55 @@ SVA_DEV uint32_t wave_sum_dpp(uint32_t v) {
          (uint32_t)__builtin_amdgcn_readlane((int)v, 47) + (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Row shift within each 16-lane DPP row: lane j receives lane j + N of its
+// row (lanes past the row end receive 0).
+template <int N>
+SVA_DEV float row_down(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
+}
+
+// Rank score of a 64-float k_low row in torch's sum order, computed by the
+// 16 lanes of one DPP row (lane j holds float4 j of the row in r and of the
+// query in qq): element e < 32 pairs with e + 32, the lane chains g, g+2,
+// g+4, g+6 form accumulator lane 4g + c, then the eight in order, as in
+// torch_order_dot64.  The result is valid in the row's first lane.
+SVA_DEV float rank_dot64_row16(const float4 r, const float4 qq) {
+#pragma clang fp contract(off)
+  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
+  const float a0 = (0.0f + p0) + row_down<8>(p0);
+  const float a1 = (0.0f + p1) + row_down<8>(p1);
+  const float a2 = (0.0f + p2) + row_down<8>(p2);
+  const float a3 = (0.0f + p3) + row_down<8>(p3);
+  const float v0 = ((a0 + row_down<2>(a0)) + row_down<4>(a0)) + row_down<6>(a0);
+  const float v1 = ((a1 + row_down<2>(a1)) + row_down<4>(a1)) + row_down<6>(a1);
+  const float v2 = ((a2 + row_down<2>(a2)) + row_down<4>(a2)) + row_down<6>(a2);
+  const float v3 = ((a3 + row_down<2>(a3)) + row_down<4>(a3)) + row_down<6>(a3);
+  const float w0 = row_down<1>(v0), w1 = row_down<1>(v1), w2 = row_down<1>(v2), w3 = row_down<1>(v3);
+  return (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
+}
+
+// Maximum of a uint64 over the wave (all 64 lanes active), wave-uniform:
+// DPP row shifts of both halves from the same source lane, then the four
+// row maxima.
+SVA_DEV uint64_t wave_max_u64(uint64_t x) {
+  auto step = [](uint64_t v, uint32_t lo, uint32_t hi) {
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    return o > v ? o : v;
+  };
+  x = step(x, row_shr_keep<1>((uint32_t)x), row_shr_keep<1>((uint32_t)(x >> 32)));
+  x = step(x, row_shr_keep<2>((uint32_t)x), row_shr_keep<2>((uint32_t)(x >> 32)));
+  x = step(x, row_shr_keep<4>((uint32_t)x), row_shr_keep<4>((uint32_t)(x >> 32)));
+  x = step(x, row_shr_keep<8>((uint32_t)x), row_shr_keep<8>((uint32_t)(x >> 32)));
+  uint64_t m = 0ull;
+#pragma unroll
+  for (int r = 15; r < WAVE; r += 16) {
+    const uint64_t v = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), r) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, r);
+    m = v > m ? v : m;
+  }
+  return m;
+}
+
 // Minimum and maximum of a uint32 over the wave (all 64 lanes active), wave-uniform.
 SVA_DEV void wave_min_max_u32(uint32_t& mn, uint32_t& mx) {
   mn = min(mn, row_shr_keep<1>(mn));
@@ -268,6 +317,73 @@ SVA_DEV uint64_t select_largest_with_bounds(Visit visit, int k, uint64_t vor, ui
       shared[0] = 255u - threadIdx.x;
       shared[1] = above;
       shared[2] = tot;
+    }
+    __syncthreads();
+    const uint32_t b = shared[0];
+    need -= (int)shared[1];
+    prefix |= (uint64_t)b << shift;
+    pmask |= (uint64_t)dmask << shift;
+    const bool done = shared[2] == (uint32_t)need || shift == 0;
+    __syncthreads();
+    if (done) return prefix;
+    top = shift - 1;
+  }
+}
+
+// select_largest_with_bounds with 12-bit digits over one shared 4096-bin
+// LDS histogram (hist, 4096 uint32, 4-byte aligned; BLOCK = 1024): two
+// passes where the 8-bit form needs three or four on wide value ranges.
+template <int BLOCK, typename Visit>
+SVA_DEV uint64_t select_largest12(Visit visit, int k, uint64_t vor, uint64_t vand, uint32_t* hist, uint32_t* scratch,
+                                  uint64_t* shared64, uint32_t* shared) {
+  static_assert(BLOCK == 1024, "4 bins per thread");
+  for (int off = 1; off < WAVE; off <<= 1) {
+    vor |= __shfl_xor(vor, off, WAVE);
+    vand &= __shfl_xor(vand, off, WAVE);
+  }
+  if (threadIdx.x == 0) {
+    shared64[0] = 0ull;
+    shared64[1] = ~0ull;
+  }
+  __syncthreads();
+  if (lane_id() == 0) {
+    atomicOr((unsigned long long*)&shared64[0], (unsigned long long)vor);
+    atomicAnd((unsigned long long*)&shared64[1], (unsigned long long)vand);
+  }
+  __syncthreads();
+  const uint64_t diff = shared64[0] ^ shared64[1];
+  if (diff == 0ull) return shared64[0];  // a single element
+  int top = 63 - __clzll((long long)diff);
+  uint64_t pmask = top == 63 ? 0ull : ~0ull << (top + 1);
+  uint64_t prefix = shared64[1] & pmask;
+  int need = k;
+  while (true) {
+    const int shift = max(top - 11, 0);
+    const uint32_t dmask = (1u << (top - shift + 1)) - 1u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hist[4 * threadIdx.x + j] = 0u;  // 4-byte aligned words (hist need not be 16)
+    __syncthreads();
+    visit([&](uint64_t x) {
+      if ((x & pmask) == prefix) atomicAdd(&hist[(uint32_t)(x >> shift) & dmask], 1u);
+    });
+    __syncthreads();
+    // thread t owns bins 4095 - 4t .. 4092 - 4t, from the top
+    const uint32_t* hq = hist + 4 * (BLOCK - 1 - threadIdx.x);
+    const uint4 hb = uint4{hq[0], hq[1], hq[2], hq[3]};
+    uint32_t total;
+    const uint32_t above = block_excl_scan<BLOCK>(hb.x + hb.y + hb.z + hb.w, scratch, &total);
+    {
+      const uint32_t c[4] = {hb.w, hb.z, hb.y, hb.x};
+      uint32_t a = above;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (a < (uint32_t)need && a + c[j] >= (uint32_t)need) {
+          shared[0] = 4095u - 4u * threadIdx.x - (uint32_t)j;
+          shared[1] = a;
+          shared[2] = c[j];
+        }
+        a += c[j];
+      }
     }
     __syncthreads();
     const uint32_t b = shared[0];

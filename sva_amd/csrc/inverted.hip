@@ -136,6 +136,7 @@ __global__ void __launch_bounds__(PB)
 
 constexpr int CT = 256;          // threads per candidate workgroup
 constexpr int TAIL_ROWS = 256;   // tail rows per workgroup
+constexpr int SCORE_U = 4;       // entries in flight per 16-lane group while scoring
 constexpr int kMaxCells = 64;
 constexpr int kMaxSub = 16;
 
@@ -169,6 +170,7 @@ struct CandParams {
   const int64_t* klens;
   int tail_cap;
   int64_t ids_rows;  // row dimension of ids: [H, S, ids_rows]
+  int32_t* nlist;    // ragged: [items] list entries of each item (list slots past them are left as they are)
 };
 
 SVA_DEV bool row_allowed(const CandParams& p, int n) {
@@ -222,28 +224,57 @@ SVA_DEV uint64_t entry_comp(bool valid, float score, int n) {
   return composite(f2key(valid ? score : -FLT_MAX), (uint32_t)n);
 }
 
-// Scores up to 16 keys per pass (16 lanes each) and stores their entries.
+// Scores the entries [0, count) (16 lanes per entry, 4 entries per lane
+// group in flight) and stores them; key_at(i) gives entry i's key, or -1 for
+// a slot left empty.
 template <typename KeyAt>
 SVA_DEV void score_entries(const CandParams& p, int h, int item, int64_t r0, int count, KeyAt key_at, uint64_t* comp,
                            uint8_t* flag, uint8_t extra_flag) {
+#pragma clang fp contract(off)
+  constexpr int GROUPS = CT / 16;
+  constexpr int U = SCORE_U;
   const int g = threadIdx.x >> 4;
-  for (int b = 0; b < count; b += CT / 16) {
-    const int i = b + g;
-    const bool live = i < count;
-    int n = live ? key_at(i) : -1;
-    const bool keep = n >= 0;  // key_at returns -1 for a slot left empty
-    const int nn = keep ? n : 0;
-    const float sc = rank_score16(p, h, item, r0, nn);
-    if (live && (lane_id() & 15) == 0) {
-      if (keep) {
-        const bool ok = row_allowed(p, nn);
-        comp[i] = entry_comp(ok, sc, nn);
-        flag[i] = (uint8_t)((ok ? 1 : 0) | extra_flag);
-      } else {
-        comp[i] = 0ull;
-        flag[i] = 0;
+  const int j = lane_id() & 15;
+  auto store = [&](int i, int n, float sc) {
+    if (n >= 0) {
+      const bool ok = row_allowed(p, n);
+      comp[i] = entry_comp(ok, sc, n);
+      flag[i] = (uint8_t)((ok ? 1 : 0) | extra_flag);
+    } else {
+      comp[i] = 0ull;
+      flag[i] = 0;
+    }
+  };
+  if (p.R == 64) {
+    const float* klow = p.k_low + (int64_t)h * p.klow_hs;
+    const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * 64)[j];
+    for (int b0 = 0; b0 < count; b0 += GROUPS * U) {
+      int n[U];
+      float4 rv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = b0 + g + u * GROUPS;
+        n[u] = i < count ? key_at(i) : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        rv[u] = n[u] >= 0 ? reinterpret_cast<const float4*>(klow + (r0 + n[u]) * 64)[j]
+                          : float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float dot = rank_dot64_row16(rv[u], qq);  // valid in the row's first lane
+        const int i = b0 + g + u * GROUPS;
+        if (i < count && j == 0) store(i, n[u], dot / p.sqrt_r);
       }
     }
+    return;
+  }
+  for (int b = 0; b < count; b += GROUPS) {
+    const int i = b + g;
+    const bool live = i < count;
+    const int n = live ? key_at(i) : -1;
+    const float sc = rank_score16(p, h, item, r0, n >= 0 ? n : 0);
+    if (live && j == 0) store(i, n, sc);
   }
 }
 
@@ -258,49 +289,101 @@ SVA_DEV bool in_chosen_cells(const CandParams& p, const uint32_t* member, int64_
   return false;
 }
 
-__global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
+// The chosen lists of an item: the top `cells` cells of every subspace by
+// LUT / sqrt(R) (ties: lower cell index) in topc (rank order), their cells
+// as bits in member, and lbase[j] = the slot of list j's first entry
+// (lbase[S * cells] = all list entries).  Every thread of the block calls it.
+SVA_DEV void choose_lists(const CandParams& p, int item, float* score, int* topc, uint32_t* member, int* lbase,
+                          uint32_t* scan_scratch) {
 #pragma clang fp contract(off)
-  __shared__ float score[kMaxSub * 256];
-  __shared__ int topc[kMaxSub * kMaxCells];
-  __shared__ uint32_t member[kMaxSub * 8];  // bit c of subspace s: cell c chosen (C <= 256)
-  __shared__ int lbase[kMaxSub * kMaxCells + 1];
-  const int item = blockIdx.y;
-  const int h = item % p.H;
-  const ItemRows ir = item_rows(p, item / p.H);
   const int S = p.S, C = p.C, cells = p.cells;
-  // top cells of every subspace: rank of each cell among its subspace
-  for (int e = threadIdx.x; e < S * C; e += CT) score[e] = p.lut[(int64_t)item * S * C + e] / p.sqrt_r;
+  // top cells of every subspace by LUT / sqrt(R), ties to the lower cell
+  const float* item_lut = p.lut + (int64_t)item * S * C;
   for (int e = threadIdx.x; e < S * 8; e += CT) member[e] = 0u;
-  for (int e = threadIdx.x; e < S * cells; e += CT) topc[e] = 0;  // NaN scores may leave ranks unfilled
-  __syncthreads();
-  for (int e = threadIdx.x; e < S * C; e += CT) {
-    const int s = e / C, c = e - s * C;
-    const float v = score[e];
-    int rank = 0;
-    for (int o = 0; o < C; ++o) {
-      const float u = score[s * C + o];
-      rank += (u > v) || (u == v && o < c);
+  for (int e = threadIdx.x; e < S * cells; e += CT) topc[e] = 0;
+  if (cells <= 16) {
+    // one wave per subspace: `cells` rounds of a wave arg-max over composite
+    // keys (score key, cell), 4 cells per lane
+    __syncthreads();
+    const int lane = lane_id();
+    for (int s = (int)threadIdx.x / WAVE; s < S; s += CT / WAVE) {
+      uint64_t k[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = lane + WAVE * q;
+        k[q] = c < C ? composite(f2key(item_lut[s * C + c] / p.sqrt_r), (uint32_t)c) : 0ull;
+      }
+      for (int r = 0; r < cells; ++r) {
+        uint64_t m = k[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) m = k[q] > m ? k[q] : m;
+        m = wave_max_u64(m);
+        const uint32_t c = composite_index(m);
+        if (lane == 0) {
+          topc[s * cells + r] = (int)c;
+          atomicOr(&member[s * 8 + (c >> 5)], 1u << (c & 31));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (k[q] == m) k[q] = 0ull;
+      }
     }
-    if (rank < cells) {
-      topc[s * cells + rank] = c;
-      if (c < 256) atomicOr(&member[s * 8 + (c >> 5)], 1u << (c & 31));
+  } else {
+    // rank of each cell among its subspace
+    for (int e = threadIdx.x; e < S * C; e += CT) score[e] = item_lut[e] / p.sqrt_r;
+    __syncthreads();
+    for (int e = threadIdx.x; e < S * C; e += CT) {
+      const int s = e / C, c = e - s * C;
+      const float v = score[e];
+      int rank = 0;
+      for (int o = 0; o < C; ++o) {
+        const float u = score[s * C + o];
+        rank += (u > v) || (u == v && o < c);
+      }
+      if (rank < cells) {
+        topc[s * cells + rank] = c;
+        if (c < 256) atomicOr(&member[s * 8 + (c >> 5)], 1u << (c & 31));
+      }
     }
   }
   __syncthreads();
   const int nlists = S * cells;
   const int32_t* item_off = p.offsets + (int64_t)item * S * (C + 1);  // [S, C + 1] of this item
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int j = 0; j < nlists; ++j) {
-      const int s = j / cells;
-      const int32_t* off = item_off + s * (C + 1);
-      const int c = min(max(topc[j], 0), C - 1);
-      lbase[j] = acc;
-      acc += off[c + 1] - off[c];
+  {
+    // list sizes, all loaded at once, and their prefix
+    uint32_t carry = 0;
+    for (int j0 = 0; j0 < nlists; j0 += CT) {
+      const int jj = j0 + (int)threadIdx.x;
+      uint32_t sz = 0;
+      if (jj < nlists) {
+        const int32_t* off = item_off + (jj / cells) * (C + 1);
+        const int c = min(max(topc[jj], 0), C - 1);
+        sz = (uint32_t)max(0, off[c + 1] - off[c]);
+      }
+      uint32_t tot;
+      const uint32_t ex = block_excl_scan<CT>(sz, scan_scratch, &tot);
+      if (jj < nlists) lbase[jj] = (int)(carry + ex);
+      carry += tot;
     }
-    lbase[nlists] = acc;
+    if (threadIdx.x == 0) lbase[nlists] = (int)carry;
   }
   __syncthreads();
+}
+
+__global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ float score[];  // [S * C] for the ranking path (cells > 16) only
+  __shared__ int topc[kMaxSub * kMaxCells];
+  __shared__ uint32_t member[kMaxSub * 8];  // bit c of subspace s: cell c chosen (C <= 256)
+  __shared__ int lbase[kMaxSub * kMaxCells + 1];
+  __shared__ uint32_t scan_scratch[CT / WAVE + 1];
+  const int item = blockIdx.y;
+  const int h = item % p.H;
+  const ItemRows ir = item_rows(p, item / p.H);
+  choose_lists(p, item, score, topc, member, lbase, scan_scratch);
+  const int S = p.S, C = p.C, cells = p.cells;
+  const int nlists = S * cells;
+  const int32_t* item_off = p.offsets + (int64_t)item * S * (C + 1);  // [S, C + 1] of this item
   uint64_t* comp = p.comp + (int64_t)item * p.W;
   uint8_t* flag = p.flag + (int64_t)item * p.W;
   const int tail_len = max(0, ir.k_len - ir.tail_start);
@@ -341,8 +424,13 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
         },
         comp + tail_slot0 + t0, flag + tail_slot0 + t0, 0);
   } else {
-    // the extra slot, and clearing of list slots past the lists' total
-    for (int i = min(lbase[nlists], tail_slot0) + (int)threadIdx.x; i < tail_slot0; i += CT) comp[i] = 0ull, flag[i] = 0;
+    // the extra slot, and the list slots past the lists' total: cleared, or
+    // (ragged) their count recorded so that the selection skips them
+    if (p.nlist != nullptr) {
+      if (threadIdx.x == 0) p.nlist[item] = min(lbase[nlists], tail_slot0);
+    } else {
+      for (int i = min(lbase[nlists], tail_slot0) + (int)threadIdx.x; i < tail_slot0; i += CT) comp[i] = 0ull, flag[i] = 0;
+    }
     int n = -1;
     uint8_t extra = 0;
     if (!p.adaptive) {
@@ -360,6 +448,131 @@ __global__ void __launch_bounds__(CT) inverted_candidates_kernel(CandParams p) {
       }
     }
     score_entries(p, h, item, ir.r0, 1, [&](int) { return n; }, comp + extra_slot, flag + extra_slot, extra);
+  }
+}
+
+// Ragged static batches, two launches balanced over the items' entries:
+//   prep:  one workgroup per item chooses its lists (choose_lists), records
+//          the item's list entries in nlist[item] and copies the lists' keys
+//          into the item's list slots (coalesced runs of ids);
+//   score: a fixed grid splits the live slots of all items (list entries,
+//          tail slots, the extra slot) evenly over its workgroups, so one
+//          oversized cell is scored by many CUs; each slot gets its
+//          composite and flag as in inverted_candidates_kernel.
+__global__ void __launch_bounds__(CT) ragged_cand_prep_kernel(CandParams p) {
+  __shared__ int topc[kMaxSub * kMaxCells];
+  __shared__ uint32_t member[kMaxSub * 8];
+  __shared__ int lbase[kMaxSub * kMaxCells + 1];
+  __shared__ uint32_t scan_scratch[CT / WAVE + 1];
+  extern __shared__ float score[];
+  const int item = blockIdx.x;
+  const int h = item % p.H;
+  const ItemRows ir = item_rows(p, item / p.H);
+  choose_lists(p, item, score, topc, member, lbase, scan_scratch);
+  const int S = p.S, C = p.C, cells = p.cells;
+  const int nlists = S * cells;
+  const int tail_slot0 = S * p.postings_len;
+  const int32_t* item_off = p.offsets + (int64_t)item * S * (C + 1);
+  uint64_t* comp = p.comp + (int64_t)item * p.W;
+  for (int j = 0; j < nlists; ++j) {
+    const int s = j / cells;
+    const int c = min(max(topc[j], 0), C - 1);
+    const int o0 = item_off[s * (C + 1) + c];
+    const int count = max(0, min(lbase[j + 1] - lbase[j], tail_slot0 - lbase[j]));
+    const int32_t* lst = p.ids + ((int64_t)h * S + s) * p.ids_rows + ir.r0 + o0;
+    for (int i = threadIdx.x; i < count; i += CT) comp[lbase[j] + i] = (uint64_t)(uint32_t)lst[i];
+  }
+  if (threadIdx.x == 0) p.nlist[item] = min(lbase[nlists], tail_slot0);
+}
+
+constexpr int MAX_RAGGED_ITEMS = 8192;  // items of a ragged launch (the score kernel's prefix in LDS)
+
+__global__ void __launch_bounds__(CT) ragged_cand_score_kernel(CandParams p, int items) {
+#pragma clang fp contract(off)
+  extern __shared__ int pre[];  // [items + 1] first live entry of each item
+  __shared__ uint32_t scan_scratch[CT / WAVE + 1];
+  const int live_extra = p.tail_cap + 1;  // tail slots and the extra slot of every item
+  {
+    uint32_t carry = 0;
+    for (int i0 = 0; i0 < items; i0 += CT) {
+      const int it = i0 + (int)threadIdx.x;
+      const uint32_t v = it < items ? (uint32_t)(max(p.nlist[it], 0) + live_extra) : 0u;
+      uint32_t tot;
+      const uint32_t ex = block_excl_scan<CT>(v, scan_scratch, &tot);
+      if (it < items) pre[it] = (int)(carry + ex);
+      carry += tot;
+    }
+    if (threadIdx.x == 0) pre[items] = (int)carry;
+  }
+  __syncthreads();
+  constexpr int GROUPS = CT / 16;
+  constexpr int U = SCORE_U;
+  const int total = pre[items];
+  const int per = ((total + (int)gridDim.x - 1) / (int)gridDim.x + GROUPS * U - 1) / (GROUPS * U) * (GROUPS * U);
+  const int e_begin = (int)blockIdx.x * per, e_end = min(total, e_begin + per);
+  const int g = threadIdx.x >> 4;
+  const int j = lane_id() & 15;
+  const int tail_slot0 = p.S * p.postings_len;
+  for (int b0 = e_begin; b0 < e_end; b0 += GROUPS * U) {
+    int it[U], slot[U], n[U];
+    int64_t r0[U];
+    float4 rv[U], qq[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = b0 + g + u * GROUPS;
+      it[u] = -1;
+      n[u] = -1;
+      slot[u] = 0;
+      r0[u] = 0;
+      if (e < e_end) {
+        int lo = 0, hi = items;  // last item whose first entry is <= e
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (pre[mid] <= e) lo = mid;
+          else hi = mid;
+        }
+        it[u] = lo;
+        const ItemRows ir = item_rows(p, lo / p.H);
+        r0[u] = ir.r0;
+        const int i = e - pre[lo];
+        const int nl = pre[lo + 1] - pre[lo] - live_extra;
+        const int tail_len = max(0, ir.k_len - ir.tail_start);
+        if (i < nl) {
+          slot[u] = i;
+          n[u] = (int)(uint32_t)p.comp[(int64_t)lo * p.W + i];
+        } else if (i < nl + p.tail_cap) {
+          const int t = i - nl;
+          slot[u] = tail_slot0 + t;
+          n[u] = t < tail_len ? ir.tail_start + t : -1;
+        } else {
+          slot[u] = p.W - 1;
+          n[u] = tail_len == 0 ? ir.k_len - 1 : -1;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = n[u] >= 0;
+      const int hh = live ? it[u] % p.H : 0;
+      rv[u] = live ? reinterpret_cast<const float4*>(p.k_low + (int64_t)hh * p.klow_hs + (r0[u] + n[u]) * 64)[j]
+                   : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      qq[u] = live ? reinterpret_cast<const float4*>(p.q_low + (int64_t)it[u] * 64)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float dot = rank_dot64_row16(rv[u], qq[u]);  // valid in the row's first lane
+      if (it[u] >= 0 && j == 0) {
+        uint64_t* comp = p.comp + (int64_t)it[u] * p.W;
+        uint8_t* flag = p.flag + (int64_t)it[u] * p.W;
+        if (n[u] >= 0) {
+          comp[slot[u]] = entry_comp(true, dot / p.sqrt_r, n[u]);
+          flag[slot[u]] = 1;
+        } else {
+          comp[slot[u]] = 0ull;
+          flag[slot[u]] = 0;
+        }
+      }
+    }
   }
 }
 
@@ -402,6 +615,8 @@ struct SelParams {
   const int64_t* klens;
   int H;
   int amin, amid;
+  const int32_t* nlist;  // ragged: live slots are [0, nlist[row]) and [tail_slot0, W)
+  int tail_slot0;
 };
 
 SVA_DEV uint32_t hash_key(uint32_t n, int hash) { return (n * 2654435761u) & (uint32_t)(hash - 1); }
@@ -422,6 +637,11 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   const uint8_t* flag = p.flag + (int64_t)h * p.W;
   uint64_t* win = p.win + (int64_t)h * p.win_cap;
   const int W = p.W;
+  // live slots in slot order: every slot, or (ragged) the row's list entries,
+  // then its tail slots and the extra slot
+  const int nl = p.nlist != nullptr ? min(max(p.nlist[h], 0), p.tail_slot0) : 0;
+  const int WL = p.nlist != nullptr ? nl + (W - p.tail_slot0) : W;
+  auto at = [&](int i) { return (p.nlist != nullptr && i >= nl) ? p.tail_slot0 + (i - nl) : i; };
   int Bi = p.B, min_b = p.min_budget, mid_b = p.mid_budget;
   int64_t tail_extra = p.tail_extra;
   const int32_t* mc = p.max_count;
@@ -435,12 +655,20 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
     tail_extra = kl - pl > 0 ? kl - pl : 1;
     mc = p.max_count + (int64_t)b * p.n_max;
   }
-  // counts: real entries, valid entries
+  // counts: real entries, valid entries; bounds of the real entries
   uint32_t real = 0, nvalid = 0;
-  for (int i = threadIdx.x; i < W; i += UB) {
-    const uint64_t c = comp[i];
-    real += c != 0ull && !(flag[i] & 2);
-    nvalid += c != 0ull && (flag[i] & 1) && !(flag[i] & 2);
+  uint64_t ror = 0ull, rand_ = ~0ull;
+  for (int i = threadIdx.x; i < WL; i += UB) {
+    const int j = at(i);
+    const uint64_t c = comp[j];
+    const uint8_t f = flag[j];
+    const bool is_real = c != 0ull && !(f & 2);
+    real += is_real;
+    nvalid += is_real && (f & 1);
+    if (is_real) {
+      ror |= c;
+      rand_ &= c;
+    }
   }
   uint32_t Real, Valid;
   block_excl_scan<UB>(real, scratch, &Real);
@@ -458,9 +686,10 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   if (p.mode == 1) refill = Real;
   else refill = min(width, (int64_t)max(Bi, Bi * p.refill_factor));
   auto visit_real = [&](auto&& f) {
-    for (int i = threadIdx.x; i < W; i += UB) {
-      const uint64_t c = comp[i];
-      if (c != 0ull && !(flag[i] & 2)) f(c);
+    for (int i = threadIdx.x; i < WL; i += UB) {
+      const int j = at(i);
+      const uint64_t c = comp[j];
+      if (c != 0ull && !(flag[j] & 2)) f(c);
     }
   };
   // adaptive mode: the candidates are distinct keys already, so U is read
@@ -470,7 +699,7 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
   if (!direct) {
     uint64_t X1 = 1ull;
     if (refill > 0 && (int64_t)Real > refill)
-      X1 = select_largest<UB>(visit_real, (int)refill, whist, scratch, shared64, shared);
+      X1 = select_largest12<UB>(visit_real, (int)refill, ror, rand_, &whist[0][0], scratch, shared64, shared);
     if (refill <= 0) X1 = ~0ull;
     // window entries in slot order, with their valid flag in bit 0 of the stored word
     for (int i = threadIdx.x; i < HASH; i += UB) {
@@ -480,18 +709,20 @@ __global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
     }
     __syncthreads();
     {
-      const int per = (W + UB - 1) / UB;
-      const int i0 = min(W, (int)threadIdx.x * per), i1 = min(W, i0 + per);
+      const int per = (WL + UB - 1) / UB;
+      const int i0 = min(WL, (int)threadIdx.x * per), i1 = min(WL, i0 + per);
       uint32_t cnt = 0;
       for (int i = i0; i < i1; ++i) {
-        const uint64_t c = comp[i];
-        cnt += c != 0ull && !(flag[i] & 2) && c >= X1;
+        const int j = at(i);
+        const uint64_t c = comp[j];
+        cnt += c != 0ull && !(flag[j] & 2) && c >= X1;
       }
       uint32_t tot;
       uint32_t o = block_excl_scan<UB>(cnt, scratch, &tot);
       for (int i = i0; i < i1; ++i) {
-        const uint64_t c = comp[i];
-        if (c != 0ull && !(flag[i] & 2) && c >= X1) {
+        const int j = at(i);
+        const uint64_t c = comp[j];
+        if (c != 0ull && !(flag[j] & 2) && c >= X1) {
           if (o < (uint32_t)p.win_cap) {
             win[o] = c;
             // key table: best composite per key, then first window position of it
@@ -819,10 +1050,11 @@ extern "C" int sva_inverted_candidates(const float* lut, const float* q_low, con
   p.klens = nullptr;
   p.tail_cap = (int)tail_len;
   p.ids_rows = postings_len;
+  p.nlist = nullptr;
   const int64_t wgs = S * cells + (tail_len + TAIL_ROWS - 1) / TAIL_ROWS + 1;
   SVA_REQUIRE(wgs < (1ll << 31) && slots < (1ll << 31), "sva_inverted_candidates: too many rows");
-  hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)H), dim3(CT), 0, (hipStream_t)stream,
-                     p);
+  hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)H), dim3(CT),
+                     cells > 16 ? sizeof(float) * (size_t)(S * C) : 0, (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("inverted_candidates_kernel");
   return SVA_OK;
 }
@@ -837,11 +1069,11 @@ extern "C" int sva_inverted_candidates_ragged(const float* lut, const float* q_l
                                               int64_t rows, const int64_t* seq_offsets, const int64_t* postings_lens,
                                               const int64_t* k_lens, int64_t n_seq, int64_t max_postings_len,
                                               int64_t max_tail, int64_t H, int64_t S, int64_t C, int64_t R,
-                                              int64_t cells, uint64_t* comp, uint8_t* flag, int64_t slots,
-                                              void* stream) {
+                                              int64_t cells, uint64_t* comp, uint8_t* flag, int32_t* list_counts,
+                                              int64_t slots, void* stream) {
   sva::clear_error();
   SVA_REQUIRE(lut && q_low && k_low && codes && offsets && ids && seq_offsets && postings_lens && k_lens && comp &&
-                  flag,
+                  flag && list_counts,
               "sva_inverted_candidates_ragged: null pointer");
   SVA_REQUIRE(n_seq > 0 && H > 0 && n_seq * H <= 65535 && rows > 0 && rows < (1ll << 31) && max_postings_len >= 0 &&
                   max_postings_len <= rows && max_tail >= 0 && max_tail <= rows,
@@ -884,11 +1116,19 @@ extern "C" int sva_inverted_candidates_ragged(const float* lut, const float* q_l
   p.klens = k_lens;
   p.tail_cap = (int)max_tail;
   p.ids_rows = rows;
-  const int64_t wgs = S * cells + (max_tail + TAIL_ROWS - 1) / TAIL_ROWS + 1;
-  SVA_REQUIRE(wgs < (1ll << 31) && slots < (1ll << 31), "sva_inverted_candidates_ragged: too many rows");
-  hipLaunchKernelGGL(inverted_candidates_kernel, dim3((unsigned)wgs, (unsigned)(n_seq * H)), dim3(CT), 0,
-                     (hipStream_t)stream, p);
-  SVA_CHECK_LAUNCH("inverted_candidates_kernel");
+  p.nlist = list_counts;
+  const int64_t items = n_seq * H;
+  SVA_UNSUPPORTED(items <= MAX_RAGGED_ITEMS, "sva_inverted_candidates_ragged: %lld items (at most %d)",
+                  (long long)items, MAX_RAGGED_ITEMS);
+  SVA_UNSUPPORTED(R == 64, "sva_inverted_candidates_ragged: rank %lld (64 only)", (long long)R);
+  SVA_REQUIRE(slots < (1ll << 31) && items * slots < (1ll << 40), "sva_inverted_candidates_ragged: too many rows");
+  hipLaunchKernelGGL(ragged_cand_prep_kernel, dim3((unsigned)items), dim3(CT),
+                     cells > 16 ? sizeof(float) * (size_t)(S * C) : 0, (hipStream_t)stream, p);
+  SVA_CHECK_LAUNCH("ragged_cand_prep_kernel");
+  const int score_wgs = 4 * sva::device_cu_count();
+  hipLaunchKernelGGL(ragged_cand_score_kernel, dim3((unsigned)score_wgs), dim3(CT), sizeof(int) * (size_t)(items + 1),
+                     (hipStream_t)stream, p, (int)items);
+  SVA_CHECK_LAUNCH("ragged_cand_score_kernel");
   return SVA_OK;
 }
 
@@ -950,11 +1190,15 @@ extern "C" int sva_unique_refill_select_ragged(const uint64_t* comp, const uint8
                                                int64_t adaptive_mid_budget, double low_margin, double high_margin,
                                                int64_t refill_factor, const int32_t* max_count, int64_t S,
                                                int64_t cells, const int64_t* postings_lens, const int64_t* k_lens,
-                                               int32_t* fin_idx, int32_t* fin_count, float* stats, void* workspace,
+                                               const int32_t* list_counts, int64_t max_postings_len, int32_t* fin_idx,
+                                               int32_t* fin_count, float* stats, void* workspace,
                                                size_t workspace_bytes, void* stream) {
   sva::clear_error();
-  SVA_REQUIRE(comp && flag && max_count && postings_lens && k_lens && fin_idx && fin_count && stats && workspace,
+  SVA_REQUIRE(comp && flag && max_count && postings_lens && k_lens && list_counts && fin_idx && fin_count && stats &&
+                  workspace,
               "sva_unique_refill_select_ragged: null pointer");
+  SVA_REQUIRE(max_postings_len >= 0 && S * max_postings_len < slots,
+              "sva_unique_refill_select_ragged: slots must be sva_inverted_slots_ragged(...)");
   SVA_REQUIRE(n_seq > 0 && H > 0 && n_seq * H < (1ll << 31) && slots > 0 && slots < (1ll << 31) && budget > 0 &&
                   adaptive_min_budget >= 0 && adaptive_mid_budget >= 0 && refill_factor >= 1 && S > 0 && cells > 0,
               "sva_unique_refill_select_ragged: bad sizes");
@@ -995,6 +1239,8 @@ extern "C" int sva_unique_refill_select_ragged(const uint64_t* comp, const uint8
   p.H = (int)H;
   p.amin = (int)std::min<int64_t>(adaptive_min_budget, budget);
   p.amid = (int)std::min<int64_t>(adaptive_mid_budget, budget);
+  p.nlist = list_counts;
+  p.tail_slot0 = (int)(S * max_postings_len);
   return launch_select(p, n_seq * H, (hipStream_t)stream);
 }
 

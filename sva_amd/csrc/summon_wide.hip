@@ -288,33 +288,6 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
   if (!CHECK) n_allowed = KEYS_PT;
 }
 
-// Row shift within each 16-lane DPP row: lane j receives lane j + N of its
-// row (lanes past the row end receive 0).
-template <int N>
-SVA_DEV float row_down(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xF, 0xF, true));
-}
-
-// Rank score of a 64-float k_low row in torch's sum order, computed by the
-// 16 lanes of one DPP row (lane j holds float4 j of the row in r and of the
-// query in qq): element e < 32 pairs with e + 32, the lane chains g, g+2,
-// g+4, g+6 form accumulator lane 4g + c, then the eight in order, as in
-// torch_order_dot64.  The result is valid in the row's first lane.
-SVA_DEV float rank_dot64_row16(const float4 r, const float4 qq) {
-#pragma clang fp contract(off)
-  const float p0 = r.x * qq.x, p1 = r.y * qq.y, p2 = r.z * qq.z, p3 = r.w * qq.w;
-  const float a0 = (0.0f + p0) + row_down<8>(p0);
-  const float a1 = (0.0f + p1) + row_down<8>(p1);
-  const float a2 = (0.0f + p2) + row_down<8>(p2);
-  const float a3 = (0.0f + p3) + row_down<8>(p3);
-  const float v0 = ((a0 + row_down<2>(a0)) + row_down<4>(a0)) + row_down<6>(a0);
-  const float v1 = ((a1 + row_down<2>(a1)) + row_down<4>(a1)) + row_down<6>(a1);
-  const float v2 = ((a2 + row_down<2>(a2)) + row_down<4>(a2)) + row_down<6>(a2);
-  const float v3 = ((a3 + row_down<2>(a3)) + row_down<4>(a3)) + row_down<6>(a3);
-  const float w0 = row_down<1>(v0), w1 = row_down<1>(v1), w2 = row_down<1>(v2), w3 = row_down<1>(v3);
-  return (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
-}
-
 // Rank scores of a scan wave's nc candidates (keys in the LDS list while
 // they fit, else from the wave's candidate list): one 16-lane DPP row per
 // candidate, 16 candidates in flight per wave; written beside the list.

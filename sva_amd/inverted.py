@@ -235,12 +235,13 @@ def ragged_static_decode(query, q_proj, scale, codebooks, keys, values, k_low, c
     items = n_seq * heads
     comp = torch.empty(items, slots, device=device, dtype=torch.int64)
     flag = torch.empty(items, slots, device=device, dtype=torch.uint8)
+    list_counts = torch.empty(items, device=device, dtype=torch.int32)
     stream = stream_handle(device)
     check(L.sva_inverted_candidates_ragged(
         ptr(lut), ptr(q_low), ptr(k_low), k_low.stride(0), ptr(codes), code_type(codes), codes.stride(0),
         ptr(postings.offsets), ptr(postings.ids), rows, ptr(seq_offsets), ptr(postings.postings_lens), ptr(k_lens),
-        n_seq, postings.max_len, max_tail, heads, subspaces, codewords, rank, cells, ptr(comp), ptr(flag), slots,
-        stream), "sva_inverted_candidates_ragged")
+        n_seq, postings.max_len, max_tail, heads, subspaces, codewords, rank, cells, ptr(comp), ptr(flag),
+        ptr(list_counts), slots, stream), "sva_inverted_candidates_ragged")
     fin_idx = torch.empty(items, budget, device=device, dtype=torch.int32)
     fin_count = torch.empty(items, device=device, dtype=torch.int32)
     stats = torch.empty(items, 4, device=device, dtype=torch.float32)
@@ -248,7 +249,8 @@ def ragged_static_decode(query, q_proj, scale, codebooks, keys, values, k_low, c
     check(L.sva_unique_refill_select_ragged(
         ptr(comp), ptr(flag), slots, n_seq, heads, budget, adaptive_min or 0, adaptive_mid or 0, float(low_margin),
         float(high_margin), 2, ptr(postings.max_count), subspaces, cells, ptr(postings.postings_lens), ptr(k_lens),
-        ptr(fin_idx), ptr(fin_count), ptr(stats), ptr(ws), ws.numel(), stream), "sva_unique_refill_select_ragged")
+        ptr(list_counts), postings.max_len, ptr(fin_idx), ptr(fin_count), ptr(stats), ptr(ws), ws.numel(), stream),
+        "sva_unique_refill_select_ragged")
     out = kernels.verify(query, keys, values, fin_idx, fin_count, rows, scaling, out_dtype=query.dtype,
                          seq_offsets=seq_offsets, seq_lens=k_lens)
     if return_selection:
