@@ -621,7 +621,7 @@ struct SelParams {
 
 SVA_DEV uint32_t hash_key(uint32_t n, int hash) { return (n * 2654435761u) & (uint32_t)(hash - 1); }
 
-__global__ void __launch_bounds__(UB) unique_select_kernel(SelParams p) {
+__global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  // 8 waves per SIMD: two workgroups per CU
   extern __shared__ __align__(16) unsigned char lds[];
   const int HASH = p.hash;
   uint64_t* hcomp = (uint64_t*)lds;                        // [HASH] best composite per key
