@@ -303,6 +303,21 @@ int sva_unique_refill_select_ragged(const uint64_t *comp, const uint8_t *flag, i
                                     void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Residual output adapter of the late-layer socket, one fused launch for T
+ * tokens: out = attn + (up(gelu(down([hidden, attn]))) * scale).to(attn
+ * dtype), with down [rank, 2 * hidden] and up [hidden, rank] fp32 and the
+ * exact (erf) GELU.
+ * Replaces experiments/sva_late4_logit_distill.py:47-51
+ * (SVAResidualOutputAdapter.forward after the attention).
+ *   hidden / attn / out: token t's row at t * row_stride (contiguous rows)
+ *   rank <= 64
+ */
+int sva_residual_adapter(const void *hidden, int hidden_dtype, int64_t hidden_row_stride, const void *attn,
+                         int attn_dtype, int64_t attn_row_stride, const float *down_w, const float *up_w, float scale,
+                         int64_t n_tokens, int64_t hidden_size, int64_t rank, void *out, int out_dtype,
+                         int64_t out_row_stride, void *stream);
+
+/*
  * Unique refill selection over arbitrary rows of candidates
  * (SVALlamaAttention._top_unique_candidates, sva/llama.py:83-116): per row,
  * the best min(W, max(budget, refill_factor * budget)) entries by masked

@@ -30,6 +30,10 @@ Pinning (what checks each function; see tests/test_oracle.py):
       fp64 closed form (softmax-weighted sum) against a float64 torch softmax.
   rebuild_postings / static / inverted candidate sets
       partition and bincount invariants, brute-force membership.
+  residual_adapter
+      torch-CPU's own nn.Linear / F.gelu module of the reference on the same
+      inputs (float64), the zero-initialised up projection (output = input),
+      and gelu at known points.
   golden fixtures (tests/golden/) written from the reference's own functions.
 """
 
@@ -549,6 +553,20 @@ def decode(q, q_low, keys, values, k_low, codebooks, codes, shortlist: int, budg
         codes.dtype.itemsize, shortlist, budget, float(scaling), _ptr(sl), _ptr(fin), _ptr(out),
     )
     return sl, fin, out, threads
+
+
+def residual_adapter(hidden, attn, down_w, up_w, scale: float) -> np.ndarray:
+    """SVAResidualOutputAdapter.forward after the attention
+    (experiments/sva_late4_logit_distill.py:47-51) in float64:
+    attn + up(gelu(down([hidden, attn]))) * scale, gelu the erf form.
+    hidden / attn [T, H]; down [rank, 2H]; up [H, rank]."""
+
+    x = np.concatenate([np.asarray(hidden, np.float64), np.asarray(attn, np.float64)], axis=-1)
+    pre = x @ np.asarray(down_w, np.float64).T
+    erf = np.vectorize(math.erf)
+    z = 0.5 * pre * (1.0 + erf(pre / math.sqrt(2.0)))
+    corr = (z @ np.asarray(up_w, np.float64).T) * scale
+    return np.asarray(attn, np.float64) + corr
 
 
 def set_threads(n: int) -> None:

@@ -1,0 +1,139 @@
+// Residual output adapter of the late-layer socket
+// (experiments/sva_late4_logit_distill.py:37-51): for every token,
+//   x    = [hidden_states, attn_output]                  (2 * hidden, fp32)
+//   corr = up(gelu(down(x))) * scale                     (fp32; exact erf GELU)
+//   out  = attn_output + corr.to(attn dtype)             (in the attn dtype)
+// down [rank, 2 * hidden] and up [hidden, rank] are fp32 (nn.Linear weights).
+//
+// One workgroup per TOK tokens: the tokens' inputs are staged in LDS as
+// fp32, each thread forms down-projection outputs (token, o) as a
+// sequential fma chain over the 2 * hidden inputs, the GELU values go to
+// LDS, then each output (token, j) is a sequential chain over the rank.
+#include <cmath>
+
+#include "capi_internal.h"
+#include "common.cuh"
+#include "summon.h"
+
+using namespace sva;
+
+namespace {
+
+constexpr int AB = 256;          // threads per workgroup
+constexpr int MAX_RANK = 64;
+constexpr int MAX_TOK = 16;
+
+struct AdapterParams {
+  const void* hidden;
+  int h_dtype;
+  int64_t h_rs;
+  const void* attn;
+  int a_dtype;
+  int64_t a_rs;
+  const float* down;  // [rank, 2 * H]
+  const float* up;    // [H, rank]
+  float scale;
+  int64_t T;
+  int H, rank, tok;
+  void* out;
+  int o_dtype;
+  int64_t o_rs;
+};
+
+// The value a float takes after a cast to dtype (round to nearest even).
+SVA_DEV float round_to(float v, int dtype) {
+  if (dtype == F32) return v;
+  if (dtype == BF16) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7F800000u) == 0x7F800000u) return v;  // inf and nan pass through
+    u += 0x7FFFu + ((u >> 16) & 1u);                 // as store_elem rounds
+    return __uint_as_float(u & 0xFFFF0000u);
+  }
+  return __half2float(__float2half_rn(v));
+}
+
+__global__ void __launch_bounds__(AB) residual_adapter_kernel(AdapterParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) float xs[];  // [tok][2 * H], then z [tok][rank]
+  const int H2 = 2 * p.H;
+  float* z = xs + p.tok * H2;
+  const int64_t t0 = (int64_t)blockIdx.x * p.tok;
+  const int nt = (int)min((int64_t)p.tok, p.T - t0);
+  for (int e = threadIdx.x; e < nt * H2; e += AB) {
+    const int t = e / H2, k = e - t * H2;
+    xs[e] = k < p.H ? load_elem(p.hidden, (t0 + t) * p.h_rs + k, p.h_dtype)
+                    : load_elem(p.attn, (t0 + t) * p.a_rs + (k - p.H), p.a_dtype);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nt * p.rank; e += AB) {
+    const int t = e / p.rank, o = e - t * p.rank;
+    const float* x = xs + t * H2;
+    const float* w = p.down + (int64_t)o * H2;
+    float acc = 0.0f;
+    for (int k = 0; k < H2; ++k) acc = __builtin_fmaf(x[k], w[k], acc);
+    z[e] = 0.5f * acc * (1.0f + erff(acc * 0.70710678118654752f));  // F.gelu (erf form)
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nt * p.H; e += AB) {
+    const int t = e / p.H, j = e - t * p.H;
+    const float* zz = z + t * p.rank;
+    const float* w = p.up + (int64_t)j * p.rank;
+    float acc = 0.0f;
+    for (int o = 0; o < p.rank; ++o) acc = __builtin_fmaf(zz[o], w[o], acc);
+    const float corr = round_to(acc * p.scale, p.a_dtype);
+    const float a = xs[t * H2 + p.H + j];
+    store_elem(p.out, (t0 + t) * p.o_rs + j, p.o_dtype, a + corr);
+  }
+}
+
+}  // namespace
+
+extern "C" int sva_residual_adapter(const void* hidden, int hidden_dtype, int64_t hidden_row_stride, const void* attn,
+                                    int attn_dtype, int64_t attn_row_stride, const float* down_w, const float* up_w,
+                                    float scale, int64_t n_tokens, int64_t hidden_size, int64_t rank, void* out,
+                                    int out_dtype, int64_t out_row_stride, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(hidden && attn && down_w && up_w && out, "sva_residual_adapter: null pointer");
+  SVA_REQUIRE(n_tokens >= 0 && hidden_size > 0 && hidden_size <= 8192, "sva_residual_adapter: bad sizes");
+  SVA_UNSUPPORTED(rank > 0 && rank <= MAX_RANK, "sva_residual_adapter: rank %lld (at most %d)", (long long)rank,
+                  MAX_RANK);
+  SVA_REQUIRE(hidden_dtype >= 0 && hidden_dtype <= 2 && attn_dtype >= 0 && attn_dtype <= 2 && out_dtype >= 0 &&
+                  out_dtype <= 2,
+              "sva_residual_adapter: bad dtype");
+  if (n_tokens == 0) return SVA_OK;
+  // tokens per workgroup: as many as fit 64 KB of staged fp32 inputs, at most MAX_TOK
+  const int64_t per_tok = sizeof(float) * (2 * hidden_size + rank);
+  const int tok = (int)std::max<int64_t>(1, std::min<int64_t>(MAX_TOK, (64 * 1024) / per_tok));
+  const size_t lds = (size_t)tok * (size_t)per_tok;
+  SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_residual_adapter: hidden size %lld needs %zu bytes of LDS",
+                  (long long)hidden_size, lds);
+  const int64_t blocks = (n_tokens + tok - 1) / tok;
+  SVA_REQUIRE(blocks < (1ll << 31), "sva_residual_adapter: too many tokens");
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)residual_adapter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      sva::kMaxLds),
+                  "hipFuncSetAttribute(residual_adapter_kernel)");
+    attr_set = true;
+  }
+  AdapterParams p;
+  p.hidden = hidden;
+  p.h_dtype = hidden_dtype;
+  p.h_rs = hidden_row_stride;
+  p.attn = attn;
+  p.a_dtype = attn_dtype;
+  p.a_rs = attn_row_stride;
+  p.down = down_w;
+  p.up = up_w;
+  p.scale = scale;
+  p.T = n_tokens;
+  p.H = (int)hidden_size;
+  p.rank = (int)rank;
+  p.tok = tok;
+  p.out = out;
+  p.o_dtype = out_dtype;
+  p.o_rs = out_row_stride;
+  hipLaunchKernelGGL(residual_adapter_kernel, dim3((unsigned)blocks), dim3(AB), lds, (hipStream_t)stream, p);
+  SVA_CHECK_LAUNCH("residual_adapter_kernel");
+  return SVA_OK;
+}

@@ -331,3 +331,30 @@ class ScanDecodePlan:
                            head_dim, budget, float(scaling), out.data_ptr(), dtype_code(out), out.stride(0),
                            out.stride(1), out.stride(2), vws.data_ptr(), vws.numel(), stream), "sva_verify")
         return out
+
+
+def residual_adapter(hidden_states: torch.Tensor, attn_output: torch.Tensor, down_w: torch.Tensor,
+                     up_w: torch.Tensor, scale: float) -> torch.Tensor:
+    """attn_output + (up(gelu(down([hidden_states, attn_output]))) * scale).to(attn dtype)
+    for every token (experiments/sva_late4_logit_distill.py:47-51), one launch."""
+
+    if hidden_states.shape != attn_output.shape:
+        raise ValueError("hidden_states and attn_output must have the same shape")
+    hidden = int(attn_output.shape[-1])
+    rank = int(down_w.shape[0])
+    if tuple(down_w.shape) != (rank, 2 * hidden) or tuple(up_w.shape) != (hidden, rank):
+        raise ValueError(f"adapter weights down {tuple(down_w.shape)} / up {tuple(up_w.shape)} do not match "
+                         f"hidden size {hidden}")
+    h = hidden_states.reshape(-1, hidden)
+    a = attn_output.reshape(-1, hidden)
+    if h.stride(-1) != 1:
+        h = h.contiguous()
+    if a.stride(-1) != 1:
+        a = a.contiguous()
+    device = require_device(h, a, down_w, up_w)
+    down_w, up_w = _f32c(down_w), _f32c(up_w)
+    out = torch.empty_like(a)
+    check(lib().sva_residual_adapter(ptr(h), dtype_code(h), h.stride(0), ptr(a), dtype_code(a), a.stride(0),
+                                     ptr(down_w), ptr(up_w), float(scale), h.shape[0], hidden, rank, ptr(out),
+                                     dtype_code(out), out.stride(0), stream_handle(device)), "sva_residual_adapter")
+    return out.reshape(attn_output.shape)

@@ -278,3 +278,27 @@ def test_decode_in_c_matches_numpy_restatement():
         assert set(fin[h].tolist()) == set(final.tolist())
         ref = oracle.verify(q[h], keys[h // 3], values[h // 3], np.sort(final), D ** -0.5)
         np.testing.assert_allclose(out[h], ref, rtol=1e-12, atol=1e-12)
+
+
+def test_residual_adapter_matches_torch_module():
+    # the reference's module (nn.Linear without bias, F.gelu) in float64 on the CPU
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(4)
+    T, H, rank = 7, 24, 4
+    hidden = rng.standard_normal((T, H))
+    attn = rng.standard_normal((T, H))
+    down = rng.standard_normal((rank, 2 * H)) * 0.3
+    up = rng.standard_normal((H, rank)) * 0.3
+    got = oracle.residual_adapter(hidden, attn, down, up, 0.5)
+    x = torch.cat([torch.from_numpy(hidden), torch.from_numpy(attn)], dim=-1)
+    want = torch.from_numpy(attn) + F.linear(F.gelu(F.linear(x, torch.from_numpy(down))), torch.from_numpy(up)) * 0.5
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-12, atol=1e-12)
+    # the reference initialises up to zero: the adapter starts as the identity
+    np.testing.assert_array_equal(oracle.residual_adapter(hidden, attn, down, np.zeros_like(up), 1.0), attn)
+    # gelu at known points: 0 -> 0, large -> identity, -large -> 0
+    one = np.ones((1, 1))
+    for v, expect in ((0.0, 0.0), (40.0, 40.0), (-40.0, 0.0)):
+        out = oracle.residual_adapter(one, np.zeros((1, 1)), np.array([[v, 0.0]]), one, 1.0)  # pre-activation v
+        assert abs(out[0, 0] - expect) < 1e-12
