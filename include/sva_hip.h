@@ -318,6 +318,21 @@ int sva_residual_adapter(const void *hidden, int hidden_dtype, int64_t hidden_ro
                          int64_t out_row_stride, void *stream);
 
 /*
+ * k-means centroid update of the product-codebook fit, per (head, subspace,
+ * cell): the mean of the cell's rows (weighted: sum of w * x over sum of w),
+ * summed in ascending key order; empty cells keep their centroid.  The
+ * cells are sva_postings_build's CSR of the current labels.
+ * Replaces the update step of experiments/sva_pq_lookup_test.py:92-100 and
+ * experiments/sva_supervised_coarse_pq_test.py:117-126.
+ *   x [H, n_rows, R] fp32 (head stride x_head_stride), weights [H, n_rows] or NULL
+ *   offsets [H, S, C + 1], ids [H, S, n_rows]; centroids / next [H, S, C, R / S]
+ *   R / S <= 64
+ */
+int sva_centroid_update(const float *x, int64_t x_head_stride, int64_t n_rows, int64_t H, int64_t R, int64_t S,
+                        int64_t C, const float *weights, const int32_t *offsets, const int32_t *ids,
+                        const float *centroids, float *next_centroids, void *stream);
+
+/*
  * Unique refill selection over arbitrary rows of candidates
  * (SVALlamaAttention._top_unique_candidates, sva/llama.py:83-116): per row,
  * the best min(W, max(budget, refill_factor * budget)) entries by masked

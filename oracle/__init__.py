@@ -34,6 +34,10 @@ Pinning (what checks each function; see tests/test_oracle.py):
       torch-CPU's own nn.Linear / F.gelu module of the reference on the same
       inputs (float64), the zero-initialised up projection (output = input),
       and gelu at known points.
+  kmeans_update / kmeans_fit
+      bit-exact against the reference's update step run by torch-CPU
+      (index_add_, bincount, division) on the same labels, plain and weighted;
+      empty cells keep their centroid.
   golden fixtures (tests/golden/) written from the reference's own functions.
 """
 
@@ -567,6 +571,49 @@ def residual_adapter(hidden, attn, down_w, up_w, scale: float) -> np.ndarray:
     z = 0.5 * pre * (1.0 + erf(pre / math.sqrt(2.0)))
     corr = (z @ np.asarray(up_w, np.float64).T) * scale
     return np.asarray(attn, np.float64) + corr
+
+
+def kmeans_update(x, labels, centroids, weights=None) -> np.ndarray:
+    """One centroid update of the reference's codebook fits
+    (experiments/sva_pq_lookup_test.py:92-100; weighted:
+    experiments/sva_supervised_coarse_pq_test.py:117-126) in float32, sums in
+    ascending row order.  x [N, sub], labels [N], centroids [C, sub], weights [N]."""
+
+    x = _f32(x)
+    labels = np.asarray(labels, np.int64)
+    cent = _f32(centroids)
+    sums = np.zeros_like(cent)
+    if weights is None:
+        np.add.at(sums, labels, x)
+        counts = np.bincount(labels, minlength=cent.shape[0]).astype(F32)
+    else:
+        w = _f32(weights)
+        np.add.at(sums, labels, x * w[:, None])
+        counts = np.zeros(cent.shape[0], F32)
+        np.add.at(counts, labels, w)
+    out = cent.copy()
+    nonempty = counts > 0
+    out[nonempty] = sums[nonempty] / counts[nonempty][:, None]
+    return out
+
+
+def kmeans_fit(k_low, subspaces: int, iterations: int, initial, weights=None) -> np.ndarray:
+    """The reference's fit loop (experiments/sva_pq_lookup_test.py:66-106,
+    experiments/sva_supervised_coarse_pq_test.py:88-131) from given initial
+    centroids [H, S, C, sub]: assign_to_centroids, then kmeans_update."""
+
+    k_low = _f32(k_low)
+    cent = _f32(initial).copy()
+    heads, _, rank = k_low.shape
+    sub = rank // subspaces
+    for h in range(heads):
+        w = None if weights is None else np.maximum(_f32(weights)[h], F32(1e-6))
+        for s in range(subspaces):
+            x = k_low[h, :, s * sub:(s + 1) * sub]
+            for _ in range(iterations):
+                labels = assign_to_centroids(x, cent[h, s])
+                cent[h, s] = kmeans_update(x, labels, cent[h, s], w)
+    return cent
 
 
 def set_threads(n: int) -> None:

@@ -137,3 +137,4 @@ extern "C" int sva_residual_adapter(const void* hidden, int hidden_dtype, int64_
   SVA_CHECK_LAUNCH("residual_adapter_kernel");
   return SVA_OK;
 }
+

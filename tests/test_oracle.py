@@ -302,3 +302,34 @@ def test_residual_adapter_matches_torch_module():
     for v, expect in ((0.0, 0.0), (40.0, 40.0), (-40.0, 0.0)):
         out = oracle.residual_adapter(one, np.zeros((1, 1)), np.array([[v, 0.0]]), one, 1.0)  # pre-activation v
         assert abs(out[0, 0] - expect) < 1e-12
+
+
+def test_kmeans_update_matches_torch_cpu_step():
+    # the reference's update body run by torch on the CPU (index_add_ sums in row order)
+    import torch
+
+    rng = np.random.default_rng(8)
+    N, C, sub = 500, 16, 8
+    x = rng.standard_normal((N, sub)).astype(np.float32)
+    labels = rng.integers(0, C - 2, N)  # cells C-2, C-1 empty: they keep their centroid
+    cent = rng.standard_normal((C, sub)).astype(np.float32)
+    w = rng.random(N).astype(np.float32) + 0.1
+    xt, lt, ct, wt = map(torch.from_numpy, (x, labels, cent, w))
+    sums = torch.zeros(C, sub)
+    sums.index_add_(0, lt, xt)
+    counts = torch.bincount(lt, minlength=C)
+    want = ct.clone()
+    ne = counts > 0
+    want[ne] = sums[ne] / counts[ne].float()[:, None]
+    got = oracle.kmeans_update(x, labels, cent)
+    np.testing.assert_array_equal(got.view(np.uint32), want.numpy().view(np.uint32))
+    np.testing.assert_array_equal(got[C - 2:], cent[C - 2:])
+    sums = torch.zeros(C, sub)
+    sums.index_add_(0, lt, xt * wt[:, None])
+    counts = torch.zeros(C)
+    counts.index_add_(0, lt, wt)
+    want = ct.clone()
+    ne = counts > 0
+    want[ne] = sums[ne] / counts[ne, None]
+    got = oracle.kmeans_update(x, labels, cent, w)
+    np.testing.assert_array_equal(got.view(np.uint32), want.numpy().view(np.uint32))
