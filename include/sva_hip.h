@@ -110,7 +110,8 @@ int sva_pq_scores(const float *lut, const void *codes, int code_type, int64_t co
  * Replaces sva/llama.py:270-292 (product_quantized_scores, masked topk(L),
  * candidate_counts, gather of k_low and the rank-score sum).
  *   k_low    (h, row, r) at h*k_low_head_stride + row*R + r, fp32
- *   mask     (t, n) at t*mask_tok_stride + n (single sequence only), or NULL
+ *   mask     (t, n) at t*mask_tok_stride + n with n the sequence-local key, the same
+ *            rows for every sequence (equal-length batches), or NULL
  *   sl_idx   [items, L] key indices of the shortlist (first sl_count[item] valid)
  *   sl_rank  [items, L] their rank scores sum(k_low * q_low) / sqrt(R)
  *   sl_count [items] = min(L, #allowed keys)

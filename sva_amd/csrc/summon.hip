@@ -218,7 +218,6 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   SVA_REQUIRE(mask_type >= 0 && mask_type <= 4, "%s: bad mask type", fn);
   SVA_REQUIRE(mask_type == SVA_MASK_NONE || mask_type == SVA_MASK_BOOL || mask != nullptr,
               "%s: mask type given without a mask", fn);
-  SVA_REQUIRE(mask_type == SVA_MASK_NONE || n_seq == 1, "%s: masks apply to a single sequence", fn);
   SVA_REQUIRE(R != 64 || (((uintptr_t)k_low & 15u) == 0 && k_low_head_stride % 4 == 0),
               "%s: k_low must be 16-byte aligned", fn);
   const int64_t items = n_seq * H * Q;

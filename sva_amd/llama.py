@@ -152,10 +152,12 @@ class SVALlamaAttention(nn.Module):
 
         batch, n_heads, q_len, head_dim = query.shape
         k_len = key.shape[2]
-        if batch != 1:
-            raise ValueError("SVA Llama adapter currently expects batch size 1.")
         kernels.require_device(query, key, value)
         mode = self.serving.summon_mode
+        if batch != 1:
+            if mode != "scan":
+                raise ValueError("SVA Llama adapter runs batches larger than 1 in summon_mode='scan' only.")
+            return self._scan_attention_batched(query, key, value, attention_mask)
         static_decode = mode == "inverted_static" and q_len == 1
         profile = self.serving.profile_components and static_decode
         outer = {}
@@ -236,6 +238,99 @@ class SVALlamaAttention(nn.Module):
             self.stats.add_device_rows(int(self.layer_idx or 0), (("summoned",), ("exact_scored", "verified")),
                                        plan.counts, {"queries": float(heads)})
         return out
+
+    def _scan_attention_batched(self, query, key, value, attention_mask):
+        """Scan mode for a batch of B equal-length sequences (the reference
+        decodes batch 1): one packed launch per stage for the whole batch.
+        The catalog holds sequence b at rows [b * cap, b * cap + N); K and V
+        are read in place from the cache [B, G, N, D] (row offsets b * G * N
+        for a contiguous cache).  Every sequence must share the attention
+        mask (no padding)."""
+
+        batch, heads, q_len, head_dim = query.shape
+        k_len = key.shape[2]
+        device = query.device
+        k_low, codes, cap = self._key_catalog_batched(key, q_len)
+        shortlist = min(self.serving.coarse_shortlist, k_len)
+        budget = min(self.serving.budget, shortlist)
+        mask = None
+        if attention_mask is not None:
+            m = attention_mask[..., :q_len, :k_len]
+            if m.shape[0] > 1 and q_len > 1 and not torch.equal(m[1:], m[:1].expand_as(m[1:])):
+                raise ValueError("Batched SVA attention needs the same attention mask for every sequence (no padding).")
+            mask = m[:1]
+        if key.stride(0) % key.stride(2) != 0 or value.stride() != key.stride() or key.stride(-1) != 1:
+            key, value = key.contiguous(), value.contiguous()
+        rows_per_seq = key.stride(0) // key.stride(2)
+        rows = (batch - 1) * rows_per_seq + k_len
+        keys = torch.as_strided(key, (key.shape[1], rows, head_dim), (key.stride(1), key.stride(2), 1),
+                                key.storage_offset())
+        values = torch.as_strided(value, (value.shape[1], rows, head_dim), (value.stride(1), value.stride(2), 1),
+                                  value.storage_offset())
+        seq = torch.arange(batch, device=device, dtype=torch.int64)
+        cat_off, kv_off = seq * cap, seq * rows_per_seq
+        lens = torch.full((batch,), k_len, device=device, dtype=torch.int64)
+        chunk = self.serving.query_chunk_size
+        if chunk is None:
+            chunk = 128 if (q_len >= 4096 or shortlist >= 2048) else q_len
+        chunk = max(1, int(chunk))
+        outs = []
+        for qs in range(0, q_len, chunk):
+            qe = min(q_len, qs + chunk)
+            if mask is not None:
+                m = mask[..., qs:qe, :]
+            elif qe - qs == q_len:
+                m = None  # the kernels' causal rule
+            else:
+                pos = torch.arange(k_len - q_len + qs, k_len - q_len + qe, device=device)
+                keep = torch.arange(k_len, device=device)[None, :] <= pos[:, None]
+                m = torch.zeros(keep.shape, device=device).masked_fill_(~keep, float("-inf"))
+            qc = query[:, :, qs:qe, :]
+            q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks)
+            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, k_len, shortlist,
+                                                                       budget, mask=m, seq_offsets=cat_off,
+                                                                       seq_lens=lens)
+            outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, rows, self.scaling, out_dtype=query.dtype,
+                                       seq_offsets=kv_off, seq_lens=lens))
+            if self.stats is not None:
+                self.stats.add_device(int(self.layer_idx or 0), {
+                    "summoned": sl_count, "exact_scored": fin_count, "verified": fin_count,
+                    "queries": float(sl_count.numel())})
+        return outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)
+
+    def _key_catalog_batched(self, key: torch.Tensor, q_len: int):
+        """The catalog of a batch of equal-length sequences (sva/llama.py:578-624
+        per sequence): appended when every cache grew by at most q_len rows,
+        rebuilt otherwise.  Returns (k_low, codes, cap)."""
+
+        batch, _, k_len, head_dim = key.shape
+        heads, rank = self.sva_q_proj.shape[0], self.sva_q_proj.shape[2]
+        subspaces, codewords = self.sva_coarse_codebooks.shape[1], self.sva_coarse_codebooks.shape[2]
+        sig = ("batch", batch, key.device, key.dtype, heads, head_dim, rank)
+        same = self._signature == sig and self._k_low is not None
+        can_append = (same and self._key_len > 0 and k_len > self._key_len and k_len - self._key_len <= max(q_len, 1)
+                      and q_len < k_len)
+        cap = self._k_low.shape[1] // batch if same else 0
+        if k_len > cap:
+            new_cap = max(k_len, 2 * cap, 256)
+            k_low = torch.empty(heads, batch * new_cap, rank, device=key.device, dtype=torch.float32)
+            codes = torch.empty(heads, batch * new_cap, subspaces, device=key.device, dtype=_code_dtype(codewords))
+            if can_append:
+                for b in range(batch):
+                    k_low[:, b * new_cap:b * new_cap + self._key_len].copy_(
+                        self._k_low[:, b * cap:b * cap + self._key_len])
+                    codes[:, b * new_cap:b * new_cap + self._key_len].copy_(
+                        self._codes[:, b * cap:b * cap + self._key_len])
+            self._k_low, self._codes, cap = k_low, codes, new_cap
+        start = self._key_len if can_append else 0
+        for b in range(batch):
+            kernels.write_encode(key[b], self.sva_k_proj, self.sva_coarse_codebooks,
+                                 self._k_low[:, b * cap:(b + 1) * cap], self._codes[:, b * cap:(b + 1) * cap], start,
+                                 k_len - start)
+        self._key_len = self._codes_len = k_len
+        self._postings = None
+        self._signature = sig
+        return self._k_low, self._codes, cap
 
     # ------------------------------------------------------------------
     def _ensure_capacity(self, rows: int, device: torch.device) -> None:

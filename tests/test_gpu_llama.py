@@ -175,3 +175,41 @@ def test_full_budget_equals_dense_attention(device, mode):
     for r, g in zip(ref_logits, got_logits):
         err = (r - g).abs().max().item() / r.abs().max().item()
         assert err < 2e-4, f"{mode}: logits differ by {err}"
+
+
+@pytest.mark.parametrize("attn", ["eager", "sdpa"])
+def test_batch_of_sequences_equals_each_alone(device, attn):
+    # batch 3 through the packed scan path == each sequence decoded on its own
+    # (a shortlist / budget well below the cache, so the selection matters)
+    heads, kv_heads, head_dim, n_tok = 4, 2, 64, 48
+    model = make_tiny_model(device, hidden=heads * head_dim, heads=heads, kv_heads=kv_heads, attn=attn, seed=5)
+    bundle = make_tiny_bundle(heads=heads, head_dim=head_dim, rank=64, subspaces=2, codewords=16, shortlist=24,
+                              budget=8)
+    g = torch.Generator().manual_seed(9)
+    prompts = torch.randint(0, 64, (3, n_tok), generator=g).to(device)
+    steps = torch.randint(0, 64, (3, 3), generator=g).to(device)
+    with torch.no_grad(), patch_llama_attention(model, bundle, summon_mode="scan") as handle:
+        out = model(input_ids=prompts, use_cache=True)
+        batched, past = [out.logits], out.past_key_values
+        for j in range(steps.shape[1]):
+            out = model(input_ids=steps[:, j:j + 1], use_cache=True, past_key_values=past)
+            batched.append(out.logits)
+            past = out.past_key_values
+        for b in range(3):
+            handle.reset_catalogs()
+            out = model(input_ids=prompts[b:b + 1], use_cache=True)
+            single, past = [out.logits], out.past_key_values
+            for j in range(steps.shape[1]):
+                out = model(input_ids=steps[b:b + 1, j:j + 1], use_cache=True, past_key_values=past)
+                single.append(out.logits)
+                past = out.past_key_values
+            for r, s in zip(batched, single):
+                err = (r[b] - s[0]).abs().max().item() / s.abs().max().item()
+                assert err < 1e-4, f"sequence {b}: logits differ by {err}"
+
+
+def test_batch_needs_scan_mode(device):
+    model = make_tiny_model(device)
+    with torch.no_grad(), patch_llama_attention(model, make_tiny_bundle(), summon_mode="inverted_static"):
+        with pytest.raises(ValueError, match="summon_mode='scan'"):
+            model(input_ids=torch.tensor([[1, 2, 3], [4, 5, 6]], device=device), use_cache=False)
