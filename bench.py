@@ -49,10 +49,13 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
-    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged"),
+    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged", "socket"),
                     help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA; "
                          "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched; "
-                         "ragged: continuous-batch static inverted decode over packed sequences")
+                         "ragged: continuous-batch static inverted decode over packed sequences; "
+                         "socket: batch-8 decode with SVA and residual adapters in the last four layers")
+    ap.add_argument("--socket-prefill", type=int, default=32768, help="socket suite: prompt tokens per sequence")
+    ap.add_argument("--socket-batch", type=int, default=8, help="socket suite: sequences")
     ap.add_argument("--batch", type=int, default=32, help="ragged suite: sequences per batch")
     ap.add_argument("--pool", type=int, default=48, help="ragged suite: resident sequences batches are drawn from")
     ap.add_argument("--reshuffle", type=int, default=16, help="ragged suite: steps between batch reshuffles")
@@ -363,6 +366,107 @@ def ragged_suite(args):
     }), flush=True)
 
 
+def socket_suite(args):
+    """Late-layer socket on a SmolLM2-135M-architecture decoder (random init,
+    bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64): full attention in
+    layers 0-25, SVA (scan, shortlist 8192 / budget 2048, synthetic 2x256
+    artifacts) plus a residual output adapter (rank 16, N(0, 0.02) weights,
+    110,592 parameters over the four layers) in layers 26-29, batch
+    --socket-batch.  The --socket-prefill prompt is prefilled with full
+    attention in chunks of 2048 tokens (an SVA prefill scores every prompt
+    token against the whole cache), then 4 untimed and --decode-steps timed
+    greedy decode steps run through the socket; the same model unpatched is
+    timed the same way."""
+
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from sva_amd import adapter as sva_adapter
+    from sva_amd.artifacts import SVAArtifactBundle, SVALayerArtifacts
+    from sva_amd.llama import patch_llama_attention
+
+    device = torch.device("cuda:0")
+    heads, kv_heads, head_dim, rank, subspaces, codewords = 9, 3, 64, 64, 2, 256
+    n_layers, socket = 30, [26, 27, 28, 29]
+    torch.manual_seed(args.seed)
+    config = LlamaConfig(vocab_size=49152, hidden_size=576, intermediate_size=1536, num_hidden_layers=n_layers,
+                         num_attention_heads=heads, num_key_value_heads=kv_heads,
+                         max_position_embeddings=args.socket_prefill + args.decode_steps + 64, rope_theta=100000.0,
+                         tie_word_embeddings=True, attn_implementation="sdpa")
+    model = LlamaForCausalLM(config).to(device=device, dtype=torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(args.seed + 1)
+    arts = {i: SVALayerArtifacts(q_proj=torch.randn(heads, head_dim, rank, generator=g) / 8.0,
+                                 k_proj=torch.randn(heads, head_dim, rank, generator=g) / 8.0,
+                                 logit_scale=torch.zeros(heads),
+                                 coarse_codebooks=torch.randn(heads, subspaces, codewords, rank // subspaces,
+                                                              generator=g),
+                                 train_loss=0.0, hard_loss=0.0)
+            for i in socket}
+    manifest = {"schema_version": 1, "artifact_type": "summon_verify_attention", "rank_dim": rank,
+                "coarse_subspaces": subspaces, "coarse_codewords": codewords, "default_shortlist": 8192,
+                "default_budget": 2048, "layer_count": n_layers, "layers": socket}
+    bundle = SVAArtifactBundle(manifest=manifest, layers=arts)
+    batch = args.socket_batch
+    prompt = torch.randint(0, config.vocab_size, (batch, args.socket_prefill), generator=g).to(device)
+
+    def prefill():
+        past, out = None, None
+        for s0 in range(0, args.socket_prefill, 2048):
+            out = model(input_ids=prompt[:, s0:s0 + 2048], past_key_values=past, use_cache=True)
+            past = out.past_key_values
+        return past, out.logits[:, -1:].argmax(-1)
+
+    def decode(past, tok):
+        for _ in range(4):
+            out = model(input_ids=tok, past_key_values=past, use_cache=True)
+            past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.decode_steps):
+            out = model(input_ids=tok, past_key_values=past, use_cache=True)
+            past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        past, tok = prefill()
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        dense_s = decode(past, tok)
+        del past
+        past, tok = prefill()
+        with patch_llama_attention(model, bundle, shortlist=8192, budget=2048, summon_mode="scan",
+                                   layers=socket) as handle:
+            sva_adapter.wrap_socket_layers_with_adapters(model, socket, rank=16, scale=1.0)
+            for i in socket:
+                a = model.model.layers[i].self_attn
+                torch.nn.init.normal_(a.up.weight, mean=0.0, std=0.02)
+                a.down.weight.requires_grad_(False)
+                a.up.weight.requires_grad_(False)
+            n_params = sum(model.model.layers[i].self_attn.down.weight.numel() +
+                           model.model.layers[i].self_attn.up.weight.numel() for i in socket)
+            sva_s = decode(past, tok)
+            summary = handle.stats.summary()
+            for i in socket:
+                model.model.layers[i].self_attn = model.model.layers[i].self_attn.sva_attn
+    tok_s = batch * args.decode_steps / sva_s
+    print(json.dumps({
+        "metric": "socket decode tok/s (batch, SVA + residual adapter in layers 26-29)", "value": round(tok_s, 1),
+        "unit": "tok/s", "n_gpus": 1, "steps": args.decode_steps, "warmup": 4,
+        "ms_per_step": round(1e3 * sva_s / args.decode_steps, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (fp32 scores)",
+        "data": "synthetic (random-init weights, uniform random prompts, synthetic 2x256 artifacts)",
+        "config": {"workload": f"SmolLM2-135M-shape decoder, batch {batch}, {args.socket_prefill}-token context, "
+                               f"SVA + residual adapter in layers 26-29", "shortlist": 8192, "budget": 2048,
+                   "adapter_parameters": n_params, "intermediate_size": 1536},
+        "dense_attention": {"tok_s": round(batch * args.decode_steps / dense_s, 1), "attention": "torch sdpa, bf16"},
+        "prefill_s_full_attention": round(prefill_s, 3),
+        "sva_stats": {k: round(v, 3) for k, v in summary.items() if isinstance(v, float) and v == v},
+    }), flush=True)
+
+
 def model_suite(args):
     """Decode tokens/s of a SmolLM2-135M-architecture decoder (random init,
     bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64, RoPE theta 1e5)
@@ -442,10 +546,10 @@ def main():
     if args.write_profiles:
         write_profiles(args)
         return
-    if args.suite in ("write", "model", "ragged"):
+    if args.suite in ("write", "model", "ragged", "socket"):
         if args.gpus != 1:
             sys.exit(2)
-        {"write": write_suite, "model": model_suite, "ragged": ragged_suite}[args.suite](args)
+        {"write": write_suite, "model": model_suite, "ragged": ragged_suite, "socket": socket_suite}[args.suite](args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "
