@@ -193,33 +193,42 @@ class SVALlamaAttention(nn.Module):
         q_len = query.shape[2]
         if q_len == 1 and mask is None and query.shape[0] == 1:
             return self._scan_decode(query, keys, values, k_low, codes, k_len, shortlist, budget)
-        chunk = self.serving.query_chunk_size
-        if chunk is None:
-            chunk = 128 if (q_len >= 4096 or shortlist >= 2048) else q_len
-        chunk = max(1, int(chunk))
         outs = []
-        for qs in range(0, q_len, chunk):
-            qe = min(q_len, qs + chunk)
-            if mask is not None:
-                m = mask[..., qs:qe, :]
-            elif qe - qs == q_len:
-                m = None  # the kernels' causal rule: key n for token t iff n <= N - Q + t
-            else:
-                pos = torch.arange(k_len - q_len + qs, k_len - q_len + qe, device=query.device)
-                keep = torch.arange(k_len, device=query.device)[None, :] <= pos[:, None]
-                m = torch.zeros(keep.shape, device=query.device).masked_fill_(~keep, float("-inf"))
+        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist):
             qc = query[:, :, qs:qe, :]
             q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks,
-                                                codes, k_len, shortlist)
-            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, k_len, shortlist,
+                                                codes, n, shortlist)
+            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, n, shortlist,
                                                                        budget, mask=m)
-            outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, k_len, self.scaling,
+            outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, n, self.scaling,
                                        out_dtype=query.dtype))
             if self.stats is not None:
                 self.stats.add_device(int(self.layer_idx or 0), {
                     "summoned": sl_count, "exact_scored": fin_count, "verified": fin_count,
                     "queries": float(sl_count.numel())})
         return outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)
+
+    def _query_chunks(self, query, k_len, mask, shortlist):
+        """(qs, qe, mask, n_keys) per chunk of query tokens (sva/llama.py:221-223,
+        262-268).  Every token's result is independent of the chunking, so the
+        default chunk bounds the per-launch shortlist buffers (about 512 MiB)
+        rather than following the reference's 128.  Without a mask the
+        kernels' causal rule (key n for token t of Q iff n <= N - Q + t) is
+        kept by handing chunk [qs, qe) the first N - Q + qe keys: token qs + t
+        then keeps n <= N - Q + qs + t, as over the whole prompt."""
+
+        n_seq, heads, q_len = query.shape[0], query.shape[1], query.shape[2]
+        chunk = self.serving.query_chunk_size
+        if chunk is None:
+            per_token = n_seq * heads * max(shortlist, 1) * 8
+            chunk = q_len if q_len * per_token <= (512 << 20) else max(128, ((512 << 20) // per_token) // 128 * 128)
+        chunk = max(1, int(chunk))
+        for qs in range(0, q_len, chunk):
+            qe = min(q_len, qs + chunk)
+            if mask is not None:
+                yield qs, qe, mask[..., qs:qe, :], k_len
+            else:
+                yield qs, qe, None, k_len - q_len + qe
 
     def _scan_decode(self, query, keys, values, k_low, codes, k_len, shortlist, budget):
         """One decode token (q = 1, causal): the same three calls through a
@@ -269,25 +278,12 @@ class SVALlamaAttention(nn.Module):
                                   value.storage_offset())
         seq = torch.arange(batch, device=device, dtype=torch.int64)
         cat_off, kv_off = seq * cap, seq * rows_per_seq
-        lens = torch.full((batch,), k_len, device=device, dtype=torch.int64)
-        chunk = self.serving.query_chunk_size
-        if chunk is None:
-            chunk = 128 if (q_len >= 4096 or shortlist >= 2048) else q_len
-        chunk = max(1, int(chunk))
         outs = []
-        for qs in range(0, q_len, chunk):
-            qe = min(q_len, qs + chunk)
-            if mask is not None:
-                m = mask[..., qs:qe, :]
-            elif qe - qs == q_len:
-                m = None  # the kernels' causal rule
-            else:
-                pos = torch.arange(k_len - q_len + qs, k_len - q_len + qe, device=device)
-                keep = torch.arange(k_len, device=device)[None, :] <= pos[:, None]
-                m = torch.zeros(keep.shape, device=device).masked_fill_(~keep, float("-inf"))
+        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist):
+            lens = torch.full((batch,), n, device=device, dtype=torch.int64)
             qc = query[:, :, qs:qe, :]
             q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks)
-            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, k_len, shortlist,
+            _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, n, shortlist,
                                                                        budget, mask=m, seq_offsets=cat_off,
                                                                        seq_lens=lens)
             outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, rows, self.scaling, out_dtype=query.dtype,

@@ -213,3 +213,31 @@ def test_batch_needs_scan_mode(device):
     with torch.no_grad(), patch_llama_attention(model, make_tiny_bundle(), summon_mode="inverted_static"):
         with pytest.raises(ValueError, match="summon_mode='scan'"):
             model(input_ids=torch.tensor([[1, 2, 3], [4, 5, 6]], device=device), use_cache=False)
+
+
+@pytest.mark.parametrize("attn", ["eager", "sdpa"])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_query_chunks_equal_one_pass(device, attn, batch):
+    # A prefill and a multi-token extension split into chunks of 7 query
+    # tokens give what one pass gives (sva/llama.py:262-328 scores every token
+    # on its own); without a mask each chunk sees the first N - Q + chunk_end
+    # keys, which keeps the causal rule.
+    heads, kv_heads, head_dim = 4, 2, 64
+    model = make_tiny_model(device, hidden=heads * head_dim, heads=heads, kv_heads=kv_heads, attn=attn, seed=7)
+    bundle = make_tiny_bundle(heads=heads, head_dim=head_dim, rank=64, subspaces=2, codewords=16, shortlist=24,
+                              budget=8)
+    g = torch.Generator().manual_seed(13)
+    prompt = torch.randint(0, 64, (batch, 45), generator=g).to(device)
+    more = torch.randint(0, 64, (batch, 19), generator=g).to(device)
+    results = []
+    for chunk in (None, 7):
+        with torch.no_grad(), patch_llama_attention(model, bundle, summon_mode="scan", query_chunk_size=chunk) as h:
+            out = model(input_ids=prompt, use_cache=True)
+            ext = model(input_ids=more, use_cache=True, past_key_values=out.past_key_values)
+            results.append((out.logits, ext.logits, h.stats.summary()))
+    (a0, a1, sa), (b0, b1, sb) = results
+    for r, c in ((a0, b0), (a1, b1)):
+        err = (r - c).abs().max().item() / r.abs().max().item()
+        assert err < 1e-5, f"chunked logits differ by {err}"
+    for key in ("queries", "avg_summoned", "avg_verified"):
+        assert sa[key] == sb[key], key
