@@ -35,6 +35,8 @@ struct SummonParams {
 };
 
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
+bool summon_regs_eligible(const SummonParams& p);
+int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);

@@ -9,7 +9,13 @@
 // shortlisted key is rescored against q_low in torch's summation order.
 // Keys live in LDS when they fit, otherwise they are recomputed per pass.
 //
+// Fused item path (summon_regs_kernel): caches of up to 16K keys with a
+// budget run shortlist, rescore and budget in one workgroup per item from
+// registers (the prefill shape).
+//
 // The long-context q=1 path (many workgroups per item) is in summon_wide.hip.
+#include <type_traits>
+
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -152,9 +158,275 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   if (threadIdx.x == 0) p.sl_count[item] = leff;
 }
 
+
+// ---------------------------------------------------------------------------
+// Fused item path for caches of up to 16K keys with a budget (R = 64,
+// L <= 2048): shortlist, rescore and budget in one workgroup per item, the
+// prefill shape (thousands of items of a few thousand keys each).  Thread t
+// holds keys i * BLOCK + t (i < NPT) in registers as unique composites (scan
+// key, key index); a register radix select finds the L-th largest; the
+// shortlist is compacted in ascending key order (per-slot wave ballots and
+// one scan of the wave counts); each DPP row of 16 lanes rescores shortlisted
+// rows in torch's sum order, REG_ROWS rows in flight; the budget is a second
+// register select over the shortlist's (rank key, key index) composites,
+// compacted in shortlist order, which is ascending key order, as the budget
+// select writes it.
+constexpr int REG_MAX_L = 2048;
+constexpr int REG_NW = ITEM_BLOCK / WAVE;
+constexpr int REG_ROWS = 8;  // shortlist rows per DPP row in flight
+
+struct RegLds {
+  int tab, hist, small, shared64, scratch, shared, wbase, slidx, rank, total;
+};
+
+__host__ __device__ inline RegLds reg_lds_layout(int S, int C, int L, int npt) {
+  RegLds l;
+  int o = 0;
+  l.tab = o;
+  o = align16(o + 4 * S * C);
+  l.hist = o;
+  o = align16(o + 4 * TOP_BINS);
+  l.small = o;
+  o = align16(o + 8 * TOP_SMALL);
+  l.shared64 = o;
+  o = align16(o + 8 * 2);
+  l.scratch = o;
+  o = align16(o + 4 * (REG_NW + 1));
+  l.shared = o;
+  o = align16(o + 4 * 4);
+  l.wbase = o;
+  o = align16(o + 4 * npt * REG_NW);
+  l.slidx = o;
+  o = align16(o + 4 * L);
+  l.rank = o;
+  o = align16(o + 4 * L);
+  l.total = o;
+  return l;
+}
+
+template <int NPT, int SB>
+__global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kernel(SummonParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const RegLds Ly = reg_lds_layout(p.S, p.C, p.L, NPT);
+  float* tab = (float*)(lds + Ly.tab);
+  uint32_t* shared = (uint32_t*)(lds + Ly.shared);
+  uint32_t* wbase = (uint32_t*)(lds + Ly.wbase);
+  int32_t* slidx = (int32_t*)(lds + Ly.slidx);
+  float* rank = (float*)(lds + Ly.rank);
+  const TopLds tl{(uint32_t*)(lds + Ly.hist), (uint64_t*)(lds + Ly.small), (uint32_t*)(lds + Ly.scratch), shared,
+                  (uint64_t*)(lds + Ly.shared64)};
+  const int item = blockIdx.x;
+  const int t = item % p.Q;
+  const int h = (item / p.Q) % p.H;
+  const int b = item / (p.Q * p.H);
+  // the host admits N <= NPT * BLOCK and every length is at most N
+  const int64_t len = min(p.lens ? p.lens[b] : p.N, (int64_t)NPT * ITEM_BLOCK);
+  const int64_t off = p.offs ? p.offs[b] : 0;
+  const int SC = p.S * p.C;
+  const float* lsrc = p.lut + (int64_t)item * SC;
+  for (int e = threadIdx.x; e < SC; e += ITEM_BLOCK) tab[e] = lsrc[e];
+  __syncthreads();
+
+  const int64_t code_base = (int64_t)h * p.code_hs + off * p.S;
+  const int64_t causal_last = len - p.Q + t;
+  const int S = p.S, C = p.C;
+  const float sqrt_r = p.sqrt_r;
+  // SB > 0: uint8 codes of SB subspaces, read as one SB-byte load per key,
+  // every load of the thread issued before any is used (e[] holds the raw
+  // code bytes until the composites replace them); SB = 0: any code type
+  uint64_t e[NPT];
+  uint32_t okm = 0;  // bit i: key i * BLOCK + t is allowed
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int64_t n = (int64_t)i * ITEM_BLOCK + threadIdx.x;
+    const bool ok = n < len && (p.mask_type == MASK_NONE ? n <= causal_last
+                                                         : mask_allows(p.mask, (int64_t)t * p.mask_ts + n, p.mask_type));
+    okm |= (ok ? 1u : 0u) << i;
+    e[i] = 0ull;
+  }
+  if constexpr (SB > 0) {
+    using Word = typename std::conditional<SB == 1, uint8_t,
+                 typename std::conditional<SB == 2, uint16_t, uint32_t>::type>::type;
+    const Word* cw = (const Word*)((const uint8_t*)p.codes + code_base);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+      if ((okm >> i) & 1u) e[i] = cw[(int64_t)i * ITEM_BLOCK + threadIdx.x];
+  }
+  uint64_t vor = 0ull, vand = ~0ull;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const int64_t n = (int64_t)i * ITEM_BLOCK + threadIdx.x;
+    if ((okm >> i) & 1u) {
+      float acc = 0.0f;
+      if constexpr (SB > 0) {
+#pragma unroll
+        for (int s = 0; s < SB; ++s) {
+          const int c = (int)((e[i] >> (8 * s)) & 0xFFu);
+          acc = acc + tab[s * C + (c >= C ? C - 1 : c)];
+        }
+      } else {
+        const int64_t row = code_base + n * S;
+        for (int s = 0; s < S; ++s) {
+          int64_t c = load_code(p.codes, row + s, p.ctype);
+          c = c < 0 ? 0 : (c >= C ? C - 1 : c);
+          acc = acc + tab[s * C + c];
+        }
+      }
+      e[i] = composite(f2key(acc / sqrt_r), (uint32_t)n);
+      vor |= e[i];
+      vand &= e[i];
+      ++cnt;
+    }
+  }
+  uint32_t allowed_total;
+  block_excl_scan<ITEM_BLOCK>(cnt, tl.scratch, &allowed_total);
+  const int leff = (int)min((uint32_t)p.L, allowed_total);
+  const int beff = min(p.B, leff);
+  if (threadIdx.x == 0) {
+    p.sl_count[item] = leff;
+    p.fin_count[item] = beff;
+  }
+  if (leff == 0) return;
+  const uint64_t X = leff == (int)allowed_total ? 1ull : select_top_regs<ITEM_BLOCK, NPT>(e, leff, vor, vand, tl);
+
+  // shortlist in ascending key order: slot-major (i, wave, lane) is key order
+  const int lane = lane_id(), wid = (int)threadIdx.x / WAVE;
+  uint64_t m[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    m[i] = __builtin_amdgcn_ballot_w64(e[i] != 0ull && e[i] >= X);
+    if (lane == 0) wbase[i * REG_NW + wid] = (uint32_t)__popcll(m[i]);
+  }
+  __syncthreads();
+  const uint32_t wc = threadIdx.x < NPT * REG_NW ? wbase[threadIdx.x] : 0u;
+  const uint32_t wpre = block_excl_scan<ITEM_BLOCK>(wc, tl.scratch, nullptr);
+  if (threadIdx.x < NPT * REG_NW) wbase[threadIdx.x] = wpre;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    if ((m[i] >> lane) & 1ull) {
+      const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m[i], 0u));
+      const uint32_t pos = wbase[i * REG_NW + wid] + below;
+      if (pos < (uint32_t)leff) slidx[pos] = i * ITEM_BLOCK + (int)threadIdx.x;
+    }
+  }
+  __syncthreads();
+
+  // rescore: DPP row r of 16 lanes takes shortlist entries r, r + 64, ...
+  {
+    const int row16 = (int)threadIdx.x >> 4, g = (int)threadIdx.x & 15;
+    const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * 64)[g];
+    const float* kl = p.k_low + (int64_t)h * p.klow_hs + off * 64;
+    for (int j0 = 0; j0 < leff; j0 += REG_ROWS * 64) {
+      float4 r[REG_ROWS];
+#pragma unroll
+      for (int u = 0; u < REG_ROWS; ++u) {
+        const int j = j0 + u * 64 + row16;
+        const int64_t n = slidx[j < leff ? j : 0];
+        r[u] = reinterpret_cast<const float4*>(kl + n * 64)[g];
+      }
+#pragma unroll
+      for (int u = 0; u < REG_ROWS; ++u) {
+        const int j = j0 + u * 64 + row16;
+        const float d = rank_dot64_row16(r[u], qq);
+        if (g == 0 && j < leff) rank[j] = d / sqrt_r;
+      }
+    }
+  }
+  __syncthreads();
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
+    out_idx[j] = slidx[j];
+    out_rank[j] = rank[j];
+  }
+
+  // budget: top beff by (rank desc, key index asc), ascending key order
+  uint64_t e2[REG_MAX_L / ITEM_BLOCK];
+  uint64_t vor2 = 0ull, vand2 = ~0ull;
+#pragma unroll
+  for (int i = 0; i < REG_MAX_L / ITEM_BLOCK; ++i) {
+    const int j = (int)threadIdx.x + i * ITEM_BLOCK;
+    e2[i] = 0ull;
+    if (j < leff) {
+      e2[i] = composite(f2key(rank[j]), (uint32_t)slidx[j]);
+      vor2 |= e2[i];
+      vand2 &= e2[i];
+    }
+  }
+  const uint64_t X2 = beff == leff ? 1ull
+                                   : select_top_regs<ITEM_BLOCK, REG_MAX_L / ITEM_BLOCK>(
+                                         e2, beff, vor2, vand2, tl, (leff + ITEM_BLOCK - 1) / ITEM_BLOCK);
+  // shortlist slot j = i * BLOCK + t is in ascending key order, so an ordered
+  // compaction of the chosen slots writes the budget in ascending key order
+  constexpr int NB = REG_MAX_L / ITEM_BLOCK;
+  uint64_t m2[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    m2[i] = __builtin_amdgcn_ballot_w64(e2[i] != 0ull && e2[i] >= X2);
+    if (lane == 0) wbase[i * REG_NW + wid] = (uint32_t)__popcll(m2[i]);
+  }
+  __syncthreads();
+  const uint32_t wc2 = threadIdx.x < NB * REG_NW ? wbase[threadIdx.x] : 0u;
+  const uint32_t wpre2 = block_excl_scan<ITEM_BLOCK>(wc2, tl.scratch, nullptr);
+  if (threadIdx.x < NB * REG_NW) wbase[threadIdx.x] = wpre2;
+  __syncthreads();
+  int32_t* out_fin = p.fin_idx + (int64_t)item * p.B;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if ((m2[i] >> lane) & 1ull) {
+      const uint32_t below =
+          __builtin_amdgcn_mbcnt_hi((uint32_t)(m2[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m2[i], 0u));
+      const uint32_t pos = wbase[i * REG_NW + wid] + below;
+      if (pos < (uint32_t)beff) out_fin[pos] = composite_index(e2[i]);
+    }
+  }
+}
+
+template <int NPT, int SB>
+int launch_regs(const SummonParams& p, int64_t items, size_t lds, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)summon_regs_kernel<NPT, SB>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
+                  "hipFuncSetAttribute(summon_regs_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((summon_regs_kernel<NPT, SB>), dim3((unsigned)items), dim3(ITEM_BLOCK), lds, stream, p);
+  SVA_CHECK_LAUNCH("summon_regs_kernel");
+  return SVA_OK;
+}
+
+template <int NPT>
+int launch_regs_codes(const SummonParams& p, int64_t items, size_t lds, hipStream_t stream) {
+  // one load per key for uint8 codes of 1, 2 or 4 subspaces at aligned rows
+  const int64_t S = p.S;
+  const bool u8 = p.ctype == CODE_U8 && (S == 1 || S == 2 || S == 4) && p.code_hs % S == 0 &&
+                  ((uintptr_t)p.codes % (uintptr_t)S) == 0;
+  if (u8 && S == 1) return launch_regs<NPT, 1>(p, items, lds, stream);
+  if (u8 && S == 2) return launch_regs<NPT, 2>(p, items, lds, stream);
+  if (u8 && S == 4) return launch_regs<NPT, 4>(p, items, lds, stream);
+  return launch_regs<NPT, 0>(p, items, lds, stream);
+}
 }  // namespace
 
 namespace sva {
+
+bool summon_regs_eligible(const SummonParams& p) {
+  if (p.B <= 0 || p.R != 64 || p.L > REG_MAX_L || p.N > 16 * ITEM_BLOCK) return false;
+  if (((uintptr_t)p.k_low & 15u) != 0 || p.klow_hs % 4 != 0 || ((uintptr_t)p.q_low & 15u) != 0) return false;
+  return reg_lds_layout(p.S, p.C, p.L, 16).total <= kMaxLds;
+}
+
+int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream) {
+  const int npt = p.N <= 4 * ITEM_BLOCK ? 4 : (p.N <= 8 * ITEM_BLOCK ? 8 : 16);
+  const size_t lds = (size_t)reg_lds_layout(p.S, p.C, p.L, npt).total;
+  if (npt == 4) return launch_regs_codes<4>(p, items, lds, stream);
+  if (npt == 8) return launch_regs_codes<8>(p, items, lds, stream);
+  return launch_regs_codes<16>(p, items, lds, stream);
+}
 
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream) {
   const bool keys_fit = item_lds_layout(p.S, p.C, p.R, p.L, p.N, true).total <= kMaxLds;
@@ -258,6 +530,7 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   if (sva::summon_wide_eligible(p, items)) {
     return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream);
   }
+  if (sva::summon_regs_eligible(p)) return sva::summon_regs_path(p, items, (hipStream_t)stream);
   int rc = sva::summon_item_path(p, items, (hipStream_t)stream);
   if (rc == SVA_OK && B > 0)
     rc = sva::budget_select_launch(sl_idx, sl_rank, sl_count, items, L, B, fin_idx, fin_count, (hipStream_t)stream);
