@@ -13,6 +13,11 @@
 // maximum m, the sum z of exp(score - m) and the exp-weighted V sum.
 // verify_combine: one workgroup per query item merges the slices (all loaded
 // at once, max-rescaled sums) and stores acc / z in the output dtype.
+// Many groups (the prefill shape: thousands of tokens): one workgroup per
+// (sequence, KV head, token) walks all its slices in order instead, keeping
+// a running maximum, exp-sum and weighted V sum per head (each slice's sums
+// rescaled to the new maximum), and stores the output itself: the groups
+// alone fill the GPU, and no slice partials go through HBM.
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -26,6 +31,8 @@ constexpr int EPW = VB / 4;  // union entries per slice
 constexpr int MAX_GRP = 8;
 constexpr int MAX_D = 256;
 constexpr int CB = 256;   // threads per combine workgroup
+constexpr int SEQ_MIN_GROUPS = 2048;  // groups from which one workgroup walks all slices of a group
+constexpr int ACC = (MAX_GRP * MAX_D + VB - 1) / VB;  // (head, dim) outputs per thread, walking form
 
 SVA_DEV int bsearch_i32(const int32_t* a, int n, int32_t x) {
   int lo = 0, hi = n;
@@ -86,14 +93,14 @@ SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[
 // DT: compile-time head_dim (0: runtime p.D, a multiple of 16; -1: any
 // head_dim, elementwise).  Each of the 4 lanes of an entry holds D/4
 // consecutive dimensions of its K and V rows (every 4th one for DT = -1).
-template <int DT>
+template <int DT, bool SEQ>
 __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
   const int D = DT > 0 ? DT : p.D;
   const int grp = p.H / p.G;
-  const int s = blockIdx.x;
-  const int gi = blockIdx.y;
+  const int s = SEQ ? 0 : (int)blockIdx.x;
+  const int gi = SEQ ? (int)blockIdx.x : (int)blockIdx.y;
   const int t = gi % p.Q;
   const int g = (gi / p.Q) % p.G;
   const int b = gi / (p.Q * p.G);
@@ -104,6 +111,7 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   float* wt = vrow + EPW * (D + 1);                   // [EPW][MAX_GRP] scores, then weights
   int* cnt = (int*)(wt + EPW * MAX_GRP);              // [MAX_GRP + 1] prefix of list lengths
   float* stat = (float*)(cnt + MAX_GRP + 1);          // [MAX_GRP][2]
+  float* run = stat + 2 * MAX_GRP;                    // [MAX_GRP][3] running m, z and rescale factor (SEQ)
 
   const int64_t len = p.lens ? p.lens[b] : p.N;
   const int64_t off = p.offs ? p.offs[b] : 0;
@@ -126,8 +134,18 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   }
   __syncthreads();
   const int M = cnt[grp];
-  const int e0 = (int)((int64_t)s * M / p.split);
-  const int n = (int)((int64_t)(s + 1) * M / p.split) - e0;  // <= EPW
+  constexpr int NACC = !SEQ ? 1 : (DT > 0 ? (MAX_GRP * DT + VB - 1) / VB : ACC);
+  float acc_run[NACC];
+#pragma unroll
+  for (int k = 0; k < NACC; ++k) acc_run[k] = 0.0f;
+  if (SEQ && (int)threadIdx.x < grp) {
+    run[3 * threadIdx.x] = -INFINITY;
+    run[3 * threadIdx.x + 1] = 0.0f;
+  }
+  const int n_slices = SEQ ? (M + EPW - 1) / EPW : 1;
+  for (int sl = 0; sl < n_slices; ++sl) {
+  const int e0 = SEQ ? sl * EPW : (int)((int64_t)s * M / p.split);
+  const int n = SEQ ? min(EPW, M - e0) : (int)((int64_t)(s + 1) * M / p.split) - e0;  // <= EPW
   // phase 2: first occurrences of the slice and the heads holding each; the
   // 4 lanes of an entry search lists qt and qt + 4.  The 4 lanes of an entry
   // share a wave, so the entry state stays in registers.
@@ -208,31 +226,69 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
     }
   }
   __syncthreads();
-  // phase 4: per head, max and exp-sum over the slice (one wave per head)
+  // phase 4: per head, max and exp-sum over the slice (one wave per head);
+  // walking all slices, the maximum is the running one and the running sums
+  // are rescaled to it
   const int wid = threadIdx.x / WAVE;
   for (int j = wid; j < grp; j += VB / WAVE) {
     const int r = lane_id();
     const float sc = r < n ? wt[r * MAX_GRP + j] : -INFINITY;
-    const float m = wave_max(sc);
+    const float m_old = SEQ ? run[3 * j] : -INFINITY;
+    const float m = fmaxf(wave_max(sc), m_old);
     const float e = (m == -INFINITY || sc == -INFINITY) ? 0.0f : expf(sc - m);
     wt[r * MAX_GRP + j] = e;
     const float z = wave_sum(e);
     if (r == 0) {
-      stat[2 * j] = m;
-      stat[2 * j + 1] = z;
+      if (SEQ) {
+        const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m);
+        run[3 * j] = m;
+        run[3 * j + 1] = run[3 * j + 1] * f + z;
+        run[3 * j + 2] = f;
+      } else {
+        stat[2 * j] = m;
+        stat[2 * j + 1] = z;
+      }
     }
   }
   __syncthreads();
   // phase 5: exp-weighted V sums, one (head, dim) per thread
-  for (int e = threadIdx.x; e < grp * D; e += VB) {
-    const int j = e / D, d = e - j * D;
-    float acc = 0.0f;
-    for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * (D + 1) + d];
-    float* dst = p.part + ((item0 + (int64_t)j * p.Q) * p.split + s) * (D + 2);
-    dst[2 + d] = acc;
-    if (d == 0) {
-      dst[0] = stat[2 * j];
-      dst[1] = stat[2 * j + 1];
+  if (SEQ) {
+#pragma unroll
+    for (int k = 0; k < NACC; ++k) {
+      const int e = (int)threadIdx.x + k * VB;
+      if (e < grp * D) {
+        const int j = e / D, d = e - j * D;
+        float acc = 0.0f;
+        for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * (D + 1) + d];
+        acc_run[k] = acc_run[k] * run[3 * j + 2] + acc;
+      }
+    }
+    __syncthreads();  // the next slice overwrites the rows and weights
+  } else {
+    for (int e = threadIdx.x; e < grp * D; e += VB) {
+      const int j = e / D, d = e - j * D;
+      float acc = 0.0f;
+      for (int r = 0; r < n; ++r) acc = acc + wt[r * MAX_GRP + j] * vrow[r * (D + 1) + d];
+      float* dst = p.part + ((item0 + (int64_t)j * p.Q) * p.split + s) * (D + 2);
+      dst[2 + d] = acc;
+      if (d == 0) {
+        dst[0] = stat[2 * j];
+        dst[1] = stat[2 * j + 1];
+      }
+    }
+  }
+  }  // slices
+  if (SEQ) {
+#pragma unroll
+    for (int k = 0; k < NACC; ++k) {
+      const int e = (int)threadIdx.x + k * VB;
+      if (e < grp * D) {
+        const int j = e / D, d = e - j * D;
+        const float m = run[3 * j], z = run[3 * j + 1];
+        const float v = (m > -INFINITY && z > 0.0f) ? acc_run[k] / z : 0.0f;
+        const int64_t o = (int64_t)b * p.o_bs + (int64_t)(g * grp + j) * p.o_hs + (int64_t)t * p.o_ts + d;
+        store_elem(p.out, o, p.out_dtype, v);
+      }
     }
   }
 }
@@ -296,27 +352,38 @@ int verify_split(int64_t grp, int64_t B) {
 size_t verify_lds_bytes(int64_t grp, int64_t B, int64_t D) {
   return sizeof(int32_t) * grp * B + sizeof(float) * grp * D + sizeof(float) * EPW * (D + 1) +
          sizeof(float) * EPW * MAX_GRP + sizeof(int) * (MAX_GRP + 1) +
-         sizeof(float) * 2 * MAX_GRP + 16;
+         sizeof(float) * 5 * MAX_GRP + 16;
 }
 
-template <int DT>
+template <int DT, bool SEQ>
 int launch_part(const VerifyParams& p, dim3 grid, size_t lds, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)verify_part_kernel<DT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      sva::kMaxLds),
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)verify_part_kernel<DT, SEQ>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
                   "hipFuncSetAttribute(verify_part_kernel)");
     attr_set = true;
   }
-  hipLaunchKernelGGL(verify_part_kernel<DT>, grid, dim3(VB), lds, stream, p);
+  hipLaunchKernelGGL((verify_part_kernel<DT, SEQ>), grid, dim3(VB), lds, stream, p);
   SVA_CHECK_LAUNCH("verify_part_kernel");
   return SVA_OK;
 }
+
+template <bool SEQ>
+int launch_part_dim(const VerifyParams& p, dim3 grid, size_t lds, hipStream_t stream) {
+  if (p.D == 64) return launch_part<64, SEQ>(p, grid, lds, stream);
+  if (p.D == 128) return launch_part<128, SEQ>(p, grid, lds, stream);
+  if (p.D % 16 == 0) return launch_part<0, SEQ>(p, grid, lds, stream);
+  return launch_part<-1, SEQ>(p, grid, lds, stream);
+}
+
+bool verify_walks_slices(int64_t n_seq, int64_t G, int64_t Q) { return n_seq * G * Q >= SEQ_MIN_GROUPS; }
 
 }  // namespace
 
 extern "C" size_t sva_verify_workspace_bytes(int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B) {
   if (n_seq <= 0 || H <= 0 || G <= 0 || Q <= 0 || D <= 0 || B <= 0 || H % G != 0) return 0;
+  if (verify_walks_slices(n_seq, G, Q)) return 256;  // no slice partials
   return sizeof(float) * (size_t)(n_seq * H * Q) * (size_t)verify_split(H / G, B) * (size_t)(D + 2) + 256;
 }
 
@@ -376,12 +443,9 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.o_bs = out_seq_stride;
   p.o_hs = out_head_stride;
   p.o_ts = out_tok_stride;
-  const dim3 grid((unsigned)split, (unsigned)(n_seq * G * Q));
-  int rc = SVA_OK;
-  if (D == 64) rc = launch_part<64>(p, grid, lds, (hipStream_t)stream);
-  else if (D == 128) rc = launch_part<128>(p, grid, lds, (hipStream_t)stream);
-  else if (D % 16 == 0) rc = launch_part<0>(p, grid, lds, (hipStream_t)stream);
-  else rc = launch_part<-1>(p, grid, lds, (hipStream_t)stream);
+  if (verify_walks_slices(n_seq, G, Q))
+    return launch_part_dim<true>(p, dim3((unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
+  int rc = launch_part_dim<false>(p, dim3((unsigned)split, (unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
   if (rc != SVA_OK) return rc;
   hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,
                      (hipStream_t)stream, p);

@@ -136,3 +136,54 @@ def test_budget_select_matches_oracle(device, L, B, distinct):
         want = np.sort(idx[it, :c][keep])
         assert fcnt[it] == len(want)
         np.testing.assert_array_equal(fin[it, :len(want)], want)
+
+
+@pytest.mark.parametrize("D,H,G,Q,dtype", [(64, 9, 3, 700, torch.float32), (64, 9, 3, 700, torch.bfloat16),
+                                           (128, 8, 2, 1030, torch.float32), (40, 6, 3, 690, torch.float32)])
+def test_verify_many_tokens_walks_slices(device, D, H, G, Q, dtype):
+    # 2048 or more (KV head, token) groups: one workgroup walks all slices of
+    # its group with a running maximum; checked against the oracle per item
+    # and against the same tokens verified in calls of 16 tokens (the
+    # slice-split form with its combine kernel)
+    from sva_amd import kernels
+
+    rng = np.random.default_rng(D + Q)
+    n, budget = 3000, 512
+    grp = H // G
+    fin = np.zeros((H, Q, budget), np.int32)
+    counts = np.zeros((H, Q), np.int64)
+    for t in range(Q):
+        c = rng.integers(0, budget + 1, H)
+        c[0] = budget
+        if t % 7 == 0:
+            c[:] = 0 if t % 14 == 0 else c  # some tokens with no entries at all
+        counts[:, t] = c
+        fin[:, t] = _lists(rng, H, G, n, budget, c, overlap=0.5)
+    q = rng.standard_normal((1, H, Q, D)).astype(np.float32)
+    keys = rng.standard_normal((G, n, D)).astype(np.float32)
+    values = rng.standard_normal((G, n, D)).astype(np.float32)
+    kt, vt, qt = (torch.from_numpy(a).to(device, dtype) for a in (keys, values, q))
+    fin_t = torch.from_numpy(fin.reshape(H * Q, budget)).to(device)
+    cnt_t = torch.from_numpy(counts.reshape(H * Q).astype(np.int32)).to(device)
+    out = kernels.verify(qt, kt, vt, fin_t, cnt_t, n, D ** -0.5).float().cpu().numpy()
+    parts = []
+    for t0 in range(0, Q, 16):
+        t1 = min(Q, t0 + 16)
+        sel = (np.arange(H)[:, None] * Q + np.arange(t0, t1)[None, :]).reshape(-1)
+        sel_t = torch.from_numpy(sel).to(device)
+        parts.append(kernels.verify(qt[:, :, t0:t1], kt, vt, fin_t[sel_t].contiguous(), cnt_t[sel_t].contiguous(), n,
+                                    D ** -0.5).float().cpu().numpy())
+    split = np.concatenate(parts, axis=2)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    kq, vq, qq = kt.float().cpu().numpy(), vt.float().cpu().numpy(), qt.float().cpu().numpy()
+    scale = np.maximum(np.abs(split).max(axis=-1, keepdims=True), 1e-30)
+    assert np.all(np.abs(out - split) / scale <= tol), "walking form differs from the split form"
+    for h in range(H):
+        for t in list(range(0, Q, 37)) + [Q - 1]:
+            c = int(counts[h, t])
+            if c == 0:
+                assert np.all(out[0, h, t] == 0)
+                continue
+            ref = oracle.verify(qq[0, h, t], kq[h // grp], vq[h // grp], fin[h, t, :c], D ** -0.5)
+            err = np.abs(out[0, h, t] - ref).max() / np.abs(ref).max()
+            assert err <= tol, f"head {h} token {t}: rel err {err}"
