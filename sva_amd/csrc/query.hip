@@ -205,6 +205,119 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   }
 }
 
+// Many query tokens per head (prefill): one workgroup per MT consecutive
+// tokens of one (sequence, head).  The head's map is staged in LDS once for
+// all of them; thread e keeps codebook row e (SUB floats) in registers and
+// forms table entry e for every token; q_low, the table and the bounds are
+// the same fma chains and folds as in query_lut_kernel (no sampled floor:
+// the per-item summon does not use one).
+constexpr int MT = 32;          // tokens per workgroup
+constexpr int MT_BLOCK = 512;
+
+template <int SUB>
+__global__ void __launch_bounds__(MT_BLOCK) query_lut_multi_kernel(LutParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int tiles = (p.Q + MT - 1) / MT;
+  const int bh = blockIdx.x / tiles;
+  const int t0 = (blockIdx.x - bh * tiles) * MT;
+  const int h = bh % p.H;
+  const int b = bh / p.H;
+  const int nt = min(MT, p.Q - t0);
+  float* W = (float*)lds;                    // [D * R]
+  float* qf = W + D * R;                     // [MT][D]
+  float* ql = qf + MT * D;                   // [MT][R]
+  uint32_t* kmin = (uint32_t*)(ql + MT * R);  // [MT][S]
+  uint32_t* kmax = kmin + MT * S;            // [MT][S]
+  const int t = threadIdx.x;
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * D * R);
+    for (int i = t; i < D * R / 4; i += MT_BLOCK) reinterpret_cast<float4*>(W)[i] = w4[i];
+  }
+  const int64_t qb = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
+  for (int e = t; e < nt * D; e += MT_BLOCK) {
+    const int tt = e / D, d = e - tt * D;
+    qf[e] = load_elem(p.q, qb + (int64_t)(t0 + tt) * p.q_ts + d, p.q_dtype);
+  }
+  for (int e = t; e < MT * S; e += MT_BLOCK) {
+    kmin[e] = 0xFFFFFFFFu;
+    kmax[e] = 0u;
+  }
+  __syncthreads();
+  const int64_t item0 = ((int64_t)b * p.H + h) * p.Q + t0;
+  const float sc = p.scale[h];
+  for (int e = t; e < nt * R; e += MT_BLOCK) {
+    const int tt = e / R, r = e - tt * R;
+    const float* qq = qf + tt * D;
+    float acc = 0.0f;
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qq[d], W[d * R + r], acc);
+    const float v = acc * sc;
+    ql[e] = v;
+    p.q_low[(item0 + tt) * R + r] = v;
+  }
+  __syncthreads();
+  const bool wave_subspace = C % WAVE == 0;
+  for (int e = t; e < S * C; e += MT_BLOCK) {  // uniform trip count when S * C is a multiple of the block
+    const int s = e / C;
+    float w[SUB];
+    const float4* row = reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB);
+#pragma unroll
+    for (int j = 0; j < SUB / 4; ++j) {
+      const float4 v = row[j];
+      w[4 * j] = v.x, w[4 * j + 1] = v.y, w[4 * j + 2] = v.z, w[4 * j + 3] = v.w;
+    }
+    for (int tt = 0; tt < nt; ++tt) {
+      const float* qs = ql + tt * R + s * SUB;
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(qs[j], w[j], acc);
+      p.lut[(item0 + tt) * S * C + e] = acc;
+      uint32_t kn = f2key(acc), kx = kn;
+      if (wave_subspace) {
+        for (int off = 32; off > 0; off >>= 1) {
+          kn = min(kn, (uint32_t)__shfl_xor((int)kn, off, WAVE));
+          kx = max(kx, (uint32_t)__shfl_xor((int)kx, off, WAVE));
+        }
+        if (lane_id() == 0) {
+          atomicMin(&kmin[tt * S + s], kn);
+          atomicMax(&kmax[tt * S + s], kx);
+        }
+      } else {
+        atomicMin(&kmin[tt * S + s], kn);
+        atomicMax(&kmax[tt * S + s], kx);
+      }
+    }
+  }
+  __syncthreads();
+  if (t < nt) {
+    float lo = 0.0f, hi = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      lo = lo + key2f(kmin[t * S + s]);
+      hi = hi + key2f(kmax[t * S + s]);
+    }
+    float* rg = p.range + (item0 + t) * 4;
+    rg[0] = lo;
+    rg[1] = hi;
+    rg[2] = -INFINITY;
+    rg[3] = 0.0f;
+  }
+}
+
+template <int SUB>
+int launch_lut_multi(const LutParams& p, int64_t blocks, size_t lds, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)query_lut_multi_kernel<SUB>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
+                  "hipFuncSetAttribute(query_lut_multi_kernel)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(query_lut_multi_kernel<SUB>, dim3((unsigned)blocks), dim3(MT_BLOCK), lds, stream, p);
+  SVA_CHECK_LAUNCH("query_lut_multi_kernel");
+  return SVA_OK;
+}
+
 constexpr int SCORE_BLOCK = 256;
 
 __global__ void __launch_bounds__(SCORE_BLOCK)
@@ -295,6 +408,15 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   p.code_hs = code_head_stride;
   p.n_keys = n_keys;
   p.shortlist = shortlist;
+  // many tokens per head: the head's weights are staged once per MT tokens
+  const int64_t sub = R / S;
+  const size_t mlds = sizeof(float) * (size_t)(D * R + MT * D + MT * R) + sizeof(uint32_t) * (size_t)(2 * MT * S);
+  if (Q >= 8 && !sample && (sub == 16 || sub == 32 || sub == 64) && mlds <= (size_t)sva::kMaxLds) {
+    const int64_t blocks = n_seq * H * ((Q + MT - 1) / MT);
+    if (sub == 16) return launch_lut_multi<16>(p, blocks, mlds, (hipStream_t)stream);
+    if (sub == 32) return launch_lut_multi<32>(p, blocks, mlds, (hipStream_t)stream);
+    return launch_lut_multi<64>(p, blocks, mlds, (hipStream_t)stream);
+  }
   hipLaunchKernelGGL(query_lut_kernel, dim3((unsigned)items), dim3(PREP_BLOCK), lds, (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("query_lut_kernel");
   return SVA_OK;

@@ -120,3 +120,25 @@ def test_fused_item_packed_sequences(device):
     offs = torch.tensor([0, 4000], device=device, dtype=torch.int64)
     lens = torch.tensor(lens_list, device=device, dtype=torch.int64)
     _run(device, codes, k_low, q, q_proj, scale, cb, max(lens_list), 2048, 512, offs=offs, lens=lens)
+
+
+@pytest.mark.parametrize("S,C,Q,dtype", [(2, 256, 75, torch.bfloat16), (4, 64, 40, torch.float32),
+                                         (1, 256, 9, torch.float16), (4, 48, 33, torch.float32)])
+def test_query_lut_many_tokens_matches_per_token(device, S, C, Q, dtype):
+    # 8 or more tokens per head take the multi-token table kernel (weights
+    # staged once per 32 tokens); every output equals the per-token kernel's
+    from sva_amd import kernels
+
+    H, D, R = 3, 64, 64
+    rng = np.random.default_rng(S * C + Q)
+    q = torch.from_numpy(rng.standard_normal((2, H, Q, D)).astype(np.float32)).to(device, dtype)
+    q_proj = torch.from_numpy((rng.standard_normal((H, D, R)) / 8).astype(np.float32)).to(device)
+    scale = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).to(device)
+    cb = torch.from_numpy(rng.standard_normal((H, S, C, R // S)).astype(np.float32)).to(device)
+    q_low, lut, rng_out = kernels.query_lut(q, q_proj, scale, cb)
+    for t in range(Q):
+        ql1, lut1, rg1 = kernels.query_lut(q[:, :, t:t + 1], q_proj, scale, cb)
+        assert torch.equal(q_low[:, :, t:t + 1].view(torch.int32), ql1.view(torch.int32)), f"q_low token {t}"
+        assert torch.equal(lut[:, :, t:t + 1].view(torch.int32), lut1.view(torch.int32)), f"table token {t}"
+        assert torch.equal(rng_out[:, :, t:t + 1, :2].view(torch.int32), rg1[..., :2].view(torch.int32)), f"bounds {t}"
+        assert torch.all(rng_out[:, :, t, 2] == float("-inf"))
