@@ -300,6 +300,8 @@ class ScanDecodePlan:
         self.fin_idx = torch.empty(items, budget, device=self.device, dtype=i32)
         self.fin_count = self.counts[1]
         self._lib = lib()
+        self._ws, self._ws_keys = None, -1  # summon workspace, sized for caches of up to _ws_keys keys
+        self._vws, self._vws_kv = None, -1  # verify workspace (independent of the cache length)
 
     def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,
             mask=None):
@@ -313,8 +315,13 @@ class ScanDecodePlan:
                               shortlist, self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), stream),
               "sva_query_lut")
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
-        ws_bytes = int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
-        ws = workspace(self.device, ws_bytes)
+        if n_keys > self._ws_keys:
+            # the summon workspace grows with the key count: sized for the next
+            # multiple of 64K keys, so a decode loop re-queries it rarely
+            self._ws_keys = (n_keys + 65535) // 65536 * 65536
+            self._ws = workspace(self.device, int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, self._ws_keys,
+                                                                                shortlist)), "plan")
+        ws = self._ws
         check(L.sva_summon_select(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(), codes.data_ptr(),
                                   code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), None, None,
                                   n_seq, heads, q_len, n_keys, rank, subspaces, codewords, shortlist, ptr(m), mtype,
@@ -323,8 +330,11 @@ class ScanDecodePlan:
                                   ws.numel(), stream), "sva_summon_select")
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
-        vws = workspace(self.device, int(L.sva_verify_workspace_bytes(n_seq, heads, keys.shape[0], q_len, head_dim,
-                                                                        budget)), "verify")
+        if self._vws is None or self._vws_kv != keys.shape[0]:
+            self._vws_kv = keys.shape[0]
+            self._vws = workspace(self.device, int(L.sva_verify_workspace_bytes(n_seq, heads, keys.shape[0], q_len,
+                                                                                  head_dim, budget)), "verify")
+        vws = self._vws
         check(L.sva_verify(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), keys.data_ptr(),
                            values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1), None, None, n_keys,
                            self.fin_idx.data_ptr(), self.fin_count.data_ptr(), n_seq, heads, keys.shape[0], q_len,

@@ -53,27 +53,32 @@ class SVAStats:
     def add_device_rows(self, layer_idx: int, names: tuple[tuple[str, ...], ...], counts: torch.Tensor,
                         host: dict[str, float] | None = None) -> None:
         """Accumulate the row sums of a device count matrix `counts` [rows,
-        n]: row i adds to every statistic named in names[i].  Two small
-        device kernels per call, no sync."""
+        n]: row i adds to every statistic named in names[i].  One small
+        device kernel per call (an int64 running matrix), no sync."""
 
-        total = counts.sum(dim=1, dtype=torch.float64)
         key = (layer_idx, names)
         slot = self._pending_rows.get(key)
-        if slot is None:
-            self._pending_rows[key] = total
+        if slot is None or slot.shape != counts.shape:
+            if slot is not None:
+                self._fold_rows(key, slot)
+            self._pending_rows[key] = counts.to(torch.int64)
         else:
-            slot.add_(total)
+            slot.add_(counts)  # one launch; the rows are summed when the statistics are read
         if host:
             self.add(layer_idx, host)
+
+    def _fold_rows(self, key: tuple[int, tuple[tuple[str, ...], ...]], mat: torch.Tensor) -> None:
+        layer_idx, names = key
+        for row_names, v in zip(names, mat.sum(dim=1).tolist()):
+            for name in row_names:
+                self._totals[name] += float(v)
+                self._by_layer[layer_idx][name] += float(v)
 
     def _flush(self) -> None:
         if self._pending_rows:
             rows, self._pending_rows = self._pending_rows, {}
-            for (layer_idx, names), vec in rows.items():
-                for row_names, v in zip(names, vec.tolist()):
-                    for key in row_names:
-                        self._totals[key] += v
-                        self._by_layer[layer_idx][key] += v
+            for key, mat in rows.items():
+                self._fold_rows(key, mat)
         if not self._pending:
             return
         pending, self._pending = self._pending, {}
