@@ -86,10 +86,11 @@ class Layer:
 def algorithmic_bytes(n_keys, heads, subspaces, codewords, shortlist, budget, rank=64, head_dim=64, kv_elem=2):
     scan = heads * n_keys * subspaces
     lut = heads * subspaces * codewords * 4
+    query = heads * (head_dim * rank + codewords * rank) * 4  # q_proj [D, R] and codebooks [S, C, R/S] per head
     rescore = heads * shortlist * rank * 4
     verify = heads * budget * head_dim * kv_elem * 2
-    return {"scan": scan, "lut": lut, "rescore": rescore, "verify": verify,
-            "summon": scan + lut + rescore, "total": scan + lut + rescore + verify}
+    return {"scan": scan, "lut": lut, "query": query, "rescore": rescore, "verify": verify,
+            "summon": scan + lut + query + rescore, "total": scan + lut + query + rescore + verify}
 
 
 def cpu_baseline(torch, layer, shortlist, budget, repeats):
@@ -147,7 +148,7 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 SUMMON_KERNELS = ("wide_scan_kernel", "wide_finish_kernel")
 PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel",
                                                          "verify_combine_kernel")
-PROFILE_STEM = "summon_select_decode_1m_{layout}"
+PROFILE_STEM = "lookup_select_decode_1m_{layout}"
 REF_US_PER_QUERY = 1024.0  # the reference's published decode lookup, 1M keys, 4x64, 2048/512 (H100)
 REF_MODEL_TOK_S = 8.05     # the reference's SmolLM2-135M 30-layer SVA decode at 8192 context (H100)
 
@@ -219,10 +220,11 @@ def write_profiles(args):
         if k in SUMMON_KERNELS:
             summon_bytes += b
         lines.append(f"| {k} | {fk:.1f} | {wk:.1f} | {b:,.0f} |")
-    lines += ["", f"sva_summon_select (the wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
+    entry = "sva_lookup_select" if args.layout == "4x64" else "sva_summon_select"
+    lines += ["", f"{entry} (the wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
     (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
     (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
-        {"entry_point": "sva_summon_select", "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
+        {"entry_point": entry, "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
          "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}) + "\n")
     print(f"wrote profiles/{stem}_*.md/json")
 
@@ -574,10 +576,12 @@ def main():
     layers = [Layer(torch, device, n, subspaces, codewords, args.seed + n * 13 + 101 + 7919 * i)
               for i in range(args.layers)]
     strategy = _lib.lib().sva_summon_strategy(1, heads, 1, n, 64, subspaces, codewords, args.shortlist, 0, 0)
+    # sva_lookup_select computes the query side inside the scan for 4x64 codes on the wide path
+    fused = strategy == 1 and (subspaces, codewords) == (4, 64)
     shortlist = min(args.shortlist, n)
     budget = min(args.budget, shortlist)
     scaling = 64 ** -0.5
-    stages = ("query_lut", "summon", "verify")
+    stages = ("lookup", "verify")
 
     plan = kernels.ScanDecodePlan(device, 1, heads, 1, 64, 64, subspaces, codewords, shortlist, budget)
     outs = [torch.empty(1, heads, 1, 64, device=device, dtype=torch.bfloat16) for _ in layers]
@@ -588,17 +592,13 @@ def main():
                  layer.values, n, scaling, out=outs[i % len(layers)])
 
     def step_staged(i, ev):
-        # the same three calls with an event between stages (per-stage times)
+        # the same calls with an event between the lookup (query side, shortlist, budget) and the verifier
         layer = layers[i % len(layers)]
         ev[0].record()
-        q_low, lut, rng = kernels.query_lut(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, n,
-                                            shortlist)
+        plan.summon(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, layer.k_low, n)
         ev[1].record()
-        _, _, _, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, layer.codes, layer.k_low, n, shortlist,
-                                                            budget)
+        plan.verify(layer.q, layer.keys, layer.values, n, scaling, out=outs[i % len(layers)])
         ev[2].record()
-        kernels.verify(layer.q, layer.keys, layer.values, fin_idx, fin_count, n, scaling)
-        ev[3].record()
 
     if args.calibrate_copy:
         src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=device).fill_(1)
@@ -638,7 +638,7 @@ def main():
     gpu_us = sum(per_stage_us.values())
 
     bytes_ = algorithmic_bytes(n, heads, subspaces, codewords, shortlist, budget)
-    summon_us = per_stage_us["summon"]
+    summon_us = per_stage_us["lookup"]
     achieved = bytes_["summon"] / (summon_us * 1e-6) / 1e9
     traffic = None
     pmc = ROOT / "profiles" / (PROFILE_STEM.format(layout=args.layout) + "_traffic.json")
@@ -675,8 +675,10 @@ def main():
         "gpu_us_per_query": round(gpu_us, 2),
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": ("sva_summon_select: wide_scan + wide_finish" if strategy == 1
-                       else "sva_summon_select: summon_item_kernel + budget_select_kernel"),
+            "kernel": ("sva_lookup_select: wide_scan (query side fused) + wide_finish"
+                       if strategy == 1 and fused else
+                       "sva_query_lut + sva_summon_select: query_lut + wide_scan + wide_finish" if strategy == 1
+                       else "sva_query_lut + sva_summon_select: query_lut + summon_item + budget_select"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -16,12 +16,6 @@ using namespace sva;
 namespace {
 
 constexpr int PREP_BLOCK = 1024;
-constexpr int SAMPLE_BLOCKS = 16;       // contiguous sample blocks spread over the cache
-constexpr int SAMPLE_KEYS = 128;        // keys per sample block
-constexpr int SAMPLE_BINS = 1024;       // one per thread
-constexpr double SAMPLE_TARGET = 3.5;   // sampled threshold aims at ~3.5x the shortlist above it
-constexpr int SAMPLE_MAX_S = 8;         // subspaces of the sampled scan
-constexpr int N_SAMPLE = SAMPLE_BLOCKS * SAMPLE_KEYS;
 constexpr int SPT = N_SAMPLE / PREP_BLOCK;  // samples per thread
 static_assert(SAMPLE_BINS == PREP_BLOCK && SPT * PREP_BLOCK == N_SAMPLE, "sampling layout");
 

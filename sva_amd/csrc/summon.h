@@ -7,6 +7,18 @@ namespace sva {
 
 constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
+// Sampled shortlist-floor estimate of a single-query uint8 scan (the query
+// table kernel and the fused lookup compute it alike): SAMPLE_BLOCKS
+// contiguous blocks of SAMPLE_KEYS keys spread over the cache, a histogram of
+// their sums over SAMPLE_BINS bins, and the bin of the k-th largest, k ~
+// SAMPLE_TARGET * L * samples / N.
+constexpr int SAMPLE_BLOCKS = 16;
+constexpr int SAMPLE_KEYS = 128;
+constexpr int SAMPLE_BINS = 1024;
+constexpr double SAMPLE_TARGET = 3.5;
+constexpr int SAMPLE_MAX_S = 8;  // subspaces of the sampled scan
+constexpr int N_SAMPLE = SAMPLE_BLOCKS * SAMPLE_KEYS;
+
 struct SummonParams {
   const float* lut;    // [items, S*C]
   const float* range;  // [items, 4]: bounds of any scan sum, sampled floor, 0
@@ -34,13 +46,29 @@ struct SummonParams {
   int32_t* fin_count;
 };
 
+// Query side of the fused lookup (sva_lookup_select): the scan computes the
+// item's q_low, table, bounds and sampled floor itself and writes them to
+// q_low / lut / range.
+struct FusedQuery {
+  const void* q;
+  int q_dtype;
+  int64_t q_hs;  // head stride of q (one sequence, one token)
+  int64_t D;
+  const float* q_proj;
+  const float* scale;
+  const float* codebooks;
+  int sample_k;  // rank of the sampled floor among the samples; 0: no sampled floor
+};
+
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
+bool summon_wide_fused_eligible(const SummonParams& p, const FusedQuery& f);
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const FusedQuery* f = nullptr);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);
 
 inline int next_pow2_host(int x) {

@@ -9,6 +9,9 @@
 //                 reaches the item's sampled floor t_lo to its wave's own
 //                 candidate list as a unique 64-bit composite (score key,
 //                 key index); counts go to the wave's own counter words.
+//                 In the fused lookup (sva_lookup_select, 4x64 codes) each
+//                 scan workgroup first computes its item's q_low, table,
+//                 bounds and sampled floor itself (FusedPrologue).
 //   wide_finish   one workgroup per item.  Gathers the candidates (~4x the
 //                 shortlist for the sampled floor) into LDS, selects the L
 //                 largest composites exactly (shortlist), scores them with
@@ -53,6 +56,7 @@ struct WideArgs {
   uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
   float* cand_rank;  // [items, W * NW, WAVE_KEYS] rank score of each listed candidate
   int W;             // scan workgroups per item
+  FusedQuery f;      // fused lookup: the query side (p.q_low, p.lut, p.range are its outputs)
 };
 
 SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
@@ -96,14 +100,15 @@ SVA_DEV void load_chunk(const uint8_t* __restrict__ codes, int cs, int ce, u32x4
 }
 
 // Per-query tables for the scan, in LDS.  SMALLC (C <= 64): a pair table of
-// subspaces 0 and 1, entry c0 + 64 c1 = T0[c0] + T1[c1], and 64-entry tables
-// of the other subspaces; the pair sum equals the reference's (0 + T0) + T1
-// up to the sign of a zero, which f2key folds.  Otherwise 256-entry tables.
+// subspaces 0 and 1, entry c0 + 64 c1 = T0[c0] + T1[c1], then the 64-entry
+// tables of every subspace (the scan reads those of subspaces 2..); the pair
+// sum equals the reference's (0 + T0) + T1 up to the sign of a zero, which
+// f2key folds.  Otherwise 256-entry tables.
 // Entries past C repeat entry C - 1, so every code stays in bounds.
 template <int S, bool SMALLC>
 struct ScanTables {
   static constexpr int PAIR = (SMALLC && S >= 2) ? 4096 : 0;
-  static constexpr int SINGLE = SMALLC ? (S >= 2 ? S - 2 : 1) * 64 : S * 256;  // entries of the single tables
+  static constexpr int SINGLE = SMALLC ? S * 64 : S * 256;  // entries of the single tables
   static constexpr int LDS_FLOATS = PAIR + SINGLE;
   static constexpr int NP = PAIR / WB;                 // pair entries per thread
   static constexpr int NS = (SINGLE + WB - 1) / WB;    // single entries per thread
@@ -125,7 +130,7 @@ struct ScanTables {
       const int e = t + k * WB;
       ts[k] = 0.0f;
       if (e < SINGLE) {
-        if (SMALLC) ts[k] = src[((S >= 2 ? 2 : 0) + (e >> 6)) * p.C + min(e & 63, cm)];
+        if (SMALLC) ts[k] = src[(e >> 6) * p.C + min(e & 63, cm)];
         else ts[k] = src[(e >> 8) * p.C + min(e & 255, cm)];
       }
     }
@@ -170,14 +175,14 @@ SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, SMALLC>& T, float
         const uint32_t word = raw[j >> 2];
         const int sh = 8 * (j & 3);
         const uint32_t off = ((sh == 0 ? word << 2 : word >> (sh - 2)) & 0xFCu) +
-                             (uint32_t)(4 * (ScanTables<S, SMALLC>::PAIR + (S >= 2 ? s - 2 : 0) * 64));
+                             (uint32_t)(4 * (ScanTables<S, SMALLC>::PAIR + s * 64));
         const float v = T.at_byte(off);
         a = (S >= 2 || s > 0) ? a + v : v;
       }
     } else {
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const float v = T.tab[s * 256 + byte_of(raw, k * S + s)];  // SINGLE = S * 256 here
+        const float v = T.tab[s * 256 + byte_of(raw, k * S + s)];  // PAIR = 0 here
         a = s == 0 ? v : a + v;
       }
     }
@@ -291,12 +296,12 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
 // Rank scores of a scan wave's nc candidates (keys in the LDS list while
 // they fit, else from the wave's candidate list): one 16-lane DPP row per
 // candidate, 16 candidates in flight per wave; written beside the list.
-SVA_DEV void rank_candidates(const SummonParams& p, int item, const uint32_t* keys, const uint64_t* out,
-                             float* rank, uint32_t nc) {
+// qq: floats 4j .. 4j + 3 of the item's q_low for lane j of each DPP row.
+SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint32_t* keys,
+                             const uint64_t* out, float* rank, uint32_t nc) {
 #pragma clang fp contract(off)
   const int j = lane_id() & 15;
   const int row = lane_id() >> 4;
-  const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[j];
   const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
   if (nc > (uint32_t)KL_CAP) __threadfence();  // keys past the LDS list are read back from `out`
   constexpr int RU = 4;
@@ -318,10 +323,175 @@ SVA_DEV void rank_candidates(const SummonParams& p, int item, const uint32_t* ke
   }
 }
 
+// LDS of the fused prologue beside the scan tables.
+struct FusedLds {
+  float qf[64];
+  __align__(16) float ql[64];
+  uint32_t kmin[8], kmax[8];
+  uint32_t misc[4];
+  uint32_t scratch[NW + 2];
+};
+
+// Query side of the fused lookup for one item, computed by every scan
+// workgroup of the item (D = R = 64, 4x64 codes) with the arithmetic
+// of sva_query_lut: q_low by a sequential fma chain over d times the scale,
+// each table entry by a sequential fma chain over its subspace, the bounds of
+// any sum folded over s, and the sampled floor from the same samples and
+// histogram; tables and floors are therefore bit-identical to the two-call
+// path.  issue() starts the loads (before the chunk's codes); build() leaves
+// the scan tables in LDS and returns the floor.  The item's first workgroup
+// writes q_low, the table and the bounds to global memory.
+template <int S>
+struct FusedPrologue {
+  static constexpr int SUB = 64 / S;         // floats per codebook row
+  static constexpr int ROWS = S * 64 / WB;   // table entries (codebook rows) per thread
+  static constexpr int SPT = N_SAMPLE / WB;  // sampled keys per thread
+  static constexpr int SW = S / 4;           // 32-bit words of codes per key
+  static_assert(ROWS * SUB == 16 && S * 64 <= 2 * WB && SAMPLE_BINS == 4 * WB, "fused prologue layout");
+  float4 w[4];   // floats 16 t .. 16 t + 15 of the head's map q_proj[h] ([D][R])
+  float4 cb[4];  // codebook rows t + k * WB
+  uint32_t smp[SPT][SW];
+  float qv, sc;
+  SVA_DEV void issue(const WideArgs& a, int item) {
+    const FusedQuery& f = a.f;
+    const int t = threadIdx.x;
+    const int h = item % a.p.H;
+    const float4* w4 = reinterpret_cast<const float4*>(f.q_proj + (int64_t)h * 64 * 64);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = w4[4 * t + i];
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+      const float4* c4 = reinterpret_cast<const float4*>(f.codebooks + ((int64_t)h * S * 64 + t + k * WB) * SUB);
+#pragma unroll
+      for (int i = 0; i < SUB / 4; ++i) cb[k * (SUB / 4) + i] = c4[i];
+    }
+    qv = t < 64 ? load_elem(f.q, (int64_t)h * f.q_hs + t, f.q_dtype) : 0.0f;
+    sc = f.scale[h];
+    if (f.sample_k > 0) {
+      const uint8_t* head = (const uint8_t*)a.p.codes + (int64_t)h * a.p.code_hs;
+      const int64_t N = a.p.N;
+#pragma unroll
+      for (int u = 0; u < SPT; ++u) {
+        const int i = t + u * WB;
+        const int blk = i / SAMPLE_KEYS;
+        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(head + (n0 + i % SAMPLE_KEYS) * S);
+#pragma unroll
+        for (int j = 0; j < SW; ++j) smp[u][j] = src[j];
+      }
+    }
+  }
+  SVA_DEV float build(const WideArgs& a, int item, bool first, float* tab, FusedLds& L) {
+#pragma clang fp contract(off)
+    const FusedQuery& f = a.f;
+    const int t = threadIdx.x;
+    constexpr int PAIR = 4096;
+    // 1. map and query into LDS (the map in the pair table's place)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(tab)[4 * t + i] = w[i];
+    if (t < 64) L.qf[t] = qv;
+    if (t == 0) L.misc[0] = 0u;  // floor bin 0 unless the samples place it
+    __syncthreads();
+    // 2. q_low, one lane per output
+    if (t < 64) {
+      float acc = 0.0f;
+#pragma unroll 16
+      for (int d = 0; d < 64; ++d) acc = __builtin_fmaf(L.qf[d], tab[d * 64 + t], acc);
+      const float v = acc * sc;
+      L.ql[t] = v;
+      if (first) const_cast<float*>(a.p.q_low)[(int64_t)item * 64 + t] = v;
+    }
+    __syncthreads();
+    // 3. table entries (every wave's 64 entries share a subspace), per-subspace
+    // bounds, histogram cleared (the map is no longer read)
+    float* raw = tab + PAIR;
+    uint32_t* hist = reinterpret_cast<uint32_t*>(tab);
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+      const int e = t + k * WB;
+      const int s = e >> 6;
+      const float* row = reinterpret_cast<const float*>(&cb[k * (SUB / 4)]);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(L.ql[s * SUB + j], row[j], acc);
+      raw[e] = acc;
+      if (first) const_cast<float*>(a.p.lut)[(int64_t)item * S * 64 + e] = acc;
+      uint32_t kn = f2key(acc), kx = kn;
+      for (int off = 32; off > 0; off >>= 1) {
+        kn = min(kn, (uint32_t)__shfl_xor((int)kn, off, WAVE));
+        kx = max(kx, (uint32_t)__shfl_xor((int)kx, off, WAVE));
+      }
+      if (lane_id() == 0) {
+        L.kmin[s] = kn;
+        L.kmax[s] = kx;
+      }
+    }
+    reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    // 4. bounds of any sum, in the scan's order
+    float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      lo = lo + key2f(L.kmin[s]);
+      hi = hi + key2f(L.kmax[s]);
+    }
+    // 5. sampled floor: the histogram bin of the k-th largest sampled sum
+    float t_lo = -INFINITY;
+    const int k = f.sample_k;
+    if (k > 0 && hi > lo) {
+      const float inv_w = (float)SAMPLE_BINS / (hi - lo);
+#pragma unroll
+      for (int u = 0; u < SPT; ++u) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int c = min((int)((smp[u][s >> 2] >> (8 * (s & 3))) & 0xFFu), 63);
+          acc = acc + raw[s * 64 + c];
+        }
+        int bin = (int)((acc - lo) * inv_w);
+        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
+        atomicAdd(&hist[bin], 1u);
+      }
+      __syncthreads();
+      // thread t holds bins SAMPLE_BINS - 1 - 4 t - j (j = 0..3), from the top
+      uint32_t c[4], mine = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = hist[SAMPLE_BINS - 1 - 4 * t - j];
+        mine += c[j];
+      }
+      uint32_t total;
+      uint32_t above = block_excl_scan<WB>(mine, L.scratch, &total);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (above < (uint32_t)k && above + c[j] >= (uint32_t)k) L.misc[0] = (uint32_t)(SAMPLE_BINS - 1 - 4 * t - j);
+        above += c[j];
+      }
+      __syncthreads();
+      t_lo = lo + (float)L.misc[0] / inv_w;
+    }
+    if (first && t == 0) {
+      float* rg = const_cast<float*>(a.p.range) + (int64_t)item * 4;
+      rg[0] = lo;
+      rg[1] = hi;
+      rg[2] = t_lo;
+      rg[3] = 0.0f;
+    }
+    __syncthreads();  // histogram read before the pair table replaces it
+    // 6. pair table: entry t + k WB = T0[t & 63] + T1[(t >> 6) + 4 k]
+    const float t0 = raw[t & 63];
+#pragma unroll
+    for (int kk = 0; kk < PAIR / WB; ++kk) tab[t + kk * WB] = t0 + raw[64 + (t >> 6) + kk * (WB / 64)];
+    __syncthreads();
+    return t_lo > lo ? t_lo : lo;
+  }
+};
+
 // One scan workgroup's chunk.  CHECK: a partial or masked chunk (every key
-// tested for being allowed, guarded loads).
-template <int S, bool SMALLC, bool CHECK, bool MASKED>
-SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint32_t (*klist)[KL_CAP]) {
+// tested for being allowed, guarded loads).  FUSED: the query side is
+// computed here (FusedPrologue) instead of read.
+template <int S, bool SMALLC, bool CHECK, bool MASKED, bool FUSED>
+SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint32_t (*klist)[KL_CAP], FusedLds& fl) {
 #pragma clang fp contract(off)
   const SummonParams& p = a.p;
   const int h = item % p.H;
@@ -332,19 +502,31 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint
   // tables are stored while the codes stream and each round of codes is
   // scored as soon as its own load lands
   ScanTables<S, SMALLC> T;
-  T.load(p, item);
   u32x4 raw[KEYS_PT * S / 16];
-  load_chunk<S, !CHECK>(codes, cs, ce, raw);
-  T.store(tab_lds);
-  const float t_lo = item_floor(p, item);
-  __syncthreads();  // tables in LDS
+  float t_lo;
+  if constexpr (FUSED) {
+    FusedPrologue<S> F;
+    F.issue(a, item);
+    load_chunk<S, !CHECK>(codes, cs, ce, raw);
+    t_lo = F.build(a, item, w == 0, tab_lds, fl);  // tables in LDS
+    T.tab = tab_lds;
+  } else {
+    T.load(p, item);
+    load_chunk<S, !CHECK>(codes, cs, ce, raw);
+    T.store(tab_lds);
+    t_lo = item_floor(p, item);
+    __syncthreads();  // tables in LDS
+  }
   const int wid = threadIdx.x / WAVE;
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
   scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
-  rank_candidates(p, item, klist[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
+  float4 qq;
+  if constexpr (FUSED) qq = reinterpret_cast<const float4*>(fl.ql)[lane_id() & 15];
+  else qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[lane_id() & 15];
+  rank_candidates(p, item, qq, klist[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane_id() == 0) {
     a.ncand[sub] = wc;
@@ -352,16 +534,19 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint
   }
 }
 
-template <int S, bool SMALLC, bool MASKED>
-__global__ void __launch_bounds__(WB) wide_scan_kernel(WideArgs a) {
+// Five workgroups per CU (at most 102 VGPRs) keep every workgroup of a
+// million-key, nine-head scan resident at once (up to four subspaces).
+template <int S, bool SMALLC, bool MASKED, bool FUSED>
+__global__ void __launch_bounds__(WB, S <= 4 ? 5 : 1) wide_scan_kernel(WideArgs a) {
   __shared__ __align__(16) float tab_lds[ScanTables<S, SMALLC>::LDS_FLOATS];
   __shared__ uint32_t klist[NW][KL_CAP];
+  __shared__ FusedLds fl;
   const int item = blockIdx.x / a.W;
   const int w = blockIdx.x % a.W;
   if (!MASKED && (int64_t)(w + 1) * CHUNK <= a.p.N) {
-    scan_chunk<S, SMALLC, false, false>(a, item, w, tab_lds, klist);
+    scan_chunk<S, SMALLC, false, false, FUSED>(a, item, w, tab_lds, klist, fl);
   } else {
-    scan_chunk<S, SMALLC, true, MASKED>(a, item, w, tab_lds, klist);
+    scan_chunk<S, SMALLC, true, MASKED, FUSED>(a, item, w, tab_lds, klist, fl);
   }
 }
 
@@ -796,9 +981,10 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   finish_budget<NPB>(p, item, leff, beff, e2, rb ? b_hi : vor, rb ? b_lo : vand, rb, tl, wcnt, scratch);
 }
 
-template <int S, bool SMALLC, bool MASKED>
+template <int S, bool SMALLC, bool MASKED, bool FUSED = false>
 int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED, FUSED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream,
+                     a);
   SVA_CHECK_LAUNCH("wide_scan_kernel");
   static bool attr_set = false;
   if (!attr_set) {
@@ -848,7 +1034,17 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
 }
 
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+bool summon_wide_fused_eligible(const SummonParams& p, const FusedQuery& f) {
+  if (!summon_wide_eligible(p, p.H) || p.offs != nullptr || p.Q != 1) return false;
+  if (f.D != 64 || p.R != 64 || p.C != 64 || p.S != 4) return false;
+  if (p.mask_type != MASK_NONE && p.mask_type != MASK_BOOL) return false;  // every key allowed
+  if (f.q_dtype < 0 || f.q_dtype > 2 || f.q == nullptr || f.scale == nullptr) return false;
+  if (((uintptr_t)f.q_proj & 15u) != 0 || ((uintptr_t)f.codebooks & 15u) != 0) return false;
+  return true;
+}
+
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const FusedQuery* f) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const size_t need = summon_wide_workspace_bytes(1, p.H, 1, p.N, p.L);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
@@ -861,6 +1057,10 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   a.nallow = a.ncand + items * a.W * NW;
   a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
   a.cand_rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
+  if (f != nullptr) {
+    a.f = *f;
+    return launch_wide<4, true, false, true>(a, items, stream);
+  }
   // a bool mask allows every key (the reference's `mask > -1e4` rule)
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
   switch (p.S) {

@@ -229,6 +229,47 @@ def summon_select(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist:
     return sl_idx, sl_rank, sl_count, fin_idx, fin_count
 
 
+def lookup_select(q, q_proj, scale, codebooks, codes, k_low, n_keys: int, shortlist: int, budget: int,
+                  mask: torch.Tensor | None = None):
+    """Query side and summon of one decode token in one call (sva/llama.py:211, sva/ops.py:50-71,
+    sva/llama.py:276-302): (q_low, lut, score_range, sl_idx, sl_rank, sl_count, fin_idx, fin_count), equal to
+    query_lut followed by summon_select.  q: [1, H, 1, D] or [H, 1, D]."""
+
+    q = _as_query(q)
+    q_proj, scale, codebooks = _f32c(q_proj), _f32c(scale), _f32c(codebooks)
+    n_seq, heads, q_len, head_dim = q.shape
+    if n_seq != 1 or q_len != 1:
+        raise ValueError("lookup_select takes one token of one sequence")
+    rank = q_proj.shape[-1]
+    subspaces, codewords = codebooks.shape[1], codebooks.shape[2]
+    if tuple(q_proj.shape) != (heads, head_dim, rank):
+        raise ValueError(f"q_proj shape {tuple(q_proj.shape)} != {(heads, head_dim, rank)}")
+    _check_catalog("codes", codes, heads, subspaces)
+    _check_catalog("k_low", k_low, heads, rank)
+    device = require_device(q, q_proj, scale, codebooks, codes, k_low, mask)
+    f32, i32 = torch.float32, torch.int32
+    q_low = torch.empty(1, heads, 1, rank, device=device, dtype=f32)
+    lut = torch.empty(1, heads, 1, subspaces, codewords, device=device, dtype=f32)
+    rng = torch.empty(1, heads, 1, 4, device=device, dtype=f32)
+    sl_idx = torch.empty(heads, shortlist, device=device, dtype=i32)
+    sl_rank = torch.empty(heads, shortlist, device=device, dtype=f32)
+    sl_count = torch.empty(heads, device=device, dtype=i32)
+    fin_idx = torch.empty(heads, budget, device=device, dtype=i32)
+    fin_count = torch.empty(heads, device=device, dtype=i32)
+    m, mtype, mstride = mask_args(mask, 1, n_keys)
+    ws = workspace(device, int(lib().sva_summon_workspace_bytes(1, heads, 1, n_keys, shortlist)))
+    check(
+        lib().sva_lookup_select(
+            ptr(q), dtype_code(q), q.stride(1), heads, head_dim, rank, subspaces, codewords, ptr(q_proj), ptr(scale),
+            ptr(codebooks), ptr(codes), code_type(codes), codes.stride(0), ptr(k_low), k_low.stride(0), n_keys,
+            shortlist, ptr(m), mtype, mstride, ptr(q_low), ptr(lut), ptr(rng), ptr(sl_idx), ptr(sl_rank),
+            ptr(sl_count), budget, ptr(fin_idx), ptr(fin_count), ptr(ws), ws.numel(), stream_handle(device),
+        ),
+        "sva_lookup_select",
+    )
+    return q_low, lut, rng, sl_idx, sl_rank, sl_count, fin_idx, fin_count
+
+
 def verify(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, fin_idx: torch.Tensor,
            fin_count: torch.Tensor, n_keys: int, scaling: float, out_dtype: torch.dtype | None = None,
            seq_offsets: torch.Tensor | None = None, seq_lens: torch.Tensor | None = None) -> torch.Tensor:
@@ -305,15 +346,17 @@ class ScanDecodePlan:
 
     def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,
             mask=None):
+        """The whole lookup: summon() then verify(); returns the verified output."""
+        self.summon(q, q_proj, scale, codebooks, codes, k_low, n_keys, mask=mask)
+        return self.verify(q, keys, values, n_keys, scaling, out=out)
+
+    def summon(self, q, q_proj, scale, codebooks, codes, k_low, n_keys: int, mask=None) -> None:
+        """Query side, shortlist and budget into the plan's buffers (one C-ABI call for one token of one
+        sequence, sva_lookup_select; otherwise sva_query_lut and sva_summon_select)."""
         n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
         q = _as_query(q)
         L = self._lib
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        check(L.sva_query_lut(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), n_seq, heads, q_len,
-                              head_dim, rank, subspaces, codewords, q_proj.data_ptr(), scale.data_ptr(),
-                              codebooks.data_ptr(), codes.data_ptr(), code_type(codes), codes.stride(0), n_keys,
-                              shortlist, self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), stream),
-              "sva_query_lut")
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
         if n_keys > self._ws_keys:
             # the summon workspace grows with the key count: sized for the next
@@ -322,12 +365,36 @@ class ScanDecodePlan:
             self._ws = workspace(self.device, int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, self._ws_keys,
                                                                                 shortlist)), "plan")
         ws = self._ws
-        check(L.sva_summon_select(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(), codes.data_ptr(),
-                                  code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), None, None,
-                                  n_seq, heads, q_len, n_keys, rank, subspaces, codewords, shortlist, ptr(m), mtype,
-                                  mstride, self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(),
-                                  budget, self.fin_idx.data_ptr(), self.fin_count.data_ptr(), ws.data_ptr(),
-                                  ws.numel(), stream), "sva_summon_select")
+        if n_seq == 1 and q_len == 1:
+            # one token: query side and summon in one call (fused where the shapes allow)
+            check(L.sva_lookup_select(q.data_ptr(), dtype_code(q), q.stride(1), heads, head_dim, rank, subspaces,
+                                      codewords, q_proj.data_ptr(), scale.data_ptr(), codebooks.data_ptr(),
+                                      codes.data_ptr(), code_type(codes), codes.stride(0), k_low.data_ptr(),
+                                      k_low.stride(0), n_keys, shortlist, ptr(m), mtype, mstride,
+                                      self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(),
+                                      self.sl_idx.data_ptr(), self.sl_rank.data_ptr(), self.sl_count.data_ptr(),
+                                      budget, self.fin_idx.data_ptr(), self.fin_count.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), stream), "sva_lookup_select")
+        else:
+            check(L.sva_query_lut(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), n_seq, heads,
+                                  q_len, head_dim, rank, subspaces, codewords, q_proj.data_ptr(), scale.data_ptr(),
+                                  codebooks.data_ptr(), codes.data_ptr(), code_type(codes), codes.stride(0), n_keys,
+                                  shortlist, self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), stream),
+                  "sva_query_lut")
+            check(L.sva_summon_select(self.lut.data_ptr(), self.rng.data_ptr(), self.q_low.data_ptr(),
+                                      codes.data_ptr(), code_type(codes), codes.stride(0), k_low.data_ptr(),
+                                      k_low.stride(0), None, None, n_seq, heads, q_len, n_keys, rank, subspaces,
+                                      codewords, shortlist, ptr(m), mtype, mstride, self.sl_idx.data_ptr(),
+                                      self.sl_rank.data_ptr(), self.sl_count.data_ptr(), budget,
+                                      self.fin_idx.data_ptr(), self.fin_count.data_ptr(), ws.data_ptr(), ws.numel(),
+                                      stream), "sva_summon_select")
+
+    def verify(self, q, keys, values, n_keys: int, scaling: float, out=None):
+        """Exact verifier over the budget lists of the last summon()."""
+        n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
+        q = _as_query(q)
+        L = self._lib
+        stream = torch.cuda.current_stream(self.device).cuda_stream
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
         if self._vws is None or self._vws_kv != keys.shape[0]:

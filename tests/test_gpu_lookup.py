@@ -1,0 +1,121 @@
+"""GPU parity of the one-call decode lookup (sva_lookup_select).
+
+The fused path (4x64 codes, every key allowed) computes the query side inside
+the scan's workgroups; its q_low, table, bounds and sampled floor must equal
+sva_query_lut's bit for bit, and its shortlist and budget those of
+sva_query_lut + sva_summon_select on the same inputs.  Shapes outside the
+fused path run the two calls and must agree the same way.  The fused
+shortlists are also checked as sets against the oracle's top-L on the table.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(device, N, S, C, q_dtype, seed, H=9, R=64, D=64):
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(1, H, 1, D, device=device, generator=g).to(q_dtype)
+    q_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
+    scale = torch.rand(H, device=device, generator=g) + 0.5
+    cb = torch.randn(H, S, C, R // S, device=device, generator=g)
+    codes = torch.randint(0, C, (H, N, S), device=device, generator=g, dtype=torch.int32).to(torch.uint8)
+    k_low = torch.randn(H, N, R, device=device, generator=g)
+    return q, q_proj, scale, cb, codes, k_low
+
+
+def _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B, mask=None):
+    from sva_amd import kernels
+
+    q_low, lut, rng = kernels.query_lut(q, q_proj, scale, cb, codes, N, L)
+    out = kernels.summon_select(lut, rng, q_low, codes, k_low, N, L, B, mask=mask)
+    return (q_low, lut, rng) + tuple(out)
+
+
+def _assert_same(fused, ref):
+    names = ("q_low", "lut", "score_range", "sl_idx", "sl_rank", "sl_count", "fin_idx", "fin_count")
+    f_cnt, r_cnt = fused[5].cpu(), ref[5].cpu()
+    assert torch.equal(f_cnt, r_cnt), "shortlist counts differ"
+    b_cnt = fused[7].cpu()
+    assert torch.equal(b_cnt, ref[7].cpu()), "budget counts differ"
+    for name, a, b in zip(names, fused, ref):
+        a, b = a.cpu(), b.cpu()
+        if name in ("sl_idx", "sl_rank"):
+            for h in range(a.shape[0]):
+                c = int(f_cnt[h])
+                assert torch.equal(a[h, :c], b[h, :c]), f"{name} differs in head {h}"
+        elif name == "fin_idx":
+            for h in range(a.shape[0]):
+                c = int(b_cnt[h])
+                assert torch.equal(a[h, :c], b[h, :c]), f"{name} differs in head {h}"
+        elif name not in ("sl_count", "fin_count"):
+            assert torch.equal(a, b), f"{name} differs"
+
+
+@pytest.mark.parametrize("N,S,C,q_dtype,L,B", [
+    (1 << 20, 4, 64, torch.bfloat16, 2048, 512),   # the million-key decode workload
+    (1 << 20, 4, 64, torch.float32, 512, 128),     # tight budget
+    (40000, 4, 64, torch.bfloat16, 2048, 512),     # partial last chunk
+    (32768, 4, 64, torch.float16, 1024, 256),      # smallest fused cache
+    (1 << 18, 2, 256, torch.bfloat16, 2048, 512),  # outside the fused path: two calls
+    (20000, 4, 64, torch.bfloat16, 2048, 512),     # too short for the wide scan: two calls
+])
+def test_lookup_select_equals_two_calls(N, S, C, q_dtype, L, B):
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    print(f"lookup_select N={N} {S}x{C} {q_dtype} L={L} B={B}", flush=True)
+    q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, q_dtype, seed=N + S)
+    ref = _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B)
+    fused = kernels.lookup_select(q, q_proj, scale, cb, codes, k_low, N, L, B)
+    torch.cuda.synchronize()
+    _assert_same(fused, ref)
+
+
+def test_lookup_select_shortlist_matches_oracle():
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C, L, B = 65536 + 4096, 4, 64, 2048, 512
+    q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=5)
+    q_low, lut, _, sl_idx, sl_rank, sl_count, fin_idx, fin_count = kernels.lookup_select(
+        q, q_proj, scale, cb, codes, k_low, N, L, B)
+    torch.cuda.synchronize()
+    lut_np, codes_np = lut[0, :, 0].cpu().numpy(), codes.cpu().numpy()
+    q_low_np, k_low_np = q_low[0, :, 0].cpu().numpy(), k_low.cpu().numpy()
+    for h in range(q.shape[1]):
+        scores = oracle.pq_scores_from_lut(lut_np[h], codes_np[h], 64)
+        sl = oracle.topk(scores, L)
+        cnt = int(sl_count[h])
+        got = sl_idx[h, :cnt].cpu().numpy().astype(np.int64)
+        assert set(got.tolist()) == set(sl.tolist()), f"head {h}: shortlist set differs"
+        ranks = oracle.rank_scores(k_low_np[h], got, q_low_np[h], 64)
+        assert np.array_equal(sl_rank[h, :cnt].cpu().numpy(), ranks), f"head {h}: rank scores differ"
+        fin = oracle.topk(ranks, B, key_index=got)
+        want = np.sort(got[fin])
+        assert np.array_equal(fin_idx[h, :int(fin_count[h])].cpu().numpy(), want), f"head {h}: budget differs"
+
+
+def test_lookup_select_decode_plan_uses_one_call():
+    """The decode plan's one-token step equals the three-call lookup (query table, summon + budget, verify)."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C, L, B = 1 << 19, 4, 64, 2048, 512
+    q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=11)
+    g = torch.Generator(device=device).manual_seed(12)
+    keys = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    plan = kernels.ScanDecodePlan(device, 1, 9, 1, 64, 64, S, C, L, B)
+    outs = [plan.run(q, q_proj, scale, cb, codes, k_low, keys, values, N, 0.125).clone() for _ in range(2)]
+    _, _, _, _, _, _, fin_idx, fin_count = _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B)
+    ref = kernels.verify(q, keys, values, fin_idx, fin_count, N, 0.125)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, ref)
