@@ -69,13 +69,8 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   // 0. sampled codes (k-th largest of the samples, k ~ SAMPLE_TARGET * L *
   // samples / N; sample blocks start at multiples of 16 keys)
   const int64_t N = p.n_keys;
-  int k = 0;
-  bool sample = false;
-  if (p.codes != nullptr && N >= 4 * (int64_t)N_SAMPLE) {
-    const double want = (double)SAMPLE_TARGET * (double)p.shortlist * (double)N_SAMPLE / (double)N;
-    k = (int)want + 1;
-    sample = k < N_SAMPLE / 2;
-  }
+  const int k = p.codes != nullptr ? sample_floor_rank(p.shortlist, N) : 0;
+  const bool sample = k > 0;
   if (sample) {
     // staged in LDS with the weights: the loads complete by the first barrier
     const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;

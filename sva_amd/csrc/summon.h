@@ -11,13 +11,27 @@ constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 // table kernel and the fused lookup compute it alike): SAMPLE_BLOCKS
 // contiguous blocks of SAMPLE_KEYS keys spread over the cache, a histogram of
 // their sums over SAMPLE_BINS bins, and the bin of the k-th largest, k ~
-// SAMPLE_TARGET * L * samples / N.
-constexpr int SAMPLE_BLOCKS = 16;
-constexpr int SAMPLE_KEYS = 128;
+// max(SAMPLE_TARGET * L, SAMPLE_MIN_CAND) * samples / N.  The floor is only a
+// hint (an overshoot, fewer than L keys above it, costs the slow all-keys
+// select, never a result): the minimum keeps k >= ~12 for small shortlists,
+// where the k-th largest of few samples would overshoot often.
+constexpr int SAMPLE_BLOCKS = 64;
+constexpr int SAMPLE_KEYS = 32;
 constexpr int SAMPLE_BINS = 1024;
 constexpr double SAMPLE_TARGET = 3.5;
+constexpr double SAMPLE_MIN_CAND = 6144.0;
 constexpr int SAMPLE_MAX_S = 8;  // subspaces of the sampled scan
 constexpr int N_SAMPLE = SAMPLE_BLOCKS * SAMPLE_KEYS;
+
+// Rank of the sampled floor among the N_SAMPLE sampled sums for a shortlist
+// of L over n_keys keys; 0: no sampled floor (every key is a candidate).
+__host__ __device__ inline int sample_floor_rank(int64_t L, int64_t n_keys) {
+  if (n_keys < 4 * (int64_t)N_SAMPLE) return 0;
+  double target = SAMPLE_TARGET * (double)L;
+  if (target < SAMPLE_MIN_CAND) target = SAMPLE_MIN_CAND;
+  const int k = (int)(target * (double)N_SAMPLE / (double)n_keys) + 1;
+  return k < N_SAMPLE / 2 ? k : 0;
+}
 
 struct SummonParams {
   const float* lut;    // [items, S*C]

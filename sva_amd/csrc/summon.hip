@@ -587,12 +587,7 @@ extern "C" int sva_lookup_select(const void* q, int q_dtype, int64_t q_head_stri
   SVA_REQUIRE(B > 0 && B <= 8192, "sva_lookup_select: budget %lld out of range (1..8192)", (long long)B);
   SVA_REQUIRE(H > 0 && n_keys >= 0 && L > 0, "sva_lookup_select: bad sizes");
   // the sampled floor of sva_query_lut for one sequence and one token
-  int sample_k = 0;
-  if (code_type == SVA_CODE_U8 && S <= sva::SAMPLE_MAX_S && n_keys >= 4 * (int64_t)sva::N_SAMPLE) {
-    const double want = (double)sva::SAMPLE_TARGET * (double)L * (double)sva::N_SAMPLE / (double)n_keys;
-    const int k = (int)want + 1;
-    if (k < sva::N_SAMPLE / 2) sample_k = k;
-  }
+  const int sample_k = code_type == SVA_CODE_U8 && S <= sva::SAMPLE_MAX_S ? sva::sample_floor_rank(L, n_keys) : 0;
   sva::FusedQuery f;
   f.q = q;
   f.q_dtype = q_dtype;
