@@ -119,3 +119,29 @@ def test_lookup_select_decode_plan_uses_one_call():
     torch.cuda.synchronize()
     for o in outs:
         assert torch.equal(o, ref)
+
+
+@pytest.mark.parametrize("L,B", [(2048, 512), (512, 128), (256, 64)])
+def test_sampled_floor_leaves_a_full_shortlist(L, B):
+    """The sampled floor is a performance hint: an overshoot (fewer than L keys at or above it) sends the
+    finish kernel to its all-keys select (milliseconds instead of microseconds).  On seeded million-key caches
+    the floor must leave at least L keys for every head, small shortlists included (the floor aims at
+    max(3.5 L, 6144) keys), and the lookup must still equal the two-call path."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C = 1 << 20, 4, 64
+    for seed in range(3):
+        print(f"floor L={L} seed={seed}", flush=True)
+        q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=100 + seed)
+        fused = kernels.lookup_select(q, q_proj, scale, cb, codes, k_low, N, L, B)
+        lut, rng = fused[1][0, :, 0], fused[2][0, :, 0]
+        idx = codes.long() + torch.arange(S, device=device).view(1, 1, S) * C
+        sums = torch.zeros(codes.shape[0], N, device=device)
+        for s in range(S):  # the scan's order: ((0 + T0) + T1) + ...
+            sums = sums + torch.gather(lut.reshape(codes.shape[0], S * C), 1, idx[:, :, s])
+        floor = torch.maximum(rng[:, 2], rng[:, 0])
+        above = (sums >= floor[:, None]).sum(1)
+        assert bool((above >= L).all()), f"floor overshoots: {above.tolist()} keys at or above it, L={L}"
+        assert bool((above <= 8 * max(3.5 * L, 6144)).all()), f"floor far too low: {above.tolist()}"
+        _assert_same(fused, _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B))
