@@ -119,23 +119,35 @@ def test_wide_workspace_shared_across_shapes(device):
 
 
 def test_wide_sampled_floor_overshoot(device):
-    # The threshold estimate samples 16 blocks of 128 keys spread evenly over
+    # The threshold estimate samples 64 blocks of 32 keys spread evenly over
     # the cache (block starts rounded down to 16 keys).  Giving exactly those
     # keys the best code of every subspace puts the estimate at the top of
     # the score range, so fewer than L keys reach it and the exact all-keys
     # selection must take over; with L equal to the sample size the rigged
-    # keys alone fill the shortlist.
-    N, S, C, H = 100000, 4, 64, 3
+    # keys alone fill the shortlist.  Both the two-call path and the fused
+    # lookup (which samples the same keys) are checked.
+    from sva_amd import kernels
+
+    N, S, C, H, BLOCKS, KEYS = 100000, 4, 64, 3, 64, 32
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=19)
     ql = oracle.query_low(q, q_proj, scale)[:, 0]
     for h in range(H):
         best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
-        for blk in range(16):
-            n0 = (blk * (N - 128) // 15) & ~15
-            codes[h, n0:n0 + 128] = best
+        for blk in range(BLOCKS):
+            n0 = (blk * (N - KEYS) // (BLOCKS - 1)) & ~15
+            codes[h, n0:n0 + KEYS] = best
     for L in (3000, 2048):
         res = _summon(device, codes, k_low, q, q_proj, scale, cb, L)
         _check(codes, k_low, *res, L)
+        q_low, lut, rng, sl_idx, sl_rank, sl_count, _, _ = kernels.lookup_select(
+            torch.from_numpy(q).to(device), torch.from_numpy(q_proj).to(device), torch.from_numpy(scale).to(device),
+            torch.from_numpy(cb).to(device), torch.from_numpy(codes).to(device), k_low, N, L, 64)
+        torch.cuda.synchronize()
+        floor = np.maximum(rng[0, :, 0, 2].cpu().numpy(), rng[0, :, 0, 0].cpu().numpy())
+        top = np.array([oracle.lut(ql[h], cb[h]).max(axis=1).sum() for h in range(H)], np.float32)
+        assert bool((floor > 0.99 * top).all()), "the rigged samples must put the floor at the top of the range"
+        _check(codes, k_low, q_low[0, :, 0].cpu().numpy(), lut[0, :, 0].cpu().numpy(), sl_idx.cpu().numpy(),
+               sl_rank.cpu().numpy(), sl_count.cpu().numpy(), L)
 
 
 def test_wide_candidates_beyond_lds_stage(device):
