@@ -204,21 +204,6 @@ SVA_DEV bool key_ok(const SummonParams& p, int n, int ce) {
   return ok;
 }
 
-// Exact score of key n from the global table (the reference's order, with the
-// leading 0 + T0 and the division).  Used by the all-keys fallback only.
-SVA_DEV float score_at(const SummonParams& p, const uint8_t* __restrict__ codes, int item, int n) {
-#pragma clang fp contract(off)
-  const float* lut = p.lut + (int64_t)item * p.S * p.C;
-  float acc = 0.0f;
-  for (int s = 0; s < p.S; ++s) {
-    uint32_t c = codes[(int64_t)n * p.S + s];
-    c = c < (uint32_t)p.C ? c : (uint32_t)(p.C - 1);
-    acc = acc + lut[s * p.C + c];
-  }
-  return acc / p.sqrt_r;
-}
-
-
 // Candidate floor of an item: the sampled estimate, or the table minimum
 // (every allowed key is a candidate) when there is none.
 SVA_DEV float item_floor(const SummonParams& p, int item) {
@@ -563,7 +548,8 @@ constexpr size_t kFinHist = 0;                                                  
 constexpr size_t kFinSl = kFinHist + sizeof(uint32_t) * TOP_BINS;               // uint32[FIN_MAX_L]
 constexpr size_t kFinRk = kFinSl + sizeof(uint32_t) * FIN_MAX_L;                // uint64[FIN_MAX_L]
 constexpr size_t kFinSmall = kFinRk + sizeof(uint64_t) * FIN_MAX_L;             // uint64[TOP_SMALL]
-static_assert(kFinSmall + sizeof(uint64_t) * TOP_SMALL <= kFinStage, "finish LDS overlay");
+constexpr size_t kFinLut = kFinSmall + sizeof(uint64_t) * TOP_SMALL;          // float[S * C], all-keys path
+static_assert(kFinLut + sizeof(float) * 8 * 256 <= kFinStage, "finish LDS overlay");
 // small arrays after the staging area (offsets keep every pointer in LDS)
 constexpr size_t kFinWcnt = kFinStage;                                          // uint32[SNW * SNW]
 constexpr size_t kFinScratch = kFinWcnt + sizeof(uint32_t) * SNW * SNW;         // uint32[SNW + 1]
@@ -927,9 +913,22 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     const int h = item % p.H;
     const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
     const int N = (int)p.N;
+    // the item's table in LDS: every pass below rescores every key from it
+    float* lut_l = (float*)(lds + kFinLut);
+    const float* lut_g = p.lut + (int64_t)item * p.S * p.C;
+    for (int e = t; e < p.S * p.C; e += SB) lut_l[e] = lut_g[e];
+    __syncthreads();
+    const int S = p.S, C = p.C;
     auto key_at = [&](int n) -> uint64_t {
       if (!mask_allows(p.mask, n, p.mask_type)) return 0ull;
-      return composite(f2key(score_at(p, codes, item, n)), (uint32_t)n);
+      // the reference's exact score ((0 + T0[c0]) + T1[c1]) + ... then / sqrt(R)
+      float acc = 0.0f;
+      for (int s2 = 0; s2 < S; ++s2) {
+        uint32_t c = codes[(int64_t)n * S + s2];
+        c = c < (uint32_t)C ? c : (uint32_t)(C - 1);
+        acc = acc + lut_l[s2 * C + c];
+      }
+      return composite(f2key(acc / p.sqrt_r), (uint32_t)n);
     };
     auto visit = [&](auto&& f) {
       for (int n = t; n < N; n += SB) {
