@@ -87,3 +87,55 @@ def config1_inputs(seed: int = 20260514):
         "shortlist": 2048,
         "budget": 512,
     }
+
+
+# Inverted-index decode cases recorded from the reference's own
+# _inverted_static_decode_attention / _inverted_decode_attention
+# (tests/golden/make_inverted_golden.py writes inverted_reference.npz).
+# mode, N, tail (static: rows behind the postings), budget, cells, adaptive
+# min / mid budgets (0 = the reference's default), low / high margins,
+# fraction of keys masked out (0: no mask), current row masked, seed.
+INVERTED_CASES = [
+    ("inverted_static", 6000, 10, 128, 8, 0, 0, 0.35, 0.70, 0.0, False, 101),
+    ("inverted_static", 6000, 0, 128, 8, 32, 64, 0.35, 0.70, 0.0, False, 102),
+    ("inverted_static", 6000, 37, 512, 8, 16, 48, 0.35, 0.70, 0.3, False, 103),
+    ("inverted_static", 6000, 63, 64, 8, 1, 2, 0.20, 1.20, 0.0, False, 104),
+    ("inverted_static", 6000, 0, 256, 4, 0, 0, 0.35, 0.70, 0.4, True, 105),
+    ("inverted_static", 6000, 5, 128, 8, 8, 32, 0.60, 1.00, 0.0, False, 106),
+    ("inverted", 6000, 0, 128, 8, 0, 0, 0.35, 0.70, 0.0, False, 201),
+    ("inverted", 6000, 0, 128, 8, 16, 48, 0.35, 0.70, 0.0, False, 202),
+    ("inverted", 6000, 0, 64, 8, 32, 48, 0.20, 1.20, 0.4, True, 203),
+    ("inverted", 6000, 0, 512, 8, 0, 0, 0.35, 0.70, 0.0, False, 204),
+    ("inverted", 6000, 0, 128, 8, 8, 32, 0.60, 1.00, 0.1, False, 207),
+    # almost every key masked: heads whose chosen cells hold no allowed key
+    # fall back to the last allowed row
+    ("inverted", 500, 0, 16, 2, 0, 0, 0.35, 0.70, 0.995, True, 205),
+]
+
+
+def inverted_inputs(seed: int, N: int, mask_frac: float = 0.0, current_masked: bool = False,
+                    H: int = 9, G: int = 3, D: int = 64, R: int = 64, S: int = 2, C: int = 256):
+    """Seeded decode inputs of one token over an N-key catalog (numpy only):
+    q [H, 1, D], keys / values [G, N, D] N(0, 1); q_proj [H, D, R] N(0, 1/64),
+    logit scale field 0.1 * N(0, 1); codebooks [H, S, C, R/S] N(0, 1); the
+    catalog itself drawn directly: k_low [H, N, R] N(0, 1) and codes uniform
+    in [0, C); allowed [N] (mask_frac of the keys masked out, the current
+    row too when current_masked)."""
+
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    out = {
+        "q": rng.standard_normal((H, 1, D)).astype(f),
+        "keys": rng.standard_normal((G, N, D)).astype(f),
+        "values": rng.standard_normal((G, N, D)).astype(f),
+        "q_proj": (rng.standard_normal((H, D, R)) / 8).astype(f),
+        "logit_scale": (0.1 * rng.standard_normal(H)).astype(f),
+        "codebooks": rng.standard_normal((H, S, C, R // S)).astype(f),
+        "k_low": rng.standard_normal((H, N, R)).astype(f),
+        "codes": rng.integers(0, C, (H, N, S)).astype(np.uint8),
+    }
+    allowed = rng.random(N) >= mask_frac
+    if current_masked:
+        allowed[N - 1] = False
+    out["allowed"] = allowed
+    return out

@@ -1,5 +1,5 @@
 """The drop-in adapter on the GPU: the reference's adapter tests
-(tests/test_sva_llama_adapter.py of the reference) run against sva_amd with
+(tests/test_sva_llama_adapter.py of the reference) run against `sva` with
 the model on cuda:0, plus end-to-end equivalence: with a shortlist and a
 budget that cover every key, SVA attention is exact attention, so the patched
 model's logits equal the unpatched model's (eager attention, fp32) for
@@ -12,7 +12,7 @@ import pytest
 import torch
 from transformers import LlamaConfig, LlamaForCausalLM
 
-from sva_amd import SVAArtifactBundle, SVALayerArtifacts, SVALlamaAttention, patch_llama_attention
+from sva import SVAArtifactBundle, SVALayerArtifacts, SVALlamaAttention, patch_llama_attention
 
 pytestmark = pytest.mark.gpu
 
