@@ -199,6 +199,28 @@ int sva_verify(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_
                float scaling, void *out, int out_dtype, int64_t out_seq_stride, int64_t out_head_stride,
                int64_t out_tok_stride, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * sva_verify without a workspace argument; it allocates nothing.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The slice partials live in a static device array of
+ * SVA_VERIFY_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it
+ * runs on until the process ends; a call whose sva_verify_workspace_bytes()
+ * exceeds it fails with SVA_ERR_UNSUPPORTED (use sva_verify then).  Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (concurrent streams or host threads) race: the caller serializes them.
+ * Nothing in the array needs to start at zero: each call writes every
+ * partial it reads.  Results equal sva_verify's on the same arguments.
+ */
+#define SVA_VERIFY_NOALLOC_SCRATCH_BYTES (4u << 20)
+int sva_verify_noalloc(const void *q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride,
+                       int64_t q_tok_stride, const void *keys, const void *values, int kv_dtype,
+                       int64_t kv_head_stride, int64_t kv_row_stride, const int64_t *seq_offsets,
+                       const int64_t *seq_lens, int64_t n_keys, const int32_t *fin_idx, const int32_t *fin_count,
+                       int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B, float scaling, void *out,
+                       int out_dtype, int64_t out_seq_stride, int64_t out_head_stride, int64_t out_tok_stride,
+                       void *stream);
+
 /* ---------------------------------------------------------------------------
  * Inverted-index summon for q = 1 decode (summon_mode "inverted" and
  * "inverted_static").

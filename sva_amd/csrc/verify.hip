@@ -18,6 +18,8 @@
 // a running maximum, exp-sum and weighted V sum per head (each slice's sums
 // rescaled to the new maximum), and stores the output itself: the groups
 // alone fill the GPU, and no slice partials go through HBM.
+#include <mutex>
+
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -379,6 +381,33 @@ int launch_part_dim(const VerifyParams& p, dim3 grid, size_t lds, hipStream_t st
 
 bool verify_walks_slices(int64_t n_seq, int64_t G, int64_t Q) { return n_seq * G * Q >= SEQ_MIN_GROUPS; }
 
+// Slice partials of sva_verify_noalloc: a static device array, one copy per
+// GPU the library runs on, held until the process ends.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in
+// symbol): each device's address comes from hipGetSymbolAddress, taken once
+// with that device current, and is used wherever host code needs the array.
+static __device__ __align__(256) unsigned char scratch[SVA_VERIFY_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Address of the current device's scratch (set up on its first call).
+int current_device_scratch(void** out) {
+  int dev = -1;
+  SVA_CHECK_HIP(hipGetDevice(&dev), "sva_verify_noalloc: hipGetDevice");
+  SVA_UNSUPPORTED(dev >= 0 && dev < kMaxScratchDevices, "sva_verify_noalloc: device %d beyond the %d supported", dev,
+                  kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    SVA_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "sva_verify_noalloc: hipGetSymbolAddress(scratch)");
+    SVA_REQUIRE(ptr != nullptr && ((uintptr_t)ptr & 255u) == 0, "sva_verify_noalloc: scratch address unusable");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SVA_OK;
+}
+
 }  // namespace
 
 extern "C" size_t sva_verify_workspace_bytes(int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D, int64_t B) {
@@ -451,4 +480,27 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
                      (hipStream_t)stream, p);
   SVA_CHECK_LAUNCH("verify_combine_kernel");
   return SVA_OK;
+}
+
+extern "C" int sva_verify_noalloc(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride,
+                                  int64_t q_tok_stride, const void* keys, const void* values, int kv_dtype,
+                                  int64_t kv_head_stride, int64_t kv_row_stride, const int64_t* seq_offsets,
+                                  const int64_t* seq_lens, int64_t n_keys, const int32_t* fin_idx,
+                                  const int32_t* fin_count, int64_t n_seq, int64_t H, int64_t G, int64_t Q, int64_t D,
+                                  int64_t B, float scaling, void* out, int out_dtype, int64_t out_seq_stride,
+                                  int64_t out_head_stride, int64_t out_tok_stride, void* stream) {
+  sva::clear_error();
+  const size_t need = sva_verify_workspace_bytes(n_seq, H, G, Q, D, B);
+  SVA_REQUIRE(need > 0, "sva_verify_noalloc: bad sizes");
+  SVA_UNSUPPORTED(need <= (size_t)SVA_VERIFY_NOALLOC_SCRATCH_BYTES,
+                  "sva_verify_noalloc: this call needs %zu bytes of slice partials, more than the %zu-byte static "
+                  "scratch; use sva_verify with a workspace",
+                  need, (size_t)SVA_VERIFY_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = current_device_scratch(&ws);
+  if (rc != SVA_OK) return rc;
+  return sva_verify(q, q_dtype, q_seq_stride, q_head_stride, q_tok_stride, keys, values, kv_dtype, kv_head_stride,
+                    kv_row_stride, seq_offsets, seq_lens, n_keys, fin_idx, fin_count, n_seq, H, G, Q, D, B, scaling,
+                    out, out_dtype, out_seq_stride, out_head_stride, out_tok_stride, ws,
+                    (size_t)SVA_VERIFY_NOALLOC_SCRATCH_BYTES, stream);
 }
