@@ -16,8 +16,7 @@ using namespace sva;
 namespace {
 
 constexpr int PREP_BLOCK = 1024;
-constexpr int SPT = N_SAMPLE / PREP_BLOCK;  // samples per thread
-static_assert(SAMPLE_BINS == PREP_BLOCK && SPT * PREP_BLOCK == N_SAMPLE, "sampling layout");
+static_assert(SAMPLE_BINS == PREP_BLOCK, "one histogram bin per thread");
 
 struct LutParams {
   const void* q;
@@ -31,10 +30,10 @@ struct LutParams {
   float* lut;
   float* range;  // [items, 4]
   const void* codes;  // optional uint8 codes: sample for the threshold estimate
-
   int64_t code_hs;
   int64_t n_keys;
-  int64_t shortlist;
+  int sample_blocks;  // blocks of SAMPLE_KEYS sampled keys (codes != nullptr)
+  int sample_k;       // rank of the floor among the sampled sums; 0: no floor
 };
 
 // One workgroup per query item.  The sampled codes and the head's weights
@@ -64,27 +63,29 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   uint32_t* shist = kmax + S;                    // [SAMPLE_BINS]
   uint32_t* misc = shist + SAMPLE_BINS;          // [4]
   uint32_t* scratch = misc + 4;                  // [PREP_BLOCK / 64 + 1]
-  uint8_t* scodes = (uint8_t*)(scratch + PREP_BLOCK / 64 + 1);  // [N_SAMPLE * S] sampled codes
+  uint8_t* scodes = (uint8_t*)(scratch + PREP_BLOCK / 64 + 1);  // [sample_blocks * SAMPLE_KEYS * S] sampled codes
 
-  // 0. sampled codes (k-th largest of the samples, k ~ SAMPLE_TARGET * L *
-  // samples / N; sample blocks start at multiples of 16 keys)
+  // 0. sampled codes: blocks of SAMPLE_KEYS keys spread over the cache (block
+  // starts at multiples of 16 keys), staged in LDS with the weights: the loads
+  // complete by the first barrier
   const int64_t N = p.n_keys;
-  const int k = p.codes != nullptr ? sample_floor_rank(p.shortlist, N) : 0;
+  const int k = p.codes != nullptr ? p.sample_k : 0;
   const bool sample = k > 0;
+  const int n_blocks = p.sample_blocks;
+  const int n_samples = n_blocks * SAMPLE_KEYS;
   if (sample) {
-    // staged in LDS with the weights: the loads complete by the first barrier
     const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
     const int wpb = SAMPLE_KEYS * S / 4;  // 32-bit words per sample block (block starts are 16-byte multiples)
     if (((uintptr_t)head & 3u) == 0) {
-      for (int w = t; w < SAMPLE_BLOCKS * wpb; w += PREP_BLOCK) {
+      for (int w = t; w < n_blocks * wpb; w += PREP_BLOCK) {
         const int blk = w / wpb;
-        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (n_blocks - 1)) & ~(int64_t)15;
         reinterpret_cast<uint32_t*>(scodes)[w] = reinterpret_cast<const uint32_t*>(head + n0 * S)[w - blk * wpb];
       }
     } else {
-      for (int e = t; e < N_SAMPLE * S; e += PREP_BLOCK) {
+      for (int e = t; e < n_samples * S; e += PREP_BLOCK) {
         const int blk = e / (SAMPLE_KEYS * S);
-        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
+        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (n_blocks - 1)) & ~(int64_t)15;
         scodes[e] = head[n0 * S + e % (SAMPLE_KEYS * S)];
       }
     }
@@ -115,7 +116,10 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   // 1. q_low
   const float sc = p.scale[h];
   for (int r = t; r < R; r += PREP_BLOCK) {
+    // sequential over d; unrolled so that each group's LDS reads are in
+    // flight together instead of one dependent round trip per step
     float acc = 0.0f;
+#pragma unroll 16
     for (int d = 0; d < D; ++d) acc = __builtin_fmaf(qf[d], W[d * R + r], acc);
     const float v = acc * sc;
     ql[r] = v;
@@ -163,17 +167,54 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   // whatever it returns.
   if (sample && hi > lo) {
     const float inv_w = (float)SAMPLE_BINS / (hi - lo);
-#pragma unroll
-    for (int u = 0; u < SPT; ++u) {
-      const int i = t + u * PREP_BLOCK;
-      float acc = 0.0f;
-      for (int s = 0; s < S; ++s) {
-        const int c = min((int)scodes[i * S + s], C - 1);
-        acc = acc + tab[s * C + c];
-      }
+    auto count = [&](float acc) {
       int bin = (int)((acc - lo) * inv_w);
       bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
       atomicAdd(&shist[bin], 1u);
+    };
+    if (S == 4 && C <= 64 && D * R >= 4096 && S * C * cbs >= 4096) {
+      // two pair tables (in the place of the map and the codebooks, both
+      // read for the last time above): a sampled sum is P01 + P23, two reads
+      float* p01 = W;
+      float* p23 = cb;
+      for (int e = t; e < 4096; e += PREP_BLOCK) {
+        const int c0 = min(e & 63, C - 1), c1 = min(e >> 6, C - 1);
+        p01[e] = tab[c0] + tab[C + c1];
+        p23[e] = tab[2 * C + c0] + tab[3 * C + c1];
+      }
+      __syncthreads();
+      const uint32_t* sc4 = reinterpret_cast<const uint32_t*>(scodes);
+      const uint32_t cm = (uint32_t)(C - 1);
+      for (int i0 = t; i0 < n_samples; i0 += 4 * PREP_BLOCK) {
+        float acc[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int i = i0 + u * PREP_BLOCK;
+          const uint32_t w = i < n_samples ? sc4[i] : 0u;
+          const uint32_t a0 = min(w & 0xFFu, cm), a1 = min((w >> 8) & 0xFFu, cm);
+          const uint32_t a2 = min((w >> 16) & 0xFFu, cm), a3 = min(w >> 24, cm);
+          acc[u] = p01[a0 | (a1 << 6)] + p23[a2 | (a3 << 6)];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i0 + u * PREP_BLOCK < n_samples) count(acc[u]);
+      }
+    } else {
+      // four samples in flight per thread, one table read per subspace
+      for (int i0 = t; i0 < n_samples; i0 += 4 * PREP_BLOCK) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int i = min(i0 + u * PREP_BLOCK, n_samples - 1);
+            const int c = min((int)scodes[i * S + s], C - 1);
+            acc[u] = acc[u] + tab[s * C + c];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (i0 + u * PREP_BLOCK < n_samples) count(acc[u]);
+      }
     }
     __syncthreads();
     // thread j owns bin SAMPLE_BINS - 1 - j: a scan from the top finds the
@@ -335,10 +376,10 @@ __global__ void __launch_bounds__(SCORE_BLOCK)
   scores[(int64_t)item * N + n] = acc / sqrt_r;
 }
 
-size_t lut_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C, bool sample) {
+size_t lut_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C, int sample_blocks) {
   return sizeof(float) * (size_t)(D * R + S * C * (R / S + 1) + D + R + S * C) +
          sizeof(uint32_t) * (size_t)(2 * S + SAMPLE_BINS + 4 + PREP_BLOCK / 64 + 1) +
-         (sample ? (size_t)(N_SAMPLE * S) : 0);
+         (size_t)sample_blocks * SAMPLE_KEYS * (size_t)S;
 }
 
 }  // namespace
@@ -363,8 +404,14 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   SVA_REQUIRE(codes == nullptr || (code_type >= 0 && code_type <= 3 && n_keys >= 0 && shortlist > 0),
               "sva_query_lut: bad sampling arguments");
   // the threshold estimate serves the single-query uint8 scan; otherwise skipped
-  const bool sample = codes != nullptr && n_seq == 1 && Q == 1 && code_type == 0 && S <= SAMPLE_MAX_S;
-  const size_t lds = lut_lds_bytes(D, R, S, C, sample);
+  bool sample = codes != nullptr && n_seq == 1 && Q == 1 && code_type == 0 && S <= SAMPLE_MAX_S;
+  int blocks = sample ? sva::sample_blocks(n_keys, S) : 0;
+  // fewer sampled blocks when the head's weights leave less LDS
+  while (blocks > SAMPLE_MIN_BLOCKS && lut_lds_bytes(D, R, S, C, blocks) > (size_t)sva::kMaxLds) blocks /= 2;
+  const int sample_k = sample ? sva::sample_floor_rank(shortlist, n_keys, blocks * SAMPLE_KEYS) : 0;
+  sample = sample && sample_k > 0;
+  if (!sample) blocks = 0;
+  const size_t lds = lut_lds_bytes(D, R, S, C, blocks);
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_query_lut: head weights of %zu bytes exceed LDS", lds);
   const int64_t items = n_seq * H * Q;
   SVA_REQUIRE(items < (1ll << 31), "sva_query_lut: too many query items");
@@ -396,7 +443,8 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   p.codes = sample ? codes : nullptr;
   p.code_hs = code_head_stride;
   p.n_keys = n_keys;
-  p.shortlist = shortlist;
+  p.sample_blocks = blocks;
+  p.sample_k = sample_k;
   // many tokens per head: the head's weights are staged once per MT tokens
   const int64_t sub = R / S;
   const size_t mlds = sizeof(float) * (size_t)(D * R + MT * D + MT * R) + sizeof(uint32_t) * (size_t)(2 * MT * S);

@@ -7,30 +7,43 @@ namespace sva {
 
 constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
-// Sampled shortlist-floor estimate of a single-query uint8 scan (the query
-// table kernel and the fused lookup compute it alike): SAMPLE_BLOCKS
-// contiguous blocks of SAMPLE_KEYS keys spread over the cache, a histogram of
-// their sums over SAMPLE_BINS bins, and the bin of the k-th largest, k ~
-// max(SAMPLE_TARGET * L, SAMPLE_MIN_CAND) * samples / N.  The floor is only a
-// hint (an overshoot, fewer than L keys above it, costs the slow all-keys
-// select, never a result): the minimum keeps k >= ~12 for small shortlists,
-// where the k-th largest of few samples would overshoot often.
-constexpr int SAMPLE_BLOCKS = 64;
+// Sampled shortlist-floor estimate of a single-query uint8 scan, computed by
+// the query table kernel: `blocks` contiguous blocks of SAMPLE_KEYS keys
+// spread over the cache (one block per 256 keys, at least SAMPLE_MIN_BLOCKS,
+// at most SAMPLE_MAX_BYTES of codes), a histogram of their sums over
+// SAMPLE_BINS bins, and the bin of the k-th largest sum, k chosen so that
+// about max(SAMPLE_TARGET * L, SAMPLE_MIN_CAND) keys reach the floor.  The
+// floor is only a hint: an overshoot (fewer than L keys above it) costs the
+// slower all-keys select, never a result.  With n_s samples, the number of
+// samples above the L-th largest key is ~Poisson(n_s L / N); k is about
+// twice that mean and at least SAMPLE_MIN_RANK, so an overshoot is rare
+// (about 1e-4 at 1M keys, L = 2048, 8K samples).
 constexpr int SAMPLE_KEYS = 32;
 constexpr int SAMPLE_BINS = 1024;
-constexpr double SAMPLE_TARGET = 3.5;
-constexpr double SAMPLE_MIN_CAND = 6144.0;
+constexpr int SAMPLE_MIN_BLOCKS = 64;
+constexpr int SAMPLE_MAX_BYTES = 32768;
+constexpr double SAMPLE_TARGET = 2.0;
+constexpr double SAMPLE_MIN_CAND = 4096.0;
+constexpr int SAMPLE_MIN_RANK = 16;
 constexpr int SAMPLE_MAX_S = 8;  // subspaces of the sampled scan
-constexpr int N_SAMPLE = SAMPLE_BLOCKS * SAMPLE_KEYS;
 
-// Rank of the sampled floor among the N_SAMPLE sampled sums for a shortlist
-// of L over n_keys keys; 0: no sampled floor (every key is a candidate).
-__host__ __device__ inline int sample_floor_rank(int64_t L, int64_t n_keys) {
-  if (n_keys < 4 * (int64_t)N_SAMPLE) return 0;
+// Sample blocks for a cache of n_keys keys with S subspaces.
+__host__ __device__ inline int sample_blocks(int64_t n_keys, int64_t S) {
+  const int64_t cap = SAMPLE_MAX_BYTES / (SAMPLE_KEYS * S);
+  int64_t b = n_keys / 256;
+  b = b < SAMPLE_MIN_BLOCKS ? SAMPLE_MIN_BLOCKS : b;
+  return (int)(b < cap ? b : cap);
+}
+
+// Rank of the sampled floor among n_samples sampled sums for a shortlist of
+// L over n_keys keys; 0: no sampled floor (every key is a candidate).
+__host__ __device__ inline int sample_floor_rank(int64_t L, int64_t n_keys, int n_samples) {
+  if (n_samples <= 0 || n_keys < 4 * (int64_t)n_samples) return 0;
   double target = SAMPLE_TARGET * (double)L;
   if (target < SAMPLE_MIN_CAND) target = SAMPLE_MIN_CAND;
-  const int k = (int)(target * (double)N_SAMPLE / (double)n_keys) + 1;
-  return k < N_SAMPLE / 2 ? k : 0;
+  int k = (int)(target * (double)n_samples / (double)n_keys) + 1;
+  k = k < SAMPLE_MIN_RANK ? SAMPLE_MIN_RANK : k;
+  return k < n_samples / 2 ? k : 0;
 }
 
 struct SummonParams {
@@ -60,29 +73,13 @@ struct SummonParams {
   int32_t* fin_count;
 };
 
-// Query side of the fused lookup (sva_lookup_select): the scan computes the
-// item's q_low, table, bounds and sampled floor itself and writes them to
-// q_low / lut / range.
-struct FusedQuery {
-  const void* q;
-  int q_dtype;
-  int64_t q_hs;  // head stride of q (one sequence, one token)
-  int64_t D;
-  const float* q_proj;
-  const float* scale;
-  const float* codebooks;
-  int sample_k;  // rank of the sampled floor among the samples; 0: no sampled floor
-};
-
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
-bool summon_wide_fused_eligible(const SummonParams& p, const FusedQuery& f);
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                     const FusedQuery* f = nullptr);
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);
 
 inline int next_pow2_host(int x) {

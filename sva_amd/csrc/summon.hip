@@ -478,8 +478,7 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
                 int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
-                int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
-                const sva::FusedQuery* fq = nullptr) {
+                int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream) {
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
   SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "%s: bad sizes", fn);
@@ -527,10 +526,6 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
     int rc = sva::fill_i32(sl_count, items, 0, (hipStream_t)stream);
     if (rc == SVA_OK && B > 0) rc = sva::fill_i32(fin_count, items, 0, (hipStream_t)stream);
     return rc;
-  }
-  if (fq != nullptr) {
-    SVA_REQUIRE(sva::summon_wide_fused_eligible(p, *fq), "%s: shapes outside the fused path", fn);
-    return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream, fq);
   }
   if (sva::summon_wide_eligible(p, items)) {
     return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream);
@@ -586,45 +581,10 @@ extern "C" int sva_lookup_select(const void* q, int q_dtype, int64_t q_head_stri
   SVA_REQUIRE(fin_idx && fin_count, "sva_lookup_select: null pointer");
   SVA_REQUIRE(B > 0 && B <= 8192, "sva_lookup_select: budget %lld out of range (1..8192)", (long long)B);
   SVA_REQUIRE(H > 0 && n_keys >= 0 && L > 0, "sva_lookup_select: bad sizes");
-  // the sampled floor of sva_query_lut for one sequence and one token
-  const int sample_k = code_type == SVA_CODE_U8 && S <= sva::SAMPLE_MAX_S ? sva::sample_floor_rank(L, n_keys) : 0;
-  sva::FusedQuery f;
-  f.q = q;
-  f.q_dtype = q_dtype;
-  f.q_hs = q_head_stride;
-  f.D = D;
-  f.q_proj = q_proj;
-  f.scale = scale;
-  f.codebooks = codebooks;
-  f.sample_k = sample_k;
-  sva::SummonParams e{};
-  e.q_low = q_low;
-  e.codes = codes;
-  e.ctype = code_type;
-  e.code_hs = code_head_stride;
-  e.k_low = k_low;
-  e.klow_hs = k_low_head_stride;
-  e.H = (int)H;
-  e.Q = 1;
-  e.N = n_keys;
-  e.R = (int)R;
-  e.S = (int)S;
-  e.C = (int)C;
-  e.L = (int)L;
-  e.mask = mask;
-  e.mask_type = mask_type;
-  const bool fused = H <= 64 && R <= 511 && S > 0 && S <= 64 && C > 0 && C <= 16384 && L <= 16384 &&
-                     n_keys < (1ll << 31) && sva::summon_wide_fused_eligible(e, f);
-  if (!fused) {
-    const int rc = sva_query_lut(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
-                                 code_type, code_head_stride, n_keys, L, q_low, lut, score_range, stream);
-    if (rc != SVA_OK) return rc;
-    return sva_summon_select(lut, score_range, q_low, codes, code_type, code_head_stride, k_low, k_low_head_stride,
-                             nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride, sl_idx,
-                             sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream);
-  }
-  return summon_impl("sva_lookup_select", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
-                     k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type,
-                     mask_tok_stride, sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes,
-                     stream, &f);
+  const int rc = sva_query_lut(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
+                               code_type, code_head_stride, n_keys, L, q_low, lut, score_range, stream);
+  if (rc != SVA_OK) return rc;
+  return sva_summon_select(lut, score_range, q_low, codes, code_type, code_head_stride, k_low, k_low_head_stride,
+                           nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride, sl_idx,
+                           sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream);
 }

@@ -2,27 +2,30 @@
 // per item for the scan, one per item for the rest; two kernels, no
 // grid-wide synchronisation and no atomics on shared global words.
 //
-//   wide_scan     one workgroup per chunk of WB * 32 keys.  Streams the
-//                 chunk's packed uint8 codes (16-byte loads, all in flight
-//                 before use), scores every key through the LUT in the
-//                 reference's order, and appends each allowed key whose sum
-//                 reaches the item's sampled floor t_lo to its wave's own
-//                 candidate list as a unique 64-bit composite (score key,
-//                 key index); counts go to the wave's own counter words.
-//                 In the fused lookup (sva_lookup_select, 4x64 codes) each
-//                 scan workgroup first computes its item's q_low, table,
-//                 bounds and sampled floor itself (FusedPrologue).
-//   wide_finish   one workgroup per item.  Gathers the candidates (~4x the
-//                 shortlist for the sampled floor) into LDS, selects the L
-//                 largest composites exactly (shortlist), scores them with
-//                 k_low . q_low in torch's sum order (rank), and, when a
-//                 budget is asked for, selects the B best ranks and writes
-//                 them in ascending key order.  When the floor overshot
-//                 (fewer than L candidates) the shortlist is selected over
-//                 every key of the item instead: slower, same result.
+//   wide_scan     one workgroup per chunk of WB * 32 keys.  Loads the item's
+//                 table and floor (sva_query_lut's outputs) first, then
+//                 streams the chunk's packed uint8 codes (16-byte loads, all
+//                 in flight before use), scores every key through the table
+//                 in the reference's order, and appends each allowed key whose
+//                 sum reaches the item's sampled floor t_lo to its wave's own
+//                 candidate list as a unique 64-bit composite (score key, key
+//                 index), with the candidate's rank score (k_low . q_low in
+//                 torch's sum order) beside it; counts go to the wave's own
+//                 counter words.
+//   wide_finish   one workgroup per item.  Gathers the candidates (about
+//                 twice the shortlist for the sampled floor) and their ranks,
+//                 compacts them through LDS into a dense register layout in
+//                 ascending key order, selects the L largest composites
+//                 exactly (shortlist) and, when a budget is asked for, the B
+//                 best rank composites among them, and writes both in
+//                 ascending key order.  When the floor overshot (fewer than L
+//                 candidates) the shortlist is selected over every key of the
+//                 item instead: slower, same result.
 // Selection equals a full sort by (score desc, key index asc): with R = 64
 // the score is the sum / 8 exactly, so every key below the floor ranks
 // strictly below every candidate.
+#include <mutex>
+
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
@@ -43,7 +46,8 @@ constexpr int STAGE_LISTS = 4096;  // lists whose staging offsets the finish ker
 // The wide path has R = 64: dividing by sqrt(R) = 8 equals multiplying by
 // 0.125 exactly (both are the correctly rounded value of x / 8).
 constexpr float kInvSqrtR = 0.125f;
-constexpr int KL_CAP = 256;      // candidate keys per scan wave kept in LDS for the rank scores
+constexpr int KL_CAP = 256;      // candidates per scan wave kept in LDS (composite and rank)
+constexpr int WG_CAP = 64;       // candidates of a scan workgroup in its compact list
 constexpr int64_t kWideMinKeys = 32768;
 constexpr int64_t kMaxWideItems = 64;
 
@@ -55,8 +59,10 @@ struct WideArgs {
   uint32_t* nallow;  // [items, W * NW] allowed keys of each scan wave
   uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
   float* cand_rank;  // [items, W * NW, WAVE_KEYS] rank score of each listed candidate
+  uint32_t* wg_count;  // [items, W, 2] candidates and allowed keys of each scan workgroup
+  uint64_t* wg_cand;   // [items, W, WG_CAP] a workgroup's candidates in key order (when they fit)
+  float* wg_rank;      // [items, W, WG_CAP] their rank scores
   int W;             // scan workgroups per item
-  FusedQuery f;      // fused lookup: the query side (p.q_low, p.lut, p.range are its outputs)
 };
 
 SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
@@ -215,10 +221,10 @@ SVA_DEV float item_floor(const SummonParams& p, int item) {
 // Appends the flagged keys of one round (key n0 + k for flag c[k]) to the
 // wave's candidate list in ascending key order (lanes in order, each lane's
 // keys in order), as composites of the exact score acc / sqrt(R); the first
-// KL_CAP key indices also go to the wave's LDS list `keys`.
+// KL_CAP composites also go to the wave's LDS list `kc`.
 template <int KPT>
 SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const float (&acc)[KPT], int n0, uint64_t* out,
-                          uint32_t* keys, uint32_t& wc) {
+                          uint64_t* kc, uint32_t& wc) {
 #pragma clang fp contract(off)
   uint32_t below = 0, tot = 0;
 #pragma unroll
@@ -231,8 +237,9 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
     if (c[k]) {
-      out[o] = composite(f2key(acc[k] * kInvSqrtR), (uint32_t)(n0 + k));
-      if (o < (uint32_t)KL_CAP) keys[o] = (uint32_t)(n0 + k);
+      const uint64_t x = composite(f2key(acc[k] * kInvSqrtR), (uint32_t)(n0 + k));
+      out[o] = x;
+      if (o < (uint32_t)KL_CAP) kc[o] = x;
       ++o;
     }
   }
@@ -245,7 +252,7 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 // sum reaches the floor.
 template <int S, bool SMALLC, bool CHECK, bool MASKED>
 SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, SMALLC>& T,
-                         float t_lo, int cs, int ce, uint64_t* out, uint32_t* keys, uint32_t& wc,
+                         float t_lo, int cs, int ce, uint64_t* out, uint64_t* kc, uint32_t& wc,
                          uint32_t& n_allowed) {
   constexpr int KPT = 16 / S;
 #pragma unroll
@@ -262,7 +269,7 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
         c[k] = ok && acc[k] >= t_lo;
         any = any || c[k];
       }
-      if (__builtin_amdgcn_ballot_w64(any) != 0ull) append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, keys, wc);
+      if (__builtin_amdgcn_ballot_w64(any) != 0ull) append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
     } else {
       float mx = acc[0];
 #pragma unroll
@@ -271,18 +278,19 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
         bool c[KPT];
 #pragma unroll
         for (int k = 0; k < KPT; ++k) c[k] = acc[k] >= t_lo;
-        append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, keys, wc);
+        append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
       }
     }
   }
   if (!CHECK) n_allowed = KEYS_PT;
 }
 
-// Rank scores of a scan wave's nc candidates (keys in the LDS list while
-// they fit, else from the wave's candidate list): one 16-lane DPP row per
-// candidate, 16 candidates in flight per wave; written beside the list.
+// Rank scores of a scan wave's nc candidates (composites in the LDS list
+// while they fit, else from the wave's candidate list): one 16-lane DPP row
+// per candidate, 16 candidates in flight per wave; written beside the list
+// and, for the first KL_CAP, to the wave's LDS ranks `kr`.
 // qq: floats 4j .. 4j + 3 of the item's q_low for lane j of each DPP row.
-SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint32_t* keys,
+SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint64_t* kc, float* kr,
                              const uint64_t* out, float* rank, uint32_t nc) {
 #pragma clang fp contract(off)
   const int j = lane_id() & 15;
@@ -297,244 +305,98 @@ SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, c
     for (int u = 0; u < RU; ++u) {
       const uint32_t c = c0 + 4 * u + row;
       key[u] = 0u;
-      if (c < nc) key[u] = c < (uint32_t)KL_CAP ? keys[c] : composite_index(out[c]);
+      if (c < nc) key[u] = composite_index(c < (uint32_t)KL_CAP ? kc[c] : out[c]);
       rv[u] = c < nc ? reinterpret_cast<const float4*>(klow + (int64_t)key[u] * p.R)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const float dot = rank_dot64_row16(rv[u], qq);
-      if (c0 + 4 * u + row < nc && j == 0) rank[c0 + 4 * u + row] = dot * kInvSqrtR;
+      const uint32_t c = c0 + 4 * u + row;
+      if (c < nc && j == 0) {
+        rank[c] = dot * kInvSqrtR;
+        if (c < (uint32_t)KL_CAP) kr[c] = dot * kInvSqrtR;
+      }
     }
   }
 }
 
-// LDS of the fused prologue beside the scan tables.
-struct FusedLds {
-  float qf[64];
-  __align__(16) float ql[64];
-  uint32_t kmin[8], kmax[8];
-  uint32_t misc[4];
-  uint32_t scratch[NW + 2];
-};
-
-// Query side of the fused lookup for one item, computed by every scan
-// workgroup of the item (D = R = 64, 4x64 codes) with the arithmetic
-// of sva_query_lut: q_low by a sequential fma chain over d times the scale,
-// each table entry by a sequential fma chain over its subspace, the bounds of
-// any sum folded over s, and the sampled floor from the same samples and
-// histogram; tables and floors are therefore bit-identical to the two-call
-// path.  issue() starts the loads (before the chunk's codes); build() leaves
-// the scan tables in LDS and returns the floor.  The item's first workgroup
-// writes q_low, the table and the bounds to global memory.
-template <int S>
-struct FusedPrologue {
-  static constexpr int SUB = 64 / S;         // floats per codebook row
-  static constexpr int ROWS = S * 64 / WB;   // table entries (codebook rows) per thread
-  static constexpr int SPT = N_SAMPLE / WB;  // sampled keys per thread
-  static constexpr int SW = S / 4;           // 32-bit words of codes per key
-  static_assert(ROWS * SUB == 16 && S * 64 <= 2 * WB && SAMPLE_BINS == 4 * WB, "fused prologue layout");
-  float4 w[4];   // floats 16 t .. 16 t + 15 of the head's map q_proj[h] ([D][R])
-  float4 cb[4];  // codebook rows t + k * WB
-  uint32_t smp[SPT][SW];
-  float qv, sc;
-  SVA_DEV void issue(const WideArgs& a, int item) {
-    const FusedQuery& f = a.f;
-    const int t = threadIdx.x;
-    const int h = item % a.p.H;
-    const float4* w4 = reinterpret_cast<const float4*>(f.q_proj + (int64_t)h * 64 * 64);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = w4[4 * t + i];
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const float4* c4 = reinterpret_cast<const float4*>(f.codebooks + ((int64_t)h * S * 64 + t + k * WB) * SUB);
-#pragma unroll
-      for (int i = 0; i < SUB / 4; ++i) cb[k * (SUB / 4) + i] = c4[i];
-    }
-    qv = t < 64 ? load_elem(f.q, (int64_t)h * f.q_hs + t, f.q_dtype) : 0.0f;
-    sc = f.scale[h];
-    if (f.sample_k > 0) {
-      const uint8_t* head = (const uint8_t*)a.p.codes + (int64_t)h * a.p.code_hs;
-      const int64_t N = a.p.N;
-#pragma unroll
-      for (int u = 0; u < SPT; ++u) {
-        const int i = t + u * WB;
-        const int blk = i / SAMPLE_KEYS;
-        const int64_t n0 = ((int64_t)blk * (N - SAMPLE_KEYS) / (SAMPLE_BLOCKS - 1)) & ~(int64_t)15;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(head + (n0 + i % SAMPLE_KEYS) * S);
-#pragma unroll
-        for (int j = 0; j < SW; ++j) smp[u][j] = src[j];
-      }
-    }
-  }
-  SVA_DEV float build(const WideArgs& a, int item, bool first, float* tab, FusedLds& L) {
-#pragma clang fp contract(off)
-    const FusedQuery& f = a.f;
-    const int t = threadIdx.x;
-    constexpr int PAIR = 4096;
-    // 1. map and query into LDS (the map in the pair table's place)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(tab)[4 * t + i] = w[i];
-    if (t < 64) L.qf[t] = qv;
-    if (t == 0) L.misc[0] = 0u;  // floor bin 0 unless the samples place it
-    __syncthreads();
-    // 2. q_low, one lane per output
-    if (t < 64) {
-      float acc = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < 64; ++d) acc = __builtin_fmaf(L.qf[d], tab[d * 64 + t], acc);
-      const float v = acc * sc;
-      L.ql[t] = v;
-      if (first) const_cast<float*>(a.p.q_low)[(int64_t)item * 64 + t] = v;
-    }
-    __syncthreads();
-    // 3. table entries (every wave's 64 entries share a subspace), per-subspace
-    // bounds, histogram cleared (the map is no longer read)
-    float* raw = tab + PAIR;
-    uint32_t* hist = reinterpret_cast<uint32_t*>(tab);
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const int e = t + k * WB;
-      const int s = e >> 6;
-      const float* row = reinterpret_cast<const float*>(&cb[k * (SUB / 4)]);
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(L.ql[s * SUB + j], row[j], acc);
-      raw[e] = acc;
-      if (first) const_cast<float*>(a.p.lut)[(int64_t)item * S * 64 + e] = acc;
-      uint32_t kn = f2key(acc), kx = kn;
-      for (int off = 32; off > 0; off >>= 1) {
-        kn = min(kn, (uint32_t)__shfl_xor((int)kn, off, WAVE));
-        kx = max(kx, (uint32_t)__shfl_xor((int)kx, off, WAVE));
-      }
-      if (lane_id() == 0) {
-        L.kmin[s] = kn;
-        L.kmax[s] = kx;
-      }
-    }
-    reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
-    __syncthreads();
-    // 4. bounds of any sum, in the scan's order
-    float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      lo = lo + key2f(L.kmin[s]);
-      hi = hi + key2f(L.kmax[s]);
-    }
-    // 5. sampled floor: the histogram bin of the k-th largest sampled sum
-    float t_lo = -INFINITY;
-    const int k = f.sample_k;
-    if (k > 0 && hi > lo) {
-      const float inv_w = (float)SAMPLE_BINS / (hi - lo);
-#pragma unroll
-      for (int u = 0; u < SPT; ++u) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const int c = min((int)((smp[u][s >> 2] >> (8 * (s & 3))) & 0xFFu), 63);
-          acc = acc + raw[s * 64 + c];
-        }
-        int bin = (int)((acc - lo) * inv_w);
-        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
-        atomicAdd(&hist[bin], 1u);
-      }
-      __syncthreads();
-      // thread t holds bins SAMPLE_BINS - 1 - 4 t - j (j = 0..3), from the top
-      uint32_t c[4], mine = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        c[j] = hist[SAMPLE_BINS - 1 - 4 * t - j];
-        mine += c[j];
-      }
-      uint32_t total;
-      uint32_t above = block_excl_scan<WB>(mine, L.scratch, &total);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (above < (uint32_t)k && above + c[j] >= (uint32_t)k) L.misc[0] = (uint32_t)(SAMPLE_BINS - 1 - 4 * t - j);
-        above += c[j];
-      }
-      __syncthreads();
-      t_lo = lo + (float)L.misc[0] / inv_w;
-    }
-    if (first && t == 0) {
-      float* rg = const_cast<float*>(a.p.range) + (int64_t)item * 4;
-      rg[0] = lo;
-      rg[1] = hi;
-      rg[2] = t_lo;
-      rg[3] = 0.0f;
-    }
-    __syncthreads();  // histogram read before the pair table replaces it
-    // 6. pair table: entry t + k WB = T0[t & 63] + T1[(t >> 6) + 4 k]
-    const float t0 = raw[t & 63];
-#pragma unroll
-    for (int kk = 0; kk < PAIR / WB; ++kk) tab[t + kk * WB] = t0 + raw[64 + (t >> 6) + kk * (WB / 64)];
-    __syncthreads();
-    return t_lo > lo ? t_lo : lo;
-  }
-};
-
 // One scan workgroup's chunk.  CHECK: a partial or masked chunk (every key
-// tested for being allowed, guarded loads).  FUSED: the query side is
-// computed here (FusedPrologue) instead of read.
-template <int S, bool SMALLC, bool CHECK, bool MASKED, bool FUSED>
-SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, uint32_t (*klist)[KL_CAP], FusedLds& fl) {
+// tested for being allowed, guarded loads).  The item's table, floor and
+// q_low are requested before the chunk's codes: every wave's loads return in
+// order, so the tables are in LDS while the codes still stream and each
+// round of codes is scored as soon as its own load lands.
+// LDS of a scan workgroup beside its tables: each wave's first KL_CAP
+// candidates (composites, ranks) and the waves' counts.
+struct ScanLds {
+  uint64_t kc[NW][KL_CAP];
+  float kr[NW][KL_CAP];
+  uint32_t wcnt[NW], walw[NW];
+};
+
+template <int S, bool SMALLC, bool CHECK, bool MASKED>
+SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, ScanLds& L) {
 #pragma clang fp contract(off)
   const SummonParams& p = a.p;
   const int h = item % p.H;
   const int cs = w * CHUNK;
   const int ce = (int)min((int64_t)cs + CHUNK, p.N);
   const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
-  // table loads first, then the codes: loads complete in order, so the
-  // tables are stored while the codes stream and each round of codes is
-  // scored as soon as its own load lands
-  // The tables come first and the chunk's codes are requested only once they
-  // are in LDS: all workgroups start together, and query-side loads issued
-  // after the first workgroups' code loads wait behind the whole code stream
-  // in the memory pipeline (measured: the fused lookup 2.6 us faster this way).
   ScanTables<S, SMALLC> T;
+  T.load(p, item);
+  const float t_lo = item_floor(p, item);
+  const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[lane_id() & 15];
   u32x4 raw[KEYS_PT * S / 16];
-  float t_lo;
-  if constexpr (FUSED) {
-    FusedPrologue<S> F;
-    F.issue(a, item);
-    t_lo = F.build(a, item, w == 0, tab_lds, fl);  // tables in LDS
-    T.tab = tab_lds;
-  } else {
-    T.load(p, item);
-    T.store(tab_lds);
-    t_lo = item_floor(p, item);
-    __syncthreads();  // tables in LDS
-  }
   load_chunk<S, !CHECK>(codes, cs, ce, raw);
+  T.store(tab_lds);
+  __syncthreads();  // tables in LDS
   const int wid = threadIdx.x / WAVE;
+  const int lane = lane_id();
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
-  scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, klist[wid], wc, n_allowed);
-  float4 qq;
-  if constexpr (FUSED) qq = reinterpret_cast<const float4*>(fl.ql)[lane_id() & 15];
-  else qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[lane_id() & 15];
-  rank_candidates(p, item, qq, klist[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
+  scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, L.kc[wid], wc, n_allowed);
+  rank_candidates(p, item, qq, L.kc[wid], L.kr[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
-  if (lane_id() == 0) {
+  if (lane == 0) {
     a.ncand[sub] = wc;
     a.nallow[sub] = wa;
+    L.wcnt[wid] = wc;
+    L.walw[wid] = wa;
+  }
+  // the workgroup's compact list: its waves' candidates in wave order (key
+  // order), when there are at most WG_CAP of them; its counts either way
+  __syncthreads();
+  uint32_t off = 0, tot = 0, alw = 0;
+#pragma unroll
+  for (int v = 0; v < NW; ++v) {
+    off += v < wid ? L.wcnt[v] : 0u;
+    tot += L.wcnt[v];
+    alw += L.walw[v];
+  }
+  const int64_t g = (int64_t)item * a.W + w;
+  if (tot <= (uint32_t)WG_CAP && lane < (int)wc) {
+    a.wg_cand[g * WG_CAP + off + lane] = L.kc[wid][lane];
+    a.wg_rank[g * WG_CAP + off + lane] = L.kr[wid][lane];
+  }
+  if (threadIdx.x == 0) {
+    a.wg_count[2 * g] = tot;
+    a.wg_count[2 * g + 1] = alw;
   }
 }
 
 // Five workgroups per CU (at most 102 VGPRs) keep every workgroup of a
 // million-key, nine-head scan resident at once (up to four subspaces).
-template <int S, bool SMALLC, bool MASKED, bool FUSED>
+template <int S, bool SMALLC, bool MASKED>
 __global__ void __launch_bounds__(WB, S <= 4 ? 5 : 1) wide_scan_kernel(WideArgs a) {
   __shared__ __align__(16) float tab_lds[ScanTables<S, SMALLC>::LDS_FLOATS];
-  __shared__ uint32_t klist[NW][KL_CAP];
-  __shared__ FusedLds fl;
+  __shared__ ScanLds lds;
   const int item = blockIdx.x / a.W;
   const int w = blockIdx.x % a.W;
   if (!MASKED && (int64_t)(w + 1) * CHUNK <= a.p.N) {
-    scan_chunk<S, SMALLC, false, false, FUSED>(a, item, w, tab_lds, klist, fl);
+    scan_chunk<S, SMALLC, false, false>(a, item, w, tab_lds, lds);
   } else {
-    scan_chunk<S, SMALLC, true, MASKED, FUSED>(a, item, w, tab_lds, klist, fl);
+    scan_chunk<S, SMALLC, true, MASKED>(a, item, w, tab_lds, lds);
   }
 }
 
@@ -562,13 +424,16 @@ constexpr size_t kFinLds = kFinLoff + sizeof(uint32_t) * STAGE_LISTS;
 static_assert(kFinShared64 % 8 == 0, "8-byte LDS words");
 static_assert(kFinLds <= (size_t)kMaxLds, "finish LDS");
 
-// Direct path of the finish: lists gathered straight into registers when
-// every list holds at most DCAP candidates and there are at most DL_LISTS
-// lists (16 lanes per list, entries l + 16 h of lists k * 64 + q).
+// Dense path of the finish: every list holds at most DH * 16 candidates
+// (DH = 2 or 3), there are at most DL_LISTS lists and at most NPD * SB
+// candidates in all (the sampled floor aims at about 4K).  The lists are gathered straight into registers (16
+// lanes per list, entries l + 16 h of lists k * DQ + q), then compacted
+// through LDS into the dense order: candidate j of the concatenated lists at
+// thread j % SB, slot j / SB, which is ascending key order.
 constexpr int DQ = SB / 16;          // list groups of 16 lanes
 constexpr int DK = 8;                // lists per group
-constexpr int DCAP = 48;             // entries per list (up to 3 per lane)
 constexpr int DL_LISTS = DQ * DK;    // 512 lists: caches up to 1M keys
+constexpr int NPD = 8;              // dense slots per thread
 
 // Rank score of a 64-float k_low row in torch's sum order, computed here
 // for the all-keys path: rows r of sl, one 16-lane DPP row each.
@@ -631,100 +496,263 @@ SVA_DEV void finish_budget(const SummonParams& p, int item, int leff, int beff, 
                            [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
 }
 
-// Direct path of the finish (see wide_finish_kernel): DH entries per lane
-// and list, slot DH * k + h = list k * DQ + q, entry l + 16 h.
-template <int DH, typename Emit>
-SVA_DEV void finish_direct(const WideArgs& a, int item, int nsub, int leff, uint32_t M, uint64_t c_lo, uint64_t c_hi,
-                           const uint32_t* lcnt, uint32_t* loff, const TopLds& tl, uint32_t* scratch, Emit emit) {
-  const uint64_t* cand = a.cand + (int64_t)item * nsub * WAVE_KEYS;
-  const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
-  const int t = threadIdx.x;
-  const int q = t >> 4, l = t & 15;
+// Sparse gather of the dense path: lane (q, l) loads entries l + 16 h of
+// lists k * DQ + q of `src` (entries past a list's count are read but
+// unused; every read stays inside the list's capacity).
+template <int DH, typename T>
+SVA_DEV void gather_lists(const T* src, int nsub, T (&v)[DH * DK]) {
+  const int q = threadIdx.x >> 4, l = threadIdx.x & 15;
   const int kq = (nsub + DQ - 1) / DQ;
-  constexpr int NS = DH * DK;
-  uint64_t e[NS];
 #pragma unroll
   for (int k = 0; k < DK; ++k) {
 #pragma unroll
-    for (int h = 0; h < DH; ++h) e[DH * k + h] = 0ull;
-    if (k < kq) {  // uniform; entries < DCAP are inside every list's capacity
-      const int64_t off = (int64_t)min(k * DQ + q, nsub - 1) * WAVE_KEYS;
+    for (int h = 0; h < DH; ++h) v[DH * k + h] = T(0);
+    if (k < kq) {  // uniform
+      const int64_t off = (int64_t)min(k * DQ + q, nsub - 1) * WAVE_KEYS + l;
 #pragma unroll
-      for (int h = 0; h < DH; ++h) e[DH * k + h] = cand[off + l + 16 * h];
+      for (int h = 0; h < DH; ++h) v[DH * k + h] = src[off + 16 * h];
     }
   }
+}
+
+// Moves sparse register entries (list sidx, entry j) to dense slots:
+// position loff[sidx] + j of the concatenated lists goes to thread
+// position % SB, slot position / SB.  stage: LDS of at least M elements.
+template <int DH, typename T>
+SVA_DEV void densify(const T (&v)[DH * DK], T (&d)[NPD], T* stage, const uint32_t* lcnt, const uint32_t* loff,
+                     int nsub, int dslots, uint32_t M) {
+  const int t = threadIdx.x, q = t >> 4, l = t & 15;
+  const int kq = (nsub + DQ - 1) / DQ;
 #pragma unroll
   for (int k = 0; k < DK; ++k) {
     const int sidx = k * DQ + q;
-    const uint32_t c = (k < kq && sidx < nsub) ? lcnt[sidx] : 0u;
+    if (k < kq && sidx < nsub) {
+      const uint32_t c = lcnt[sidx], base = loff[sidx];
 #pragma unroll
-    for (int h = 0; h < DH; ++h)
-      if ((uint32_t)(l + 16 * h) >= c) e[DH * k + h] = 0ull;
-  }
-  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NS>(e, leff, c_hi, c_lo, tl, DH * kq, true);
-  // the selected load their ranks (written beside the lists by the scan)
-  float rnk[NS];
-#pragma unroll
-  for (int k = 0; k < DK; ++k) {
-    const int64_t off = (int64_t)min(k * DQ + q, nsub - 1) * WAVE_KEYS;
-#pragma unroll
-    for (int h = 0; h < DH; ++h) {
-      const uint64_t x = e[DH * k + h];
-      rnk[DH * k + h] = (k < kq && x != 0ull && x >= X) ? crank[off + l + 16 * h] : 0.0f;
+      for (int h = 0; h < DH; ++h)
+        if ((uint32_t)(l + 16 * h) < c) stage[base + l + 16 * h] = v[DH * k + h];
     }
-  }
-  // list-ordered compaction: per-list counts of the selected (ballot
-  // bits of the list's 16 lanes), their scan over the lists, then each
-  // entry at its list's base plus the selected before it in the list
-  uint32_t mk[NS];
-  const int qs = 16 * (q & 3);
-#pragma unroll
-  for (int k = 0; k < DK; ++k) {
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int h = 0; h < DH; ++h) {
-      mk[DH * k + h] = 0u;
-      if (k < kq) {
-        const uint64_t x = e[DH * k + h];
-        const uint64_t b = __builtin_amdgcn_ballot_w64(x != 0ull && x >= X);
-        mk[DH * k + h] = (uint32_t)(b >> qs) & 0xFFFFu;
-        cnt += (uint32_t)__popc(mk[DH * k + h]);
-      }
-    }
-    const int sidx = k * DQ + q;
-    if (k < kq && l == 0 && sidx < nsub) loff[sidx] = cnt;
   }
   __syncthreads();
-  {
-    const uint32_t c = t < nsub ? loff[t] : 0u;
-    uint32_t tot;
-    const uint32_t o = block_excl_scan<SB>(c, scratch, &tot);
-    if (t < nsub) loff[t] = o;
-    __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    const uint32_t j = (uint32_t)(t + i * SB);
+    d[i] = (i < dslots && j < M) ? stage[j] : T(0);
   }
-  const uint32_t below = (1u << l) - 1u;
+  __syncthreads();  // the staging area is free again
+}
+
+// Dense path (see wide_finish_kernel): the item's leff shortlist keys and
+// beff budget keys, both in ascending key order, from its M candidates held
+// sparse in e_sp.  The ranks are gathered here, behind the composites'
+// compaction and shortlist select.
+template <int DH>
+SVA_DEV void finish_dense(const WideArgs& a, int item, int nsub, int leff, int beff, uint32_t M, uint64_t c_lo,
+                          uint64_t c_hi, const uint64_t (&e_sp)[DH * DK], unsigned char* stage, const uint32_t* lcnt,
+                          const uint32_t* loff, uint32_t* rkb, uint32_t* wcnt, uint32_t* scratch, const TopLds& tl) {
+#pragma clang fp contract(off)
+  const SummonParams& p = a.p;
+  const int dslots = ((int)M + SB - 1) / SB;
+  float r_sp[DH * DK];
+  gather_lists<DH>(a.cand_rank + (int64_t)item * nsub * WAVE_KEYS, nsub, r_sp);
+  uint64_t e[NPD];
+  densify<DH>(e_sp, e, (uint64_t*)stage, lcnt, loff, nsub, dslots, M);
+  // shortlist: the leff largest score composites
+  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPD>(e, leff, c_hi, c_lo, tl, dslots, true);
+  float r[NPD];
+  densify<DH>(r_sp, r, (float*)stage, lcnt, loff, nsub, dslots, M);
+  // budget: the beff largest (rank key, key index) composites of the shortlist
+  uint64_t rc[NPD];
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
 #pragma unroll
-  for (int k = 0; k < DK; ++k) {
-    if (k < kq) {
-      const int sidx = k * DQ + q;
-      uint32_t o = sidx < nsub ? loff[sidx] : 0u;
+  for (int i = 0; i < NPD; ++i) {
+    rc[i] = 0ull;
+    if (i < dslots && e[i] != 0ull && e[i] >= X) {
+      const uint32_t rkey = f2key(r[i]);
+      rc[i] = composite(rkey, composite_index(e[i]));
+      kmin = min(kmin, rkey);
+      kmax = max(kmax, rkey);
+    }
+  }
+  uint64_t XB = 1ull;
+  if (p.B > 0 && beff < leff) {
+    wave_min_max_u32(kmin, kmax);
+    if (lane_id() == 0 && kmin <= kmax) {
+      atomicMin(&rkb[0], kmin);
+      atomicMax(&rkb[1], kmax);
+    }
+    __syncthreads();
+    const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
+    XB = select_top_regs<SB, NPD>(rc, beff, b_hi, b_lo, tl, dslots, true);
+  }
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  compact_ordered<SB, NPD>(e, X, leff, wcnt, scratch, dslots, [&](uint32_t o, uint64_t x, int i) {
+    out_idx[o] = (int32_t)composite_index(x);
+    out_rank[o] = r[i];
+  });
+  if (p.B > 0) {
+    int32_t* fin = p.fin_idx + (int64_t)item * p.B;
+    compact_ordered<SB, NPD>(rc, XB, beff, wcnt, scratch, dslots,
+                             [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast finish (every scan workgroup's candidates fit its compact list, at
+// most FAST_LISTS workgroups per item, at most FAST_M candidates): every wave
+// loads its share of the compact lists and places them in LDS in list order
+// (ascending key order) at offsets from a wave-level scan of the list counts;
+// after one barrier every thread takes its dense slots into registers, and
+// the two selects and the ordered compactions run there.
+constexpr int FAST_LISTS = 256;  // scan workgroups per item (caches up to 2M keys)
+constexpr int FAST_M = 8192;     // candidates staged in LDS
+constexpr size_t kFastComp = 0;                                              // uint64[FAST_M]
+constexpr size_t kFastRank = kFastComp + sizeof(uint64_t) * FAST_M;          // float[FAST_M]
+static_assert(FAST_M == NPD * SB && kFastRank + sizeof(float) * FAST_M <= kFinStage,
+              "the fast finish stages inside the finish kernel's staging area");
+
+// Exclusive scan within a wave (all 64 lanes active).
+SVA_DEV uint32_t wave_excl_scan(uint32_t v) { return wave_incl_scan(v) - v; }
+
+// The fast finish of an item; false (uniformly, before any output or LDS
+// write) when its conditions do not hold.
+SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32_t* rkb, uint32_t* wcnt,
+                         uint32_t* scratch, const TopLds& tl) {
+#pragma clang fp contract(off)
+  const SummonParams& p = a.p;
+  const int W = a.W;
+  if (W > FAST_LISTS) return false;
+  const int lane = lane_id();
+  const int wid = threadIdx.x / WAVE;
+  const int64_t g0 = (int64_t)item * W;
+  // list counts: lane j holds lists 4j .. 4j + 3
+  uint32_t tot[4], alw[4], lsum = 0, asum = 0;
+  bool over = false;
 #pragma unroll
-      for (int h = 0; h < DH; ++h) {
-        const uint32_t mm = mk[DH * k + h];
-        if ((mm >> l) & 1u) emit(o + (uint32_t)__popc(mm & below), e[DH * k + h], rnk[DH * k + h]);
-        o += (uint32_t)__popc(mm);
+  for (int i = 0; i < 4; ++i) {
+    const int l = 4 * lane + i;
+    tot[i] = l < W ? a.wg_count[2 * (g0 + l)] : 0u;
+    alw[i] = l < W ? a.wg_count[2 * (g0 + l) + 1] : 0u;
+  }
+  // this wave's lists 16 k + wid: entry `lane` of each, issued with the counts
+  constexpr int KW = FAST_LISTS / SNW;
+  uint64_t comp[KW];
+  float rank[KW];
+#pragma unroll
+  for (int k = 0; k < KW; ++k) {
+    const int l = SNW * k + wid;
+    comp[k] = 0ull;
+    rank[k] = 0.0f;
+    if (l < W) {
+      comp[k] = a.wg_cand[(g0 + l) * WG_CAP + lane];
+      rank[k] = a.wg_rank[(g0 + l) * WG_CAP + lane];
+    }
+  }
+  uint32_t loc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    loc[i] = lsum;
+    lsum += tot[i];
+    asum += alw[i];
+    over = over || tot[i] > (uint32_t)WG_CAP;
+  }
+  const uint32_t M = wave_sum_dpp(lsum), A = wave_sum_dpp(asum);
+  const bool overflow = __builtin_amdgcn_ballot_w64(over) != 0ull;
+  const int leff = (int)min((uint32_t)p.L, A);
+  const int beff = min(p.B, leff);
+  if (overflow || M > (uint32_t)FAST_M || M < (uint32_t)leff) return false;
+  if (threadIdx.x == 0) {
+    p.sl_count[item] = leff;
+    if (p.B > 0) p.fin_count[item] = beff;
+  }
+  if (leff == 0) return true;
+  if (threadIdx.x == 0) {
+    rkb[0] = 0xFFFFFFFFu;  // smallest and largest rank key of the shortlist
+    rkb[1] = 0u;
+  }
+  uint64_t* lcomp = (uint64_t*)(lds + kFastComp);
+  float* lrank = (float*)(lds + kFastRank);
+  const uint32_t base = wave_excl_scan(lsum);
+  // list 16 k + wid lives in lane (16 k + wid) / 4 at element wid % 4
+  const int el = wid & 3;
+  const uint32_t my_off = base + (el == 0 ? loc[0] : el == 1 ? loc[1] : el == 2 ? loc[2] : loc[3]);
+  const uint32_t my_tot = el == 0 ? tot[0] : el == 1 ? tot[1] : el == 2 ? tot[2] : tot[3];
+#pragma unroll
+  for (int k = 0; k < KW; ++k) {
+    const int l = SNW * k + wid;
+    if (l < W) {  // uniform
+      const int src = l >> 2;
+      const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
+      const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
+      if ((uint32_t)lane < c) {
+        lcomp[o + lane] = comp[k];
+        lrank[o + lane] = rank[k];
       }
     }
   }
+  __syncthreads();
+  // dense slots in registers: candidate t + i SB at thread t, slot i (list order)
+  const int t = threadIdx.x;
+  const int dslots = ((int)M + SB - 1) / SB;
+  uint64_t e[NPD];
+  float r[NPD];
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    const int j = t + i * SB;
+    const bool in = i < dslots && j < (int)M;
+    e[i] = in ? lcomp[j] : 0ull;
+    r[i] = in ? lrank[j] : 0.0f;
+  }
+  __syncthreads();  // the staging area is free: the selects' histograms overlay it
+  const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
+  const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
+  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPD>(e, leff, c_hi, c_lo, tl, dslots, true);
+  // budget: the beff largest (rank key, key index) composites of the shortlist
+  uint64_t rc[NPD];
+  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    rc[i] = 0ull;
+    if (i < dslots && e[i] != 0ull && e[i] >= X) {
+      const uint32_t rkey = f2key(r[i]);
+      rc[i] = composite(rkey, composite_index(e[i]));
+      kmin = min(kmin, rkey);
+      kmax = max(kmax, rkey);
+    }
+  }
+  uint64_t XB = 1ull;
+  if (p.B > 0 && beff < leff) {
+    wave_min_max_u32(kmin, kmax);
+    if (lane == 0 && kmin <= kmax) {
+      atomicMin(&rkb[0], kmin);
+      atomicMax(&rkb[1], kmax);
+    }
+    __syncthreads();
+    const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
+    XB = select_top_regs<SB, NPD>(rc, beff, b_hi, b_lo, tl, dslots, true);
+  }
+  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+  float* out_rank = p.sl_rank + (int64_t)item * p.L;
+  compact_ordered<SB, NPD>(e, X, leff, wcnt, scratch, dslots, [&](uint32_t o, uint64_t x, int i) {
+    out_idx[o] = (int32_t)composite_index(x);
+    out_rank[o] = r[i];
+  });
+  if (p.B > 0) {
+    int32_t* fin = p.fin_idx + (int64_t)item * p.B;
+    compact_ordered<SB, NPD>(rc, XB, beff, wcnt, scratch, dslots,
+                             [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
+  }
+  return true;
 }
 
 // Finish of an item: shortlist select, its outputs with the ranks the scan
 // computed, and (B > 0) the budget select, one workgroup per item.  The
 // candidate lists are in ascending key order, and so is every output.
-//   direct  (every list <= DCAP entries, <= 512 lists): lists gathered into
-//           registers, 16 lanes per list; the selected load their ranks;
-//           list-ordered compaction by per-list ballots and a scan over the
-//           lists;
+//   dense   (every list <= 48 entries, <= 512 lists, M <= 8192): lists
+//           and ranks gathered into registers, 16 lanes per list, moved
+//           through LDS to dense slots in ascending key order, both selects
+//           and both ordered compactions there;
 //   staged  (M <= LDS_CAND, <= STAGE_LISTS lists): lists staged in LDS in
 //           list order, then into registers; the selected find their list
 //           (binary search over the staging offsets) for their ranks;
@@ -752,6 +780,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
   const int item = blockIdx.x;
+  if (finish_fast(a, item, lds, rkb, wcnt, scratch, tl)) return;
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int nsub = a.W * NW;
@@ -761,11 +790,10 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   const float* crank = a.cand_rank + (int64_t)item * nsub * WAVE_KEYS;
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
   float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  // 1. totals: candidates M, allowed keys A, longest list; list counts
+  // 1. list counts, their offsets in list order (nsub <= SB), totals:
+  // candidates M, allowed keys A, longest list
   if (t == 0) {
-    shared[0] = 0u;  // M
-    shared[1] = 0u;  // longest list (when nsub <= SB), if over 32
-    shared[2] = 0u;  // some list longer than DCAP
+    shared[1] = 0u;  // longest list (nsub <= SB)
     shared[3] = 0u;  // A
     rkb[0] = 0xFFFFFFFFu;  // smallest and largest rank key of the shortlist
     rkb[1] = 0u;
@@ -776,16 +804,21 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     al += nallow[sidx];
   }
   if (nsub <= SB) lcnt[t] = m;
-  const uint32_t wm = wave_sum_dpp(m), wa = wave_sum_dpp(al);
-  __syncthreads();
-  if (lane == 0) {
-    atomicAdd(&shared[0], wm);
-    atomicAdd(&shared[3], wa);
+  uint32_t M;
+  const uint32_t list_off = block_excl_scan<SB>(m, scratch, &M);
+  if (nsub <= SB) loff[t] = list_off;
+  {
+    const uint32_t wa = wave_sum_dpp(al);
+    uint32_t mn = m, mx = m;
+    wave_min_max_u32(mn, mx);
+    if (lane == 0) {
+      atomicAdd(&shared[3], wa);
+      atomicMax(&shared[1], mx);
+    }
   }
-  if (m > (uint32_t)DCAP) atomicOr(&shared[2], 1u);
-  if (m > 32u) atomicMax(&shared[1], m);
   __syncthreads();
-  const uint32_t M = shared[0], A = shared[3];
+  const uint32_t A = shared[3];
+  const uint32_t longest = shared[1];
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
   if (t == 0) {
@@ -793,11 +826,21 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     if (p.B > 0) p.fin_count[item] = beff;
   }
   if (leff == 0) return;
-  const bool long_lists = shared[2] != 0u;
-  const uint32_t longest = shared[1];
   // bounds of every candidate composite: sums in [floor, upper bound of any sum]
   const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
   const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
+  if (M >= (uint32_t)leff && M <= (uint32_t)(NPD * SB) && nsub <= DL_LISTS && longest <= 48u) {
+    if (longest <= 32u) {
+      uint64_t e_sp[2 * DK];
+      gather_lists<2>(cand, nsub, e_sp);
+      finish_dense<2>(a, item, nsub, leff, beff, M, c_lo, c_hi, e_sp, lds, lcnt, loff, rkb, wcnt, scratch, tl);
+    } else {
+      uint64_t e3[3 * DK];
+      gather_lists<3>(cand, nsub, e3);
+      finish_dense<3>(a, item, nsub, leff, beff, M, c_lo, c_hi, e3, lds, lcnt, loff, rkb, wcnt, scratch, tl);
+    }
+    return;
+  }
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;  // rank keys this thread emitted
   auto emit = [&](uint32_t o, uint64_t x, float rank) {
     const uint32_t key = composite_index(x);
@@ -809,10 +852,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     kmax = max(kmax, rkey);
   };
   bool dense = true;  // rank composites in rk (else sl + ranks in LDS)
-  if (M >= (uint32_t)leff && nsub <= DL_LISTS && !long_lists) {
-    if (longest > 32u) finish_direct<3>(a, item, nsub, leff, M, c_lo, c_hi, lcnt, loff, tl, scratch, emit);
-    else finish_direct<2>(a, item, nsub, leff, M, c_lo, c_hi, lcnt, loff, tl, scratch, emit);
-  } else if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND && nsub <= STAGE_LISTS) {
+  if (M >= (uint32_t)leff && M <= (uint32_t)LDS_CAND && nsub <= STAGE_LISTS) {
     // staged: lists into LDS in list order
     if (nsub <= SB) {
       loff[t] = block_excl_scan<SB>(m, scratch, nullptr);
@@ -983,18 +1023,17 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   finish_budget<NPB>(p, item, leff, beff, e2, rb ? b_hi : vor, rb ? b_lo : vand, rb, tl, wcnt, scratch);
 }
 
-template <int S, bool SMALLC, bool MASKED, bool FUSED = false>
+template <int S, bool SMALLC, bool MASKED>
 int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED, FUSED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream,
-                     a);
+  hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
   SVA_CHECK_LAUNCH("wide_scan_kernel");
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)wide_finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (int)kFinLds),
-                  "hipFuncSetAttribute(wide_finish_kernel)");
-    attr_set = true;
-  }
+  static std::once_flag attr_once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(attr_once, [] {
+    attr_err = hipFuncSetAttribute((const void*)wide_finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)kFinLds);
+  });
+  SVA_CHECK_HIP(attr_err, "hipFuncSetAttribute(wide_finish_kernel)");
   hipLaunchKernelGGL(wide_finish_kernel, dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
   SVA_CHECK_LAUNCH("wide_finish_kernel");
   return SVA_OK;
@@ -1007,11 +1046,14 @@ int launch_wide_s(const WideArgs& a, int64_t items, bool masked, hipStream_t str
   return masked ? launch_wide<S, false, true>(a, items, stream) : launch_wide<S, false, false>(a, items, stream);
 }
 
-// Workspace: per-wave counters, then per-wave candidate lists.  Every word a
-// call reads was written earlier in the same call, so no state is carried
-// between calls and calls of any shape can share one buffer.
+// Workspace: per-wave counters, per-workgroup counters, the workgroups'
+// compact lists, then the per-wave candidate lists.  Every word a call reads
+// was written earlier in the same call, so no state is carried between calls
+// and calls of any shape can share one buffer.
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t counters_bytes(int64_t items, int64_t W) {
-  return ((size_t)(2 * items * W * NW) * sizeof(uint32_t) + 255) & ~(size_t)255;
+  return align256((size_t)(2 * items * W * NW) * sizeof(uint32_t)) + align256((size_t)(2 * items * W) * sizeof(uint32_t)) +
+         align256((size_t)(items * W * WG_CAP) * (sizeof(uint64_t) + sizeof(float)));
 }
 
 }  // namespace
@@ -1036,17 +1078,7 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
 }
 
-bool summon_wide_fused_eligible(const SummonParams& p, const FusedQuery& f) {
-  if (!summon_wide_eligible(p, p.H) || p.offs != nullptr || p.Q != 1) return false;
-  if (f.D != 64 || p.R != 64 || p.C != 64 || p.S != 4) return false;
-  if (p.mask_type != MASK_NONE && p.mask_type != MASK_BOOL) return false;  // every key allowed
-  if (f.q_dtype < 0 || f.q_dtype > 2 || f.q == nullptr || f.scale == nullptr) return false;
-  if (((uintptr_t)f.q_proj & 15u) != 0 || ((uintptr_t)f.codebooks & 15u) != 0) return false;
-  return true;
-}
-
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                     const FusedQuery* f) {
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const size_t need = summon_wide_workspace_bytes(1, p.H, 1, p.N, p.L);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
@@ -1057,12 +1089,11 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   char* ws = (char*)workspace;
   a.ncand = (uint32_t*)ws;
   a.nallow = a.ncand + items * a.W * NW;
+  a.wg_count = (uint32_t*)(ws + align256((size_t)(2 * items * a.W * NW) * sizeof(uint32_t)));
+  a.wg_cand = (uint64_t*)((char*)a.wg_count + align256((size_t)(2 * items * a.W) * sizeof(uint32_t)));
+  a.wg_rank = (float*)(a.wg_cand + items * a.W * WG_CAP);
   a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
   a.cand_rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
-  if (f != nullptr) {
-    a.f = *f;
-    return launch_wide<4, true, false, true>(a, items, stream);
-  }
   // a bool mask allows every key (the reference's `mask > -1e4` rule)
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
   switch (p.S) {

@@ -118,25 +118,32 @@ def test_wide_workspace_shared_across_shapes(device):
         _check(codes, k_low, *res, 1024)
 
 
+def _sample_blocks(N, S):
+    # the floor estimate's sample layout: one block of 32 keys per 256 keys,
+    # at least 64 blocks, at most 32 KB of codes, block starts spread evenly
+    # over the cache and rounded down to 16 keys
+    return min(max(N // 256, 64), 32768 // (32 * S))
+
+
 def test_wide_sampled_floor_overshoot(device):
-    # The threshold estimate samples 64 blocks of 32 keys spread evenly over
-    # the cache (block starts rounded down to 16 keys).  Giving exactly those
-    # keys the best code of every subspace puts the estimate at the top of
-    # the score range, so fewer than L keys reach it and the exact all-keys
-    # selection must take over; with L equal to the sample size the rigged
-    # keys alone fill the shortlist.  Both the two-call path and the fused
-    # lookup (which samples the same keys) are checked.
+    # Giving exactly the sampled keys the best code of every subspace puts
+    # the estimate at the top of the score range, so only the rigged keys
+    # reach it: with L above the sample size fewer than L keys do, and the
+    # exact all-keys selection must take over; with L equal to the sample
+    # size the rigged keys alone fill the shortlist.  Both the two-call path
+    # and the one-call lookup are checked.
     from sva_amd import kernels
 
-    N, S, C, H, BLOCKS, KEYS = 100000, 4, 64, 3, 64, 32
+    N, S, C, H, KEYS = 40000, 4, 64, 3, 32
+    blocks = _sample_blocks(N, S)
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=19)
     ql = oracle.query_low(q, q_proj, scale)[:, 0]
     for h in range(H):
         best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
-        for blk in range(BLOCKS):
-            n0 = (blk * (N - KEYS) // (BLOCKS - 1)) & ~15
+        for blk in range(blocks):
+            n0 = (blk * (N - KEYS) // (blocks - 1)) & ~15
             codes[h, n0:n0 + KEYS] = best
-    for L in (3000, 2048):
+    for L in (blocks * KEYS + 1000, blocks * KEYS):
         res = _summon(device, codes, k_low, q, q_proj, scale, cb, L)
         _check(codes, k_low, *res, L)
         q_low, lut, rng, sl_idx, sl_rank, sl_count, _, _ = kernels.lookup_select(
