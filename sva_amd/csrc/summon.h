@@ -10,7 +10,7 @@ constexpr int kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 // Sampled shortlist-floor estimate of a single-query uint8 scan, computed by
 // the query table kernel: `blocks` contiguous blocks of SAMPLE_KEYS keys
 // spread over the cache (one block per 256 keys, at least SAMPLE_MIN_BLOCKS,
-// at most SAMPLE_MAX_BYTES of codes), a histogram of their sums over
+// at most SAMPLE_MAX_BLOCKS and SAMPLE_MAX_BYTES of codes), a histogram of their sums over
 // SAMPLE_BINS bins, and the bin of the k-th largest sum, k chosen so that
 // about max(SAMPLE_TARGET * L, SAMPLE_MIN_CAND) keys reach the floor.  The
 // floor is only a hint: an overshoot (fewer than L keys above it) costs the
@@ -22,6 +22,7 @@ constexpr int SAMPLE_KEYS = 32;
 constexpr int SAMPLE_BINS = 1024;
 constexpr int SAMPLE_MIN_BLOCKS = 64;
 constexpr int SAMPLE_MAX_BYTES = 32768;
+constexpr int SAMPLE_MAX_BLOCKS = 256;  // at most 8K sampled keys
 constexpr double SAMPLE_TARGET = 2.0;
 constexpr double SAMPLE_MIN_CAND = 4096.0;
 constexpr int SAMPLE_MIN_RANK = 16;
@@ -29,7 +30,8 @@ constexpr int SAMPLE_MAX_S = 8;  // subspaces of the sampled scan
 
 // Sample blocks for a cache of n_keys keys with S subspaces.
 __host__ __device__ inline int sample_blocks(int64_t n_keys, int64_t S) {
-  const int64_t cap = SAMPLE_MAX_BYTES / (SAMPLE_KEYS * S);
+  int64_t cap = SAMPLE_MAX_BYTES / (SAMPLE_KEYS * S);
+  cap = cap < SAMPLE_MAX_BLOCKS ? cap : SAMPLE_MAX_BLOCKS;
   int64_t b = n_keys / 256;
   b = b < SAMPLE_MIN_BLOCKS ? SAMPLE_MIN_BLOCKS : b;
   return (int)(b < cap ? b : cap);

@@ -47,7 +47,7 @@ constexpr int STAGE_LISTS = 4096;  // lists whose staging offsets the finish ker
 // 0.125 exactly (both are the correctly rounded value of x / 8).
 constexpr float kInvSqrtR = 0.125f;
 constexpr int KL_CAP = 256;      // candidates per scan wave kept in LDS (composite and rank)
-constexpr int WG_CAP = 64;       // candidates of a scan workgroup in its compact list
+constexpr int WG_CAP = 128;      // candidates of a scan workgroup in its compact list
 constexpr int64_t kWideMinKeys = 32768;
 constexpr int64_t kMaxWideItems = 64;
 
@@ -375,9 +375,11 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, Scan
     alw += L.walw[v];
   }
   const int64_t g = (int64_t)item * a.W + w;
-  if (tot <= (uint32_t)WG_CAP && lane < (int)wc) {
-    a.wg_cand[g * WG_CAP + off + lane] = L.kc[wid][lane];
-    a.wg_rank[g * WG_CAP + off + lane] = L.kr[wid][lane];
+  if (tot <= (uint32_t)WG_CAP) {
+    for (uint32_t j = (uint32_t)lane; j < wc; j += WAVE) {
+      a.wg_cand[g * WG_CAP + off + j] = L.kc[wid][j];
+      a.wg_rank[g * WG_CAP + off + j] = L.kr[wid][j];
+    }
   }
   if (threadIdx.x == 0) {
     a.wg_count[2 * g] = tot;
@@ -433,7 +435,7 @@ static_assert(kFinLds <= (size_t)kMaxLds, "finish LDS");
 constexpr int DQ = SB / 16;          // list groups of 16 lanes
 constexpr int DK = 8;                // lists per group
 constexpr int DL_LISTS = DQ * DK;    // 512 lists: caches up to 1M keys
-constexpr int NPD = 8;              // dense slots per thread
+constexpr int NPD = 7;              // dense slots per thread
 
 // Rank score of a 64-float k_low row in torch's sum order, computed here
 // for the all-keys path: rows r of sl, one 16-lane DPP row each.
@@ -600,20 +602,118 @@ SVA_DEV void finish_dense(const WideArgs& a, int item, int nsub, int leff, int b
 
 // ---------------------------------------------------------------------------
 // Fast finish (every scan workgroup's candidates fit its compact list, at
-// most FAST_LISTS workgroups per item, at most FAST_M candidates): every wave
-// loads its share of the compact lists and places them in LDS in list order
-// (ascending key order) at offsets from a wave-level scan of the list counts;
-// after one barrier every thread takes its dense slots into registers, and
-// the two selects and the ordered compactions run there.
+// most FAST_LISTS workgroups per item, at most FAST_M candidates).
+//   fill     every wave loads its share of the compact lists and places them
+//            in LDS in list order (ascending key order) at offsets from a
+//            wave-level scan of the list counts;
+//   select   each thread takes its dense slots into registers; the shortlist
+//            threshold comes from one histogram pass over the 32-bit score
+//            keys in value bins over [floor, highest candidate], then an exact
+//            rank of the boundary bin's members; the budget threshold the
+//            same way over the shortlist's rank keys;
+//   output   one ordered compaction writes the shortlist and the budget.
+// Selection equals the (score desc, key index asc) top-k: bins are monotone
+// in the score and the boundary bin is resolved on the full composites.
 constexpr int FAST_LISTS = 256;  // scan workgroups per item (caches up to 2M keys)
-constexpr int FAST_M = 8192;     // candidates staged in LDS
+constexpr int FAST_M = NPD * SB;  // candidates staged in LDS
+constexpr int FAST_BATCH = 8;     // lists a wave loads per round
+constexpr int SMALL_CAP = 256;    // boundary-bin members ranked directly
 constexpr size_t kFastComp = 0;                                              // uint64[FAST_M]
 constexpr size_t kFastRank = kFastComp + sizeof(uint64_t) * FAST_M;          // float[FAST_M]
-static_assert(FAST_M == NPD * SB && kFastRank + sizeof(float) * FAST_M <= kFinStage,
-              "the fast finish stages inside the finish kernel's staging area");
+constexpr size_t kFastHist = kFastRank + sizeof(float) * FAST_M;             // uint32[4096]
+constexpr size_t kFastSmall = kFastHist + sizeof(uint32_t) * 4096;           // uint64[SMALL_CAP]
+constexpr size_t kFastMisc = kFastSmall + sizeof(uint64_t) * SMALL_CAP;      // uint32[64]
+constexpr size_t kFastEnd = kFastMisc + sizeof(uint32_t) * 64;
+static_assert(WG_CAP == 2 * WAVE, "two compact-list entries per lane");
+static_assert(kFastEnd <= kFinStage, "the fast finish stays inside the finish kernel's staging area");
 
 // Exclusive scan within a wave (all 64 lanes active).
 SVA_DEV uint32_t wave_excl_scan(uint32_t v) { return wave_incl_scan(v) - v; }
+SVA_DEV uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// LDS scalars of the fast finish (misc): per-wave values at [16 * slot + wave].
+struct FastMisc {
+  uint32_t* m;
+  SVA_DEV uint32_t& wave(int slot, int w) const { return m[16 * slot + w]; }
+  SVA_DEV uint32_t& res(int k) const { return m[48 + k]; }
+  SVA_DEV uint64_t& res64() const { return *reinterpret_cast<uint64_t*>(m + 56); }
+};
+
+// Threshold of the k largest nonzero composites held in e[] (dense slots;
+// the key part of every nonzero one inside [klo, khi]): values >= the result
+// are exactly the k largest.  Every thread of the block calls it; hist must
+// be zero on entry.  Uses misc slots 0 and res.
+SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32_t klo, uint32_t khi, uint32_t* hist,
+                             uint64_t* small, const FastMisc& f, const TopLds& tl, bool* exact) {
+  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  const uint32_t range = khi - klo;
+  const int sh = range < 4096u ? 0 : (32 - __clz((int)range)) - 12;
+#pragma unroll
+  for (int i = 0; i < NPD; ++i)
+    if (i < dslots && e[i] != 0ull) atomicAdd(&hist[((uint32_t)(e[i] >> 32) - klo) >> sh], 1u);
+  __syncthreads();
+  // thread t owns bins 4095 - 4 t - j (j = 0..3), from the top
+  const uint4 h = reinterpret_cast<const uint4*>(hist)[1023 - t];
+  const uint32_t c[4] = {h.w, h.z, h.y, h.x};
+  const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+  const uint32_t incl = wave_incl_scan(mine);
+  if (lane == WAVE - 1) f.wave(0, wid) = incl;
+  __syncthreads();
+  uint32_t above = incl - mine;
+  for (int v = 0; v < wid; ++v) above += f.wave(0, v);
+  {
+    uint32_t a = above;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (a < (uint32_t)k && a + c[j] >= (uint32_t)k) {
+        f.res(0) = 4095u - 4u * (uint32_t)t - (uint32_t)j;
+        f.res(1) = a;
+        f.res(2) = c[j];
+      }
+      a += c[j];
+    }
+  }
+  if (t == 0) f.res(3) = 0u;
+  __syncthreads();
+  const uint32_t b = f.res(0), need = (uint32_t)k - f.res(1), cnt = f.res(2);
+  const uint32_t bkey = klo + (b << sh);  // lowest score key of the boundary bin
+  *exact = true;
+  if (cnt == need) return (uint64_t)bkey << 32;
+  if (cnt > (uint32_t)SMALL_CAP) {
+    // a massive tie class: the general register select
+    *exact = false;
+    return 0ull;
+  }
+  // the boundary bin's members, then each one's rank among them
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    if (i < dslots) {  // uniform
+      const bool in = e[i] != 0ull && (((uint32_t)(e[i] >> 32) - klo) >> sh) == b;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(in);
+      if (m != 0ull) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&f.res(3), (uint32_t)__popcll(m));
+        base = (uint32_t)__shfl((int)base, 0, WAVE);
+        if (in) small[base + lanes_below(m)] = e[i];
+      }
+    }
+  }
+  __syncthreads();
+  {
+    // four lanes per member: lane q of member g compares it with members q, q + 4, ...
+    const int g = t >> 2, q = t & 3;
+    const uint64_t v = g < (int)cnt ? small[g] : 0ull;
+    uint32_t greater = 0;
+    for (int o = q; o < (int)cnt; o += 4) greater += small[o] > v ? 1u : 0u;
+    greater += __shfl_xor(greater, 1, WAVE);
+    greater += __shfl_xor(greater, 2, WAVE);
+    if (q == 0 && g < (int)cnt && greater == need - 1u) f.res64() = v;
+  }
+  __syncthreads();
+  return f.res64();
+}
 
 // The fast finish of an item; false (uniformly, before any output or LDS
 // write) when its conditions do not hold.
@@ -623,38 +723,43 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const SummonParams& p = a.p;
   const int W = a.W;
   if (W > FAST_LISTS) return false;
+  const int t = threadIdx.x;
   const int lane = lane_id();
-  const int wid = threadIdx.x / WAVE;
+  const int wid = t / WAVE;
   const int64_t g0 = (int64_t)item * W;
   // list counts: lane j holds lists 4j .. 4j + 3
-  uint32_t tot[4], alw[4], lsum = 0, asum = 0;
+  uint32_t tot[4], lsum = 0, asum = 0;
   bool over = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int l = 4 * lane + i;
     tot[i] = l < W ? a.wg_count[2 * (g0 + l)] : 0u;
-    alw[i] = l < W ? a.wg_count[2 * (g0 + l) + 1] : 0u;
+    asum += l < W ? a.wg_count[2 * (g0 + l) + 1] : 0u;
   }
-  // this wave's lists 16 k + wid: entry `lane` of each, issued with the counts
-  constexpr int KW = FAST_LISTS / SNW;
-  uint64_t comp[KW];
-  float rank[KW];
+  // the first round of this wave's lists (16 k + wid, k < FAST_BATCH), issued with the counts
+  uint64_t comp[2 * FAST_BATCH];
+  float rank[2 * FAST_BATCH];
+  auto load_round = [&](int r) {
 #pragma unroll
-  for (int k = 0; k < KW; ++k) {
-    const int l = SNW * k + wid;
-    comp[k] = 0ull;
-    rank[k] = 0.0f;
-    if (l < W) {
-      comp[k] = a.wg_cand[(g0 + l) * WG_CAP + lane];
-      rank[k] = a.wg_rank[(g0 + l) * WG_CAP + lane];
+    for (int k = 0; k < FAST_BATCH; ++k) {
+      const int l = SNW * (r * FAST_BATCH + k) + wid;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        comp[2 * k + h] = 0ull;
+        rank[2 * k + h] = 0.0f;
+        if (l < W) {
+          comp[2 * k + h] = a.wg_cand[(g0 + l) * WG_CAP + lane + WAVE * h];
+          rank[2 * k + h] = a.wg_rank[(g0 + l) * WG_CAP + lane + WAVE * h];
+        }
+      }
     }
-  }
+  };
+  load_round(0);
   uint32_t loc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     loc[i] = lsum;
     lsum += tot[i];
-    asum += alw[i];
     over = over || tot[i] > (uint32_t)WG_CAP;
   }
   const uint32_t M = wave_sum_dpp(lsum), A = wave_sum_dpp(asum);
@@ -662,86 +767,149 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
   if (overflow || M > (uint32_t)FAST_M || M < (uint32_t)leff) return false;
-  if (threadIdx.x == 0) {
+  if (t == 0) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
   }
   if (leff == 0) return true;
-  if (threadIdx.x == 0) {
-    rkb[0] = 0xFFFFFFFFu;  // smallest and largest rank key of the shortlist
-    rkb[1] = 0u;
-  }
   uint64_t* lcomp = (uint64_t*)(lds + kFastComp);
   float* lrank = (float*)(lds + kFastRank);
+  uint32_t* hist = (uint32_t*)(lds + kFastHist);
+  uint64_t* small = (uint64_t*)(lds + kFastSmall);
+  const FastMisc f{(uint32_t*)(lds + kFastMisc)};
   const uint32_t base = wave_excl_scan(lsum);
   // list 16 k + wid lives in lane (16 k + wid) / 4 at element wid % 4
   const int el = wid & 3;
   const uint32_t my_off = base + (el == 0 ? loc[0] : el == 1 ? loc[1] : el == 2 ? loc[2] : loc[3]);
   const uint32_t my_tot = el == 0 ? tot[0] : el == 1 ? tot[1] : el == 2 ? tot[2] : tot[3];
+  uint32_t kmax = 0u;  // highest score key placed by this lane
+  for (int r = 0; r * FAST_BATCH * SNW < W; ++r) {
+    if (r > 0) load_round(r);
 #pragma unroll
-  for (int k = 0; k < KW; ++k) {
-    const int l = SNW * k + wid;
-    if (l < W) {  // uniform
-      const int src = l >> 2;
-      const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
-      const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
-      if ((uint32_t)lane < c) {
-        lcomp[o + lane] = comp[k];
-        lrank[o + lane] = rank[k];
+    for (int k = 0; k < FAST_BATCH; ++k) {
+      const int l = SNW * (r * FAST_BATCH + k) + wid;
+      if (l < W) {  // uniform
+        const int src = l >> 2;
+        const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
+        const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t j = (uint32_t)(lane + WAVE * h);
+          if (j < c) {
+            lcomp[o + j] = comp[2 * k + h];
+            lrank[o + j] = rank[2 * k + h];
+            kmax = max(kmax, (uint32_t)(comp[2 * k + h] >> 32));
+          }
+        }
       }
     }
   }
+  {
+    uint32_t mn = 0u;
+    wave_min_max_u32(mn, kmax);
+    if (lane == 0) f.wave(1, wid) = kmax;
+  }
+  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
   // dense slots in registers: candidate t + i SB at thread t, slot i (list order)
-  const int t = threadIdx.x;
   const int dslots = ((int)M + SB - 1) / SB;
   uint64_t e[NPD];
-  float r[NPD];
+  float rv[NPD];
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
     const int j = t + i * SB;
     const bool in = i < dslots && j < (int)M;
     e[i] = in ? lcomp[j] : 0ull;
-    r[i] = in ? lrank[j] : 0.0f;
+    rv[i] = in ? lrank[j] : 0.0f;
   }
-  __syncthreads();  // the staging area is free: the selects' histograms overlay it
-  const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
-  const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
-  const uint64_t X = (uint32_t)leff == M ? 1ull : select_top_regs<SB, NPD>(e, leff, c_hi, c_lo, tl, dslots, true);
-  // budget: the beff largest (rank key, key index) composites of the shortlist
+  uint32_t khi = 0u;
+  for (int v = 0; v < SNW; ++v) khi = max(khi, f.wave(1, v));
+  const uint32_t klo = f2key(item_floor(p, item) * kInvSqrtR);
+  bool exact = true;
+  uint64_t X = 1ull;
+  if ((uint32_t)leff < M) {
+    X = fast_select(e, dslots, leff, klo, max(khi, klo), hist, small, f, tl, &exact);
+    if (!exact) {
+      __syncthreads();
+      return false;  // a tie class too large to rank directly: the general paths
+    }
+  }
+  // budget composites of the shortlist: (rank key, key index)
   uint64_t rc[NPD];
-  uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
+  uint32_t rmin = 0xFFFFFFFFu, rmax = 0u;
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
     rc[i] = 0ull;
     if (i < dslots && e[i] != 0ull && e[i] >= X) {
-      const uint32_t rkey = f2key(r[i]);
-      rc[i] = composite(rkey, composite_index(e[i]));
-      kmin = min(kmin, rkey);
-      kmax = max(kmax, rkey);
+      const uint32_t rk = f2key(rv[i]);
+      rc[i] = composite(rk, composite_index(e[i]));
+      rmin = min(rmin, rk);
+      rmax = max(rmax, rk);
     }
   }
   uint64_t XB = 1ull;
   if (p.B > 0 && beff < leff) {
-    wave_min_max_u32(kmin, kmax);
-    if (lane == 0 && kmin <= kmax) {
-      atomicMin(&rkb[0], kmin);
-      atomicMax(&rkb[1], kmax);
+    wave_min_max_u32(rmin, rmax);
+    if (lane == 0) {
+      f.wave(1, wid) = rmin;
+      f.wave(2, wid) = rmax;
     }
+    reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
     __syncthreads();
-    const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
-    XB = select_top_regs<SB, NPD>(rc, beff, b_hi, b_lo, tl, dslots, true);
+    uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+    for (int v = 0; v < SNW; ++v) {
+      lo = min(lo, f.wave(1, v));
+      hi = max(hi, f.wave(2, v));
+    }
+    bool ex2 = true;
+    XB = fast_select(rc, dslots, beff, lo, hi, hist, small, f, tl, &ex2);
+    if (!ex2) {
+      __syncthreads();
+      return false;
+    }
+  }
+  // outputs in list order (ascending key order): per (slot, wave) counts of
+  // both selections packed in one word, one scan, then the writes
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    if (i < dslots) {  // uniform
+      const bool sl = e[i] != 0ull && e[i] >= X;
+      const uint64_t ml = __builtin_amdgcn_ballot_w64(sl);
+      const uint64_t mb = __builtin_amdgcn_ballot_w64(sl && rc[i] >= XB);
+      if (lane == 0) wcnt[i * SNW + wid] = (uint32_t)__popcll(ml) | ((uint32_t)__popcll(mb) << 16);
+    }
+  }
+  __syncthreads();
+  {
+    const uint32_t v = t < dslots * SNW ? wcnt[t] : 0u;
+    const uint32_t off = block_excl_scan<SB>(v, scratch, nullptr);
+    if (t < dslots * SNW) wcnt[t] = off;
+    __syncthreads();
   }
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
   float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  compact_ordered<SB, NPD>(e, X, leff, wcnt, scratch, dslots, [&](uint32_t o, uint64_t x, int i) {
-    out_idx[o] = (int32_t)composite_index(x);
-    out_rank[o] = r[i];
-  });
-  if (p.B > 0) {
-    int32_t* fin = p.fin_idx + (int64_t)item * p.B;
-    compact_ordered<SB, NPD>(rc, XB, beff, wcnt, scratch, dslots,
-                             [&](uint32_t o, uint64_t x, int) { fin[o] = (int32_t)composite_index(x); });
+  int32_t* fin = p.B > 0 ? p.fin_idx + (int64_t)item * p.B : nullptr;
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    if (i < dslots) {  // uniform
+      const uint32_t w = wcnt[i * SNW + wid];
+      const uint32_t key = composite_index(e[i]);
+      const bool sl = e[i] != 0ull && e[i] >= X;
+      const bool sb = sl && rc[i] >= XB;
+      const uint64_t ml = __builtin_amdgcn_ballot_w64(sl);
+      const uint64_t mb = __builtin_amdgcn_ballot_w64(sb);
+      if (sl) {
+        const uint32_t o = (w & 0xFFFFu) + lanes_below(ml);
+        if (o < (uint32_t)leff) {
+          out_idx[o] = (int32_t)key;
+          out_rank[o] = rv[i];
+        }
+      }
+      if (fin != nullptr && sb) {
+        const uint32_t o = (w >> 16) + lanes_below(mb);
+        if (o < (uint32_t)beff) fin[o] = (int32_t)key;
+      }
+    }
   }
   return true;
 }
