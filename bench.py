@@ -46,6 +46,7 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=8, help="distinct layer caches rotated per step")
     ap.add_argument("--cpu-repeats", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the decode lookups")
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
@@ -109,13 +110,20 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
     codes = layer.codes.cpu().numpy()
     times = []
     used = 1
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
+    warmups = 3
+    cpu_s = 0.0
+    for i in range(repeats + warmups):
+        c0, t0 = time.process_time(), time.perf_counter()
         _, _, _, used = oracle.decode(q, q_low, keys, values, k_low, cb, codes, shortlist, budget, 64 ** -0.5)
         dt = time.perf_counter() - t0
-        if i > 0:
+        if i >= warmups:
             times.append(dt)
+            cpu_s += time.process_time() - c0
     avg_us = 1e6 * sum(times) / len(times)
+    # threads actually busy: process CPU time over wall time of the timed runs
+    # (the checker's OpenMP loop runs over the 9 heads, so at most 9 of the
+    # team's threads have work)
+    busy = cpu_s / sum(times)
     cpu_model = platform.processor() or ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -132,10 +140,12 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
     return {
         "value": round(avg_us, 1),
         "unit": "us/query",
-        "cores": int(used),
+        "cores": max(1, round(busy)),
         "kind": "port",
-        "sample": f"{repeats} decode lookups (after 1 warmup) of the same 1M-key workload, all 9 heads, "
+        "sample": f"{repeats} decode lookups (after {warmups} warmups) of the same 1M-key workload, all 9 heads, "
                   f"oracle/sva_oracle.c with OpenMP over heads",
+        "busy_threads": round(busy, 2),
+        "team_threads": int(used),
         "p50_us": round(1e6 * float(np.percentile(times, 50)), 1),
         "p95_us": round(1e6 * float(np.percentile(times, 95)), 1),
         "host_threads": threads,
@@ -553,6 +563,54 @@ def model_suite(args):
     }), flush=True)
 
 
+def graph_replay(torch, np, args, layers, plan, outs, step):
+    """The decode lookups of every rotated layer captured in one HIP graph
+    (sva_lookup_select + sva_verify through the plan's static buffers, cache
+    length fixed at capture) and replayed: whole-run µs per lookup and the
+    p50 over event-timed replays.  The first replay's outputs must equal the
+    eager outputs bit for bit, or no figure is reported."""
+
+    device = plan.device
+    n_layers = len(layers)
+    eager = [o.clone() for o in outs]
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for i in range(n_layers):
+            step(i)
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n_layers):
+            step(i)
+    for o in outs:
+        o.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(o, e) for o, e in zip(outs, eager)):
+        return {"error": "graph replay differs from the eager lookups"}
+    reps = max(1, args.steps // n_layers)
+    for _ in range(max(1, args.warmup // n_layers)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n_ev = min(reps, 100)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
+    torch.cuda._sleep(int(2e8))
+    for a, b in ev:
+        a.record()
+        graph.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = [1e3 * a.elapsed_time(b) / n_layers for a, b in ev]
+    return {"us_per_query": round(1e6 * wall / (reps * n_layers), 2), "p50_us_per_query": round(
+        float(np.percentile(per, 50)), 2), "replays": reps, "lookups_per_replay": n_layers}
+
+
 def main():
     args = parse_args()
     if args.write_profiles:
@@ -568,6 +626,7 @@ def main():
                                    "sequence (see DESIGN.md) but no multi-GPU figure is produced",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    import numpy as np
     import torch
 
     from sva_amd import _lib, kernels
@@ -639,6 +698,9 @@ def main():
             per_stage[s] += ev[j].elapsed_time(ev[j + 1])
     per_stage_us = {s: round(1e3 * v / n_ev, 2) for s, v in per_stage.items()}
     gpu_us = sum(per_stage_us.values())
+    step_us = [1e3 * ev[0].elapsed_time(ev[-1]) for ev in events]
+    eager_p50 = float(np.percentile(step_us, 50))
+    graph_res = None if args.no_graph else graph_replay(torch, np, args, layers, plan, outs, step)
 
     bytes_ = algorithmic_bytes(n, heads, subspaces, codewords, shortlist, budget)
     summon_us = per_stage_us["lookup"]
@@ -676,6 +738,9 @@ def main():
         },
         "stage_us": per_stage_us,
         "gpu_us_per_query": round(gpu_us, 2),
+        # eager: HIP events around each of the staged lookups above (stream held while the host enqueues)
+        "eager_p50_us_per_query": round(eager_p50, 2),
+        "graph": graph_res,
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
             "kernel": ("sva_lookup_select: wide_scan (query side fused) + wide_finish"

@@ -306,7 +306,12 @@ ORACLE_API int sva_oracle_decode(int64_t H, int64_t G, int64_t N, int64_t D, int
     const int64_t Lh = L < N ? L : N;
     const int64_t Bh = B < Lh ? B : Lh;
     int threads = 1;
-#pragma omp parallel
+    /* one thread per head at most: a larger team only spins at the barrier */
+    int team = 1;
+#ifdef _OPENMP
+    team = omp_get_max_threads() < H ? omp_get_max_threads() : (int)H;
+#endif
+#pragma omp parallel num_threads(team)
     {
 #ifdef _OPENMP
 #pragma omp single

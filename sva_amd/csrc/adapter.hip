@@ -109,13 +109,7 @@ extern "C" int sva_residual_adapter(const void* hidden, int hidden_dtype, int64_
                   (long long)hidden_size, lds);
   const int64_t blocks = (n_tokens + tok - 1) / tok;
   SVA_REQUIRE(blocks < (1ll << 31), "sva_residual_adapter: too many tokens");
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)residual_adapter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      sva::kMaxLds),
-                  "hipFuncSetAttribute(residual_adapter_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE(residual_adapter_kernel, sva::kMaxLds, "hipFuncSetAttribute(residual_adapter_kernel)");
   AdapterParams p;
   p.hidden = hidden;
   p.h_dtype = hidden_dtype;

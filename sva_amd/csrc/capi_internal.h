@@ -3,6 +3,7 @@
 // and leaves a message readable through sva_last_error().
 #pragma once
 #include <hip/hip_runtime.h>
+#include <mutex>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -47,4 +48,18 @@ int device_cu_count();
       sva::set_error("%s: %s", name, hipGetErrorString(e_));                     \
       return SVA_ERR_HIP;                                                        \
     }                                                                            \
+  } while (0)
+
+// Raises a kernel's dynamic LDS limit on its first launch.  The flag is a
+// std::once_flag, so host threads launching at once set it exactly once; the
+// call's result is kept and checked on every launch.
+#define SVA_SET_MAX_LDS_ONCE(fn, bytes, name)                                                    \
+  do {                                                                                           \
+    static std::once_flag once_;                                                                 \
+    static hipError_t err_ = hipSuccess;                                                         \
+    std::call_once(once_, [] {                                                                   \
+      err_ = hipFuncSetAttribute((const void*)(fn), hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                 (int)(bytes));                                                  \
+    });                                                                                          \
+    SVA_CHECK_HIP(err_, name);                                                                   \
   } while (0)

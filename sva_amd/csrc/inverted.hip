@@ -923,28 +923,10 @@ int win_cap_for(int64_t B, int refill_factor, int64_t W) {
 }
 
 int launch_select(const SelParams& p, int64_t H, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)unique_select_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      sva::kMaxLds),
-                  "hipFuncSetAttribute(unique_select_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE(unique_select_kernel, sva::kMaxLds, "hipFuncSetAttribute(unique_select_kernel)");
   hipLaunchKernelGGL(unique_select_kernel, dim3((unsigned)H), dim3(UB),
                      select_lds_bytes(std::max(p.B, p.sel_cap), p.hash), stream, p);
   SVA_CHECK_LAUNCH("unique_select_kernel");
-  return SVA_OK;
-}
-
-}  // namespace
-
-namespace {
-
-int launch_attr_once(const void* fn, bool& done, const char* name) {
-  if (!done) {
-    SVA_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds), name);
-    done = true;
-  }
   return SVA_OK;
 }
 
@@ -960,9 +942,7 @@ extern "C" int sva_postings_build(const void* codes, int code_type, int64_t code
   SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_postings_build: bad code type");
   SVA_UNSUPPORTED(C > 0 && C <= kMaxPostingCells, "sva_postings_build: %lld codewords (at most %d)", (long long)C,
                   kMaxPostingCells);
-  static bool attr = false;
-  if (int rc = launch_attr_once((const void*)postings_build_kernel, attr, "hipFuncSetAttribute(postings_build)"))
-    return rc;
+  SVA_SET_MAX_LDS_ONCE(postings_build_kernel, sva::kMaxLds, "hipFuncSetAttribute(postings_build)");
   const size_t lds = sizeof(uint32_t) * (size_t)(2 * C + PNW * C + PNW + 2);
   hipLaunchKernelGGL(postings_build_kernel, dim3((unsigned)(H * S)), dim3(PB), lds, (hipStream_t)stream, codes,
                      code_type, code_head_stride, (int)H, (int)S, (int)n_rows, (int)C, nullptr, nullptr, n_rows,
@@ -983,9 +963,7 @@ extern "C" int sva_postings_build_ragged(const void* codes, int code_type, int64
   SVA_REQUIRE(code_type >= 0 && code_type <= 3, "sva_postings_build_ragged: bad code type");
   SVA_UNSUPPORTED(C > 0 && C <= kMaxPostingCells, "sva_postings_build_ragged: %lld codewords (at most %d)",
                   (long long)C, kMaxPostingCells);
-  static bool attr = false;
-  if (int rc = launch_attr_once((const void*)postings_build_kernel, attr, "hipFuncSetAttribute(postings_build)"))
-    return rc;
+  SVA_SET_MAX_LDS_ONCE(postings_build_kernel, sva::kMaxLds, "hipFuncSetAttribute(postings_build)");
   const size_t lds = sizeof(uint32_t) * (size_t)(2 * C + PNW * C + PNW + 2);
   hipLaunchKernelGGL(postings_build_kernel, dim3((unsigned)(n_seq * H * S)), dim3(PB), lds, (hipStream_t)stream, codes,
                      code_type, code_head_stride, (int)H, (int)S, 0, (int)C, seq_offsets, postings_lens, rows,

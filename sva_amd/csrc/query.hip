@@ -525,13 +525,7 @@ __global__ void __launch_bounds__(MT_BLOCK) query_lut_multi_kernel(LutParams p) 
 
 template <int SUB>
 int launch_lut_multi(const LutParams& p, int64_t blocks, size_t lds, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)query_lut_multi_kernel<SUB>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
-                  "hipFuncSetAttribute(query_lut_multi_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE((query_lut_multi_kernel<SUB>), sva::kMaxLds, "hipFuncSetAttribute(query_lut_multi_kernel)");
   hipLaunchKernelGGL(query_lut_multi_kernel<SUB>, dim3((unsigned)blocks), dim3(MT_BLOCK), lds, stream, p);
   SVA_CHECK_LAUNCH("query_lut_multi_kernel");
   return SVA_OK;
@@ -604,13 +598,7 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_query_lut: head weights of %zu bytes exceed LDS", lds);
   const int64_t items = n_seq * H * Q;
   SVA_REQUIRE(items < (1ll << 31), "sva_query_lut: too many query items");
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)query_lut_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      sva::kMaxLds),
-                  "hipFuncSetAttribute(query_lut_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE(query_lut_kernel, sva::kMaxLds, "hipFuncSetAttribute(query_lut_kernel)");
   LutParams p;
   p.q = q;
   p.q_dtype = q_dtype;

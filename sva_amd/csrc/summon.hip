@@ -387,13 +387,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
 
 template <int NPT, int SB>
 int launch_regs(const SummonParams& p, int64_t items, size_t lds, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)summon_regs_kernel<NPT, SB>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds),
-                  "hipFuncSetAttribute(summon_regs_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE((summon_regs_kernel<NPT, SB>), kMaxLds, "hipFuncSetAttribute(summon_regs_kernel)");
   hipLaunchKernelGGL((summon_regs_kernel<NPT, SB>), dim3((unsigned)items), dim3(ITEM_BLOCK), lds, stream, p);
   SVA_CHECK_LAUNCH("summon_regs_kernel");
   return SVA_OK;
@@ -432,13 +426,7 @@ int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream) {
   const bool keys_fit = item_lds_layout(p.S, p.C, p.R, p.L, p.N, true).total <= kMaxLds;
   const ItemLds layout = item_lds_layout(p.S, p.C, p.R, p.L, p.N, keys_fit);
   SVA_UNSUPPORTED(layout.total <= kMaxLds, "sva_summon: shortlist %d with %dx%d codes exceeds LDS", p.L, p.S, p.C);
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)summon_item_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      kMaxLds),
-                  "hipFuncSetAttribute(summon_item_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE(summon_item_kernel, kMaxLds, "hipFuncSetAttribute(summon_item_kernel)");
   hipLaunchKernelGGL(summon_item_kernel, dim3((unsigned)items), dim3(ITEM_BLOCK), (size_t)layout.total, stream, p,
                      keys_fit ? 1 : 0);
   SVA_CHECK_LAUNCH("summon_item_kernel");

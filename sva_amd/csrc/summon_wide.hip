@@ -1195,13 +1195,7 @@ template <int S, bool SMALLC, bool MASKED>
 int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
   hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
   SVA_CHECK_LAUNCH("wide_scan_kernel");
-  static std::once_flag attr_once;
-  static hipError_t attr_err = hipSuccess;
-  std::call_once(attr_once, [] {
-    attr_err = hipFuncSetAttribute((const void*)wide_finish_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)kFinLds);
-  });
-  SVA_CHECK_HIP(attr_err, "hipFuncSetAttribute(wide_finish_kernel)");
+  SVA_SET_MAX_LDS_ONCE(wide_finish_kernel, kFinLds, "hipFuncSetAttribute(wide_finish_kernel)");
   hipLaunchKernelGGL(wide_finish_kernel, dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
   SVA_CHECK_LAUNCH("wide_finish_kernel");
   return SVA_OK;

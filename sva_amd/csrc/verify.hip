@@ -359,13 +359,7 @@ size_t verify_lds_bytes(int64_t grp, int64_t B, int64_t D) {
 
 template <int DT, bool SEQ>
 int launch_part(const VerifyParams& p, dim3 grid, size_t lds, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)verify_part_kernel<DT, SEQ>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
-                  "hipFuncSetAttribute(verify_part_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE((verify_part_kernel<DT, SEQ>), sva::kMaxLds, "hipFuncSetAttribute(verify_part_kernel)");
   hipLaunchKernelGGL((verify_part_kernel<DT, SEQ>), grid, dim3(VB), lds, stream, p);
   SVA_CHECK_LAUNCH("verify_part_kernel");
   return SVA_OK;

@@ -563,13 +563,7 @@ size_t write_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C) {
 
 template <int SUB>
 int launch_write(const WriteParams& p, dim3 grid, size_t lds, hipStream_t stream) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    SVA_CHECK_HIP(hipFuncSetAttribute((const void*)write_encode_kernel<SUB>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
-                  "hipFuncSetAttribute(write_encode_kernel)");
-    attr_set = true;
-  }
+  SVA_SET_MAX_LDS_ONCE((write_encode_kernel<SUB>), sva::kMaxLds, "hipFuncSetAttribute(write_encode_kernel)");
   hipLaunchKernelGGL(write_encode_kernel<SUB>, grid, dim3(WT), lds, stream, p);
   SVA_CHECK_LAUNCH("write_encode_kernel");
   return SVA_OK;
@@ -639,13 +633,7 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
       return D == 64 ? launch_persistent<64, 4, 16, 64>(p, tiles, st) : launch_persistent<128, 4, 16, 64>(p, tiles, st);
   }
   if (R % 16 == 0 && C % 16 == 0 && D % 4 == 0) {
-    static bool attr_set = false;
-    if (!attr_set) {
-      SVA_CHECK_HIP(hipFuncSetAttribute((const void*)write_encode_mfma_kernel,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, sva::kMaxLds),
-                    "hipFuncSetAttribute(write_encode_mfma_kernel)");
-      attr_set = true;
-    }
+    SVA_SET_MAX_LDS_ONCE(write_encode_mfma_kernel, sva::kMaxLds, "hipFuncSetAttribute(write_encode_mfma_kernel)");
     hipLaunchKernelGGL(write_encode_mfma_kernel, grid, dim3(WT), lds, (hipStream_t)stream, p);
     SVA_CHECK_LAUNCH("write_encode_mfma_kernel");
     return SVA_OK;

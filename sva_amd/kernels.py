@@ -16,16 +16,16 @@ from . import _lib
 from ._lib import check, code_type, dtype_code, lib, ptr, require_device, stream_handle
 
 
-_workspaces: dict[tuple[torch.device, str], torch.Tensor] = {}
+_workspaces: dict[tuple[torch.device, str, int], torch.Tensor] = {}
 
 
 def workspace(device: torch.device, nbytes: int, kind: str = "summon") -> torch.Tensor:
-    """Per-device scratch buffers, one per kind, grown on demand.  The kernels
-    carry no state in them between calls, so one buffer serves every call made
-    on the device's current stream (calls on concurrent streams must not share
-    it)."""
+    """Scratch buffers, one per (device, kind, stream), grown on demand.  The
+    kernels carry no state in them between calls, so one buffer serves every
+    call made on one stream in turn; calls on another stream get their own,
+    so concurrent streams never share one."""
 
-    key = (device, kind)
+    key = (device, kind, torch.cuda.current_stream(device).cuda_stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), device=device, dtype=torch.uint8)
@@ -142,11 +142,20 @@ def pq_scores(lut: torch.Tensor, codes: torch.Tensor, n_keys: int, rank: int,
 
 
 def mask_args(mask: torch.Tensor | None, q_len: int, n_keys: int):
-    """(tensor, mask type, token stride) for an HF attention mask [..., Q, >=N]."""
+    """(tensor, mask type, token stride) for an HF attention mask [..., Q, >=N].
+
+    The kernels take one [Q, N] mask for every head and sequence, so a mask
+    whose leading dims (batch, heads) hold more than one slice must repeat
+    the same slice; a mask that differs per head or per sequence raises
+    ValueError rather than being cut to its first slice."""
 
     if mask is None:
         return None, 0, 0
-    m = mask.reshape(-1, *mask.shape[-2:])[0][:q_len, :n_keys]
+    lead = mask.reshape(-1, *mask.shape[-2:])[:, :q_len, :n_keys]
+    if lead.shape[0] > 1 and not torch.equal(lead[1:], lead[:1].expand_as(lead[1:])):
+        raise ValueError(f"attention mask {tuple(mask.shape)} differs across its leading (batch / head) dims; the "
+                         f"kernels take one mask for every sequence and head")
+    m = lead[0]
     if m.dtype not in _lib.MASK_TYPES:
         m = m.float()
     if m.stride(-1) != 1:
@@ -328,6 +337,8 @@ class ScanDecodePlan:
     def __init__(self, device, n_seq: int, heads: int, q_len: int, head_dim: int, rank: int, subspaces: int,
                  codewords: int, shortlist: int, budget: int):
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.shape = (n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget)
         items = n_seq * heads * q_len
         f32, i32 = torch.float32, torch.int32
@@ -343,6 +354,44 @@ class ScanDecodePlan:
         self._lib = lib()
         self._ws, self._ws_keys = None, -1  # summon workspace, sized for caches of up to _ws_keys keys
         self._vws, self._vws_kv = None, -1  # verify workspace (independent of the cache length)
+        self._checked_weights = set()  # (data_ptr, version, dtype, shape, strides) of weights that passed
+
+    def _check_weights(self, q_proj, scale, codebooks) -> None:
+        """fp32, contiguous, on the plan's device and of the plan's shape; the
+        result is kept per weight storage (one entry per layer that shares the
+        plan), so a decode loop pays it once per layer."""
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.shape, t.stride()) for t in (q_proj, scale, codebooks))
+        if key in self._checked_weights:
+            return
+        _, heads, _, head_dim, rank, subspaces, codewords, _, _ = self.shape
+        want = {"q_proj": (q_proj, (heads, head_dim, rank)), "scale": (scale, (heads,)),
+                "codebooks": (codebooks, (heads, subspaces, codewords, rank // subspaces))}
+        for name, (t, shape) in want.items():
+            if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shape or t.device != self.device:
+                raise ValueError(f"ScanDecodePlan: {name} must be contiguous fp32 {shape} on {self.device}, got "
+                                 f"{t.dtype} {tuple(t.shape)} strides {t.stride()} on {t.device}")
+        if len(self._checked_weights) >= 1024:
+            self._checked_weights.clear()
+        self._checked_weights.add(key)
+
+    def _check_catalog(self, codes, k_low, n_keys: int) -> None:
+        _, heads, _, _, rank, subspaces, _, _, _ = self.shape
+        _check_catalog("codes", codes, heads, subspaces)
+        _check_catalog("k_low", k_low, heads, rank)
+        if k_low.dtype != torch.float32:
+            raise ValueError(f"ScanDecodePlan: k_low must be fp32, got {k_low.dtype}")
+        if codes.dtype not in (torch.uint8, torch.int16, torch.int32, torch.int64):
+            raise ValueError(f"ScanDecodePlan: codes must be an integer tensor, got {codes.dtype}")
+        if codes.shape[1] < n_keys or k_low.shape[1] < n_keys or codes.device != self.device or \
+                k_low.device != self.device:
+            raise ValueError(f"ScanDecodePlan: a catalog of {codes.shape[1]} / {k_low.shape[1]} rows on "
+                             f"{codes.device} / {k_low.device} for {n_keys} keys on {self.device}")
+
+    def _check_query(self, q) -> None:
+        n_seq, heads, q_len, head_dim = self.shape[:4]
+        if tuple(q.shape) != (n_seq, heads, q_len, head_dim) or q.device != self.device:
+            raise ValueError(f"ScanDecodePlan: query {tuple(q.shape)} on {q.device}, planned "
+                             f"{(n_seq, heads, q_len, head_dim)} on {self.device}")
 
     def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,
             mask=None):
@@ -355,6 +404,9 @@ class ScanDecodePlan:
         sequence, sva_lookup_select; otherwise sva_query_lut and sva_summon_select)."""
         n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
         q = _as_query(q)
+        self._check_query(q)
+        self._check_weights(q_proj, scale, codebooks)
+        self._check_catalog(codes, k_low, n_keys)
         L = self._lib
         stream = torch.cuda.current_stream(self.device).cuda_stream
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
@@ -393,6 +445,15 @@ class ScanDecodePlan:
         """Exact verifier over the budget lists of the last summon()."""
         n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
         q = _as_query(q)
+        self._check_query(q)
+        if keys.dim() != 3 or keys.shape[1] < n_keys or keys.shape[2] != head_dim or keys.stride(-1) != 1 or \
+                heads % keys.shape[0] != 0 or keys.device != self.device:
+            raise ValueError(f"ScanDecodePlan: keys must be [G, >={n_keys}, {head_dim}] with contiguous rows on "
+                             f"{self.device}, got {tuple(keys.shape)} strides {keys.stride()} on {keys.device}")
+        if values.shape != keys.shape or values.stride() != keys.stride() or values.dtype != keys.dtype or \
+                values.device != keys.device:
+            raise ValueError(f"ScanDecodePlan: values {tuple(values.shape)} {values.dtype} strides {values.stride()} "
+                             f"must match keys {tuple(keys.shape)} {keys.dtype} strides {keys.stride()}")
         L = self._lib
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if out is None:

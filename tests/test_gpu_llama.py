@@ -241,3 +241,62 @@ def test_query_chunks_equal_one_pass(device, attn, batch):
         assert err < 1e-5, f"chunked logits differ by {err}"
     for key in ("queries", "avg_summoned", "avg_verified"):
         assert sa[key] == sb[key], key
+
+
+def _decode_layer(device, heads=4, kv_heads=2, head_dim=64):
+    model = make_tiny_model(device, hidden=heads * head_dim, heads=heads, kv_heads=kv_heads, seed=3)
+    bundle = make_tiny_bundle(heads=heads, head_dim=head_dim, rank=64, subspaces=2, codewords=16, shortlist=12,
+                              budget=6)
+    return model, bundle
+
+
+def test_padded_batch_decode_raises(device):
+    # A left-padded batch gives each sequence its own mask row at every decode
+    # step; the packed launch takes one mask, so it refuses rather than
+    # applying sequence 0's row to all.  Equal rows decode as each sequence
+    # alone.
+    heads, kv_heads, head_dim, n = 4, 2, 64, 40
+    model, bundle = _decode_layer(device, heads, kv_heads, head_dim)
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(2, heads, 1, head_dim, generator=g).to(device)
+    k = torch.randn(2, kv_heads, n, head_dim, generator=g).to(device)
+    v = torch.randn(2, kv_heads, n, head_dim, generator=g).to(device)
+    fmin = torch.finfo(torch.float32).min
+    with torch.no_grad(), patch_llama_attention(model, bundle, summon_mode="scan") as handle:
+        attn = model.model.layers[0].self_attn
+        padded = torch.zeros(2, 1, 1, n, device=device)
+        padded[1, :, :, :5] = fmin
+        with pytest.raises(ValueError, match="same attention mask"):
+            attn.sva_attention(q, k, v, padded)
+        shared = torch.zeros(2, 1, 1, n, device=device)
+        shared[:, :, :, :5] = fmin
+        handle.reset_catalogs()
+        both = attn.sva_attention(q, k, v, shared)
+        for b in range(2):
+            handle.reset_catalogs()
+            alone = attn.sva_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1], shared[b:b + 1])
+            err = (both[b] - alone[0]).abs().max().item() / alone.abs().max().item()
+            assert err < 1e-5, f"sequence {b}: {err}"
+
+
+def test_per_head_mask(device):
+    # a mask with a head dim: equal heads act as one mask, differing heads raise
+    heads, kv_heads, head_dim, n = 4, 2, 64, 40
+    model, bundle = _decode_layer(device, heads, kv_heads, head_dim)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, heads, 1, head_dim, generator=g).to(device)
+    k = torch.randn(1, kv_heads, n, head_dim, generator=g).to(device)
+    v = torch.randn(1, kv_heads, n, head_dim, generator=g).to(device)
+    fmin = torch.finfo(torch.float32).min
+    one = torch.zeros(1, 1, 1, n, device=device)
+    one[..., 7:19] = fmin
+    with torch.no_grad(), patch_llama_attention(model, bundle, summon_mode="scan") as handle:
+        attn = model.model.layers[0].self_attn
+        ref = attn.sva_attention(q, k, v, one)
+        handle.reset_catalogs()
+        got = attn.sva_attention(q, k, v, one.expand(1, heads, 1, n).contiguous())
+        assert torch.equal(ref, got)
+        differ = one.expand(1, heads, 1, n).clone()
+        differ[0, 2, 0, 30] = fmin
+        with pytest.raises(ValueError, match="leading"):
+            attn.sva_attention(q, k, v, differ)

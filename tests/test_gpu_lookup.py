@@ -144,3 +144,72 @@ def test_sampled_floor_leaves_a_full_shortlist(L, B):
         assert bool((above >= L).all()), f"floor overshoots: {above.tolist()} keys at or above it, L={L}"
         assert bool((above <= 4 * max(2 * L, 4096)).all()), f"floor far too low: {above.tolist()}"
         _assert_same(fused, _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B))
+
+
+def test_decode_plan_rejects_bad_inputs():
+    """The plan hands raw pointers to the kernels, so it checks dtypes, shapes and strides first."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C, L, B = 8192, 4, 64, 256, 64
+    q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=5)
+    keys = torch.randn(3, N, 64, device=device).to(torch.bfloat16)
+    values = torch.randn(3, N, 64, device=device).to(torch.bfloat16)
+    plan = kernels.ScanDecodePlan(device, 1, 9, 1, 64, 64, S, C, L, B)
+    good = plan.run(q, q_proj, scale, cb, codes, k_low, keys, values, N, 0.125).clone()
+    with pytest.raises(ValueError, match="q_proj"):
+        plan.summon(q, q_proj.double(), scale, cb, codes, k_low, N)
+    with pytest.raises(ValueError, match="codebooks"):
+        plan.summon(q, q_proj, scale, cb.transpose(2, 3), codes, k_low, N)
+    with pytest.raises(ValueError, match="k_low"):
+        plan.summon(q, q_proj, scale, cb, codes, k_low.half(), N)
+    with pytest.raises(ValueError, match="catalog"):
+        plan.summon(q, q_proj, scale, cb, codes, k_low, N + 1)
+    with pytest.raises(ValueError, match="query"):
+        plan.summon(q[:, :3], q_proj, scale, cb, codes, k_low, N)
+    plan.summon(q, q_proj, scale, cb, codes, k_low, N)
+    strided = torch.empty(3, N, 128, device=device, dtype=torch.bfloat16)[:, :, :64]
+    strided.copy_(values)
+    with pytest.raises(ValueError, match="values"):
+        plan.verify(q, keys, strided, N, 0.125)
+    assert torch.equal(plan.verify(q, keys, values, N, 0.125), good)
+
+
+def test_decode_plan_graph_replays_equal_eager():
+    """The q=1 lookup (sva_lookup_select + sva_verify through the plan's static buffers) captured in one HIP
+    graph for two layers: every replay, with eager lookups on the same plan between replays, gives the eager
+    outputs bit for bit."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C, L, B = 1 << 18, 4, 64, 2048, 512
+    layers = []
+    for seed in (31, 32):
+        q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=seed)
+        g = torch.Generator(device=device).manual_seed(seed + 100)
+        keys = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+        values = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+        layers.append((q, q_proj, scale, cb, codes, k_low, keys, values))
+    plan = kernels.ScanDecodePlan(device, 1, 9, 1, 64, 64, S, C, L, B)
+    eager = [plan.run(*lay, N, 0.125).clone() for lay in layers]
+    outs = [torch.empty_like(e) for e in eager]
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for lay, o in zip(layers, outs):
+            plan.run(*lay, N, 0.125, out=o)
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for lay, o in zip(layers, outs):
+            plan.run(*lay, N, 0.125, out=o)
+    for rep in range(3):
+        between = plan.run(*layers[rep % 2], N, 0.125).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(between, eager[rep % 2])
+        for o in outs:
+            o.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), f"replay {rep}, layer {i}"
