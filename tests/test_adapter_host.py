@@ -74,3 +74,27 @@ def test_unwrapped_layer_is_rejected():
     model = _model()
     with pytest.raises(TypeError, match="not wrapped"):
         adapter.collect_adapter_state(model, [0])
+
+
+def test_bundle_validation(tmp_path):
+    model = _model()
+    made = adapter.wrap_socket_layers_with_adapters(model, [2], rank=8, scale=1.0)
+    assert made == [model.model.layers[2].self_attn]
+    adapter.save_adapter_bundle(tmp_path, model, [2], {})
+    _, state = adapter.load_adapter_bundle(tmp_path)
+    other = _model()
+    adapter.wrap_socket_layers_with_adapters(other, [2], rank=4, scale=1.0)
+    with pytest.raises(ValueError, match="down.weight"):
+        adapter.load_adapter_weights(other, [2], state)  # rank 8 stored, rank 4 expected
+    with pytest.raises(KeyError, match="layers.2.up.weight"):
+        adapter.load_adapter_weights(model, [2], {"layers.2.down.weight": state["layers.2.down.weight"]})
+    cfg = json.loads((tmp_path / "adapter_config.json").read_text())
+    cfg["format"] = "something_else"
+    (tmp_path / "adapter_config.json").write_text(json.dumps(cfg))
+    with pytest.raises(ValueError, match="format"):
+        adapter.load_adapter_bundle(tmp_path)
+    # a bare state dict (no "state_dict" wrapper) is accepted too
+    cfg["format"] = adapter.ADAPTER_FORMAT
+    (tmp_path / "adapter_config.json").write_text(json.dumps(cfg))
+    torch.save(state, tmp_path / "adapter_weights.pt")
+    assert sorted(adapter.load_adapter_bundle(tmp_path)[1]) == sorted(state)
