@@ -376,6 +376,18 @@ int sva_centroid_update(const float *x, int64_t x_head_stride, int64_t n_rows, i
                         const float *centroids, float *next_centroids, void *stream);
 
 /*
+ * Attention-weighted key weights of the codebook refresh: weights[h, n] =
+ * 1 + boost added once per valid top-k hit of key n in head h (indices
+ * clamped into [0, n_keys)), each addition rounded in turn, as index_add_
+ * gives.  Replaces topk_key_weights,
+ * experiments/sva_codebook_refresh_benchmark.py:136-153.
+ *   top_idx [H, per_head] int64, top_valid [H, per_head] bool (uint8)
+ *   weights [H, n_keys] fp32 (written; also the hit counter between passes)
+ */
+int sva_key_weights(const int64_t *top_idx, const uint8_t *top_valid, int64_t H, int64_t per_head, int64_t n_keys,
+                    float boost, float *weights, void *stream);
+
+/*
  * Unique refill selection over arbitrary rows of candidates
  * (SVALlamaAttention._top_unique_candidates, sva/llama.py:83-116): per row,
  * the best min(W, max(budget, refill_factor * budget)) entries by masked

@@ -38,6 +38,17 @@ Pinning (what checks each function; see tests/test_oracle.py):
       bit-exact against the reference's update step run by torch-CPU
       (index_add_, bincount, division) on the same labels, plain and weighted;
       empty cells keep their centroid.
+  topk_key_weights
+      closed form (a key with c hits weighs the c-fold rounded sum
+      1 + boost + ... + boost) and torch-CPU's index_add_ on the same hits,
+      invalid and out-of-range entries included.
+  topk_targets
+      brute force per row (sort of the allowed keys), causal counts
+      (valid entries = min(k, position + 1)), every valid key at or before
+      its query's position.
+  query_positions
+      torch.linspace(...).long().unique() on the CPU for a sweep of lengths,
+      sample counts and start rows.
   golden fixtures (tests/golden/) written from the reference's own functions.
 """
 
@@ -614,6 +625,64 @@ def kmeans_fit(k_low, subspaces: int, iterations: int, initial, weights=None) ->
                 labels = assign_to_centroids(x, cent[h, s])
                 cent[h, s] = kmeans_update(x, labels, cent[h, s], w)
     return cent
+
+
+def topk_key_weights(top_idx, top_valid, seq_len: int, boost: float) -> np.ndarray:
+    """experiments/sva_codebook_refresh_benchmark.py:136-153: weights [H,
+    seq_len] fp32 = 1, plus `boost` added (rounded to fp32 each time) once per
+    valid top-k hit of the key in that head, indices clamped into
+    [0, seq_len).  top_idx / top_valid [H, ...]."""
+
+    top_idx = np.asarray(top_idx, np.int64)
+    top_valid = np.asarray(top_valid, bool)
+    heads = top_idx.shape[0]
+    w = np.ones((heads, seq_len), F32)
+    for h in range(heads):
+        hits = np.clip(top_idx[h][top_valid[h]], 0, seq_len - 1)
+        if hits.size:
+            np.add.at(w[h], hits, F32(boost))  # unbuffered: one rounded add per hit, in order
+    return w
+
+
+def topk_targets(scores, query_positions, topk: int):
+    """experiments/sva_rotation_diagnostic.py:86-116: per (head, sampled
+    query) the top-k keys of the causally masked scores (keys after the
+    query's position set to the fp32 minimum), and valid[rank] = rank <=
+    position (a query at position p has p + 1 keys).  scores [H, Qs, N];
+    returns (idx [H, Qs, k] int64, valid [H, Qs, k] bool), ties by the lower
+    key (torch.topk leaves them unspecified)."""
+
+    scores = _f32(scores)
+    pos = np.asarray(query_positions, np.int64)
+    n = scores.shape[-1]
+    allowed = np.arange(n)[None, None, :] <= pos[None, :, None]
+    masked = np.where(allowed, scores, FMIN)
+    k = min(topk, n)
+    keys = np.broadcast_to(np.arange(n), masked.shape)
+    order = np.lexsort((keys, -masked.astype(np.float64)), axis=-1)[..., :k]
+    valid = np.broadcast_to(np.arange(k)[None, None, :] <= pos[None, :, None], order.shape)
+    return order.astype(np.int64), valid.copy()
+
+
+def query_positions(seq_len: int, samples: int, min_pos: int) -> np.ndarray:
+    """The calibration query rows of experiments/export_refreshed_sva_artifact.py:98-104:
+    round toward zero of linspace(start, seq_len - 1, min(samples, seq_len))
+    in fp32, start = clamp(min_pos, 0, seq_len - 1), then unique."""
+
+    start = max(0, min(min_pos, seq_len - 1))
+    steps = min(samples, seq_len)
+    if steps == 1:
+        pts = np.array([start], np.float64)
+    else:
+        # torch.linspace on the CPU in fp32: start + i * step for the first
+        # half, end - (steps - 1 - i) * step after, each one fused
+        # multiply-add (the exact product in fp64, one rounding to fp32)
+        step = np.float64(F32((seq_len - 1 - start) / (steps - 1)))
+        i = np.arange(steps, dtype=np.float64)
+        half = steps // 2
+        pts = np.where(i < half, (start + i * step).astype(F32),
+                       ((seq_len - 1) - (steps - 1 - i) * step).astype(F32))
+    return np.unique(np.trunc(pts).astype(np.int64))
 
 
 def set_threads(n: int) -> None:

@@ -59,6 +59,7 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
                                              ctypes.c_double, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _P, _P,
                                              _P, _SZ, _P]),
     "sva_centroid_update": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "sva_key_weights": (_I, [_P, _P, _I64, _I64, _I64, _F, _P, _P]),
     "sva_residual_adapter": (_I, [_P, _I, _I64, _P, _I, _I64, _P, _P, _F, _I64, _I64, _I64, _P, _I, _I64, _P]),
     "sva_top_unique_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64]),
     "sva_top_unique": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
