@@ -1,0 +1,172 @@
+"""The model-shaped workloads at their real sizes, bounded so each runs in
+seconds on one GPU:
+
+* the SmolLM2-135M-shape decoder layer (hidden 576, 9 q / 3 KV heads,
+  head_dim 64, RoPE theta 1e5, bf16) with an 8192-token prefill through the
+  scan path at shortlist 2048 / budget 512: the tokens either side of every
+  query-chunk boundary (the prefill splits the prompt into chunks of 3584
+  tokens) against the oracle's scan attention, and the property that a
+  shortlist and budget covering every key give exact causal attention;
+* the late-layer socket on the 30-layer model: batch 8, a 32768-token
+  prefill, SVA with a residual adapter in layers 26-29 at 8192 / 2048: the
+  packed batch's decode output of a socket layer equals each sequence
+  decoded on its own, and sampled heads equal the oracle's scan attention.
+
+The oracle runs on the captured inputs of the patched layer (its q, K, V and
+the layer's own catalog rows), in float64 after the verifier; outputs are
+bf16, so the tolerance is bf16's (rel 1e-2)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from transformers import LlamaConfig, LlamaForCausalLM
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+HEADS, KV_HEADS, HEAD_DIM, RANK, SUB, CW = 9, 3, 64, 64, 2, 256
+
+
+def _smollm2(device, layers, vocab=49152, context=8192, seed=0):
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=576, intermediate_size=1536, num_hidden_layers=layers,
+                      num_attention_heads=HEADS, num_key_value_heads=KV_HEADS, max_position_embeddings=context + 64,
+                      rope_theta=100000.0, tie_word_embeddings=True, attn_implementation="sdpa")
+    return LlamaForCausalLM(cfg).to(device=device, dtype=torch.bfloat16).eval()
+
+
+def _bundle(layers, shortlist, budget, layer_count=None, seed=1):
+    from sva import SVAArtifactBundle, SVALayerArtifacts
+
+    g = torch.Generator().manual_seed(seed)
+    arts = {i: SVALayerArtifacts(q_proj=torch.randn(HEADS, HEAD_DIM, RANK, generator=g) / 8.0,
+                                 k_proj=torch.randn(HEADS, HEAD_DIM, RANK, generator=g) / 8.0,
+                                 logit_scale=torch.zeros(HEADS),
+                                 coarse_codebooks=torch.randn(HEADS, SUB, CW, RANK // SUB, generator=g),
+                                 train_loss=0.0, hard_loss=0.0) for i in layers}
+    manifest = {"schema_version": 1, "artifact_type": "summon_verify_attention", "rank_dim": RANK,
+                "coarse_subspaces": SUB, "coarse_codewords": CW, "default_shortlist": shortlist,
+                "default_budget": budget, "layer_count": layer_count or len(layers), "layers": list(layers)}
+    return SVAArtifactBundle(manifest=manifest, layers=arts)
+
+
+def _capture(attn, store):
+    """Record (q, k, v, mask, out) of every sva_attention call of one layer."""
+
+    inner = attn.sva_attention
+
+    def wrapped(query, key, value, attention_mask):
+        out = inner(query, key, value, attention_mask)
+        store.append((query.detach().clone(), key.detach().clone(), value.detach().clone(), attention_mask,
+                      out.detach().clone()))
+        return out
+
+    attn.sva_attention = wrapped
+    return inner
+
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def _oracle_scan(attn, q, keys, values, k_len, shortlist, budget, mask=None):
+    """oracle.scan_attention on one sequence: q [H, Q, D], keys / values [G, N, D] (torch, any dtype)."""
+
+    qf = q.float().cpu().numpy()
+    ql = oracle.query_low(qf, attn.sva_q_proj.cpu().numpy(), attn.sva_scale.cpu().numpy())
+    k_low = attn._k_low[:, :k_len].cpu().numpy()
+    codes = attn._codes[:, :k_len].cpu().numpy()
+    return oracle.scan_attention(qf, keys.float().cpu().numpy(), values.float().cpu().numpy(), ql, k_low,
+                                 attn.sva_coarse_codebooks.cpu().numpy(), codes, shortlist, budget, attn.scaling,
+                                 attention_mask=mask)
+
+
+def test_smollm2_layer_prefill_8192(device):
+    from sva import patch_llama_attention
+
+    n = 8192
+    model = _smollm2(device, layers=1, vocab=512)
+    prompt = torch.randint(0, 512, (1, n), generator=torch.Generator().manual_seed(2)).to(device)
+    store = []
+    with torch.no_grad(), patch_llama_attention(model, _bundle([0], 2048, 512), shortlist=2048, budget=512,
+                                                summon_mode="scan"):
+        attn = model.model.layers[0].self_attn
+        _capture(attn, store)
+        model(input_ids=prompt, use_cache=False)
+        q, k, v, mask, out = store[0]
+        assert mask is None and tuple(q.shape) == (1, HEADS, n, HEAD_DIM)
+        # the prefill's query chunks: 3584 tokens (512 MiB of shortlist per launch)
+        chunk = max(128, ((512 << 20) // (HEADS * 2048 * 8)) // 128 * 128)
+        assert chunk == 3584
+        tokens = sorted({0, chunk - 1, chunk, 2 * chunk - 1, 2 * chunk, n - 1})
+        allowed = np.where(np.arange(n)[None, :] <= np.asarray(tokens)[:, None], 0.0, -np.inf).astype(np.float32)
+        print(f"prefill 8192: oracle on tokens {tokens}", flush=True)
+        ref = _oracle_scan(attn, q[0][:, tokens], k[0], v[0], n, 2048, 512, mask=allowed)
+        got = out[0][:, tokens].float().cpu().numpy()
+        for h in range(HEADS):
+            err = _rel(got[h], ref["out"][h])
+            assert err <= 1e-2, f"head {h}: rel err {err}"
+
+    # shortlist = budget = every key: exact causal attention
+    store.clear()
+    with torch.no_grad(), patch_llama_attention(model, _bundle([0], n, n), shortlist=n, budget=n,
+                                                summon_mode="scan"):
+        attn = model.model.layers[0].self_attn
+        _capture(attn, store)
+        model(input_ids=prompt, use_cache=False)
+        q, k, v, _, out = store[0]
+        kf = k[0].float().repeat_interleave(HEADS // KV_HEADS, dim=0)
+        vf = v[0].float().repeat_interleave(HEADS // KV_HEADS, dim=0)
+        dense = torch.nn.functional.scaled_dot_product_attention(q[0].float(), kf, vf, is_causal=True,
+                                                                 scale=attn.scaling)
+        err = ((out[0].float() - dense).abs().max() / dense.abs().max()).item()
+        assert err <= 1e-2, f"full budget differs from dense attention by {err}"
+
+
+def test_late_socket_batch8_32k(device):
+    from sva import patch_llama_attention
+    from sva_amd import adapter as sva_adapter
+
+    batch, n, socket, layer = 8, 32768, [26, 27, 28, 29], 27
+    model = _smollm2(device, layers=30, context=n + 8)
+    prompt = torch.randint(0, 49152, (batch, n), generator=torch.Generator().manual_seed(3)).to(device)
+    store = []
+    with torch.no_grad():
+        past = None
+        for s0 in range(0, n, 2048):  # full-attention prefill, as the socket serves it
+            out = model(input_ids=prompt[:, s0:s0 + 2048], past_key_values=past, use_cache=True)
+            past = out.past_key_values
+        print("socket: prefill done", flush=True)
+        tok = out.logits[:, -1:].argmax(-1)
+        with patch_llama_attention(model, _bundle(socket, 8192, 2048, layer_count=30), shortlist=8192, budget=2048,
+                                   summon_mode="scan", layers=socket) as handle:
+            adapters = sva_adapter.wrap_socket_layers_with_adapters(model, socket, rank=16, scale=1.0)
+            for a in adapters:
+                torch.nn.init.normal_(a.up.weight, mean=0.0, std=0.02)
+                a.down.weight.requires_grad_(False)
+                a.up.weight.requires_grad_(False)
+            attn = model.model.layers[layer].self_attn.sva_attn
+            _capture(attn, store)
+            out = model(input_ids=tok, past_key_values=past, use_cache=True)
+            assert torch.isfinite(out.logits.float()).all()
+            q, k, v, mask, got = store[0]
+            assert tuple(q.shape) == (batch, HEADS, 1, HEAD_DIM) and k.shape[2] == n + 1
+            for b in (0, 5):
+                attn.reset_catalog()
+                alone = attn.sva_attention(q[b:b + 1], k[b:b + 1], v[b:b + 1],
+                                           None if mask is None else mask[b:b + 1])
+                err = ((alone[0].float() - got[b].float()).abs().max() / alone.float().abs().max()).item()
+                assert err <= 1e-5, f"sequence {b}: packed batch differs from decoding it alone by {err}"
+                if b == 0:
+                    print("socket: oracle on sequence 0", flush=True)
+                    ref = _oracle_scan(attn, q[0], k[0], v[0], n + 1, 8192, 2048)
+                    for h in (0, 4, 8):
+                        e = _rel(got[0, h, 0].float().cpu().numpy(), ref["out"][h, 0])
+                        assert e <= 1e-2, f"head {h}: rel err {e} against the oracle"
+            summary = handle.stats.summary()
+            assert summary["queries"] > 0
+            for i in socket:
+                model.model.layers[i].self_attn = model.model.layers[i].self_attn.sva_attn

@@ -274,3 +274,70 @@ def test_ragged_static_decode_matches_oracle(device, amin, amid, budget):
         assert float(stats[items, 0].sum()) == ref["stats"]["summoned"], f"sequence {b}"
         assert float(fin_count[items].sum()) == ref["stats"]["verified"], f"sequence {b}"
         assert float(stats[items, 1].sum()) == ref["stats"]["refill_pool"], f"sequence {b}"
+
+
+def test_config5_packed_batch_static_decode(device):
+    # The ragged continuous-batch workload at its real shape: 32 sequences
+    # with cache lengths log-uniform in [4096, 131072] packed contiguously,
+    # bf16 K/V, 2x256 codes, static postings over all but a tail of up to 63
+    # rows, 512/128 (static mode verifies min(128, 512, N) keys), cells 8.
+    # The longest, the shortest and two other sequences are checked against
+    # the oracle; every sequence is checked for counts and for sorted,
+    # unique, in-range budget ids.
+    from sva_amd import inverted, kernels
+
+    H, G, D, R, S, C, budget, cells = 9, 3, 64, 64, 2, 256, 128, 8
+    rng = np.random.default_rng(55)
+    lens = np.exp(rng.uniform(np.log(4096), np.log(131072), 32)).astype(np.int64)
+    tails = rng.integers(0, 64, 32).astype(np.int64)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
+    rows = int(lens.sum())
+    print(f"config5: {rows} rows, lengths {lens.min()}..{lens.max()}", flush=True)
+    g = torch.Generator(device=device).manual_seed(56)
+    keys = torch.randn(G, rows, D, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(G, rows, D, device=device, generator=g).to(torch.bfloat16)
+    q = rng.standard_normal((32, H, 1, D)).astype(np.float32)
+    q_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    k_proj = (rng.standard_normal((H, D, R)) / 8).astype(np.float32)
+    scale = np.exp(0.1 * rng.standard_normal(H)).astype(np.float32)
+    cb = rng.standard_normal((H, S, C, R // S)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    k_low = torch.empty(H, rows, R, device=device)
+    codes = torch.empty(H, rows, S, device=device, dtype=torch.uint8)
+    kernels.write_encode(keys, t(k_proj), t(cb), k_low, codes)
+    plens = lens - tails
+    post = inverted.build_postings_ragged(codes, t(offs), t(plens), int(plens.max()), C)
+    qb = t(q).to(torch.bfloat16)
+    out, fin_idx, fin_count, stats = inverted.ragged_static_decode(
+        qb, t(q_proj), t(scale), t(cb), keys, values, k_low, codes, t(offs), t(lens), post, int(tails.max()), budget,
+        cells, D ** -0.5, return_selection=True)
+    out = out[:, :, 0].float().cpu().numpy()
+    fin_idx, fin_count, stats = fin_idx.cpu().numpy(), fin_count.cpu().numpy(), stats.cpu().numpy()
+    for b in range(32):
+        for h in range(H):
+            it = b * H + h
+            ids = fin_idx[it, : fin_count[it]]
+            assert 0 < fin_count[it] <= budget, f"sequence {b} head {h}: {fin_count[it]} verified"
+            assert np.all(np.diff(ids) > 0) and ids[0] >= 0 and ids[-1] < lens[b], f"sequence {b} head {h}"
+    order = np.argsort(lens)
+    sample = sorted({int(order[-1]), int(order[0]), int(order[10]), int(order[21])})
+    qf = qb.float().cpu().numpy()
+    for b in sample:
+        r0, n, pl = int(offs[b]), int(lens[b]), int(plens[b])
+        print(f"config5: oracle on sequence {b} ({n} keys, tail {n - pl})", flush=True)
+        kb = keys[:, r0:r0 + n].float().cpu().numpy()
+        vb = values[:, r0:r0 + n].float().cpu().numpy()
+        kl = k_low[:, r0:r0 + n].cpu().numpy()
+        cd = codes[:, r0:r0 + pl].cpu().numpy()
+        ql = oracle.query_low(qf[b], q_proj, scale)
+        ref = oracle.static_decode(qf[b], kb, vb, ql, kl, cb, oracle.rebuild_postings(cd, C), pl, budget, cells,
+                                   D ** -0.5)
+        for h in range(H):
+            it = b * H + h
+            want = np.sort(ref["heads"][h]["final"])
+            np.testing.assert_array_equal(fin_idx[it, : fin_count[it]], want, err_msg=f"sequence {b} head {h}")
+            err = np.abs(out[b, h] - ref["out"][h]).max() / max(np.abs(ref["out"][h]).max(), 1e-30)
+            assert err <= 1e-2, f"sequence {b} head {h}: rel err {err}"  # bf16 output
+        items = slice(b * H, (b + 1) * H)
+        assert float(stats[items, 0].sum()) == ref["stats"]["summoned"], f"sequence {b}"
+        assert float(fin_count[items].sum()) == ref["stats"]["verified"], f"sequence {b}"
