@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--cpu-repeats", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the decode lookups")
+    ap.add_argument("--no-decode", action="store_true", help="skip the model decode tok/s figure of the decode line")
+    ap.add_argument("--cpu-decode-steps", type=int, default=8, help="timed CPU decode steps of the model decode")
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
@@ -484,14 +486,93 @@ def socket_suite(args):
     }), flush=True)
 
 
-def model_suite(args):
+def cpu_decode_baseline(torch, model, past, tok, steps: int, warmups: int = 3):
+    """Greedy decode of the same model on the host's cores: the weights in
+    fp32 on the CPU (torch), every layer's SVA attention through the oracle's
+    C decode (OpenMP over heads) over the GPU run's cache and catalog copied
+    to host arrays with room for the new rows; each new key row is projected
+    and coded by the oracle.  `warmups` untimed steps, then `steps` timed."""
+
+    import numpy as np
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    import oracle
+
+    config = model.config
+    cpu = type(model)(config).float().eval()
+    # the patched attention holds the original module too: its weights are the same tensors
+    cpu.load_state_dict({k: v.detach().float().cpu() for k, v in model.state_dict().items() if ".original." not in k})
+    layers = model.model.layers
+    n0 = past.get_seq_length()
+    cap = n0 + steps + warmups
+    heads, kv_heads = config.num_attention_heads, config.num_key_value_heads
+    group = heads // kv_heads
+    state = []
+    for i, layer in enumerate(layers):
+        attn = layer.self_attn
+        k, v = past.layers[i].keys, past.layers[i].values   # [1, G, n0, D]
+        K = np.zeros((kv_heads, cap, attn.head_dim), np.float32)
+        V = np.zeros_like(K)
+        K[:, :n0] = k[0].float().cpu().numpy()
+        V[:, :n0] = v[0].float().cpu().numpy()
+        k_low = np.zeros((heads, cap, attn.sva_q_proj.shape[2]), np.float32)
+        codes = np.zeros((heads, cap, attn.sva_coarse_codebooks.shape[1]), np.uint8)
+        k_low[:, :n0] = attn._k_low[:, :n0].cpu().numpy()
+        codes[:, :n0] = attn._codes[:, :n0].cpu().numpy()
+        state.append({"K": K, "V": V, "k_low": k_low, "codes": codes,
+                      "q_proj": attn.sva_q_proj.cpu().numpy(), "k_proj": attn.sva_k_proj.cpu().numpy(),
+                      "scale": attn.sva_scale.cpu().numpy(), "cb": attn.sva_coarse_codebooks.cpu().numpy(),
+                      "scaling": attn.scaling})
+    token = tok.cpu()
+    n = n0
+    times, cpu_s = [], 0.0
+    with torch.no_grad():
+        for step in range(warmups + steps):
+            c0, t0 = time.process_time(), time.perf_counter()
+            h = cpu.model.embed_tokens(token)
+            pos = torch.tensor([[n]])
+            for i, layer in enumerate(cpu.model.layers):
+                st = state[i]
+                x = layer.input_layernorm(h)
+                a = layer.self_attn
+                q = a.q_proj(x).view(1, 1, heads, a.head_dim).transpose(1, 2)
+                k = a.k_proj(x).view(1, 1, kv_heads, a.head_dim).transpose(1, 2)
+                v = a.v_proj(x).view(1, 1, kv_heads, a.head_dim).transpose(1, 2)
+                cos, sin = cpu.model.rotary_emb(x, pos)
+                q, k = apply_rotary_pos_emb(q, k, cos, sin)
+                st["K"][:, n] = k[0, :, 0].numpy()
+                st["V"][:, n] = v[0, :, 0].numpy()
+                for hh in range(heads):
+                    row = oracle.project(st["K"][hh // group, n][None], st["k_proj"][hh])
+                    st["k_low"][hh, n] = row[0]
+                    st["codes"][hh, n] = oracle.encode_product_keys(row[None], st["cb"][hh][None])[0, 0]
+                qh = q[0, :, 0].numpy()
+                q_low = oracle.query_low(qh[:, None], st["q_proj"], st["scale"])[:, 0]
+                _, _, o, _ = oracle.decode(qh, q_low, st["K"], st["V"], st["k_low"], st["cb"], st["codes"], 2048, 512,
+                                           st["scaling"], n_keys=n + 1)
+                h = h + a.o_proj(torch.from_numpy(o.astype(np.float32)).reshape(1, 1, -1))
+                h = h + layer.mlp(layer.post_attention_layernorm(h))
+            token = cpu.lm_head(cpu.model.norm(h))[:, -1:].argmax(-1)
+            n += 1
+            if step >= warmups:
+                times.append(time.perf_counter() - t0)
+                cpu_s += time.process_time() - c0
+    wall = sum(times)
+    return {"value": round(steps / wall, 2), "unit": "tok/s", "cores": max(1, round(cpu_s / wall)), "kind": "port",
+            "sample": f"{steps} greedy decode steps (after {warmups} warmups) of the same model from the GPU run's "
+                      f"{n0}-token cache: torch fp32 weights, oracle/sva_oracle.c SVA attention per layer",
+            "busy_threads": round(cpu_s / wall, 2), "ms_per_token": round(1e3 * wall / steps, 1)}
+
+
+def model_decode(args, with_cpu: bool):
     """Decode tokens/s of a SmolLM2-135M-architecture decoder (random init,
     bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64, RoPE theta 1e5)
     with every attention layer SVA-patched (synthetic 2x256 artifacts, rank
     64, shortlist 2048 / budget 512): a prefill of uniform random token ids,
     8 untimed greedy decode steps, then `--decode-steps` timed greedy steps
     (torch.cuda.synchronize on both sides).  The same model unpatched (torch
-    sdpa attention, bf16) is timed the same way for reference."""
+    sdpa attention, bf16) is timed the same way for reference, and the CPU
+    leg decodes from the patched run's cache."""
 
     import torch
     from transformers import LlamaConfig, LlamaForCausalLM
@@ -520,7 +601,7 @@ def model_suite(args):
     bundle = SVAArtifactBundle(manifest=manifest, layers=arts)
     prompt = torch.randint(0, config.vocab_size, (1, args.prefill), generator=g).to(device)
 
-    def run(patched):
+    def run():
         with torch.no_grad():
             model(input_ids=prompt[:, :256], use_cache=True)  # untimed: first-call setup of every kernel
             torch.cuda.synchronize()
@@ -539,27 +620,46 @@ def model_suite(args):
                 out = model(input_ids=tok, past_key_values=past, use_cache=True)
                 past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
             torch.cuda.synchronize()
-            return prefill_s, time.perf_counter() - t0
+            return prefill_s, time.perf_counter() - t0, past, tok
 
-    dense_prefill, dense_decode = run(False)
+    dense_prefill, dense_decode, past, _ = run()
+    del past
+    cpu = None
     with patch_llama_attention(model, bundle, shortlist=2048, budget=512, summon_mode="scan") as handle:
-        sva_prefill, sva_decode = run(True)
+        sva_prefill, sva_decode, past, tok = run()
         summary = handle.stats.summary()
+        if with_cpu:
+            cpu = cpu_decode_baseline(torch, model, past, tok, args.cpu_decode_steps)
+    del past
     tok_s = args.decode_steps / sva_decode
-    print(json.dumps({
-        "metric": "decode tok/s", "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1,
-        "steps": args.decode_steps, "warmup": 8, "ms_per_step": round(1e3 * sva_decode / args.decode_steps, 3),
-        "higher_is_better": True, "scaling": "weak",
-        # the reference's own figure for this workload: 124.21 ms/token (8.05 tok/s) on an H100
-        "vs_baseline": round(tok_s / REF_MODEL_TOK_S, 3), "baseline": f"{REF_MODEL_TOK_S} tok/s, reference on H100",
-        "dtype": "bf16 (fp32 scores)",
-        "data": "synthetic (random-init weights, uniform random prompt, synthetic 2x256 artifacts)",
-        "config": {"workload": "SmolLM2-135M-shape decoder, 30 SVA layers, batch 1", "prefill": args.prefill,
+    return {
+        "tok_s": round(tok_s, 1), "ms_per_token": round(1e3 * sva_decode / args.decode_steps, 3),
+        "steps": args.decode_steps, "warmup": 8,
+        "vs_reference": round(tok_s / REF_MODEL_TOK_S, 3), "reference": f"{REF_MODEL_TOK_S} tok/s on H100",
+        "config": {"workload": "SmolLM2-135M-shape decoder, 30 SVA layers, batch 1, bf16", "prefill": args.prefill,
                    "shortlist": 2048, "budget": 512, "summon_mode": "scan", "intermediate_size": 1536},
         "prefill_s": round(sva_prefill, 3), "prefill_tok_s": round(args.prefill / sva_prefill, 1),
         "dense_attention": {"tok_s": round(args.decode_steps / dense_decode, 1), "prefill_s": round(dense_prefill, 3),
                             "prefill_tok_s": round(args.prefill / dense_prefill, 1), "attention": "torch sdpa, bf16"},
         "sva_stats": {k: round(v, 3) for k, v in summary.items() if isinstance(v, float) and v == v},
+        "cpu_baseline": cpu,
+    }
+
+
+def model_suite(args):
+    """The model decode as its own JSON line (metric decode tok/s)."""
+
+    res = model_decode(args, with_cpu=not args.no_cpu_baseline)
+    print(json.dumps({
+        "metric": "decode tok/s", "value": res["tok_s"], "unit": "tok/s", "n_gpus": 1,
+        "steps": res["steps"], "warmup": res["warmup"], "ms_per_step": res["ms_per_token"],
+        "higher_is_better": True, "scaling": "weak",
+        # the reference's own figure for this workload: 124.21 ms/token (8.05 tok/s) on an H100
+        "vs_baseline": res["vs_reference"], "baseline": res["reference"],
+        "dtype": "bf16 (fp32 scores)",
+        "data": "synthetic (random-init weights, uniform random prompt, synthetic 2x256 artifacts)",
+        "config": res["config"], "prefill_s": res["prefill_s"], "prefill_tok_s": res["prefill_tok_s"],
+        "dense_attention": res["dense_attention"], "sva_stats": res["sva_stats"], "cpu_baseline": res["cpu_baseline"],
     }), flush=True)
 
 
@@ -765,6 +865,10 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, layers[0], shortlist, budget, args.cpu_repeats)
+    if not args.no_decode:
+        del layers, plan, outs
+        torch.cuda.empty_cache()
+        result["decode"] = model_decode(args, with_cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
 
 

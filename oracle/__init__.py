@@ -100,7 +100,7 @@ def lib() -> ctypes.CDLL:
         _lib.sva_oracle_topk.argtypes = [c_p, c_p, c_p, i64, i64, c_p]
         _lib.sva_oracle_verify.argtypes = [c_p, c_p, c_p, i64, c_p, i64, ctypes.c_double, c_p]
         _lib.sva_oracle_decode.restype = ctypes.c_int
-        _lib.sva_oracle_decode.argtypes = [i64] * 7 + [c_p] * 7 + [ctypes.c_int, i64, i64, ctypes.c_double, c_p, c_p, c_p]
+        _lib.sva_oracle_decode.argtypes = [i64] * 8 + [c_p] * 7 + [ctypes.c_int, i64, i64, ctypes.c_double, c_p, c_p, c_p]
     return _lib
 
 
@@ -544,9 +544,13 @@ def inverted_decode(query, keys, values, q_low, k_low, codebooks, codes, budget:
     return {"heads": results, "out": out, "stats": stats}
 
 
-def decode(q, q_low, keys, values, k_low, codebooks, codes, shortlist: int, budget: int, scaling: float):
+def decode(q, q_low, keys, values, k_low, codebooks, codes, shortlist: int, budget: int, scaling: float,
+           n_keys: int | None = None):
     """Whole q=1 decode lookup in C (OpenMP over heads): returns
-    (shortlist [H, L], final [H, B], out [H, D] float64, threads used)."""
+    (shortlist [H, L], final [H, B], out [H, D] float64, threads used).
+    keys / values [G, cap, D], k_low [H, cap, R], codes [H, cap, S]: the
+    first n_keys (default cap) rows are the cache, so a growing cache held
+    in preallocated arrays is read in place."""
 
     q = _f32(q)
     q_low = _f32(q_low)
@@ -556,14 +560,17 @@ def decode(q, q_low, keys, values, k_low, codebooks, codes, shortlist: int, budg
     codebooks = _f32(codebooks)
     codes = np.ascontiguousarray(codes)
     h_count, head_dim = q.shape
-    g_count, n, _ = keys.shape
+    g_count, cap, _ = keys.shape
+    n = cap if n_keys is None else int(n_keys)
+    if not (0 < n <= cap and values.shape == keys.shape and k_low.shape[1] == cap and codes.shape[1] == cap):
+        raise ValueError("decode: cache arrays must share their row capacity, and 0 < n_keys <= capacity")
     rank_dim = q_low.shape[1]
     s_count, c_count = codebooks.shape[1], codebooks.shape[2]
     sl = np.full((h_count, shortlist), -1, np.int64)
     fin = np.full((h_count, budget), -1, np.int64)
     out = np.zeros((h_count, head_dim), np.float64)
     threads = lib().sva_oracle_decode(
-        h_count, g_count, n, head_dim, rank_dim, s_count, c_count,
+        h_count, g_count, n, cap, head_dim, rank_dim, s_count, c_count,
         _ptr(q), _ptr(q_low), _ptr(keys), _ptr(values), _ptr(k_low), _ptr(codebooks), _ptr(codes),
         codes.dtype.itemsize, shortlist, budget, float(scaling), _ptr(sl), _ptr(fin), _ptr(out),
     )

@@ -292,11 +292,13 @@ ORACLE_API void sva_oracle_verify(const float *q, const float *K, const float *V
  * (the synthetic cached-decode workload of
  * experiments/sva_million_cached_decode_benchmark.py:224-249, GQA-indexed):
  *   lut -> PQ scores -> top-L -> rank scores -> top-B -> verifier.
- * Inputs: q [H][D], q_low [H][R], K/V [G][N][D] float, k_low [H][N][R],
- * codebooks [H][S][C][sub], codes [H][N][S] (code_bytes wide).
+ * Inputs: q [H][D], q_low [H][R], K/V [G][cap][D] float, k_low [H][cap][R],
+ * codebooks [H][S][C][sub], codes [H][cap][S] (code_bytes wide); the first N
+ * of the cap rows of every head are the cache.
  * Outputs: shortlist [H][L], final [H][B] (key indices in selection order),
  * out [H][D].  Heads run in parallel (OpenMP).  Returns the thread count. */
-ORACLE_API int sva_oracle_decode(int64_t H, int64_t G, int64_t N, int64_t D, int64_t R, int64_t S, int64_t C,
+ORACLE_API int sva_oracle_decode(int64_t H, int64_t G, int64_t N, int64_t cap, int64_t D, int64_t R, int64_t S,
+                                 int64_t C,
                                  const float *q, const float *q_low, const float *K, const float *V,
                                  const float *k_low, const float *codebooks, const void *codes, int code_bytes,
                                  int64_t L, int64_t B, double scaling, int64_t *shortlist, int64_t *final_idx,
@@ -323,7 +325,7 @@ ORACLE_API int sva_oracle_decode(int64_t H, int64_t G, int64_t N, int64_t D, int
             float *lut = (float *)malloc(sizeof(float) * (size_t)(S * C));
             float *sc = (float *)malloc(sizeof(float) * (size_t)N);
             sva_oracle_lut(q_low + h * R, S, C, sub, codebooks + h * S * C * sub, lut);
-            const char *hc = (const char *)codes + (size_t)h * (size_t)N * (size_t)S * (size_t)code_bytes;
+            const char *hc = (const char *)codes + (size_t)h * (size_t)cap * (size_t)S * (size_t)code_bytes;
             for (int64_t i = 0; i < N; ++i) {
                 float acc = 0.0f;
                 for (int64_t s = 0; s < S; ++s) acc = acc + lut[s * C + load_code(hc, code_bytes, i * S + s)];
@@ -332,11 +334,11 @@ ORACLE_API int sva_oracle_decode(int64_t H, int64_t G, int64_t N, int64_t D, int
             int64_t *sl = shortlist + h * L;
             const int64_t got = sva_oracle_topk(sc, NULL, NULL, N, Lh, sl);
             float *rank = (float *)malloc(sizeof(float) * (size_t)(got > 0 ? got : 1));
-            sva_oracle_rank_scores(k_low + (size_t)h * (size_t)N * (size_t)R, R, sl, got, q_low + h * R, sqrt_r, rank);
+            sva_oracle_rank_scores(k_low + (size_t)h * (size_t)cap * (size_t)R, R, sl, got, q_low + h * R, sqrt_r, rank);
             int64_t *pos = (int64_t *)malloc(sizeof(int64_t) * (size_t)(Bh > 0 ? Bh : 1));
             const int64_t kept = sva_oracle_topk(rank, NULL, sl, got, Bh, pos);
             for (int64_t b = 0; b < kept; ++b) final_idx[h * B + b] = sl[pos[b]];
-            sva_oracle_verify(q + h * D, K + (size_t)g * (size_t)N * (size_t)D, V + (size_t)g * (size_t)N * (size_t)D, D,
+            sva_oracle_verify(q + h * D, K + (size_t)g * (size_t)cap * (size_t)D, V + (size_t)g * (size_t)cap * (size_t)D, D,
                               final_idx + h * B, kept, scaling, out + h * D);
             free(pos);
             free(rank);

@@ -278,6 +278,14 @@ def test_decode_in_c_matches_numpy_restatement():
         assert set(fin[h].tolist()) == set(final.tolist())
         ref = oracle.verify(q[h], keys[h // 3], values[h // 3], np.sort(final), D ** -0.5)
         np.testing.assert_allclose(out[h], ref, rtol=1e-12, atol=1e-12)
+    # the same cache held in arrays with spare rows (a growing cache read in place)
+    cap = N + 37
+    pad = lambda a: np.concatenate([a, np.full((a.shape[0], cap - N) + a.shape[2:], 7, a.dtype)], axis=1)  # noqa
+    sl2, fin2, out2, _ = oracle.decode(q, q_low, pad(keys), pad(values), pad(k_low), cb, pad(codes), 1024, 256,
+                                       D ** -0.5, n_keys=N)
+    np.testing.assert_array_equal(sl2, sl)
+    np.testing.assert_array_equal(fin2, fin)
+    np.testing.assert_array_equal(out2, out)
 
 
 def test_residual_adapter_matches_torch_module():
