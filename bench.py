@@ -156,10 +156,9 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
     }
 
 
-# kernels of one decode lookup, by entry point
-SUMMON_KERNELS = ("wide_scan_kernel", "wide_finish_kernel")
-PATH_KERNELS = ("query_lut_kernel",) + SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel",
-                                                         "verify_combine_kernel")
+# kernels of one decode step (sva_lookup_verify), by entry point
+SUMMON_KERNELS = ("query_decode_kernel", "query_lut_kernel", "wide_scan_kernel", "wide_finish_kernel")
+PATH_KERNELS = SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel", "verify_combine_kernel")
 PROFILE_STEM = "lookup_select_decode_1m_{layout}"
 REF_US_PER_QUERY = 1024.0  # the reference's published decode lookup, 1M keys, 4x64, 2048/512 (H100)
 # the reference's published lookups at 1M keys, q=1, by (layout, shortlist, budget) (H100, PyTorch bf16)
@@ -235,8 +234,9 @@ def write_profiles(args):
         if k in SUMMON_KERNELS:
             summon_bytes += b
         lines.append(f"| {k} | {fk:.1f} | {wk:.1f} | {b:,.0f} |")
-    entry = "sva_lookup_select" if args.layout == "4x64" else "sva_summon_select"
-    lines += ["", f"{entry} (the wide_* kernels): {summon_bytes:,.0f} bytes per lookup.", ""]
+    entry = "sva_lookup_verify"
+    lines += ["", f"{entry} (query table, scan, finish with the verifier): {summon_bytes:,.0f} bytes per decode "
+                  f"step.", ""]
     (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
     (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
         {"entry_point": entry, "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
@@ -738,12 +738,10 @@ def main():
     layers = [Layer(torch, device, n, subspaces, codewords, args.seed + n * 13 + 101 + 7919 * i)
               for i in range(args.layers)]
     strategy = _lib.lib().sva_summon_strategy(1, heads, 1, n, 64, subspaces, codewords, args.shortlist, 0, 0)
-    # sva_lookup_select computes the query side inside the scan for 4x64 codes on the wide path
-    fused = strategy == 1 and (subspaces, codewords) == (4, 64)
     shortlist = min(args.shortlist, n)
     budget = min(args.budget, shortlist)
     scaling = 64 ** -0.5
-    stages = ("lookup", "verify")
+    stages = ("lookup_verify",)
 
     plan = kernels.ScanDecodePlan(device, 1, heads, 1, 64, 64, subspaces, codewords, shortlist, budget)
     outs = [torch.empty(1, heads, 1, 64, device=device, dtype=torch.bfloat16) for _ in layers]
@@ -754,13 +752,12 @@ def main():
                  layer.values, n, scaling, out=outs[i % len(layers)])
 
     def step_staged(i, ev):
-        # the same calls with an event between the lookup (query side, shortlist, budget) and the verifier
+        # the same call bracketed by events on its stream
         layer = layers[i % len(layers)]
         ev[0].record()
-        plan.summon(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, layer.k_low, n)
+        plan.run(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, layer.k_low, layer.keys,
+                 layer.values, n, scaling, out=outs[i % len(layers)])
         ev[1].record()
-        plan.verify(layer.q, layer.keys, layer.values, n, scaling, out=outs[i % len(layers)])
-        ev[2].record()
 
     if args.calibrate_copy:
         src = torch.empty(args.calibrate_copy << 20, dtype=torch.uint8, device=device).fill_(1)
@@ -803,8 +800,8 @@ def main():
     graph_res = None if args.no_graph else graph_replay(torch, np, args, layers, plan, outs, step)
 
     bytes_ = algorithmic_bytes(n, heads, subspaces, codewords, shortlist, budget)
-    summon_us = per_stage_us["lookup"]
-    achieved = bytes_["summon"] / (summon_us * 1e-6) / 1e9
+    step_us_avg = per_stage_us["lookup_verify"]
+    achieved = bytes_["total"] / (step_us_avg * 1e-6) / 1e9
     traffic = None
     pmc = ROOT / "profiles" / (PROFILE_STEM.format(layout=args.layout) + "_traffic.json")
     if pmc.exists() and n == 1_048_576:
@@ -843,23 +840,18 @@ def main():
         "graph": graph_res,
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": ("sva_lookup_select: wide_scan (query side fused) + wide_finish"
-                       if strategy == 1 and fused else
-                       "sva_query_lut + sva_summon_select: query_lut + wide_scan + wide_finish" if strategy == 1
-                       else "sva_query_lut + sva_summon_select: query_lut + summon_item + budget_select"),
+            "kernel": ("sva_lookup_verify: query_decode_kernel + wide_scan_kernel + wide_finish_kernel (verifier "
+                       "inside the finish)" if strategy == 1 else
+                       "sva_lookup_verify: query_lut_kernel + summon_item + budget_select + verify_part + "
+                       "verify_combine"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "algorithmic_bytes": bytes_["summon"],
-        },
-        "verify_roofline": {
-            "achieved": round(bytes_["verify"] / (per_stage_us["verify"] * 1e-6) / 1e9, 1),
-            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(bytes_["verify"] / (per_stage_us["verify"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes": bytes_["verify"],
+            "algorithmic_bytes": bytes_["total"],
+            "algorithmic_split": {k: bytes_[k] for k in ("scan", "lut", "query", "rescore", "verify")},
         },
         "cpu_baseline": None,
     }

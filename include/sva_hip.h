@@ -146,11 +146,7 @@ int sva_summon_select(const float *lut, const float *score_range, const float *q
  * score_range [H, 4]) followed by sva_summon_select (shortlist and budget)
  * on the same arguments.  Replaces sva/llama.py:211 (q_low), sva/ops.py:50-71
  * (table and scan) and sva/llama.py:276-302 (shortlist, rescore, budget) for
- * q_len = 1.  With D = R = 64, 4x64 uint8 codes,
- * every key allowed (mask NULL, SVA_MASK_NONE or SVA_MASK_BOOL) and a cache
- * of 32K..1G keys, the scan's workgroups compute the query side themselves
- * (bit-identical tables and floors, no separate table launch); other shapes
- * run the two calls.  workspace: sva_summon_workspace_bytes(1, H, 1, n_keys, L).
+ * q_len = 1.  workspace: sva_summon_workspace_bytes(1, H, 1, n_keys, L).
  */
 int sva_lookup_select(const void *q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R, int64_t S,
                       int64_t C, const float *q_proj, const float *scale, const float *codebooks, const void *codes,
@@ -159,6 +155,30 @@ int sva_lookup_select(const void *q, int q_dtype, int64_t q_head_stride, int64_t
                       float *q_low, float *lut, float *score_range, int32_t *sl_idx, float *sl_rank,
                       int32_t *sl_count, int64_t B, int32_t *fin_idx, int32_t *fin_count, void *workspace,
                       size_t workspace_bytes, void *stream);
+
+/*
+ * The whole decode step of one token of one sequence: sva_lookup_select
+ * followed by sva_verify on its budget lists, writing the attention output
+ * out [H, D] (head stride out_head_stride) besides every lookup output.
+ * Replaces sva/llama.py:211-317 for q_len = 1 (q_low, scan, shortlist,
+ * rescore, budget, exact verifier).  On the wide path (sva_summon_strategy
+ * 1) with D = 64 or 128 the verifier runs inside the finish kernel, each
+ * item's workgroup over the list it has just selected; otherwise
+ * sva_verify runs after the lookup with verify_workspace
+ * (sva_verify_workspace_bytes(1, H, G, 1, D, B)).  K / V rows of KV head g
+ * at g * kv_head_stride + n * kv_row_stride elements; query head h reads KV
+ * head h / (H / G).
+ */
+int sva_lookup_verify(const void *q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R, int64_t S,
+                      int64_t C, const float *q_proj, const float *scale, const float *codebooks, const void *codes,
+                      int code_type, int64_t code_head_stride, const float *k_low, int64_t k_low_head_stride,
+                      int64_t n_keys, int64_t L, const void *mask, int mask_type, int64_t mask_tok_stride,
+                      float *q_low, float *lut, float *score_range, int32_t *sl_idx, float *sl_rank,
+                      int32_t *sl_count, int64_t B, int32_t *fin_idx, int32_t *fin_count, void *workspace,
+                      size_t workspace_bytes, const void *keys, const void *values, int kv_dtype,
+                      int64_t kv_head_stride, int64_t kv_row_stride, int64_t G, float scaling, void *out,
+                      int out_dtype, int64_t out_head_stride, void *verify_workspace, size_t verify_workspace_bytes,
+                      void *stream);
 
 /*
  * Which summon strategy a call with these shapes takes (16-byte aligned

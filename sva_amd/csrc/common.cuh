@@ -50,6 +50,30 @@ SVA_DEV float load_elem(const void* p, int64_t i, int dtype) {
   return __half2float(((const __half*)p)[i]);
 }
 
+// Four consecutive elements of a K/V row as floats.
+SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[4]) {
+  if (vec) {
+    if (dtype == F32) {
+      const float4 x = *reinterpret_cast<const float4*>((const float*)base + e);
+      v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
+      return;
+    }
+    const uint2 x = *reinterpret_cast<const uint2*>((const uint16_t*)base + e);
+    if (dtype == BF16) {
+      v[0] = __uint_as_float(x.x << 16), v[1] = __uint_as_float(x.x & 0xFFFF0000u);
+      v[2] = __uint_as_float(x.y << 16), v[3] = __uint_as_float(x.y & 0xFFFF0000u);
+    } else {
+      v[0] = __half2float(__ushort_as_half((unsigned short)(x.x & 0xFFFFu)));
+      v[1] = __half2float(__ushort_as_half((unsigned short)(x.x >> 16)));
+      v[2] = __half2float(__ushort_as_half((unsigned short)(x.y & 0xFFFFu)));
+      v[3] = __half2float(__ushort_as_half((unsigned short)(x.y >> 16)));
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = load_elem(base, e + k, dtype);
+}
+
 SVA_DEV void store_elem(void* p, int64_t i, int dtype, float v) {
   if (dtype == F32) {
     ((float*)p)[i] = v;

@@ -75,13 +75,36 @@ struct SummonParams {
   int32_t* fin_count;
 };
 
+// The exact verifier run by the wide path's finish kernel right after each
+// item's budget list (one sequence, one query token: item = query head h):
+// q of head h at q + h * q_hs; K / V rows of KV head g = h / (H / G) at
+// g * kv_hs + n * kv_rs; out of head h at out + h * o_hs.  D is 64 or 128.
+struct FusedVerify {
+  const void* q;
+  int q_dtype;
+  int64_t q_hs;
+  const void* keys;
+  const void* values;
+  int kv_dtype;
+  int64_t kv_hs, kv_rs;
+  bool kv_vec;  // rows start 8-byte (half types) / 16-byte (fp32) aligned
+  int G, D;
+  float scaling;
+  void* out;  // nullptr: no fused verifier
+  int out_dtype;
+  int64_t o_hs;
+};
+
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream);
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const FusedVerify* fv = nullptr);
+// Whether summon_wide_path can run `fv` in its finish kernel for these sizes.
+bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);
 
 inline int next_pow2_host(int x) {

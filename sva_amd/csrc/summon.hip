@@ -466,7 +466,9 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 const int64_t* seq_offsets, const int64_t* seq_lens, int64_t n_seq, int64_t H, int64_t Q,
                 int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
-                int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream) {
+                int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
+                const sva::FusedVerify* fv = nullptr, bool* fused = nullptr) {
+  if (fused != nullptr) *fused = false;
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
   SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "%s: bad sizes", fn);
@@ -516,7 +518,10 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
     return rc;
   }
   if (sva::summon_wide_eligible(p, items)) {
-    return sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream);
+    const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
+    const int rc = sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr);
+    if (rc == SVA_OK && fused != nullptr) *fused = with_fv;
+    return rc;
   }
   if (sva::summon_regs_eligible(p)) return sva::summon_regs_path(p, items, (hipStream_t)stream);
   int rc = sva::summon_item_path(p, items, (hipStream_t)stream);
@@ -575,4 +580,53 @@ extern "C" int sva_lookup_select(const void* q, int q_dtype, int64_t q_head_stri
   return sva_summon_select(lut, score_range, q_low, codes, code_type, code_head_stride, k_low, k_low_head_stride,
                            nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride, sl_idx,
                            sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
+                                 int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
+                                 const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
+                                 int64_t k_low_head_stride, int64_t n_keys, int64_t L, const void* mask, int mask_type,
+                                 int64_t mask_tok_stride, float* q_low, float* lut, float* score_range,
+                                 int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx,
+                                 int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
+                                 const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                                 int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
+                                 void* verify_workspace, size_t verify_workspace_bytes, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(q && q_proj && scale && codebooks && codes && q_low && lut && score_range,
+              "sva_lookup_verify: null pointer");
+  SVA_REQUIRE(fin_idx && fin_count && keys && values && out, "sva_lookup_verify: null pointer");
+  SVA_REQUIRE(B > 0 && B <= 8192, "sva_lookup_verify: budget %lld out of range (1..8192)", (long long)B);
+  SVA_REQUIRE(H > 0 && G > 0 && H % G == 0 && n_keys > 0 && L > 0, "sva_lookup_verify: bad sizes");
+  SVA_REQUIRE(q_dtype >= 0 && q_dtype <= 2 && kv_dtype >= 0 && kv_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
+              "sva_lookup_verify: bad dtype");
+  int rc = sva_query_lut(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
+                         code_type, code_head_stride, n_keys, L, q_low, lut, score_range, stream);
+  if (rc != SVA_OK) return rc;
+  sva::FusedVerify fv{};
+  fv.q = q;
+  fv.q_dtype = q_dtype;
+  fv.q_hs = q_head_stride;
+  fv.keys = keys;
+  fv.values = values;
+  fv.kv_dtype = kv_dtype;
+  fv.kv_hs = kv_head_stride;
+  fv.kv_rs = kv_row_stride;
+  const uintptr_t kv_align = kv_dtype == 0 ? 15u : 7u;
+  fv.kv_vec = (((uintptr_t)keys | (uintptr_t)values) & kv_align) == 0 && kv_head_stride % 4 == 0 &&
+              kv_row_stride % 4 == 0;
+  fv.G = (int)G;
+  fv.D = (int)D;
+  fv.scaling = scaling;
+  fv.out = out;
+  fv.out_dtype = out_dtype;
+  fv.o_hs = out_head_stride;
+  bool fused = false;
+  rc = summon_impl("sva_lookup_verify", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
+                   k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride,
+                   sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused);
+  if (rc != SVA_OK || fused) return rc;
+  return sva_verify(q, q_dtype, 0, q_head_stride, 0, keys, values, kv_dtype, kv_head_stride, kv_row_stride, nullptr,
+                    nullptr, n_keys, fin_idx, fin_count, 1, H, G, 1, D, B, scaling, out, out_dtype, 0, out_head_stride,
+                    0, verify_workspace, verify_workspace_bytes, stream);
 }

@@ -63,6 +63,7 @@ struct WideArgs {
   uint64_t* wg_cand;   // [items, W, WG_CAP] a workgroup's candidates in key order (when they fit)
   float* wg_rank;      // [items, W, WG_CAP] their rank scores
   int W;             // scan workgroups per item
+  FusedVerify fv;    // fv.out != nullptr: the finish kernel also runs the verifier
 };
 
 SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
@@ -718,7 +719,7 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32
 // The fast finish of an item; false (uniformly, before any output or LDS
 // write) when its conditions do not hold.
 SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32_t* rkb, uint32_t* wcnt,
-                         uint32_t* scratch, const TopLds& tl) {
+                         uint32_t* scratch, const TopLds& tl, int32_t* kidl) {
 #pragma clang fp contract(off)
   const SummonParams& p = a.p;
   const int W = a.W;
@@ -907,7 +908,10 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
       }
       if (fin != nullptr && sb) {
         const uint32_t o = (w >> 16) + lanes_below(mb);
-        if (o < (uint32_t)beff) fin[o] = (int32_t)key;
+        if (o < (uint32_t)beff) {
+          fin[o] = (int32_t)key;
+          if (kidl != nullptr) kidl[o] = (int32_t)key;
+        }
       }
     }
   }
@@ -930,9 +934,8 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
 //           over every key of the item, ranks computed here.
 // The last two are slower and give the same result.  The shortlist's rank
 // composites go to LDS in shortlist order for the budget.
-__global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
+SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_t* kidl) {
 #pragma clang fp contract(off)
-  extern __shared__ __align__(16) unsigned char lds[];
   uint64_t* cl = (uint64_t*)lds;                                   // staged candidates [LDS_CAND]
   uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // overlays, once staging is done
   uint32_t* sl = (uint32_t*)(lds + kFinSl);
@@ -947,8 +950,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   uint32_t* loff = (uint32_t*)(lds + kFinLoff);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
-  const int item = blockIdx.x;
-  if (finish_fast(a, item, lds, rkb, wcnt, scratch, tl)) return;
+  if (finish_fast(a, item, lds, rkb, wcnt, scratch, tl, kidl)) return kidl != nullptr;
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int nsub = a.W * NW;
@@ -993,7 +995,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
   }
-  if (leff == 0) return;
+  if (leff == 0) return false;
   // bounds of every candidate composite: sums in [floor, upper bound of any sum]
   const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
   const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
@@ -1007,7 +1009,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
       gather_lists<3>(cand, nsub, e3);
       finish_dense<3>(a, item, nsub, leff, beff, M, c_lo, c_hi, e3, lds, lcnt, loff, rkb, wcnt, scratch, tl);
     }
-    return;
+    return false;
   }
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;  // rank keys this thread emitted
   auto emit = [&](uint32_t o, uint64_t x, float rank) {
@@ -1185,20 +1187,261 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
       vand &= e2[i];
     }
   }
-  if (p.B <= 0) return;
+  if (p.B <= 0) return false;
   const bool rb = dense && rkb[0] <= rkb[1];
   const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
   finish_budget<NPB>(p, item, leff, beff, e2, rb ? b_hi : vor, rb ? b_lo : vand, rb, tl, wcnt, scratch);
+  return false;
+}
+
+// The verifier of a decode item (query head h = item), run by its finish
+// workgroup over the budget list it has just selected.  Every wave takes 32
+// (head_dim 128: 16) consecutive list entries per round and requests all their K and V rows at
+// once (a K row by 8 lanes, 16-byte pieces; a V row by the wave, one
+// dimension per lane), so a row costs two cache-line requests; scores are
+// fp32 dot(K[n], q) * scaling (fused multiply-adds over each lane's piece,
+// then the 8 lanes pairwise), and the wave keeps a running maximum m, exp-sum
+// z and exp-weighted V sum (rescaled when m grows).  The waves' partials are
+// merged at the end: out = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) z_w,
+// 0 for an empty list.  The list is read from LDS when the finish left it
+// there, else from the budget output (visible after the caller's barrier).
+constexpr int VLPR = 8;    // lanes per K row
+constexpr int VEPW = 32;   // list entries per wave per round (D = 64; half that for D = 128)
+constexpr size_t kVerifyKid = kFastEnd;  // LDS of the list: int32[B]
+constexpr int kVerifyKidCap = (int)((kFinStage - kFastEnd) / sizeof(int32_t));
+
+// n consecutive K / V elements of a compile-time dtype as floats (n a multiple of 4).
+template <int KV, int NE>
+SVA_DEV void kv_load(const void* base, int64_t e, bool vec, float (&v)[NE]) {
+  if (vec && KV == F32) {
+#pragma unroll
+    for (int c = 0; c < NE / 4; ++c) {
+      const float4 x = reinterpret_cast<const float4*>((const float*)base + e)[c];
+      v[4 * c] = x.x, v[4 * c + 1] = x.y, v[4 * c + 2] = x.z, v[4 * c + 3] = x.w;
+    }
+  } else if (vec) {
+#pragma unroll
+    for (int c = 0; c < NE / 4; ++c) {
+      const uint2 x = reinterpret_cast<const uint2*>((const uint16_t*)base + e)[c];
+      const uint32_t w[4] = {x.x & 0xFFFFu, x.x >> 16, x.y & 0xFFFFu, x.y >> 16};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        v[4 * c + k] = KV == BF16 ? __uint_as_float(w[k] << 16) : __half2float(__ushort_as_half((unsigned short)w[k]));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+      if (KV == F32) {
+        v[k] = ((const float*)base)[e + k];
+      } else {
+        const uint16_t x = ((const uint16_t*)base)[e + k];
+        v[k] = KV == BF16 ? __uint_as_float((uint32_t)x << 16) : __half2float(__ushort_as_half(x));
+      }
+    }
+  }
+}
+
+template <int KV>
+SVA_DEV float kv_one(const void* base, int64_t e) {
+  if (KV == F32) return ((const float*)base)[e];
+  const uint16_t x = ((const uint16_t*)base)[e];
+  return KV == BF16 ? __uint_as_float((uint32_t)x << 16) : __half2float(__ushort_as_half(x));
+}
+
+template <int D, int KV>
+SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool kid_in_lds, const float* qsh) {
+#pragma clang fp contract(off)
+  const SummonParams& p = a.p;
+  const FusedVerify& v = a.fv;
+  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  constexpr int EPL = D / VLPR;      // K elements per lane of a row
+  constexpr int RPI = WAVE / VLPR;   // K rows per load group
+  constexpr int EPR = VEPW * 64 / D;  // list entries per wave per round
+  constexpr int KI = EPR / RPI;      // K load groups per round
+  constexpr int DL = D / WAVE;       // V dimensions per lane
+  // 16-bit V rows at head_dim 64: a load serves two rows, lanes 0-31 the first and 32-63 the second,
+  // two dimensions per lane (needs 4-byte aligned rows); vv[2j] / vv[2j + 1] then hold the lane's two
+  // dimensions of its row of the pair
+  const bool PAIRV = KV != F32 && D == 64 && v.kv_vec;
+  int32_t* kid = (int32_t*)(lds + kVerifyKid);
+  float* part = (float*)(lds + kVerifyKid) + (kid_in_lds ? p.B : 0);  // [SNW][D + 2]: m, z, acc
+  if (!kid_in_lds) {
+    part = (float*)lds;
+    kid = (int32_t*)(part + SNW * (D + 2));
+  }
+  const int cnt = min(max(p.fin_count[item], 0), p.B);
+  const int g = item / (p.H / v.G);
+  const int64_t kvb = (int64_t)g * v.kv_hs;
+  const int sub = lane & (VLPR - 1);
+  float qv[EPL];
+#pragma unroll
+  for (int k = 0; k < EPL; ++k) qv[k] = qsh[sub * EPL + k];
+  if (!kid_in_lds) {
+    for (int j = t; j < cnt; j += SB) kid[j] = p.fin_idx[(int64_t)item * p.B + j];
+    __syncthreads();
+  }
+  float m = -INFINITY, z = 0.0f, acc[DL], acc2[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int d = 0; d < DL; ++d) acc[d] = 0.0f;
+  for (int r0 = wid * EPR; r0 < cnt; r0 += SNW * EPR) {  // uniform per wave
+    // every K and V row of the round requested before any is used
+    float kk[KI][EPL], vv[EPR][DL];
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+      const int e = r0 + k * RPI + lane / VLPR;
+      const int64_t row = kvb + (int64_t)kid[min(e, cnt - 1)] * v.kv_rs + sub * EPL;
+      kv_load<KV, EPL>(v.keys, row, v.kv_vec, kk[k]);
+    }
+    if (PAIRV) {
+      // row r0 + 2 j + (lane >= 32), dimensions 2 (lane & 31) and 2 (lane & 31) + 1
+#pragma unroll
+      for (int j = 0; j < EPR / 2; ++j) {
+        const int64_t row = kvb + (int64_t)kid[min(r0 + 2 * j + (lane >> 5), cnt - 1)] * v.kv_rs + 2 * (lane & 31);
+        const uint32_t x = *reinterpret_cast<const uint32_t*>((const uint16_t*)v.values + row);
+        vv[2 * j][0] = KV == BF16 ? __uint_as_float(x << 16) : __half2float(__ushort_as_half((unsigned short)(x & 0xFFFFu)));
+        vv[2 * j + 1][0] = KV == BF16 ? __uint_as_float(x & 0xFFFF0000u) : __half2float(__ushort_as_half((unsigned short)(x >> 16)));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < EPR; ++j) {
+        const int64_t row = kvb + (int64_t)kid[min(r0 + j, cnt - 1)] * v.kv_rs + lane;
+#pragma unroll
+        for (int d = 0; d < DL; ++d) vv[j][d] = kv_one<KV>(v.values, row + WAVE * d);
+      }
+    }
+    float sc[KI], mr = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+      float dot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) dot = __builtin_fmaf(kk[k][i], qv[i], dot);
+      dot += __shfl_xor(dot, 1, VLPR);
+      dot += __shfl_xor(dot, 2, VLPR);
+      dot += __shfl_xor(dot, 4, VLPR);
+      const int e = r0 + k * RPI + lane / VLPR;
+      sc[k] = e < cnt ? dot * v.scaling : -INFINITY;
+      mr = fmaxf(mr, sc[k]);
+    }
+    mr = wave_max(mr);
+    const float mn = fmaxf(m, mr);
+    const float f = m == -INFINITY ? 0.0f : expf(m - mn);
+    float pr[KI], zr = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+      pr[k] = sc[k] == -INFINITY ? 0.0f : expf(sc[k] - mn);
+      zr = zr + (sub == 0 ? pr[k] : 0.0f);
+    }
+    zr = wave_sum(zr);
+    z = z * f + zr;
+#pragma unroll
+    for (int d = 0; d < DL; ++d) acc[d] = acc[d] * f;
+    acc2[0] = acc2[0] * f;
+    acc2[1] = acc2[1] * f;
+    if (PAIRV) {
+      // weight of entry r0 + 2 j + (lane >= 32): a readlane per row, the half's own
+#pragma unroll
+      for (int j = 0; j < EPR / 2; ++j) {
+        const int e0 = 2 * j, e1 = 2 * j + 1;
+        const float x0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[e0 / RPI]), (e0 % RPI) * VLPR));
+        const float x1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[e1 / RPI]), (e1 % RPI) * VLPR));
+        const float x = lane < 32 ? x0 : x1;
+        acc2[0] = acc2[0] + x * vv[2 * j][0];
+        acc2[1] = acc2[1] + x * vv[2 * j + 1][0];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < EPR; ++j) {
+        // weight of entry r0 + j (0 past the list), from the lane that holds it
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[j / RPI]), (j % RPI) * VLPR));
+#pragma unroll
+        for (int d = 0; d < DL; ++d) acc[d] = acc[d] + x * vv[j][d];
+      }
+    }
+    m = mn;
+  }
+  float* mine = part + wid * (D + 2);
+  if (lane == 0) {
+    mine[0] = m;
+    mine[1] = z;
+  }
+  if (PAIRV) {
+    // the two halves hold the same dimensions for different rows: add them
+    const float s0 = acc2[0] + __shfl_xor(acc2[0], 32, WAVE);
+    const float s1 = acc2[1] + __shfl_xor(acc2[1], 32, WAVE);
+    if (lane < 32) {
+      mine[2 + 2 * lane] = s0;
+      mine[2 + 2 * lane + 1] = s1;
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < DL; ++d) mine[2 + lane + WAVE * d] = acc[d];
+  }
+  __syncthreads();
+  // wave factors e^(m_w - M) and the total exp-sum, by the first wave
+  float* fw = part + SNW * (D + 2);  // [SNW + 1]
+  if (wid == 0) {
+    const float mw = lane < SNW ? part[lane * (D + 2)] : -INFINITY;
+    const float M = wave_max(mw);
+    const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
+    const float Z = wave_sum(lane < SNW ? f * part[lane * (D + 2) + 1] : 0.0f);
+    if (lane < SNW) fw[lane] = f;
+    if (lane == 0) fw[SNW] = Z;
+  }
+  __syncthreads();
+  if (t < D) {
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < SNW; ++w) o = o + fw[w] * part[w * (D + 2) + 2 + t];
+    const float Z = fw[SNW];
+    store_elem(v.out, (int64_t)item * v.o_hs + t, v.out_dtype, (cnt > 0 && Z > 0.0f) ? o / Z : 0.0f);
+  }
+}
+
+// LDS the fused verifier needs when the list comes from the budget output.
+size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B + SNW * (size_t)(D + 2) + SNW + 1); }
+
+// Finish of an item, then (VD > 0: head_dim VD, K / V dtype VKV) its verifier.
+template <int VD, int VKV>
+__global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ float qsh[VD > 0 ? VD : 1];  // the verifier's query row, requested before the finish starts
+  const int item = blockIdx.x;
+  if (VD > 0 && (int)threadIdx.x < VD)
+    qsh[threadIdx.x] = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
+  const bool keep = VD > 0 && a.p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
+  const bool in_lds = finish_item(a, item, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
+  if (VD > 0) {
+    __syncthreads();  // the budget list (LDS or global) and the LDS the finish used
+    verify_item<(VD > 0 ? VD : 64), VKV>(a, item, lds, in_lds, qsh);
+  }
+}
+
+template <int VD, int VKV>
+int launch_finish(const WideArgs& a, int64_t items, hipStream_t stream) {
+  SVA_SET_MAX_LDS_ONCE((wide_finish_kernel<VD, VKV>), kFinLds, "hipFuncSetAttribute(wide_finish_kernel)");
+  hipLaunchKernelGGL((wide_finish_kernel<VD, VKV>), dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
+  SVA_CHECK_LAUNCH("wide_finish_kernel");
+  return SVA_OK;
+}
+
+int launch_finish_any(const WideArgs& a, int64_t items, hipStream_t stream) {
+  if (a.fv.out == nullptr) return launch_finish<0, F32>(a, items, stream);
+  const int kv = a.fv.kv_dtype;
+  if (a.fv.D == 64) {
+    if (kv == BF16) return launch_finish<64, BF16>(a, items, stream);
+    if (kv == F16) return launch_finish<64, F16>(a, items, stream);
+    return launch_finish<64, F32>(a, items, stream);
+  }
+  if (kv == BF16) return launch_finish<128, BF16>(a, items, stream);
+  if (kv == F16) return launch_finish<128, F16>(a, items, stream);
+  return launch_finish<128, F32>(a, items, stream);
 }
 
 template <int S, bool SMALLC, bool MASKED>
 int launch_wide(const WideArgs& a, int64_t items, hipStream_t stream) {
   hipLaunchKernelGGL((wide_scan_kernel<S, SMALLC, MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
   SVA_CHECK_LAUNCH("wide_scan_kernel");
-  SVA_SET_MAX_LDS_ONCE(wide_finish_kernel, kFinLds, "hipFuncSetAttribute(wide_finish_kernel)");
-  hipLaunchKernelGGL(wide_finish_kernel, dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
-  SVA_CHECK_LAUNCH("wide_finish_kernel");
-  return SVA_OK;
+  return launch_finish_any(a, items, stream);
 }
 
 template <int S>
@@ -1240,7 +1483,17 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
 }
 
-int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv) {
+  if (!summon_wide_eligible(p, items) || p.offs != nullptr || items != p.H || p.B <= 0) return false;
+  if (fv.D != 64 && fv.D != 128) return false;
+  if (fv.G <= 0 || p.H % fv.G != 0) return false;
+  if (fv.q_dtype < 0 || fv.q_dtype > 2 || fv.kv_dtype < 0 || fv.kv_dtype > 2 || fv.out_dtype < 0 || fv.out_dtype > 2)
+    return false;
+  return verify_item_lds(p.B, fv.D) <= kFinLds;
+}
+
+int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const FusedVerify* fv) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const size_t need = summon_wide_workspace_bytes(1, p.H, 1, p.N, p.L);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
@@ -1248,6 +1501,12 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   WideArgs a;
   a.p = p;
   a.W = (int)((p.N + CHUNK - 1) / CHUNK);
+  a.fv = FusedVerify{};
+  a.fv.out = nullptr;
+  if (fv != nullptr) {
+    SVA_REQUIRE(fused_verify_eligible(p, items, *fv), "summon_wide_path: the fused verifier does not fit these sizes");
+    a.fv = *fv;
+  }
   char* ws = (char*)workspace;
   a.ncand = (uint32_t*)ws;
   a.nallow = a.ncand + items * a.W * NW;

@@ -68,30 +68,6 @@ struct VerifyParams {
   int64_t o_bs, o_hs, o_ts;
 };
 
-// Four consecutive elements of a K/V row as floats.
-SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[4]) {
-  if (vec) {
-    if (dtype == F32) {
-      const float4 x = *reinterpret_cast<const float4*>((const float*)base + e);
-      v[0] = x.x, v[1] = x.y, v[2] = x.z, v[3] = x.w;
-      return;
-    }
-    const uint2 x = *reinterpret_cast<const uint2*>((const uint16_t*)base + e);
-    if (dtype == BF16) {
-      v[0] = __uint_as_float(x.x << 16), v[1] = __uint_as_float(x.x & 0xFFFF0000u);
-      v[2] = __uint_as_float(x.y << 16), v[3] = __uint_as_float(x.y & 0xFFFF0000u);
-    } else {
-      v[0] = __half2float(__ushort_as_half((unsigned short)(x.x & 0xFFFFu)));
-      v[1] = __half2float(__ushort_as_half((unsigned short)(x.x >> 16)));
-      v[2] = __half2float(__ushort_as_half((unsigned short)(x.y & 0xFFFFu)));
-      v[3] = __half2float(__ushort_as_half((unsigned short)(x.y >> 16)));
-    }
-    return;
-  }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) v[k] = load_elem(base, e + k, dtype);
-}
-
 // DT: compile-time head_dim (0: runtime p.D, a multiple of 16; -1: any
 // head_dim, elementwise).  Each of the 4 lanes of an entry holds D/4
 // consecutive dimensions of its K and V rows (every 4th one for DT = -1).

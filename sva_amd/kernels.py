@@ -395,9 +395,68 @@ class ScanDecodePlan:
 
     def run(self, q, q_proj, scale, codebooks, codes, k_low, keys, values, n_keys: int, scaling: float, out=None,
             mask=None):
-        """The whole lookup: summon() then verify(); returns the verified output."""
-        self.summon(q, q_proj, scale, codebooks, codes, k_low, n_keys, mask=mask)
-        return self.verify(q, keys, values, n_keys, scaling, out=out)
+        """The whole lookup; returns the verified output.  One token of one
+        sequence is one C-ABI call (sva_lookup_verify: on the wide path the
+        verifier runs inside the finish kernel); otherwise summon() then
+        verify()."""
+        n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
+        if n_seq != 1 or q_len != 1:
+            self.summon(q, q_proj, scale, codebooks, codes, k_low, n_keys, mask=mask)
+            return self.verify(q, keys, values, n_keys, scaling, out=out)
+        q = _as_query(q)
+        self._check_query(q)
+        self._check_weights(q_proj, scale, codebooks)
+        self._check_catalog(codes, k_low, n_keys)
+        self._check_kv(keys, values, n_keys)
+        L = self._lib
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        m, mtype, mstride = mask_args(mask, q_len, n_keys)
+        ws = self._summon_ws(n_keys)
+        vws = self._verify_ws(keys)
+        if out is None:
+            out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
+        if out.stride(-1) != 1 or tuple(out.shape) != (1, heads, 1, head_dim):
+            raise ValueError(f"ScanDecodePlan: out must be [1, {heads}, 1, {head_dim}] with contiguous rows")
+        check(L.sva_lookup_verify(q.data_ptr(), dtype_code(q), q.stride(1), heads, head_dim, rank, subspaces, codewords,
+                                  q_proj.data_ptr(), scale.data_ptr(), codebooks.data_ptr(), codes.data_ptr(),
+                                  code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), n_keys,
+                                  shortlist, ptr(m), mtype, mstride, self.q_low.data_ptr(), self.lut.data_ptr(),
+                                  self.rng.data_ptr(), self.sl_idx.data_ptr(), self.sl_rank.data_ptr(),
+                                  self.sl_count.data_ptr(), budget, self.fin_idx.data_ptr(),
+                                  self.fin_count.data_ptr(), ws.data_ptr(), ws.numel(), keys.data_ptr(),
+                                  values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1),
+                                  keys.shape[0], float(scaling), out.data_ptr(), dtype_code(out), out.stride(1),
+                                  vws.data_ptr(), vws.numel(), stream), "sva_lookup_verify")
+        return out
+
+    def _summon_ws(self, n_keys: int) -> torch.Tensor:
+        n_seq, heads, q_len, _, _, _, _, shortlist, _ = self.shape
+        if n_keys > self._ws_keys:
+            # the summon workspace grows with the key count: sized for the next
+            # multiple of 64K keys, so a decode loop re-queries it rarely
+            self._ws_keys = (n_keys + 65535) // 65536 * 65536
+            self._ws = workspace(self.device, int(self._lib.sva_summon_workspace_bytes(
+                n_seq, heads, q_len, self._ws_keys, shortlist)), "plan")
+        return self._ws
+
+    def _verify_ws(self, keys) -> torch.Tensor:
+        n_seq, heads, q_len, head_dim, _, _, _, _, budget = self.shape
+        if self._vws is None or self._vws_kv != keys.shape[0]:
+            self._vws_kv = keys.shape[0]
+            self._vws = workspace(self.device, int(self._lib.sva_verify_workspace_bytes(
+                n_seq, heads, keys.shape[0], q_len, head_dim, budget)), "verify")
+        return self._vws
+
+    def _check_kv(self, keys, values, n_keys: int) -> None:
+        _, heads, _, head_dim = self.shape[:4]
+        if keys.dim() != 3 or keys.shape[1] < n_keys or keys.shape[2] != head_dim or keys.stride(-1) != 1 or \
+                heads % keys.shape[0] != 0 or keys.device != self.device:
+            raise ValueError(f"ScanDecodePlan: keys must be [G, >={n_keys}, {head_dim}] with contiguous rows on "
+                             f"{self.device}, got {tuple(keys.shape)} strides {keys.stride()} on {keys.device}")
+        if values.shape != keys.shape or values.stride() != keys.stride() or values.dtype != keys.dtype or \
+                values.device != keys.device:
+            raise ValueError(f"ScanDecodePlan: values {tuple(values.shape)} {values.dtype} strides {values.stride()} "
+                             f"must match keys {tuple(keys.shape)} {keys.dtype} strides {keys.stride()}")
 
     def summon(self, q, q_proj, scale, codebooks, codes, k_low, n_keys: int, mask=None) -> None:
         """Query side, shortlist and budget into the plan's buffers (one C-ABI call for one token of one
@@ -410,13 +469,7 @@ class ScanDecodePlan:
         L = self._lib
         stream = torch.cuda.current_stream(self.device).cuda_stream
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
-        if n_keys > self._ws_keys:
-            # the summon workspace grows with the key count: sized for the next
-            # multiple of 64K keys, so a decode loop re-queries it rarely
-            self._ws_keys = (n_keys + 65535) // 65536 * 65536
-            self._ws = workspace(self.device, int(L.sva_summon_workspace_bytes(n_seq, heads, q_len, self._ws_keys,
-                                                                                shortlist)), "plan")
-        ws = self._ws
+        ws = self._summon_ws(n_keys)
         if n_seq == 1 and q_len == 1:
             # one token: query side and summon in one call (fused where the shapes allow)
             check(L.sva_lookup_select(q.data_ptr(), dtype_code(q), q.stride(1), heads, head_dim, rank, subspaces,
@@ -446,23 +499,12 @@ class ScanDecodePlan:
         n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = self.shape
         q = _as_query(q)
         self._check_query(q)
-        if keys.dim() != 3 or keys.shape[1] < n_keys or keys.shape[2] != head_dim or keys.stride(-1) != 1 or \
-                heads % keys.shape[0] != 0 or keys.device != self.device:
-            raise ValueError(f"ScanDecodePlan: keys must be [G, >={n_keys}, {head_dim}] with contiguous rows on "
-                             f"{self.device}, got {tuple(keys.shape)} strides {keys.stride()} on {keys.device}")
-        if values.shape != keys.shape or values.stride() != keys.stride() or values.dtype != keys.dtype or \
-                values.device != keys.device:
-            raise ValueError(f"ScanDecodePlan: values {tuple(values.shape)} {values.dtype} strides {values.stride()} "
-                             f"must match keys {tuple(keys.shape)} {keys.dtype} strides {keys.stride()}")
+        self._check_kv(keys, values, n_keys)
         L = self._lib
         stream = torch.cuda.current_stream(self.device).cuda_stream
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
-        if self._vws is None or self._vws_kv != keys.shape[0]:
-            self._vws_kv = keys.shape[0]
-            self._vws = workspace(self.device, int(L.sva_verify_workspace_bytes(n_seq, heads, keys.shape[0], q_len,
-                                                                                  head_dim, budget)), "verify")
-        vws = self._vws
+        vws = self._verify_ws(keys)
         check(L.sva_verify(q.data_ptr(), dtype_code(q), q.stride(0), q.stride(1), q.stride(2), keys.data_ptr(),
                            values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1), None, None, n_keys,
                            self.fin_idx.data_ptr(), self.fin_count.data_ptr(), n_seq, heads, keys.shape[0], q_len,

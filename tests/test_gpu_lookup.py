@@ -112,12 +112,20 @@ def test_lookup_select_decode_plan_uses_one_call():
     keys = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
     values = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
     plan = kernels.ScanDecodePlan(device, 1, 9, 1, 64, 64, S, C, L, B)
-    outs = [plan.run(q, q_proj, scale, cb, codes, k_low, keys, values, N, 0.125).clone() for _ in range(2)]
+    outs = []
+    for _ in range(2):
+        o = torch.empty(1, 9, 1, 64, device=device, dtype=torch.float32)
+        plan.run(q, q_proj, scale, cb, codes, k_low, keys, values, N, 0.125, out=o)
+        outs.append((o, plan.fin_idx.clone(), plan.fin_count.clone()))
     _, _, _, _, _, _, fin_idx, fin_count = _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B)
-    ref = kernels.verify(q, keys, values, fin_idx, fin_count, N, 0.125)
+    ref = kernels.verify(q, keys, values, fin_idx, fin_count, N, 0.125, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    for o in outs:
-        assert torch.equal(o, ref)
+    assert torch.equal(outs[0][0], outs[1][0])  # deterministic
+    for o, fi, fc in outs:
+        assert torch.equal(fc, fin_count) and torch.equal(fi, fin_idx)
+        # the verifier inside the finish kernel sums the softmax in another order than sva_verify
+        err = ((o - ref).abs().max() / ref.abs().max()).item()
+        assert err <= 1e-5, f"fused verifier differs from sva_verify by {err}"
 
 
 @pytest.mark.parametrize("L,B", [(2048, 512), (512, 128), (256, 64)])
@@ -213,3 +221,46 @@ def test_decode_plan_graph_replays_equal_eager():
         torch.cuda.synchronize()
         for i, (o, e) in enumerate(zip(outs, eager)):
             assert torch.equal(o, e), f"replay {rep}, layer {i}"
+
+
+@pytest.mark.parametrize("G,D,kv_dtype,L,B,masked", [
+    (3, 64, torch.bfloat16, 2048, 512, False),
+    (3, 64, torch.float32, 512, 128, False),
+    (9, 64, torch.float16, 8192, 2048, False),
+    (1, 128, torch.bfloat16, 1024, 256, False),
+    (3, 64, torch.bfloat16, 2048, 512, True),
+])
+def test_lookup_verify_matches_oracle(G, D, kv_dtype, L, B, masked):
+    """sva_lookup_verify (the verifier inside the finish kernel on the wide path) against the oracle's fp64
+    verifier over the budget lists the call selected: every head, fp32 output, rel 1e-5; a mask allowing only a
+    few hundred keys, and one allowing none (empty lists give zeros)."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    N, S, C, H = 40000, 4, 64, 9
+    q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=41 + G + D, D=D)
+    g = torch.Generator(device=device).manual_seed(42)
+    keys = torch.randn(G, N, D, device=device, generator=g).to(kv_dtype)
+    values = torch.randn(G, N, D, device=device, generator=g).to(kv_dtype)
+    masks = [None]
+    if masked:
+        few = torch.full((1, 1, 1, N), -1e9, device=device)
+        few[..., ::97] = 0.0
+        masks = [few, torch.full((1, 1, 1, N), -1e9, device=device)]
+    plan = kernels.ScanDecodePlan(device, 1, H, 1, D, 64, S, C, L, B)
+    scaling = D ** -0.5
+    for mask in masks:
+        out = torch.empty(1, H, 1, D, device=device, dtype=torch.float32)
+        plan.run(q, q_proj, scale, cb, codes, k_low, keys, values, N, scaling, out=out, mask=mask)
+        torch.cuda.synchronize()
+        fin_idx, fin_count = plan.fin_idx.cpu().numpy(), plan.fin_count.cpu().numpy()
+        qf, kf, vf = q.float().cpu().numpy()[0, :, 0], keys.float().cpu().numpy(), values.float().cpu().numpy()
+        got = out.cpu().numpy()[0, :, 0]
+        for h in range(H):
+            sel = fin_idx[h, : fin_count[h]]
+            if len(sel) == 0:
+                assert np.all(got[h] == 0.0), f"head {h}: empty list must give zeros"
+                continue
+            ref = oracle.verify(qf[h], kf[h // (H // G)], vf[h // (H // G)], np.sort(sel), scaling)
+            err = np.abs(got[h] - ref).max() / max(np.abs(ref).max(), 1e-30)
+            assert err <= 1e-5, f"head {h}: rel err {err}"
