@@ -642,18 +642,26 @@ struct FastMisc {
   SVA_DEV uint64_t& res64() const { return *reinterpret_cast<uint64_t*>(m + 56); }
 };
 
-// Threshold of the k largest nonzero composites held in e[] (dense slots;
-// the key part of every nonzero one inside [klo, khi]): values >= the result
-// are exactly the k largest.  Every thread of the block calls it; hist must
-// be zero on entry.  Uses misc slots 0 and res.
-SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32_t klo, uint32_t khi, uint32_t* hist,
-                             uint64_t* small, const FastMisc& f, const TopLds& tl, bool* exact) {
+// Threshold of the k largest nonzero composites held in e[] (dense slots),
+// binned by their scores v[] (the float each composite's key encodes) into
+// 4096 bins linear in [lo, lo + 4096 / inv_w): bin = (v - lo) * inv_w
+// (clamped), a non-decreasing function of v, so the bins order the
+// composites and only the boundary bin's members need ranking.  Values >=
+// the result are exactly the k largest.  Every thread of the block calls
+// it; hist must be zero on entry.  Uses misc slots 0 and res.  *exact is
+// false (result 0) when the boundary bin holds more than SMALL_CAP members.
+SVA_DEV int lin_bin(float v, float lo, float inv_w) {
+  const float b = (v - lo) * inv_w;
+  return b < 1.0f ? 0 : (b >= 4095.0f ? 4095 : (int)b);
+}
+
+SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], int dslots, int k, float lo, float inv_w,
+                             uint32_t* hist, uint64_t* small, const FastMisc& f, bool* exact) {
+#pragma clang fp contract(off)
   const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
-  const uint32_t range = khi - klo;
-  const int sh = range < 4096u ? 0 : (32 - __clz((int)range)) - 12;
 #pragma unroll
   for (int i = 0; i < NPD; ++i)
-    if (i < dslots && e[i] != 0ull) atomicAdd(&hist[((uint32_t)(e[i] >> 32) - klo) >> sh], 1u);
+    if (i < dslots && e[i] != 0ull) atomicAdd(&hist[lin_bin(v[i], lo, inv_w)], 1u);
   __syncthreads();
   // thread t owns bins 4095 - 4 t - j (j = 0..3), from the top
   const uint4 h = reinterpret_cast<const uint4*>(hist)[1023 - t];
@@ -663,7 +671,7 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32
   if (lane == WAVE - 1) f.wave(0, wid) = incl;
   __syncthreads();
   uint32_t above = incl - mine;
-  for (int v = 0; v < wid; ++v) above += f.wave(0, v);
+  for (int w = 0; w < wid; ++w) above += f.wave(0, w);
   {
     uint32_t a = above;
 #pragma unroll
@@ -678,10 +686,9 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32
   }
   if (t == 0) f.res(3) = 0u;
   __syncthreads();
-  const uint32_t b = f.res(0), need = (uint32_t)k - f.res(1), cnt = f.res(2);
-  const uint32_t bkey = klo + (b << sh);  // lowest score key of the boundary bin
+  const int b = (int)f.res(0);
+  const uint32_t need = (uint32_t)k - f.res(1), cnt = f.res(2);
   *exact = true;
-  if (cnt == need) return (uint64_t)bkey << 32;
   if (cnt > (uint32_t)SMALL_CAP) {
     // a massive tie class: the general register select
     *exact = false;
@@ -691,7 +698,7 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
     if (i < dslots) {  // uniform
-      const bool in = e[i] != 0ull && (((uint32_t)(e[i] >> 32) - klo) >> sh) == b;
+      const bool in = e[i] != 0ull && lin_bin(v[i], lo, inv_w) == b;
       const uint64_t m = __builtin_amdgcn_ballot_w64(in);
       if (m != 0ull) {
         uint32_t base = 0;
@@ -705,16 +712,19 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], int dslots, int k, uint32
   {
     // four lanes per member: lane q of member g compares it with members q, q + 4, ...
     const int g = t >> 2, q = t & 3;
-    const uint64_t v = g < (int)cnt ? small[g] : 0ull;
+    const uint64_t x = g < (int)cnt ? small[g] : 0ull;
     uint32_t greater = 0;
-    for (int o = q; o < (int)cnt; o += 4) greater += small[o] > v ? 1u : 0u;
+    for (int o = q; o < (int)cnt; o += 4) greater += small[o] > x ? 1u : 0u;
     greater += __shfl_xor(greater, 1, WAVE);
     greater += __shfl_xor(greater, 2, WAVE);
-    if (q == 0 && g < (int)cnt && greater == need - 1u) f.res64() = v;
+    if (q == 0 && g < (int)cnt && greater == need - 1u) f.res64() = x;
   }
   __syncthreads();
   return f.res64();
 }
+
+// 4096 / (hi - lo), or 0 (one bin) when the range is empty.
+SVA_DEV float lin_scale(float lo, float hi) { return hi > lo ? 4096.0f / (hi - lo) : 0.0f; }
 
 // The fast finish of an item; false (uniformly, before any output or LDS
 // write) when its conditions do not hold.
@@ -825,11 +835,14 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   }
   uint32_t khi = 0u;
   for (int v = 0; v < SNW; ++v) khi = max(khi, f.wave(1, v));
-  const uint32_t klo = f2key(item_floor(p, item) * kInvSqrtR);
+  const float vlo = item_floor(p, item) * kInvSqrtR;
   bool exact = true;
   uint64_t X = 1ull;
   if ((uint32_t)leff < M) {
-    X = fast_select(e, dslots, leff, klo, max(khi, klo), hist, small, f, tl, &exact);
+    float sv[NPD];
+#pragma unroll
+    for (int i = 0; i < NPD; ++i) sv[i] = key2f((uint32_t)(e[i] >> 32));
+    X = fast_select(e, sv, dslots, leff, vlo, lin_scale(vlo, key2f(khi)), hist, small, f, &exact);
     if (!exact) {
       __syncthreads();
       return false;  // a tie class too large to rank directly: the general paths
@@ -863,7 +876,8 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
       hi = max(hi, f.wave(2, v));
     }
     bool ex2 = true;
-    XB = fast_select(rc, dslots, beff, lo, hi, hist, small, f, tl, &ex2);
+    const float rlo = key2f(lo);
+    XB = fast_select(rc, rv, dslots, beff, rlo, lin_scale(rlo, key2f(hi)), hist, small, f, &ex2);
     if (!ex2) {
       __syncthreads();
       return false;
@@ -1260,9 +1274,9 @@ SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool k
   constexpr int KI = EPR / RPI;      // K load groups per round
   constexpr int DL = D / WAVE;       // V dimensions per lane
   // 16-bit V rows at head_dim 64: a load serves two rows, lanes 0-31 the first and 32-63 the second,
-  // two dimensions per lane (needs 4-byte aligned rows); vv[2j] / vv[2j + 1] then hold the lane's two
-  // dimensions of its row of the pair
-  const bool PAIRV = KV != F32 && D == 64 && v.kv_vec;
+  // two dimensions per lane (one 4-byte load on aligned rows); vv[2j] / vv[2j + 1] then hold the lane's
+  // two dimensions of its row of the pair
+  constexpr bool PAIRV = KV != F32 && D == 64;
   int32_t* kid = (int32_t*)(lds + kVerifyKid);
   float* part = (float*)(lds + kVerifyKid) + (kid_in_lds ? p.B : 0);  // [SNW][D + 2]: m, z, acc
   if (!kid_in_lds) {
@@ -1292,12 +1306,14 @@ SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool k
       const int64_t row = kvb + (int64_t)kid[min(e, cnt - 1)] * v.kv_rs + sub * EPL;
       kv_load<KV, EPL>(v.keys, row, v.kv_vec, kk[k]);
     }
-    if (PAIRV) {
+    if constexpr (PAIRV) {
       // row r0 + 2 j + (lane >= 32), dimensions 2 (lane & 31) and 2 (lane & 31) + 1
 #pragma unroll
       for (int j = 0; j < EPR / 2; ++j) {
         const int64_t row = kvb + (int64_t)kid[min(r0 + 2 * j + (lane >> 5), cnt - 1)] * v.kv_rs + 2 * (lane & 31);
-        const uint32_t x = *reinterpret_cast<const uint32_t*>((const uint16_t*)v.values + row);
+        const uint16_t* src = (const uint16_t*)v.values + row;
+        const uint32_t x = v.kv_vec ? *reinterpret_cast<const uint32_t*>(src)
+                                    : (uint32_t)src[0] | ((uint32_t)src[1] << 16);
         vv[2 * j][0] = KV == BF16 ? __uint_as_float(x << 16) : __half2float(__ushort_as_half((unsigned short)(x & 0xFFFFu)));
         vv[2 * j + 1][0] = KV == BF16 ? __uint_as_float(x & 0xFFFF0000u) : __half2float(__ushort_as_half((unsigned short)(x >> 16)));
       }
@@ -1337,7 +1353,7 @@ SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool k
     for (int d = 0; d < DL; ++d) acc[d] = acc[d] * f;
     acc2[0] = acc2[0] * f;
     acc2[1] = acc2[1] * f;
-    if (PAIRV) {
+    if constexpr (PAIRV) {
       // weight of entry r0 + 2 j + (lane >= 32): a readlane per row, the half's own
 #pragma unroll
       for (int j = 0; j < EPR / 2; ++j) {
@@ -1364,7 +1380,7 @@ SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool k
     mine[0] = m;
     mine[1] = z;
   }
-  if (PAIRV) {
+  if constexpr (PAIRV) {
     // the two halves hold the same dimensions for different rows: add them
     const float s0 = acc2[0] + __shfl_xor(acc2[0], 32, WAVE);
     const float s1 = acc2[1] + __shfl_xor(acc2[1], 32, WAVE);
