@@ -587,7 +587,9 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   SVA_REQUIRE(codes == nullptr || (code_type >= 0 && code_type <= 3 && n_keys >= 0 && shortlist > 0),
               "sva_query_lut: bad sampling arguments");
   // the threshold estimate serves the single-query uint8 scan; otherwise skipped
-  bool sample = codes != nullptr && n_seq == 1 && Q == 1 && code_type == 0 && S <= SAMPLE_MAX_S;
+  // (one subspace of at most 256 codewords selects by code class instead)
+  bool sample = codes != nullptr && n_seq == 1 && Q == 1 && code_type == 0 && S <= SAMPLE_MAX_S &&
+                !sva::class_shape(S, C, shortlist);
   int blocks = sample ? sva::sample_blocks(n_keys, S) : 0;
   // fewer sampled blocks when the head's weights leave less LDS
   while (blocks > SAMPLE_MIN_BLOCKS && lut_lds_bytes(D, R, S, C, blocks) > (size_t)sva::kMaxLds) blocks /= 2;

@@ -517,6 +517,12 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
     if (rc == SVA_OK && B > 0) rc = sva::fill_i32(fin_count, items, 0, (hipStream_t)stream);
     return rc;
   }
+  if (sva::summon_class_eligible(p, items)) {
+    const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
+    const int rc = sva::summon_class_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr);
+    if (rc == SVA_OK && fused != nullptr) *fused = with_fv;
+    return rc;
+  }
   if (sva::summon_wide_eligible(p, items)) {
     const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
     const int rc = sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr);

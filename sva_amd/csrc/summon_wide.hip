@@ -1263,10 +1263,9 @@ SVA_DEV float kv_one(const void* base, int64_t e) {
 }
 
 template <int D, int KV>
-SVA_DEV void verify_item(const WideArgs& a, int item, unsigned char* lds, bool kid_in_lds, const float* qsh) {
+SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, unsigned char* lds, bool kid_in_lds,
+                         const float* qsh) {
 #pragma clang fp contract(off)
-  const SummonParams& p = a.p;
-  const FusedVerify& v = a.fv;
   const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
   constexpr int EPL = D / VLPR;      // K elements per lane of a row
   constexpr int RPI = WAVE / VLPR;   // K rows per load group
@@ -1428,7 +1427,7 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   const bool in_lds = finish_item(a, item, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
   if (VD > 0) {
     __syncthreads();  // the budget list (LDS or global) and the LDS the finish used
-    verify_item<(VD > 0 ? VD : 64), VKV>(a, item, lds, in_lds, qsh);
+    verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, in_lds, qsh);
   }
 }
 
@@ -1451,6 +1450,443 @@ int launch_finish_any(const WideArgs& a, int64_t items, hipStream_t stream) {
   if (kv == BF16) return launch_finish<128, BF16>(a, items, stream);
   if (kv == F16) return launch_finish<128, F16>(a, items, stream);
   return launch_finish<128, F32>(a, items, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Code classes: one subspace of at most 256 codewords (1x256 codes).  A key's
+// scan score is T[code] / sqrt(R), so the keys fall into at most 256 score
+// classes and the top L keys (score descending, then lower key index) are
+// whole classes plus the lowest-index keys of one boundary class.  Four
+// launches replace the scan and the finish:
+//   class_count   per (item, chunk of CLASS_CHUNK keys): the histogram of
+//                 the chunk's allowed keys' codes;
+//   class_select  per item: class totals, the boundary class (score key kb,
+//                 `need` of its keys kept, shortlist length leff), and per
+//                 chunk its shortlist offset and the boundary keys in earlier
+//                 chunks;
+//   class_extract per (item, chunk): the chunk's kept keys in key order into
+//                 the shortlist, with their rank scores (computed as the scan
+//                 computes them);
+//   class_budget  per item: the budget select over the shortlist's rank
+//                 composites, the budget list in key order and (fused) the
+//                 verifier.
+// The results equal the scan path's: the same scores, ranks and tie rule.
+constexpr int CK_PT = 64;                 // keys per thread of a class chunk
+constexpr int CLASS_CHUNK = WB * CK_PT;   // 16384
+constexpr int CLASS_MAX_W = 4096;         // chunks per item: caches of up to 64M keys
+static_assert(FAST_M == CLASS_MAX_L, "the class path's shortlist fits the fast finish's dense slots");
+
+struct ClassArgs {
+  SummonParams p;
+  FusedVerify fv;
+  int W;             // chunks per item
+  uint32_t* counts;  // [items, W, 256] code histogram of each chunk's allowed keys
+  uint32_t* bound;   // [items, 4]: boundary score key, its keys kept, shortlist length, 0
+  uint32_t* woff;    // [items, W, 2]: shortlist offset of each chunk's keys, boundary keys in earlier chunks
+};
+
+// Codes of thread t's keys cs + 64 t .. + 63 (a partial chunk reads bytes under a guard).
+SVA_DEV void class_load(const uint8_t* __restrict__ codes, int k0, int ce, u32x4 (&raw)[4]) {
+  if (k0 + CK_PT <= ce) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) raw[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(codes + k0 + 16 * r));
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      uint32_t wv[4] = {0u, 0u, 0u, 0u};
+      for (int j = 0; j < 16; ++j)
+        if (k0 + 16 * r + j < ce) wv[j >> 2] |= (uint32_t)codes[k0 + 16 * r + j] << (8 * (j & 3));
+      raw[r] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+    }
+  }
+}
+
+// Score key of code c of an item: f2key(T[min(c, C - 1)] / sqrt(R)) (R = 64: exactly * 1/8), the key the
+// scan gives a key with this code.
+SVA_DEV uint32_t class_key(const SummonParams& p, int item, int c) {
+  return f2key(p.lut[(int64_t)item * p.C + min(c, p.C - 1)] * kInvSqrtR);
+}
+
+template <bool MASKED>
+__global__ void __launch_bounds__(WB) class_count_kernel(ClassArgs a) {
+  __shared__ uint32_t hist[NW][256];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x / a.W, w = blockIdx.x % a.W;
+  const int t = threadIdx.x, wid = t / WAVE;
+  const int cs = w * CLASS_CHUNK, ce = (int)min((int64_t)cs + CLASS_CHUNK, p.N);
+  const int k0 = cs + t * CK_PT;
+  const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)(item % p.H) * p.code_hs;
+  u32x4 raw[4];
+  class_load(codes, k0, ce, raw);
+#pragma unroll
+  for (int i = 0; i < NW; ++i) hist[i][t] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int n = k0 + 16 * r + j;
+      bool ok = n < ce;
+      if (MASKED && ok) ok = mask_allows(p.mask, n, p.mask_type);
+      if (ok) atomicAdd(&hist[wid][byte_of(raw[r], j)], 1u);
+    }
+  }
+  __syncthreads();
+  a.counts[((int64_t)item * a.W + w) * 256 + t] = hist[0][t] + hist[1][t] + hist[2][t] + hist[3][t];
+}
+
+constexpr int CSEL_PER = CLASS_MAX_W / SB;  // chunks per thread of class_select (prefix sums)
+constexpr int CSEL_G = SB / 256;              // thread groups over the chunks (code totals)
+
+// Every phase keeps its loads in flight together: the counts were written
+// by workgroups on other XCDs, so each dependent round trip is long.
+__global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
+  __shared__ uint32_t key[256], tot[256], flags[256], part[CSEL_G][256], abv[CSEL_G][256], eqv[CSEL_G][256];
+  __shared__ uint32_t scratch[SNW + 1], res[4];
+  __shared__ uint32_t sa[CLASS_MAX_W], sb[CLASS_MAX_W];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x, t = threadIdx.x, W = a.W;
+  const int c = t & 255, g = t >> 8;
+  const uint32_t* cnt = a.counts + (int64_t)item * W * 256;
+  // code c's total: group g sums chunks g, g + CSEL_G, ..., 16 loads in flight at a time
+  {
+    uint32_t acc = 0;
+    for (int w0 = g; w0 < W; w0 += 16 * CSEL_G) {
+      uint32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int w = w0 + u * CSEL_G;
+        v[u] = w < W ? cnt[(int64_t)w * 256 + c] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc += v[u];
+    }
+    part[g][c] = acc;
+  }
+  if (t < 256) key[t] = class_key(p, item, t);
+  if (t == 0) {
+    res[0] = 0xFFFFFFFFu;  // no boundary class (empty shortlist): no key matches
+    res[1] = 0u;
+  }
+  __syncthreads();
+  if (t < 256) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int q = 0; q < CSEL_G; ++q) n += part[q][t];
+    tot[t] = n;
+  }
+  __syncthreads();
+  uint32_t A = 0;
+  for (int q = 0; q < 256; q += 64) A += tot[q + lane_id()];  // every wave sums all 256 totals
+  A = wave_sum_u32(A);
+  const int leff = (int)min((uint32_t)p.L, A);
+  // keys strictly above code c's class and in it: group g over codes [64 g, 64 g + 64)
+  {
+    const uint32_t k = key[c];
+    uint32_t above = 0, eq = 0;
+    for (int q = 64 * g; q < 64 * g + 64; ++q) {
+      const uint32_t kq = key[q], tq = tot[q];
+      above += kq > k ? tq : 0u;
+      eq += kq == k ? tq : 0u;
+    }
+    abv[g][c] = above;
+    eqv[g][c] = eq;
+  }
+  __syncthreads();
+  if (t < 256) {
+    uint32_t above = 0, eq = 0;
+#pragma unroll
+    for (int q = 0; q < CSEL_G; ++q) {
+      above += abv[q][t];
+      eq += eqv[q][t];
+    }
+    if (tot[t] > 0 && above < (uint32_t)leff && above + eq >= (uint32_t)leff) {
+      res[0] = key[t];  // every code of the boundary class writes the same values
+      res[1] = (uint32_t)leff - above;
+    }
+  }
+  __syncthreads();
+  const uint32_t kb = res[0], need = res[1];
+  if (t < 256) flags[t] = (key[t] > kb ? 1u : 0u) | (key[t] == kb ? 2u : 0u);
+  __syncthreads();
+  // per chunk: kept keys above the boundary class, keys of the boundary class; 16 lanes per chunk, each
+  // over 16 codes (four 16-byte loads issued together), summed over the lanes
+  {
+    const int q = t & 15;
+    uint32_t fl[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) fl[e] = flags[16 * q + e];
+    for (int w0 = 0; w0 < W; w0 += SB / 16) {
+      const int w = w0 + t / 16;
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = w < W ? reinterpret_cast<const uint4*>(cnt + (int64_t)w * 256 + 16 * q)[u] : uint4{0u, 0u, 0u, 0u};
+      uint32_t x = 0, y = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x += (fl[4 * u + e] & 1u) ? vv[e] : 0u;
+          y += (fl[4 * u + e] & 2u) ? vv[e] : 0u;
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        x += __shfl_xor(x, o, 16);
+        y += __shfl_xor(y, o, 16);
+      }
+      if (q == 0 && w < W) {
+        sa[w] = x;
+        sb[w] = y;
+      }
+    }
+  }
+  __syncthreads();
+  // thread t: chunks [t * CSEL_PER, (t + 1) * CSEL_PER); boundary keys before each, then its kept keys
+  const int w0 = t * CSEL_PER;
+  uint32_t bsum = 0;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) bsum += w0 + i < W ? sb[w0 + i] : 0u;
+  uint32_t bpre = block_excl_scan<SB>(bsum, scratch, nullptr);  // boundary keys in chunks before w0
+  uint32_t kept[CSEL_PER], ksum = 0;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) {
+    const int w = w0 + i;
+    kept[i] = 0u;
+    if (w < W) {
+      const uint32_t b = sb[w];
+      kept[i] = sa[w] + (need > bpre ? min(need - bpre, b) : 0u);
+      sb[w] = bpre;  // this thread's own chunks only
+      bpre += b;
+      ksum += kept[i];
+    }
+  }
+  uint32_t koff = block_excl_scan<SB>(ksum, scratch, nullptr);
+  uint32_t* wo = a.woff + (int64_t)item * W * 2;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) {
+    const int w = w0 + i;
+    if (w < W) {
+      wo[2 * w] = koff;
+      wo[2 * w + 1] = sb[w];
+      koff += kept[i];
+    }
+  }
+  if (t == 0) {
+    a.bound[4 * item] = kb;
+    a.bound[4 * item + 1] = need;
+    a.bound[4 * item + 2] = (uint32_t)leff;
+    a.bound[4 * item + 3] = 0u;
+    p.sl_count[item] = leff;
+  }
+}
+
+template <bool MASKED>
+__global__ void __launch_bounds__(WB) class_extract_kernel(ClassArgs a) {
+#pragma clang fp contract(off)
+  __shared__ uint32_t key[256], scratch[NW + 1];
+  __shared__ int32_t kept_keys[CLASS_MAX_L];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x / a.W, w = blockIdx.x % a.W;
+  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  const int cs = w * CLASS_CHUNK, ce = (int)min((int64_t)cs + CLASS_CHUNK, p.N);
+  const int k0 = cs + t * CK_PT;
+  const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)(item % p.H) * p.code_hs;
+  u32x4 raw[4];
+  class_load(codes, k0, ce, raw);
+  key[t] = class_key(p, item, t);
+  const uint32_t kb = a.bound[4 * item], need = a.bound[4 * item + 1], leff = a.bound[4 * item + 2];
+  const uint32_t* wo = a.woff + ((int64_t)item * a.W + w) * 2;
+  const uint32_t off = wo[0], bpre = wo[1];
+  const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[lane & 15];
+  __syncthreads();
+  // this thread's keys above the boundary class and in it (bit i: key k0 + i)
+  uint64_t am = 0ull, bm = 0ull;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int i = 16 * r + j;
+      bool ok = k0 + i < ce;
+      if (MASKED && ok) ok = mask_allows(p.mask, k0 + i, p.mask_type);
+      const uint32_t kk = key[byte_of(raw[r], j)];
+      am |= (uint64_t)(ok && kk > kb) << i;
+      bm |= (uint64_t)(ok && kk == kb) << i;
+    }
+  }
+  // boundary keys are kept in key order up to `need` over the whole item
+  const uint32_t nb = (uint32_t)__popcll(bm);
+  const uint32_t before = bpre + block_excl_scan<WB>(nb, scratch, nullptr);
+  uint32_t take = need > before ? min(need - before, nb) : 0u;
+  uint64_t keep = am;
+  for (uint64_t m = bm; take > 0u; --take) {
+    const uint64_t low = m & (~m + 1ull);
+    keep |= low;
+    m ^= low;
+  }
+  uint32_t total;
+  uint32_t o = block_excl_scan<WB>((uint32_t)__popcll(keep), scratch, &total);
+  int32_t* sl = p.sl_idx + (int64_t)item * p.L;
+  while (keep != 0ull) {
+    const int i = __ffsll((long long)keep) - 1;
+    keep &= keep - 1ull;
+    if (off + o < leff) sl[off + o] = k0 + i;
+    if (o < (uint32_t)CLASS_MAX_L) kept_keys[o] = k0 + i;
+    ++o;
+  }
+  __syncthreads();
+  // rank scores as the scan computes them: one 16-lane DPP row per key, 16 keys per wave in flight
+  total = min(total, (uint32_t)CLASS_MAX_L);
+  const int j = lane & 15, row = lane >> 4;
+  const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
+  float* rank_out = p.sl_rank + (int64_t)item * p.L + off;
+  constexpr int RU = 4;
+  for (uint32_t c0 = (uint32_t)wid * 4 * RU; c0 < total; c0 += NW * 4 * RU) {
+    float4 rv[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const uint32_t c = c0 + 4 * u + row;
+      const int n = c < total ? kept_keys[c] : 0;
+      rv[u] = c < total ? reinterpret_cast<const float4*>(klow + (int64_t)n * p.R)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const float dot = rank_dot64_row16(rv[u], qq);
+      const uint32_t c = c0 + 4 * u + row;
+      if (c < total && off + c < leff && j == 0) rank_out[c] = dot * kInvSqrtR;
+    }
+  }
+}
+
+// Budget of a class-path item over its shortlist (key order, leff entries),
+// then (VD > 0) the verifier, in the finish kernel's LDS layout.
+template <int VD, int VKV>
+__global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ float qsh[VD > 0 ? VD : 1];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x, t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  if (VD > 0 && t < VD) qsh[t] = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + t, a.fv.q_dtype);
+  const int leff = (int)a.bound[4 * item + 2];
+  const int beff = min(p.B, leff);
+  if (t == 0) p.fin_count[item] = beff;
+  uint32_t* hist = (uint32_t*)(lds + kFastHist);
+  uint64_t* small = (uint64_t*)(lds + kFastSmall);
+  const FastMisc f{(uint32_t*)(lds + kFastMisc)};
+  uint32_t* wcnt = (uint32_t*)(lds + kFinWcnt);
+  uint32_t* scratch = (uint32_t*)(lds + kFinScratch);
+  const bool keep_kid = p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
+  int32_t* kidl = (int32_t*)(lds + kVerifyKid);
+  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+  const int dslots = (leff + SB - 1) / SB;
+  const int32_t* sl = p.sl_idx + (int64_t)item * p.L;
+  const float* sr = p.sl_rank + (int64_t)item * p.L;
+  uint64_t rc[NPD];
+  float rv[NPD];
+  uint32_t rmin = 0xFFFFFFFFu, rmax = 0u;
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    const int jj = t + i * SB;
+    const bool in = i < dslots && jj < leff;
+    rv[i] = in ? sr[jj] : 0.0f;
+    const uint32_t k = f2key(rv[i]);
+    rc[i] = in ? composite(k, (uint32_t)sl[jj]) : 0ull;
+    if (in) {
+      rmin = min(rmin, k);
+      rmax = max(rmax, k);
+    }
+  }
+  wave_min_max_u32(rmin, rmax);
+  if (lane == 0) {
+    f.wave(1, wid) = rmin;
+    f.wave(2, wid) = rmax;
+  }
+  __syncthreads();
+  uint32_t lo = 0xFFFFFFFFu, hi = 0u;
+  for (int v = 0; v < SNW; ++v) {
+    lo = min(lo, f.wave(1, v));
+    hi = max(hi, f.wave(2, v));
+  }
+  uint64_t XB = 1ull;
+  if (beff < leff) {
+    bool ex = true;
+    const float rlo = key2f(lo);
+    XB = fast_select(rc, rv, dslots, beff, rlo, lin_scale(rlo, key2f(hi)), hist, small, f, &ex);
+    if (!ex) {
+      // a tie class too large to rank directly: the general register select
+      __syncthreads();
+      const TopLds tl{(uint32_t*)(lds + kFinHist), (uint64_t*)(lds + kFinSmall), scratch, (uint32_t*)(lds + kFinShared),
+                      (uint64_t*)(lds + kFinShared64)};
+      XB = select_top_regs<SB, NPD>(rc, beff, ((uint64_t)hi << 32) | 0xFFFFFFFFull, (uint64_t)lo << 32, tl, dslots,
+                                    true);
+    }
+  }
+  // the budget list in shortlist (key) order
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    if (i < dslots) {  // uniform
+      const uint64_t mb = __builtin_amdgcn_ballot_w64(rc[i] != 0ull && rc[i] >= XB);
+      if (lane == 0) wcnt[i * SNW + wid] = (uint32_t)__popcll(mb);
+    }
+  }
+  __syncthreads();
+  {
+    const uint32_t v = t < dslots * SNW ? wcnt[t] : 0u;
+    const uint32_t o = block_excl_scan<SB>(v, scratch, nullptr);
+    if (t < dslots * SNW) wcnt[t] = o;
+    __syncthreads();
+  }
+  int32_t* fin = p.fin_idx + (int64_t)item * p.B;
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    if (i < dslots) {  // uniform
+      const bool sb = rc[i] != 0ull && rc[i] >= XB;
+      const uint64_t mb = __builtin_amdgcn_ballot_w64(sb);
+      if (sb) {
+        const uint32_t o = wcnt[i * SNW + wid] + lanes_below(mb);
+        if (o < (uint32_t)beff) {
+          fin[o] = (int32_t)composite_index(rc[i]);
+          if (keep_kid) kidl[o] = (int32_t)composite_index(rc[i]);
+        }
+      }
+    }
+  }
+  if (VD > 0) {
+    __syncthreads();
+    verify_item<(VD > 0 ? VD : 64), VKV>(p, a.fv, item, lds, keep_kid, qsh);
+  }
+}
+
+template <int VD, int VKV>
+int launch_class_budget(const ClassArgs& a, int64_t items, hipStream_t stream) {
+  SVA_SET_MAX_LDS_ONCE((class_budget_kernel<VD, VKV>), kFinLds, "hipFuncSetAttribute(class_budget_kernel)");
+  hipLaunchKernelGGL((class_budget_kernel<VD, VKV>), dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
+  SVA_CHECK_LAUNCH("class_budget_kernel");
+  return SVA_OK;
+}
+
+template <bool MASKED>
+int launch_class(const ClassArgs& a, int64_t items, hipStream_t stream) {
+  hipLaunchKernelGGL((class_count_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_count_kernel");
+  hipLaunchKernelGGL(class_select_kernel, dim3((unsigned)items), dim3(SB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_select_kernel");
+  hipLaunchKernelGGL((class_extract_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_extract_kernel");
+  if (a.p.B <= 0) return SVA_OK;
+  if (a.fv.out == nullptr) return launch_class_budget<0, F32>(a, items, stream);
+  const int kv = a.fv.kv_dtype;
+  if (a.fv.D == 64) {
+    if (kv == BF16) return launch_class_budget<64, BF16>(a, items, stream);
+    if (kv == F16) return launch_class_budget<64, F16>(a, items, stream);
+    return launch_class_budget<64, F32>(a, items, stream);
+  }
+  if (kv == BF16) return launch_class_budget<128, BF16>(a, items, stream);
+  if (kv == F16) return launch_class_budget<128, F16>(a, items, stream);
+  return launch_class_budget<128, F32>(a, items, stream);
 }
 
 template <int S, bool SMALLC, bool MASKED>
@@ -1497,6 +1933,37 @@ size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   if (n_seq != 1 || Q != 1 || n_keys < kWideMinKeys || items > kMaxWideItems) return 256;
   const int64_t W = (n_keys + CHUNK - 1) / CHUNK;
   return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
+}
+
+bool summon_class_eligible(const SummonParams& p, int64_t items) {
+  if (!summon_wide_eligible(p, items) || !class_shape(p.S, p.C, p.L)) return false;
+  return (p.N + CLASS_CHUNK - 1) / CLASS_CHUNK <= CLASS_MAX_W;
+}
+
+int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                      const FusedVerify* fv) {
+  const int64_t items = (int64_t)p.H;  // one sequence, q = 1
+  const int64_t W = (p.N + CLASS_CHUNK - 1) / CLASS_CHUNK;
+  const size_t counts = align256((size_t)(items * W * 256) * sizeof(uint32_t));
+  const size_t bound = align256((size_t)(items * 4) * sizeof(uint32_t));
+  const size_t need = counts + bound + align256((size_t)(items * W * 2) * sizeof(uint32_t));
+  SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
+              "sva_summon: workspace of %zu bytes (256-byte aligned) required, got %zu", need, workspace_bytes);
+  ClassArgs a;
+  a.p = p;
+  a.W = (int)W;
+  a.fv = FusedVerify{};
+  a.fv.out = nullptr;
+  if (fv != nullptr) {
+    SVA_REQUIRE(fused_verify_eligible(p, items, *fv), "summon_class_path: the fused verifier does not fit these sizes");
+    a.fv = *fv;
+  }
+  char* ws = (char*)workspace;
+  a.counts = (uint32_t*)ws;
+  a.bound = (uint32_t*)(ws + counts);
+  a.woff = (uint32_t*)(ws + counts + bound);
+  const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
+  return masked ? launch_class<true>(a, items, stream) : launch_class<false>(a, items, stream);
 }
 
 bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv) {

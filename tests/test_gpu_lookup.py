@@ -229,6 +229,7 @@ def test_decode_plan_graph_replays_equal_eager():
     (9, 64, torch.float16, 8192, 2048, False),
     (1, 128, torch.bfloat16, 1024, 256, False),
     (3, 64, torch.bfloat16, 2048, 512, True),
+    (3, 64, torch.bfloat16, 2048, 512, "1x256"),
 ])
 def test_lookup_verify_matches_oracle(G, D, kv_dtype, L, B, masked):
     """sva_lookup_verify (the verifier inside the finish kernel on the wide path) against the oracle's fp64
@@ -238,6 +239,8 @@ def test_lookup_verify_matches_oracle(G, D, kv_dtype, L, B, masked):
 
     device = torch.device("cuda:0")
     N, S, C, H = 40000, 4, 64, 9
+    if masked == "1x256":  # the code-class path, verifier inside its budget kernel
+        S, C, masked = 1, 256, False
     q, q_proj, scale, cb, codes, k_low = _inputs(device, N, S, C, torch.bfloat16, seed=41 + G + D, D=D)
     g = torch.Generator(device=device).manual_seed(42)
     keys = torch.randn(G, N, D, device=device, generator=g).to(kv_dtype)

@@ -272,3 +272,25 @@ def test_summon_select_staged_paths(device, case):
             codes[h, 50000:51000] = best
     fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, 2048, 512)
     _check_fused(codes, k_low, fused, split, q_low, lut, 2048, 512)
+
+
+@pytest.mark.parametrize("N,C,L,B,few,masked", [
+    (1048576, 256, 2048, 512, False, False),   # 1M keys, ~4K keys per score class
+    (300000, 100, 1024, 256, False, True),     # fewer codewords, float mask
+    (120000, 256, 2048, 512, True, False),     # 3 codes: a boundary class of ~40K keys
+    (70001, 256, 7168, 2048, False, False),    # the largest shortlist of the class path, partial chunk
+    (1048576, 256, 512, 128, False, False),    # tight shortlist / budget
+])
+def test_class_path_single_subspace(device, N, C, L, B, few, masked):
+    """One subspace of <= 256 codewords selects by code class (count, boundary class, ordered extraction,
+    budget): shortlist and ranks equal the oracle's top-L (score desc, key asc) and the standalone budget
+    select's lists, every head."""
+    assert _strategy(9, N, 64, 1, C, L) == 1, "wide path not selected"
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, 1, C, seed=(N + C + L) % 83, few=few)
+    mask = allowed = None
+    if masked:
+        rng = np.random.default_rng(9)
+        m = np.where(rng.random(N) < 0.4, np.finfo(np.float32).min, 0.0).astype(np.float32)[None, None, None, :]
+        mask, allowed = torch.from_numpy(m).to(device), m[0, 0, 0] > -1e4
+    fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B, mask=mask)
+    _check_fused(codes, k_low, fused, split, q_low, lut, L, B, allowed=allowed)
