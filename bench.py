@@ -157,9 +157,15 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 
 
 # kernels of one decode step (sva_lookup_verify), by entry point
-SUMMON_KERNELS = ("query_decode_kernel", "query_lut_kernel", "wide_scan_kernel", "wide_finish_kernel")
+SUMMON_KERNELS = ("query_decode_kernel", "query_lut_kernel", "wide_scan_kernel", "wide_finish_kernel",
+                  "class_count_kernel", "class_select_kernel", "class_extract_kernel", "class_budget_kernel")
 PATH_KERNELS = SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel", "verify_combine_kernel")
-PROFILE_STEM = "lookup_select_decode_1m_{layout}"
+PROFILE_STEM = "lookup_verify_decode_1m_{layout}{lb}"
+
+
+def profile_stem(args) -> str:
+    lb = "" if (args.shortlist, args.budget) == (2048, 512) else f"_{args.shortlist}_{args.budget}"
+    return PROFILE_STEM.format(layout=args.layout, lb=lb)
 REF_US_PER_QUERY = 1024.0  # the reference's published decode lookup, 1M keys, 4x64, 2048/512 (H100)
 # the reference's published lookups at 1M keys, q=1, by (layout, shortlist, budget) (H100, PyTorch bf16)
 REF_US_BY_CONFIG = {("4x64", 2048, 512): REF_US_PER_QUERY, ("1x256", 2048, 512): 649.0, ("2x256", 2048, 512): 776.0,
@@ -183,7 +189,7 @@ def write_profiles(args):
     import csv
 
     stats_csv, fetch_csv, write_csv = args.write_profiles
-    stem = PROFILE_STEM.format(layout=args.layout)
+    stem = profile_stem(args)
     out_dir = ROOT / "profiles"
     out_dir.mkdir(exist_ok=True)
     rows = {}
@@ -203,11 +209,14 @@ def write_profiles(args):
     copy_kib = float(args.calibrate_copy << 10)
     fetch_scale = copy_kib / avg[("__amd_rocclr_copyBuffer", "FETCH_SIZE")]
     write_scale = copy_kib / avg[("__amd_rocclr_copyBuffer", "WRITE_SIZE")]
+    cfg = f"--layout {args.layout} --shortlist {args.shortlist} --budget {args.budget}"
     cmd_trace = (f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o ks -- python bench.py --steps 300 "
-                 f"--warmup 50 --no-cpu-baseline --calibrate-copy {args.calibrate_copy} --layout {args.layout}")
+                 f"--warmup 50 --no-cpu-baseline --no-decode --no-graph --calibrate-copy {args.calibrate_copy} {cfg}")
     cmd_pmc = (f"rocprofv3 --pmc {{FETCH_SIZE|WRITE_SIZE}} --output-format csv -d OUT -o pf -- python bench.py "
-               f"--steps 20 --warmup 5 --no-cpu-baseline --calibrate-copy {args.calibrate_copy} --layout {args.layout}")
-    lines = [f"# Kernel durations: decode lookup at 1M keys, {args.layout} codes, L/B 2048/512, q=1, 9 q-heads / 3 KV heads",
+               f"--steps 20 --warmup 5 --no-cpu-baseline --no-decode --no-graph --calibrate-copy {args.calibrate_copy} "
+               f"{cfg}")
+    lines = [f"# Kernel durations: decode step (sva_lookup_verify) at 1M keys, {args.layout} codes, L/B "
+             f"{args.shortlist}/{args.budget}, q=1, 9 q-heads / 3 KV heads",
              "", f"Command: `{cmd_trace}` (file `ks_kernel_stats.csv`).", "",
              "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
     total = 0.0
@@ -216,10 +225,11 @@ def write_profiles(args):
             c, a, mn, mx = rows[k]
             total += a
             lines.append(f"| {k} | {c} | {a / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |")
-    lines += [f"| **sum per lookup** | | {total / 1e3:.2f} | | |", ""]
+    lines += [f"| **sum per decode step** | | {total / 1e3:.2f} | | |", ""]
     (out_dir / f"{stem}_kernel_trace.md").write_text("\n".join(lines))
     summon_bytes = 0.0
-    lines = [f"# HBM traffic per dispatch: decode lookup at 1M keys, {args.layout} codes", "",
+    lines = [f"# HBM traffic per dispatch: decode step (sva_lookup_verify) at 1M keys, {args.layout} codes, L/B "
+             f"{args.shortlist}/{args.budget}", "",
              f"Commands: `{cmd_pmc}`, one run per counter.", "",
              f"Calibration: the {args.calibrate_copy} MiB device copy (`__amd_rocclr_copyBuffer`) reads "
              f"FETCH_SIZE {avg[('__amd_rocclr_copyBuffer', 'FETCH_SIZE')]:.0f} KiB and WRITE_SIZE "
@@ -231,8 +241,7 @@ def write_profiles(args):
         if fk is None or wk is None:
             continue
         b = 1024.0 * (fk * fetch_scale + wk * write_scale)
-        if k in SUMMON_KERNELS:
-            summon_bytes += b
+        summon_bytes += b  # every kernel of the decode step that ran
         lines.append(f"| {k} | {fk:.1f} | {wk:.1f} | {b:,.0f} |")
     entry = "sva_lookup_verify"
     lines += ["", f"{entry} (query table, scan, finish with the verifier): {summon_bytes:,.0f} bytes per decode "
@@ -803,7 +812,7 @@ def main():
     step_us_avg = per_stage_us["lookup_verify"]
     achieved = bytes_["total"] / (step_us_avg * 1e-6) / 1e9
     traffic = None
-    pmc = ROOT / "profiles" / (PROFILE_STEM.format(layout=args.layout) + "_traffic.json")
+    pmc = ROOT / "profiles" / (profile_stem(args) + "_traffic.json")
     if pmc.exists() and n == 1_048_576:
         try:
             traffic = json.loads(pmc.read_text()).get("hbm_bytes_per_launch")
