@@ -28,8 +28,13 @@ Pinning (what checks each function; see tests/test_oracle.py):
       and brute force.
   verify
       fp64 closed form (softmax-weighted sum) against a float64 torch softmax.
-  rebuild_postings / static / inverted candidate sets
+  rebuild_postings
       partition and bincount invariants, brute-force membership.
+  static_decode / inverted_decode / cell_choice
+      the reference's own _inverted_static_decode_attention and
+      _inverted_decode_attention recorded on seeded tie-free cases
+      (tests/golden/inverted_reference.npz): candidate, refill and final
+      sets, stats and outputs; a planted wrong cell rule is caught.
   residual_adapter
       torch-CPU's own nn.Linear / F.gelu module of the reference on the same
       inputs (float64), the zero-initialised up projection (output = input),
