@@ -52,7 +52,7 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
-    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged", "socket"),
+    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged", "socket", "overshoot"),
                     help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA; "
                          "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched; "
                          "ragged: continuous-batch static inverted decode over packed sequences; "
@@ -655,6 +655,58 @@ def model_decode(args, with_cpu: bool):
     }
 
 
+def overshoot_suite(args):
+    """The decode step when the sampled shortlist floor overshoots for every
+    head: the first key of each sampled block of a 1M-key 4x64 cache gets
+    the best code of every subspace, so only those 256 keys reach the floor
+    (fewer than L) and the finish selects over all keys.  HIP events around
+    `--steps` calls (after `--warmup`), the overshoot flags checked."""
+
+    import torch
+
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    n, subspaces, codewords, heads = args.keys, 4, 64, 9
+    layer = Layer(torch, device, n, subspaces, codewords, args.seed + 5)
+    shortlist, budget = min(args.shortlist, n), min(args.budget, args.shortlist, n)
+    # the best code of each subspace from the layer's own table
+    q_low = torch.einsum("hd,hdr->hr", layer.q[0, :, 0].float(), layer.q_proj) * layer.scale[:, None]
+    sub = 64 // subspaces
+    lut = torch.einsum("hsd,hscd->hsc", q_low.view(heads, subspaces, sub), layer.codebooks)
+    best = lut.argmax(dim=-1).to(torch.uint8)  # [H, S]
+    blocks = min(max(n // 256, 64), 32768 // (32 * subspaces), 256)
+    rows = torch.tensor([(b * (n - 32) // (blocks - 1)) & ~15 for b in range(blocks)], device=device)
+    layer.codes[:, rows] = best[:, None, :]
+    plan = kernels.ScanDecodePlan(device, 1, heads, 1, 64, 64, subspaces, codewords, shortlist, budget)
+    out = torch.empty(1, heads, 1, 64, device=device, dtype=torch.bfloat16)
+
+    def step():
+        plan.run(layer.q, layer.q_proj, layer.scale, layer.codebooks, layer.codes, layer.k_low, layer.keys,
+                 layer.values, n, 64 ** -0.5, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    hits = int(plan.overshoot.sum().item())
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in ev:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    us = sorted(1e3 * a.elapsed_time(b) for a, b in ev)
+    print(json.dumps({
+        "metric": "us/query with the sampled floor overshooting (all-keys select, 1M keys, 4x64)",
+        "value": round(sum(us) / len(us), 1), "unit": "us/query", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": False, "p50_us": round(us[len(us) // 2], 1),
+        "heads_overshooting": hits, "heads": heads, "dtype": "fp32 scores / u8 codes / bf16 K,V",
+        "data": "synthetic (seeded N(0,1) caches, uniform codes, 256 sampled keys rigged to the best code)",
+        "config": {"workload": "million-key cached decode lookup with a forced floor overshoot", "keys": n,
+                   "shortlist": shortlist, "budget": budget},
+    }), flush=True)
+
+
 def model_suite(args):
     """The model decode as its own JSON line (metric decode tok/s)."""
 
@@ -725,10 +777,11 @@ def main():
     if args.write_profiles:
         write_profiles(args)
         return
-    if args.suite in ("write", "model", "ragged", "socket"):
+    if args.suite in ("write", "model", "ragged", "socket", "overshoot"):
         if args.gpus != 1:
             sys.exit(2)
-        {"write": write_suite, "model": model_suite, "ragged": ragged_suite, "socket": socket_suite}[args.suite](args)
+        {"write": write_suite, "model": model_suite, "ragged": ragged_suite, "socket": socket_suite,
+         "overshoot": overshoot_suite}[args.suite](args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "

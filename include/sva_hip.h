@@ -165,9 +165,13 @@ int sva_lookup_select(const void *q, int q_dtype, int64_t q_head_stride, int64_t
  * 1) with D = 64 or 128 the verifier runs inside the finish kernel, each
  * item's workgroup over the list it has just selected; otherwise
  * sva_verify runs after the lookup with verify_workspace
- * (sva_verify_workspace_bytes(1, H, G, 1, D, B)).  K / V rows of KV head g
- * at g * kv_head_stride + n * kv_row_stride elements; query head h reads KV
- * head h / (H / G).
+ * (sva_verify_workspace_bytes(1, H, G, 1, D, B)).  One subspace of at most
+ * 256 codewords selects by code class (count, boundary class, ordered
+ * extraction, budget) with the verifier inside its budget kernel.  K / V rows
+ * of KV head g at g * kv_head_stride + n * kv_row_stride elements; query head
+ * h reads KV head h / (H / G).  floor_overshoot (optional, int32 [H]): 1 for
+ * a head whose sampled shortlist floor overshot (fewer than L keys above
+ * it), so that the finish selected over every key; 0 otherwise.
  */
 int sva_lookup_verify(const void *q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R, int64_t S,
                       int64_t C, const float *q_proj, const float *scale, const float *codebooks, const void *codes,
@@ -178,7 +182,7 @@ int sva_lookup_verify(const void *q, int q_dtype, int64_t q_head_stride, int64_t
                       size_t workspace_bytes, const void *keys, const void *values, int kv_dtype,
                       int64_t kv_head_stride, int64_t kv_row_stride, int64_t G, float scaling, void *out,
                       int out_dtype, int64_t out_head_stride, void *verify_workspace, size_t verify_workspace_bytes,
-                      void *stream);
+                      int32_t *floor_overshoot, void *stream);
 
 /*
  * Which summon strategy a call with these shapes takes (16-byte aligned

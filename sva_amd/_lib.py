@@ -43,7 +43,7 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
                                _I64, _P, _I, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _SZ, _P]),
     "sva_lookup_verify": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I, _I64, _P, _I64, _I64,
                                _I64, _P, _I, _I64, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _SZ,
-                               _P, _P, _I, _I64, _I64, _I64, _F, _P, _I, _I64, _P, _SZ, _P]),
+                               _P, _P, _I, _I64, _I64, _I64, _F, _P, _I, _I64, _P, _SZ, _P, _P]),
     "sva_summon_strategy": (_I, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I]),
     "sva_budget_select": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P, _P]),
     "sva_verify_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),

@@ -101,15 +101,17 @@ int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
+// overshoot (optional, [items]): 1 where the sampled floor overshot and the
+// finish selected over every key, else 0.
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                     const FusedVerify* fv = nullptr);
+                     const FusedVerify* fv = nullptr, int32_t* overshoot = nullptr);
 // One subspace of at most 256 codewords with a shortlist of at most
 // CLASS_MAX_L: the wide path selects by code class (no sampled floor needed).
 constexpr int CLASS_MAX_L = 7168;
 inline bool class_shape(int64_t S, int64_t C, int64_t L) { return S == 1 && C <= 256 && L <= CLASS_MAX_L; }
 bool summon_class_eligible(const SummonParams& p, int64_t items);
 int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                      const FusedVerify* fv = nullptr);
+                      const FusedVerify* fv = nullptr, int32_t* overshoot = nullptr);
 // Whether summon_wide_path can run `fv` in its finish kernel for these sizes.
 bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);

@@ -467,7 +467,7 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
                 int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
-                const sva::FusedVerify* fv = nullptr, bool* fused = nullptr) {
+                const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr) {
   if (fused != nullptr) *fused = false;
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
@@ -519,15 +519,21 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   }
   if (sva::summon_class_eligible(p, items)) {
     const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
-    const int rc = sva::summon_class_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr);
+    const int rc = sva::summon_class_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr,
+                                          overshoot);
     if (rc == SVA_OK && fused != nullptr) *fused = with_fv;
     return rc;
   }
   if (sva::summon_wide_eligible(p, items)) {
     const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
-    const int rc = sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr);
+    const int rc = sva::summon_wide_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr,
+                                         overshoot);
     if (rc == SVA_OK && fused != nullptr) *fused = with_fv;
     return rc;
+  }
+  if (overshoot != nullptr) {  // the per-item paths use no sampled floor
+    const int rc = sva::fill_i32(overshoot, items, 0, (hipStream_t)stream);
+    if (rc != SVA_OK) return rc;
   }
   if (sva::summon_regs_eligible(p)) return sva::summon_regs_path(p, items, (hipStream_t)stream);
   int rc = sva::summon_item_path(p, items, (hipStream_t)stream);
@@ -597,7 +603,8 @@ extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stri
                                  int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
                                  const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                                  int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
-                                 void* verify_workspace, size_t verify_workspace_bytes, void* stream) {
+                                 void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
+                                 void* stream) {
   sva::clear_error();
   SVA_REQUIRE(q && q_proj && scale && codebooks && codes && q_low && lut && score_range,
               "sva_lookup_verify: null pointer");
@@ -630,7 +637,8 @@ extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stri
   bool fused = false;
   rc = summon_impl("sva_lookup_verify", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
                    k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride,
-                   sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused);
+                   sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused,
+                   floor_overshoot);
   if (rc != SVA_OK || fused) return rc;
   return sva_verify(q, q_dtype, 0, q_head_stride, 0, keys, values, kv_dtype, kv_head_stride, kv_row_stride, nullptr,
                     nullptr, n_keys, fin_idx, fin_count, 1, H, G, 1, D, B, scaling, out, out_dtype, 0, out_head_stride,

@@ -64,6 +64,12 @@ struct WideArgs {
   float* wg_rank;      // [items, W, WG_CAP] their rank scores
   int W;             // scan workgroups per item
   FusedVerify fv;    // fv.out != nullptr: the finish kernel also runs the verifier
+  int32_t* overshoot;  // [items] or nullptr: 1 where the sampled floor overshot (all-keys select), else 0
+  int items;           // items of the call
+  int K;               // slices of the all-keys select per item (finish grid: items * K workgroups)
+  uint32_t* arrive;    // [items] slices of the all-keys select completed (zeroed by the scan kernel)
+  uint32_t* slice_n;   // [items, K] entries of each slice list
+  uint64_t* slice_list;  // [items, K, L] each slice's top composites in key order
 };
 
 SVA_DEV uint32_t byte_of(const u32x4& v, int j) { return (v[j >> 2] >> (8 * (j & 3))) & 0xFFu; }
@@ -396,6 +402,8 @@ __global__ void __launch_bounds__(WB, S <= 4 ? 5 : 1) wide_scan_kernel(WideArgs 
   __shared__ ScanLds lds;
   const int item = blockIdx.x / a.W;
   const int w = blockIdx.x % a.W;
+  if (blockIdx.x == 0)  // arrival counters of the finish kernel's all-keys select
+    for (int i = threadIdx.x; i < a.items; i += WB) a.arrive[i] = 0u;
   if (!MASKED && (int64_t)(w + 1) * CHUNK <= a.p.N) {
     scan_chunk<S, SMALLC, false, false>(a, item, w, tab_lds, lds);
   } else {
@@ -948,7 +956,313 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
 //           over every key of the item, ranks computed here.
 // The last two are slower and give the same result.  The shortlist's rank
 // composites go to LDS in shortlist order for the budget.
-SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_t* kidl) {
+// ---------------------------------------------------------------------------
+// The all-keys select, for an item whose sampled floor overshot (fewer than
+// leff candidates at or above it): the item's keys are cut into a.K slices of
+// consecutive keys, one finish workgroup each (slice 0 is the item's own
+// workgroup, slices 1 .. K-1 extra workgroups of the grid that return at once
+// when the floor held).  Each slice writes its min(leff, allowed) largest
+// composites in key order to the workspace; the workgroup that completes the
+// item's last slice (a device-wide arrival counter, zeroed by the scan
+// kernel) selects the item's leff largest among the slices' lists (a superset
+// of them: no key outside a slice's top leff can be among the item's top
+// leff) and finishes the item.  No workgroup waits for another.
+//
+// A slice is selected in two passes over its codes, read as 16-byte words,
+// sixteen per thread in flight with every load instruction of a wave covering
+// 1 KB in a row, and scored from the table in LDS exactly as the scan scores
+// them:
+//   pass 1: histogram of the scores over 4096 bins linear in [lo, hi] (the
+//           bounds of any sum); b = the bin holding the k-th largest;
+//   pass 2: composites of higher bins (fewer than k) into a list, bin b's
+//           members (at most kOverBound) into LDS, sorted descending: the
+//           first `need` of them complete the list, which is then sorted into
+//           key order.
+// A boundary bin beyond kOverBound members (a tie class) falls back to the
+// radix select over the slice.
+constexpr int kOverBound = 4096;     // boundary-bin members sorted in LDS
+constexpr int kOverWords = 16;       // code words per thread in flight
+constexpr int kOverSlicesMax = 16;   // slices per item
+constexpr int kOverGrid = 256;       // items * slices at most (one workgroup per CU)
+constexpr size_t kOverList = kFinSl;                                    // uint64[FIN_MAX_L] slice list
+constexpr size_t kOverBnd = kOverList + sizeof(uint64_t) * FIN_MAX_L;   // uint64[kOverBound]
+static_assert(kOverBnd + sizeof(uint64_t) * kOverBound <= kFinSmall, "slice select LDS below the table");
+
+// Slices of the all-keys select for `items` items.
+int over_slices(int64_t items) { return (int)std::max<int64_t>(1, std::min<int64_t>(kOverSlicesMax, kOverGrid / items)); }
+
+// Keys per slice: a multiple of 16, so every slice starts on a 16-byte code word.
+SVA_DEV int slice_keys(int N, int K) { return ((((N + K - 1) / K) + 15) / 16) * 16; }
+
+// Composite <-> (key index, score key) in key-major order, for sorting by key.
+SVA_DEV uint64_t by_key(uint64_t x) { return ((uint64_t)composite_index(x) << 32) | (x >> 32); }
+SVA_DEV uint64_t from_key(uint64_t y) { return composite((uint32_t)y, (uint32_t)(y >> 32)); }
+
+// Calls f(key, composite) for every key of [n0, n1) (n0 a multiple of 16):
+// the exact scan score's composite, 0 for a key the mask excludes.
+template <int S, typename F>
+SVA_DEV void overshoot_visit(const SummonParams& p, const uint8_t* __restrict__ codes, const float* lut_l, int n0,
+                             int n1, F&& f) {
+#pragma clang fp contract(off)
+  constexpr int KPW = 16 / S;  // keys per 16-byte code word
+  const int C = p.C;
+  const uint32_t cm = (uint32_t)(C - 1);
+  const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
+  const int wbeg = n0 / KPW, wend = (n1 + KPW - 1) / KPW;
+  // word w0 + u * SB + t for u < kOverWords: every load instruction of a wave reads 1 KB in a row
+  for (int w0 = wbeg; w0 < wend; w0 += kOverWords * SB) {
+    u32x4 w[kOverWords];
+#pragma unroll
+    for (int u = 0; u < kOverWords; ++u) {
+      const int base = (w0 + u * SB + (int)threadIdx.x) * KPW;
+      if (base + KPW <= n1) {
+        w[u] = *reinterpret_cast<const u32x4*>(codes + (int64_t)base * S);
+      } else {
+        uint32_t wv[4] = {0u, 0u, 0u, 0u};
+        for (int j = 0; j < KPW * S; ++j)
+          if (base + j / S < n1) wv[j >> 2] |= (uint32_t)codes[(int64_t)base * S + j] << (8 * (j & 3));
+        w[u] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kOverWords; ++u) {
+      const int base = (w0 + u * SB + (int)threadIdx.x) * KPW;
+#pragma unroll
+      for (int j = 0; j < KPW; ++j) {
+        const int key = base + j;
+        if (key < n1) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) acc = acc + lut_l[s2 * C + min(byte_of(w[u], j * S + s2), cm)];
+          const bool ok = !masked || mask_allows(p.mask, key, p.mask_type);
+          f(key, ok ? composite(f2key(acc * kInvSqrtR), (uint32_t)key) : 0ull);
+        }
+      }
+    }
+  }
+}
+
+// Bitonic sort of P (a power of two) LDS elements in place, descending or ascending.
+template <typename T, bool DESC>
+SVA_DEV void lds_bitonic(T* a, int P) {
+  const int t = threadIdx.x;
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = t; i < P / 2; i += SB) {
+        const int lo_i = 2 * i - (i & (j - 1));  // index with bit j clear
+        const int hi_i = lo_i + j;
+        const bool desc = ((lo_i & k) == 0) == DESC;
+        const T x = a[lo_i], y = a[hi_i];
+        if ((x < y) == desc) {
+          a[lo_i] = y;
+          a[hi_i] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// The bin of the k-th largest of a 4096-bin histogram (block-wide).
+struct Boundary {
+  uint32_t k;      // min(k, total counted)
+  uint32_t b;      // the bin of the k-th largest (when k > 0)
+  uint32_t above;  // elements in higher bins (< k)
+  uint32_t cnt;    // elements in bin b
+};
+
+SVA_DEV Boundary hist_boundary(const uint32_t* hist, uint32_t k, uint32_t* scratch, uint32_t* shared) {
+  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  // thread t owns bins 4095 - 4 t - j, from the top
+  const uint4 hv = reinterpret_cast<const uint4*>(hist)[SB - 1 - t];
+  const uint32_t c[4] = {hv.w, hv.z, hv.y, hv.x};
+  const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+  const uint32_t incl = wave_incl_scan(mine);
+  if (lane == WAVE - 1) scratch[wid] = incl;
+  __syncthreads();
+  uint32_t a = incl - mine, total = 0u;
+  for (int v = 0; v < SNW; ++v) {
+    total += scratch[v];
+    if (v < wid) a += scratch[v];
+  }
+  const uint32_t kk = min(k, total);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (a < kk && a + c[j] >= kk) {
+      shared[1] = 4095u - 4u * (uint32_t)t - (uint32_t)j;
+      shared[2] = a;
+      shared[3] = c[j];
+    }
+    a += c[j];
+  }
+  __syncthreads();
+  const Boundary r{kk, shared[1], shared[2], shared[3]};
+  __syncthreads();
+  return r;
+}
+
+// Exact composite of key n (0 when masked out), scalar: the tie-class fallback's visitor.
+SVA_DEV uint64_t key_composite(const SummonParams& p, const uint8_t* codes, const float* lut_l, int n) {
+#pragma clang fp contract(off)
+  if (!mask_allows(p.mask, n, p.mask_type)) return 0ull;
+  // the reference's exact score ((0 + T0[c0]) + T1[c1]) + ... then / sqrt(R)
+  float acc = 0.0f;
+  for (int s2 = 0; s2 < p.S; ++s2) {
+    uint32_t c = codes[(int64_t)n * p.S + s2];
+    c = c < (uint32_t)p.C ? c : (uint32_t)(p.C - 1);
+    acc = acc + lut_l[s2 * p.C + c];
+  }
+  return composite(f2key(acc * kInvSqrtR), (uint32_t)n);
+}
+
+// The top min(k, allowed) composites of keys [n0, n1) of an item, in key
+// order, to out (global); returns their number (block-uniform).
+template <int S>
+SVA_DEV uint32_t slice_select(const SummonParams& p, int item, uint32_t k, int n0, int n1, const float* lut_l,
+                              unsigned char* lds, uint32_t* scratch, uint32_t* shared, uint64_t* shared64,
+                              uint64_t* __restrict__ out) {
+  const int t = threadIdx.x;
+  uint32_t* hist = (uint32_t*)(lds + kFinHist);
+  uint64_t* lst = (uint64_t*)(lds + kOverList);
+  uint64_t* bnd = (uint64_t*)(lds + kOverBnd);
+  const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)(item % p.H) * p.code_hs;
+  const float lo = p.range[4 * item] * kInvSqrtR, hi = p.range[4 * item + 1] * kInvSqrtR;
+  const float inv_w = lin_scale(lo, hi);
+  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  overshoot_visit<S>(p, codes, lut_l, n0, n1, [&](int, uint64_t x) {
+    if (x != 0ull) atomicAdd(&hist[lin_bin(key2f((uint32_t)(x >> 32)), lo, inv_w)], 1u);
+  });
+  __syncthreads();
+  const Boundary bd = hist_boundary(hist, k, scratch, shared);
+  if (bd.k == 0u) return 0u;
+  if (bd.cnt > (uint32_t)kOverBound) {
+    // a tie class beyond the LDS sort: radix passes over the slice, then its keys >= X in key order
+    uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
+    auto visit = [&](auto&& f) {
+      for (int n = n0 + t; n < n1; n += SB) {
+        const uint64_t x = key_composite(p, codes, lut_l, n);
+        if (x != 0ull) f(x);
+      }
+    };
+    const uint64_t X = select_largest<SB>(visit, (int)bd.k, whist, scratch, shared64, shared);
+    const int per = (n1 - n0 + SB - 1) / SB;
+    const int m0 = min(n1, n0 + t * per), m1 = min(n1, m0 + per);
+    uint32_t cnt = 0;
+    for (int n = m0; n < m1; ++n) cnt += key_composite(p, codes, lut_l, n) >= X;
+    uint32_t o = block_excl_scan<SB>(cnt, scratch, nullptr);
+    for (int n = m0; n < m1; ++n) {
+      const uint64_t x = key_composite(p, codes, lut_l, n);
+      if (x >= X && o < bd.k) out[o++] = x;
+    }
+    return bd.k;
+  }
+  if (t == 0) {
+    shared[0] = 0u;       // boundary-bin members
+    scratch[SNW] = 0u;    // higher-bin composites
+  }
+  __syncthreads();
+  overshoot_visit<S>(p, codes, lut_l, n0, n1, [&](int, uint64_t x) {
+    if (x == 0ull) return;
+    const uint32_t bin = (uint32_t)lin_bin(key2f((uint32_t)(x >> 32)), lo, inv_w);
+    if (bin > bd.b) lst[atomicAdd(&scratch[SNW], 1u)] = by_key(x);
+    else if (bin == bd.b) bnd[atomicAdd(&shared[0], 1u)] = x;
+  });
+  __syncthreads();
+  int P = 1;
+  while (P < (int)bd.cnt) P <<= 1;
+  for (int i = (int)bd.cnt + t; i < P; i += SB) bnd[i] = 0ull;
+  __syncthreads();
+  lds_bitonic<uint64_t, true>(bnd, P);
+  // the higher bins' composites, then the best `need` of the boundary bin, sorted by key
+  const uint32_t need = bd.k - bd.above;
+  for (int i = t; i < (int)need; i += SB) lst[bd.above + i] = by_key(bnd[i]);
+  int PL = 1;
+  while (PL < (int)bd.k) PL <<= 1;
+  for (int i = (int)bd.k + t; i < PL; i += SB) lst[i] = ~0ull;
+  __syncthreads();
+  lds_bitonic<uint64_t, false>(lst, PL);
+  for (int i = t; i < (int)bd.k; i += SB) out[i] = from_key(lst[i]);
+  return bd.k;
+}
+
+// The item's leff largest composites among its K slice lists (key order
+// within a list, lists in key-range order), as key indices in key order into
+// sl (LDS).  offs: LDS uint32[K + 1].
+SVA_DEV void merge_slices(const WideArgs& a, int item, uint32_t leff, unsigned char* lds, uint32_t* sl, uint32_t* offs,
+                          uint32_t* scratch, uint32_t* shared, uint64_t* shared64) {
+  const SummonParams& p = a.p;
+  const int t = threadIdx.x, K = a.K;
+  uint32_t* hist = (uint32_t*)(lds + kFinHist);
+  uint64_t* bnd = (uint64_t*)(lds + kOverBnd);
+  const uint64_t* lists = a.slice_list + (int64_t)item * K * p.L;
+  if (t == 0) {
+    uint32_t o = 0u;
+    for (int j = 0; j < K; ++j) {
+      offs[j] = o;
+      o += a.slice_n[(int64_t)item * K + j];
+    }
+    offs[K] = o;
+  }
+  __syncthreads();
+  const uint32_t U = offs[K];
+  auto visit = [&](auto&& f) {
+    for (int j = 0; j < K; ++j) {
+      const uint32_t n = offs[j + 1] - offs[j];
+      for (uint32_t e = t; e < n; e += SB) f(lists[(int64_t)j * p.L + e]);
+    }
+  };
+  uint64_t X = 1ull;  // every listed composite (U == leff)
+  if (U > leff) {
+    const float lo = p.range[4 * item] * kInvSqrtR, hi = p.range[4 * item + 1] * kInvSqrtR;
+    const float inv_w = lin_scale(lo, hi);
+    reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    visit([&](uint64_t x) { atomicAdd(&hist[lin_bin(key2f((uint32_t)(x >> 32)), lo, inv_w)], 1u); });
+    __syncthreads();
+    const Boundary bd = hist_boundary(hist, leff, scratch, shared);
+    if (bd.cnt > (uint32_t)kOverBound) {
+      X = select_largest<SB>(visit, (int)leff, (uint32_t(*)[256])hist, scratch, shared64, shared);
+    } else {
+      if (t == 0) shared[0] = 0u;
+      __syncthreads();
+      visit([&](uint64_t x) {
+        if ((uint32_t)lin_bin(key2f((uint32_t)(x >> 32)), lo, inv_w) == bd.b) bnd[atomicAdd(&shared[0], 1u)] = x;
+      });
+      __syncthreads();
+      int P = 1;
+      while (P < (int)bd.cnt) P <<= 1;
+      for (int i = (int)bd.cnt + t; i < P; i += SB) bnd[i] = 0ull;
+      __syncthreads();
+      lds_bitonic<uint64_t, true>(bnd, P);
+      X = bnd[leff - bd.above - 1];
+      __syncthreads();
+    }
+  }
+  // composites >= X in key order: thread t takes entries [t c, (t + 1) c) of the lists laid end to end
+  const uint32_t c = (U + SB - 1) / SB;
+  const uint32_t e0 = min(U, (uint32_t)t * c), e1 = min(U, e0 + c);
+  auto at = [&](uint32_t e, int& j) {
+    while (offs[j + 1] <= e) ++j;
+    return lists[(int64_t)j * p.L + (e - offs[j])];
+  };
+  uint32_t cnt = 0;
+  int j = 0;
+  for (uint32_t e = e0; e < e1; ++e) cnt += at(e, j) >= X;
+  uint32_t o = block_excl_scan<SB>(cnt, scratch, nullptr);
+  j = 0;
+  for (uint32_t e = e0; e < e1; ++e) {
+    const uint64_t x = at(e, j);
+    if (x >= X && o < leff) sl[o++] = composite_index(x);
+  }
+  __syncthreads();
+}
+
+// Finish of an item by slice `slice` of its finish workgroups: returns 1
+// (budget list in LDS) or 0 (in the budget output) when this workgroup
+// finished the item, -1 when it has nothing more to do (a slice workgroup
+// whose item's floor held, or that did not complete the item's last slice).
+SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* lds, int32_t* kidl) {
 #pragma clang fp contract(off)
   uint64_t* cl = (uint64_t*)lds;                                   // staged candidates [LDS_CAND]
   uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // overlays, once staging is done
@@ -964,7 +1278,7 @@ SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_
   uint32_t* loff = (uint32_t*)(lds + kFinLoff);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
-  if (finish_fast(a, item, lds, rkb, wcnt, scratch, tl, kidl)) return kidl != nullptr;
+  if (slice == 0 && finish_fast(a, item, lds, rkb, wcnt, scratch, tl, kidl)) return kidl != nullptr ? 1 : 0;
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int nsub = a.W * NW;
@@ -1005,11 +1319,12 @@ SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_
   const uint32_t longest = shared[1];
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
+  if (slice > 0 && (leff == 0 || M >= (uint32_t)leff)) return -1;  // the floor held: slice 0 finishes
   if (t == 0) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
   }
-  if (leff == 0) return false;
+  if (leff == 0) return 0;
   // bounds of every candidate composite: sums in [floor, upper bound of any sum]
   const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
   const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
@@ -1023,7 +1338,7 @@ SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_
       gather_lists<3>(cand, nsub, e3);
       finish_dense<3>(a, item, nsub, leff, beff, M, c_lo, c_hi, e3, lds, lcnt, loff, rkb, wcnt, scratch, tl);
     }
-    return false;
+    return 0;
   }
   uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;  // rank keys this thread emitted
   auto emit = [&](uint32_t o, uint64_t x, float rank) {
@@ -1131,45 +1446,38 @@ SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_
       __syncthreads();
     }
   } else {
-    // all keys: the sampled floor overshot
+    // all keys: the sampled floor overshot; this workgroup selects slice `slice`
     dense = false;
-    uint32_t(*whist)[256] = (uint32_t(*)[256])hist;
-    const int h = item % p.H;
-    const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
-    const int N = (int)p.N;
-    // the item's table in LDS: every pass below rescores every key from it
+    if (t == 0 && slice == 0 && a.overshoot != nullptr) a.overshoot[item] = 1;
+    const int N = (int)p.N, K = a.K;
+    // the item's table in LDS: the slice select scores every key of the slice from it
     float* lut_l = (float*)(lds + kFinLut);
     const float* lut_g = p.lut + (int64_t)item * p.S * p.C;
     for (int e = t; e < p.S * p.C; e += SB) lut_l[e] = lut_g[e];
     __syncthreads();
-    const int S = p.S, C = p.C;
-    auto key_at = [&](int n) -> uint64_t {
-      if (!mask_allows(p.mask, n, p.mask_type)) return 0ull;
-      // the reference's exact score ((0 + T0[c0]) + T1[c1]) + ... then / sqrt(R)
-      float acc = 0.0f;
-      for (int s2 = 0; s2 < S; ++s2) {
-        uint32_t c = codes[(int64_t)n * S + s2];
-        c = c < (uint32_t)C ? c : (uint32_t)(C - 1);
-        acc = acc + lut_l[s2 * C + c];
-      }
-      return composite(f2key(acc / p.sqrt_r), (uint32_t)n);
-    };
-    auto visit = [&](auto&& f) {
-      for (int n = t; n < N; n += SB) {
-        const uint64_t x = key_at(n);
-        if (x != 0ull) f(x);
-      }
-    };
-    const uint64_t X = (uint32_t)leff == A ? 1ull : select_largest<SB>(visit, leff, whist, scratch, shared64, shared);
-    const int per = (N + SB - 1) / SB;
-    const int n0 = min(N, t * per), n1 = min(N, n0 + per);
-    uint32_t cnt = 0;
-    for (int n = n0; n < n1; ++n) cnt += key_at(n) >= X;
-    uint32_t tot;
-    uint32_t o = block_excl_scan<SB>(cnt, scratch, &tot);
-    for (int n = n0; n < n1; ++n)
-      if (key_at(n) >= X && o < (uint32_t)leff) sl[o++] = (uint32_t)n;
+    const int per = slice_keys(N, K);
+    const int n0 = min(N, slice * per), n1 = min(N, n0 + per);
+    uint64_t* out = a.slice_list + ((int64_t)item * K + slice) * p.L;
+    uint32_t nj;
+    switch (p.S) {
+      case 1: nj = slice_select<1>(p, item, (uint32_t)leff, n0, n1, lut_l, lds, scratch, shared, shared64, out); break;
+      case 2: nj = slice_select<2>(p, item, (uint32_t)leff, n0, n1, lut_l, lds, scratch, shared, shared64, out); break;
+      case 4: nj = slice_select<4>(p, item, (uint32_t)leff, n0, n1, lut_l, lds, scratch, shared, shared64, out); break;
+      default: nj = slice_select<8>(p, item, (uint32_t)leff, n0, n1, lut_l, lds, scratch, shared, shared64, out); break;
+    }
+    // publish the slice (release), then count it in; the item's last slice finishes the item
+    if (t == 0) a.slice_n[(int64_t)item * K + slice] = nj;
+    __threadfence();
     __syncthreads();
+    if (t == 0) {
+      const uint32_t done = atomicAdd(&a.arrive[item], 1u);
+      __threadfence();
+      shared[0] = done == (uint32_t)(K - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (shared[0] == 0u) return -1;
+    __threadfence();  // acquire: the other slices' lists
+    merge_slices(a, item, (uint32_t)leff, lds, sl, lcnt, scratch, shared, shared64);
     rank_rows(p, item, sl, leff, (float*)rk);
   }
   // bounds of the emitted rank keys (direct and staged paths) for the budget select
@@ -1201,11 +1509,11 @@ SVA_DEV bool finish_item(const WideArgs& a, int item, unsigned char* lds, int32_
       vand &= e2[i];
     }
   }
-  if (p.B <= 0) return false;
+  if (p.B <= 0) return 0;
   const bool rb = dense && rkb[0] <= rkb[1];
   const uint64_t b_lo = (uint64_t)rkb[0] << 32, b_hi = ((uint64_t)rkb[1] << 32) | 0xFFFFFFFFull;
   finish_budget<NPB>(p, item, leff, beff, e2, rb ? b_hi : vor, rb ? b_lo : vand, rb, tl, wcnt, scratch);
-  return false;
+  return 0;
 }
 
 // The verifier of a decode item (query head h = item), run by its finish
@@ -1415,26 +1723,30 @@ SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, 
 // LDS the fused verifier needs when the list comes from the budget output.
 size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B + SNW * (size_t)(D + 2) + SNW + 1); }
 
-// Finish of an item, then (VD > 0: head_dim VD, K / V dtype VKV) its verifier.
+// Finish of an item, then (VD > 0: head_dim VD, K / V dtype VKV) its
+// verifier.  Workgroup g takes item g % items as slice g / items of the
+// all-keys select; slice 0 is the item's finish.
 template <int VD, int VKV>
 __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float qsh[VD > 0 ? VD : 1];  // the verifier's query row, requested before the finish starts
-  const int item = blockIdx.x;
+  const int item = blockIdx.x % a.items, slice = blockIdx.x / a.items;
   if (VD > 0 && (int)threadIdx.x < VD)
     qsh[threadIdx.x] = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
+  if (slice == 0 && threadIdx.x == 0 && a.overshoot != nullptr) a.overshoot[item] = 0;  // the all-keys select sets 1
   const bool keep = VD > 0 && a.p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
-  const bool in_lds = finish_item(a, item, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
+  const int done = finish_item(a, item, slice, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
+  if (done < 0) return;  // block-uniform
   if (VD > 0) {
     __syncthreads();  // the budget list (LDS or global) and the LDS the finish used
-    verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, in_lds, qsh);
+    verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, done == 1, qsh);
   }
 }
 
 template <int VD, int VKV>
 int launch_finish(const WideArgs& a, int64_t items, hipStream_t stream) {
   SVA_SET_MAX_LDS_ONCE((wide_finish_kernel<VD, VKV>), kFinLds, "hipFuncSetAttribute(wide_finish_kernel)");
-  hipLaunchKernelGGL((wide_finish_kernel<VD, VKV>), dim3((unsigned)items), dim3(SB), kFinLds, stream, a);
+  hipLaunchKernelGGL((wide_finish_kernel<VD, VKV>), dim3((unsigned)(items * a.K)), dim3(SB), kFinLds, stream, a);
   SVA_CHECK_LAUNCH("wide_finish_kernel");
   return SVA_OK;
 }
@@ -1483,6 +1795,7 @@ struct ClassArgs {
   uint32_t* counts;  // [items, W, 256] code histogram of each chunk's allowed keys
   uint32_t* bound;   // [items, 4]: boundary score key, its keys kept, shortlist length, 0
   uint32_t* woff;    // [items, W, 2]: shortlist offset of each chunk's keys, boundary keys in earlier chunks
+  int32_t* overshoot;  // [items] or nullptr: always 0 here (no sampled floor)
 };
 
 // Codes of thread t's keys cs + 64 t .. + 63 (a partial chunk reads bytes under a guard).
@@ -1680,6 +1993,7 @@ __global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
     a.bound[4 * item + 2] = (uint32_t)leff;
     a.bound[4 * item + 3] = 0u;
     p.sl_count[item] = leff;
+    if (a.overshoot != nullptr) a.overshoot[item] = 0;
   }
 }
 
@@ -1908,6 +2222,12 @@ int launch_wide_s(const WideArgs& a, int64_t items, bool masked, hipStream_t str
 // was written earlier in the same call, so no state is carried between calls
 // and calls of any shape can share one buffer.
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// the all-keys select's arrival counters, slice counts and slice lists
+size_t over_bytes(int64_t items, int64_t L) {
+  const int64_t K = over_slices(items);
+  return align256((size_t)items * sizeof(uint32_t)) + align256((size_t)(items * K) * sizeof(uint32_t)) +
+         align256((size_t)(items * K * L) * sizeof(uint64_t));
+}
 size_t counters_bytes(int64_t items, int64_t W) {
   return align256((size_t)(2 * items * W * NW) * sizeof(uint32_t)) + align256((size_t)(2 * items * W) * sizeof(uint32_t)) +
          align256((size_t)(items * W * WG_CAP) * (sizeof(uint64_t) + sizeof(float)));
@@ -1928,11 +2248,12 @@ bool summon_wide_eligible(const SummonParams& p, int64_t items) {
   return true;
 }
 
-size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t) {
+size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L) {
   const int64_t items = n_seq * H * Q;
   if (n_seq != 1 || Q != 1 || n_keys < kWideMinKeys || items > kMaxWideItems) return 256;
   const int64_t W = (n_keys + CHUNK - 1) / CHUNK;
-  return counters_bytes(items, W) + (size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float));
+  return counters_bytes(items, W) + align256((size_t)items * (size_t)W * CHUNK * (sizeof(uint64_t) + sizeof(float))) +
+         over_bytes(items, std::max<int64_t>(L, 1));
 }
 
 bool summon_class_eligible(const SummonParams& p, int64_t items) {
@@ -1941,7 +2262,7 @@ bool summon_class_eligible(const SummonParams& p, int64_t items) {
 }
 
 int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                      const FusedVerify* fv) {
+                      const FusedVerify* fv, int32_t* overshoot) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const int64_t W = (p.N + CLASS_CHUNK - 1) / CLASS_CHUNK;
   const size_t counts = align256((size_t)(items * W * 256) * sizeof(uint32_t));
@@ -1952,6 +2273,7 @@ int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_b
   ClassArgs a;
   a.p = p;
   a.W = (int)W;
+  a.overshoot = overshoot;
   a.fv = FusedVerify{};
   a.fv.out = nullptr;
   if (fv != nullptr) {
@@ -1976,7 +2298,7 @@ bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVeri
 }
 
 int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                     const FusedVerify* fv) {
+                     const FusedVerify* fv, int32_t* overshoot) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const size_t need = summon_wide_workspace_bytes(1, p.H, 1, p.N, p.L);
   SVA_REQUIRE(workspace != nullptr && workspace_bytes >= need && ((uintptr_t)workspace & 255u) == 0,
@@ -1984,6 +2306,7 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   WideArgs a;
   a.p = p;
   a.W = (int)((p.N + CHUNK - 1) / CHUNK);
+  a.overshoot = overshoot;
   a.fv = FusedVerify{};
   a.fv.out = nullptr;
   if (fv != nullptr) {
@@ -1998,6 +2321,14 @@ int summon_wide_path(const SummonParams& p, void* workspace, size_t workspace_by
   a.wg_rank = (float*)(a.wg_cand + items * a.W * WG_CAP);
   a.cand = (uint64_t*)(ws + counters_bytes(items, a.W));
   a.cand_rank = (float*)(ws + counters_bytes(items, a.W) + (size_t)items * (size_t)a.W * CHUNK * sizeof(uint64_t));
+  a.items = (int)items;
+  a.K = over_slices(items);
+  char* over = ws + counters_bytes(items, a.W) +
+               align256((size_t)items * (size_t)a.W * CHUNK * (sizeof(uint64_t) + sizeof(float)));
+  a.arrive = (uint32_t*)over;
+  a.slice_n = (uint32_t*)(over + align256((size_t)items * sizeof(uint32_t)));
+  a.slice_list = (uint64_t*)(over + align256((size_t)items * sizeof(uint32_t)) +
+                             align256((size_t)(items * a.K) * sizeof(uint32_t)));
   // a bool mask allows every key (the reference's `mask > -1e4` rule)
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
   switch (p.S) {

@@ -347,8 +347,10 @@ class ScanDecodePlan:
         self.rng = torch.empty(n_seq, heads, q_len, 4, device=self.device, dtype=f32)
         self.sl_idx = torch.empty(items, shortlist, device=self.device, dtype=i32)
         self.sl_rank = torch.empty(items, shortlist, device=self.device, dtype=f32)
-        self.counts = torch.empty(2, items, device=self.device, dtype=i32)  # shortlist and budget sizes
+        # shortlist and budget sizes, and 1 where the sampled floor overshot (one-call step only)
+        self.counts = torch.zeros(3, items, device=self.device, dtype=i32)
         self.sl_count = self.counts[0]
+        self.overshoot = self.counts[2]
         self.fin_idx = torch.empty(items, budget, device=self.device, dtype=i32)
         self.fin_count = self.counts[1]
         self._lib = lib()
@@ -426,7 +428,8 @@ class ScanDecodePlan:
                                   self.fin_count.data_ptr(), ws.data_ptr(), ws.numel(), keys.data_ptr(),
                                   values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1),
                                   keys.shape[0], float(scaling), out.data_ptr(), dtype_code(out), out.stride(1),
-                                  vws.data_ptr(), vws.numel(), stream), "sva_lookup_verify")
+                                  vws.data_ptr(), vws.numel(), self.overshoot.data_ptr(), stream),
+              "sva_lookup_verify")
         return out
 
     def _summon_ws(self, n_keys: int) -> torch.Tensor:

@@ -244,7 +244,8 @@ class SVALlamaAttention(nn.Module):
         out = plan.run(query, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks, codes, k_low, keys, values,
                        k_len, self.scaling)
         if self.stats is not None:
-            self.stats.add_device_rows(int(self.layer_idx or 0), (("summoned",), ("exact_scored", "verified")),
+            self.stats.add_device_rows(int(self.layer_idx or 0),
+                                       (("summoned",), ("exact_scored", "verified"), ("floor_overshoots",)),
                                        plan.counts, {"queries": float(heads)})
         return out
 

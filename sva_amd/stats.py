@@ -119,4 +119,6 @@ class SVAStats:
             out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_calls")
         for k in ("projection", "key_catalog", "outer_total"):
             out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_outer_calls")
+        # decode heads whose sampled shortlist floor overshot (the exact all-keys select ran); no reference key
+        out["floor_overshoots"] = self.totals.get("floor_overshoots", 0.0)
         return out

@@ -294,3 +294,49 @@ def test_class_path_single_subspace(device, N, C, L, B, few, masked):
         mask, allowed = torch.from_numpy(m).to(device), m[0, 0, 0] > -1e4
     fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B, mask=mask)
     _check_fused(codes, k_low, fused, split, q_low, lut, L, B, allowed=allowed)
+
+
+def test_overshoot_at_a_million_keys_is_exact_and_reported(device):
+    """The first key of every sampled block rigged to the best code of each subspace puts the sampled floor at
+    the top score, so only those 256 keys reach it (fewer than L = 2048): the finish's three-pass all-keys
+    select runs for every head.  The one-call decode step must still equal the oracle's shortlist, budget and
+    verified output, and report the overshoot per head; the same caches unrigged report none."""
+    from sva_amd import kernels
+
+    N, S, C, H, L, B = 1 << 20, 4, 64, 9, 2048, 512
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=31)
+    blocks = _sample_blocks(N, S)
+    ql = oracle.query_low(q, q_proj, scale)[:, 0]
+    rigged = codes.copy()
+    for h in range(H):
+        best = oracle.lut(ql[h], cb[h]).argmax(axis=1).astype(np.uint8)
+        for blk in range(blocks):
+            rigged[h, (blk * (N - 32) // (blocks - 1)) & ~15] = best
+    g = torch.Generator(device=device).manual_seed(32)
+    keys = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    qb = t(q)[None].to(torch.bfloat16)
+    for cds, expect in ((rigged, 1), (codes, 0)):
+        plan = kernels.ScanDecodePlan(device, 1, H, 1, 64, 64, S, C, L, B)
+        out = torch.empty(1, H, 1, 64, device=device, dtype=torch.float32)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        plan.run(qb, t(q_proj), t(scale), t(cb), t(cds), k_low, keys, values, N, 0.125, out=out)
+        ev[0].record()
+        plan.run(qb, t(q_proj), t(scale), t(cb), t(cds), k_low, keys, values, N, 0.125, out=out)
+        ev[1].record()
+        torch.cuda.synchronize()
+        print(f"overshoot={expect}: {1e3 * ev[0].elapsed_time(ev[1]):.1f} us per step", flush=True)
+        assert plan.overshoot.cpu().tolist() == [expect] * H
+        lut = plan.lut[0, :, 0].cpu().numpy()
+        _check(cds, k_low, plan.q_low[0, :, 0].cpu().numpy(), lut, plan.sl_idx.cpu().numpy(),
+               plan.sl_rank.cpu().numpy(), plan.sl_count.cpu().numpy(), L)
+        fin_idx, fin_count = plan.fin_idx.cpu().numpy(), plan.fin_count.cpu().numpy()
+        sl_idx, sl_rank = plan.sl_idx.cpu().numpy(), plan.sl_rank.cpu().numpy()
+        qf, kf, vf = qb.float().cpu().numpy()[0, :, 0], keys.float().cpu().numpy(), values.float().cpu().numpy()
+        got = out.cpu().numpy()[0, :, 0]
+        for h in range(H):
+            keep = oracle.topk(sl_rank[h, :L], B, key_index=sl_idx[h, :L])
+            np.testing.assert_array_equal(fin_idx[h, :fin_count[h]], np.sort(sl_idx[h, :L][keep]))
+            ref = oracle.verify(qf[h], kf[h // 3], vf[h // 3], np.sort(sl_idx[h, :L][keep]), 0.125)
+            assert np.abs(got[h] - ref).max() / np.abs(ref).max() <= 1e-5, f"head {h}"
