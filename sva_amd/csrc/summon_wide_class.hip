@@ -1,0 +1,188 @@
+// Code-class path of the long-context summon (one subspace of at most 256
+// codewords): the count, select and extract launches; the budget launch's
+// variants live with the finish kernels of their K / V dtype.
+#include "summon_wide.cuh"
+
+namespace sva {
+namespace wide {
+namespace {
+
+// Every phase keeps its loads in flight together: the counts were written
+// by workgroups on other XCDs, so each dependent round trip is long.
+__global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
+  __shared__ uint32_t key[256], tot[256], flags[256], part[CSEL_G][256], abv[CSEL_G][256], eqv[CSEL_G][256];
+  __shared__ uint32_t scratch[SNW + 1], res[4];
+  __shared__ uint32_t sa[CLASS_MAX_W], sb[CLASS_MAX_W];
+  const SummonParams& p = a.p;
+  const int item = blockIdx.x, t = threadIdx.x, W = a.W;
+  const int c = t & 255, g = t >> 8;
+  const uint32_t* cnt = a.counts + (int64_t)item * W * 256;
+  // code c's total: group g sums chunks g, g + CSEL_G, ..., 16 loads in flight at a time
+  {
+    uint32_t acc = 0;
+    for (int w0 = g; w0 < W; w0 += 16 * CSEL_G) {
+      uint32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int w = w0 + u * CSEL_G;
+        v[u] = w < W ? cnt[(int64_t)w * 256 + c] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc += v[u];
+    }
+    part[g][c] = acc;
+  }
+  if (t < 256) key[t] = class_key(p, item, t);
+  if (t == 0) {
+    res[0] = 0xFFFFFFFFu;  // no boundary class (empty shortlist): no key matches
+    res[1] = 0u;
+  }
+  __syncthreads();
+  if (t < 256) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int q = 0; q < CSEL_G; ++q) n += part[q][t];
+    tot[t] = n;
+  }
+  __syncthreads();
+  uint32_t A = 0;
+  for (int q = 0; q < 256; q += 64) A += tot[q + lane_id()];  // every wave sums all 256 totals
+  A = wave_sum_u32(A);
+  const int leff = (int)min((uint32_t)p.L, A);
+  // keys strictly above code c's class and in it: group g over codes [64 g, 64 g + 64)
+  {
+    const uint32_t k = key[c];
+    uint32_t above = 0, eq = 0;
+    for (int q = 64 * g; q < 64 * g + 64; ++q) {
+      const uint32_t kq = key[q], tq = tot[q];
+      above += kq > k ? tq : 0u;
+      eq += kq == k ? tq : 0u;
+    }
+    abv[g][c] = above;
+    eqv[g][c] = eq;
+  }
+  __syncthreads();
+  if (t < 256) {
+    uint32_t above = 0, eq = 0;
+#pragma unroll
+    for (int q = 0; q < CSEL_G; ++q) {
+      above += abv[q][t];
+      eq += eqv[q][t];
+    }
+    if (tot[t] > 0 && above < (uint32_t)leff && above + eq >= (uint32_t)leff) {
+      res[0] = key[t];  // every code of the boundary class writes the same values
+      res[1] = (uint32_t)leff - above;
+    }
+  }
+  __syncthreads();
+  const uint32_t kb = res[0], need = res[1];
+  if (t < 256) flags[t] = (key[t] > kb ? 1u : 0u) | (key[t] == kb ? 2u : 0u);
+  __syncthreads();
+  // per chunk: kept keys above the boundary class, keys of the boundary class; 16 lanes per chunk, each
+  // over 16 codes (four 16-byte loads issued together), summed over the lanes
+  {
+    const int q = t & 15;
+    uint32_t fl[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) fl[e] = flags[16 * q + e];
+    for (int w0 = 0; w0 < W; w0 += SB / 16) {
+      const int w = w0 + t / 16;
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        v[u] = w < W ? reinterpret_cast<const uint4*>(cnt + (int64_t)w * 256 + 16 * q)[u] : uint4{0u, 0u, 0u, 0u};
+      uint32_t x = 0, y = 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x += (fl[4 * u + e] & 1u) ? vv[e] : 0u;
+          y += (fl[4 * u + e] & 2u) ? vv[e] : 0u;
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        x += __shfl_xor(x, o, 16);
+        y += __shfl_xor(y, o, 16);
+      }
+      if (q == 0 && w < W) {
+        sa[w] = x;
+        sb[w] = y;
+      }
+    }
+  }
+  __syncthreads();
+  // thread t: chunks [t * CSEL_PER, (t + 1) * CSEL_PER); boundary keys before each, then its kept keys
+  const int w0 = t * CSEL_PER;
+  uint32_t bsum = 0;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) bsum += w0 + i < W ? sb[w0 + i] : 0u;
+  uint32_t bpre = block_excl_scan<SB>(bsum, scratch, nullptr);  // boundary keys in chunks before w0
+  uint32_t kept[CSEL_PER], ksum = 0;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) {
+    const int w = w0 + i;
+    kept[i] = 0u;
+    if (w < W) {
+      const uint32_t b = sb[w];
+      kept[i] = sa[w] + (need > bpre ? min(need - bpre, b) : 0u);
+      sb[w] = bpre;  // this thread's own chunks only
+      bpre += b;
+      ksum += kept[i];
+    }
+  }
+  uint32_t koff = block_excl_scan<SB>(ksum, scratch, nullptr);
+  uint32_t* wo = a.woff + (int64_t)item * W * 2;
+#pragma unroll
+  for (int i = 0; i < CSEL_PER; ++i) {
+    const int w = w0 + i;
+    if (w < W) {
+      wo[2 * w] = koff;
+      wo[2 * w + 1] = sb[w];
+      koff += kept[i];
+    }
+  }
+  if (t == 0) {
+    a.bound[4 * item] = kb;
+    a.bound[4 * item + 1] = need;
+    a.bound[4 * item + 2] = (uint32_t)leff;
+    a.bound[4 * item + 3] = 0u;
+    p.sl_count[item] = leff;
+    if (a.overshoot != nullptr) a.overshoot[item] = 0;
+  }
+}
+
+template <bool MASKED>
+int launch_class_m(const ClassArgs& a, int64_t items, hipStream_t stream) {
+  hipLaunchKernelGGL((class_count_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_count_kernel");
+  hipLaunchKernelGGL(class_select_kernel, dim3((unsigned)items), dim3(SB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_select_kernel");
+  hipLaunchKernelGGL((class_extract_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+  SVA_CHECK_LAUNCH("class_extract_kernel");
+  if (a.p.B <= 0) return SVA_OK;
+  if (a.fv.out == nullptr) return launch_class_budget_nov(a, items, stream);
+  const int kv = a.fv.kv_dtype;
+  if (a.fv.D == 64) {
+    if (kv == BF16) return launch_class_budget_v64_bf16(a, items, stream);
+    if (kv == F16) return launch_class_budget_v64_f16(a, items, stream);
+    return launch_class_budget_v64_f32(a, items, stream);
+  }
+  if (kv == BF16) return launch_class_budget_v128_bf16(a, items, stream);
+  if (kv == F16) return launch_class_budget_v128_f16(a, items, stream);
+  return launch_class_budget_v128_f32(a, items, stream);
+}
+
+}  // namespace
+
+int launch_class(const ClassArgs& a, int64_t items, bool masked, hipStream_t stream) {
+  return masked ? launch_class_m<true>(a, items, stream) : launch_class_m<false>(a, items, stream);
+}
+
+int launch_class_budget_nov(const ClassArgs& a, int64_t items, hipStream_t stream) {
+  return launch_class_budget<0, F32>(a, items, stream);
+}
+
+}  // namespace wide
+}  // namespace sva

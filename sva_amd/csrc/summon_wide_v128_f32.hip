@@ -1,0 +1,17 @@
+// Finish and class-budget kernels with the fused verifier: head_dim 128,
+// float32 K / V.
+#include "summon_wide.cuh"
+
+namespace sva {
+namespace wide {
+
+int launch_finish_v128_f32(const WideArgs& a, int64_t items, hipStream_t stream) {
+  return launch_finish<128, F32>(a, items, stream);
+}
+
+int launch_class_budget_v128_f32(const ClassArgs& a, int64_t items, hipStream_t stream) {
+  return launch_class_budget<128, F32>(a, items, stream);
+}
+
+}  // namespace wide
+}  // namespace sva
