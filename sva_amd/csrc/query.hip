@@ -9,34 +9,16 @@
 // score     = (((0 + lut[0][c0]) + lut[1][c1]) + ...) / sqrt(R)   (sva/ops.py:64-71)
 #include "capi_internal.h"
 #include "common.cuh"
+#include "query_decode.cuh"
 #include "summon.h"
 
 using namespace sva;
 
 namespace {
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int PREP_BLOCK = 1024;
 static_assert(SAMPLE_BINS == PREP_BLOCK, "one histogram bin per thread");
 
-struct LutParams {
-  const void* q;
-  int q_dtype;
-  int64_t q_bs, q_hs, q_ts;
-  int H, Q, D, R, S, C;
-  const float* q_proj;
-  const float* scale;
-  const float* codebooks;
-  float* q_low;
-  float* lut;
-  float* range;  // [items, 4]
-  const void* codes;  // optional uint8 codes: sample for the threshold estimate
-  int64_t code_hs;
-  int64_t n_keys;
-  int sample_blocks;  // blocks of SAMPLE_KEYS sampled keys (codes != nullptr)
-  int sample_k;       // rank of the floor among the sampled sums; 0: no floor
-};
 
 // One workgroup per query item.  The sampled codes and the head's weights
 // are staged in LDS in one round of loads; then q_low (one thread per
@@ -237,191 +219,11 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
   }
 }
 
-// Decode form (one token of one sequence, D = R = 64, uint8 codes, 16-byte
-// aligned code rows, 1x256, 2x256 or 4x64 codes): one 256-thread workgroup per
-// head with the layout's sizes at compile time.  The same arithmetic as query_lut_kernel (q_low and
-// table entries by sequential fma chains, bounds folded per subspace, the
-// floor from the same sample blocks and histogram), with the sampled code
-// words loaded 16 bytes at a time into registers and, for four subspaces,
-// pair tables so that a sampled sum takes two reads (the floor is only a
-// hint, so the pair sums' rounding does not matter there).
-constexpr int QD = 256;
-constexpr int QD_WORDS = 8;  // sampled 16-byte code words per thread (at most 32 KB per head)
-
+// Decode form: the body lives in query_decode.cuh (the code-class path runs
+// it in one grid with its code counts).
 template <int S, int CMAX>
 __global__ void __launch_bounds__(QD) query_decode_kernel(LutParams p) {
-#pragma clang fp contract(off)
-  constexpr int SUB = 64 / S;
-  constexpr int NPAIR = S >= 4 ? S / 2 : 0;
-  constexpr int EPT = (S * CMAX + QD - 1) / QD;  // table entries per thread
-  constexpr int KPW = 16 / S;                     // keys per 16-byte code word
-  __shared__ __align__(16) float W[64 * 64];
-  __shared__ float qf[64], ql[64];
-  __shared__ float tab[S * CMAX];
-  __shared__ float pairs[NPAIR > 0 ? NPAIR * 4096 : 1];
-  __shared__ uint32_t kmin[S], kmax[S];
-  __shared__ __align__(16) uint32_t hist[SAMPLE_BINS];
-  __shared__ uint32_t wsum[QD / WAVE], res[2];
-  const int h = blockIdx.x;
-  const int t = threadIdx.x;
-  const int lane = lane_id(), wid = t / WAVE;
-  const int C = p.C;
-  // 1. every load at once: map, query, codebook rows, sampled code words
-  float4 wv[4];
-  const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * 4096);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) wv[i] = w4[t + i * QD];
-  const float qv = t < 64 ? load_elem(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0.0f;
-  float4 row[EPT][SUB / 4];
-#pragma unroll
-  for (int k = 0; k < EPT; ++k) {
-    const int e = min(t + k * QD, S * C - 1);
-    const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB);
-#pragma unroll
-    for (int j = 0; j < SUB / 4; ++j) row[k][j] = c4[j];
-  }
-  const int k_rank = p.codes != nullptr ? p.sample_k : 0;
-  const int nb = p.sample_blocks;
-  const int n_words = nb * 2 * S;  // 32 keys x S bytes per block = 2 S words
-  const int64_t N = p.n_keys;
-  u32x4_t words[QD_WORDS];
-  if (k_rank > 0) {
-    const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
-#pragma unroll
-    for (int i = 0; i < QD_WORDS; ++i) {
-      const int gw = t + i * QD;
-      const int b = gw / (2 * S), wi = gw % (2 * S);
-      const int64_t n0 = ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15;
-      words[i] = gw < n_words ? *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16) : u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
-  const float sc = p.scale[h];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(W)[t + i * QD] = wv[i];
-  if (t < 64) qf[t] = qv;
-  if (t < S) {
-    kmin[t] = 0xFFFFFFFFu;
-    kmax[t] = 0u;
-  }
-  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
-  if (t == 0) res[0] = 0u;  // floor bin 0 unless the samples place it
-  __syncthreads();
-  // 2. q_low: one lane per output, a sequential fma chain over d
-  if (t < 64) {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int d = 0; d < 64; ++d) acc = __builtin_fmaf(qf[d], W[d * 64 + t], acc);
-    const float v = acc * sc;
-    ql[t] = v;
-    p.q_low[(int64_t)h * 64 + t] = v;
-  }
-  __syncthreads();
-  // 3. table entries (sequential fma chain over the subspace) and bounds
-  float* lut_out = p.lut + (int64_t)h * S * C;
-#pragma unroll
-  for (int k = 0; k < EPT; ++k) {
-    const int e = t + k * QD;
-    if (e < S * C) {
-      const int s = e / C;
-      const float* rr = reinterpret_cast<const float*>(row[k]);
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(ql[s * SUB + j], rr[j], acc);
-      tab[e] = acc;
-      lut_out[e] = acc;
-      atomicMin(&kmin[s], f2key(acc));
-      atomicMax(&kmax[s], f2key(acc));
-    }
-  }
-  __syncthreads();
-  float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    lo = lo + key2f(kmin[s]);
-    hi = hi + key2f(kmax[s]);
-  }
-  float t_lo = -INFINITY;
-  if (k_rank > 0 && hi > lo) {
-    const uint32_t cm = (uint32_t)(C - 1);
-    if (NPAIR > 0) {
-      // pair m: entry c0 + 64 c1 = T_{2m}[c0] + T_{2m+1}[c1]; thread t writes
-      // entries t + 256 r, whose c0 = t & 63 is its own and c1 = t / 64 + 4 r
-#pragma unroll
-      for (int m = 0; m < NPAIR; ++m) {
-        const float a0 = tab[2 * m * C + min((uint32_t)(t & 63), cm)];
-        float b[4096 / QD];
-#pragma unroll
-        for (int r = 0; r < 4096 / QD; ++r) b[r] = tab[(2 * m + 1) * C + min((uint32_t)((t >> 6) + 4 * r), cm)];
-#pragma unroll
-        for (int r = 0; r < 4096 / QD; ++r) pairs[m * 4096 + t + QD * r] = a0 + b[r];
-      }
-      __syncthreads();
-    }
-    // 4. sampled sums, kept in registers
-    float sums[QD_WORDS * KPW];
-#pragma unroll
-    for (int i = 0; i < QD_WORDS; ++i) {
-      const bool valid = t + i * QD < n_words;  // invalid words are zero: their reads stay in bounds
-#pragma unroll
-      for (int q = 0; q < KPW; ++q) {
-        float acc = 0.0f;
-        if (NPAIR > 0) {
-#pragma unroll
-          for (int m = 0; m < NPAIR; ++m) {
-            const int j = q * S + 2 * m;  // byte of subspace 2m
-            const uint32_t x = words[i][j >> 2] >> (8 * (j & 3));
-            const uint32_t c0 = min(x & 0xFFu, cm), c1 = min((x >> 8) & 0xFFu, cm);
-            const float v = pairs[m * 4096 + (c0 | (c1 << 6))];
-            acc = m == 0 ? v : acc + v;
-          }
-        } else {
-#pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) {
-            const int j = q * S + s2;
-            const uint32_t c = min((words[i][j >> 2] >> (8 * (j & 3))) & 0xFFu, cm);
-            acc = acc + tab[s2 * C + c];
-          }
-        }
-        sums[i * KPW + q] = valid ? acc : -INFINITY;
-      }
-    }
-    // every sum first, then every bin: an LDS atomic between two table reads
-    // would keep the reads from being issued together
-    const float base = lo;
-    const float inv_w = (float)SAMPLE_BINS / (hi - lo);
-#pragma unroll
-    for (int i = 0; i < QD_WORDS * KPW; ++i) {
-      if (sums[i] != -INFINITY) {
-        int bin = (int)((sums[i] - lo) * inv_w);
-        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
-        atomicAdd(&hist[bin], 1u);
-      }
-    }
-    __syncthreads();
-    // 5. the bin of the k-th largest sampled sum: thread t owns bins 1023 - 4 t - j
-    const uint4 hv = reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - t];
-    const uint32_t c[4] = {hv.w, hv.z, hv.y, hv.x};
-    const uint32_t mine = c[0] + c[1] + c[2] + c[3];
-    const uint32_t incl = wave_incl_scan(mine);
-    if (lane == WAVE - 1) wsum[wid] = incl;
-    __syncthreads();
-    uint32_t a = incl - mine;
-    for (int v = 0; v < wid; ++v) a += wsum[v];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (a < (uint32_t)k_rank && a + c[j] >= (uint32_t)k_rank) res[0] = (uint32_t)(SAMPLE_BINS - 1 - 4 * t - j);
-      a += c[j];
-    }
-    __syncthreads();
-    t_lo = base + (float)res[0] / inv_w;
-  }
-  if (t == 0) {
-    float* rg = p.range + (int64_t)h * 4;
-    rg[0] = lo;
-    rg[1] = hi;
-    rg[2] = t_lo;
-    rg[3] = 0.0f;
-  }
+  query_decode_item<S, CMAX>(p, (int)blockIdx.x);
 }
 
 // Many query tokens per head (prefill): one workgroup per MT consecutive
@@ -567,12 +369,13 @@ size_t lut_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C, int sample_bloc
 
 }  // namespace
 
-extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride,
-                             int64_t q_tok_stride, int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R,
-                             int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
-                             const void* codes, int code_type, int64_t code_head_stride, int64_t n_keys,
-                             int64_t shortlist, float* q_low, float* lut, float* score_range, void* stream) {
-  sva::clear_error();
+namespace sva {
+
+int query_lut_setup(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride, int64_t q_tok_stride,
+                    int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R, int64_t S, int64_t C,
+                    const float* q_proj, const float* scale, const float* codebooks, const void* codes, int code_type,
+                    int64_t code_head_stride, int64_t n_keys, int64_t shortlist, float* q_low, float* lut,
+                    float* score_range, QueryLaunch* out) {
   SVA_REQUIRE(q && q_proj && scale && codebooks && q_low && lut && score_range, "sva_query_lut: null pointer");
   SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0, "sva_query_lut: empty query batch");
   SVA_REQUIRE(D > 0 && D <= 512 && R > 0 && R <= 512, "sva_query_lut: head_dim %lld / rank %lld out of range",
@@ -600,8 +403,7 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_query_lut: head weights of %zu bytes exceed LDS", lds);
   const int64_t items = n_seq * H * Q;
   SVA_REQUIRE(items < (1ll << 31), "sva_query_lut: too many query items");
-  SVA_SET_MAX_LDS_ONCE(query_lut_kernel, sva::kMaxLds, "hipFuncSetAttribute(query_lut_kernel)");
-  LutParams p;
+  LutParams& p = out->p;
   p.q = q;
   p.q_dtype = q_dtype;
   p.q_bs = q_seq_stride;
@@ -624,40 +426,75 @@ extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, i
   p.n_keys = n_keys;
   p.sample_blocks = blocks;
   p.sample_k = sample_k;
+  out->form = QUERY_GENERAL;
+  out->blocks = items;
+  out->lds = lds;
   // many tokens per head: the head's weights are staged once per MT tokens
   const int64_t sub = R / S;
   const size_t mlds = sizeof(float) * (size_t)(D * R + MT * D + MT * R) + sizeof(uint32_t) * (size_t)(2 * MT * S);
   if (Q >= 8 && !sample && (sub == 16 || sub == 32 || sub == 64) && mlds <= (size_t)sva::kMaxLds) {
-    const int64_t blocks = n_seq * H * ((Q + MT - 1) / MT);
-    if (sub == 16) return launch_lut_multi<16>(p, blocks, mlds, (hipStream_t)stream);
-    if (sub == 32) return launch_lut_multi<32>(p, blocks, mlds, (hipStream_t)stream);
-    return launch_lut_multi<64>(p, blocks, mlds, (hipStream_t)stream);
+    out->form = sub == 16 ? QUERY_MULTI16 : (sub == 32 ? QUERY_MULTI32 : QUERY_MULTI64);
+    out->blocks = n_seq * H * ((Q + MT - 1) / MT);
+    out->lds = mlds;
+    return SVA_OK;
   }
   // one token of one sequence at D = R = 64: the decode form
   const bool aligned = ((uintptr_t)q_proj & 15u) == 0 && ((uintptr_t)codebooks & 15u) == 0 &&
                        (!sample || (((uintptr_t)codes & 15u) == 0 && code_head_stride % 16 == 0));
-  if (n_seq == 1 && Q == 1 && D == 64 && R == 64 && aligned && (!sample || blocks * SAMPLE_KEYS * S <= QD * QD_WORDS * 16)) {
-    const dim3 grid((unsigned)H), block(QD);
-    const hipStream_t st = (hipStream_t)stream;
-    if (S == 4 && C <= 64) {
-      hipLaunchKernelGGL((query_decode_kernel<4, 64>), grid, block, 0, st, p);
-      SVA_CHECK_LAUNCH("query_decode_kernel");
-      return SVA_OK;
-    }
-    if (S == 2 && C <= 256) {
-      hipLaunchKernelGGL((query_decode_kernel<2, 256>), grid, block, 0, st, p);
-      SVA_CHECK_LAUNCH("query_decode_kernel");
-      return SVA_OK;
-    }
-    if (S == 1 && C <= 256) {
-      hipLaunchKernelGGL((query_decode_kernel<1, 256>), grid, block, 0, st, p);
-      SVA_CHECK_LAUNCH("query_decode_kernel");
-      return SVA_OK;
+  if (n_seq == 1 && Q == 1 && D == 64 && R == 64 && aligned && (!sample || blocks * SAMPLE_KEYS * S <= QD * 16 * (S == 4 ? qd_words<4>() : S == 2 ? qd_words<2>() : qd_words<1>()))) {
+    const int form = S == 4 && C <= 64 ? QUERY_DECODE_4_64
+                     : S == 2 && C <= 256 ? QUERY_DECODE_2_256
+                     : S == 1 && C <= 256 ? QUERY_DECODE_1_256
+                                          : QUERY_GENERAL;
+    if (form != QUERY_GENERAL) {
+      out->form = form;
+      out->blocks = H;
+      out->lds = 0;
     }
   }
-  hipLaunchKernelGGL(query_lut_kernel, dim3((unsigned)items), dim3(PREP_BLOCK), lds, (hipStream_t)stream, p);
-  SVA_CHECK_LAUNCH("query_lut_kernel");
   return SVA_OK;
+}
+
+int query_lut_launch(const QueryLaunch& ql, hipStream_t st) {
+  const LutParams& p = ql.p;
+  switch (ql.form) {
+    case QUERY_MULTI16: return launch_lut_multi<16>(p, ql.blocks, ql.lds, st);
+    case QUERY_MULTI32: return launch_lut_multi<32>(p, ql.blocks, ql.lds, st);
+    case QUERY_MULTI64: return launch_lut_multi<64>(p, ql.blocks, ql.lds, st);
+    case QUERY_DECODE_4_64:
+      hipLaunchKernelGGL((query_decode_kernel<4, 64>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      SVA_CHECK_LAUNCH("query_decode_kernel");
+      return SVA_OK;
+    case QUERY_DECODE_2_256:
+      hipLaunchKernelGGL((query_decode_kernel<2, 256>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      SVA_CHECK_LAUNCH("query_decode_kernel");
+      return SVA_OK;
+    case QUERY_DECODE_1_256:
+      hipLaunchKernelGGL((query_decode_kernel<1, 256>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      SVA_CHECK_LAUNCH("query_decode_kernel");
+      return SVA_OK;
+    default:
+      SVA_SET_MAX_LDS_ONCE(query_lut_kernel, sva::kMaxLds, "hipFuncSetAttribute(query_lut_kernel)");
+      hipLaunchKernelGGL(query_lut_kernel, dim3((unsigned)ql.blocks), dim3(PREP_BLOCK), ql.lds, st, p);
+      SVA_CHECK_LAUNCH("query_lut_kernel");
+      return SVA_OK;
+  }
+}
+
+}  // namespace sva
+
+extern "C" int sva_query_lut(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_head_stride,
+                             int64_t q_tok_stride, int64_t n_seq, int64_t H, int64_t Q, int64_t D, int64_t R,
+                             int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
+                             const void* codes, int code_type, int64_t code_head_stride, int64_t n_keys,
+                             int64_t shortlist, float* q_low, float* lut, float* score_range, void* stream) {
+  sva::clear_error();
+  sva::QueryLaunch ql;
+  const int rc = sva::query_lut_setup(q, q_dtype, q_seq_stride, q_head_stride, q_tok_stride, n_seq, H, Q, D, R, S, C,
+                                      q_proj, scale, codebooks, codes, code_type, code_head_stride, n_keys, shortlist,
+                                      q_low, lut, score_range, &ql);
+  if (rc != SVA_OK) return rc;
+  return sva::query_lut_launch(ql, (hipStream_t)stream);
 }
 
 extern "C" int sva_pq_scores(const float* lut, const void* codes, int code_type, int64_t code_head_stride,

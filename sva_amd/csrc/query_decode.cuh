@@ -1,0 +1,220 @@
+#pragma once
+// Decode form of the query kernel (one token, one sequence, D = R = 64),
+// shared by the query launch and the code-class path's fused launch.
+#include "common.cuh"
+#include "query.h"
+#include "summon.h"
+
+namespace sva {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Decode form (one token of one sequence, D = R = 64, uint8 codes, 16-byte
+// aligned code rows, 1x256, 2x256 or 4x64 codes): one 256-thread workgroup per
+// head with the layout's sizes at compile time.  The same arithmetic as query_lut_kernel (q_low and
+// table entries by sequential fma chains, bounds folded per subspace, the
+// floor from the same sample blocks and histogram), with the sampled code
+// words loaded 16 bytes at a time into registers and, for four subspaces,
+// pair tables so that a sampled sum takes two reads (the floor is only a
+// hint, so the pair sums' rounding does not matter there).
+constexpr int QD = 256;
+constexpr int QD_WORDS = 8;  // sampled 16-byte code words per thread (at most 32 KB per head)
+// Sampled code words a thread holds for S subspaces: at most SAMPLE_MAX_BLOCKS
+// blocks of SAMPLE_KEYS keys, S bytes each, over QD threads.
+template <int S>
+constexpr int qd_words() {
+  return SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / QD < QD_WORDS ? SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / QD
+                                                                    : QD_WORDS;
+}
+
+template <int S, int CMAX>
+SVA_DEV void query_decode_item(const LutParams& p, int h) {
+#pragma clang fp contract(off)
+  constexpr int SUB = 64 / S;
+  constexpr int NPAIR = S >= 4 ? S / 2 : 0;
+  constexpr int EPT = (S * CMAX + QD - 1) / QD;  // table entries per thread
+  constexpr int KPW = 16 / S;                     // keys per 16-byte code word
+  __shared__ __align__(16) float W[64 * 64];
+  __shared__ float qf[64], ql[64];
+  __shared__ float tab[S * CMAX];
+  __shared__ float pairs[NPAIR > 0 ? NPAIR * 4096 : 1];
+  __shared__ uint32_t kmin[S], kmax[S];
+  __shared__ __align__(16) uint32_t hist[SAMPLE_BINS];
+  __shared__ uint32_t wsum[QD / WAVE], res[2];
+  const int t = threadIdx.x;
+  const int lane = lane_id(), wid = t / WAVE;
+  const int C = p.C;
+  // 1. every load at once: map, query, codebook rows, sampled code words
+  float4 wv[4];
+  const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * 4096);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wv[i] = w4[t + i * QD];
+  const float qv = t < 64 ? load_elem(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0.0f;
+  float4 row[EPT][SUB / 4];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = min(t + k * QD, S * C - 1);
+    const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB);
+#pragma unroll
+    for (int j = 0; j < SUB / 4; ++j) row[k][j] = c4[j];
+  }
+  const int k_rank = p.codes != nullptr ? p.sample_k : 0;
+  const int nb = p.sample_blocks;
+  const int n_words = nb * 2 * S;  // 32 keys x S bytes per block = 2 S words
+  const int64_t N = p.n_keys;
+  constexpr int QW = qd_words<S>();
+  u32x4_t words[QW];
+  if (k_rank > 0) {
+    const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+#pragma unroll
+    for (int i = 0; i < QW; ++i) {
+      const int gw = t + i * QD;
+      const int b = gw / (2 * S), wi = gw % (2 * S);
+      const int64_t n0 = ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15;
+      words[i] = gw < n_words ? *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  const float sc = p.scale[h];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(W)[t + i * QD] = wv[i];
+  if (t < 64) qf[t] = qv;
+  if (t < S) {
+    kmin[t] = 0xFFFFFFFFu;
+    kmax[t] = 0u;
+  }
+  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+  if (t == 0) res[0] = 0u;  // floor bin 0 unless the samples place it
+  __syncthreads();
+  // 2. q_low: one lane per output, a sequential fma chain over d
+  if (t < 64) {
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int d = 0; d < 64; ++d) acc = __builtin_fmaf(qf[d], W[d * 64 + t], acc);
+    const float v = acc * sc;
+    ql[t] = v;
+    p.q_low[(int64_t)h * 64 + t] = v;
+  }
+  __syncthreads();
+  // 3. table entries (sequential fma chain over the subspace) and bounds;
+  // with C a multiple of 64 every wave's entries share a subspace, so the
+  // bounds fold over the wave first (one atomic per wave, not per entry)
+  float* lut_out = p.lut + (int64_t)h * S * C;
+  const bool wave_sub = C % WAVE == 0;
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    const int e = t + k * QD;
+    const int s = min(e, S * C - 1) / C;
+    uint32_t kl = 0xFFFFFFFFu, kh = 0u;
+    if (e < S * C) {
+      const float* rr = reinterpret_cast<const float*>(row[k]);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(ql[s * SUB + j], rr[j], acc);
+      tab[e] = acc;
+      lut_out[e] = acc;
+      kl = kh = f2key(acc);
+      if (!wave_sub) {
+        atomicMin(&kmin[s], kl);
+        atomicMax(&kmax[s], kh);
+      }
+    }
+    if (wave_sub && k * QD + WAVE * wid < S * C) {  // uniform: the wave's entries exist
+      wave_min_max_u32(kl, kh);
+      if (lane == 0) {
+        atomicMin(&kmin[s], kl);
+        atomicMax(&kmax[s], kh);
+      }
+    }
+  }
+  __syncthreads();
+  float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    lo = lo + key2f(kmin[s]);
+    hi = hi + key2f(kmax[s]);
+  }
+  float t_lo = -INFINITY;
+  if (k_rank > 0 && hi > lo) {
+    const uint32_t cm = (uint32_t)(C - 1);
+    if (NPAIR > 0) {
+      // pair m: entry c0 + 64 c1 = T_{2m}[c0] + T_{2m+1}[c1]; thread t writes
+      // entries t + 256 r, whose c0 = t & 63 is its own and c1 = t / 64 + 4 r
+#pragma unroll
+      for (int m = 0; m < NPAIR; ++m) {
+        const float a0 = tab[2 * m * C + min((uint32_t)(t & 63), cm)];
+        float b[4096 / QD];
+#pragma unroll
+        for (int r = 0; r < 4096 / QD; ++r) b[r] = tab[(2 * m + 1) * C + min((uint32_t)((t >> 6) + 4 * r), cm)];
+#pragma unroll
+        for (int r = 0; r < 4096 / QD; ++r) pairs[m * 4096 + t + QD * r] = a0 + b[r];
+      }
+      __syncthreads();
+    }
+    // 4. sampled sums, kept in registers
+    float sums[QW * KPW];
+#pragma unroll
+    for (int i = 0; i < QW; ++i) {
+      const bool valid = t + i * QD < n_words;  // invalid words are zero: their reads stay in bounds
+#pragma unroll
+      for (int q = 0; q < KPW; ++q) {
+        float acc = 0.0f;
+        if (NPAIR > 0) {
+#pragma unroll
+          for (int m = 0; m < NPAIR; ++m) {
+            const int j = q * S + 2 * m;  // byte of subspace 2m
+            const uint32_t x = words[i][j >> 2] >> (8 * (j & 3));
+            const uint32_t c0 = min(x & 0xFFu, cm), c1 = min((x >> 8) & 0xFFu, cm);
+            const float v = pairs[m * 4096 + (c0 | (c1 << 6))];
+            acc = m == 0 ? v : acc + v;
+          }
+        } else {
+#pragma unroll
+          for (int s2 = 0; s2 < S; ++s2) {
+            const int j = q * S + s2;
+            const uint32_t c = min((words[i][j >> 2] >> (8 * (j & 3))) & 0xFFu, cm);
+            acc = acc + tab[s2 * C + c];
+          }
+        }
+        sums[i * KPW + q] = valid ? acc : -INFINITY;
+      }
+    }
+    // every sum first, then every bin: an LDS atomic between two table reads
+    // would keep the reads from being issued together
+    const float base = lo;
+    const float inv_w = (float)SAMPLE_BINS / (hi - lo);
+#pragma unroll
+    for (int i = 0; i < QW * KPW; ++i) {
+      if (sums[i] != -INFINITY) {
+        int bin = (int)((sums[i] - lo) * inv_w);
+        bin = bin < 0 ? 0 : (bin >= SAMPLE_BINS ? SAMPLE_BINS - 1 : bin);
+        atomicAdd(&hist[bin], 1u);
+      }
+    }
+    __syncthreads();
+    // 5. the bin of the k-th largest sampled sum: thread t owns bins 1023 - 4 t - j
+    const uint4 hv = reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - t];
+    const uint32_t c[4] = {hv.w, hv.z, hv.y, hv.x};
+    const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+    const uint32_t incl = wave_incl_scan(mine);
+    if (lane == WAVE - 1) wsum[wid] = incl;
+    __syncthreads();
+    uint32_t a = incl - mine;
+    for (int v = 0; v < wid; ++v) a += wsum[v];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (a < (uint32_t)k_rank && a + c[j] >= (uint32_t)k_rank) res[0] = (uint32_t)(SAMPLE_BINS - 1 - 4 * t - j);
+      a += c[j];
+    }
+    __syncthreads();
+    t_lo = base + (float)res[0] / inv_w;
+  }
+  if (t == 0) {
+    float* rg = p.range + (int64_t)h * 4;
+    rg[0] = lo;
+    rg[1] = hi;
+    rg[2] = t_lo;
+    rg[3] = 0.0f;
+  }
+}
+
+}  // namespace sva

@@ -48,6 +48,8 @@ __host__ __device__ inline int sample_floor_rank(int64_t L, int64_t n_keys, int 
   return k < n_samples / 2 ? k : 0;
 }
 
+struct QueryLaunch;  // query.h: a prepared query launch the class path may fuse
+
 struct SummonParams {
   const float* lut;    // [items, S*C]
   const float* range;  // [items, 4]: bounds of any scan sum, sampled floor, 0
@@ -111,7 +113,8 @@ constexpr int CLASS_MAX_L = 7168;
 inline bool class_shape(int64_t S, int64_t C, int64_t L) { return S == 1 && C <= 256 && L <= CLASS_MAX_L; }
 bool summon_class_eligible(const SummonParams& p, int64_t items);
 int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                      const FusedVerify* fv = nullptr, int32_t* overshoot = nullptr);
+                      const FusedVerify* fv = nullptr, int32_t* overshoot = nullptr,
+                      const QueryLaunch* query = nullptr);
 // Whether summon_wide_path can run `fv` in its finish kernel for these sizes.
 bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv);
 size_t summon_wide_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L);

@@ -18,6 +18,7 @@
 
 #include "capi_internal.h"
 #include "common.cuh"
+#include "query.h"
 #include "summon.h"
 
 using namespace sva;
@@ -467,7 +468,8 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 int64_t n_keys, int64_t R, int64_t S, int64_t C, int64_t L, const void* mask, int mask_type,
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
                 int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
-                const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr) {
+                const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr,
+                const sva::QueryLaunch* query = nullptr) {
   if (fused != nullptr) *fused = false;
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
@@ -512,15 +514,24 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   p.B = (int)B;
   p.fin_idx = fin_idx;
   p.fin_count = fin_count;
+  // a prepared query launch (the tables this call reads): the code-class
+  // path runs its decode form in one grid with the code counts; every other
+  // path launches it first
+  const bool class_path = n_keys > 0 && sva::summon_class_eligible(p, items);
+  if (query != nullptr && !(class_path && query->form == sva::QUERY_DECODE_1_256)) {
+    const int rc = sva::query_lut_launch(*query, (hipStream_t)stream);
+    if (rc != SVA_OK) return rc;
+    query = nullptr;
+  }
   if (n_keys == 0) {
     int rc = sva::fill_i32(sl_count, items, 0, (hipStream_t)stream);
     if (rc == SVA_OK && B > 0) rc = sva::fill_i32(fin_count, items, 0, (hipStream_t)stream);
     return rc;
   }
-  if (sva::summon_class_eligible(p, items)) {
+  if (class_path) {
     const bool with_fv = fv != nullptr && sva::fused_verify_eligible(p, items, *fv);
     const int rc = sva::summon_class_path(p, workspace, workspace_bytes, (hipStream_t)stream, with_fv ? fv : nullptr,
-                                          overshoot);
+                                          overshoot, query);
     if (rc == SVA_OK && fused != nullptr) *fused = with_fv;
     return rc;
   }
@@ -586,12 +597,14 @@ extern "C" int sva_lookup_select(const void* q, int q_dtype, int64_t q_head_stri
   SVA_REQUIRE(fin_idx && fin_count, "sva_lookup_select: null pointer");
   SVA_REQUIRE(B > 0 && B <= 8192, "sva_lookup_select: budget %lld out of range (1..8192)", (long long)B);
   SVA_REQUIRE(H > 0 && n_keys >= 0 && L > 0, "sva_lookup_select: bad sizes");
-  const int rc = sva_query_lut(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
-                               code_type, code_head_stride, n_keys, L, q_low, lut, score_range, stream);
+  sva::QueryLaunch ql;
+  const int rc = sva::query_lut_setup(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks,
+                                      codes, code_type, code_head_stride, n_keys, L, q_low, lut, score_range, &ql);
   if (rc != SVA_OK) return rc;
-  return sva_summon_select(lut, score_range, q_low, codes, code_type, code_head_stride, k_low, k_low_head_stride,
-                           nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride, sl_idx,
-                           sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream);
+  return summon_impl("sva_lookup_select", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
+                     k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type,
+                     mask_tok_stride, sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes,
+                     stream, nullptr, nullptr, nullptr, &ql);
 }
 
 extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
@@ -613,8 +626,9 @@ extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stri
   SVA_REQUIRE(H > 0 && G > 0 && H % G == 0 && n_keys > 0 && L > 0, "sva_lookup_verify: bad sizes");
   SVA_REQUIRE(q_dtype >= 0 && q_dtype <= 2 && kv_dtype >= 0 && kv_dtype <= 2 && out_dtype >= 0 && out_dtype <= 2,
               "sva_lookup_verify: bad dtype");
-  int rc = sva_query_lut(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
-                         code_type, code_head_stride, n_keys, L, q_low, lut, score_range, stream);
+  sva::QueryLaunch ql;
+  int rc = sva::query_lut_setup(q, q_dtype, 0, q_head_stride, 0, 1, H, 1, D, R, S, C, q_proj, scale, codebooks, codes,
+                                code_type, code_head_stride, n_keys, L, q_low, lut, score_range, &ql);
   if (rc != SVA_OK) return rc;
   sva::FusedVerify fv{};
   fv.q = q;
@@ -638,7 +652,7 @@ extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stri
   rc = summon_impl("sva_lookup_verify", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
                    k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride,
                    sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused,
-                   floor_overshoot);
+                   floor_overshoot, &ql);
   if (rc != SVA_OK || fused) return rc;
   return sva_verify(q, q_dtype, 0, q_head_stride, 0, keys, values, kv_dtype, kv_head_stride, kv_row_stride, nullptr,
                     nullptr, n_keys, fin_idx, fin_count, 1, H, G, 1, D, B, scaling, out, out_dtype, 0, out_head_stride,

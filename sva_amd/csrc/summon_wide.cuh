@@ -38,6 +38,7 @@
 
 #include "capi_internal.h"
 #include "common.cuh"
+#include "query.h"
 #include "summon.h"
 
 namespace sva {
@@ -1810,10 +1811,10 @@ SVA_DEV uint32_t class_key(const SummonParams& p, int item, int c) {
 }
 
 template <bool MASKED>
-__global__ void __launch_bounds__(WB) class_count_kernel(ClassArgs a) {
+SVA_DEV void class_count_chunk(const ClassArgs& a, int block) {
   __shared__ uint32_t hist[NW][256];
   const SummonParams& p = a.p;
-  const int item = blockIdx.x / a.W, w = blockIdx.x % a.W;
+  const int item = block / a.W, w = block % a.W;
   const int t = threadIdx.x, wid = t / WAVE;
   const int cs = w * CLASS_CHUNK, ce = (int)min((int64_t)cs + CLASS_CHUNK, p.N);
   const int k0 = cs + t * CK_PT;
@@ -1835,6 +1836,11 @@ __global__ void __launch_bounds__(WB) class_count_kernel(ClassArgs a) {
   }
   __syncthreads();
   a.counts[((int64_t)item * a.W + w) * 256 + t] = hist[0][t] + hist[1][t] + hist[2][t] + hist[3][t];
+}
+
+template <bool MASKED>
+__global__ void __launch_bounds__(WB) class_count_kernel(ClassArgs a) {
+  class_count_chunk<MASKED>(a, (int)blockIdx.x);
 }
 
 constexpr int CSEL_PER = CLASS_MAX_W / SB;  // chunks per thread of class_select (prefix sums)
@@ -2053,7 +2059,7 @@ int launch_class_budget(const ClassArgs& a, int64_t items, hipStream_t stream) {
 // Launchers, defined one translation unit per kernel family or verifier
 // variant (head_dim, K / V dtype) so that the variants compile in parallel.
 int launch_scan(const WideArgs& a, int64_t items, bool masked, hipStream_t stream);
-int launch_class(const ClassArgs& a, int64_t items, bool masked, hipStream_t stream);
+int launch_class(const ClassArgs& a, int64_t items, bool masked, const QueryLaunch* query, hipStream_t stream);
 int launch_finish_nov(const WideArgs& a, int64_t items, hipStream_t stream);
 int launch_class_budget_nov(const ClassArgs& a, int64_t items, hipStream_t stream);
 int launch_finish_v64_bf16(const WideArgs& a, int64_t items, hipStream_t stream);

@@ -48,7 +48,7 @@ bool summon_class_eligible(const SummonParams& p, int64_t items) {
 }
 
 int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                      const FusedVerify* fv, int32_t* overshoot) {
+                      const FusedVerify* fv, int32_t* overshoot, const QueryLaunch* query) {
   const int64_t items = (int64_t)p.H;  // one sequence, q = 1
   const int64_t W = (p.N + CLASS_CHUNK - 1) / CLASS_CHUNK;
   const size_t counts = align256((size_t)(items * W * 256) * sizeof(uint32_t));
@@ -71,7 +71,7 @@ int summon_class_path(const SummonParams& p, void* workspace, size_t workspace_b
   a.bound = (uint32_t*)(ws + counts);
   a.woff = (uint32_t*)(ws + counts + bound);
   const bool masked = p.mask_type == MASK_F32 || p.mask_type == MASK_BF16 || p.mask_type == MASK_F16;
-  return launch_class(a, items, masked, stream);
+  return launch_class(a, items, masked, query, stream);
 }
 
 bool fused_verify_eligible(const SummonParams& p, int64_t items, const FusedVerify& fv) {

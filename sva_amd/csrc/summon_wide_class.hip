@@ -1,6 +1,7 @@
 // Code-class path of the long-context summon (one subspace of at most 256
 // codewords): the count, select and extract launches; the budget launch's
 // variants live with the finish kernels of their K / V dtype.
+#include "query_decode.cuh"
 #include "summon_wide.cuh"
 
 namespace sva {
@@ -153,10 +154,30 @@ __global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
   }
 }
 
+// The decode query of every head (workgroups g < H) and the code counts of
+// every chunk (the rest) in one grid: the counts need nothing the query
+// computes, so they run while its dependent chain does.
 template <bool MASKED>
-int launch_class_m(const ClassArgs& a, int64_t items, hipStream_t stream) {
-  hipLaunchKernelGGL((class_count_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
-  SVA_CHECK_LAUNCH("class_count_kernel");
+__global__ void __launch_bounds__(WB) class_query_count_kernel(LutParams q, ClassArgs a) {
+  static_assert(QD == WB, "one block size for both roles");
+  if ((int)blockIdx.x < q.H) query_decode_item<1, 256>(q, (int)blockIdx.x);
+  else class_count_chunk<MASKED>(a, (int)blockIdx.x - q.H);
+}
+
+template <bool MASKED>
+int launch_class_m(const ClassArgs& a, int64_t items, const QueryLaunch* query, hipStream_t stream) {
+  if (query != nullptr && query->form == QUERY_DECODE_1_256) {
+    hipLaunchKernelGGL((class_query_count_kernel<MASKED>), dim3((unsigned)(query->blocks + items * a.W)), dim3(WB), 0,
+                       stream, query->p, a);
+    SVA_CHECK_LAUNCH("class_query_count_kernel");
+  } else {
+    if (query != nullptr) {
+      const int rc = query_lut_launch(*query, stream);
+      if (rc != SVA_OK) return rc;
+    }
+    hipLaunchKernelGGL((class_count_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
+    SVA_CHECK_LAUNCH("class_count_kernel");
+  }
   hipLaunchKernelGGL(class_select_kernel, dim3((unsigned)items), dim3(SB), 0, stream, a);
   SVA_CHECK_LAUNCH("class_select_kernel");
   hipLaunchKernelGGL((class_extract_kernel<MASKED>), dim3((unsigned)(items * a.W)), dim3(WB), 0, stream, a);
@@ -176,8 +197,8 @@ int launch_class_m(const ClassArgs& a, int64_t items, hipStream_t stream) {
 
 }  // namespace
 
-int launch_class(const ClassArgs& a, int64_t items, bool masked, hipStream_t stream) {
-  return masked ? launch_class_m<true>(a, items, stream) : launch_class_m<false>(a, items, stream);
+int launch_class(const ClassArgs& a, int64_t items, bool masked, const QueryLaunch* query, hipStream_t stream) {
+  return masked ? launch_class_m<true>(a, items, query, stream) : launch_class_m<false>(a, items, query, stream);
 }
 
 int launch_class_budget_nov(const ClassArgs& a, int64_t items, hipStream_t stream) {
