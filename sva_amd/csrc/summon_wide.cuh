@@ -766,21 +766,20 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     tot[i] = l < W ? a.wg_count[2 * (g0 + l)] : 0u;
     asum += l < W ? a.wg_count[2 * (g0 + l) + 1] : 0u;
   }
-  // the first round of this wave's lists (16 k + wid, k < FAST_BATCH), issued with the counts
-  uint64_t comp[2 * FAST_BATCH];
-  float rank[2 * FAST_BATCH];
+  // the first round of this wave's lists (16 k + wid, k < FAST_BATCH), issued
+  // with the counts: the first WAVE slots of each list (a list's later slots,
+  // rarely filled, are requested once its count shows them used)
+  uint64_t comp[FAST_BATCH];
+  float rank[FAST_BATCH];
   auto load_round = [&](int r) {
 #pragma unroll
     for (int k = 0; k < FAST_BATCH; ++k) {
       const int l = SNW * (r * FAST_BATCH + k) + wid;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        comp[2 * k + h] = 0ull;
-        rank[2 * k + h] = 0.0f;
-        if (l < W) {
-          comp[2 * k + h] = a.wg_cand[(g0 + l) * WG_CAP + lane + WAVE * h];
-          rank[2 * k + h] = a.wg_rank[(g0 + l) * WG_CAP + lane + WAVE * h];
-        }
+      comp[k] = 0ull;
+      rank[k] = 0.0f;
+      if (l < W) {
+        comp[k] = a.wg_cand[(g0 + l) * WG_CAP + lane];
+        rank[k] = a.wg_rank[(g0 + l) * WG_CAP + lane];
       }
     }
   };
@@ -822,14 +821,16 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
         const int src = l >> 2;
         const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
         const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t j = (uint32_t)(lane + WAVE * h);
-          if (j < c) {
-            lcomp[o + j] = comp[2 * k + h];
-            lrank[o + j] = rank[2 * k + h];
-            kmax = max(kmax, (uint32_t)(comp[2 * k + h] >> 32));
-          }
+        if ((uint32_t)lane < c) {
+          lcomp[o + lane] = comp[k];
+          lrank[o + lane] = rank[k];
+          kmax = max(kmax, (uint32_t)(comp[k] >> 32));
+        }
+        for (uint32_t j = WAVE + lane; j < c; j += WAVE) {  // a list beyond its first WAVE slots
+          const uint64_t x = a.wg_cand[(g0 + l) * WG_CAP + j];
+          lcomp[o + j] = x;
+          lrank[o + j] = a.wg_rank[(g0 + l) * WG_CAP + j];
+          kmax = max(kmax, (uint32_t)(x >> 32));
         }
       }
     }
