@@ -158,7 +158,8 @@ def cpu_baseline(torch, layer, shortlist, budget, repeats):
 
 # kernels of one decode step (sva_lookup_verify), by entry point
 SUMMON_KERNELS = ("query_decode_kernel", "query_lut_kernel", "wide_scan_kernel", "wide_finish_kernel",
-                  "class_count_kernel", "class_select_kernel", "class_extract_kernel", "class_budget_kernel")
+                  "class_query_count_kernel", "class_count_kernel", "class_select_kernel", "class_extract_kernel",
+                  "class_budget_kernel")
 PATH_KERNELS = SUMMON_KERNELS + ("budget_select_kernel", "verify_part_kernel", "verify_combine_kernel")
 PROFILE_STEM = "lookup_verify_decode_1m_{layout}{lb}"
 
@@ -893,7 +894,7 @@ def main():
             "workload": f"million-key cached decode lookup, one layer, q=1, {args.layout} codes",
             "keys": n, "q_heads": heads, "kv_heads": kv_heads, "head_dim": 64, "rank": 64,
             "shortlist": shortlist, "budget": budget, "layers_rotated": args.layers,
-            "summon_strategy": "wide" if strategy == 1 else "per-item",
+            "summon_strategy": {1: "wide", 2: "code-class"}.get(strategy, "per-item"),
         },
         "stage_us": per_stage_us,
         "gpu_us_per_query": round(gpu_us, 2),
@@ -902,10 +903,12 @@ def main():
         "graph": graph_res,
         "hbm_frac_end_to_end": round(bytes_["total"] / (us_per_query * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": ("sva_lookup_verify: query_decode_kernel + wide_scan_kernel + wide_finish_kernel (verifier "
-                       "inside the finish)" if strategy == 1 else
-                       "sva_lookup_verify: query_lut_kernel + summon_item + budget_select + verify_part + "
-                       "verify_combine"),
+            "kernel": {1: "sva_lookup_verify: query_decode_kernel + wide_scan_kernel + wide_finish_kernel (verifier "
+                          "inside the finish)",
+                       2: "sva_lookup_verify: class_query_count_kernel + class_select_kernel + class_extract_kernel "
+                          "+ class_budget_kernel (verifier inside the budget)"}.get(
+                strategy, "sva_lookup_verify: query_lut_kernel + summon_item + budget_select + verify_part + "
+                          "verify_combine"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

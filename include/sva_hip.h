@@ -187,7 +187,10 @@ int sva_lookup_verify(const void *q, int q_dtype, int64_t q_head_stride, int64_t
 /*
  * Which summon strategy a call with these shapes takes (16-byte aligned
  * catalogs assumed): 0 = one workgroup per query item, 1 = wide path (q = 1
- * over a long cache: many workgroups per item, one pass over the codes).
+ * over a long cache: many workgroups per item, one pass over the codes),
+ * 2 = code-class path (the wide path's shapes with one subspace of at most
+ * 256 codewords: the shortlist taken by code class from per-chunk code
+ * counts).
  */
 int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S, int64_t C,
                         int64_t L, int code_type, int mask_type);

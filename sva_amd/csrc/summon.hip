@@ -453,6 +453,7 @@ extern "C" int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   p.L = (int)L;
   p.mask = dummy;
   p.mask_type = mask_type;
+  if (sva::summon_class_eligible(p, n_seq * H * Q)) return 2;
   return sva::summon_wide_eligible(p, n_seq * H * Q) ? 1 : 0;
 }
 

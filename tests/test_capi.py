@@ -51,6 +51,8 @@ def test_summon_strategy_selection():
     lib = _lib()
     # 1M keys, q = 1, 4x64 codes: many workgroups per item
     assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 4, 64, 2048, 0, 0) == 1
+    # one subspace of <= 256 codewords: the shortlist by code class
+    assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 1, 256, 2048, 0, 0) == 2
     # short cache, prefill, or wide codes: one workgroup per item
     assert lib.sva_summon_strategy(1, 9, 1, 8192, 64, 2, 256, 2048, 0, 0) == 0
     assert lib.sva_summon_strategy(1, 9, 16, 1 << 20, 64, 4, 64, 2048, 0, 0) == 0

@@ -65,7 +65,7 @@ def _check(codes, k_low, q_low, lut, sl_idx, sl_rank, sl_count, L, allowed=None)
 
 @pytest.mark.parametrize("N,S,C", [(65536, 4, 64), (200003, 2, 256), (1048576, 4, 64), (1048576, 1, 256)])
 def test_wide_matches_oracle(device, N, S, C):
-    assert _strategy(9, N, 64, S, C, 2048) == 1, "wide path not selected"
+    assert _strategy(9, N, 64, S, C, 2048) == (2 if S == 1 else 1), "wide or code-class path not selected"
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=N % 97)
     res = _summon(device, codes, k_low, q, q_proj, scale, cb, 2048)
     _check(codes, k_low, *res, 2048)
@@ -206,7 +206,7 @@ def _check_fused(codes, k_low, fused, split, q_low, lut, L, B, allowed=None):
                                            (65536, 1, 256, 2048, 3000, False), (120000, 2, 256, 2048, 512, True),
                                            (1048576, 2, 256, 512, 128, False)])
 def test_wide_summon_select_fused(device, N, S, C, L, B, few):
-    assert _strategy(9, N, 64, S, C, L) == 1, "wide path not selected"
+    assert _strategy(9, N, 64, S, C, L) == (2 if S == 1 else 1), "wide or code-class path not selected"
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=(N + L) % 89, few=few)
     fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B)
     _check_fused(codes, k_low, fused, split, q_low, lut, L, B)
@@ -285,7 +285,7 @@ def test_class_path_single_subspace(device, N, C, L, B, few, masked):
     """One subspace of <= 256 codewords selects by code class (count, boundary class, ordered extraction,
     budget): shortlist and ranks equal the oracle's top-L (score desc, key asc) and the standalone budget
     select's lists, every head."""
-    assert _strategy(9, N, 64, 1, C, L) == 1, "wide path not selected"
+    assert _strategy(9, N, 64, 1, C, L) == 2, "code-class path not selected"
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, 1, C, seed=(N + C + L) % 83, few=few)
     mask = allowed = None
     if masked:
