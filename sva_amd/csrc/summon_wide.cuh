@@ -136,19 +136,17 @@ struct ScanTables {
   static constexpr int LDS_FLOATS = PAIR + SINGLE;
   static constexpr int NP = PAIR / WB;                 // pair entries per thread
   static constexpr int NS = (SINGLE + WB - 1) / WB;    // single entries per thread
-  float t0, t1[NP ? NP : 1], ts[NS];
+  float ts[NS];
   const float* tab;
-  // Table values into registers: every load issued, none waited for, so
-  // the caller can issue its code loads behind them.
+  // The single tables into registers, one coalesced read of the item's table
+  // per workgroup (every workgroup of an item reads the same lines, so a
+  // read per pair entry would queue thousands of requests on them): every
+  // load issued, none waited for, so the caller can issue its code loads
+  // behind them.
   SVA_DEV void load(const SummonParams& p, int item) {
     const float* src = p.lut + (int64_t)item * S * p.C;
     const int t = threadIdx.x;
     const int cm = p.C - 1;
-    if (NP) {
-      t0 = src[min(t & 63, cm)];  // (t + k * WB) & 63 == t & 63
-#pragma unroll
-      for (int k = 0; k < NP; ++k) t1[k] = src[p.C + min((t + k * WB) >> 6, cm)];
-    }
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
       const int e = t + k * WB;
@@ -159,16 +157,22 @@ struct ScanTables {
       }
     }
   }
-  // Writes the tables to LDS (the caller synchronizes before use).
+  // Writes the tables to LDS (the caller synchronizes before use): the
+  // single tables, then the pair table built from them (entry c0 + 64 c1 =
+  // T0[c0] + T1[c1], thread t's c0 = t & 63 and c1 = t / 64 + 4 k).
   SVA_DEV void store(float* lds_tab) {
 #pragma clang fp contract(off)
     const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < NP; ++k) lds_tab[t + k * WB] = t0 + t1[k];
-#pragma unroll
     for (int k = 0; k < NS; ++k)
       if (t + k * WB < SINGLE) lds_tab[PAIR + t + k * WB] = ts[k];
     tab = lds_tab;
+    if (NP) {
+      __syncthreads();  // the single tables
+      const float a0 = lds_tab[PAIR + (t & 63)];
+#pragma unroll
+      for (int k = 0; k < NP; ++k) lds_tab[t + k * WB] = a0 + lds_tab[PAIR + 64 + ((t + k * WB) >> 6)];
+    }
   }
   SVA_DEV float at_byte(uint32_t byte_offset) const {
     return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(tab) + byte_offset);
