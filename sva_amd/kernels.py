@@ -25,7 +25,7 @@ def workspace(device: torch.device, nbytes: int, kind: str = "summon") -> torch.
     call made on one stream in turn; calls on another stream get their own,
     so concurrent streams never share one."""
 
-    key = (device, kind, torch.cuda.current_stream(device).cuda_stream)
+    key = (device, kind, stream_handle(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 256), device=device, dtype=torch.uint8)
@@ -354,6 +354,10 @@ class ScanDecodePlan:
         self.fin_idx = torch.empty(items, budget, device=self.device, dtype=i32)
         self.fin_count = self.counts[1]
         self._lib = lib()
+        # the plan's own buffers, as the one-call step passes them
+        self._bufs = (self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), self.sl_idx.data_ptr(),
+                      self.sl_rank.data_ptr(), self.sl_count.data_ptr(), self.fin_idx.data_ptr(),
+                      self.fin_count.data_ptr(), self.overshoot.data_ptr())
         self._ws, self._ws_keys = None, -1  # summon workspace, sized for caches of up to _ws_keys keys
         self._vws, self._vws_kv = None, -1  # verify workspace (independent of the cache length)
         self._checked_weights = set()  # (data_ptr, version, dtype, shape, strides) of weights that passed
@@ -411,7 +415,7 @@ class ScanDecodePlan:
         self._check_catalog(codes, k_low, n_keys)
         self._check_kv(keys, values, n_keys)
         L = self._lib
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = stream_handle(self.device)
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
         ws = self._summon_ws(n_keys)
         vws = self._verify_ws(keys)
@@ -419,16 +423,15 @@ class ScanDecodePlan:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
         if out.stride(-1) != 1 or tuple(out.shape) != (1, heads, 1, head_dim):
             raise ValueError(f"ScanDecodePlan: out must be [1, {heads}, 1, {head_dim}] with contiguous rows")
+        b_qlow, b_lut, b_rng, b_slidx, b_slrank, b_slcount, b_finidx, b_fincount, b_over = self._bufs
         check(L.sva_lookup_verify(q.data_ptr(), dtype_code(q), q.stride(1), heads, head_dim, rank, subspaces, codewords,
                                   q_proj.data_ptr(), scale.data_ptr(), codebooks.data_ptr(), codes.data_ptr(),
                                   code_type(codes), codes.stride(0), k_low.data_ptr(), k_low.stride(0), n_keys,
-                                  shortlist, ptr(m), mtype, mstride, self.q_low.data_ptr(), self.lut.data_ptr(),
-                                  self.rng.data_ptr(), self.sl_idx.data_ptr(), self.sl_rank.data_ptr(),
-                                  self.sl_count.data_ptr(), budget, self.fin_idx.data_ptr(),
-                                  self.fin_count.data_ptr(), ws.data_ptr(), ws.numel(), keys.data_ptr(),
-                                  values.data_ptr(), dtype_code(keys), keys.stride(0), keys.stride(1),
-                                  keys.shape[0], float(scaling), out.data_ptr(), dtype_code(out), out.stride(1),
-                                  vws.data_ptr(), vws.numel(), self.overshoot.data_ptr(), stream),
+                                  shortlist, ptr(m), mtype, mstride, b_qlow, b_lut, b_rng, b_slidx, b_slrank,
+                                  b_slcount, budget, b_finidx, b_fincount, ws.data_ptr(), ws.numel(),
+                                  keys.data_ptr(), values.data_ptr(), dtype_code(keys), keys.stride(0),
+                                  keys.stride(1), keys.shape[0], float(scaling), out.data_ptr(), dtype_code(out),
+                                  out.stride(1), vws.data_ptr(), vws.numel(), b_over, stream),
               "sva_lookup_verify")
         return out
 
@@ -470,7 +473,7 @@ class ScanDecodePlan:
         self._check_weights(q_proj, scale, codebooks)
         self._check_catalog(codes, k_low, n_keys)
         L = self._lib
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = stream_handle(self.device)
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
         ws = self._summon_ws(n_keys)
         if n_seq == 1 and q_len == 1:
@@ -504,7 +507,7 @@ class ScanDecodePlan:
         self._check_query(q)
         self._check_kv(keys, values, n_keys)
         L = self._lib
-        stream = torch.cuda.current_stream(self.device).cuda_stream
+        stream = stream_handle(self.device)
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
         vws = self._verify_ws(keys)
