@@ -646,8 +646,12 @@ constexpr size_t kFastComp = 0;                                              // 
 constexpr size_t kFastRank = kFastComp + sizeof(uint64_t) * FAST_M;          // float[FAST_M]
 constexpr size_t kFastHist = kFastRank + sizeof(float) * FAST_M;             // uint32[4096]
 constexpr size_t kFastSmall = kFastHist + sizeof(uint32_t) * 4096;           // uint64[SMALL_CAP]
-constexpr size_t kFastMisc = kFastSmall + sizeof(uint64_t) * SMALL_CAP;      // uint32[64]
-constexpr size_t kFastEnd = kFastMisc + sizeof(uint32_t) * 64;
+constexpr size_t kFastMisc = kFastSmall + sizeof(uint64_t) * SMALL_CAP;      // uint32[96]
+constexpr size_t kFastEnd = kFastMisc + sizeof(uint32_t) * 96;
+// over the staged candidates once they sit in registers (fused budget histogram)
+constexpr size_t kFastRHist = kFastComp;                                      // uint32[4096]
+constexpr size_t kFastSmallR = kFastRHist + sizeof(uint32_t) * 4096;          // float[SMALL_CAP]
+static_assert(kFastSmallR + sizeof(float) * SMALL_CAP <= kFastRank, "budget histogram over the staged composites");
 static_assert(WG_CAP == 2 * WAVE, "two compact-list entries per lane");
 static_assert(kFastEnd <= kFinStage, "the fast finish stays inside the finish kernel's staging area");
 
@@ -657,12 +661,22 @@ SVA_DEV uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-// LDS scalars of the fast finish (misc): per-wave values at [16 * slot + wave].
+// LDS scalars of the fast finish (misc): per-wave values at [16 * slot + wave], slots 0..4.
 struct FastMisc {
   uint32_t* m;
   SVA_DEV uint32_t& wave(int slot, int w) const { return m[16 * slot + w]; }
-  SVA_DEV uint32_t& res(int k) const { return m[48 + k]; }
-  SVA_DEV uint64_t& res64() const { return *reinterpret_cast<uint64_t*>(m + 56); }
+  SVA_DEV uint32_t& res(int k) const { return m[80 + k]; }
+  SVA_DEV uint64_t& res64() const { return *reinterpret_cast<uint64_t*>(m + 88); }
+};
+
+// Optional work of a shortlist select for the budget select that follows:
+// the rank of every shortlisted key binned into rhist (4096 bins linear in
+// the candidates' rank range [rlo, rlo + 4096 / rinv)), so the budget select
+// starts from a built histogram.  smallr holds the boundary members' ranks.
+struct RankFuse {
+  uint32_t* rhist;
+  float* smallr;
+  float rlo, rinv;
 };
 
 // Threshold of the k largest nonzero composites held in e[] (dense slots),
@@ -678,14 +692,21 @@ SVA_DEV int lin_bin(float v, float lo, float inv_w) {
   return b < 1.0f ? 0 : (b >= 4095.0f ? 4095 : (int)b);
 }
 
+// FUSE: rf's rank histogram is built on the way (rv: the elements' ranks);
+// built: hist already holds the elements' bins (phase 1 skipped).
+template <bool FUSE = false>
 SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], int dslots, int k, float lo, float inv_w,
-                             uint32_t* hist, uint64_t* small, const FastMisc& f, bool* exact) {
+                             uint32_t* hist, uint64_t* small, const FastMisc& f, bool* exact, bool built = false,
+                             const float (*rv)[NPD] = nullptr, const RankFuse* rf = nullptr) {
 #pragma clang fp contract(off)
   const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  if (!built) {
 #pragma unroll
-  for (int i = 0; i < NPD; ++i)
-    if (i < dslots && e[i] != 0ull) atomicAdd(&hist[lin_bin(v[i], lo, inv_w)], 1u);
+    for (int i = 0; i < NPD; ++i)
+      if (i < dslots && e[i] != 0ull) atomicAdd(&hist[lin_bin(v[i], lo, inv_w)], 1u);
+  }
   __syncthreads();
+  if (FUSE) reinterpret_cast<uint4*>(rf->rhist)[t] = uint4{0u, 0u, 0u, 0u};  // the staging it overlays is read
   // thread t owns bins 4095 - 4 t - j (j = 0..3), from the top
   const uint4 h = reinterpret_cast<const uint4*>(hist)[1023 - t];
   const uint32_t c[4] = {h.w, h.z, h.y, h.x};
@@ -717,17 +738,23 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], in
     *exact = false;
     return 0ull;
   }
-  // the boundary bin's members, then each one's rank among them
+  // the boundary bin's members, then each one's rank among them (FUSE: the
+  // keys of higher bins, all shortlisted, bin their ranks)
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
     if (i < dslots) {  // uniform
-      const bool in = e[i] != 0ull && lin_bin(v[i], lo, inv_w) == b;
+      const int bin = lin_bin(v[i], lo, inv_w);
+      const bool in = e[i] != 0ull && bin == b;
+      if (FUSE && e[i] != 0ull && bin > b) atomicAdd(&rf->rhist[lin_bin((*rv)[i], rf->rlo, rf->rinv)], 1u);
       const uint64_t m = __builtin_amdgcn_ballot_w64(in);
       if (m != 0ull) {
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd(&f.res(3), (uint32_t)__popcll(m));
         base = (uint32_t)__shfl((int)base, 0, WAVE);
-        if (in) small[base + lanes_below(m)] = e[i];
+        if (in) {
+          small[base + lanes_below(m)] = e[i];
+          if (FUSE) rf->smallr[base + lanes_below(m)] = (*rv)[i];
+        }
       }
     }
   }
@@ -741,6 +768,8 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], in
     greater += __shfl_xor(greater, 1, WAVE);
     greater += __shfl_xor(greater, 2, WAVE);
     if (q == 0 && g < (int)cnt && greater == need - 1u) f.res64() = x;
+    if (FUSE && q == 0 && g < (int)cnt && greater < need)  // a selected boundary member
+      atomicAdd(&rf->rhist[lin_bin(rf->smallr[g], rf->rlo, rf->rinv)], 1u);
   }
   __syncthreads();
   return f.res64();
@@ -816,6 +845,7 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const uint32_t my_off = base + (el == 0 ? loc[0] : el == 1 ? loc[1] : el == 2 ? loc[2] : loc[3]);
   const uint32_t my_tot = el == 0 ? tot[0] : el == 1 ? tot[1] : el == 2 ? tot[2] : tot[3];
   uint32_t kmax = 0u;  // highest score key placed by this lane
+  uint32_t rkmin = 0xFFFFFFFFu, rkmax = 0u;  // rank keys placed by this lane
   for (int r = 0; r * FAST_BATCH * SNW < W; ++r) {
     if (r > 0) load_round(r);
 #pragma unroll
@@ -829,12 +859,17 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
           lcomp[o + lane] = comp[k];
           lrank[o + lane] = rank[k];
           kmax = max(kmax, (uint32_t)(comp[k] >> 32));
+          rkmin = min(rkmin, f2key(rank[k]));
+          rkmax = max(rkmax, f2key(rank[k]));
         }
         for (uint32_t j = WAVE + lane; j < c; j += WAVE) {  // a list beyond its first WAVE slots
           const uint64_t x = a.wg_cand[(g0 + l) * WG_CAP + j];
+          const float rj = a.wg_rank[(g0 + l) * WG_CAP + j];
           lcomp[o + j] = x;
-          lrank[o + j] = a.wg_rank[(g0 + l) * WG_CAP + j];
+          lrank[o + j] = rj;
           kmax = max(kmax, (uint32_t)(x >> 32));
+          rkmin = min(rkmin, f2key(rj));
+          rkmax = max(rkmax, f2key(rj));
         }
       }
     }
@@ -842,7 +877,12 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   {
     uint32_t mn = 0u;
     wave_min_max_u32(mn, kmax);
-    if (lane == 0) f.wave(1, wid) = kmax;
+    wave_min_max_u32(rkmin, rkmax);
+    if (lane == 0) {
+      f.wave(1, wid) = kmax;
+      f.wave(3, wid) = rkmin;
+      f.wave(4, wid) = rkmax;
+    }
   }
   reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
@@ -857,16 +897,27 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     e[i] = in ? lcomp[j] : 0ull;
     rv[i] = in ? lrank[j] : 0.0f;
   }
-  uint32_t khi = 0u;
-  for (int v = 0; v < SNW; ++v) khi = max(khi, f.wave(1, v));
+  uint32_t khi = 0u, rklo = 0xFFFFFFFFu, rkhi = 0u;
+  for (int v = 0; v < SNW; ++v) {
+    khi = max(khi, f.wave(1, v));
+    rklo = min(rklo, f.wave(3, v));
+    rkhi = max(rkhi, f.wave(4, v));
+  }
   const float vlo = item_floor(p, item) * kInvSqrtR;
   bool exact = true;
   uint64_t X = 1ull;
+  // the budget select's histogram is built by the shortlist select, over the
+  // rank range of every candidate
+  const bool fuse = (uint32_t)leff < M && p.B > 0 && beff < leff;
+  const RankFuse rf{(uint32_t*)(lds + kFastRHist), (float*)(lds + kFastSmallR), key2f(rklo),
+                    lin_scale(key2f(rklo), key2f(rkhi))};
   if ((uint32_t)leff < M) {
     float sv[NPD];
 #pragma unroll
     for (int i = 0; i < NPD; ++i) sv[i] = key2f((uint32_t)(e[i] >> 32));
-    X = fast_select(e, sv, dslots, leff, vlo, lin_scale(vlo, key2f(khi)), hist, small, f, &exact);
+    const float inv = lin_scale(vlo, key2f(khi));
+    X = fuse ? fast_select<true>(e, sv, dslots, leff, vlo, inv, hist, small, f, &exact, false, &rv, &rf)
+             : fast_select(e, sv, dslots, leff, vlo, inv, hist, small, f, &exact);
     if (!exact) {
       __syncthreads();
       return false;  // a tie class too large to rank directly: the general paths
@@ -886,7 +937,14 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     }
   }
   uint64_t XB = 1ull;
-  if (p.B > 0 && beff < leff) {
+  if (fuse) {
+    bool ex2 = true;
+    XB = fast_select(rc, rv, dslots, beff, rf.rlo, rf.rinv, rf.rhist, small, f, &ex2, true);
+    if (!ex2) {
+      __syncthreads();
+      return false;
+    }
+  } else if (p.B > 0 && beff < leff) {
     wave_min_max_u32(rmin, rmax);
     if (lane == 0) {
       f.wave(1, wid) = rmin;
