@@ -817,6 +817,14 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     }
   };
   load_round(0);
+  // the shortlist select's score histogram, filled as the candidates are
+  // placed: 4096 bins linear in [floor, bound of any sum] (zeroed while the
+  // loads are in flight)
+  uint32_t* hist = (uint32_t*)(lds + kFastHist);
+  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  const float vlo = item_floor(p, item) * kInvSqrtR;
+  const float vinv = lin_scale(vlo, p.range[4 * item + 1] * kInvSqrtR);
   uint32_t loc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -836,7 +844,6 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   if (leff == 0) return true;
   uint64_t* lcomp = (uint64_t*)(lds + kFastComp);
   float* lrank = (float*)(lds + kFastRank);
-  uint32_t* hist = (uint32_t*)(lds + kFastHist);
   uint64_t* small = (uint64_t*)(lds + kFastSmall);
   const FastMisc f{(uint32_t*)(lds + kFastMisc)};
   const uint32_t base = wave_excl_scan(lsum);
@@ -844,7 +851,6 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const int el = wid & 3;
   const uint32_t my_off = base + (el == 0 ? loc[0] : el == 1 ? loc[1] : el == 2 ? loc[2] : loc[3]);
   const uint32_t my_tot = el == 0 ? tot[0] : el == 1 ? tot[1] : el == 2 ? tot[2] : tot[3];
-  uint32_t kmax = 0u;  // highest score key placed by this lane
   uint32_t rkmin = 0xFFFFFFFFu, rkmax = 0u;  // rank keys placed by this lane
   for (int r = 0; r * FAST_BATCH * SNW < W; ++r) {
     if (r > 0) load_round(r);
@@ -858,7 +864,7 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
         if ((uint32_t)lane < c) {
           lcomp[o + lane] = comp[k];
           lrank[o + lane] = rank[k];
-          kmax = max(kmax, (uint32_t)(comp[k] >> 32));
+          atomicAdd(&hist[lin_bin(key2f((uint32_t)(comp[k] >> 32)), vlo, vinv)], 1u);
           rkmin = min(rkmin, f2key(rank[k]));
           rkmax = max(rkmax, f2key(rank[k]));
         }
@@ -867,24 +873,18 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
           const float rj = a.wg_rank[(g0 + l) * WG_CAP + j];
           lcomp[o + j] = x;
           lrank[o + j] = rj;
-          kmax = max(kmax, (uint32_t)(x >> 32));
+          atomicAdd(&hist[lin_bin(key2f((uint32_t)(x >> 32)), vlo, vinv)], 1u);
           rkmin = min(rkmin, f2key(rj));
           rkmax = max(rkmax, f2key(rj));
         }
       }
     }
   }
-  {
-    uint32_t mn = 0u;
-    wave_min_max_u32(mn, kmax);
-    wave_min_max_u32(rkmin, rkmax);
-    if (lane == 0) {
-      f.wave(1, wid) = kmax;
-      f.wave(3, wid) = rkmin;
-      f.wave(4, wid) = rkmax;
-    }
+  wave_min_max_u32(rkmin, rkmax);
+  if (lane == 0) {
+    f.wave(3, wid) = rkmin;
+    f.wave(4, wid) = rkmax;
   }
-  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
   // dense slots in registers: candidate t + i SB at thread t, slot i (list order)
   const int dslots = ((int)M + SB - 1) / SB;
@@ -897,13 +897,11 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     e[i] = in ? lcomp[j] : 0ull;
     rv[i] = in ? lrank[j] : 0.0f;
   }
-  uint32_t khi = 0u, rklo = 0xFFFFFFFFu, rkhi = 0u;
+  uint32_t rklo = 0xFFFFFFFFu, rkhi = 0u;
   for (int v = 0; v < SNW; ++v) {
-    khi = max(khi, f.wave(1, v));
     rklo = min(rklo, f.wave(3, v));
     rkhi = max(rkhi, f.wave(4, v));
   }
-  const float vlo = item_floor(p, item) * kInvSqrtR;
   bool exact = true;
   uint64_t X = 1ull;
   // the budget select's histogram is built by the shortlist select, over the
@@ -915,9 +913,8 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     float sv[NPD];
 #pragma unroll
     for (int i = 0; i < NPD; ++i) sv[i] = key2f((uint32_t)(e[i] >> 32));
-    const float inv = lin_scale(vlo, key2f(khi));
-    X = fuse ? fast_select<true>(e, sv, dslots, leff, vlo, inv, hist, small, f, &exact, false, &rv, &rf)
-             : fast_select(e, sv, dslots, leff, vlo, inv, hist, small, f, &exact);
+    X = fuse ? fast_select<true>(e, sv, dslots, leff, vlo, vinv, hist, small, f, &exact, true, &rv, &rf)
+             : fast_select(e, sv, dslots, leff, vlo, vinv, hist, small, f, &exact, true);
     if (!exact) {
       __syncthreads();
       return false;  // a tie class too large to rank directly: the general paths
