@@ -661,6 +661,20 @@ SVA_DEV uint32_t lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Exclusive prefix sums, in place, of the n <= 2 * WAVE per-(slot, wave)
+// count words wcnt[] (two packed 16-bit counts each), by the first wave
+// alone; the caller synchronizes before and after.
+SVA_DEV void slot_wave_offsets(uint32_t* wcnt, int n) {
+  if (threadIdx.x >= WAVE) return;
+  const int lane = lane_id();
+  const uint32_t v0 = 2 * lane < n ? wcnt[2 * lane] : 0u;
+  const uint32_t v1 = 2 * lane + 1 < n ? wcnt[2 * lane + 1] : 0u;
+  const uint32_t b = wave_excl_scan(v0 + v1);
+  if (2 * lane < n) wcnt[2 * lane] = b;
+  if (2 * lane + 1 < n) wcnt[2 * lane + 1] = b + v0;
+}
+static_assert(NPD * SNW <= 2 * WAVE, "two (slot, wave) counts per lane of one wave");
+
 // LDS scalars of the fast finish (misc): per-wave values at [16 * slot + wave], slots 0..4.
 struct FastMisc {
   uint32_t* m;
@@ -974,12 +988,8 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
     }
   }
   __syncthreads();
-  {
-    const uint32_t v = t < dslots * SNW ? wcnt[t] : 0u;
-    const uint32_t off = block_excl_scan<SB>(v, scratch, nullptr);
-    if (t < dslots * SNW) wcnt[t] = off;
-    __syncthreads();
-  }
+  slot_wave_offsets(wcnt, dslots * SNW);
+  __syncthreads();
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
   float* out_rank = p.sl_rank + (int64_t)item * p.L;
   int32_t* fin = p.B > 0 ? p.fin_idx + (int64_t)item * p.B : nullptr;
@@ -2056,12 +2066,8 @@ __global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
     }
   }
   __syncthreads();
-  {
-    const uint32_t v = t < dslots * SNW ? wcnt[t] : 0u;
-    const uint32_t o = block_excl_scan<SB>(v, scratch, nullptr);
-    if (t < dslots * SNW) wcnt[t] = o;
-    __syncthreads();
-  }
+  slot_wave_offsets(wcnt, dslots * SNW);
+  __syncthreads();
   int32_t* fin = p.fin_idx + (int64_t)item * p.B;
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
