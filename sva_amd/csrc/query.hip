@@ -220,10 +220,14 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
 }
 
 // Decode form: the body lives in query_decode.cuh (the code-class path runs
-// it in one grid with its code counts).
-template <int S, int CMAX>
-__global__ void __launch_bounds__(QD) query_decode_kernel(LutParams p) {
-  query_decode_item<S, CMAX>(p, (int)blockIdx.x);
+// it in one grid with its code counts).  Two and four subspaces run 1024
+// threads per head: their table, pair and histogram phases are LDS-latency
+// bound, and 16 waves hide what 4 cannot.
+constexpr int QD_WIDE = 1024;
+
+template <int S, int CMAX, int NT>
+__global__ void __launch_bounds__(NT) query_decode_kernel(LutParams p) {
+  query_decode_item<S, CMAX, NT>(p, (int)blockIdx.x);
 }
 
 // Many query tokens per head (prefill): one workgroup per MT consecutive
@@ -441,7 +445,10 @@ int query_lut_setup(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_
   // one token of one sequence at D = R = 64: the decode form
   const bool aligned = ((uintptr_t)q_proj & 15u) == 0 && ((uintptr_t)codebooks & 15u) == 0 &&
                        (!sample || (((uintptr_t)codes & 15u) == 0 && code_head_stride % 16 == 0));
-  if (n_seq == 1 && Q == 1 && D == 64 && R == 64 && aligned && (!sample || blocks * SAMPLE_KEYS * S <= QD * 16 * (S == 4 ? qd_words<4>() : S == 2 ? qd_words<2>() : qd_words<1>()))) {
+  const int64_t word_room = S == 4   ? (int64_t)QD_WIDE * qd_words<4, QD_WIDE>()
+                            : S == 2 ? (int64_t)QD_WIDE * qd_words<2, QD_WIDE>()
+                                     : (int64_t)QD * qd_words<1>();  // sampled 16-byte words the form holds
+  if (n_seq == 1 && Q == 1 && D == 64 && R == 64 && aligned && (!sample || blocks * SAMPLE_KEYS * S <= 16 * word_room)) {
     const int form = S == 4 && C <= 64 ? QUERY_DECODE_4_64
                      : S == 2 && C <= 256 ? QUERY_DECODE_2_256
                      : S == 1 && C <= 256 ? QUERY_DECODE_1_256
@@ -462,15 +469,15 @@ int query_lut_launch(const QueryLaunch& ql, hipStream_t st) {
     case QUERY_MULTI32: return launch_lut_multi<32>(p, ql.blocks, ql.lds, st);
     case QUERY_MULTI64: return launch_lut_multi<64>(p, ql.blocks, ql.lds, st);
     case QUERY_DECODE_4_64:
-      hipLaunchKernelGGL((query_decode_kernel<4, 64>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      hipLaunchKernelGGL((query_decode_kernel<4, 64, QD_WIDE>), dim3((unsigned)ql.blocks), dim3(QD_WIDE), 0, st, p);
       SVA_CHECK_LAUNCH("query_decode_kernel");
       return SVA_OK;
     case QUERY_DECODE_2_256:
-      hipLaunchKernelGGL((query_decode_kernel<2, 256>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      hipLaunchKernelGGL((query_decode_kernel<2, 256, QD_WIDE>), dim3((unsigned)ql.blocks), dim3(QD_WIDE), 0, st, p);
       SVA_CHECK_LAUNCH("query_decode_kernel");
       return SVA_OK;
     case QUERY_DECODE_1_256:
-      hipLaunchKernelGGL((query_decode_kernel<1, 256>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
+      hipLaunchKernelGGL((query_decode_kernel<1, 256, QD>), dim3((unsigned)ql.blocks), dim3(QD), 0, st, p);
       SVA_CHECK_LAUNCH("query_decode_kernel");
       return SVA_OK;
     default:

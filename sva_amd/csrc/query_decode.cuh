@@ -21,18 +21,23 @@ constexpr int QD = 256;
 constexpr int QD_WORDS = 8;  // sampled 16-byte code words per thread (at most 32 KB per head)
 // Sampled code words a thread holds for S subspaces: at most SAMPLE_MAX_BLOCKS
 // blocks of SAMPLE_KEYS keys, S bytes each, over QD threads.
-template <int S>
+template <int S, int NT = QD>
 constexpr int qd_words() {
-  return SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / QD < QD_WORDS ? SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / QD
-                                                                    : QD_WORDS;
+  return SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / NT < 1           ? 1
+         : SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / NT < QD_WORDS ? SAMPLE_MAX_BLOCKS * SAMPLE_KEYS * S / 16 / NT
+                                                                     : QD_WORDS;
 }
 
-template <int S, int CMAX>
+// NT threads per workgroup (256, or 1024 so that more waves hide the
+// latency of the table, pair and histogram phases).
+template <int S, int CMAX, int NT = QD>
 SVA_DEV void query_decode_item(const LutParams& p, int h) {
 #pragma clang fp contract(off)
+  static_assert(NT % 256 == 0 && NT <= 1024, "256 or more threads, whole 64-entry table rows per wave");
   constexpr int SUB = 64 / S;
   constexpr int NPAIR = S >= 4 ? S / 2 : 0;
-  constexpr int EPT = (S * CMAX + QD - 1) / QD;  // table entries per thread
+  constexpr int EPT = (S * CMAX + NT - 1) / NT;  // table entries per thread
+  constexpr int NW4 = 1024 / NT;                  // float4s of the map per thread
   constexpr int KPW = 16 / S;                     // keys per 16-byte code word
   __shared__ __align__(16) float W[64 * 64];
   __shared__ float qf[64], ql[64];
@@ -40,20 +45,20 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   __shared__ float pairs[NPAIR > 0 ? NPAIR * 4096 : 1];
   __shared__ uint32_t kmin[S], kmax[S];
   __shared__ __align__(16) uint32_t hist[SAMPLE_BINS];
-  __shared__ uint32_t wsum[QD / WAVE], res[2];
+  __shared__ uint32_t wsum[NT / WAVE], res[2];
   const int t = threadIdx.x;
   const int lane = lane_id(), wid = t / WAVE;
   const int C = p.C;
   // 1. every load at once: map, query, codebook rows, sampled code words
-  float4 wv[4];
+  float4 wv[NW4];
   const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * 4096);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) wv[i] = w4[t + i * QD];
+  for (int i = 0; i < NW4; ++i) wv[i] = w4[t + i * NT];
   const float qv = t < 64 ? load_elem(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0.0f;
   float4 row[EPT][SUB / 4];
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = min(t + k * QD, S * C - 1);
+    const int e = min(t + k * NT, S * C - 1);
     const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB);
 #pragma unroll
     for (int j = 0; j < SUB / 4; ++j) row[k][j] = c4[j];
@@ -62,13 +67,13 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   const int nb = p.sample_blocks;
   const int n_words = nb * 2 * S;  // 32 keys x S bytes per block = 2 S words
   const int64_t N = p.n_keys;
-  constexpr int QW = qd_words<S>();
+  constexpr int QW = qd_words<S, NT>();
   u32x4_t words[QW];
   if (k_rank > 0) {
     const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-      const int gw = t + i * QD;
+      const int gw = t + i * NT;
       const int b = gw / (2 * S), wi = gw % (2 * S);
       const int64_t n0 = ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15;
       words[i] = gw < n_words ? *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16) : u32x4_t{0u, 0u, 0u, 0u};
@@ -76,13 +81,13 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   }
   const float sc = p.scale[h];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(W)[t + i * QD] = wv[i];
+  for (int i = 0; i < NW4; ++i) reinterpret_cast<float4*>(W)[t + i * NT] = wv[i];
   if (t < 64) qf[t] = qv;
   if (t < S) {
     kmin[t] = 0xFFFFFFFFu;
     kmax[t] = 0u;
   }
-  reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
+  if (t < SAMPLE_BINS / 4) reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   if (t == 0) res[0] = 0u;  // floor bin 0 unless the samples place it
   __syncthreads();
   // 2. q_low: one lane per output, a sequential fma chain over d
@@ -102,7 +107,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   const bool wave_sub = C % WAVE == 0;
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = t + k * QD;
+    const int e = t + k * NT;
     const int s = min(e, S * C - 1) / C;
     uint32_t kl = 0xFFFFFFFFu, kh = 0u;
     if (e < S * C) {
@@ -118,7 +123,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
         atomicMax(&kmax[s], kh);
       }
     }
-    if (wave_sub && k * QD + WAVE * wid < S * C) {  // uniform: the wave's entries exist
+    if (wave_sub && k * NT + WAVE * wid < S * C) {  // uniform: the wave's entries exist
       wave_min_max_u32(kl, kh);
       if (lane == 0) {
         atomicMin(&kmin[s], kl);
@@ -138,15 +143,16 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
     const uint32_t cm = (uint32_t)(C - 1);
     if (NPAIR > 0) {
       // pair m: entry c0 + 64 c1 = T_{2m}[c0] + T_{2m+1}[c1]; thread t writes
-      // entries t + 256 r, whose c0 = t & 63 is its own and c1 = t / 64 + 4 r
+      // entries t + NT r, whose c0 = t & 63 is its own and c1 = t / 64 + (NT / 64) r
 #pragma unroll
       for (int m = 0; m < NPAIR; ++m) {
         const float a0 = tab[2 * m * C + min((uint32_t)(t & 63), cm)];
-        float b[4096 / QD];
+        float b[4096 / NT];
 #pragma unroll
-        for (int r = 0; r < 4096 / QD; ++r) b[r] = tab[(2 * m + 1) * C + min((uint32_t)((t >> 6) + 4 * r), cm)];
+        for (int r = 0; r < 4096 / NT; ++r)
+          b[r] = tab[(2 * m + 1) * C + min((uint32_t)((t >> 6) + (NT / 64) * r), cm)];
 #pragma unroll
-        for (int r = 0; r < 4096 / QD; ++r) pairs[m * 4096 + t + QD * r] = a0 + b[r];
+        for (int r = 0; r < 4096 / NT; ++r) pairs[m * 4096 + t + NT * r] = a0 + b[r];
       }
       __syncthreads();
     }
@@ -154,7 +160,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
     float sums[QW * KPW];
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-      const bool valid = t + i * QD < n_words;  // invalid words are zero: their reads stay in bounds
+      const bool valid = t + i * NT < n_words;  // invalid words are zero: their reads stay in bounds
 #pragma unroll
       for (int q = 0; q < KPW; ++q) {
         float acc = 0.0f;
@@ -191,8 +197,9 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
       }
     }
     __syncthreads();
-    // 5. the bin of the k-th largest sampled sum: thread t owns bins 1023 - 4 t - j
-    const uint4 hv = reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - t];
+    // 5. the bin of the k-th largest sampled sum: thread t < 256 owns bins 1023 - 4 t - j
+    const uint4 hv = t < SAMPLE_BINS / 4 ? reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - t]
+                                         : uint4{0u, 0u, 0u, 0u};
     const uint32_t c[4] = {hv.w, hv.z, hv.y, hv.x};
     const uint32_t mine = c[0] + c[1] + c[2] + c[3];
     const uint32_t incl = wave_incl_scan(mine);
