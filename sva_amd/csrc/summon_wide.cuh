@@ -242,8 +242,9 @@ SVA_DEV float item_floor(const SummonParams& p, int item) {
 
 // Appends the flagged keys of one round (key n0 + k for flag c[k]) to the
 // wave's candidate list in ascending key order (lanes in order, each lane's
-// keys in order), as composites of the exact score acc / sqrt(R); the first
-// KL_CAP composites also go to the wave's LDS list `kc`.
+// keys in order), as composites of the exact score acc / sqrt(R): the first
+// KL_CAP to the wave's LDS list `kc`, later ones to its global list `out`
+// (the LDS part follows there only if the workgroup has no compact list).
 template <int KPT>
 SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const float (&acc)[KPT], int n0, uint64_t* out,
                           uint64_t* kc, uint32_t& wc) {
@@ -260,8 +261,11 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
   for (int k = 0; k < KPT; ++k) {
     if (c[k]) {
       const uint64_t x = composite(f2key(acc[k] * kInvSqrtR), (uint32_t)(n0 + k));
-      out[o] = x;
-      if (o < (uint32_t)KL_CAP) kc[o] = x;
+      if (o < (uint32_t)KL_CAP) {
+        kc[o] = x;
+      } else {
+        out[o] = x;
+      }
       ++o;
     }
   }
@@ -309,8 +313,8 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
 
 // Rank scores of a scan wave's nc candidates (composites in the LDS list
 // while they fit, else from the wave's candidate list): one 16-lane DPP row
-// per candidate, 16 candidates in flight per wave; written beside the list
-// and, for the first KL_CAP, to the wave's LDS ranks `kr`.
+// per candidate, 16 candidates in flight per wave; the first KL_CAP to the
+// wave's LDS ranks `kr`, later ones beside the global list.
 // qq: floats 4j .. 4j + 3 of the item's q_low for lane j of each DPP row.
 SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint64_t* kc, float* kr,
                              const uint64_t* out, float* rank, uint32_t nc) {
@@ -335,8 +339,11 @@ SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, c
       const float dot = rank_dot64_row16(rv[u], qq);
       const uint32_t c = c0 + 4 * u + row;
       if (c < nc && j == 0) {
-        rank[c] = dot * kInvSqrtR;
-        if (c < (uint32_t)KL_CAP) kr[c] = dot * kInvSqrtR;
+        if (c < (uint32_t)KL_CAP) {
+          kr[c] = dot * kInvSqrtR;
+        } else {
+          rank[c] = dot * kInvSqrtR;
+        }
       }
     }
   }
@@ -375,10 +382,11 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, Scan
   const int lane = lane_id();
   const int64_t sub = ((int64_t)item * a.W + w) * NW + wid;
   uint64_t* out = a.cand + sub * WAVE_KEYS;
+  float* out_rank = a.cand_rank + sub * WAVE_KEYS;
   uint32_t n_allowed = 0;
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
   scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, L.kc[wid], wc, n_allowed);
-  rank_candidates(p, item, qq, L.kc[wid], L.kr[wid], out, a.cand_rank + sub * WAVE_KEYS, wc);
+  rank_candidates(p, item, qq, L.kc[wid], L.kr[wid], out, out_rank, wc);
   const uint32_t wa = wave_sum_u32(n_allowed);
   if (lane == 0) {
     a.ncand[sub] = wc;
@@ -387,7 +395,8 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, Scan
     L.walw[wid] = wa;
   }
   // the workgroup's compact list: its waves' candidates in wave order (key
-  // order), when there are at most WG_CAP of them; its counts either way
+  // order), when there are at most WG_CAP of them (else each wave's LDS part
+  // completes its global list); its counts either way
   __syncthreads();
   uint32_t off = 0, tot = 0, alw = 0;
 #pragma unroll
@@ -401,6 +410,12 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, Scan
     for (uint32_t j = (uint32_t)lane; j < wc; j += WAVE) {
       a.wg_cand[g * WG_CAP + off + j] = L.kc[wid][j];
       a.wg_rank[g * WG_CAP + off + j] = L.kr[wid][j];
+    }
+  } else {
+    const uint32_t nl = min(wc, (uint32_t)KL_CAP);
+    for (uint32_t j = (uint32_t)lane; j < nl; j += WAVE) {
+      out[j] = L.kc[wid][j];
+      out_rank[j] = L.kr[wid][j];
     }
   }
   if (threadIdx.x == 0) {
@@ -1406,6 +1421,29 @@ SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* l
     if (p.B > 0) p.fin_count[item] = beff;
   }
   if (leff == 0) return 0;
+  if (M >= (uint32_t)leff) {
+    // the per-wave lists of scan workgroups that wrote a compact list hold
+    // only candidates past their wave's first KL_CAP (none: a compact list
+    // has at most WG_CAP < KL_CAP entries): copy the compact list back, one
+    // finish wave per scan workgroup
+    static_assert(WG_CAP < KL_CAP && NW == 4, "a compact list covers whole waves of four");
+    const int wid = t / WAVE;
+    for (int g = wid; g < a.W; g += SNW) {
+      const int64_t gg = (int64_t)item * a.W + g;
+      const uint32_t tot = a.wg_count[2 * gg];
+      if (tot > (uint32_t)WG_CAP) continue;  // uniform: its per-wave lists are whole
+      const uint32_t p1 = ncand[g * NW], p2 = p1 + ncand[g * NW + 1], p3 = p2 + ncand[g * NW + 2];
+      for (uint32_t sidx = (uint32_t)lane; sidx < tot; sidx += WAVE) {
+        const int v = (sidx >= p1) + (sidx >= p2) + (sidx >= p3);
+        const uint32_t o = v == 0 ? 0u : v == 1 ? p1 : v == 2 ? p2 : p3;
+        const int64_t dst = (gg * NW + v) * WAVE_KEYS + (sidx - o);
+        a.cand[dst] = a.wg_cand[gg * WG_CAP + sidx];
+        a.cand_rank[dst] = a.wg_rank[gg * WG_CAP + sidx];
+      }
+    }
+    __threadfence();
+    __syncthreads();
+  }
   // bounds of every candidate composite: sums in [floor, upper bound of any sum]
   const uint64_t c_lo = (uint64_t)f2key(item_floor(p, item) * kInvSqrtR) << 32;
   const uint64_t c_hi = ((uint64_t)f2key(p.range[4 * item + 1] * kInvSqrtR) << 32) | 0xFFFFFFFFull;
