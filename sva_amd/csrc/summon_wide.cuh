@@ -848,12 +848,13 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   load_round(0);
   // the shortlist select's score histogram, filled as the candidates are
   // placed: 4096 bins linear in [floor, bound of any sum] (zeroed while the
-  // loads are in flight)
+  // loads are in flight; the bounds are read before the barrier, which no
+  // load may cross)
+  const float vlo = item_floor(p, item) * kInvSqrtR;
+  const float vinv = lin_scale(vlo, p.range[4 * item + 1] * kInvSqrtR);
   uint32_t* hist = (uint32_t*)(lds + kFastHist);
   reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
-  const float vlo = item_floor(p, item) * kInvSqrtR;
-  const float vinv = lin_scale(vlo, p.range[4 * item + 1] * kInvSqrtR);
   uint32_t loc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1848,16 +1849,19 @@ inline size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B 
 template <int VD, int VKV>
 __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
-  __shared__ float qsh[VD > 0 ? VD : 1];  // the verifier's query row, requested before the finish starts
+  __shared__ float qsh[VD > 0 ? VD : 1];  // the verifier's query row
   const int item = blockIdx.x % a.items, slice = blockIdx.x / a.items;
-  if (VD > 0 && (int)threadIdx.x < VD)
-    qsh[threadIdx.x] = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
+  // the query row is requested before the finish starts and parked in LDS
+  // after it (a store now would wait for the load ahead of the finish's own)
+  float qv = 0.0f;
+  if (VD > 0 && (int)threadIdx.x < VD) qv = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
   if (slice == 0 && threadIdx.x == 0 && a.overshoot != nullptr) a.overshoot[item] = 0;  // the all-keys select sets 1
   const bool keep = VD > 0 && a.p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
   const int done = finish_item(a, item, slice, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
   if (done < 0) return;  // block-uniform
   if (VD > 0) {
-    __syncthreads();  // the budget list (LDS or global) and the LDS the finish used
+    if ((int)threadIdx.x < VD) qsh[threadIdx.x] = qv;
+    __syncthreads();  // the query row, the budget list (LDS or global) and the LDS the finish used
     verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, done == 1, qsh);
   }
 }
