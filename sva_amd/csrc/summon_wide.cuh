@@ -240,6 +240,13 @@ SVA_DEV float item_floor(const SummonParams& p, int item) {
   return est > lo ? est : lo;
 }
 
+// LDS views of a scan wave's candidate lists.  A store that goes either to
+// LDS or to global memory would otherwise be merged into one flat store, and
+// a flat store makes the next round wait for every code load still in flight
+// (a flat store may complete through either counter).
+typedef __attribute__((address_space(3))) uint64_t lds_u64;
+typedef __attribute__((address_space(3))) float lds_f32;
+
 // Appends the flagged keys of one round (key n0 + k for flag c[k]) to the
 // wave's candidate list in ascending key order (lanes in order, each lane's
 // keys in order), as composites of the exact score acc / sqrt(R): the first
@@ -262,7 +269,7 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
     if (c[k]) {
       const uint64_t x = composite(f2key(acc[k] * kInvSqrtR), (uint32_t)(n0 + k));
       if (o < (uint32_t)KL_CAP) {
-        kc[o] = x;
+        ((lds_u64*)kc)[o] = x;
       } else {
         out[o] = x;
       }
@@ -340,7 +347,7 @@ SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, c
       const uint32_t c = c0 + 4 * u + row;
       if (c < nc && j == 0) {
         if (c < (uint32_t)KL_CAP) {
-          kr[c] = dot * kInvSqrtR;
+          ((lds_f32*)kr)[c] = dot * kInvSqrtR;
         } else {
           rank[c] = dot * kInvSqrtR;
         }
