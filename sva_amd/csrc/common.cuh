@@ -127,18 +127,6 @@ SVA_DEV bool mask_allows(const void* mask, int64_t i, int mtype) {
 
 SVA_DEV int lane_id() { return (int)__lane_id(); }
 
-SVA_DEV float wave_sum(float v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
-}
-SVA_DEV float wave_max(float v) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
-  return v;
-}
-SVA_DEV uint32_t wave_sum_u32(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
-}
 
 // DPP row shifts (a DPP row is 16 lanes): lane j receives lane j - N of its
 // row.  Lanes with no source lane receive 0 (row_shr0) or keep their own
@@ -175,6 +163,26 @@ SVA_DEV uint32_t wave_sum_dpp(uint32_t v) {
   v += row_shr0<8>(v);
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 15) + (uint32_t)__builtin_amdgcn_readlane((int)v, 31) +
          (uint32_t)__builtin_amdgcn_readlane((int)v, 47) + (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Sum and maximum of a float over the wave (all 64 lanes active),
+// wave-uniform: DPP row folds, then the four row results in a fixed order
+// (short dependent steps instead of a chain of cross-lane permutes).
+SVA_DEV float wave_sum(float v) {
+  v = v + __int_as_float((int)row_shr0<1>((uint32_t)__float_as_int(v)));
+  v = v + __int_as_float((int)row_shr0<2>((uint32_t)__float_as_int(v)));
+  v = v + __int_as_float((int)row_shr0<4>((uint32_t)__float_as_int(v)));
+  v = v + __int_as_float((int)row_shr0<8>((uint32_t)__float_as_int(v)));
+  const auto rl = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+  return ((rl(v, 15) + rl(v, 31)) + rl(v, 47)) + rl(v, 63);
+}
+SVA_DEV float wave_max(float v) {
+  v = fmaxf(v, __int_as_float((int)row_shr_keep<1>((uint32_t)__float_as_int(v))));
+  v = fmaxf(v, __int_as_float((int)row_shr_keep<2>((uint32_t)__float_as_int(v))));
+  v = fmaxf(v, __int_as_float((int)row_shr_keep<4>((uint32_t)__float_as_int(v))));
+  v = fmaxf(v, __int_as_float((int)row_shr_keep<8>((uint32_t)__float_as_int(v))));
+  const auto rl = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+  return fmaxf(fmaxf(rl(v, 15), rl(v, 31)), fmaxf(rl(v, 47), rl(v, 63)));
 }
 
 // Row shift within each 16-lane DPP row: lane j receives lane j + N of its

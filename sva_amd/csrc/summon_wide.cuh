@@ -394,7 +394,7 @@ SVA_DEV void scan_chunk(const WideArgs& a, int item, int w, float* tab_lds, Scan
   uint32_t wc = 0;  // candidates of this wave so far (wave-uniform)
   scan_rounds<S, SMALLC, CHECK, MASKED>(p, raw, T, t_lo, cs, ce, out, L.kc[wid], wc, n_allowed);
   rank_candidates(p, item, qq, L.kc[wid], L.kr[wid], out, out_rank, wc);
-  const uint32_t wa = wave_sum_u32(n_allowed);
+  const uint32_t wa = CHECK ? wave_sum_dpp(n_allowed) : (uint32_t)(WAVE * KEYS_PT);  // every key allowed
   if (lane == 0) {
     a.ncand[sub] = wc;
     a.nallow[sub] = wa;

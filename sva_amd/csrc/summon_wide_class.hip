@@ -11,8 +11,9 @@ namespace {
 // Every phase keeps its loads in flight together: the counts were written
 // by workgroups on other XCDs, so each dependent round trip is long.
 __global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
-  __shared__ uint32_t key[256], tot[256], flags[256], part[CSEL_G][256], abv[CSEL_G][256], eqv[CSEL_G][256];
+  __shared__ __align__(16) uint32_t key[256], tot[256], flags[256], part[CSEL_G][256], gep[CSEL_G][256];
   __shared__ uint32_t scratch[SNW + 1], res[4];
+  __shared__ uint64_t bmin;
   __shared__ uint32_t sa[CLASS_MAX_W], sb[CLASS_MAX_W];
   const SummonParams& p = a.p;
   const int item = blockIdx.x, t = threadIdx.x, W = a.W;
@@ -37,6 +38,8 @@ __global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
   if (t == 0) {
     res[0] = 0xFFFFFFFFu;  // no boundary class (empty shortlist): no key matches
     res[1] = 0u;
+    res[2] = 0u;  // keys strictly above the boundary class
+    bmin = ~0ull;
   }
   __syncthreads();
   if (t < 256) {
@@ -48,35 +51,41 @@ __global__ void __launch_bounds__(SB) class_select_kernel(ClassArgs a) {
   __syncthreads();
   uint32_t A = 0;
   for (int q = 0; q < 256; q += 64) A += tot[q + lane_id()];  // every wave sums all 256 totals
-  A = wave_sum_u32(A);
+  A = wave_sum_dpp(A);
   const int leff = (int)min((uint32_t)p.L, A);
-  // keys strictly above code c's class and in it: group g over codes [64 g, 64 g + 64)
+  // keys in or above code c's class, ge(c): group g over codes [64 g, 64 g + 64)
   {
     const uint32_t k = key[c];
-    uint32_t above = 0, eq = 0;
-    for (int q = 64 * g; q < 64 * g + 64; ++q) {
-      const uint32_t kq = key[q], tq = tot[q];
-      above += kq > k ? tq : 0u;
-      eq += kq == k ? tq : 0u;
-    }
-    abv[g][c] = above;
-    eqv[g][c] = eq;
-  }
-  __syncthreads();
-  if (t < 256) {
-    uint32_t above = 0, eq = 0;
+    const uint4* k4 = reinterpret_cast<const uint4*>(key + 64 * g);
+    const uint4* t4 = reinterpret_cast<const uint4*>(tot + 64 * g);
+    uint32_t ge = 0;
 #pragma unroll
-    for (int q = 0; q < CSEL_G; ++q) {
-      above += abv[q][t];
-      eq += eqv[q][t];
+    for (int i = 0; i < 16; ++i) {  // both operands read before the select: no per-element branch
+      const uint4 kq = k4[i], tq = t4[i];
+      ge += (kq.x >= k ? tq.x : 0u) + (kq.y >= k ? tq.y : 0u) + (kq.z >= k ? tq.z : 0u) + (kq.w >= k ? tq.w : 0u);
     }
-    if (tot[t] > 0 && above < (uint32_t)leff && above + eq >= (uint32_t)leff) {
-      res[0] = key[t];  // every code of the boundary class writes the same values
-      res[1] = (uint32_t)leff - above;
+    gep[g][c] = ge;
+  }
+  __syncthreads();
+  // ge falls as the key rises.  The boundary class is the one of lowest ge
+  // among the classes holding keys with ge >= leff; the keys strictly above
+  // it number the largest ge below leff (0 if none).
+  if (t < 256 && leff > 0) {  // waves 0-3: every lane active
+    uint32_t ge = 0;
+#pragma unroll
+    for (int q = 0; q < CSEL_G; ++q) ge += gep[q][t];
+    const uint64_t cand = tot[t] > 0 && ge >= (uint32_t)leff ? ((uint64_t)ge << 32) | key[t] : ~0ull;
+    const uint64_t lowest = ~wave_max_u64(~cand);
+    uint32_t mn = 0u, below = ge < (uint32_t)leff ? ge : 0u;
+    wave_min_max_u32(mn, below);
+    if (lane_id() == 0) {
+      atomicMin(&bmin, lowest);
+      atomicMax(&res[2], below);
     }
   }
   __syncthreads();
-  const uint32_t kb = res[0], need = res[1];
+  const uint32_t kb = leff > 0 ? (uint32_t)bmin : res[0];
+  const uint32_t need = leff > 0 ? (uint32_t)leff - res[2] : res[1];
   if (t < 256) flags[t] = (key[t] > kb ? 1u : 0u) | (key[t] == kb ? 2u : 0u);
   __syncthreads();
   // per chunk: kept keys above the boundary class, keys of the boundary class; 16 lanes per chunk, each
