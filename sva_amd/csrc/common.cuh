@@ -165,6 +165,23 @@ SVA_DEV uint32_t wave_sum_dpp(uint32_t v) {
          (uint32_t)__builtin_amdgcn_readlane((int)v, 47) + (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Sums over the 4 lanes of each quad and over the 8 lanes of each half-row,
+// in every lane of the group (DPP quad permutes [1,0,3,2] and [2,3,0,1],
+// then the half-row mirror, which pairs the two quads once each holds its
+// own sum): the same pairings, and so the same results, as xor shuffles
+// with masks 1, 2 and 4, without a cross-lane permute's round trip.
+SVA_DEV uint32_t quad_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  return v;
+}
+SVA_DEV float octet_sum(float v) {
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 // Sum and maximum of a float over the wave (all 64 lanes active),
 // wave-uniform: DPP row folds, then the four row results in a fixed order
 // (short dependent steps instead of a chain of cross-lane permutes).

@@ -786,7 +786,7 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], in
       if (m != 0ull) {
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd(&f.res(3), (uint32_t)__popcll(m));
-        base = (uint32_t)__shfl((int)base, 0, WAVE);
+        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);  // every lane is active here
         if (in) {
           small[base + lanes_below(m)] = e[i];
           if (FUSE) rf->smallr[base + lanes_below(m)] = (*rv)[i];
@@ -801,8 +801,7 @@ SVA_DEV uint64_t fast_select(const uint64_t (&e)[NPD], const float (&v)[NPD], in
     const uint64_t x = g < (int)cnt ? small[g] : 0ull;
     uint32_t greater = 0;
     for (int o = q; o < (int)cnt; o += 4) greater += small[o] > x ? 1u : 0u;
-    greater += __shfl_xor(greater, 1, WAVE);
-    greater += __shfl_xor(greater, 2, WAVE);
+    greater = quad_sum(greater);
     if (q == 0 && g < (int)cnt && greater == need - 1u) f.res64() = x;
     if (FUSE && q == 0 && g < (int)cnt && greater < need)  // a selected boundary member
       atomicAdd(&rf->rhist[lin_bin(rf->smallr[g], rf->rlo, rf->rinv)], 1u);
@@ -1765,9 +1764,8 @@ SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, 
       float dot = 0.0f;
 #pragma unroll
       for (int i = 0; i < EPL; ++i) dot = __builtin_fmaf(kk[k][i], qv[i], dot);
-      dot += __shfl_xor(dot, 1, VLPR);
-      dot += __shfl_xor(dot, 2, VLPR);
-      dot += __shfl_xor(dot, 4, VLPR);
+      static_assert(VLPR == 8, "a K row over the 8 lanes of a half-row");
+      dot = octet_sum(dot);
       const int e = r0 + k * RPI + lane / VLPR;
       sc[k] = e < cnt ? dot * v.scaling : -INFINITY;
       mr = fmaxf(mr, sc[k]);
