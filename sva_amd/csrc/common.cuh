@@ -50,6 +50,18 @@ SVA_DEV float load_elem(const void* p, int64_t i, int dtype) {
   return __half2float(((const __half*)p)[i]);
 }
 
+// Element i's raw bits (all 32 for F32, the low 16 for BF16 / F16) and their
+// value: a load whose result is not used at once, so that loads issued after
+// it do not wait for it (a conversion on the load's own branch would).
+SVA_DEV uint32_t load_elem_bits(const void* p, int64_t i, int dtype) {
+  return dtype == F32 ? ((const uint32_t*)p)[i] : (uint32_t)((const uint16_t*)p)[i];
+}
+SVA_DEV float elem_from_bits(uint32_t b, int dtype) {
+  return dtype == F32    ? __uint_as_float(b)
+         : dtype == BF16 ? __uint_as_float(b << 16)
+                         : __half2float(__ushort_as_half((unsigned short)(b & 0xFFFFu)));
+}
+
 // Four consecutive elements of a K/V row as floats.
 SVA_DEV void load4(const void* base, int64_t e, int dtype, bool vec, float (&v)[4]) {
   if (vec) {

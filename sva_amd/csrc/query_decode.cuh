@@ -54,7 +54,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * 4096);
 #pragma unroll
   for (int i = 0; i < NW4; ++i) wv[i] = w4[t + i * NT];
-  const float qv = t < 64 ? load_elem(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0.0f;
+  const uint32_t qbits = t < 64 ? load_elem_bits(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0u;
   float4 row[EPT][SUB / 4];
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
@@ -68,21 +68,25 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   const int n_words = nb * 2 * S;  // 32 keys x S bytes per block = 2 S words
   const int64_t N = p.n_keys;
   constexpr int QW = qd_words<S, NT>();
+  // every lane loads a word (past the sample, the last one again): a load
+  // under a per-lane condition ends in a register merge that waits for it,
+  // and for every load issued before it; the sums of words past the sample
+  // are discarded
   u32x4_t words[QW];
   if (k_rank > 0) {
     const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-      const int gw = t + i * NT;
+      const int gw = min(t + i * NT, n_words - 1);
       const int b = gw / (2 * S), wi = gw % (2 * S);
       const int64_t n0 = ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15;
-      words[i] = gw < n_words ? *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16) : u32x4_t{0u, 0u, 0u, 0u};
+      words[i] = *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16);
     }
   }
   const float sc = p.scale[h];
 #pragma unroll
   for (int i = 0; i < NW4; ++i) reinterpret_cast<float4*>(W)[t + i * NT] = wv[i];
-  if (t < 64) qf[t] = qv;
+  if (t < 64) qf[t] = elem_from_bits(qbits, p.q_dtype);
   if (t < S) {
     kmin[t] = 0xFFFFFFFFu;
     kmax[t] = 0u;
@@ -160,7 +164,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
     float sums[QW * KPW];
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-      const bool valid = t + i * NT < n_words;  // invalid words are zero: their reads stay in bounds
+      const bool valid = t + i * NT < n_words;  // every code is clamped to the table: reads stay in bounds
 #pragma unroll
       for (int q = 0; q < KPW; ++q) {
         float acc = 0.0f;

@@ -1858,14 +1858,14 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   const int item = blockIdx.x % a.items, slice = blockIdx.x / a.items;
   // the query row is requested before the finish starts and parked in LDS
   // after it (a store now would wait for the load ahead of the finish's own)
-  float qv = 0.0f;
-  if (VD > 0 && (int)threadIdx.x < VD) qv = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
+  uint32_t qbits = 0u;
+  if (VD > 0 && (int)threadIdx.x < VD) qbits = load_elem_bits(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
   if (slice == 0 && threadIdx.x == 0 && a.overshoot != nullptr) a.overshoot[item] = 0;  // the all-keys select sets 1
   const bool keep = VD > 0 && a.p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
   const int done = finish_item(a, item, slice, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
   if (done < 0) return;  // block-uniform
   if (VD > 0) {
-    if ((int)threadIdx.x < VD) qsh[threadIdx.x] = qv;
+    if ((int)threadIdx.x < VD) qsh[threadIdx.x] = elem_from_bits(qbits, a.fv.q_dtype);
     __syncthreads();  // the query row, the budget list (LDS or global) and the LDS the finish used
     verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, done == 1, qsh);
   }
@@ -2049,7 +2049,8 @@ __global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
   __shared__ float qsh[VD > 0 ? VD : 1];
   const SummonParams& p = a.p;
   const int item = blockIdx.x, t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
-  if (VD > 0 && t < VD) qsh[t] = load_elem(a.fv.q, (int64_t)item * a.fv.q_hs + t, a.fv.q_dtype);
+  // the verifier's query row: requested now, parked in LDS before the verifier
+  const uint32_t qbits = VD > 0 && t < VD ? load_elem_bits(a.fv.q, (int64_t)item * a.fv.q_hs + t, a.fv.q_dtype) : 0u;
   const int leff = (int)a.bound[4 * item + 2];
   const int beff = min(p.B, leff);
   if (t == 0) p.fin_count[item] = beff;
@@ -2131,6 +2132,7 @@ __global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
     }
   }
   if (VD > 0) {
+    if (t < VD) qsh[t] = elem_from_bits(qbits, a.fv.q_dtype);
     __syncthreads();
     verify_item<(VD > 0 ? VD : 64), VKV>(p, a.fv, item, lds, keep_kid, qsh);
   }
