@@ -825,30 +825,29 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const int lane = lane_id();
   const int wid = t / WAVE;
   const int64_t g0 = (int64_t)item * W;
+  // Every load below is issued unconditionally (indices clamped to the last
+  // list, values past it ignored): a load under a condition leaves the
+  // compiler unsure how many loads follow an earlier one, and it then waits
+  // for all of them where it needs the first.
   // list counts: lane j holds lists 4j .. 4j + 3
-  uint32_t tot[4], lsum = 0, asum = 0;
-  bool over = false;
+  uint32_t cnt_raw[4], alw_raw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int l = 4 * lane + i;
-    tot[i] = l < W ? a.wg_count[2 * (g0 + l)] : 0u;
-    asum += l < W ? a.wg_count[2 * (g0 + l) + 1] : 0u;
+    const int l = min(4 * lane + i, W - 1);
+    cnt_raw[i] = a.wg_count[2 * (g0 + l)];
+    alw_raw[i] = a.wg_count[2 * (g0 + l) + 1];
   }
   // the first round of this wave's lists (16 k + wid, k < FAST_BATCH), issued
   // with the counts: the first WAVE slots of each list (a list's later slots,
-  // rarely filled, are requested once its count shows them used)
+  // rarely filled, are requested after every list's first slots are placed)
   uint64_t comp[FAST_BATCH];
   float rank[FAST_BATCH];
   auto load_round = [&](int r) {
 #pragma unroll
     for (int k = 0; k < FAST_BATCH; ++k) {
-      const int l = SNW * (r * FAST_BATCH + k) + wid;
-      comp[k] = 0ull;
-      rank[k] = 0.0f;
-      if (l < W) {
-        comp[k] = a.wg_cand[(g0 + l) * WG_CAP + lane];
-        rank[k] = a.wg_rank[(g0 + l) * WG_CAP + lane];
-      }
+      const int l = min(SNW * (r * FAST_BATCH + k) + wid, W - 1);
+      comp[k] = a.wg_cand[(g0 + l) * WG_CAP + lane];
+      rank[k] = a.wg_rank[(g0 + l) * WG_CAP + lane];
     }
   };
   load_round(0);
@@ -861,9 +860,13 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   uint32_t* hist = (uint32_t*)(lds + kFastHist);
   reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
   __syncthreads();
-  uint32_t loc[4];
+  uint32_t tot[4], loc[4], lsum = 0, asum = 0;
+  bool over = false;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const bool in = 4 * lane + i < W;
+    tot[i] = in ? cnt_raw[i] : 0u;
+    asum += in ? alw_raw[i] : 0u;
     loc[i] = lsum;
     lsum += tot[i];
     over = over || tot[i] > (uint32_t)WG_CAP;
@@ -888,6 +891,14 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const uint32_t my_off = base + (el == 0 ? loc[0] : el == 1 ? loc[1] : el == 2 ? loc[2] : loc[3]);
   const uint32_t my_tot = el == 0 ? tot[0] : el == 1 ? tot[1] : el == 2 ? tot[2] : tot[3];
   uint32_t rkmin = 0xFFFFFFFFu, rkmax = 0u;  // rank keys placed by this lane
+  auto place = [&](uint32_t at, uint64_t x, float rx) {
+    lcomp[at] = x;
+    lrank[at] = rx;
+    atomicAdd(&hist[lin_bin(key2f((uint32_t)(x >> 32)), vlo, vinv)], 1u);
+    rkmin = min(rkmin, f2key(rx));
+    rkmax = max(rkmax, f2key(rx));
+  };
+  bool tails = false;  // some list of this wave holds more than WAVE candidates
   for (int r = 0; r * FAST_BATCH * SNW < W; ++r) {
     if (r > 0) load_round(r);
 #pragma unroll
@@ -897,23 +908,18 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
         const int src = l >> 2;
         const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
         const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
-        if ((uint32_t)lane < c) {
-          lcomp[o + lane] = comp[k];
-          lrank[o + lane] = rank[k];
-          atomicAdd(&hist[lin_bin(key2f((uint32_t)(comp[k] >> 32)), vlo, vinv)], 1u);
-          rkmin = min(rkmin, f2key(rank[k]));
-          rkmax = max(rkmax, f2key(rank[k]));
-        }
-        for (uint32_t j = WAVE + lane; j < c; j += WAVE) {  // a list beyond its first WAVE slots
-          const uint64_t x = a.wg_cand[(g0 + l) * WG_CAP + j];
-          const float rj = a.wg_rank[(g0 + l) * WG_CAP + j];
-          lcomp[o + j] = x;
-          lrank[o + j] = rj;
-          atomicAdd(&hist[lin_bin(key2f((uint32_t)(x >> 32)), vlo, vinv)], 1u);
-          rkmin = min(rkmin, f2key(rj));
-          rkmax = max(rkmax, f2key(rj));
-        }
+        if ((uint32_t)lane < c) place(o + lane, comp[k], rank[k]);
+        tails = tails || c > (uint32_t)WAVE;
       }
+    }
+  }
+  if (tails) {  // uniform: the slots past WAVE of this wave's long lists
+    for (int l = wid; l < W; l += SNW) {
+      const int src = l >> 2;
+      const uint32_t o = (uint32_t)__shfl((int)my_off, src, WAVE);
+      const uint32_t c = (uint32_t)__shfl((int)my_tot, src, WAVE);
+      for (uint32_t j = WAVE + lane; j < c; j += WAVE)
+        place(o + j, a.wg_cand[(g0 + l) * WG_CAP + j], a.wg_rank[(g0 + l) * WG_CAP + j]);
     }
   }
   wave_min_max_u32(rkmin, rkmax);
