@@ -816,7 +816,7 @@ SVA_DEV float lin_scale(float lo, float hi) { return hi > lo ? 4096.0f / (hi - l
 // The fast finish of an item; false (uniformly, before any output or LDS
 // write) when its conditions do not hold.
 SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32_t* rkb, uint32_t* wcnt,
-                         uint32_t* scratch, const TopLds& tl, int32_t* kidl) {
+                         uint32_t* scratch, const TopLds& tl, int32_t* kidl, int& beff_out) {
 #pragma clang fp contract(off)
   const SummonParams& p = a.p;
   const int W = a.W;
@@ -876,6 +876,7 @@ SVA_DEV bool finish_fast(const WideArgs& a, int item, unsigned char* lds, uint32
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
   if (overflow || M > (uint32_t)FAST_M || M < (uint32_t)leff) return false;
+  beff_out = p.B > 0 ? beff : 0;
   if (t == 0) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
@@ -1371,7 +1372,7 @@ SVA_DEV void merge_slices(const WideArgs& a, int item, uint32_t leff, unsigned c
 // (budget list in LDS) or 0 (in the budget output) when this workgroup
 // finished the item, -1 when it has nothing more to do (a slice workgroup
 // whose item's floor held, or that did not complete the item's last slice).
-SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* lds, int32_t* kidl) {
+SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* lds, int32_t* kidl, int& beff_out) {
 #pragma clang fp contract(off)
   uint64_t* cl = (uint64_t*)lds;                                   // staged candidates [LDS_CAND]
   uint32_t* hist = (uint32_t*)(lds + kFinHist);                    // overlays, once staging is done
@@ -1387,7 +1388,7 @@ SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* l
   uint32_t* loff = (uint32_t*)(lds + kFinLoff);
   const TopLds tl{hist, small, scratch, shared, shared64};
   const SummonParams& p = a.p;
-  if (slice == 0 && finish_fast(a, item, lds, rkb, wcnt, scratch, tl, kidl)) return kidl != nullptr ? 1 : 0;
+  if (slice == 0 && finish_fast(a, item, lds, rkb, wcnt, scratch, tl, kidl, beff_out)) return kidl != nullptr ? 1 : 0;
   const int t = threadIdx.x;
   const int lane = lane_id();
   const int nsub = a.W * NW;
@@ -1429,6 +1430,7 @@ SVA_DEV int finish_item(const WideArgs& a, int item, int slice, unsigned char* l
   const int leff = (int)min((uint32_t)p.L, A);
   const int beff = min(p.B, leff);
   if (slice > 0 && (leff == 0 || M >= (uint32_t)leff)) return -1;  // the floor held: slice 0 finishes
+  beff_out = p.B > 0 ? beff : 0;
   if (t == 0) {
     p.sl_count[item] = leff;
     if (p.B > 0) p.fin_count[item] = beff;
@@ -1704,7 +1706,7 @@ SVA_DEV float kv_one(const void* base, int64_t e) {
 
 template <int D, int KV>
 SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, unsigned char* lds, bool kid_in_lds,
-                         const float* qsh) {
+                         const float* qsh, int budget) {
 #pragma clang fp contract(off)
   const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
   constexpr int EPL = D / VLPR;      // K elements per lane of a row
@@ -1722,7 +1724,7 @@ SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, 
     part = (float*)lds;
     kid = (int32_t*)(part + SNW * (D + 2));
   }
-  const int cnt = min(max(p.fin_count[item], 0), p.B);
+  const int cnt = min(max(budget, 0), p.B);  // the budget list's length, as the caller wrote it
   const int g = item / (p.H / v.G);
   const int64_t kvb = (int64_t)g * v.kv_hs;
   const int sub = lane & (VLPR - 1);
@@ -1868,12 +1870,13 @@ __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   if (VD > 0 && (int)threadIdx.x < VD) qbits = load_elem_bits(a.fv.q, (int64_t)item * a.fv.q_hs + threadIdx.x, a.fv.q_dtype);
   if (slice == 0 && threadIdx.x == 0 && a.overshoot != nullptr) a.overshoot[item] = 0;  // the all-keys select sets 1
   const bool keep = VD > 0 && a.p.B <= kVerifyKidCap - SNW * (VD + 2) - SNW - 1;
-  const int done = finish_item(a, item, slice, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr);
+  int beff = 0;
+  const int done = finish_item(a, item, slice, lds, keep ? (int32_t*)(lds + kVerifyKid) : nullptr, beff);
   if (done < 0) return;  // block-uniform
   if (VD > 0) {
     if ((int)threadIdx.x < VD) qsh[threadIdx.x] = elem_from_bits(qbits, a.fv.q_dtype);
     __syncthreads();  // the query row, the budget list (LDS or global) and the LDS the finish used
-    verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, done == 1, qsh);
+    verify_item<(VD > 0 ? VD : 64), VKV>(a.p, a.fv, item, lds, done == 1, qsh, beff);
   }
 }
 
@@ -2140,7 +2143,7 @@ __global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
   if (VD > 0) {
     if (t < VD) qsh[t] = elem_from_bits(qbits, a.fv.q_dtype);
     __syncthreads();
-    verify_item<(VD > 0 ? VD : 64), VKV>(p, a.fv, item, lds, keep_kid, qsh);
+    verify_item<(VD > 0 ? VD : 64), VKV>(p, a.fv, item, lds, keep_kid, qsh, beff);
   }
 }
 
