@@ -323,13 +323,17 @@ SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S /
 // per candidate, 16 candidates in flight per wave; the first KL_CAP to the
 // wave's LDS ranks `kr`, later ones beside the global list.
 // qq: floats 4j .. 4j + 3 of the item's q_low for lane j of each DPP row.
-SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint64_t* kc, float* kr,
-                             const uint64_t* out, float* rank, uint32_t nc) {
+// LDS_ONLY: every candidate is in the LDS list (nc <= KL_CAP, the usual
+// case): no key is read from global memory, so the row loads of a group wait
+// only for their keys' LDS reads (a possible global key read would make each
+// row load wait for every load before it).
+template <bool LDS_ONLY>
+SVA_DEV void rank_list(const SummonParams& p, int item, const float4 qq, const uint64_t* kc, float* kr,
+                       const uint64_t* out, float* rank, uint32_t nc) {
 #pragma clang fp contract(off)
   const int j = lane_id() & 15;
   const int row = lane_id() >> 4;
   const float* klow = p.k_low + (int64_t)(item % p.H) * p.klow_hs;
-  if (nc > (uint32_t)KL_CAP) __threadfence();  // keys past the LDS list are read back from `out`
   constexpr int RU = 4;
   for (uint32_t c0 = 0; c0 < nc; c0 += 4 * RU) {
     float4 rv[RU];
@@ -337,22 +341,32 @@ SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, c
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const uint32_t c = c0 + 4 * u + row;
-      key[u] = 0u;
-      if (c < nc) key[u] = composite_index(c < (uint32_t)KL_CAP ? kc[c] : out[c]);
-      rv[u] = c < nc ? reinterpret_cast<const float4*>(klow + (int64_t)key[u] * p.R)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      const uint32_t cc = min(c, nc - 1);  // past the list: the last candidate again, its result unused
+      key[u] = composite_index(LDS_ONLY || cc < (uint32_t)KL_CAP ? ((const lds_u64*)kc)[cc] : out[cc]);
+      rv[u] = reinterpret_cast<const float4*>(klow + (int64_t)key[u] * p.R)[j];
     }
 #pragma unroll
     for (int u = 0; u < RU; ++u) {
       const float dot = rank_dot64_row16(rv[u], qq);
       const uint32_t c = c0 + 4 * u + row;
       if (c < nc && j == 0) {
-        if (c < (uint32_t)KL_CAP) {
+        if (LDS_ONLY || c < (uint32_t)KL_CAP) {
           ((lds_f32*)kr)[c] = dot * kInvSqrtR;
         } else {
           rank[c] = dot * kInvSqrtR;
         }
       }
     }
+  }
+}
+
+SVA_DEV void rank_candidates(const SummonParams& p, int item, const float4 qq, const uint64_t* kc, float* kr,
+                             const uint64_t* out, float* rank, uint32_t nc) {
+  if (nc <= (uint32_t)KL_CAP) {
+    rank_list<true>(p, item, qq, kc, kr, out, rank, nc);
+  } else {
+    __threadfence();  // keys past the LDS list are read back from `out`
+    rank_list<false>(p, item, qq, kc, kr, out, rank, nc);
   }
 }
 
