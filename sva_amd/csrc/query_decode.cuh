@@ -72,14 +72,17 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   // under a per-lane condition ends in a register merge that waits for it,
   // and for every load issued before it; the sums of words past the sample
   // are discarded
+  // (with no sample, the first 16 bytes of the map stand in: the loads stay
+  // unconditional, and their words are not used)
   u32x4_t words[QW];
-  if (k_rank > 0) {
-    const uint8_t* head = (const uint8_t*)p.codes + (int64_t)h * p.code_hs;
+  {
+    const bool smp = k_rank > 0;
+    const uint8_t* head = smp ? (const uint8_t*)p.codes + (int64_t)h * p.code_hs : (const uint8_t*)p.q_proj;
 #pragma unroll
     for (int i = 0; i < QW; ++i) {
-      const int gw = min(t + i * NT, n_words - 1);
+      const int gw = smp ? min(t + i * NT, n_words - 1) : 0;
       const int b = gw / (2 * S), wi = gw % (2 * S);
-      const int64_t n0 = ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15;
+      const int64_t n0 = smp ? ((int64_t)b * (N - SAMPLE_KEYS) / (nb - 1)) & ~(int64_t)15 : 0;
       words[i] = *reinterpret_cast<const u32x4_t*>(head + n0 * S + wi * 16);
     }
   }
