@@ -36,7 +36,17 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   static_assert(NT % 256 == 0 && NT <= 1024, "256 or more threads, whole 64-entry table rows per wave");
   constexpr int SUB = 64 / S;
   constexpr int NPAIR = S >= 4 ? S / 2 : 0;
-  constexpr int EPT = (S * CMAX + NT - 1) / NT;  // table entries per thread
+  // With at least two threads per table entry, two consecutive lanes share a
+  // codebook row, PART floats each, instead of every lane loading a whole
+  // row (the surplus lanes the last row again); the row's fma chain runs
+  // through the pair in order (a DPP hand-off), and the second lane ends
+  // with it.  (Four lanes per row measured slower at 4x64: the longer
+  // hand-off chain costs more than the loads it saves.)
+  constexpr int TPR = NT >= 2 * S * CMAX ? 2 : 1;
+  constexpr int PART = SUB / TPR;
+  static_assert(TPR == 1 || TPR == 2 || TPR == 4, "a row over 1, 2 or 4 lanes of a DPP row");
+  static_assert(PART % 4 == 0, "whole float4s per lane");
+  constexpr int EPT = (S * CMAX * TPR + NT - 1) / NT;  // row parts per thread
   constexpr int NW4 = 1024 / NT;                  // float4s of the map per thread
   constexpr int KPW = 16 / S;                     // keys per 16-byte code word
   __shared__ __align__(16) float W[64 * 64];
@@ -55,13 +65,14 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
 #pragma unroll
   for (int i = 0; i < NW4; ++i) wv[i] = w4[t + i * NT];
   const uint32_t qbits = t < 64 ? load_elem_bits(p.q, (int64_t)h * p.q_hs + t, p.q_dtype) : 0u;
-  float4 row[EPT][SUB / 4];
+  float4 row[EPT][PART / 4];
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = min(t + k * NT, S * C - 1);
-    const float4* c4 = reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB);
+    const int e = min((t + k * NT) / TPR, S * C - 1);
+    const float4* c4 =
+        reinterpret_cast<const float4*>(p.codebooks + ((int64_t)h * S * C + e) * SUB + (t % TPR) * PART);
 #pragma unroll
-    for (int j = 0; j < SUB / 4; ++j) row[k][j] = c4[j];
+    for (int j = 0; j < PART / 4; ++j) row[k][j] = c4[j];
   }
   const int k_rank = p.codes != nullptr ? p.sample_k : 0;
   const int nb = p.sample_blocks;
@@ -112,16 +123,23 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   // bounds fold over the wave first (one atomic per wave, not per entry)
   float* lut_out = p.lut + (int64_t)h * S * C;
   const bool wave_sub = C % WAVE == 0;
+  const int g = t % TPR;  // this lane's part of its row
 #pragma unroll
   for (int k = 0; k < EPT; ++k) {
-    const int e = t + k * NT;
+    const int e = (t + k * NT) / TPR;
     const int s = min(e, S * C - 1) / C;
     uint32_t kl = 0xFFFFFFFFu, kh = 0u;
-    if (e < S * C) {
-      const float* rr = reinterpret_cast<const float*>(row[k]);
-      float acc = 0.0f;
+    const float* rr = reinterpret_cast<const float*>(row[k]);
+    float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < SUB; ++j) acc = __builtin_fmaf(ql[s * SUB + j], rr[j], acc);
+    for (int step = 0; step < TPR; ++step) {
+      // lane g's chain is the row's through part g after step g: it takes
+      // lane g - 1's (parts 0 .. g - 1) and continues with its own part
+      if (step > 0) acc = __int_as_float((int)row_shr0<1>((uint32_t)__float_as_int(acc)));
+#pragma unroll
+      for (int j = 0; j < PART; ++j) acc = __builtin_fmaf(ql[s * SUB + g * PART + j], rr[j], acc);
+    }
+    if (e < S * C && g == TPR - 1) {
       tab[e] = acc;
       lut_out[e] = acc;
       kl = kh = f2key(acc);
@@ -130,7 +148,7 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
         atomicMax(&kmax[s], kh);
       }
     }
-    if (wave_sub && k * NT + WAVE * wid < S * C) {  // uniform: the wave's entries exist
+    if (wave_sub && (k * NT + WAVE * wid) / TPR < S * C) {  // uniform: the wave's entries exist
       wave_min_max_u32(kl, kh);
       if (lane == 0) {
         atomicMin(&kmin[s], kl);
