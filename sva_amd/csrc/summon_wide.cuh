@@ -2091,13 +2091,25 @@ __global__ void __launch_bounds__(SB) class_budget_kernel(ClassArgs a) {
   uint64_t rc[NPD];
   float rv[NPD];
   uint32_t rmin = 0xFFFFFFFFu, rmax = 0u;
+  // every slot is requested before any is used, unconditionally (indices
+  // clamped to the buffer's L slots, which needs no load): the list's length
+  // arrives with them instead of ahead of them, and no load waits on another
+  // slot's use (a conditional load would end in a register merge that waits)
+  int32_t kraw[NPD];
+  float rraw[NPD];
+#pragma unroll
+  for (int i = 0; i < NPD; ++i) {
+    const int jj = min(t + i * SB, p.L - 1);
+    kraw[i] = sl[jj];
+    rraw[i] = sr[jj];
+  }
 #pragma unroll
   for (int i = 0; i < NPD; ++i) {
     const int jj = t + i * SB;
     const bool in = i < dslots && jj < leff;
-    rv[i] = in ? sr[jj] : 0.0f;
+    rv[i] = in ? rraw[i] : 0.0f;
     const uint32_t k = f2key(rv[i]);
-    rc[i] = in ? composite(k, (uint32_t)sl[jj]) : 0ull;
+    rc[i] = in ? composite(k, (uint32_t)kraw[i]) : 0ull;
     if (in) {
       rmin = min(rmin, k);
       rmax = max(rmax, k);
