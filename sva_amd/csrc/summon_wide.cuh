@@ -1989,7 +1989,7 @@ constexpr int CSEL_G = SB / 256;              // thread groups over the chunks (
 template <bool MASKED>
 __global__ void __launch_bounds__(WB) class_extract_kernel(ClassArgs a) {
 #pragma clang fp contract(off)
-  __shared__ uint32_t key[256], scratch[NW + 1];
+  __shared__ uint32_t flag[256], scratch[NW + 1];
   __shared__ int32_t kept_keys[CLASS_MAX_L];
   const SummonParams& p = a.p;
   const int item = blockIdx.x / a.W, w = blockIdx.x % a.W;
@@ -1999,26 +1999,35 @@ __global__ void __launch_bounds__(WB) class_extract_kernel(ClassArgs a) {
   const uint8_t* codes = (const uint8_t*)p.codes + (int64_t)(item % p.H) * p.code_hs;
   u32x4 raw[4];
   class_load(codes, k0, ce, raw);
-  key[t] = class_key(p, item, t);
+  const uint32_t kc = class_key(p, item, t);
   const uint32_t kb = a.bound[4 * item], need = a.bound[4 * item + 1], leff = a.bound[4 * item + 2];
+  // code t's class against the boundary class: bit 0 above it, bit 16 in it
+  flag[t] = (kc > kb ? 1u : 0u) | (kc == kb ? 0x10000u : 0u);
   const uint32_t* wo = a.woff + ((int64_t)item * a.W + w) * 2;
   const uint32_t off = wo[0], bpre = wo[1];
   const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * p.R)[lane & 15];
   __syncthreads();
-  // this thread's keys above the boundary class and in it (bit i: key k0 + i)
+  // this thread's keys above the boundary class and in it (bit i: key k0 + i):
+  // each 16-byte word of codes gathers its keys' flags shifted into one word
+  // (above in the low half, in it in the high half), one shift-or per key
   uint64_t am = 0ull, bm = 0ull;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
+    uint32_t fw = 0u;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int i = 16 * r + j;
-      bool ok = k0 + i < ce;
-      if (MASKED && ok) ok = mask_allows(p.mask, k0 + i, p.mask_type);
-      const uint32_t kk = key[byte_of(raw[r], j)];
-      am |= (uint64_t)(ok && kk > kb) << i;
-      bm |= (uint64_t)(ok && kk == kb) << i;
-    }
+    for (int j = 0; j < 16; ++j) fw |= flag[byte_of(raw[r], j)] << j;
+    am |= (uint64_t)(fw & 0xFFFFu) << (16 * r);
+    bm |= (uint64_t)(fw >> 16) << (16 * r);
   }
+  // keys past the cache's end or masked out are in neither set
+  uint64_t okm = k0 + CK_PT <= ce ? ~0ull : (k0 >= ce ? 0ull : (1ull << (ce - k0)) - 1ull);
+  if (MASKED) {
+#pragma unroll
+    for (int i = 0; i < CK_PT; ++i)
+      if (k0 + i < ce && !mask_allows(p.mask, k0 + i, p.mask_type)) okm &= ~(1ull << i);
+  }
+  am &= okm;
+  bm &= okm;
   // boundary keys are kept in key order up to `need` over the whole item
   const uint32_t nb = (uint32_t)__popcll(bm);
   const uint32_t before = bpre + block_excl_scan<WB>(nb, scratch, nullptr);
