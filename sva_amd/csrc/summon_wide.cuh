@@ -1964,14 +1964,22 @@ SVA_DEV void class_count_chunk(const ClassArgs& a, int block) {
 #pragma unroll
   for (int i = 0; i < NW; ++i) hist[i][t] = 0u;
   __syncthreads();
+  if (!MASKED && k0 + CK_PT <= ce) {  // every key of the thread counts: no test per key
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; ++r) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int n = k0 + 16 * r + j;
-      bool ok = n < ce;
-      if (MASKED && ok) ok = mask_allows(p.mask, n, p.mask_type);
-      if (ok) atomicAdd(&hist[wid][byte_of(raw[r], j)], 1u);
+      for (int j = 0; j < 16; ++j) atomicAdd(&hist[wid][byte_of(raw[r], j)], 1u);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int n = k0 + 16 * r + j;
+        bool ok = n < ce;
+        if (MASKED && ok) ok = mask_allows(p.mask, n, p.mask_type);
+        if (ok) atomicAdd(&hist[wid][byte_of(raw[r], j)], 1u);
+      }
     }
   }
   __syncthreads();
