@@ -64,19 +64,21 @@ constexpr int64_t kMaxWideItems = 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// The fields a finish workgroup needs for its first loads lead the argument
+// block, so that they share the scalar-cache lines its first loads fetch.
 struct WideArgs {
+  int W;               // scan workgroups per item
+  int items;           // items of the call
+  uint32_t* wg_count;  // [items, W, 2] candidates and allowed keys of each scan workgroup
+  uint64_t* wg_cand;   // [items, W, WG_CAP] a workgroup's candidates in key order (when they fit)
+  float* wg_rank;      // [items, W, WG_CAP] their rank scores
   SummonParams p;
   uint32_t* ncand;   // [items, W * NW] candidates of each scan wave
   uint32_t* nallow;  // [items, W * NW] allowed keys of each scan wave
   uint64_t* cand;    // [items, W * NW, WAVE_KEYS] candidate composites of each scan wave
   float* cand_rank;  // [items, W * NW, WAVE_KEYS] rank score of each listed candidate
-  uint32_t* wg_count;  // [items, W, 2] candidates and allowed keys of each scan workgroup
-  uint64_t* wg_cand;   // [items, W, WG_CAP] a workgroup's candidates in key order (when they fit)
-  float* wg_rank;      // [items, W, WG_CAP] their rank scores
-  int W;             // scan workgroups per item
   FusedVerify fv;    // fv.out != nullptr: the finish kernel also runs the verifier
   int32_t* overshoot;  // [items] or nullptr: 1 where the sampled floor overshot (all-keys select), else 0
-  int items;           // items of the call
   int K;               // slices of the all-keys select per item (finish grid: items * K workgroups)
   uint32_t* arrive;    // [items] slices of the all-keys select completed (zeroed by the scan kernel)
   uint32_t* slice_n;   // [items, K] entries of each slice list
