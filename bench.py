@@ -734,13 +734,14 @@ def graph_replay(torch, np, args, layers, plan, outs, step):
 
     device = plan.device
     n_layers = len(layers)
-    eager = [o.clone() for o in outs]
     side = torch.cuda.Stream(device)
     side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
         for i in range(n_layers):
             step(i)
     torch.cuda.current_stream(device).wait_stream(side)
+    # the eager outputs of every layer (a short timed run may not have reached them all)
+    eager = [o.clone() for o in outs]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(n_layers):
