@@ -250,7 +250,8 @@ def write_profiles(args):
     (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
     (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
         {"entry_point": entry, "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
-         "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}) + "\n")
+         "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+         "source": f"{stem}_pmc.md", "commands": f"{cmd_pmc}, one run per counter"}) + "\n")
     print(f"wrote profiles/{stem}_*.md/json")
 
 
