@@ -1849,28 +1849,25 @@ SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, 
     for (int d = 0; d < DL; ++d) mine[2 + lane + WAVE * d] = acc[d];
   }
   __syncthreads();
-  // wave factors e^(m_w - M) and the total exp-sum, by the first wave
-  float* fw = part + SNW * (D + 2);  // [SNW + 1]
-  if (wid == 0) {
+  // the merge, by the waves that hold output dimensions (whole waves): each
+  // computes the wave factors e^(m_w - M) and the total exp-sum itself and
+  // takes factor w from lane w, so no second barrier publishes them
+  static_assert(D % WAVE == 0, "output dimensions fill whole waves");
+  if (t < D) {
     const float mw = lane < SNW ? part[lane * (D + 2)] : -INFINITY;
     const float M = wave_max(mw);
     const float f = mw == -INFINITY ? 0.0f : expf(mw - M);
     const float Z = wave_sum(lane < SNW ? f * part[lane * (D + 2) + 1] : 0.0f);
-    if (lane < SNW) fw[lane] = f;
-    if (lane == 0) fw[SNW] = Z;
-  }
-  __syncthreads();
-  if (t < D) {
     float o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < SNW; ++w) o = o + fw[w] * part[w * (D + 2) + 2 + t];
-    const float Z = fw[SNW];
+    for (int w = 0; w < SNW; ++w)
+      o = o + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), w)) * part[w * (D + 2) + 2 + t];
     store_elem(v.out, (int64_t)item * v.o_hs + t, v.out_dtype, (cnt > 0 && Z > 0.0f) ? o / Z : 0.0f);
   }
 }
 
 // LDS the fused verifier needs when the list comes from the budget output.
-inline size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B + SNW * (size_t)(D + 2) + SNW + 1); }
+inline size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B + SNW * (size_t)(D + 2)); }
 
 // Finish of an item, then (VD > 0: head_dim VD, K / V dtype VKV) its
 // verifier.  Workgroup g takes item g % items as slice g / items of the
