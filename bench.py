@@ -479,6 +479,7 @@ def socket_suite(args):
                            model.model.layers[i].self_attn.up.weight.numel() for i in socket)
             sva_s = decode(past, tok)
             summary = handle.stats.summary()
+            summary["floor_overshoots"] = handle.stats.floor_overshoots()
             for i in socket:
                 model.model.layers[i].self_attn = model.model.layers[i].self_attn.sva_attn
     tok_s = batch * args.decode_steps / sva_s
@@ -639,6 +640,7 @@ def model_decode(args, with_cpu: bool):
     with patch_llama_attention(model, bundle, shortlist=2048, budget=512, summon_mode="scan") as handle:
         sva_prefill, sva_decode, past, tok = run()
         summary = handle.stats.summary()
+        summary["floor_overshoots"] = handle.stats.floor_overshoots()
         if with_cpu:
             cpu = cpu_decode_baseline(torch, model, past, tok, args.cpu_decode_steps)
     del past

@@ -248,6 +248,53 @@ int sva_verify_noalloc(const void *q, int q_dtype, int64_t q_seq_stride, int64_t
                        int out_dtype, int64_t out_seq_stride, int64_t out_head_stride, int64_t out_tok_stride,
                        void *stream);
 
+/*
+ * A patched layer's scan-mode decode step (one token of one sequence) behind
+ * a handle, so that a decode loop pays one short call per layer: the catalog
+ * append of the KV cache's new rows, the lookup with its verifier and the
+ * step's statistics.  Replaces, for q_len = 1, the per-call work of
+ * SVALlamaAttention.forward after the KV-cache update: the catalog append
+ * (sva/llama.py:597-616), the lookup and exact verifier (sva/llama.py:211-317)
+ * and the stats accounting (sva/llama.py:319-326).
+ *
+ * sva_decode_layer_create keeps the layer's sizes and weights (q_proj
+ * [H, D, R], scale [H] = clamp(exp(logit_scale), 0.01, 100), codebooks
+ * [H, S, C, R/S], k_proj [H, D, R], all fp32 on the device; the pointers must
+ * stay valid for the handle's life), the shortlist L and budget B, and the
+ * verifier's scaling.
+ *
+ * sva_decode_layer_bind points the handle at its buffers: the catalog
+ * (k_low [H, capacity, R] fp32 and codes [H, capacity, S], as sva_write_encode
+ * writes them), the lookup outputs of sva_lookup_verify (q_low [H, R], lut
+ * [H, S, C], score_range [H, 4], sl_idx [H, L], sl_rank [H, L], counts
+ * int32 [3, H] = shortlist sizes, budget sizes and floor overshoots (the
+ * last row written only by steps whose path has a sampled floor,
+ * sva_summon_strategy 1 or 2), fin_idx [H, B]), its two workspaces and
+ * stats (int64 [4] on the device, or NULL): every step adds the sums of its
+ * shortlist sizes, budget sizes and overshoots, and H, to stats[0..3].  Bind
+ * again when a buffer moves.
+ *
+ * sva_decode_layer_step encodes cache rows [row_begin, n_keys) into the
+ * catalog (keys [G, rows, D] at g * kv_head_stride + n * kv_row_stride), then
+ * runs sva_lookup_verify over the first n_keys rows (no mask: the causal
+ * decode token sees every key) and writes out [H, D] (head stride
+ * out_head_stride).  Stream-ordered; calls on one handle must not overlap.
+ */
+typedef struct sva_decode_layer sva_decode_layer;
+int sva_decode_layer_create(int64_t H, int64_t G, int64_t D, int64_t R, int64_t S, int64_t C, int64_t L, int64_t B,
+                            const float *q_proj, const float *scale, const float *codebooks, const float *k_proj,
+                            float scaling, sva_decode_layer **out);
+int sva_decode_layer_bind(sva_decode_layer *layer, float *k_low, int64_t k_low_head_stride, void *codes,
+                          int code_type, int64_t code_head_stride, int64_t capacity, float *q_low, float *lut,
+                          float *score_range, int32_t *sl_idx, float *sl_rank, int32_t *counts, int32_t *fin_idx,
+                          void *workspace, size_t workspace_bytes, void *verify_workspace,
+                          size_t verify_workspace_bytes, int64_t *stats);
+int sva_decode_layer_step(sva_decode_layer *layer, const void *q, int q_dtype, int64_t q_head_stride,
+                          const void *keys, const void *values, int kv_dtype, int64_t kv_head_stride,
+                          int64_t kv_row_stride, int64_t row_begin, int64_t n_keys, void *out, int out_dtype,
+                          int64_t out_head_stride, void *stream);
+void sva_decode_layer_destroy(sva_decode_layer *layer);
+
 /* ---------------------------------------------------------------------------
  * Inverted-index summon for q = 1 decode (summon_mode "inverted" and
  * "inverted_static").

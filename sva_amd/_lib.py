@@ -70,6 +70,12 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
                         _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P, _SZ, _P]),
     "sva_verify_noalloc": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64,
                                 _I64, _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P]),
+    "sva_decode_layer_create": (_I, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F,
+                                     ctypes.POINTER(_P)]),
+    "sva_decode_layer_bind": (_I, [_P, _P, _I64, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P, _SZ,
+                                   _P]),
+    "sva_decode_layer_step": (_I, [_P, _P, _I, _I64, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I, _I64, _P]),
+    "sva_decode_layer_destroy": (None, [_P]),
 }
 
 

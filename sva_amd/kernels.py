@@ -8,6 +8,7 @@ follow include/sva_hip.h: query items are [n_seq, H, Q], per-head catalogs are
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -358,8 +359,10 @@ class ScanDecodePlan:
         self._bufs = (self.q_low.data_ptr(), self.lut.data_ptr(), self.rng.data_ptr(), self.sl_idx.data_ptr(),
                       self.sl_rank.data_ptr(), self.sl_count.data_ptr(), self.fin_idx.data_ptr(),
                       self.fin_count.data_ptr(), self.overshoot.data_ptr())
-        self._ws, self._ws_keys = None, -1  # summon workspace, sized for caches of up to _ws_keys keys
-        self._vws, self._vws_kv = None, -1  # verify workspace (independent of the cache length)
+        # per stream: (summon workspace, keys it is sized for) and (verify workspace, KV heads), so that one
+        # plan driven from two streams never shares a scratch buffer between them
+        self._ws: dict[int, tuple[torch.Tensor, int]] = {}
+        self._vws: dict[int, tuple[torch.Tensor, int]] = {}
         self._checked_weights = set()  # (data_ptr, version, dtype, shape, strides) of weights that passed
 
     def _check_weights(self, q_proj, scale, codebooks) -> None:
@@ -417,8 +420,8 @@ class ScanDecodePlan:
         L = self._lib
         stream = stream_handle(self.device)
         m, mtype, mstride = mask_args(mask, q_len, n_keys)
-        ws = self._summon_ws(n_keys)
-        vws = self._verify_ws(keys)
+        ws = self._summon_ws(n_keys, stream)
+        vws = self._verify_ws(keys, stream)
         if out is None:
             out = torch.empty(n_seq, heads, q_len, head_dim, device=self.device, dtype=q.dtype)
         if out.stride(-1) != 1 or tuple(out.shape) != (1, heads, 1, head_dim):
@@ -435,23 +438,29 @@ class ScanDecodePlan:
               "sva_lookup_verify")
         return out
 
-    def _summon_ws(self, n_keys: int) -> torch.Tensor:
+    def _summon_ws(self, n_keys: int, stream: int | None = None) -> torch.Tensor:
         n_seq, heads, q_len, _, _, _, _, shortlist, _ = self.shape
-        if n_keys > self._ws_keys:
+        stream = stream_handle(self.device) if stream is None else stream
+        ws, cap = self._ws.get(stream, (None, -1))
+        if n_keys > cap:
             # the summon workspace grows with the key count: sized for the next
             # multiple of 64K keys, so a decode loop re-queries it rarely
-            self._ws_keys = (n_keys + 65535) // 65536 * 65536
-            self._ws = workspace(self.device, int(self._lib.sva_summon_workspace_bytes(
-                n_seq, heads, q_len, self._ws_keys, shortlist)), "plan")
-        return self._ws
+            cap = (n_keys + 65535) // 65536 * 65536
+            ws = workspace(self.device, int(self._lib.sva_summon_workspace_bytes(
+                n_seq, heads, q_len, cap, shortlist)), "plan")
+            self._ws[stream] = (ws, cap)
+        return ws
 
-    def _verify_ws(self, keys) -> torch.Tensor:
+    def _verify_ws(self, keys, stream: int | None = None, kv_heads: int | None = None) -> torch.Tensor:
         n_seq, heads, q_len, head_dim, _, _, _, _, budget = self.shape
-        if self._vws is None or self._vws_kv != keys.shape[0]:
-            self._vws_kv = keys.shape[0]
-            self._vws = workspace(self.device, int(self._lib.sva_verify_workspace_bytes(
-                n_seq, heads, keys.shape[0], q_len, head_dim, budget)), "verify")
-        return self._vws
+        stream = stream_handle(self.device) if stream is None else stream
+        kv_heads = keys.shape[0] if kv_heads is None else kv_heads
+        vws, kv = self._vws.get(stream, (None, -1))
+        if vws is None or kv != kv_heads:
+            vws = workspace(self.device, int(self._lib.sva_verify_workspace_bytes(
+                n_seq, heads, kv_heads, q_len, head_dim, budget)), "verify")
+            self._vws[stream] = (vws, kv_heads)
+        return vws
 
     def _check_kv(self, keys, values, n_keys: int) -> None:
         _, heads, _, head_dim = self.shape[:4]
@@ -516,6 +525,112 @@ class ScanDecodePlan:
                            self.fin_idx.data_ptr(), self.fin_count.data_ptr(), n_seq, heads, keys.shape[0], q_len,
                            head_dim, budget, float(scaling), out.data_ptr(), dtype_code(out), out.stride(0),
                            out.stride(1), out.stride(2), vws.data_ptr(), vws.numel(), stream), "sva_verify")
+        return out
+
+
+class DecodeLayer:
+    """The native decode step of one patched layer (sva_decode_layer_*):
+    catalog append, lookup with verifier and statistics in one C-ABI call per
+    token (sva/llama.py:597-616, :211-317, :319-326).  Uses a ScanDecodePlan's
+    buffers (one token of one sequence); `stats` is the int64 [4] device
+    counter the steps add to (summoned, verified, floor overshoots, queries)."""
+
+    STAT_ROWS = (("summoned",), ("exact_scored", "verified"), ("floor_overshoots",), ("queries",))
+
+    def __init__(self, plan: ScanDecodePlan, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor,
+                 k_proj: torch.Tensor, scaling: float):
+        n_seq, heads, q_len, head_dim, rank, subspaces, codewords, shortlist, budget = plan.shape
+        if n_seq != 1 or q_len != 1:
+            raise ValueError("DecodeLayer runs one token of one sequence")
+        plan._check_weights(q_proj, scale, codebooks)
+        if k_proj.dtype != torch.float32 or not k_proj.is_contiguous() or tuple(k_proj.shape) != (heads, head_dim,
+                                                                                                    rank):
+            raise ValueError(f"DecodeLayer: k_proj must be contiguous fp32 {(heads, head_dim, rank)}")
+        self.plan = plan
+        self.device = plan.device
+        self._weights = (q_proj, scale, codebooks, k_proj)  # kept alive: the handle points at them
+        self.stats = torch.zeros(4, device=self.device, dtype=torch.int64)
+        self._lib = plan._lib
+        self._handle = None  # created at the first step, when the KV head count is known
+        self._scaling = float(scaling)
+        self._kv_heads = -1
+        self._bound: tuple | None = None
+        self._out: torch.Tensor | None = None  # the output buffer a step writes when none is given
+
+    def _create(self, kv_heads: int) -> None:
+        _, heads, _, head_dim, rank, subspaces, codewords, shortlist, budget = self.plan.shape
+        q_proj, scale, codebooks, k_proj = self._weights
+        handle = ctypes.c_void_p()
+        check(self._lib.sva_decode_layer_create(heads, kv_heads, head_dim, rank, subspaces, codewords, shortlist,
+                                                budget, q_proj.data_ptr(), scale.data_ptr(), codebooks.data_ptr(),
+                                                k_proj.data_ptr(), self._scaling, ctypes.byref(handle)),
+              "sva_decode_layer_create")
+        self.close()
+        self._handle = handle.value
+        self._kv_heads = kv_heads
+        self._bound = None
+
+    def close(self) -> None:
+        if self._handle is not None:
+            self._lib.sva_decode_layer_destroy(self._handle)
+            self._handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001  (interpreter shutdown)
+            pass
+
+    def step(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, k_low: torch.Tensor,
+             codes: torch.Tensor, row_begin: int, n_keys: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Encode cache rows [row_begin, n_keys) into the catalog (k_low,
+        codes), look up and verify q [1, H, 1, D] against the first n_keys
+        rows of keys / values ([G, rows, D], or the cache [1, G, rows, D]),
+        and return the output [1, H, 1, D] in q's dtype (written to `out`
+        when given, else to the layer's own buffer, which the next step
+        overwrites)."""
+        plan = self.plan
+        heads, head_dim = plan.shape[1], plan.shape[3]
+        if q.shape != (1, heads, 1, head_dim) or q.stride(-1) != 1:
+            raise ValueError(f"DecodeLayer: q must be [1, {heads}, 1, {head_dim}] with contiguous rows")
+        if keys.dim() == 4:
+            if keys.shape[0] != 1:
+                raise ValueError("DecodeLayer: the cache must hold one sequence")
+        elif keys.dim() != 3:
+            raise ValueError("DecodeLayer: keys / values must be [G, rows, D] or [1, G, rows, D]")
+        if keys.shape[-2] < n_keys or keys.shape[-1] != head_dim or keys.stride(-1) != 1 or \
+                values.stride() != keys.stride() or values.shape != keys.shape or values.dtype != keys.dtype:
+            raise ValueError("DecodeLayer: keys / values must be equal caches with contiguous rows")
+        kv_heads = keys.shape[-3]
+        if kv_heads != self._kv_heads:
+            if heads % kv_heads != 0:
+                raise ValueError(f"DecodeLayer: {heads} query heads over {kv_heads} KV heads")
+            self._create(kv_heads)
+        if out is None:
+            out = self._out
+            if out is None or out.dtype != q.dtype:
+                out = self._out = torch.empty(1, heads, 1, head_dim, device=self.device, dtype=q.dtype)
+        elif out.shape != q.shape or out.stride(-1) != 1:
+            raise ValueError(f"DecodeLayer: out must be [1, {heads}, 1, {head_dim}] with contiguous rows")
+        stream = stream_handle(self.device)
+        ws = plan._summon_ws(n_keys, stream)
+        vws = plan._verify_ws(None, stream, kv_heads)
+        b = self._bound
+        if b is None or b[0] is not k_low or b[1] is not codes or b[2] is not ws or b[3] is not vws:
+            plan._check_catalog(codes, k_low, n_keys)
+            if k_low.device != self.device or codes.device != self.device or keys.device != self.device:
+                raise ValueError("DecodeLayer: catalog and cache must be on the plan's device")
+            check(self._lib.sva_decode_layer_bind(
+                self._handle, k_low.data_ptr(), k_low.stride(0), codes.data_ptr(), code_type(codes),
+                codes.stride(0), min(codes.shape[1], k_low.shape[1]), plan.q_low.data_ptr(), plan.lut.data_ptr(),
+                plan.rng.data_ptr(), plan.sl_idx.data_ptr(), plan.sl_rank.data_ptr(), plan.counts.data_ptr(),
+                plan.fin_idx.data_ptr(), ws.data_ptr(), ws.numel(), vws.data_ptr(), vws.numel(),
+                self.stats.data_ptr()), "sva_decode_layer_bind")
+            self._bound = (k_low, codes, ws, vws)
+        check(self._lib.sva_decode_layer_step(self._handle, q.data_ptr(), dtype_code(q), q.stride(1), keys.data_ptr(),
+                                              values.data_ptr(), dtype_code(keys), keys.stride(-3), keys.stride(-2),
+                                              row_begin, n_keys, out.data_ptr(), dtype_code(out), out.stride(1),
+                                              stream), "sva_decode_layer_step")
         return out
 
 

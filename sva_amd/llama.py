@@ -90,6 +90,9 @@ class SVALlamaAttention(nn.Module):
         self.register_buffer("sva_scale", a.logit_scale.detach().float().exp().clamp(0.01, 100.0).clone(),
                              persistent=False)
         self.register_buffer("sva_coarse_codebooks", a.coarse_codebooks.detach().float().clone(), persistent=False)
+        # the artifact's sizes (fixed for the module's life)
+        self._heads, _, self._rank = (int(x) for x in a.q_proj.shape)
+        self._subspaces, self._codewords = int(a.coarse_codebooks.shape[1]), int(a.coarse_codebooks.shape[2])
         self.reset_catalog()
 
     # ------------------------------------------------------------------
@@ -121,6 +124,7 @@ class SVALlamaAttention(nn.Module):
         self._signature: tuple | None = None
         self._postings: inverted.Postings | None = None
         self._decode_plan: kernels.ScanDecodePlan | None = None  # q = 1 buffers, kept across steps
+        self._decode_layer: kernels.DecodeLayer | None = None    # the native decode step over those buffers
 
     # ------------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
@@ -150,6 +154,13 @@ class SVALlamaAttention(nn.Module):
                       attention_mask: torch.Tensor | None) -> torch.Tensor:
         """query [1, H, Q, D]; key/value [1, G, N, D] (not expanded)."""
 
+        # one scan-mode decode token of one sequence with no mask (the token
+        # sees every key): the native step, behind checks kept lean because
+        # they run for every layer and token
+        if attention_mask is None and query.shape[2] == 1 and query.shape[0] == 1 and \
+                self.serving.summon_mode == "scan" and query.is_cuda and key.is_cuda and value.is_cuda and \
+                key.stride(-1) == 1 and value.stride() == key.stride() and value.shape == key.shape:
+            return self._native_decode(query, key, value)
         batch, n_heads, q_len, head_dim = query.shape
         k_len = key.shape[2]
         kernels.require_device(query, key, value)
@@ -187,12 +198,44 @@ class SVALlamaAttention(nn.Module):
             return inverted.adaptive_decode(self, query, keys, values, k_low, codes, k_len, mask, budget)
         return self._scan_attention(query, keys, values, k_low, codes, k_len, mask, shortlist, budget)
 
+    def _native_decode(self, query, key, value):
+        """One scan-mode decode token (q = 1, no mask: the token sees every
+        key) in one native call, sva_decode_layer_step: the catalog append of
+        the cache's new rows (the append rule of _key_catalog,
+        sva/llama.py:578-624), the lookup with its verifier (:211-317) and the
+        step's statistics (:319-326), summed on the device.  key / value: the
+        cache [1, G, N, D], read in place."""
+
+        k_len = key.shape[2]
+        sig = (key.device, key.dtype, self._heads, key.shape[3], self.serving.rank_dim)
+        can_append = (self._signature == sig and self._k_low is not None and self._key_len > 0
+                      and self._key_len < k_len <= self._key_len + 1)
+        self._ensure_capacity(k_len, key.device)
+        row_begin = min(self._key_len, self._codes_len) if can_append else 0
+        shortlist = min(self.serving.coarse_shortlist, k_len)
+        budget = min(self.serving.budget, shortlist)
+        layer = self._decode_layer
+        if layer is None or layer.plan.shape[-2:] != (shortlist, budget) or layer.device != query.device or \
+                layer.plan.shape[3] != query.shape[3]:
+            shape = (1, self._heads, 1, query.shape[3], self._rank, self._subspaces, self._codewords, shortlist,
+                     budget)
+            plan = self._decode_plan
+            if plan is None or plan.shape != shape or plan.device != query.device:
+                plan = self._decode_plan = kernels.ScanDecodePlan(query.device, *shape)
+            layer = self._decode_layer = kernels.DecodeLayer(plan, self.sva_q_proj, self.sva_scale,
+                                                             self.sva_coarse_codebooks, self.sva_k_proj, self.scaling)
+            if self.stats is not None:
+                self.stats.attach_device_counter(int(self.layer_idx or 0), kernels.DecodeLayer.STAT_ROWS,
+                                                 layer.stats)
+        out = layer.step(query, key, value, self._k_low, self._codes, row_begin, k_len)
+        self._key_len = self._codes_len = k_len
+        self._postings = None
+        self._signature = sig
+        return out
+
     def _scan_attention(self, query, keys, values, k_low, codes, k_len, mask, shortlist, budget):
         """sva/llama.py:226-328 on the HIP path, chunked over query tokens."""
 
-        q_len = query.shape[2]
-        if q_len == 1 and mask is None and query.shape[0] == 1:
-            return self._scan_decode(query, keys, values, k_low, codes, k_len, shortlist, budget)
         outs = []
         for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist):
             qc = query[:, :, qs:qe, :]
@@ -229,25 +272,6 @@ class SVALlamaAttention(nn.Module):
                 yield qs, qe, mask[..., qs:qe, :], k_len
             else:
                 yield qs, qe, None, k_len - q_len + qe
-
-    def _scan_decode(self, query, keys, values, k_low, codes, k_len, shortlist, budget):
-        """One decode token (q = 1, causal): the same three calls through a
-        plan that keeps its buffers across steps."""
-
-        heads, head_dim = query.shape[1], query.shape[3]
-        rank, subspaces, codewords = self.sva_q_proj.shape[2], self.sva_coarse_codebooks.shape[1], \
-            self.sva_coarse_codebooks.shape[2]
-        shape = (1, heads, 1, head_dim, rank, subspaces, codewords, shortlist, budget)
-        plan = self._decode_plan
-        if plan is None or plan.shape != shape or plan.device != query.device:
-            plan = self._decode_plan = kernels.ScanDecodePlan(query.device, *shape)
-        out = plan.run(query, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks, codes, k_low, keys, values,
-                       k_len, self.scaling)
-        if self.stats is not None:
-            self.stats.add_device_rows(int(self.layer_idx or 0),
-                                       (("summoned",), ("exact_scored", "verified"), ("floor_overshoots",)),
-                                       plan.counts, {"queries": float(heads)})
-        return out
 
     def _scan_attention_batched(self, query, key, value, attention_mask):
         """Scan mode for a batch of B equal-length sequences (the reference

@@ -1,10 +1,14 @@
 """Runtime accounting of patched attention layers (sva/stats.py:13-54).
 
 Same interface as the reference (``totals``, ``by_layer``, ``reset``, ``add``,
-``ratio``, ``summary``).  Counts that live on the GPU (shortlist and budget
-sizes of a decode step) are recorded with ``add_device`` and summed there;
-they are brought to the host only when the statistics are read, so a decode
-step never waits on a device-to-host copy for its bookkeeping.
+``ratio``, ``summary``), with the same keys.  Counts that live on the GPU
+(shortlist and budget sizes of a decode step) are recorded with
+``add_device`` / ``add_device_rows`` or kept in a device counter that the
+native decode step adds to (``attach_device_counter``); they are brought to
+the host only when the statistics are read, so a decode step never waits on
+a device-to-host copy for its bookkeeping.  Decode heads whose sampled
+shortlist floor overshot (a count the reference does not keep) are read
+with ``floor_overshoots()`` and appear in no reference key.
 """
 
 from __future__ import annotations
@@ -28,6 +32,10 @@ class SVAStats:
         self._pending: dict[tuple[int, str], torch.Tensor] = {}
         # (layer, row names) -> float64 device vector of row sums not yet folded in
         self._pending_rows: dict[tuple[int, tuple[tuple[str, ...], ...]], torch.Tensor] = {}
+        # persistent int64 device counters [rows] a native step adds to: (layer, row names, counter)
+        self._counters: list[tuple[int, tuple[tuple[str, ...], ...], torch.Tensor]] = []
+        # counts kept beside the reference's keys (not in totals / by_layer / summary)
+        self._extra: defaultdict[str, float] = _float_stats()
 
     # -- recording --------------------------------------------------------
     def add(self, layer_idx: int, values: dict[str, float]) -> None:
@@ -67,14 +75,43 @@ class SVAStats:
         if host:
             self.add(layer_idx, host)
 
+    def attach_device_counter(self, layer_idx: int, names: tuple[tuple[str, ...], ...], counter: torch.Tensor) -> None:
+        """Register a persistent int64 device vector [len(names)] that decode
+        steps add to on the device (row i adds to every statistic named in
+        names[i]); it is folded in and zeroed when the statistics are read.
+        Registering the same tensor again does nothing."""
+
+        if counter.dtype != torch.int64 or counter.dim() != 1 or counter.numel() != len(names):
+            raise ValueError(f"a device counter is int64 [{len(names)}], got {counter.dtype} {tuple(counter.shape)}")
+        if not any(c is counter for _, _, c in self._counters):
+            self._counters.append((layer_idx, names, counter))
+
+    def floor_overshoots(self) -> float:
+        """Decode heads whose sampled shortlist floor overshot (the exact all-keys select ran)."""
+
+        self._flush()
+        return self._extra.get("floor_overshoots", 0.0)
+
+    def _add_named(self, layer_idx: int, name: str, v: float) -> None:
+        if name == "floor_overshoots":
+            self._extra[name] += v
+            return
+        self._totals[name] += v
+        self._by_layer[layer_idx][name] += v
+
     def _fold_rows(self, key: tuple[int, tuple[tuple[str, ...], ...]], mat: torch.Tensor) -> None:
         layer_idx, names = key
         for row_names, v in zip(names, mat.sum(dim=1).tolist()):
             for name in row_names:
-                self._totals[name] += float(v)
-                self._by_layer[layer_idx][name] += float(v)
+                self._add_named(layer_idx, name, float(v))
 
     def _flush(self) -> None:
+        for layer_idx, names, counter in self._counters:
+            values = counter.tolist()  # synchronizes with the steps that added to it
+            counter.zero_()
+            for row_names, v in zip(names, values):
+                for name in row_names:
+                    self._add_named(layer_idx, name, float(v))
         if self._pending_rows:
             rows, self._pending_rows = self._pending_rows, {}
             for key, mat in rows.items():
@@ -99,10 +136,13 @@ class SVAStats:
         return self._by_layer
 
     def reset(self) -> None:
+        for _, _, counter in self._counters:
+            counter.zero_()
         self._pending.clear()
         self._pending_rows.clear()
         self._totals.clear()
         self._by_layer.clear()
+        self._extra.clear()
 
     def ratio(self, numerator: str, denominator: str = "queries") -> float:
         totals = self.totals
@@ -119,6 +159,4 @@ class SVAStats:
             out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_calls")
         for k in ("projection", "key_catalog", "outer_total"):
             out[f"avg_static_{k}_ms"] = self.ratio(f"static_{k}_ms", "profile_outer_calls")
-        # decode heads whose sampled shortlist floor overshot (the exact all-keys select ran); no reference key
-        out["floor_overshoots"] = self.totals.get("floor_overshoots", 0.0)
         return out

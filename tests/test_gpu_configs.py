@@ -126,6 +126,49 @@ def test_smollm2_layer_prefill_8192(device):
         assert err <= 1e-2, f"full budget differs from dense attention by {err}"
 
 
+def test_smollm2_30_layer_decode_steps(device):
+    """Config 2's model: 30 SVA-patched layers, an 8192-token prefill, then greedy decode steps through the native
+    decode step (catalog append, lookup, verifier and statistics in one call per layer).  Layers 0 and 29's
+    decode outputs equal the oracle's scan attention over their own catalogs; every step appends one catalog row;
+    the statistics count 9 queries, 2048 summoned and 512 verified keys per head per layer and step."""
+    from sva import patch_llama_attention
+
+    n, steps, layers = 8192, 3, 30
+    model = _smollm2(device, layers=layers, context=n + 64)
+    prompt = torch.randint(0, 49152, (1, n), generator=torch.Generator().manual_seed(3)).to(device)
+    stores = {0: [], 29: []}
+    with torch.no_grad(), patch_llama_attention(model, _bundle(range(layers), 2048, 512), shortlist=2048,
+                                                budget=512, summon_mode="scan") as patcher:
+        out = model(input_ids=prompt, use_cache=True)
+        past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+        attns = {i: model.model.layers[i].self_attn for i in stores}
+        for i, attn in attns.items():
+            _capture(attn, stores[i])
+        patcher.reset_stats()
+        for step in range(steps):
+            out = model(input_ids=tok, past_key_values=past, use_cache=True)
+            past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+            for i, attn in attns.items():
+                assert attn._cached_key_len == n + step + 1
+        torch.cuda.synchronize()
+        totals = patcher.stats.totals
+        assert totals["queries"] == steps * layers * HEADS
+        assert totals["summoned"] == steps * layers * HEADS * 2048
+        assert totals["verified"] == totals["exact_scored"] == steps * layers * HEADS * 512
+        assert "floor_overshoots" not in totals and "floor_overshoots" not in patcher.stats.summary()
+        for i, attn in attns.items():
+            assert len(stores[i]) == steps
+            for step, (q, k, v, mask, got) in enumerate(stores[i]):
+                k_len = n + step + 1
+                assert mask is None and tuple(q.shape) == (1, HEADS, 1, HEAD_DIM) and k.shape[2] == k_len
+                print(f"layer {i} decode step {step}: oracle over {k_len} keys", flush=True)
+                ref = _oracle_scan(attn, q[0], k[0], v[0], k_len, 2048, 512)
+                g = got[0].float().cpu().numpy()
+                for h in range(HEADS):
+                    err = _rel(g[h], ref["out"][h])
+                    assert err <= 1e-2, f"layer {i} step {step} head {h}: rel err {err}"
+
+
 def test_late_socket_batch8_32k(device):
     from sva import patch_llama_attention
     from sva_amd import adapter as sva_adapter

@@ -25,8 +25,13 @@ def _inputs(device, N, S, C, q_dtype, seed, H=9, R=64, D=64):
     scale = torch.rand(H, device=device, generator=g) + 0.5
     cb = torch.randn(H, S, C, R // S, device=device, generator=g)
     codes = torch.randint(0, C, (H, N, S), device=device, generator=g, dtype=torch.int32).to(torch.uint8)
+    # a catalog's capacity: whole 64-key blocks per head, so that the code rows stay 16-byte aligned when
+    # N is not a multiple of 16 / S (the last 16-byte word of a head is then partial)
+    cap = (N + 63) // 64 * 64
+    padded = torch.zeros(H, cap, S, device=device, dtype=torch.uint8)
+    padded[:, :N] = codes
     k_low = torch.randn(H, N, R, device=device, generator=g)
-    return q, q_proj, scale, cb, codes, k_low
+    return q, q_proj, scale, cb, padded[:, :N], k_low
 
 
 def _two_calls(q, q_proj, scale, cb, codes, k_low, N, L, B, mask=None):
@@ -63,6 +68,8 @@ def _assert_same(fused, ref):
     (40000, 4, 64, torch.bfloat16, 2048, 512),     # partial last chunk
     (32768, 4, 64, torch.float16, 1024, 256),      # smallest wide-scan cache
     (1 << 18, 2, 256, torch.bfloat16, 2048, 512),  # 2x256 codes
+    (500003, 2, 64, torch.bfloat16, 2048, 512),    # 2x64 codes (pair table), a partial last code word
+    (1048573, 4, 64, torch.float32, 2048, 512),    # a partial last code word of four-byte keys
     (20000, 4, 64, torch.bfloat16, 2048, 512),     # too short for the wide scan: two calls
 ])
 def test_lookup_select_equals_two_calls(N, S, C, q_dtype, L, B):
@@ -267,3 +274,50 @@ def test_lookup_verify_matches_oracle(G, D, kv_dtype, L, B, masked):
             ref = oracle.verify(qf[h], kf[h // (H // G)], vf[h // (H // G)], np.sort(sel), scaling)
             err = np.abs(got[h] - ref).max() / max(np.abs(ref).max(), 1e-30)
             assert err <= 1e-5, f"head {h}: rel err {err}"
+
+
+def test_decode_layer_steps_equal_plan():
+    """The native decode step (sva_decode_layer_step) over three appended rows and one rebuild equals, bit for
+    bit, the catalog encoded whole by sva_write_encode followed by the plan's sva_lookup_verify; its device
+    statistics count every head's shortlist and budget sizes and the queries."""
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    H, G, D, R, S, C, L, B, N0 = 9, 3, 64, 64, 2, 256, 2048, 512, 40000
+    g = torch.Generator(device=device).manual_seed(61)
+    q_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
+    k_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
+    scale = torch.rand(H, device=device, generator=g) + 0.5
+    cb = torch.randn(H, S, C, R // S, device=device, generator=g)
+    cap = 65536
+    keys = torch.randn(G, cap, D, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(G, cap, D, device=device, generator=g).to(torch.bfloat16)
+    k_low = torch.empty(H, cap, R, device=device)
+    codes = torch.empty(H, cap, S, device=device, dtype=torch.uint8)
+    kernels.write_encode(keys, k_proj, cb, k_low, codes, 0, N0)
+    plan = kernels.ScanDecodePlan(device, 1, H, 1, D, R, S, C, L, B)
+    layer = kernels.DecodeLayer(kernels.ScanDecodePlan(device, 1, H, 1, D, R, S, C, L, B), q_proj, scale, cb, k_proj,
+                                D ** -0.5)
+    ref_low = torch.empty_like(k_low)
+    ref_codes = torch.empty_like(codes)
+    summoned = verified = 0
+    for step, (row_begin, n) in enumerate([(N0, N0 + 1), (N0 + 1, N0 + 2), (N0 + 2, N0 + 3), (0, N0 + 3)]):
+        q = torch.randn(1, H, 1, D, device=device, generator=g).to(torch.bfloat16)
+        out = torch.empty(1, H, 1, D, device=device, dtype=torch.bfloat16)
+        layer.step(q, keys, values, k_low, codes, row_begin, n, out)
+        kernels.write_encode(keys, k_proj, cb, ref_low, ref_codes, 0, n)
+        ref = plan.run(q, q_proj, scale, cb, ref_codes, ref_low, keys, values, n, D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(k_low[:, :n], ref_low[:, :n]) and torch.equal(codes[:, :n], ref_codes[:, :n])
+        lp = layer.plan
+        assert torch.equal(lp.counts, plan.counts), f"step {step}: counts differ"
+        for h in range(H):
+            c, b = int(plan.sl_count[h]), int(plan.fin_count[h])
+            assert torch.equal(lp.sl_idx[h, :c], plan.sl_idx[h, :c]) and torch.equal(lp.fin_idx[h, :b],
+                                                                                       plan.fin_idx[h, :b])
+        assert torch.equal(out, ref), f"step {step}: outputs differ"
+        summoned += int(plan.sl_count.sum())
+        verified += int(plan.fin_count.sum())
+    assert layer.stats.tolist() == [summoned, verified, 0, 4 * H]
+    with pytest.raises(Exception, match="catalog"):
+        layer.step(q, keys, values, k_low[:, :100], codes[:, :100], 0, 200, out)

@@ -328,15 +328,60 @@ def test_overshoot_at_a_million_keys_is_exact_and_reported(device):
         torch.cuda.synchronize()
         print(f"overshoot={expect}: {1e3 * ev[0].elapsed_time(ev[1]):.1f} us per step", flush=True)
         assert plan.overshoot.cpu().tolist() == [expect] * H
-        lut = plan.lut[0, :, 0].cpu().numpy()
-        _check(cds, k_low, plan.q_low[0, :, 0].cpu().numpy(), lut, plan.sl_idx.cpu().numpy(),
-               plan.sl_rank.cpu().numpy(), plan.sl_count.cpu().numpy(), L)
-        fin_idx, fin_count = plan.fin_idx.cpu().numpy(), plan.fin_count.cpu().numpy()
-        sl_idx, sl_rank = plan.sl_idx.cpu().numpy(), plan.sl_rank.cpu().numpy()
-        qf, kf, vf = qb.float().cpu().numpy()[0, :, 0], keys.float().cpu().numpy(), values.float().cpu().numpy()
-        got = out.cpu().numpy()[0, :, 0]
-        for h in range(H):
-            keep = oracle.topk(sl_rank[h, :L], B, key_index=sl_idx[h, :L])
-            np.testing.assert_array_equal(fin_idx[h, :fin_count[h]], np.sort(sl_idx[h, :L][keep]))
-            ref = oracle.verify(qf[h], kf[h // 3], vf[h // 3], np.sort(sl_idx[h, :L][keep]), 0.125)
-            assert np.abs(got[h] - ref).max() / np.abs(ref).max() <= 1e-5, f"head {h}"
+        _check_decode_step(plan, cds, k_low, qb, keys, values, out, L, B)
+
+
+def _check_decode_step(plan, codes, k_low, qb, keys, values, out, L, B, scaling=0.125):
+    """A ScanDecodePlan step against the oracle: the shortlist as a set (bit-exact ranks) over the plan's own
+    table, the budget as the oracle's top-B of the shortlist's ranks (score desc, key asc) in key order, and the
+    verified output within rel 1e-5 of the oracle's fp64 verifier (GQA: head h reads KV head h // (H / G))."""
+    H = codes.shape[0]
+    G = keys.shape[0]
+    lut = plan.lut[0, :, 0].cpu().numpy()
+    _check(codes, k_low, plan.q_low[0, :, 0].cpu().numpy(), lut, plan.sl_idx.cpu().numpy(),
+           plan.sl_rank.cpu().numpy(), plan.sl_count.cpu().numpy(), L)
+    fin_idx, fin_count = plan.fin_idx.cpu().numpy(), plan.fin_count.cpu().numpy()
+    sl_idx, sl_rank, sl_count = plan.sl_idx.cpu().numpy(), plan.sl_rank.cpu().numpy(), plan.sl_count.cpu().numpy()
+    qf, kf, vf = qb.float().cpu().numpy()[0, :, 0], keys.float().cpu().numpy(), values.float().cpu().numpy()
+    got = out.float().cpu().numpy()[0, :, 0]
+    for h in range(H):
+        n = int(sl_count[h])
+        keep = oracle.topk(sl_rank[h, :n], min(B, n), key_index=sl_idx[h, :n])
+        want = np.sort(sl_idx[h, :n][keep])
+        np.testing.assert_array_equal(fin_idx[h, :fin_count[h]], want)
+        ref = oracle.verify(qf[h], kf[h // (H // G)], vf[h // (H // G)], want, scaling)
+        assert np.abs(got[h] - ref).max() / np.abs(ref).max() <= 1e-5, f"head {h}"
+
+
+@pytest.mark.parametrize("N,S,C,L,B", [
+    (1 << 20, 4, 64, 2048, 512),   # the million-key decode workload
+    (1 << 20, 4, 64, 512, 128),    # its tight budget
+    (1 << 20, 2, 256, 2048, 512),  # 2x256 codes
+    (1 << 20, 2, 64, 2048, 512),   # two subspaces below 64 codewords: one pair-table read per key
+    (1048573, 4, 64, 2048, 512),   # a partial last 16-byte code word
+    (300001, 2, 256, 1024, 256),   # a partial last word with eight keys per word
+])
+def test_decode_step_at_a_million_keys_matches_oracle(device, N, S, C, L, B):
+    """The one-call decode step (sva_lookup_verify: the query inside the persistent scan, then the finish with
+    the verifier) on caches of up to a million keys, seeded, against the oracle's shortlist, budget and fp64
+    verifier for every head."""
+    from sva_amd import kernels
+
+    H = 9
+    print(f"decode step N={N} {S}x{C} L={L} B={B}", flush=True)
+    codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, H=H, seed=51 + S + L)
+    g = torch.Generator(device=device).manual_seed(52)
+    keys = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    values = torch.randn(3, N, 64, device=device, generator=g).to(torch.bfloat16)
+    t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    qb = t(q)[None].to(torch.bfloat16)
+    # the catalog's capacity is whole 64-key blocks (16-byte aligned code rows; a partial last word when N is
+    # not a multiple of 16 / S)
+    padded = np.zeros((H, (N + 63) // 64 * 64, S), np.uint8)
+    padded[:, :N] = codes
+    plan = kernels.ScanDecodePlan(device, 1, H, 1, 64, 64, S, C, L, B)
+    out = torch.empty(1, H, 1, 64, device=device, dtype=torch.float32)
+    plan.run(qb, t(q_proj), t(scale), t(cb), t(padded)[:, :N], k_low, keys, values, N, 0.125, out=out)
+    torch.cuda.synchronize()
+    assert plan.overshoot.cpu().tolist() == [0] * H
+    _check_decode_step(plan, codes, k_low, qb, keys, values, out, L, B)
