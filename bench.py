@@ -34,6 +34,88 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak (AMD spec)
 LAYOUTS = {"1x256": (1, 256), "2x256": (2, 256), "4x64": (4, 64)}
 
 
+def verify_suite(args):
+    """The verifier isolated on the million-key decode workload: per step,
+    HIP events around (a) the whole lookup with the verifier inside the
+    finish kernel (sva_lookup_verify), (b) the same lookup without a
+    verifier (sva_lookup_select), (c) the standalone verifier (sva_verify)
+    over (b)'s budget lists.  With --gqa-shared the query heads of each KV
+    group share their query, maps, codebooks, codes and k_low, so the three
+    heads of a group select the same budget (the case where one KV read per
+    group pays); otherwise the heads are independent.  The verifier's
+    algorithmic bytes count each distinct (KV head, row) of the budgets once,
+    K and V."""
+
+    import numpy as np
+    import torch
+
+    from sva_amd import kernels
+
+    device = torch.device("cuda:0")
+    subspaces, codewords = LAYOUTS[args.layout]
+    n, heads, kv_heads, head_dim = args.keys, 9, 3, 64
+    shortlist, budget = min(args.shortlist, n), min(args.budget, args.shortlist, n)
+    layers = [Layer(torch, device, n, subspaces, codewords, args.seed + n * 13 + 101 + 7919 * i)
+              for i in range(args.layers)]
+    if args.gqa_shared:
+        group = torch.arange(heads, device=device) // (heads // kv_heads) * (heads // kv_heads)
+        for ly in layers:
+            ly.q = ly.q[:, group].contiguous()
+            ly.q_proj = ly.q_proj[group].contiguous()
+            ly.codebooks = ly.codebooks[group].contiguous()
+            ly.codes = ly.codes[group].contiguous()
+            ly.k_low = ly.k_low[group].contiguous()
+    plan = kernels.ScanDecodePlan(device, 1, heads, 1, head_dim, 64, subspaces, codewords, shortlist, budget)
+    out = torch.empty(1, heads, 1, head_dim, device=device, dtype=torch.bfloat16)
+    scaling = head_dim ** -0.5
+
+    def full(ly):
+        plan.run(ly.q, ly.q_proj, ly.scale, ly.codebooks, ly.codes, ly.k_low, ly.keys, ly.values, n, scaling, out=out)
+
+    def select(ly):
+        plan.summon(ly.q, ly.q_proj, ly.scale, ly.codebooks, ly.codes, ly.k_low, n)
+
+    def verify(ly):
+        plan.verify(ly.q, ly.keys, ly.values, n, scaling, out=out)
+
+    times = {}
+    for name, fn in (("lookup_verify", full), ("lookup_select", select), ("verify", verify)):
+        for i in range(args.warmup):
+            if name == "verify":
+                select(layers[i % len(layers)])
+            fn(layers[i % len(layers)])
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for i, (a, b) in enumerate(ev):
+            ly = layers[i % len(layers)]
+            if name == "verify":
+                select(ly)  # the budget lists of this layer (outside the events)
+            a.record()
+            fn(ly)
+            b.record()
+        torch.cuda.synchronize()
+        times[name] = float(np.mean([1e3 * a.elapsed_time(b) for a, b in ev]))
+    # distinct (KV head, row) pairs of the last layer's budgets
+    ly = layers[(args.steps - 1) % len(layers)]
+    select(ly)
+    fin, cnt = plan.fin_idx.cpu().numpy(), plan.fin_count.cpu().numpy()
+    rows = sum(len({(h // (heads // kv_heads), int(x)) for h in range(heads) for x in fin[h, :cnt[h]]
+                    if h // (heads // kv_heads) == g}) for g in range(kv_heads))
+    verify_bytes = rows * head_dim * 2 * 2
+    print(json.dumps({
+        "metric": "verifier us/query at 1M keys (fused in the finish: lookup_verify - lookup_select; standalone)",
+        "value": round(times["lookup_verify"] - times["lookup_select"], 2), "unit": "us/query", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "higher_is_better": False,
+        "stage_us": {k: round(v, 2) for k, v in times.items()},
+        "verify_rows_distinct": rows, "verify_bytes_algorithmic": verify_bytes,
+        "standalone_verify_GBs": round(verify_bytes / (times["verify"] * 1e-6) / 1e9, 1),
+        "dtype": "fp32 scores / bf16 K,V", "data": "synthetic (seeded N(0,1) caches, uniform codes"
+        + (", the heads of each KV group sharing query, maps, codes and k_low)" if args.gqa_shared else ")"),
+        "config": {"workload": f"million-key cached decode lookup, {args.layout} codes, verifier isolated",
+                   "keys": n, "shortlist": shortlist, "budget": budget, "gqa_shared": bool(args.gqa_shared)},
+    }), flush=True)
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -52,11 +134,15 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before warmup, one device copy of MIB MiB (scales PMC byte counters)")
-    ap.add_argument("--suite", default="decode", choices=("decode", "write", "model", "ragged", "socket", "overshoot"),
+    ap.add_argument("--suite", default="decode",
+                    choices=("decode", "write", "model", "ragged", "socket", "overshoot", "verify"),
                     help="decode: the headline lookup; write: catalog build (projection + PQ codes) on MFMA; "
                          "model: greedy decode tok/s of a SmolLM2-135M-shape model with every layer patched; "
                          "ragged: continuous-batch static inverted decode over packed sequences; "
-                         "socket: batch-8 decode with SVA and residual adapters in the last four layers")
+                         "socket: batch-8 decode with SVA and residual adapters in the last four layers; "
+                         "verify: the verifier isolated (fused in the finish and standalone)")
+    ap.add_argument("--gqa-shared", action="store_true",
+                    help="verify suite: the query heads of each KV group select the same budget")
     ap.add_argument("--socket-prefill", type=int, default=32768, help="socket suite: prompt tokens per sequence")
     ap.add_argument("--socket-batch", type=int, default=8, help="socket suite: sequences")
     ap.add_argument("--batch", type=int, default=32, help="ragged suite: sequences per batch")
@@ -782,11 +868,11 @@ def main():
     if args.write_profiles:
         write_profiles(args)
         return
-    if args.suite in ("write", "model", "ragged", "socket", "overshoot"):
+    if args.suite in ("write", "model", "ragged", "socket", "overshoot", "verify"):
         if args.gpus != 1:
             sys.exit(2)
         {"write": write_suite, "model": model_suite, "ragged": ragged_suite, "socket": socket_suite,
-         "overshoot": overshoot_suite}[args.suite](args)
+         "overshoot": overshoot_suite, "verify": verify_suite}[args.suite](args)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "

@@ -1869,14 +1869,45 @@ SVA_DEV void verify_item(const SummonParams& p, const FusedVerify& v, int item, 
 // LDS the fused verifier needs when the list comes from the budget output.
 inline size_t verify_item_lds(int B, int D) { return sizeof(float) * ((size_t)B + SNW * (size_t)(D + 2)); }
 
+// The (item, slice) workgroup b of the finish grid takes.  Workgroups go to
+// the 8 XCDs in turn (b to XCD b % 8), and each XCD has its own L2: with the
+// fused verifier (item = query head) the finishes of one KV group's heads
+// take workgroups on one XCD (group x: b = x + 8 r, member r), so K / V rows
+// that their budgets share come from HBM once and from that L2 for the
+// group's other heads.  The other workgroups take the slices > 0 in turn;
+// without a verifier, or when the groups do not fit, b takes item b % items
+// as slice b / items.
+SVA_DEV void finish_slot(const WideArgs& a, int b, int& item, int& slice) {
+  const int items = a.items;
+  const int G = a.fv.out != nullptr ? a.fv.G : 0;
+  const int per = G > 0 ? items / G : 0;  // heads per KV group
+  if (G > 0 && G <= 8 && G * per == items && G - 1 + 8 * (per - 1) < items * a.K) {
+    const int x = b % 8, r = b / 8;
+    if (x < G && r < per) {
+      item = x * per + r;
+      slice = 0;
+      return;
+    }
+    int before = 0;  // group workgroups with a smaller index
+    for (int rr = 0; rr < per; ++rr) before += min(max(b - 8 * rr, 0), G);
+    const int o = b - before;
+    item = o % items;
+    slice = 1 + o / items;
+    return;
+  }
+  item = b % items;
+  slice = b / items;
+}
+
 // Finish of an item, then (VD > 0: head_dim VD, K / V dtype VKV) its
-// verifier.  Workgroup g takes item g % items as slice g / items of the
-// all-keys select; slice 0 is the item's finish.
+// verifier.  Workgroup b takes the item and slice finish_slot gives it;
+// slice 0 is the item's finish, slices > 0 serve the all-keys select.
 template <int VD, int VKV>
 __global__ void __launch_bounds__(SB) wide_finish_kernel(WideArgs a) {
   extern __shared__ __align__(16) unsigned char lds[];
   __shared__ float qsh[VD > 0 ? VD : 1];  // the verifier's query row
-  const int item = blockIdx.x % a.items, slice = blockIdx.x / a.items;
+  int item, slice;
+  finish_slot(a, (int)blockIdx.x, item, slice);
   // the query row is requested before the finish starts and parked in LDS
   // after it (a store now would wait for the load ahead of the finish's own)
   uint32_t qbits = 0u;
