@@ -7,11 +7,15 @@ attention output::
 
     out = attn + (up @ gelu(down @ [hidden, attn]) * scale).to(attn.dtype)
 
-with ``down`` [rank, 2 * hidden] and ``up`` [hidden, rank] held in fp32 on
-the wrapped module's device.  ``down`` starts N(0, 0.02^2) and ``up`` at
-zero, so a fresh adapter is the identity on the attention output.  The
-forward is one HIP launch (``sva_residual_adapter``); the adapter serves
-inference only (the distillation that trains it is outside this package).
+with ``down`` [rank, 2 * hidden] and ``up`` [hidden, rank] the weights of two
+bias-free fp32 ``nn.Linear`` layers (so ``adapter.down(x)`` and
+``adapter.up(x)`` work as in the experiment).  They are made and initialised
+on the CPU as the experiment makes them (``down`` N(0, 0.02^2) from the
+default generator, ``up`` zero, so a fresh adapter is the identity on the
+attention output) and then moved to the wrapped module's device.  The
+forward is one HIP launch (``sva_residual_adapter``) reading the two weights;
+the adapter serves inference only (the distillation that trains it is
+outside this package).
 
 On disk an adapter set is the experiment's bundle: ``adapter_config.json``
 (``format`` = "sva_residual_output_adapter_v1", ``socket_layers`` and any
@@ -44,17 +48,6 @@ def _module_device(module: nn.Module) -> torch.device:
     return torch.device("cpu")
 
 
-class _Matrix(nn.Module):
-    """One fp32 weight matrix, so an adapter's state reads ``down.weight`` / ``up.weight``."""
-
-    def __init__(self, rows: int, cols: int, device: torch.device, std: float) -> None:
-        super().__init__()
-        w = torch.zeros(rows, cols, dtype=torch.float32, device=device)
-        if std > 0.0:
-            w.normal_(0.0, std)
-        self.weight = nn.Parameter(w)
-
-
 class SVAResidualOutputAdapter(nn.Module):
     """The socket adapter around ``sva_attn``; returns ``(corrected attention output, attn weights)``."""
 
@@ -65,8 +58,13 @@ class SVAResidualOutputAdapter(nn.Module):
         device = _module_device(sva_attn)
         self.sva_attn = sva_attn
         self.scale = float(scale)
-        self.down = _Matrix(rank, 2 * hidden_size, device, std=0.02)
-        self.up = _Matrix(hidden_size, rank, device, std=0.0)
+        # made and initialised on the CPU (the experiment's draw order), then moved
+        down = nn.Linear(2 * hidden_size, rank, bias=False, dtype=torch.float32)
+        up = nn.Linear(rank, hidden_size, bias=False, dtype=torch.float32)
+        nn.init.normal_(down.weight, mean=0.0, std=0.02)
+        nn.init.zeros_(up.weight)
+        self.down = down.to(device)
+        self.up = up.to(device)
 
     def forward(self, hidden_states: torch.Tensor, *args, **kwargs) -> tuple[torch.Tensor, Any]:
         attn_output, attn_weights = self.sva_attn(hidden_states, *args, **kwargs)

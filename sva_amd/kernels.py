@@ -142,6 +142,27 @@ def pq_scores(lut: torch.Tensor, codes: torch.Tensor, n_keys: int, rank: int,
     return scores
 
 
+_uniform_masks: dict[tuple, bool] = {}
+
+
+def mask_is_uniform(lead: torch.Tensor) -> bool:
+    """Whether every slice lead[i] equals lead[0] (lead: [n, Q, N]).  The
+    answer is kept per mask storage and version (data pointer, version
+    counter, shape, strides), so a mask reused across layers and steps costs
+    one device comparison, and one host sync, rather than one per call."""
+
+    if lead.shape[0] <= 1:
+        return True
+    key = (lead.data_ptr(), lead._version, tuple(lead.shape), tuple(lead.stride()), lead.dtype, lead.device)
+    hit = _uniform_masks.get(key)
+    if hit is None:
+        hit = bool(torch.equal(lead[1:], lead[:1].expand_as(lead[1:])))
+        if len(_uniform_masks) >= 4096:
+            _uniform_masks.clear()
+        _uniform_masks[key] = hit
+    return hit
+
+
 def mask_args(mask: torch.Tensor | None, q_len: int, n_keys: int):
     """(tensor, mask type, token stride) for an HF attention mask [..., Q, >=N].
 
@@ -153,7 +174,7 @@ def mask_args(mask: torch.Tensor | None, q_len: int, n_keys: int):
     if mask is None:
         return None, 0, 0
     lead = mask.reshape(-1, *mask.shape[-2:])[:, :q_len, :n_keys]
-    if lead.shape[0] > 1 and not torch.equal(lead[1:], lead[:1].expand_as(lead[1:])):
+    if not mask_is_uniform(lead):
         raise ValueError(f"attention mask {tuple(mask.shape)} differs across its leading (batch / head) dims; the "
                          f"kernels take one mask for every sequence and head")
     m = lead[0]

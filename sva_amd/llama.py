@@ -292,7 +292,7 @@ class SVALlamaAttention(nn.Module):
             m = attention_mask[..., :q_len, :k_len]
             # decode steps included: a left-padded batch gives each sequence
             # its own mask row, which the packed launch cannot take
-            if m.shape[0] > 1 and not torch.equal(m[1:], m[:1].expand_as(m[1:])):
+            if m.shape[0] > 1 and not kernels.mask_is_uniform(m.reshape(m.shape[0], -1, m.shape[-1])):
                 raise ValueError("Batched SVA attention needs the same attention mask for every sequence (no padding).")
             mask = m[:1]
         if key.stride(0) % key.stride(2) != 0 or value.stride() != key.stride() or key.stride(-1) != 1:

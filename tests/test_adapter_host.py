@@ -98,3 +98,23 @@ def test_bundle_validation(tmp_path):
     (tmp_path / "adapter_config.json").write_text(json.dumps(cfg))
     torch.save(state, tmp_path / "adapter_weights.pt")
     assert sorted(adapter.load_adapter_bundle(tmp_path)[1]) == sorted(state)
+
+
+def test_fresh_adapter_draws_like_the_experiment():
+    """down / up are bias-free fp32 Linear layers made on the CPU: a fresh adapter's down weight is the
+    default generator's N(0, 0.02^2) draw after Linear's own init (so the CPU generator advances as in the
+    experiment), up is zero, and both layers are callable."""
+    attn = _Attn()
+    torch.manual_seed(123)
+    a = adapter.SVAResidualOutputAdapter(attn, hidden_size=8, rank=3, scale=1.0)
+    after = torch.rand(1)
+    torch.manual_seed(123)
+    down = nn.Linear(16, 3, bias=False)
+    up = nn.Linear(3, 8, bias=False)
+    expect = torch.empty(3, 16).normal_(0.0, 0.02)
+    assert torch.equal(torch.rand(1), after), "the CPU generator advanced differently"
+    assert torch.equal(a.down.weight, expect) and down.weight.shape == a.down.weight.shape
+    assert torch.count_nonzero(a.up.weight) == 0 and up.weight.shape == a.up.weight.shape
+    assert isinstance(a.down, nn.Linear) and a.down.bias is None and a.up.bias is None
+    x = torch.randn(2, 16)
+    assert torch.equal(a.up(a.down(x)), torch.zeros(2, 8))

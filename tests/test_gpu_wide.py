@@ -280,20 +280,26 @@ def test_summon_select_staged_paths(device, case):
     (120000, 256, 2048, 512, True, False),     # 3 codes: a boundary class of ~40K keys
     (70001, 256, 7168, 2048, False, False),    # the largest shortlist of the class path, partial chunk
     (1048576, 256, 512, 128, False, False),    # tight shortlist / budget
+    (1048576, 256, 2048, 512, False, "sparse"),  # fewer allowed keys than L: the lowest class is the boundary
+    (300000, 256, 2048, 512, True, "none"),    # every key masked: empty shortlist and budget
 ])
 def test_class_path_single_subspace(device, N, C, L, B, few, masked):
     """One subspace of <= 256 codewords selects by code class (count, boundary class, ordered extraction,
     budget): shortlist and ranks equal the oracle's top-L (score desc, key asc) and the standalone budget
-    select's lists, every head."""
+    select's lists, every head; with fewer allowed keys than L every allowed key is shortlisted, and with none
+    the lists are empty."""
     assert _strategy(9, N, 64, 1, C, L) == 2, "code-class path not selected"
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, 1, C, seed=(N + C + L) % 83, few=few)
     mask = allowed = None
     if masked:
         rng = np.random.default_rng(9)
-        m = np.where(rng.random(N) < 0.4, np.finfo(np.float32).min, 0.0).astype(np.float32)[None, None, None, :]
+        keep = {True: rng.random(N) >= 0.4, "sparse": np.arange(N) % 1021 == 5, "none": np.zeros(N, bool)}[masked]
+        m = np.where(keep, 0.0, np.finfo(np.float32).min).astype(np.float32)[None, None, None, :]
         mask, allowed = torch.from_numpy(m).to(device), m[0, 0, 0] > -1e4
     fused, split, q_low, lut = _summon_select(device, codes, k_low, q, q_proj, scale, cb, L, B, mask=mask)
     _check_fused(codes, k_low, fused, split, q_low, lut, L, B, allowed=allowed)
+    if masked in ("sparse", "none"):
+        assert (fused[2] == int(allowed.sum())).all(), "every allowed key is shortlisted"
 
 
 def test_overshoot_at_a_million_keys_is_exact_and_reported(device):
