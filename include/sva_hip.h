@@ -132,6 +132,9 @@ int sva_summon(const float *lut, const float *score_range, const float *q_low, c
  * budget selects and the rescore run in one kernel per query item.
  *   fin_idx [items, B] chosen key indices sorted ascending; fin_count[item] = min(B, sl_count[item]).
  * workspace: sva_summon_workspace_bytes(...) bytes, 256-byte aligned.
+ * sl_idx and sl_rank may both be null where sva_summon_strategy is 3 (the
+ * shortlist then stays inside the kernel, as in the reference's prefill,
+ * which keeps only the budget); elsewhere a null pair is SVA_ERR_UNSUPPORTED.
  */
 int sva_summon_select(const float *lut, const float *score_range, const float *q_low, const void *codes,
                       int code_type, int64_t code_head_stride, const float *k_low, int64_t k_low_head_stride,
@@ -190,7 +193,9 @@ int sva_lookup_verify(const void *q, int q_dtype, int64_t q_head_stride, int64_t
  * over a long cache: many workgroups per item, one pass over the codes),
  * 2 = code-class path (the wide path's shapes with one subspace of at most
  * 256 codewords: the shortlist taken by code class from per-chunk code
- * counts).
+ * counts), 3 = one workgroup per query item that selects, rescores and
+ * budgets in registers (R = 64, L <= 2048, at most 16384 keys; the
+ * sva_summon_select form; sva_summon on these shapes takes strategy 0).
  */
 int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t R, int64_t S, int64_t C,
                         int64_t L, int code_type, int mask_type);

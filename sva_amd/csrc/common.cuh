@@ -139,6 +139,20 @@ SVA_DEV bool mask_allows(const void* mask, int64_t i, int mtype) {
 
 SVA_DEV int lane_id() { return (int)__lane_id(); }
 
+// Workgroups go to the 8 XCDs in turn (workgroup b to XCD b % 8), and each
+// XCD has its own L2.  A grid of xcd_range_grid(total) workgroups where
+// workgroup b takes item xcd_range_item(b, total) hands XCD x the contiguous
+// items [x * per, (x + 1) * per): items in the order of their data (e.g.
+// head-major) then share one XCD's L2 instead of every XCD caching every
+// head's rows.  -1: a workgroup past the end (it returns).
+constexpr int kXcds = 8;
+__host__ __device__ inline int64_t xcd_range_grid(int64_t total) { return (total + kXcds - 1) / kXcds * kXcds; }
+SVA_DEV int64_t xcd_range_item(int64_t b, int64_t total) {
+  const int64_t per = (total + kXcds - 1) / kXcds;
+  const int64_t item = (b % kXcds) * per + b / kXcds;
+  return item < total ? item : -1;
+}
+
 
 // DPP row shifts (a DPP row is 16 lanes): lane j receives lane j - N of its
 // row.  Lanes with no source lane receive 0 (row_shr0) or keep their own
@@ -233,6 +247,30 @@ SVA_DEV float rank_dot64_row16(const float4 r, const float4 qq) {
   const float a1 = (0.0f + p1) + row_down<8>(p1);
   const float a2 = (0.0f + p2) + row_down<8>(p2);
   const float a3 = (0.0f + p3) + row_down<8>(p3);
+  const float v0 = ((a0 + row_down<2>(a0)) + row_down<4>(a0)) + row_down<6>(a0);
+  const float v1 = ((a1 + row_down<2>(a1)) + row_down<4>(a1)) + row_down<6>(a1);
+  const float v2 = ((a2 + row_down<2>(a2)) + row_down<4>(a2)) + row_down<6>(a2);
+  const float v3 = ((a3 + row_down<2>(a3)) + row_down<4>(a3)) + row_down<6>(a3);
+  const float w0 = row_down<1>(v0), w1 = row_down<1>(v1), w2 = row_down<1>(v2), w3 = row_down<1>(v3);
+  return (((((((0.0f + v0) + v1) + v2) + v3) + w0) + w1) + w2) + w3;
+}
+
+// The same rank score computed by the 8 lanes of a lane octet, two rows of
+// each 16-lane DPP row: lane c holds floats 4c..4c+3 (r0) and 32+4c..32+4c+3
+// (r1) of the row and of the query (q0, q1), so each lane forms the four
+// pair sums a_j[l] = (0 + p[8j+l]) + p[32+8j+l] with j = c / 2,
+// l = 4 (c % 2) + i locally; lanes 0 and 1 chain a_0..a_3 of their four l
+// (lanes c, c+2, c+4, c+6), and lane 0 sums the eight in order.  Half the
+// lanes' loads cover each 128-byte line of a row, as with 16 lanes per row,
+// at about half the VALU instructions per row.  The result is valid in the
+// octet's first lane.
+SVA_DEV float rank_dot64_oct8(const float4 r0, const float4 r1, const float4 q0, const float4 q1) {
+#pragma clang fp contract(off)
+  // fma(x, y, 0) rounds x * y once and adds +0: the value of 0 + x * y
+  const float a0 = __builtin_fmaf(r0.x, q0.x, 0.0f) + r1.x * q1.x;
+  const float a1 = __builtin_fmaf(r0.y, q0.y, 0.0f) + r1.y * q1.y;
+  const float a2 = __builtin_fmaf(r0.z, q0.z, 0.0f) + r1.z * q1.z;
+  const float a3 = __builtin_fmaf(r0.w, q0.w, 0.0f) + r1.w * q1.w;
   const float v0 = ((a0 + row_down<2>(a0)) + row_down<4>(a0)) + row_down<6>(a0);
   const float v1 = ((a1 + row_down<2>(a1)) + row_down<4>(a1)) + row_down<6>(a1);
   const float v2 = ((a2 + row_down<2>(a2)) + row_down<4>(a2)) + row_down<6>(a2);

@@ -130,7 +130,8 @@ extern "C" int sva_decode_layer_step(sva_decode_layer* h, const void* q, int q_d
   // sampled floor (strategy 1 and 2) report overshoots, so the per-item path
   // is spared the fill of that row
   const int64_t H = h->H;
-  const bool with_floor = sva_summon_strategy(1, H, 1, n_keys, h->R, h->S, h->C, h->L, h->code_type, 0) != 0;
+  const int strategy = sva_summon_strategy(1, H, 1, n_keys, h->R, h->S, h->C, h->L, h->code_type, 0);
+  const bool with_floor = strategy == 1 || strategy == 2;
   rc = sva_lookup_verify(q, q_dtype, q_head_stride, H, h->D, h->R, h->S, h->C, h->q_proj, h->scale, h->codebooks,
                          h->codes, h->code_type, h->code_hs, h->k_low, h->klow_hs, n_keys, h->L, nullptr, 0, 0,
                          h->q_low, h->lut, h->range, h->sl_idx, h->sl_rank, h->counts, h->B, h->fin_idx,

@@ -167,14 +167,14 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
 // holds keys i * BLOCK + t (i < NPT) in registers as unique composites (scan
 // key, key index); a register radix select finds the L-th largest; the
 // shortlist is compacted in ascending key order (per-slot wave ballots and
-// one scan of the wave counts); each DPP row of 16 lanes rescores shortlisted
-// rows in torch's sum order, REG_ROWS rows in flight; the budget is a second
+// one scan of the wave counts); each lane octet rescores shortlisted rows in
+// torch's sum order, REG_OCT rows in flight; the budget is a second
 // register select over the shortlist's (rank key, key index) composites,
 // compacted in shortlist order, which is ascending key order, as the budget
 // select writes it.
 constexpr int REG_MAX_L = 2048;
 constexpr int REG_NW = ITEM_BLOCK / WAVE;
-constexpr int REG_ROWS = 8;  // shortlist rows per DPP row in flight
+constexpr int REG_OCT = 4;  // shortlist rows per lane octet in flight
 
 struct RegLds {
   int tab, hist, small, shared64, scratch, shared, wbase, slidx, rank, total;
@@ -205,8 +205,10 @@ __host__ __device__ inline RegLds reg_lds_layout(int S, int C, int L, int npt) {
   return l;
 }
 
+// items: n_seq * H * Q; workgroups take head-major item ranges per XCD
+// (xcd_range_item), so one XCD's L2 holds the k_low rows of one or two heads.
 template <int NPT, int SB>
-__global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kernel(SummonParams p) {
+__global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kernel(SummonParams p, int64_t items) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
   const RegLds Ly = reg_lds_layout(p.S, p.C, p.L, NPT);
@@ -217,7 +219,9 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   float* rank = (float*)(lds + Ly.rank);
   const TopLds tl{(uint32_t*)(lds + Ly.hist), (uint64_t*)(lds + Ly.small), (uint32_t*)(lds + Ly.scratch), shared,
                   (uint64_t*)(lds + Ly.shared64)};
-  const int item = blockIdx.x;
+  const int64_t item_x = xcd_range_item((int64_t)blockIdx.x, items);
+  if (item_x < 0) return;  // block-uniform: past the last item
+  const int item = (int)item_x;
   const int t = item % p.Q;
   const int h = (item / p.Q) % p.H;
   const int b = item / (p.Q * p.H);
@@ -226,8 +230,6 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   const int64_t off = p.offs ? p.offs[b] : 0;
   const int SC = p.S * p.C;
   const float* lsrc = p.lut + (int64_t)item * SC;
-  for (int e = threadIdx.x; e < SC; e += ITEM_BLOCK) tab[e] = lsrc[e];
-  __syncthreads();
 
   const int64_t code_base = (int64_t)h * p.code_hs + off * p.S;
   const int64_t causal_last = len - p.Q + t;
@@ -235,7 +237,8 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   const float sqrt_r = p.sqrt_r;
   // SB > 0: uint8 codes of SB subspaces, read as one SB-byte load per key,
   // every load of the thread issued before any is used (e[] holds the raw
-  // code bytes until the composites replace them); SB = 0: any code type
+  // code bytes until the composites replace them), and before the table's
+  // barrier, so the code and table loads overlap; SB = 0: any code type
   uint64_t e[NPT];
   uint32_t okm = 0;  // bit i: key i * BLOCK + t is allowed
 #pragma unroll
@@ -254,6 +257,8 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
     for (int i = 0; i < NPT; ++i)
       if ((okm >> i) & 1u) e[i] = cw[(int64_t)i * ITEM_BLOCK + threadIdx.x];
   }
+  for (int e2 = threadIdx.x; e2 < SC; e2 += ITEM_BLOCK) tab[e2] = lsrc[e2];
+  __syncthreads();
   uint64_t vor = 0ull, vand = ~0ull;
   uint32_t cnt = 0;
 #pragma unroll
@@ -315,33 +320,37 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   }
   __syncthreads();
 
-  // rescore: DPP row r of 16 lanes takes shortlist entries r, r + 64, ...
+  // rescore: lane octet o takes shortlist entries o, o + 128, ...
   {
-    const int row16 = (int)threadIdx.x >> 4, g = (int)threadIdx.x & 15;
-    const float4 qq = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * 64)[g];
-    const float* kl = p.k_low + (int64_t)h * p.klow_hs + off * 64;
-    for (int j0 = 0; j0 < leff; j0 += REG_ROWS * 64) {
-      float4 r[REG_ROWS];
+    const int oct = (int)threadIdx.x >> 3, c = (int)threadIdx.x & 7;
+    const float4* q4 = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * 64);
+    const float4 q0 = q4[c], q1 = q4[8 + c];
+    const float4* kl4 = reinterpret_cast<const float4*>(p.k_low + (int64_t)h * p.klow_hs + off * 64);
+    for (int j0 = 0; j0 < leff; j0 += REG_OCT * (ITEM_BLOCK / 8)) {
+      float4 r0[REG_OCT], r1[REG_OCT];
 #pragma unroll
-      for (int u = 0; u < REG_ROWS; ++u) {
-        const int j = j0 + u * 64 + row16;
+      for (int u = 0; u < REG_OCT; ++u) {
+        const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
         const int64_t n = slidx[j < leff ? j : 0];
-        r[u] = reinterpret_cast<const float4*>(kl + n * 64)[g];
+        r0[u] = kl4[n * 16 + c];
+        r1[u] = kl4[n * 16 + 8 + c];
       }
 #pragma unroll
-      for (int u = 0; u < REG_ROWS; ++u) {
-        const int j = j0 + u * 64 + row16;
-        const float d = rank_dot64_row16(r[u], qq);
-        if (g == 0 && j < leff) rank[j] = d / sqrt_r;
+      for (int u = 0; u < REG_OCT; ++u) {
+        const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
+        const float d = rank_dot64_oct8(r0[u], r1[u], q0, q1);
+        if (c == 0 && j < leff) rank[j] = d / sqrt_r;
       }
     }
   }
   __syncthreads();
-  int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
-  float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
-    out_idx[j] = slidx[j];
-    out_rank[j] = rank[j];
+  if (p.sl_idx != nullptr) {  // the shortlist outputs are optional here
+    int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
+    float* out_rank = p.sl_rank + (int64_t)item * p.L;
+    for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
+      out_idx[j] = slidx[j];
+      out_rank[j] = rank[j];
+    }
   }
 
   // budget: top beff by (rank desc, key index asc), ascending key order
@@ -389,7 +398,8 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
 template <int NPT, int SB>
 int launch_regs(const SummonParams& p, int64_t items, size_t lds, hipStream_t stream) {
   SVA_SET_MAX_LDS_ONCE((summon_regs_kernel<NPT, SB>), kMaxLds, "hipFuncSetAttribute(summon_regs_kernel)");
-  hipLaunchKernelGGL((summon_regs_kernel<NPT, SB>), dim3((unsigned)items), dim3(ITEM_BLOCK), lds, stream, p);
+  hipLaunchKernelGGL((summon_regs_kernel<NPT, SB>), dim3((unsigned)xcd_range_grid(items)), dim3(ITEM_BLOCK), lds,
+                     stream, p, items);
   SVA_CHECK_LAUNCH("summon_regs_kernel");
   return SVA_OK;
 }
@@ -454,7 +464,9 @@ extern "C" int sva_summon_strategy(int64_t n_seq, int64_t H, int64_t Q, int64_t 
   p.mask = dummy;
   p.mask_type = mask_type;
   if (sva::summon_class_eligible(p, n_seq * H * Q)) return 2;
-  return sva::summon_wide_eligible(p, n_seq * H * Q) ? 1 : 0;
+  if (sva::summon_wide_eligible(p, n_seq * H * Q)) return 1;
+  p.B = 1;
+  return sva::summon_regs_eligible(p) ? 3 : 0;
 }
 
 extern "C" size_t sva_summon_workspace_bytes(int64_t n_seq, int64_t H, int64_t Q, int64_t n_keys, int64_t L) {
@@ -472,7 +484,8 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr,
                 const sva::QueryLaunch* query = nullptr) {
   if (fused != nullptr) *fused = false;
-  SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_idx && sl_rank && sl_count, "%s: null pointer", fn);
+  SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_count, "%s: null pointer", fn);
+  SVA_REQUIRE((sl_idx == nullptr) == (sl_rank == nullptr), "%s: shortlist indices and ranks go together", fn);
   SVA_REQUIRE((seq_offsets == nullptr) == (seq_lens == nullptr), "%s: offsets and lengths go together", fn);
   SVA_REQUIRE(n_seq > 0 && H > 0 && Q > 0 && n_keys >= 0, "%s: bad sizes", fn);
   SVA_REQUIRE(n_keys < (1ll << 31), "%s: at most 2^31-1 keys per sequence", fn);
@@ -519,6 +532,10 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   // path runs its decode form in one grid with the code counts; every other
   // path launches it first
   const bool class_path = n_keys > 0 && sva::summon_class_eligible(p, items);
+  // without shortlist outputs only the fused per-item path (strategy 3) runs
+  SVA_UNSUPPORTED(sl_idx != nullptr || n_keys == 0 ||
+                      (B > 0 && !class_path && !sva::summon_wide_eligible(p, items) && sva::summon_regs_eligible(p)),
+                  "%s: these shapes keep the shortlist in memory; pass shortlist outputs", fn);
   if (query != nullptr && !(class_path && query->form == sva::QUERY_DECODE_1_256)) {
     const int rc = sva::query_lut_launch(*query, (hipStream_t)stream);
     if (rc != SVA_OK) return rc;

@@ -61,6 +61,7 @@ struct VerifyParams {
   const int32_t* fin_idx;
   const int32_t* fin_count;
   int H, G, Q, D, B, split;
+  int groups;  // n_seq * G * Q
   float scaling;
   float* part;  // [items, split, D + 2]: m, z, acc[D]
   void* out;
@@ -77,8 +78,12 @@ __global__ void __launch_bounds__(VB) verify_part_kernel(VerifyParams p) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int D = DT > 0 ? DT : p.D;
   const int grp = p.H / p.G;
+  // SEQ: one workgroup per group, head-major group ranges per XCD
+  // (xcd_range_item), so one XCD's L2 holds the K/V rows of one or two heads
   const int s = SEQ ? 0 : (int)blockIdx.x;
-  const int gi = SEQ ? (int)blockIdx.x : (int)blockIdx.y;
+  const int64_t gx = SEQ ? sva::xcd_range_item((int64_t)blockIdx.x, p.groups) : (int64_t)blockIdx.y;
+  if (gx < 0) return;  // block-uniform: past the last group
+  const int gi = (int)gx;
   const int t = gi % p.Q;
   const int g = (gi / p.Q) % p.G;
   const int b = gi / (p.Q * p.G);
@@ -435,6 +440,7 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.D = (int)D;
   p.B = (int)B;
   p.split = split;
+  p.groups = (int)(n_seq * G * Q);
   p.scaling = scaling;
   p.part = (float*)workspace;
   p.out = out;
@@ -443,7 +449,7 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.o_hs = out_head_stride;
   p.o_ts = out_tok_stride;
   if (verify_walks_slices(n_seq, G, Q))
-    return launch_part_dim<true>(p, dim3((unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
+    return launch_part_dim<true>(p, dim3((unsigned)sva::xcd_range_grid(n_seq * G * Q)), lds, (hipStream_t)stream);
   int rc = launch_part_dim<false>(p, dim3((unsigned)split, (unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
   if (rc != SVA_OK) return rc;
   hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,

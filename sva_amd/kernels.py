@@ -230,9 +230,14 @@ def budget_select(sl_idx: torch.Tensor, sl_rank: torch.Tensor, sl_count: torch.T
 
 def summon_select(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist: int, budget: int,
                   mask: torch.Tensor | None = None, seq_offsets: torch.Tensor | None = None,
-                  seq_lens: torch.Tensor | None = None):
+                  seq_lens: torch.Tensor | None = None, keep_shortlist: bool = True):
     """Shortlist and budget in one call (sva/llama.py:262-302):
-    (sl_idx, sl_rank, sl_count, fin_idx, fin_count)."""
+    (sl_idx, sl_rank, sl_count, fin_idx, fin_count).
+
+    keep_shortlist=False: where the shapes take the fused per-item path
+    (sva_summon_strategy 3) the shortlist stays inside the kernel and
+    sl_idx / sl_rank come back as None, as the reference's attention keeps
+    only the budget; elsewhere they are returned as usual."""
 
     n_seq, heads, q_len, subspaces, codewords = lut.shape
     rank = q_low.shape[-1]
@@ -240,12 +245,17 @@ def summon_select(lut, score_range, q_low, codes, k_low, n_keys: int, shortlist:
     _check_catalog("k_low", k_low, heads, rank)
     device = require_device(lut, score_range, q_low, codes, k_low, seq_offsets, seq_lens, mask)
     items = n_seq * heads * q_len
-    sl_idx = torch.empty(items, shortlist, device=device, dtype=torch.int32)
-    sl_rank = torch.empty(items, shortlist, device=device, dtype=torch.float32)
+    m, mtype, mstride = mask_args(mask, q_len, n_keys)
+    if not keep_shortlist:
+        keep_shortlist = lib().sva_summon_strategy(n_seq, heads, q_len, n_keys, rank, subspaces, codewords,
+                                                   shortlist, code_type(codes), mtype) != 3
+    sl_idx = sl_rank = None
+    if keep_shortlist:
+        sl_idx = torch.empty(items, shortlist, device=device, dtype=torch.int32)
+        sl_rank = torch.empty(items, shortlist, device=device, dtype=torch.float32)
     sl_count = torch.empty(items, device=device, dtype=torch.int32)
     fin_idx = torch.empty(items, budget, device=device, dtype=torch.int32)
     fin_count = torch.empty(items, device=device, dtype=torch.int32)
-    m, mtype, mstride = mask_args(mask, q_len, n_keys)
     ws_bytes = int(lib().sva_summon_workspace_bytes(n_seq, heads, q_len, n_keys, shortlist))
     ws = workspace(device, ws_bytes)
     check(

@@ -237,12 +237,12 @@ class SVALlamaAttention(nn.Module):
         """sva/llama.py:226-328 on the HIP path, chunked over query tokens."""
 
         outs = []
-        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist):
+        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist, budget, codes):
             qc = query[:, :, qs:qe, :]
             q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks,
                                                 codes, n, shortlist)
             _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, n, shortlist,
-                                                                       budget, mask=m)
+                                                                       budget, mask=m, keep_shortlist=False)
             outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, n, self.scaling,
                                        out_dtype=query.dtype))
             if self.stats is not None:
@@ -251,23 +251,36 @@ class SVALlamaAttention(nn.Module):
                     "queries": float(sl_count.numel())})
         return outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)
 
-    def _query_chunks(self, query, k_len, mask, shortlist):
+    def _query_chunks(self, query, k_len, mask, shortlist, budget, codes):
         """(qs, qe, mask, n_keys) per chunk of query tokens (sva/llama.py:221-223,
         262-268).  Every token's result is independent of the chunking, so the
-        default chunk bounds the per-launch shortlist buffers (about 512 MiB)
-        rather than following the reference's 128.  Without a mask the
-        kernels' causal rule (key n for token t of Q iff n <= N - Q + t) is
-        kept by handing chunk [qs, qe) the first N - Q + qe keys: token qs + t
-        then keeps n <= N - Q + qs + t, as over the whole prompt."""
+        default chunk bounds the per-launch buffers (about 512 MiB) rather
+        than following the reference's 128: the shortlist buffers, or, where
+        the fused per-item summon keeps the shortlist inside the kernel
+        (sva_summon_strategy 3), the tables and budget lists.  Without a mask
+        the kernels' causal rule (key n for token t of Q iff n <= N - Q + t)
+        is kept by handing chunk [qs, qe) the first N - Q + qe keys: token
+        qs + t then keeps n <= N - Q + qs + t, as over the whole prompt.
+        There, chunks also end where the key count crosses 4096 and 8192, the
+        fused kernel's register tiers, so early tokens take the smaller one."""
 
         n_seq, heads, q_len = query.shape[0], query.shape[1], query.shape[2]
+        fused = kernels.lib().sva_summon_strategy(
+            n_seq, heads, q_len, k_len, self._rank, self._subspaces, self._codewords, shortlist,
+            kernels.code_type(codes), 0) == 3
         chunk = self.serving.query_chunk_size
         if chunk is None:
-            per_token = n_seq * heads * max(shortlist, 1) * 8
+            if fused:
+                per_token = n_seq * heads * 4 * (budget + self._rank + self._subspaces * self._codewords + 8)
+            else:
+                per_token = n_seq * heads * max(shortlist, 1) * 8
             chunk = q_len if q_len * per_token <= (512 << 20) else max(128, ((512 << 20) // per_token) // 128 * 128)
         chunk = max(1, int(chunk))
-        for qs in range(0, q_len, chunk):
-            qe = min(q_len, qs + chunk)
+        edges = set(range(chunk, q_len, chunk))
+        if mask is None and fused:
+            edges |= {e - (k_len - q_len) for e in (4096, 8192) if 0 < e - (k_len - q_len) < q_len}
+        bounds = [0, *sorted(edges), q_len]
+        for qs, qe in zip(bounds[:-1], bounds[1:]):
             if mask is not None:
                 yield qs, qe, mask[..., qs:qe, :], k_len
             else:
@@ -306,13 +319,13 @@ class SVALlamaAttention(nn.Module):
         seq = torch.arange(batch, device=device, dtype=torch.int64)
         cat_off, kv_off = seq * cap, seq * rows_per_seq
         outs = []
-        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist):
+        for qs, qe, m, n in self._query_chunks(query, k_len, mask, shortlist, budget, codes):
             lens = torch.full((batch,), n, device=device, dtype=torch.int64)
             qc = query[:, :, qs:qe, :]
             q_low, lut, rng = kernels.query_lut(qc, self.sva_q_proj, self.sva_scale, self.sva_coarse_codebooks)
             _, _, sl_count, fin_idx, fin_count = kernels.summon_select(lut, rng, q_low, codes, k_low, n, shortlist,
                                                                        budget, mask=m, seq_offsets=cat_off,
-                                                                       seq_lens=lens)
+                                                                       seq_lens=lens, keep_shortlist=False)
             outs.append(kernels.verify(qc, keys, values, fin_idx, fin_count, rows, self.scaling, out_dtype=query.dtype,
                                        seq_offsets=kv_off, seq_lens=lens))
             if self.stats is not None:

@@ -53,10 +53,28 @@ def test_summon_strategy_selection():
     assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 4, 64, 2048, 0, 0) == 1
     # one subspace of <= 256 codewords: the shortlist by code class
     assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 1, 256, 2048, 0, 0) == 2
-    # short cache, prefill, or wide codes: one workgroup per item
-    assert lib.sva_summon_strategy(1, 9, 1, 8192, 64, 2, 256, 2048, 0, 0) == 0
+    # short caches and prefill up to 16384 keys: one workgroup per item, shortlist in registers
+    assert lib.sva_summon_strategy(1, 9, 1, 8192, 64, 2, 256, 2048, 0, 0) == 3
+    assert lib.sva_summon_strategy(1, 9, 4096, 8192, 64, 2, 256, 2048, 0, 0) == 3
+    # longer prefill, q = 1 between the two, wide codes, a long shortlist: one workgroup per item
     assert lib.sva_summon_strategy(1, 9, 16, 1 << 20, 64, 4, 64, 2048, 0, 0) == 0
+    assert lib.sva_summon_strategy(1, 9, 1, 20000, 64, 2, 256, 2048, 0, 0) == 0
     assert lib.sva_summon_strategy(1, 9, 1, 1 << 20, 64, 4, 64, 2048, 3, 0) == 0  # int64 codes
+    assert lib.sva_summon_strategy(1, 9, 1, 8192, 64, 2, 256, 4096, 0, 0) == 0
+
+
+def test_summon_select_without_shortlist_outside_the_fused_path():
+    lib = _lib()
+    p = ctypes.c_void_p(256)  # never dereferenced: the arguments are refused first
+    # 1M keys, q = 1: the wide path keeps the shortlist in memory
+    rc = lib.sva_summon_select(p, p, p, p, 0, 0, p, 0, None, None, 1, 9, 1, 1 << 20, 64, 4, 64, 2048, None, 0, 0,
+                               None, None, p, 512, p, p, p, 1 << 30, None)
+    assert rc == 3  # SVA_ERR_UNSUPPORTED
+    assert "shortlist" in lib.sva_last_error().decode()
+    # one of the pair
+    rc = lib.sva_summon_select(p, p, p, p, 0, 0, p, 0, None, None, 1, 9, 4, 8192, 64, 2, 256, 2048, None, 0, 0,
+                               p, None, p, 512, p, p, p, 1 << 30, None)
+    assert rc == 1
 
 
 @pytest.mark.parametrize("call", ["query_lut", "summon", "summon_select", "budget", "verify"])

@@ -38,9 +38,16 @@ def _run(device, codes, k_low, q, q_proj, scale, cb, n_keys, L, B, mask=None, of
                                         torch.from_numpy(scale).to(device), torch.from_numpy(cb).to(device))
     kw = dict(mask=mask, seq_offsets=offs, seq_lens=lens)
     fused = kernels.summon_select(lut, rng, q_low, codes_t, k_low, n_keys, L, B, **kw)
+    # the prefill form: the shortlist stays in the kernel, the rest is the same
+    lean = kernels.summon_select(lut, rng, q_low, codes_t, k_low, n_keys, L, B, keep_shortlist=False, **kw)
     sl_idx, sl_rank, sl_count = kernels.summon(lut, rng, q_low, codes_t, k_low, n_keys, L, **kw)
     fin_idx, fin_count = kernels.budget_select(sl_idx, sl_rank, sl_count, B)
     torch.cuda.synchronize()
+    assert lean[0] is None and lean[1] is None, "the fused per-item path returned a shortlist it was not asked for"
+    assert torch.equal(lean[2], fused[2]) and torch.equal(lean[4], fused[4]), "counts differ without shortlist outputs"
+    lean_idx, lean_count = lean[3].cpu().numpy(), lean[4].cpu().numpy()
+    for i, b in enumerate(lean_count.tolist()):
+        np.testing.assert_array_equal(lean_idx[i, :b], fused[3][i, :b].cpu().numpy())
     split = (sl_idx, sl_rank, sl_count, fin_idx, fin_count)
     fused = [t.cpu().numpy() for t in fused]
     split = [t.cpu().numpy() for t in split]
