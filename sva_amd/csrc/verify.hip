@@ -327,6 +327,172 @@ __global__ void __launch_bounds__(CB) verify_combine_kernel(VerifyParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Many-item verifier (q > 1 over many query tokens, the prefill): one wave
+// per query item walks its own budget list with an online softmax, no
+// barriers.  Lane octet o takes the item's entries o, o + 8, ...; lane c of
+// an octet holds elements [c * D/8, (c + 1) * D/8) of the query, of each K
+// and V row it reads and of its accumulator, so a row is the octet's
+// coalesced 16-byte loads and a score is one octet sum.  The eight octets'
+// running maxima, sums and accumulators merge at the end.  A row that
+// several heads of a KV group choose is read once per head: items run in
+// head-major ranges per XCD, so the group's K and V stay in that XCD's L2.
+constexpr int RB = 256;  // threads per workgroup: 4 items
+
+template <int D, int KV>
+__global__ void __launch_bounds__(RB) verify_rows_kernel(VerifyParams p, int64_t items, int64_t blocks) {
+#pragma clang fp contract(off)
+  constexpr int DL = D / 8;                             // elements per lane
+  constexpr int ES = KV == F32 ? 4 : 2;                 // element bytes
+  constexpr int NV = DL * ES / 16;                      // 16-byte loads per lane and row
+  constexpr int U = NV == 1 ? 4 : (NV == 2 ? 2 : 1);    // entries per octet in flight
+  static_assert(NV >= 1 && NV * 16 == DL * ES, "rows of whole 16-byte lane slices");
+  const int64_t blk = xcd_range_item((int64_t)blockIdx.x, blocks);
+  const int64_t item = blk * (RB / WAVE) + (int64_t)(threadIdx.x / WAVE);
+  if (blk < 0 || item >= items) return;  // wave-uniform; the kernel has no barriers
+  const int lane = lane_id(), oc = lane >> 3, c = lane & 7;
+  const int t = (int)(item % p.Q);
+  const int hq = (int)((item / p.Q) % p.H);
+  const int b = (int)(item / ((int64_t)p.Q * p.H));
+  const int g = hq / (p.H / p.G);
+  const int64_t len = p.lens ? p.lens[b] : p.N;
+  const int64_t off = p.offs ? p.offs[b] : 0;
+  // no entry is valid in an empty sequence (row 0 then need not exist)
+  const int cnt = len > 0 ? max(0, min(p.fin_count[item], p.B)) : 0;
+  float q[DL];
+  const int64_t qb = (int64_t)b * p.q_bs + (int64_t)hq * p.q_hs + (int64_t)t * p.q_ts + c * DL;
+#pragma unroll
+  for (int i = 0; i < DL; ++i) q[i] = load_elem(p.q, qb + i, p.q_dtype);
+  const int32_t* list = p.fin_idx + item * p.B;
+  const int64_t lane0 = (int64_t)g * p.kv_hs + off * p.kv_rs + c * DL;  // element offset of row 0's slice
+  const uint4* kb = reinterpret_cast<const uint4*>((const char*)p.keys + lane0 * ES);
+  const uint4* vb = reinterpret_cast<const uint4*>((const char*)p.values + lane0 * ES);
+  const int64_t rs4 = p.kv_rs * ES / 16;  // row stride in 16-byte words
+  float m = -INFINITY, z = 0.0f, acc[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) acc[i] = 0.0f;
+  auto unpack = [](const uint4 (&w)[NV], float (&x)[DL]) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const uint32_t u[4] = {w[v].x, w[v].y, w[v].z, w[v].w};
+      if constexpr (KV == F32) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[4 * v + k] = __uint_as_float(u[k]);
+      } else if constexpr (KV == BF16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          x[8 * v + 2 * k] = __uint_as_float(u[k] << 16);
+          x[8 * v + 2 * k + 1] = __uint_as_float(u[k] & 0xFFFF0000u);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          x[8 * v + 2 * k] = __half2float(__ushort_as_half((unsigned short)(u[k] & 0xFFFFu)));
+          x[8 * v + 2 * k + 1] = __half2float(__ushort_as_half((unsigned short)(u[k] >> 16)));
+        }
+      }
+    }
+  };
+  int nxt = lane < cnt ? list[lane] : -1;
+  for (int e0 = 0; e0 < cnt; e0 += WAVE) {
+    const int cur = nxt;  // entry e0 + l in lane l, -1 past the count
+    nxt = e0 + WAVE + lane < cnt ? list[e0 + WAVE + lane] : -1;
+    const int nk = min(8, (cnt - e0 + 7) / 8);  // octet rounds of this block that hold entries
+    for (int k0 = 0; k0 < nk; k0 += U) {       // k0 + u < 8: U divides 8
+      uint4 kw[U][NV], vw[U][NV];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int x = __shfl(cur, 8 * (k0 + u) + oc, WAVE);
+        ok[u] = x >= 0 && (int64_t)x < len;
+        const int64_t ro = (int64_t)(ok[u] ? x : 0) * rs4;  // an invalid entry reads row 0, weight 0
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          kw[u][v] = kb[ro + v];
+          vw[u][v] = vb[ro + v];
+        }
+      }
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float k[DL];
+        unpack(kw[u], k);
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DL; ++i) d = __builtin_fmaf(k[i], q[i], d);
+        d = octet_sum(d);
+        sc[u] = ok[u] ? d * p.scaling : -INFINITY;
+      }
+      float mn = m;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mn = fmaxf(mn, sc[u]);
+      const float corr = mn == -INFINITY ? 1.0f : __expf(m - mn);
+      z = z * corr;
+#pragma unroll
+      for (int i = 0; i < DL; ++i) acc[i] = acc[i] * corr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float w = sc[u] == -INFINITY ? 0.0f : __expf(sc[u] - mn);
+        float v[DL];
+        unpack(vw[u], v);
+        z = z + w;
+#pragma unroll
+        for (int i = 0; i < DL; ++i) acc[i] = __builtin_fmaf(w, ok[u] ? v[i] : 0.0f, acc[i]);  // weight 0 meets no NaN
+      }
+      m = mn;
+    }
+  }
+  // merge the eight octets: the wave maximum, then the rescaled sums
+  float M = m;
+  M = fmaxf(M, __shfl_xor(M, 8, WAVE));
+  M = fmaxf(M, __shfl_xor(M, 16, WAVE));
+  M = fmaxf(M, __shfl_xor(M, 32, WAVE));
+  const float f = m == -INFINITY ? 0.0f : __expf(m - M);
+  float Z = z * f;
+  Z = Z + __shfl_xor(Z, 8, WAVE);
+  Z = Z + __shfl_xor(Z, 16, WAVE);
+  Z = Z + __shfl_xor(Z, 32, WAVE);
+  const int64_t ob = (int64_t)b * p.o_bs + (int64_t)hq * p.o_hs + (int64_t)t * p.o_ts + c * DL;
+#pragma unroll
+  for (int i = 0; i < DL; ++i) {
+    float a = acc[i] * f;
+    a = a + __shfl_xor(a, 8, WAVE);
+    a = a + __shfl_xor(a, 16, WAVE);
+    a = a + __shfl_xor(a, 32, WAVE);
+    if (oc == 0) store_elem(p.out, ob + i, p.out_dtype, (M > -INFINITY && Z > 0.0f) ? a / Z : 0.0f);
+  }
+}
+
+// The many-item verifier takes D = 64 or 128 with K and V rows whose lane
+// slices are whole aligned 16-byte words.
+bool verify_rows_eligible(const void* keys, const void* values, int kv_dtype, int64_t kv_head_stride,
+                          int64_t kv_row_stride, int64_t D) {
+  if (D != 64 && D != 128) return false;
+  const int64_t es = kv_dtype == F32 ? 4 : 2;
+  return (((uintptr_t)keys | (uintptr_t)values) & 15u) == 0 && (kv_head_stride * es) % 16 == 0 &&
+         (kv_row_stride * es) % 16 == 0;
+}
+
+template <int D, int KV>
+int launch_rows(const VerifyParams& p, int64_t items, hipStream_t stream) {
+  const int64_t blocks = (items + RB / WAVE - 1) / (RB / WAVE);
+  hipLaunchKernelGGL((verify_rows_kernel<D, KV>), dim3((unsigned)xcd_range_grid(blocks)), dim3(RB), 0, stream, p,
+                     items, blocks);
+  SVA_CHECK_LAUNCH("verify_rows_kernel");
+  return SVA_OK;
+}
+
+int launch_rows_any(const VerifyParams& p, int64_t items, hipStream_t stream) {
+  if (p.D == 64) {
+    if (p.kv_dtype == BF16) return launch_rows<64, BF16>(p, items, stream);
+    if (p.kv_dtype == F16) return launch_rows<64, F16>(p, items, stream);
+    return launch_rows<64, F32>(p, items, stream);
+  }
+  if (p.kv_dtype == BF16) return launch_rows<128, BF16>(p, items, stream);
+  if (p.kv_dtype == F16) return launch_rows<128, F16>(p, items, stream);
+  return launch_rows<128, F32>(p, items, stream);
+}
+
 int verify_split(int64_t grp, int64_t B) {
   const int64_t m = grp * B;
   return (int)std::max<int64_t>(1, (m + EPW - 1) / EPW);
@@ -448,8 +614,11 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.o_bs = out_seq_stride;
   p.o_hs = out_head_stride;
   p.o_ts = out_tok_stride;
-  if (verify_walks_slices(n_seq, G, Q))
+  if (verify_walks_slices(n_seq, G, Q)) {
+    if (verify_rows_eligible(keys, values, kv_dtype, kv_head_stride, kv_row_stride, D))
+      return launch_rows_any(p, n_seq * H * Q, (hipStream_t)stream);
     return launch_part_dim<true>(p, dim3((unsigned)sva::xcd_range_grid(n_seq * G * Q)), lds, (hipStream_t)stream);
+  }
   int rc = launch_part_dim<false>(p, dim3((unsigned)split, (unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
   if (rc != SVA_OK) return rc;
   hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,

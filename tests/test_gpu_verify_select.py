@@ -72,13 +72,14 @@ def test_verify_matches_oracle(device, D, H, G, dtype):
         assert err <= tol, f"head {h}: rel err {err}"
 
 
-def test_verify_ragged_sequences(device):
+@pytest.mark.parametrize("Q", [2, 400])  # 400: 3200 (sequence, KV head, token) groups, one wave per item
+def test_verify_ragged_sequences(device, Q):
     from sva_amd import kernels
 
-    rng = np.random.default_rng(3)
+    rng = np.random.default_rng(3 + Q)
     lens = np.array([700, 1, 2500, 64], np.int64)
     offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int64)
-    H, G, D, budget, Q = 6, 2, 64, 128, 2
+    H, G, D, budget = 6, 2, 64, 128
     rows = int(lens.sum())
     keys = rng.standard_normal((G, rows, D)).astype(np.float32)
     values = rng.standard_normal((G, rows, D)).astype(np.float32)
@@ -90,7 +91,7 @@ def test_verify_ragged_sequences(device):
         for h in range(H):
             for t in range(Q):
                 it = (b * H + h) * Q + t
-                c = min(budget, int(lens[b]) - t)
+                c = max(0, min(budget, int(lens[b]) - t))
                 cnt[it] = c
                 fin[it, :c] = np.sort(rng.choice(int(lens[b]), c, replace=False))
     t = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
@@ -139,10 +140,12 @@ def test_budget_select_matches_oracle(device, L, B, distinct):
 
 
 @pytest.mark.parametrize("D,H,G,Q,dtype", [(64, 9, 3, 700, torch.float32), (64, 9, 3, 700, torch.bfloat16),
-                                           (128, 8, 2, 1030, torch.float32), (40, 6, 3, 690, torch.float32)])
+                                           (128, 8, 2, 1030, torch.float32), (128, 8, 2, 1030, torch.float16),
+                                           (40, 6, 3, 690, torch.float32)])
 def test_verify_many_tokens_walks_slices(device, D, H, G, Q, dtype):
-    # 2048 or more (KV head, token) groups: one workgroup walks all slices of
-    # its group with a running maximum; checked against the oracle per item
+    # 2048 or more (KV head, token) groups: one wave per item (head_dim 64
+    # and 128) or one workgroup walking all slices of its group (other head
+    # dims), each with running maxima; checked against the oracle per item
     # and against the same tokens verified in calls of 16 tokens (the
     # slice-split form with its combine kernel)
     from sva_amd import kernels
