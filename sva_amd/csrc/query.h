@@ -36,6 +36,9 @@ enum QueryForm : int {
   QUERY_DECODE_4_64 = 4,  // query_decode_kernel: one token, D = R = 64, 4x64 / 2x256 / 1x256 codes
   QUERY_DECODE_2_256 = 5,
   QUERY_DECODE_1_256 = 6,
+  QUERY_MFMA16 = 7,      // query_lut_mfma_kernel: the multi form on fp32 MFMA (D % 4, R % 16, C % 16 == 0)
+  QUERY_MFMA32 = 8,
+  QUERY_MFMA64 = 9,
 };
 
 struct QueryLaunch {

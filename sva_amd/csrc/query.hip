@@ -337,6 +337,134 @@ int launch_lut_multi(const LutParams& p, int64_t blocks, size_t lds, hipStream_t
   return SVA_OK;
 }
 
+// The multi form on fp32 MFMA.  v_mfma_f32_16x16x4f32 adds its four k
+// products to the running sum in k order with the rounding of the fma chain,
+// so q_low = (q . W) * scale and the table row q_low[s] . codeword are the
+// same values as query_lut_multi_kernel's (sequential fma chains from 0).
+// Operand layout of the 16x16x4 form: lane l supplies A[l % 16][k0 + l / 16]
+// and B[k0 + l / 16][l % 16] and receives D[4 * (l / 16) + i][l % 16] in
+// element i.  A tile is 16 tokens x 16 ranks (q_low) or 16 tokens x 16
+// codewords of one subspace (the table); a wave takes every eighth tile,
+// keeps a codeword tile's B operand in registers for both token tiles, and
+// folds its bounds over the tile's 16 codewords in DPP rows before one LDS
+// atomic per token.  Rows of the token-major staging are padded by a float
+// so the 16 rows an A operand reads fall in 16 banks.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int MF_BLOCK = 512;
+
+__host__ __device__ inline size_t lut_mfma_lds_bytes(int64_t D, int64_t R, int64_t S) {
+  return sizeof(float) * (size_t)(D * R + MT * (D + 1) + MT * (R + 1)) + sizeof(uint32_t) * (size_t)(2 * MT * S);
+}
+
+template <int SUB>
+__global__ void __launch_bounds__(MF_BLOCK) query_lut_mfma_kernel(LutParams p) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int DP = D + 1, RP = R + 1;
+  const int tiles = (p.Q + MT - 1) / MT;
+  const int bh = blockIdx.x / tiles;
+  const int t0 = (blockIdx.x - bh * tiles) * MT;
+  const int h = bh % p.H;
+  const int b = bh / p.H;
+  const int nt = min(MT, p.Q - t0);
+  float* W = (float*)lds;                    // [D][R]
+  float* qf = W + D * R;                     // [MT][D + 1]
+  float* ql = qf + MT * DP;                  // [MT][R + 1]
+  uint32_t* kmin = (uint32_t*)(ql + MT * RP);  // [MT][S]
+  uint32_t* kmax = kmin + MT * S;            // [MT][S]
+  const int t = threadIdx.x;
+  const int lane = lane_id(), wid = t / WAVE, li = lane & 15, lk = lane >> 4;
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(p.q_proj + (int64_t)h * D * R);
+    for (int i = t; i < D * R / 4; i += MF_BLOCK) reinterpret_cast<float4*>(W)[i] = w4[i];
+  }
+  const int64_t qb = (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
+  for (int e = t; e < MT * D; e += MF_BLOCK) {
+    const int tt = e / D, d = e - tt * D;
+    qf[tt * DP + d] = tt < nt ? load_elem(p.q, qb + (int64_t)(t0 + tt) * p.q_ts + d, p.q_dtype) : 0.0f;
+  }
+  for (int e = t; e < MT * S; e += MF_BLOCK) {
+    kmin[e] = 0xFFFFFFFFu;
+    kmax[e] = 0u;
+  }
+  __syncthreads();
+  const int64_t item0 = ((int64_t)b * p.H + h) * p.Q + t0;
+  const float sc = p.scale[h];
+  // q_low tiles: (token tile, rank tile), D / 4 steps each
+  for (int tile = wid; tile < (MT / 16) * (R / 16); tile += MF_BLOCK / WAVE) {
+    const int tt = tile / (R / 16), r0 = (tile - tt * (R / 16)) * 16;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < D; k0 += 4)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[(tt * 16 + li) * DP + k0 + lk], W[(k0 + lk) * R + r0 + li], acc,
+                                                 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = tt * 16 + 4 * lk + i;
+      const float v = acc[i] * sc;
+      ql[row * RP + r0 + li] = v;
+      if (row < nt) p.q_low[(item0 + row) * R + r0 + li] = v;
+    }
+  }
+  __syncthreads();
+  // table tiles: (subspace, codeword tile) x both token tiles, SUB / 4 steps
+  const float* cbh = p.codebooks + (int64_t)h * S * C * SUB;
+  for (int tile = wid; tile < S * (C / 16); tile += MF_BLOCK / WAVE) {
+    const int s = tile / (C / 16), c0 = (tile - s * (C / 16)) * 16;
+    float bv[SUB / 4];
+#pragma unroll
+    for (int k = 0; k < SUB / 4; ++k) bv[k] = cbh[((int64_t)s * C + c0 + li) * SUB + 4 * k + lk];
+#pragma unroll
+    for (int tt = 0; tt < MT / 16; ++tt) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k = 0; k < SUB / 4; ++k)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ql[(tt * 16 + li) * RP + s * SUB + 4 * k + lk], bv[k], acc, 0, 0,
+                                                   0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = tt * 16 + 4 * lk + i;
+        if (row < nt) p.lut[(item0 + row) * S * C + s * C + c0 + li] = acc[i];
+        // bounds over the tile's 16 codewords (one DPP row), then one atomic per token
+        uint32_t kn = f2key(acc[i]), kx = kn;
+        kn = min(kn, row_shr_keep<1>(kn));
+        kx = max(kx, row_shr_keep<1>(kx));
+        kn = min(kn, row_shr_keep<2>(kn));
+        kx = max(kx, row_shr_keep<2>(kx));
+        kn = min(kn, row_shr_keep<4>(kn));
+        kx = max(kx, row_shr_keep<4>(kx));
+        kn = min(kn, row_shr_keep<8>(kn));
+        kx = max(kx, row_shr_keep<8>(kx));
+        if (li == 15 && row < nt) {
+          atomicMin(&kmin[row * S + s], kn);
+          atomicMax(&kmax[row * S + s], kx);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (t < nt) {
+    float lo = 0.0f, hi = 0.0f;
+    for (int s = 0; s < S; ++s) {
+      lo = lo + key2f(kmin[t * S + s]);
+      hi = hi + key2f(kmax[t * S + s]);
+    }
+    float* rg = p.range + (item0 + t) * 4;
+    rg[0] = lo;
+    rg[1] = hi;
+    rg[2] = -INFINITY;
+    rg[3] = 0.0f;
+  }
+}
+
+template <int SUB>
+int launch_lut_mfma(const LutParams& p, int64_t blocks, size_t lds, hipStream_t stream) {
+  SVA_SET_MAX_LDS_ONCE((query_lut_mfma_kernel<SUB>), sva::kMaxLds, "hipFuncSetAttribute(query_lut_mfma_kernel)");
+  hipLaunchKernelGGL(query_lut_mfma_kernel<SUB>, dim3((unsigned)blocks), dim3(MF_BLOCK), lds, stream, p);
+  SVA_CHECK_LAUNCH("query_lut_mfma_kernel");
+  return SVA_OK;
+}
+
 constexpr int SCORE_BLOCK = 256;
 
 __global__ void __launch_bounds__(SCORE_BLOCK)
@@ -440,6 +568,11 @@ int query_lut_setup(const void* q, int q_dtype, int64_t q_seq_stride, int64_t q_
     out->form = sub == 16 ? QUERY_MULTI16 : (sub == 32 ? QUERY_MULTI32 : QUERY_MULTI64);
     out->blocks = n_seq * H * ((Q + MT - 1) / MT);
     out->lds = mlds;
+    const size_t flds = lut_mfma_lds_bytes(D, R, S);
+    if (D % 4 == 0 && R % 16 == 0 && C % 16 == 0 && flds <= (size_t)sva::kMaxLds) {
+      out->form = sub == 16 ? QUERY_MFMA16 : (sub == 32 ? QUERY_MFMA32 : QUERY_MFMA64);
+      out->lds = flds;
+    }
     return SVA_OK;
   }
   // one token of one sequence at D = R = 64: the decode form
@@ -468,6 +601,9 @@ int query_lut_launch(const QueryLaunch& ql, hipStream_t st) {
     case QUERY_MULTI16: return launch_lut_multi<16>(p, ql.blocks, ql.lds, st);
     case QUERY_MULTI32: return launch_lut_multi<32>(p, ql.blocks, ql.lds, st);
     case QUERY_MULTI64: return launch_lut_multi<64>(p, ql.blocks, ql.lds, st);
+    case QUERY_MFMA16: return launch_lut_mfma<16>(p, ql.blocks, ql.lds, st);
+    case QUERY_MFMA32: return launch_lut_mfma<32>(p, ql.blocks, ql.lds, st);
+    case QUERY_MFMA64: return launch_lut_mfma<64>(p, ql.blocks, ql.lds, st);
     case QUERY_DECODE_4_64:
       hipLaunchKernelGGL((query_decode_kernel<4, 64, QD_WIDE>), dim3((unsigned)ql.blocks), dim3(QD_WIDE), 0, st, p);
       SVA_CHECK_LAUNCH("query_decode_kernel");

@@ -234,7 +234,8 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   const int64_t code_base = (int64_t)h * p.code_hs + off * p.S;
   const int64_t causal_last = len - p.Q + t;
   const int S = p.S, C = p.C;
-  const float sqrt_r = p.sqrt_r;
+  // R = 64 here: dividing by sqrt(R) = 8 is multiplying by 0.125, exactly
+  constexpr float inv_sqrt_r = 0.125f;
   // SB > 0: uint8 codes of SB subspaces, read as one SB-byte load per key,
   // every load of the thread issued before any is used (e[] holds the raw
   // code bytes until the composites replace them), and before the table's
@@ -280,7 +281,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
           acc = acc + tab[s * C + c];
         }
       }
-      e[i] = composite(f2key(acc / sqrt_r), (uint32_t)n);
+      e[i] = composite(f2key(acc * inv_sqrt_r), (uint32_t)n);
       vor |= e[i];
       vand &= e[i];
       ++cnt;
@@ -339,7 +340,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
       for (int u = 0; u < REG_OCT; ++u) {
         const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
         const float d = rank_dot64_oct8(r0[u], r1[u], q0, q1);
-        if (c == 0 && j < leff) rank[j] = d / sqrt_r;
+        if (c == 0 && j < leff) rank[j] = d * inv_sqrt_r;
       }
     }
   }

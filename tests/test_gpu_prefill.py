@@ -130,10 +130,12 @@ def test_fused_item_packed_sequences(device):
 
 
 @pytest.mark.parametrize("S,C,Q,dtype", [(2, 256, 75, torch.bfloat16), (4, 64, 40, torch.float32),
-                                         (1, 256, 9, torch.float16), (4, 48, 33, torch.float32)])
+                                         (1, 256, 9, torch.float16), (4, 48, 33, torch.float32),
+                                         (2, 40, 20, torch.float32)])
 def test_query_lut_many_tokens_matches_per_token(device, S, C, Q, dtype):
     # 8 or more tokens per head take the multi-token table kernel (weights
-    # staged once per 32 tokens); every output equals the per-token kernel's
+    # staged once per 32 tokens; fp32 MFMA where C is a multiple of 16);
+    # every output equals the per-token kernel's fma chains bit for bit
     from sva_amd import kernels
 
     H, D, R = 3, 64, 64
