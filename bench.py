@@ -5,15 +5,18 @@ Workload (one step = one decode lookup of one layer for one query token):
   rank 64, PQ codes uint8 (default 4x64), shortlist 2048 / budget 512, q = 1.
   K/V bf16 [3, N, 64]; k_low fp32 [9, N, 64] (the production catalog);
   codebooks and learned maps N(0, 1) / N(0, 1/64); synthetic data, seeded.
-A step runs three HIP calls on torch's current stream:
-  query_lut -> summon_select (PQ scan, exact shortlist, rescore and budget
-  select) -> GQA verifier.
+A step is one sva_lookup_verify call on torch's current stream: the query
+table and sampled floor, the PQ scan with the rank scores of its candidates,
+and the finish (exact shortlist and budget selects, then the GQA verifier).
 Caches of `--layers` distinct layers are rotated so that the codes touched
 per step (>256 MB over the rotation) do not stay in the 256 MB Infinity Cache.
 
 Prints ONE JSON line (value = microseconds per query per layer, lower is
-better) with a roofline object for the dominant kernel (summon) and the CPU
-oracle timed on this host on a bounded sample of the same workload.
+better) with a roofline object for the step's kernels and the CPU oracle
+timed on this host on a bounded sample of the same workload.  Unless told
+otherwise the line also carries the 30-layer model's decode tok/s and
+prefill time ("decode"), the ragged continuous-batch step ("ragged") and the
+batch-8 socket model's tok/s ("socket"), each measured at its own step count.
 """
 
 from __future__ import annotations
@@ -130,6 +133,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the decode lookups")
     ap.add_argument("--no-decode", action="store_true", help="skip the model decode tok/s figure of the decode line")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the ragged-batch and socket figures of the decode line")
     ap.add_argument("--cpu-decode-steps", type=int, default=8, help="timed CPU decode steps of the model decode")
     ap.add_argument("--seed", type=int, default=17)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -387,6 +392,10 @@ def write_suite(args):
 
 
 def ragged_suite(args):
+    print(json.dumps(ragged_measure(args)), flush=True)
+
+
+def ragged_measure(args) -> dict:
     """Continuous-batch decode over packed sequences: a pool of --pool resident
     sequences (cache lengths log-uniform in [4096, 131072], 9 q-heads / 3 KV
     heads, head_dim 64, rank 64, 2x256 codes from sva_write_encode, static
@@ -468,7 +477,7 @@ def ragged_suite(args):
     e1.record()
     torch.cuda.synchronize()
     gpu_us = 1e3 * e0.elapsed_time(e1) / n_ev
-    print(json.dumps({
+    return {
         "metric": "ragged continuous-batch decode step (static inverted, 512/128 class budget 128)",
         "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(us_step / 1e3, 4), "higher_is_better": False, "dtype": "fp32 scores / bf16 K,V",
@@ -479,10 +488,14 @@ def ragged_suite(args):
         "sequences_per_s": round(args.batch / (us_step * 1e-6), 1),
         "gpu_us_per_step": round(gpu_us, 2),
         "mean_keys_per_sequence": round(keys_seen / (steps * args.batch), 1),
-    }), flush=True)
+    }
 
 
 def socket_suite(args):
+    print(json.dumps(socket_measure(args)), flush=True)
+
+
+def socket_measure(args) -> dict:
     """Late-layer socket on a SmolLM2-135M-architecture decoder (random init,
     bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64): full attention in
     layers 0-25, SVA (scan, shortlist 8192 / budget 2048, synthetic 2x256
@@ -569,7 +582,7 @@ def socket_suite(args):
             for i in socket:
                 model.model.layers[i].self_attn = model.model.layers[i].self_attn.sva_attn
     tok_s = batch * args.decode_steps / sva_s
-    print(json.dumps({
+    return {
         "metric": "socket decode tok/s (batch, SVA + residual adapter in layers 26-29)", "value": round(tok_s, 1),
         "unit": "tok/s", "n_gpus": 1, "steps": args.decode_steps, "warmup": 4,
         "ms_per_step": round(1e3 * sva_s / args.decode_steps, 3), "higher_is_better": True, "scaling": "weak",
@@ -581,7 +594,7 @@ def socket_suite(args):
         "dense_attention": {"tok_s": round(batch * args.decode_steps / dense_s, 1), "attention": "torch sdpa, bf16"},
         "prefill_s_full_attention": round(prefill_s, 3),
         "sva_stats": {k: round(v, 3) for k, v in summary.items() if isinstance(v, float) and v == v},
-    }), flush=True)
+    }
 
 
 def cpu_decode_baseline(torch, model, past, tok, steps: int, warmups: int = 3):
@@ -1016,6 +1029,12 @@ def main():
         del layers, plan, outs
         torch.cuda.empty_cache()
         result["decode"] = model_decode(args, with_cpu=not args.no_cpu_baseline)
+    if not args.no_extra:
+        # the ragged continuous batch and the batch-8 socket model at their own step counts (about 30 s)
+        torch.cuda.empty_cache()
+        result["ragged"] = ragged_measure(argparse.Namespace(**{**vars(args), "steps": 2000, "warmup": 200}))
+        torch.cuda.empty_cache()
+        result["socket"] = socket_measure(args)
     print(json.dumps(result), flush=True)
 
 
