@@ -556,6 +556,96 @@ __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p)
   }
 }
 
+// A decode step's append (at most FEW_ROWS rows): one workgroup per head,
+// the same arithmetic as the kernels above with the work spread over the
+// threads instead of over a tile of rows: thread (row, r) forms k_low[row][r]
+// by the fma chain over d, then, per subspace and row, thread c the distance
+// to codeword c, and the workgroup the first index of the least distance.
+// The bulk kernels stage a 64-row tile's map and codebooks for one row.
+constexpr int FEW_ROWS = 4;
+
+template <int SUB>
+__global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
+#pragma clang fp contract(off)
+  __shared__ float kr[FEW_ROWS][256];  // the new K rows (D <= 256)
+  __shared__ float xl[FEW_ROWS][256];  // their k_low rows (R <= 256)
+  __shared__ float rbest[WT / WAVE];
+  __shared__ int rarg[WT / WAVE];
+  const int D = p.D, R = p.R, S = p.S, C = p.C;
+  const int sub = SUB > 0 ? SUB : R / S;
+  const int h = blockIdx.x;
+  const int g = h / (p.H / p.G);
+  const int nr = (int)p.n_rows;  // <= FEW_ROWS
+  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  for (int e = t; e < nr * D; e += WT) {
+    const int j = e / D, d = e - j * D;
+    kr[j][d] = load_elem(p.keys, (int64_t)g * p.kv_hs + (p.row0 + j) * p.kv_rs + d, p.kv_dtype);
+  }
+  __syncthreads();
+  const float* W = p.k_proj + (int64_t)h * D * R;
+  for (int e = t; e < nr * R; e += WT) {
+    const int j = e / R, r = e - j * R;
+    float acc = 0.0f;
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(kr[j][d], W[d * R + r], acc);
+    xl[j][r] = acc;
+    p.k_low[(int64_t)h * p.klow_hs + (p.row0 + j) * R + r] = acc;
+  }
+  if (p.codes == nullptr) return;  // uniform
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const float* cbs = p.codebooks + ((int64_t)h * S + s) * C * sub;
+    for (int j = 0; j < nr; ++j) {
+      const float* xs = &xl[j][s * sub];
+      const float xx = torch_order_dot(xs, xs, sub);
+      // this thread's codewords in ascending order: the least distance, its
+      // first index; NaN never wins, and none at all is index INT_MAX
+      float best = INFINITY;
+      int arg = 0x7FFFFFFF;
+      for (int c = t; c < C; c += WT) {
+        const float* cr = cbs + (int64_t)c * sub;
+        float xc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < sub; ++k) xc = __builtin_fmaf(xs[k], cr[k], xc);  // sub = SUB when SUB > 0
+        const float dist = (xx - 2.0f * xc) + torch_order_dot(cr, cr, sub);
+        if (dist < best) {
+          best = dist;
+          arg = c;
+        }
+      }
+      // (best, arg) ordered by distance, then index: across the wave, then the waves
+      for (int o = 1; o < WAVE; o <<= 1) {
+        const float b2 = __shfl_xor(best, o, WAVE);
+        const int a2 = __shfl_xor(arg, o, WAVE);
+        if (b2 < best || (b2 == best && a2 < arg)) {
+          best = b2;
+          arg = a2;
+        }
+      }
+      if (lane == 0) {
+        rbest[wid] = best;
+        rarg[wid] = arg;
+      }
+      __syncthreads();
+      if (t == 0) {
+        for (int w = 1; w < WT / WAVE; ++w)
+          if (rbest[w] < best || (rbest[w] == best && rarg[w] < arg)) {
+            best = rbest[w];
+            arg = rarg[w];
+          }
+        store_code(p.codes, (int64_t)h * p.code_hs + (p.row0 + j) * S + s, p.ctype, arg == 0x7FFFFFFF ? 0 : arg);
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int SUB>
+int launch_few(const WriteParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((write_encode_few_kernel<SUB>), dim3((unsigned)p.H), dim3(WT), 0, stream, p);
+  SVA_CHECK_LAUNCH("write_encode_few_kernel");
+  return SVA_OK;
+}
+
 size_t write_lds_bytes(int64_t D, int64_t R, int64_t S, int64_t C) {
   const int64_t sub = R / S;
   return sizeof(float) * (size_t)(D * R + KT * (D + 1) + KT * (R + 1) + C * (sub + CB_PAD) + C + KT) + 16;
@@ -617,6 +707,14 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   p.ctype = code_type;
   p.code_hs = code_head_stride;
   const dim3 grid((unsigned)tiles, (unsigned)H);
+  if (n_rows <= FEW_ROWS) {  // a decode step's append
+    switch (R / S) {
+      case 16: return launch_few<16>(p, (hipStream_t)stream);
+      case 32: return launch_few<32>(p, (hipStream_t)stream);
+      case 64: return launch_few<64>(p, (hipStream_t)stream);
+      default: return launch_few<0>(p, (hipStream_t)stream);
+    }
+  }
   if (!tiled) {
     hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, (hipStream_t)stream, p);
     SVA_CHECK_LAUNCH("write_encode_rowwise_kernel");

@@ -3,7 +3,8 @@
 k_low bit-exact with the oracle's projection (itself bit-exact with torch's
 many-row einsum, tests/test_oracle.py); codes equal to the oracle's argmin
 except where the oracle's two best distances lie within a few ulp (counted
-and bounded); an append in two row ranges equals one fresh encode.
+and bounded); an append in two row ranges equals one fresh encode, and so do
+decode-step appends of one to four rows (their own kernel).
 """
 
 from __future__ import annotations
@@ -91,3 +92,31 @@ def test_write_ties_take_first_centroid(device):
     assert codes.max() < 8
     ref_codes = oracle.encode_product_keys(k_low, cb)
     np.testing.assert_array_equal(codes, ref_codes)
+
+
+@pytest.mark.parametrize("S,C,kv_dtype,code_dtype,D,R", [(2, 256, torch.bfloat16, torch.uint8, 64, 64),
+                                                         (4, 64, torch.float32, torch.uint8, 64, 64),
+                                                         (1, 256, torch.float32, torch.int64, 128, 64),
+                                                         (3, 5, torch.float32, torch.uint8, 16, 6)])
+def test_decode_appends_equal_fresh(device, S, C, kv_dtype, code_dtype, D, R):
+    # appends of 1 to 4 rows (a decode step's catalog append) give the fresh encode's bits and codes
+    N = 211
+    kt, k_proj, cb, _ = _case(device, N, S, C, kv_dtype, seed=S + C + D, H=6, G=3, D=D, R=R)
+    fresh = _encode(device, kt, k_proj, cb, code_dtype, [(0, N)])
+    ranges, a, k = [(0, 100)], 100, 0
+    while a < N:
+        b = min(N, a + 1 + k % 4)
+        ranges.append((a, b))
+        a, k = b, k + 1
+    steps = _encode(device, kt, k_proj, cb, code_dtype, ranges)
+    np.testing.assert_array_equal(fresh[0].view(np.uint32), steps[0].view(np.uint32))
+    np.testing.assert_array_equal(fresh[1], steps[1])
+
+
+def test_decode_append_ties_take_first_centroid(device):
+    N, S, C = 40, 2, 256
+    kt, k_proj, cb, _ = _case(device, N, S, C, torch.float32, seed=13)
+    cb[:, :, 128:] = cb[:, :, :128]
+    k_low, codes = _encode(device, kt, k_proj, cb, torch.uint8, [(a, a + 1) for a in range(N)])
+    assert codes.max() < 128
+    np.testing.assert_array_equal(codes, oracle.encode_product_keys(k_low, cb))
