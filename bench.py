@@ -157,6 +157,11 @@ def parse_args():
     ap.add_argument("--decode-steps", type=int, default=256, help="model suite: timed greedy decode steps")
     ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
                     help="summarize rocprofv3 outputs of this benchmark into profiles/ and exit")
+    ap.add_argument("--write-trace-profile", nargs=2, metavar=("STATS_CSV", "NAME"),
+                    help="summarize a --kernel-trace --stats file into profiles/NAME.md and exit")
+    ap.add_argument("--profile-title", default="Kernel durations")
+    ap.add_argument("--profile-command", default="")
+    ap.add_argument("--profile-rows", type=int, default=25)
     return ap.parse_args()
 
 
@@ -272,6 +277,52 @@ def _kernel_key(name):
     return None
 
 
+def _short_kernel_name(name: str) -> str:
+    """`void (anonymous namespace)::foo<4, 2>(Args...)` -> `foo<4, 2>`."""
+    base = name.split("(anonymous namespace)::", 1)[-1]
+    depth, out = 0, []
+    for ch in base:
+        if ch == "(" and depth == 0:
+            break
+        depth += ch == "<"
+        depth -= ch == ">"
+        out.append(ch)
+    short = "".join(out).strip()
+    return short[5:] if short.startswith("void ") else short
+
+
+def write_trace_profile(args):
+    """Summarize a rocprofv3 --kernel-trace --stats file of any run of this
+    benchmark (the model, ragged or socket suites) into profiles/NAME.md: the
+    kernels by total time, with this library's kernels marked."""
+
+    import csv
+
+    stats_csv, name = args.write_trace_profile
+    own = ("summon", "verify", "query_", "wide_", "class_", "write_encode", "inverted", "static_", "refill",
+           "budget_select", "decode_stats", "pq_scores", "postings", "adapter", "unique_", "ragged_", "cand_")
+    rows = []
+    with open(stats_csv) as f:
+        for r in csv.DictReader(f):
+            if "spin_kernel" in r["Name"]:  # torch.cuda._sleep, which holds the stream for event timing
+                continue
+            rows.append((_short_kernel_name(r["Name"]), int(r["Calls"]), float(r["TotalDurationNs"]),
+                         float(r["AverageNs"]), float(r["MinNs"]), float(r["MaxNs"])))
+    rows.sort(key=lambda x: -x[2])
+    total = sum(x[2] for x in rows)
+    mine = sum(x[2] for x in rows if any(o in x[0] for o in own))
+    lines = [f"# {args.profile_title}", "", f"Command: `{args.profile_command}` (file `*_kernel_stats.csv`).", "",
+             f"All kernels: {total / 1e6:.2f} ms; this library's (marked *): {mine / 1e6:.2f} ms.", "",
+             "| kernel | calls | total ms | avg us | min us | max us |", "|---|---:|---:|---:|---:|---:|"]
+    for k, c, tot, a, mn, mx in rows[:args.profile_rows]:
+        mark = " *" if any(o in k for o in own) else ""
+        k = k if len(k) < 90 else k[:87] + "..."
+        lines.append(f"| `{k}`{mark} | {c} | {tot / 1e6:.3f} | {a / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |")
+    out = ROOT / "profiles" / f"{name}.md"
+    out.write_text("\n".join(lines) + "\n")
+    print(f"wrote {out}")
+
+
 def write_profiles(args):
     """Summarize a --kernel-trace --stats run and two --pmc runs (FETCH_SIZE,
     WRITE_SIZE) of this benchmark into profiles/: per-kernel durations, HBM
@@ -303,9 +354,11 @@ def write_profiles(args):
     write_scale = copy_kib / avg[("__amd_rocclr_copyBuffer", "WRITE_SIZE")]
     cfg = f"--layout {args.layout} --shortlist {args.shortlist} --budget {args.budget}"
     cmd_trace = (f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o ks -- python bench.py --steps 300 "
-                 f"--warmup 50 --no-cpu-baseline --no-decode --no-graph --calibrate-copy {args.calibrate_copy} {cfg}")
+                 f"--warmup 50 --no-cpu-baseline --no-decode --no-extra --no-graph --calibrate-copy {args.calibrate_copy} "
+                 f"{cfg}")
     cmd_pmc = (f"rocprofv3 --pmc {{FETCH_SIZE|WRITE_SIZE}} --output-format csv -d OUT -o pf -- python bench.py "
-               f"--steps 20 --warmup 5 --no-cpu-baseline --no-decode --no-graph --calibrate-copy {args.calibrate_copy} "
+               f"--steps 20 --warmup 5 --no-cpu-baseline --no-decode --no-extra --no-graph --calibrate-copy "
+               f"{args.calibrate_copy} "
                f"{cfg}")
     lines = [f"# Kernel durations: decode step (sva_lookup_verify) at 1M keys, {args.layout} codes, L/B "
              f"{args.shortlist}/{args.budget}, q=1, 9 q-heads / 3 KV heads",
@@ -880,6 +933,9 @@ def main():
     args = parse_args()
     if args.write_profiles:
         write_profiles(args)
+        return
+    if args.write_trace_profile:
+        write_trace_profile(args)
         return
     if args.suite in ("write", "model", "ragged", "socket", "overshoot", "verify"):
         if args.gpus != 1:
