@@ -563,12 +563,14 @@ __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p)
 // to codeword c, and the workgroup the first index of the least distance.
 // The bulk kernels stage a 64-row tile's map and codebooks for one row.
 constexpr int FEW_ROWS = 4;
+constexpr int FEW_MAP = 64 * 64;  // map floats staged in LDS
 
 template <int SUB>
 __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
 #pragma clang fp contract(off)
   __shared__ float kr[FEW_ROWS][256];  // the new K rows (D <= 256)
   __shared__ float xl[FEW_ROWS][256];  // their k_low rows (R <= 256)
+  __shared__ __align__(16) float ws[FEW_MAP];  // the head's map when D * R <= FEW_MAP
   __shared__ float rbest[WT / WAVE];
   __shared__ int rarg[WT / WAVE];
   const int D = p.D, R = p.R, S = p.S, C = p.C;
@@ -577,16 +579,35 @@ __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
   const int g = h / (p.H / p.G);
   const int nr = (int)p.n_rows;  // <= FEW_ROWS
   const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
+  const float* W = p.k_proj + (int64_t)h * D * R;
+  const bool map_in_lds = D * R <= FEW_MAP && (D * R) % 4 == 0 && ((uintptr_t)W & 15u) == 0;  // uniform
+  // thread c < C holds codeword c's row of the current subspace (SUB > 0, C <= WT), requested for
+  // subspace 0 before the projection so that both loads overlap
+  const bool rows_in_regs = SUB > 0 && C <= WT;
+  float crow[SUB > 0 ? SUB : 1];
+  auto load_row = [&](int s) {
+    if constexpr (SUB > 0) {
+      const float4* src = reinterpret_cast<const float4*>(p.codebooks + (((int64_t)h * S + s) * C + min(t, C - 1)) * SUB);
+#pragma unroll
+      for (int k = 0; k < SUB / 4; ++k) {
+        const float4 v = src[k];
+        crow[4 * k] = v.x, crow[4 * k + 1] = v.y, crow[4 * k + 2] = v.z, crow[4 * k + 3] = v.w;
+      }
+    }
+  };
+  if (rows_in_regs && p.codes != nullptr) load_row(0);
+  if (map_in_lds)
+    for (int i = t; i < D * R / 4; i += WT) reinterpret_cast<float4*>(ws)[i] = reinterpret_cast<const float4*>(W)[i];
   for (int e = t; e < nr * D; e += WT) {
     const int j = e / D, d = e - j * D;
     kr[j][d] = load_elem(p.keys, (int64_t)g * p.kv_hs + (p.row0 + j) * p.kv_rs + d, p.kv_dtype);
   }
   __syncthreads();
-  const float* W = p.k_proj + (int64_t)h * D * R;
+  const float* Wm = map_in_lds ? ws : W;
   for (int e = t; e < nr * R; e += WT) {
     const int j = e / R, r = e - j * R;
     float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(kr[j][d], W[d * R + r], acc);
+    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(kr[j][d], Wm[d * R + r], acc);
     xl[j][r] = acc;
     p.k_low[(int64_t)h * p.klow_hs + (p.row0 + j) * R + r] = acc;
   }
@@ -594,6 +615,11 @@ __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
   __syncthreads();
   for (int s = 0; s < S; ++s) {
     const float* cbs = p.codebooks + ((int64_t)h * S + s) * C * sub;
+    if (rows_in_regs && s > 0) load_row(s);
+    float cn = 0.0f;  // the codeword's squared norm in torch's sum order (rows held in registers)
+    if constexpr (SUB > 0) {
+      if (rows_in_regs) cn = torch_order_dot(crow, crow, SUB);
+    }
     for (int j = 0; j < nr; ++j) {
       const float* xs = &xl[j][s * sub];
       const float xx = torch_order_dot(xs, xs, sub);
@@ -601,15 +627,27 @@ __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
       // first index; NaN never wins, and none at all is index INT_MAX
       float best = INFINITY;
       int arg = 0x7FFFFFFF;
-      for (int c = t; c < C; c += WT) {
-        const float* cr = cbs + (int64_t)c * sub;
-        float xc = 0.0f;
+      if (rows_in_regs) {
+        if (t < C) {
+          float xc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < sub; ++k) xc = __builtin_fmaf(xs[k], cr[k], xc);  // sub = SUB when SUB > 0
-        const float dist = (xx - 2.0f * xc) + torch_order_dot(cr, cr, sub);
-        if (dist < best) {
-          best = dist;
-          arg = c;
+          for (int k = 0; k < (SUB > 0 ? SUB : 1); ++k) xc = __builtin_fmaf(xs[k], crow[k], xc);
+          const float dist = (xx - 2.0f * xc) + cn;
+          if (dist < best) {
+            best = dist;
+            arg = t;
+          }
+        }
+      } else {
+        for (int c = t; c < C; c += WT) {
+          const float* cr = cbs + (int64_t)c * sub;
+          float xc = 0.0f;
+          for (int k = 0; k < sub; ++k) xc = __builtin_fmaf(xs[k], cr[k], xc);
+          const float dist = (xx - 2.0f * xc) + torch_order_dot(cr, cr, sub);
+          if (dist < best) {
+            best = dist;
+            arg = c;
+          }
         }
       }
       // (best, arg) ordered by distance, then index: across the wave, then the waves
@@ -707,7 +745,8 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   p.ctype = code_type;
   p.code_hs = code_head_stride;
   const dim3 grid((unsigned)tiles, (unsigned)H);
-  if (n_rows <= FEW_ROWS) {  // a decode step's append
+  if (n_rows <= FEW_ROWS) {  // a decode step's append (codeword rows as float4 where aligned)
+    if (((uintptr_t)codebooks & 15u) != 0) return launch_few<0>(p, (hipStream_t)stream);
     switch (R / S) {
       case 16: return launch_few<16>(p, (hipStream_t)stream);
       case 32: return launch_few<32>(p, (hipStream_t)stream);
