@@ -98,10 +98,10 @@ def test_smollm2_layer_prefill_8192(device):
         model(input_ids=prompt, use_cache=False)
         q, k, v, mask, out = store[0]
         assert mask is None and tuple(q.shape) == (1, HEADS, n, HEAD_DIM)
-        # the prefill's query chunks: 3584 tokens (512 MiB of shortlist per launch)
-        chunk = max(128, ((512 << 20) // (HEADS * 2048 * 8)) // 128 * 128)
-        assert chunk == 3584
-        tokens = sorted({0, chunk - 1, chunk, 2 * chunk - 1, 2 * chunk, n - 1})
+        # the prefill's query chunks end where the key count crosses 4096 (the
+        # fused summon's register tiers); 3584 and 7168 were the chunk ends of
+        # the form that kept 512 MiB of shortlist per launch
+        tokens = sorted({0, 3583, 3584, 4095, 4096, 7167, 7168, n - 1})
         allowed = np.where(np.arange(n)[None, :] <= np.asarray(tokens)[:, None], 0.0, -np.inf).astype(np.float32)
         print(f"prefill 8192: oracle on tokens {tokens}", flush=True)
         ref = _oracle_scan(attn, q[0][:, tokens], k[0], v[0], n, 2048, 512, mask=allowed)
