@@ -328,28 +328,37 @@ __global__ void __launch_bounds__(CB) verify_combine_kernel(VerifyParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Many-item verifier (q > 1 over many query tokens, the prefill): one wave
-// per query item walks its own budget list with an online softmax, no
-// barriers.  Lane octet o takes the item's entries o, o + 8, ...; lane c of
-// an octet holds elements [c * D/8, (c + 1) * D/8) of the query, of each K
-// and V row it reads and of its accumulator, so a row is the octet's
-// coalesced 16-byte loads and a score is one octet sum.  The eight octets'
-// running maxima, sums and accumulators merge at the end.  A row that
-// several heads of a KV group choose is read once per head: items run in
-// head-major ranges per XCD, so the group's K and V stay in that XCD's L2.
-constexpr int RB = 256;  // threads per workgroup: 4 items
+// Row-streaming verifier.  WPI = 1 (many items: the prefill): one wave per
+// query item walks its own budget list with an online softmax, no barriers,
+// four items per workgroup.  WPI > 1 (few items: a decode step, a ragged
+// batch): one workgroup of WPI waves per item, wave w taking the item's
+// octet rounds w, w + WPI, ..., so a decode head's 512 rows are one round of
+// loads per wave; the waves' partials merge through LDS.  Lane octet o takes
+// entry 8 r + o of round r; lane c of an octet holds elements
+// [c * D/8, (c + 1) * D/8) of the query, of each K and V row it reads and of
+// its accumulator, so a row is the octet's coalesced 16-byte loads and a
+// score is one octet sum.  A wave's eight octets merge by cross-lane sums.
+// A row that several heads of a KV group choose is read once per head:
+// items run in head-major ranges per XCD, so the group's K and V stay in
+// that XCD's L2.
+constexpr int RB = 256;   // threads per workgroup at WPI = 1: 4 items
+constexpr int RWPI = 16;  // waves per item of the few-item form
 
-template <int D, int KV>
-__global__ void __launch_bounds__(RB) verify_rows_kernel(VerifyParams p, int64_t items, int64_t blocks) {
+template <int D, int KV, int WPI>
+__global__ void __launch_bounds__(WPI == 1 ? RB : WPI * WAVE)
+    verify_rows_kernel(VerifyParams p, int64_t items, int64_t blocks) {
 #pragma clang fp contract(off)
   constexpr int DL = D / 8;                             // elements per lane
   constexpr int ES = KV == F32 ? 4 : 2;                 // element bytes
   constexpr int NV = DL * ES / 16;                      // 16-byte loads per lane and row
   constexpr int U = NV == 1 ? 4 : (NV == 2 ? 2 : 1);    // entries per octet in flight
   static_assert(NV >= 1 && NV * 16 == DL * ES, "rows of whole 16-byte lane slices");
+  __shared__ float part[WPI > 1 ? WPI : 1][D + 2];      // WPI > 1: each wave's m, z and sums
   const int64_t blk = xcd_range_item((int64_t)blockIdx.x, blocks);
-  const int64_t item = blk * (RB / WAVE) + (int64_t)(threadIdx.x / WAVE);
-  if (blk < 0 || item >= items) return;  // wave-uniform; the kernel has no barriers
+  const int wid = (int)threadIdx.x / WAVE;
+  const int64_t item = WPI > 1 ? blk : blk * (RB / WAVE) + wid;
+  const int w = WPI > 1 ? wid : 0;  // this wave's share of the item's rounds
+  if (blk < 0 || item >= items) return;  // uniform per workgroup (WPI > 1) or wave (WPI = 1)
   const int lane = lane_id(), oc = lane >> 3, c = lane & 7;
   const int t = (int)(item % p.Q);
   const int hq = (int)((item / p.Q) % p.H);
@@ -393,11 +402,20 @@ __global__ void __launch_bounds__(RB) verify_rows_kernel(VerifyParams p, int64_t
       }
     }
   };
-  int nxt = lane < cnt ? list[lane] : -1;
-  for (int e0 = 0; e0 < cnt; e0 += WAVE) {
-    const int cur = nxt;  // entry e0 + l in lane l, -1 past the count
-    nxt = e0 + WAVE + lane < cnt ? list[e0 + WAVE + lane] : -1;
-    const int nk = min(8, (cnt - e0 + 7) / 8);  // octet rounds of this block that hold entries
+  // this wave's rounds r = w + WPI j hold entries 8 r + o (octet o); lane
+  // 8 k + o holds the entry of round j0 + k, position o, of the current
+  // block of eight rounds
+  const int rounds = (cnt + 7) / 8;
+  const int mine = rounds > w ? (rounds - w + WPI - 1) / WPI : 0;
+  auto entry = [&](int j, int o) { return 8 * (w + WPI * j) + o; };
+  int nxt = (lane >> 3) < mine && entry(lane >> 3, lane & 7) < cnt ? list[entry(lane >> 3, lane & 7)] : -1;
+  for (int j0 = 0; j0 < mine; j0 += 8) {
+    const int cur = nxt;  // the entry of round j0 + l / 8, position l % 8, in lane l; -1 past the count
+    {
+      const int jn = j0 + 8 + (lane >> 3);
+      nxt = jn < mine && entry(jn, lane & 7) < cnt ? list[entry(jn, lane & 7)] : -1;
+    }
+    const int nk = min(8, mine - j0);          // rounds of this block
     for (int k0 = 0; k0 < nk; k0 += U) {       // k0 + u < 8: U divides 8
       uint4 kw[U][NV], vw[U][NV];
       bool ok[U];
@@ -452,14 +470,40 @@ __global__ void __launch_bounds__(RB) verify_rows_kernel(VerifyParams p, int64_t
   Z = Z + __shfl_xor(Z, 8, WAVE);
   Z = Z + __shfl_xor(Z, 16, WAVE);
   Z = Z + __shfl_xor(Z, 32, WAVE);
-  const int64_t ob = (int64_t)b * p.o_bs + (int64_t)hq * p.o_hs + (int64_t)t * p.o_ts + c * DL;
+  const int64_t ob = (int64_t)b * p.o_bs + (int64_t)hq * p.o_hs + (int64_t)t * p.o_ts;
 #pragma unroll
   for (int i = 0; i < DL; ++i) {
     float a = acc[i] * f;
     a = a + __shfl_xor(a, 8, WAVE);
     a = a + __shfl_xor(a, 16, WAVE);
     a = a + __shfl_xor(a, 32, WAVE);
-    if (oc == 0) store_elem(p.out, ob + i, p.out_dtype, (M > -INFINITY && Z > 0.0f) ? a / Z : 0.0f);
+    if constexpr (WPI == 1) {
+      if (oc == 0) store_elem(p.out, ob + c * DL + i, p.out_dtype, (M > -INFINITY && Z > 0.0f) ? a / Z : 0.0f);
+    } else {
+      if (oc == 0) part[w][2 + c * DL + i] = a;
+    }
+  }
+  if constexpr (WPI > 1) {
+    // the waves' partials: the item's maximum, then the rescaled sums
+    if (lane == 0) {
+      part[w][0] = M;
+      part[w][1] = Z;
+    }
+    __syncthreads();
+    const int d = (int)threadIdx.x;
+    if (d < D) {
+      float Mi = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < WPI; ++v) Mi = fmaxf(Mi, part[v][0]);
+      float Zi = 0.0f, a = 0.0f;
+#pragma unroll
+      for (int v = 0; v < WPI; ++v) {
+        const float fv = part[v][0] == -INFINITY ? 0.0f : __expf(part[v][0] - Mi);
+        Zi = Zi + part[v][1] * fv;
+        a = a + part[v][2 + d] * fv;
+      }
+      store_elem(p.out, ob + d, p.out_dtype, (Mi > -INFINITY && Zi > 0.0f) ? a / Zi : 0.0f);
+    }
   }
 }
 
@@ -473,24 +517,25 @@ bool verify_rows_eligible(const void* keys, const void* values, int kv_dtype, in
          (kv_row_stride * es) % 16 == 0;
 }
 
-template <int D, int KV>
+template <int D, int KV, int WPI>
 int launch_rows(const VerifyParams& p, int64_t items, hipStream_t stream) {
-  const int64_t blocks = (items + RB / WAVE - 1) / (RB / WAVE);
-  hipLaunchKernelGGL((verify_rows_kernel<D, KV>), dim3((unsigned)xcd_range_grid(blocks)), dim3(RB), 0, stream, p,
-                     items, blocks);
+  const int64_t blocks = WPI > 1 ? items : (items + RB / WAVE - 1) / (RB / WAVE);
+  hipLaunchKernelGGL((verify_rows_kernel<D, KV, WPI>), dim3((unsigned)xcd_range_grid(blocks)),
+                     dim3(WPI > 1 ? WPI * WAVE : RB), 0, stream, p, items, blocks);
   SVA_CHECK_LAUNCH("verify_rows_kernel");
   return SVA_OK;
 }
 
+template <int WPI>
 int launch_rows_any(const VerifyParams& p, int64_t items, hipStream_t stream) {
   if (p.D == 64) {
-    if (p.kv_dtype == BF16) return launch_rows<64, BF16>(p, items, stream);
-    if (p.kv_dtype == F16) return launch_rows<64, F16>(p, items, stream);
-    return launch_rows<64, F32>(p, items, stream);
+    if (p.kv_dtype == BF16) return launch_rows<64, BF16, WPI>(p, items, stream);
+    if (p.kv_dtype == F16) return launch_rows<64, F16, WPI>(p, items, stream);
+    return launch_rows<64, F32, WPI>(p, items, stream);
   }
-  if (p.kv_dtype == BF16) return launch_rows<128, BF16>(p, items, stream);
-  if (p.kv_dtype == F16) return launch_rows<128, F16>(p, items, stream);
-  return launch_rows<128, F32>(p, items, stream);
+  if (p.kv_dtype == BF16) return launch_rows<128, BF16, WPI>(p, items, stream);
+  if (p.kv_dtype == F16) return launch_rows<128, F16, WPI>(p, items, stream);
+  return launch_rows<128, F32, WPI>(p, items, stream);
 }
 
 int verify_split(int64_t grp, int64_t B) {
@@ -614,11 +659,15 @@ extern "C" int sva_verify(const void* q, int q_dtype, int64_t q_seq_stride, int6
   p.o_bs = out_seq_stride;
   p.o_hs = out_head_stride;
   p.o_ts = out_tok_stride;
+  const bool rows = verify_rows_eligible(keys, values, kv_dtype, kv_head_stride, kv_row_stride, D);
   if (verify_walks_slices(n_seq, G, Q)) {
-    if (verify_rows_eligible(keys, values, kv_dtype, kv_head_stride, kv_row_stride, D))
-      return launch_rows_any(p, n_seq * H * Q, (hipStream_t)stream);
+    if (rows) return launch_rows_any<1>(p, n_seq * H * Q, (hipStream_t)stream);
     return launch_part_dim<true>(p, dim3((unsigned)sva::xcd_range_grid(n_seq * G * Q)), lds, (hipStream_t)stream);
   }
+  // few items with budgets of up to 2048 rows: one workgroup per item
+  // (RWPI waves take at most four rounds of loads each); longer budgets
+  // spread over the slice-split form's workgroups
+  if (rows && B <= 2048) return launch_rows_any<RWPI>(p, n_seq * H * Q, (hipStream_t)stream);
   int rc = launch_part_dim<false>(p, dim3((unsigned)split, (unsigned)(n_seq * G * Q)), lds, (hipStream_t)stream);
   if (rc != SVA_OK) return rc;
   hipLaunchKernelGGL(verify_combine_kernel, dim3((unsigned)(n_seq * H * Q)), dim3(CB), sizeof(float) * (size_t)split,
