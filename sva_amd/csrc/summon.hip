@@ -173,6 +173,182 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
 // compacted in shortlist order, which is ascending key order, as the budget
 // select writes it.
 constexpr int REG_MAX_L = 2048;
+
+// The k-th largest 32-bit key among the nonzero composites of the slots (the
+// key is a composite's high word): T and need such that the k largest by
+// (key desc, index asc) are the elements with key > T and the first need
+// elements with key == T in ascending index order.  kor / kand: this
+// thread's OR / AND of its elements' keys.  Radix passes of up to 12 bits
+// from the highest bit where the keys differ; a tie class costs no pass (the
+// caller's compaction takes its first need members), and a boundary bucket
+// of at most TOP_SMALL keys is ranked directly.  Every thread of the block
+// must call it.
+template <int BLOCK, int NPT>
+SVA_DEV void select_key_regs(const uint64_t (&e)[NPT], int slots, int k, uint32_t kor, uint32_t kand,
+                             const TopLds& s, uint32_t* T_out, int* need_out) {
+  static_assert(BLOCK == 4 * 256 && TOP_BINS == 4 * BLOCK, "one uint4 of bins per thread");
+  static_assert(TOP_SMALL * 16 == BLOCK, "16 lanes per key of the last bucket");
+  const int t = (int)threadIdx.x, lane = lane_id();
+#pragma unroll
+  for (int o = 1; o <= 8; o <<= 1) {
+    const uint32_t ko = o == 1 ? row_shr_keep<1>(kor) : o == 2 ? row_shr_keep<2>(kor)
+                      : o == 4 ? row_shr_keep<4>(kor) : row_shr_keep<8>(kor);
+    const uint32_t ka = o == 1 ? row_shr_keep<1>(kand) : o == 2 ? row_shr_keep<2>(kand)
+                      : o == 4 ? row_shr_keep<4>(kand) : row_shr_keep<8>(kand);
+    kor |= ko;
+    kand &= ka;
+  }
+  const auto rl = [](uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); };
+  kor = rl(kor, 15) | rl(kor, 31) | rl(kor, 47) | rl(kor, 63);
+  kand = rl(kand, 15) & rl(kand, 31) & rl(kand, 47) & rl(kand, 63);
+  if (t == 0) {
+    s.shared[0] = 0u;
+    s.shared[1] = 0xFFFFFFFFu;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    atomicOr(&s.shared[0], kor);
+    atomicAnd(&s.shared[1], kand);
+  }
+  __syncthreads();
+  const uint32_t all_or = s.shared[0], all_and = s.shared[1];
+  __syncthreads();
+  const uint32_t diff = all_or ^ all_and;
+  if (diff == 0u) {  // one key: the first k in index order
+    *T_out = all_or;
+    *need_out = k;
+    return;
+  }
+  int top = 31 - __clz((int)diff);
+  uint32_t pmask = top == 31 ? 0u : ~0u << (top + 1);
+  uint32_t prefix = all_and & pmask;
+  int rem = k;
+  while (true) {
+    const int shift = max(top - (TOP_BITS - 1), 0);
+    const uint32_t dmask = (1u << (top - shift + 1)) - 1u;
+    reinterpret_cast<uint4*>(s.hist)[t] = uint4{0u, 0u, 0u, 0u};
+    if (t == 0) s.shared[3] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const uint32_t key = (uint32_t)(e[i] >> 32);
+      if (i < slots && e[i] != 0ull && (key & pmask) == prefix) atomicAdd(&s.hist[(key >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    // thread t owns bins 4t .. 4t+3 counted from the top
+    const uint4 h = reinterpret_cast<const uint4*>(s.hist)[BLOCK - 1 - t];
+    const uint32_t c[4] = {h.w, h.z, h.y, h.x};
+    uint32_t total;
+    uint32_t a = block_excl_scan<BLOCK>(c[0] + c[1] + c[2] + c[3], s.scratch, &total);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (a < (uint32_t)rem && a + c[j] >= (uint32_t)rem) {
+        s.shared[0] = (uint32_t)(TOP_BINS - 1 - 4 * t - j);
+        s.shared[1] = a;
+        s.shared[2] = c[j];
+      }
+      a += c[j];
+    }
+    __syncthreads();
+    const uint32_t b = s.shared[0], cb = s.shared[2];
+    rem -= (int)s.shared[1];
+    prefix |= b << shift;
+    pmask |= dmask << shift;
+    if (shift == 0) {  // every key of the bucket is prefix
+      __syncthreads();
+      *T_out = prefix;
+      *need_out = rem;
+      return;
+    }
+    if (cb <= (uint32_t)TOP_SMALL) {
+      // the bucket's keys, then the rem-th largest among them (with repeats)
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        if (i < slots) {  // uniform
+          const uint32_t key = (uint32_t)(e[i] >> 32);
+          const bool match = e[i] != 0ull && (key & pmask) == prefix;
+          const uint64_t m = __builtin_amdgcn_ballot_w64(match);
+          if (m != 0ull) {
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&s.shared[3], (uint32_t)__popcll(m));
+            base = __shfl(base, 0, WAVE);
+            if (match)
+              s.small[base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))] = key;
+          }
+        }
+      }
+      __syncthreads();
+      {
+        // 16 lanes per key: lane g counts the bucket's keys 4g .. 4g+3 above
+        // it (low half) and at or above it (high half)
+        const int i = t >> 4, g = t & 15;
+        const uint32_t v = i < (int)cb ? (uint32_t)s.small[i] : 0u;
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int o = 4 * g + j;
+          if (o < (int)cb) {
+            const uint32_t y = (uint32_t)s.small[o];
+            cnt += (y > v ? 1u : 0u) + (y >= v ? 0x10000u : 0u);
+          }
+        }
+        cnt += row_shr0<1>(cnt);
+        cnt += row_shr0<2>(cnt);
+        cnt += row_shr0<4>(cnt);
+        cnt += row_shr0<8>(cnt);
+        // keys equal to the rem-th largest write the same words
+        if (g == 15 && i < (int)cb && (cnt & 0xFFFFu) < (uint32_t)rem && (cnt >> 16) >= (uint32_t)rem) {
+          s.shared[0] = v;
+          s.shared[1] = (uint32_t)rem - (cnt & 0xFFFFu);
+        }
+      }
+      __syncthreads();
+      *T_out = s.shared[0];
+      *need_out = (int)s.shared[1];
+      __syncthreads();
+      return;
+    }
+    top = shift - 1;
+  }
+}
+
+// Ordered compaction of a selection (key > T, or key == T among the first
+// need of them): per (slot, wave) counts of both kinds packed in one word and
+// one scan; pos_out(slot, lane) receives each selected element's position in
+// ascending slot-major (slot, wave, lane) order.  Every thread must call it.
+template <int BLOCK, int NPT, typename Out>
+SVA_DEV void compact_selected(const uint64_t (&e)[NPT], int slots, uint32_t T, int need, uint32_t* wbase,
+                              uint32_t* scratch, Out out) {
+  constexpr int NW = BLOCK / WAVE;
+  const int lane = lane_id(), wid = (int)threadIdx.x / WAVE;
+  uint64_t mg[NPT], me[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    const uint32_t key = (uint32_t)(e[i] >> 32);
+    const bool nz = i < slots && e[i] != 0ull;
+    mg[i] = __builtin_amdgcn_ballot_w64(nz && key > T);
+    me[i] = __builtin_amdgcn_ballot_w64(nz && key == T);
+    if (lane == 0 && i < slots) wbase[i * NW + wid] = (uint32_t)__popcll(mg[i]) | ((uint32_t)__popcll(me[i]) << 16);
+  }
+  __syncthreads();
+  const uint32_t wc = (int)threadIdx.x < slots * NW ? wbase[threadIdx.x] : 0u;
+  const uint32_t wpre = block_excl_scan<BLOCK>(wc, scratch, nullptr);
+  if ((int)threadIdx.x < slots * NW) wbase[threadIdx.x] = wpre;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    if (i < slots && (((mg[i] | me[i]) >> lane) & 1ull)) {
+      const uint32_t w = wbase[i * NW + wid];
+      const uint32_t gb = (w & 0xFFFFu) + __builtin_amdgcn_mbcnt_hi((uint32_t)(mg[i] >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mg[i], 0u));
+      const uint32_t eb = (w >> 16) + __builtin_amdgcn_mbcnt_hi((uint32_t)(me[i] >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)me[i], 0u));
+      if ((mg[i] >> lane) & 1ull) out(i, gb + min(eb, (uint32_t)need));
+      else if (eb < (uint32_t)need) out(i, gb + eb);
+    }
+  }
+}
 constexpr int REG_NW = ITEM_BLOCK / WAVE;
 constexpr int REG_OCT = 4;  // shortlist rows per lane octet in flight
 
@@ -260,7 +436,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   }
   for (int e2 = threadIdx.x; e2 < SC; e2 += ITEM_BLOCK) tab[e2] = lsrc[e2];
   __syncthreads();
-  uint64_t vor = 0ull, vand = ~0ull;
+  uint32_t kor = 0u, kand = 0xFFFFFFFFu;
   uint32_t cnt = 0;
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
@@ -281,9 +457,10 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
           acc = acc + tab[s * C + c];
         }
       }
-      e[i] = composite(f2key(acc * inv_sqrt_r), (uint32_t)n);
-      vor |= e[i];
-      vand &= e[i];
+      const uint32_t key = f2key(acc * inv_sqrt_r);
+      e[i] = composite(key, (uint32_t)n);
+      kor |= key;
+      kand &= key;
       ++cnt;
     }
   }
@@ -296,29 +473,17 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
     p.fin_count[item] = beff;
   }
   if (leff == 0) return;
-  const uint64_t X = leff == (int)allowed_total ? 1ull : select_top_regs<ITEM_BLOCK, NPT>(e, leff, vor, vand, tl);
+  // the shortlist: keys above T, then the first need keys at T in key order
+  // (every allowed key when the shortlist takes them all)
+  uint32_t T = 0u;
+  int need = 0x7FFFFFFF;
+  if (leff < (int)allowed_total) select_key_regs<ITEM_BLOCK, NPT>(e, NPT, leff, kor, kand, tl, &T, &need);
 
   // shortlist in ascending key order: slot-major (i, wave, lane) is key order
   const int lane = lane_id(), wid = (int)threadIdx.x / WAVE;
-  uint64_t m[NPT];
-#pragma unroll
-  for (int i = 0; i < NPT; ++i) {
-    m[i] = __builtin_amdgcn_ballot_w64(e[i] != 0ull && e[i] >= X);
-    if (lane == 0) wbase[i * REG_NW + wid] = (uint32_t)__popcll(m[i]);
-  }
-  __syncthreads();
-  const uint32_t wc = threadIdx.x < NPT * REG_NW ? wbase[threadIdx.x] : 0u;
-  const uint32_t wpre = block_excl_scan<ITEM_BLOCK>(wc, tl.scratch, nullptr);
-  if (threadIdx.x < NPT * REG_NW) wbase[threadIdx.x] = wpre;
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < NPT; ++i) {
-    if ((m[i] >> lane) & 1ull) {
-      const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m[i], 0u));
-      const uint32_t pos = wbase[i * REG_NW + wid] + below;
-      if (pos < (uint32_t)leff) slidx[pos] = i * ITEM_BLOCK + (int)threadIdx.x;
-    }
-  }
+  compact_selected<ITEM_BLOCK, NPT>(e, NPT, T, need, wbase, tl.scratch, [&](int i, uint32_t pos) {
+    if (pos < (uint32_t)leff) slidx[pos] = i * ITEM_BLOCK + (int)threadIdx.x;
+  });
   __syncthreads();
 
   // rescore: lane octet o takes shortlist entries o, o + 128, ...
@@ -355,45 +520,30 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   }
 
   // budget: top beff by (rank desc, key index asc), ascending key order
-  uint64_t e2[REG_MAX_L / ITEM_BLOCK];
-  uint64_t vor2 = 0ull, vand2 = ~0ull;
+  constexpr int NB = REG_MAX_L / ITEM_BLOCK;
+  uint64_t e2[NB];
+  uint32_t kor2 = 0u, kand2 = 0xFFFFFFFFu;
 #pragma unroll
-  for (int i = 0; i < REG_MAX_L / ITEM_BLOCK; ++i) {
+  for (int i = 0; i < NB; ++i) {
     const int j = (int)threadIdx.x + i * ITEM_BLOCK;
     e2[i] = 0ull;
     if (j < leff) {
-      e2[i] = composite(f2key(rank[j]), (uint32_t)slidx[j]);
-      vor2 |= e2[i];
-      vand2 &= e2[i];
+      const uint32_t key = f2key(rank[j]);
+      e2[i] = composite(key, (uint32_t)slidx[j]);
+      kor2 |= key;
+      kand2 &= key;
     }
   }
-  const uint64_t X2 = beff == leff ? 1ull
-                                   : select_top_regs<ITEM_BLOCK, REG_MAX_L / ITEM_BLOCK>(
-                                         e2, beff, vor2, vand2, tl, (leff + ITEM_BLOCK - 1) / ITEM_BLOCK);
+  const int slots2 = (leff + ITEM_BLOCK - 1) / ITEM_BLOCK;
+  uint32_t T2 = 0u;
+  int need2 = 0x7FFFFFFF;
+  if (beff < leff) select_key_regs<ITEM_BLOCK, NB>(e2, slots2, beff, kor2, kand2, tl, &T2, &need2);
   // shortlist slot j = i * BLOCK + t is in ascending key order, so an ordered
   // compaction of the chosen slots writes the budget in ascending key order
-  constexpr int NB = REG_MAX_L / ITEM_BLOCK;
-  uint64_t m2[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    m2[i] = __builtin_amdgcn_ballot_w64(e2[i] != 0ull && e2[i] >= X2);
-    if (lane == 0) wbase[i * REG_NW + wid] = (uint32_t)__popcll(m2[i]);
-  }
-  __syncthreads();
-  const uint32_t wc2 = threadIdx.x < NB * REG_NW ? wbase[threadIdx.x] : 0u;
-  const uint32_t wpre2 = block_excl_scan<ITEM_BLOCK>(wc2, tl.scratch, nullptr);
-  if (threadIdx.x < NB * REG_NW) wbase[threadIdx.x] = wpre2;
-  __syncthreads();
   int32_t* out_fin = p.fin_idx + (int64_t)item * p.B;
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    if ((m2[i] >> lane) & 1ull) {
-      const uint32_t below =
-          __builtin_amdgcn_mbcnt_hi((uint32_t)(m2[i] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m2[i], 0u));
-      const uint32_t pos = wbase[i * REG_NW + wid] + below;
-      if (pos < (uint32_t)beff) out_fin[pos] = composite_index(e2[i]);
-    }
-  }
+  compact_selected<ITEM_BLOCK, NB>(e2, slots2, T2, need2, wbase, tl.scratch, [&](int i, uint32_t pos) {
+    if (pos < (uint32_t)beff) out_fin[pos] = composite_index(e2[i]);
+  });
 }
 
 template <int NPT, int SB>
