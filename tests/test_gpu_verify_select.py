@@ -72,6 +72,36 @@ def test_verify_matches_oracle(device, D, H, G, dtype):
         assert err <= tol, f"head {h}: rel err {err}"
 
 
+@pytest.mark.parametrize("budget,dtype", [(2048, torch.bfloat16), (2049, torch.bfloat16), (3000, torch.float32),
+                                          (1, torch.float32), (33, torch.float16)])
+def test_verify_budget_sizes(device, budget, dtype):
+    # one workgroup per item up to 2048 rows (a 2048-row list is 16 rounds per wave), the slice-split form
+    # beyond; a one-row list and a list shorter than a round
+    from sva_amd import kernels
+
+    rng = np.random.default_rng(budget)
+    H, G, D, n = 9, 3, 64, 6000
+    counts = rng.integers(0, budget + 1, H)
+    counts[0], counts[1] = budget, min(budget, 7)
+    fin = _lists(rng, H, G, n, budget, counts, overlap=0.3)
+    q = rng.standard_normal((1, H, 1, D)).astype(np.float32)
+    keys = rng.standard_normal((G, n, D)).astype(np.float32)
+    values = rng.standard_normal((G, n, D)).astype(np.float32)
+    kt, vt, qt = (torch.from_numpy(a).to(device, dtype) for a in (keys, values, q))
+    out = kernels.verify(qt, kt, vt, torch.from_numpy(fin).to(device), torch.from_numpy(counts.astype(np.int32)).to(device),
+                         n, D ** -0.5).float().cpu().numpy()
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    kq, vq, qq = kt.float().cpu().numpy(), vt.float().cpu().numpy(), qt.float().cpu().numpy()
+    for h in range(H):
+        c = int(counts[h])
+        if c == 0:
+            assert np.all(out[0, h, 0] == 0)
+            continue
+        ref = oracle.verify(qq[0, h, 0], kq[h // 3], vq[h // 3], fin[h, :c], D ** -0.5)
+        err = np.abs(out[0, h, 0] - ref).max() / np.abs(ref).max()
+        assert err <= tol, f"budget {budget} head {h} ({c} rows): rel err {err}"
+
+
 @pytest.mark.parametrize("Q", [2, 400])  # 400: 3200 (sequence, KV head, token) groups, one wave per item
 def test_verify_ragged_sequences(device, Q):
     from sva_amd import kernels
