@@ -136,7 +136,7 @@ __global__ void __launch_bounds__(PB)
 
 constexpr int CT = 256;          // threads per candidate workgroup
 constexpr int TAIL_ROWS = 256;   // tail rows per workgroup
-constexpr int SCORE_U = 4;       // entries in flight per 16-lane group while scoring
+constexpr int SCORE_U = 4;       // entries in flight per 16-lane group while scoring (2 per octet)
 constexpr int kMaxCells = 64;
 constexpr int kMaxSub = 16;
 
@@ -505,18 +505,18 @@ __global__ void __launch_bounds__(CT) ragged_cand_score_kernel(CandParams p, int
     if (threadIdx.x == 0) pre[items] = (int)carry;
   }
   __syncthreads();
-  constexpr int GROUPS = CT / 16;
-  constexpr int U = SCORE_U;
+  constexpr int GROUPS = CT / 8;  // lane octets, one entry each per round
+  constexpr int U = SCORE_U / 2;  // entries in flight per octet
   const int total = pre[items];
   const int per = ((total + (int)gridDim.x - 1) / (int)gridDim.x + GROUPS * U - 1) / (GROUPS * U) * (GROUPS * U);
   const int e_begin = (int)blockIdx.x * per, e_end = min(total, e_begin + per);
-  const int g = threadIdx.x >> 4;
-  const int j = lane_id() & 15;
+  const int g = threadIdx.x >> 3;
+  const int j = lane_id() & 7;
   const int tail_slot0 = p.S * p.postings_len;
   for (int b0 = e_begin; b0 < e_end; b0 += GROUPS * U) {
     int it[U], slot[U], n[U];
     int64_t r0[U];
-    float4 rv[U], qq[U];
+    float4 ra[U], rb[U], qa[U], qb[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int e = b0 + g + u * GROUPS;
@@ -554,13 +554,17 @@ __global__ void __launch_bounds__(CT) ragged_cand_score_kernel(CandParams p, int
     for (int u = 0; u < U; ++u) {
       const bool live = n[u] >= 0;
       const int hh = live ? it[u] % p.H : 0;
-      rv[u] = live ? reinterpret_cast<const float4*>(p.k_low + (int64_t)hh * p.klow_hs + (r0[u] + n[u]) * 64)[j]
-                   : float4{0.0f, 0.0f, 0.0f, 0.0f};
-      qq[u] = live ? reinterpret_cast<const float4*>(p.q_low + (int64_t)it[u] * 64)[j] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float4 zero = float4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float4* row = reinterpret_cast<const float4*>(p.k_low + (int64_t)hh * p.klow_hs + (r0[u] + n[u]) * 64);
+      const float4* qrow = reinterpret_cast<const float4*>(p.q_low + (int64_t)it[u] * 64);
+      ra[u] = live ? row[j] : zero;
+      rb[u] = live ? row[8 + j] : zero;
+      qa[u] = live ? qrow[j] : zero;
+      qb[u] = live ? qrow[8 + j] : zero;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float dot = rank_dot64_row16(rv[u], qq[u]);  // valid in the row's first lane
+      const float dot = rank_dot64_oct8(ra[u], rb[u], qa[u], qb[u]);  // valid in the octet's first lane
       if (it[u] >= 0 && j == 0) {
         uint64_t* comp = p.comp + (int64_t)it[u] * p.W;
         uint8_t* flag = p.flag + (int64_t)it[u] * p.W;
