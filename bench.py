@@ -182,6 +182,29 @@ class Layer:
                                    dtype=torch.int32).to(torch.uint8)
 
 
+def read_floor_measure(torch, kernels, layers, reps=200):
+    """The layers' codes, the scan's bytes, read on their own by a plain
+    streaming kernel (sva_stream_read: the scan's access pattern, nothing
+    else), rotating over the layers as the steps do: the time a read of those
+    bytes takes on this device, which the scan is priced against."""
+    bufs = [layer.codes for layer in layers]
+    sink = kernels.stream_read(bufs[0])
+    for i in range(16):
+        kernels.stream_read(bufs[i % len(bufs)], sink)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        kernels.stream_read(bufs[i % len(bufs)], sink)
+    e1.record()
+    torch.cuda.synchronize()
+    us = 1e3 * e0.elapsed_time(e1) / reps
+    nbytes = bufs[0].numel() * bufs[0].element_size()
+    gbs = nbytes / us / 1e3
+    return {"kernel": "stream_read_kernel: the codes alone, read in the scan's pattern", "bytes": nbytes,
+            "us": round(us, 2), "achieved": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": reps}
+
+
 def algorithmic_bytes(n_keys, heads, subspaces, codewords, shortlist, budget, rank=64, head_dim=64, kv_elem=2):
     scan = heads * n_keys * subspaces
     lut = heads * subspaces * codewords * 4
@@ -1042,6 +1065,7 @@ def main():
     step_us = [1e3 * ev[0].elapsed_time(ev[-1]) for ev in events]
     eager_p50 = float(np.percentile(step_us, 50))
     graph_res = None if args.no_graph else graph_replay(torch, np, args, layers, plan, outs, step)
+    read_floor = read_floor_measure(torch, kernels, layers)
 
     bytes_ = algorithmic_bytes(n, heads, subspaces, codewords, shortlist, budget)
     step_us_avg = per_stage_us["lookup_verify"]
@@ -1098,6 +1122,7 @@ def main():
             "traffic": traffic,
             "algorithmic_bytes": bytes_["total"],
             "algorithmic_split": {k: bytes_[k] for k in ("scan", "lut", "query", "rescore", "verify")},
+            "read_floor": read_floor,
         },
         "cpu_baseline": None,
     }

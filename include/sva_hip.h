@@ -482,6 +482,18 @@ int sva_top_unique(const int64_t *idx, const float *scores, const uint8_t *valid
                    int64_t refill_factor, int32_t *sel_idx, float *sel_scores, uint8_t *sel_valid, void *workspace,
                    size_t workspace_bytes, void *stream);
 
+/*
+ * A plain streaming read of `bytes` (a positive multiple of 16, the buffer
+ * 16-byte aligned): each wave reads 8 KB of consecutive 16-byte words, the
+ * code scan's access pattern, and the words are folded by XOR into `sink`
+ * (the XOR of all sink words is the XOR of all 32-bit words of the buffer).
+ * No counterpart in the reference: a measurement helper, the time a read of
+ * the scan's bytes takes on its own, which the scan is priced against.
+ *   sink: sva_stream_read_sink_words(bytes) uint32 words
+ */
+int64_t sva_stream_read_sink_words(int64_t bytes);
+int sva_stream_read(const void *src, int64_t bytes, uint32_t *sink, int64_t sink_words, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

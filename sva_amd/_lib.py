@@ -68,6 +68,8 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
     "sva_top_unique": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _SZ, _P]),
     "sva_verify": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64, _I64,
                         _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P, _SZ, _P]),
+    "sva_stream_read_sink_words": (_I64, [_I64]),
+    "sva_stream_read": (_I, [_P, _I64, _P, _I64, _P]),
     "sva_verify_noalloc": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _I, _I64, _I64, _P, _P, _I64, _P, _P, _I64, _I64,
                                 _I64, _I64, _I64, _I64, _F, _P, _I, _I64, _I64, _I64, _P]),
     "sva_decode_layer_create": (_I, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _F,

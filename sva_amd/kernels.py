@@ -690,3 +690,21 @@ def residual_adapter(hidden_states: torch.Tensor, attn_output: torch.Tensor, dow
                                      ptr(down_w), ptr(up_w), float(scale), h.shape[0], hidden, rank, ptr(out),
                                      dtype_code(out), out.stride(0), stream_handle(device)), "sva_residual_adapter")
     return out.reshape(attn_output.shape)
+
+
+def stream_read(buf: torch.Tensor, sink: torch.Tensor | None = None) -> torch.Tensor:
+    """A plain streaming read of `buf` (contiguous, 16-byte aligned, a
+    multiple of 16 bytes) by sva_stream_read: the time a read of the same
+    bytes takes on its own.  Returns the uint32 sink whose XOR is the XOR of
+    every 32-bit word of `buf` (pass `sink` to reuse one)."""
+    if not buf.is_contiguous():
+        raise ValueError("stream_read: the buffer must be contiguous")
+    device = require_device(buf)
+    nbytes = buf.numel() * buf.element_size()
+    words = int(lib().sva_stream_read_sink_words(nbytes))
+    if sink is None:
+        sink = torch.empty(max(words, 1), device=device, dtype=torch.int32)
+    elif sink.dtype != torch.int32 or sink.numel() < words or sink.device != device:
+        raise ValueError(f"stream_read: the sink must hold {words} int32 words on {device}")
+    check(lib().sva_stream_read(ptr(buf), nbytes, ptr(sink), sink.numel(), stream_handle(device)), "sva_stream_read")
+    return sink
