@@ -185,7 +185,8 @@ struct ScanTables {
 // the round's table lookups are in flight together: acc[k] = ((T0 + T1) +
 // T2) + ... (the scan sum before the 1/8 scale; the reference's leading
 // 0 + T0 only changes the sign of a zero).  On the SMALLC path a code byte
-// becomes a table byte offset with a shift and a mask (codes below 64).
+// becomes a table byte offset with a shift and a mask (codes below 64; a
+// larger byte reads the entry of its low six bits, inside the table).
 template <int S, bool SMALLC>
 SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, SMALLC>& T, float (&acc)[16 / S]) {
 #pragma clang fp contract(off)
@@ -193,7 +194,15 @@ SVA_DEV void score_round(const u32x4& raw, const ScanTables<S, SMALLC>& T, float
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
     float a = 0.0f;
-    if (SMALLC) {
+    if (SMALLC && S == 4) {
+      // codes below 64: y holds 4 c in each byte, and the pair offset
+      // 4 c0 + 256 c1 is y's byte 0 beside x's byte 1 (one byte permute)
+      const uint32_t x = raw[k] & 0x3F3F3F3Fu;
+      const uint32_t y = x << 2;
+      a = T.at_byte(__builtin_amdgcn_perm(y, x, 0x0C0C0104u));
+      a = a + T.at_byte(__builtin_amdgcn_ubfe(y, 16, 8) + (uint32_t)(4 * (ScanTables<S, SMALLC>::PAIR + 2 * 64)));
+      a = a + T.at_byte((y >> 24) + (uint32_t)(4 * (ScanTables<S, SMALLC>::PAIR + 3 * 64)));
+    } else if (SMALLC) {
       const int j0 = k * S;
       if (S >= 2) {
         const uint32_t x = raw[j0 >> 2] >> (8 * (j0 & 3));
@@ -284,36 +293,65 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 // The scan of one thread's slots.  CHECK: the chunk is partial or masked, so
 // every key is tested for being allowed; otherwise every key is, and a round
 // (one 16-byte word of codes) is examined key by key only when its largest
-// sum reaches the floor.
+// sum reaches the floor.  Full chunks of up to four subspaces score every
+// round before any append, so the rounds' table reads are in flight
+// together rather than each behind the previous round's branch (eight
+// subspaces keep the per-round order: holding every round's sums would cost
+// them a wave per SIMD).
 template <int S, bool SMALLC, bool CHECK, bool MASKED>
 SVA_DEV void scan_rounds(const SummonParams& p, const u32x4 (&raw)[KEYS_PT * S / 16], const ScanTables<S, SMALLC>& T,
                          float t_lo, int cs, int ce, uint64_t* out, uint64_t* kc, uint32_t& wc,
                          uint32_t& n_allowed) {
   constexpr int KPT = 16 / S;
+  constexpr int RND = KEYS_PT / KPT;
+  constexpr bool ALL_FIRST = !CHECK && S <= 4;
+  if (ALL_FIRST) {
+    float acc[RND][KPT];
 #pragma unroll
-  for (int r = 0; r < KEYS_PT / KPT; ++r) {
-    float acc[KPT];
-    score_round<S, SMALLC>(raw[r], T, acc);
-    if (CHECK) {
-      bool c[KPT];
-      bool any = false;
+    for (int r = 0; r < RND; ++r) score_round<S, SMALLC>(raw[r], T, acc[r]);
+    uint64_t hit[RND];
 #pragma unroll
-      for (int k = 0; k < KPT; ++k) {
-        const bool ok = key_ok<false, MASKED>(p, slot_key<S>(cs, r * KPT + k), ce);
-        n_allowed += ok;
-        c[k] = ok && acc[k] >= t_lo;
-        any = any || c[k];
-      }
-      if (__builtin_amdgcn_ballot_w64(any) != 0ull) append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
-    } else {
-      float mx = acc[0];
+    for (int r = 0; r < RND; ++r) {
+      float mx = acc[r][0];
 #pragma unroll
-      for (int k = 1; k < KPT; ++k) mx = fmaxf(mx, acc[k]);
-      if (__builtin_amdgcn_ballot_w64(mx >= t_lo) != 0ull) {  // rare: the shortlist and the keys near it
+      for (int k = 1; k < KPT; ++k) mx = fmaxf(mx, acc[r][k]);
+      hit[r] = __builtin_amdgcn_ballot_w64(mx >= t_lo);
+    }
+#pragma unroll
+    for (int r = 0; r < RND; ++r) {
+      if (hit[r] != 0ull) {  // rare: the shortlist and the keys near it
         bool c[KPT];
 #pragma unroll
-        for (int k = 0; k < KPT; ++k) c[k] = acc[k] >= t_lo;
-        append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
+        for (int k = 0; k < KPT; ++k) c[k] = acc[r][k] >= t_lo;
+        append_round<KPT>(p, c, acc[r], round_key<S>(cs, r), out, kc, wc);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RND; ++r) {
+      float acc[KPT];
+      score_round<S, SMALLC>(raw[r], T, acc);
+      if (CHECK) {
+        bool c[KPT];
+        bool any = false;
+#pragma unroll
+        for (int k = 0; k < KPT; ++k) {
+          const bool ok = key_ok<false, MASKED>(p, slot_key<S>(cs, r * KPT + k), ce);
+          n_allowed += ok;
+          c[k] = ok && acc[k] >= t_lo;
+          any = any || c[k];
+        }
+        if (__builtin_amdgcn_ballot_w64(any) != 0ull) append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
+      } else {
+        float mx = acc[0];
+#pragma unroll
+        for (int k = 1; k < KPT; ++k) mx = fmaxf(mx, acc[k]);
+        if (__builtin_amdgcn_ballot_w64(mx >= t_lo) != 0ull) {  // rare: the shortlist and the keys near it
+          bool c[KPT];
+#pragma unroll
+          for (int k = 0; k < KPT; ++k) c[k] = acc[k] >= t_lo;
+          append_round<KPT>(p, c, acc, round_key<S>(cs, r), out, kc, wc);
+        }
       }
     }
   }
