@@ -221,8 +221,8 @@ __global__ void __launch_bounds__(PREP_BLOCK) query_lut_kernel(LutParams p) {
 
 // Decode form: the body lives in query_decode.cuh (the code-class path runs
 // it in one grid with its code counts).  Two and four subspaces run 1024
-// threads per head: their table, pair and histogram phases are LDS-latency
-// bound, and 16 waves hide what 4 cannot.
+// threads per head: their table, sampled-sum and histogram phases are
+// LDS-latency bound, and 16 waves hide what 4 cannot.
 constexpr int QD_WIDE = 1024;
 
 template <int S, int CMAX, int NT>

@@ -14,9 +14,9 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // head with the layout's sizes at compile time.  The same arithmetic as query_lut_kernel (q_low and
 // table entries by sequential fma chains, bounds folded per subspace, the
 // floor from the same sample blocks and histogram), with the sampled code
-// words loaded 16 bytes at a time into registers and, for four subspaces,
-// pair tables so that a sampled sum takes two reads (the floor is only a
-// hint, so the pair sums' rounding does not matter there).
+// words loaded 16 bytes at a time into registers.  The sampled sums read the
+// single tables (pair tables for four subspaces took longer to build than
+// they saved), and one wave finds the floor's bin: only thread 0 writes it.
 constexpr int QD = 256;
 constexpr int QD_WORDS = 8;  // sampled 16-byte code words per thread (at most 32 KB per head)
 // Sampled code words a thread holds for S subspaces: at most SAMPLE_MAX_BLOCKS
@@ -29,13 +29,12 @@ constexpr int qd_words() {
 }
 
 // NT threads per workgroup (256, or 1024 so that more waves hide the
-// latency of the table, pair and histogram phases).
+// latency of the table, sampled-sum and histogram phases).
 template <int S, int CMAX, int NT = QD>
 SVA_DEV void query_decode_item(const LutParams& p, int h) {
 #pragma clang fp contract(off)
   static_assert(NT % 256 == 0 && NT <= 1024, "256 or more threads, whole 64-entry table rows per wave");
   constexpr int SUB = 64 / S;
-  constexpr int NPAIR = S >= 4 ? S / 2 : 0;
   // With at least two threads per table entry, two consecutive lanes share a
   // codebook row, PART floats each, instead of every lane loading a whole
   // row (the surplus lanes the last row again); the row's fma chain runs
@@ -52,10 +51,8 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   __shared__ __align__(16) float W[64 * 64];
   __shared__ float qf[64], ql[64];
   __shared__ float tab[S * CMAX];
-  __shared__ float pairs[NPAIR > 0 ? NPAIR * 4096 : 1];
   __shared__ uint32_t kmin[S], kmax[S];
   __shared__ __align__(16) uint32_t hist[SAMPLE_BINS];
-  __shared__ uint32_t wsum[NT / WAVE], res[2];
   const int t = threadIdx.x;
   const int lane = lane_id(), wid = t / WAVE;
   const int C = p.C;
@@ -106,7 +103,6 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
     kmax[t] = 0u;
   }
   if (t < SAMPLE_BINS / 4) reinterpret_cast<uint4*>(hist)[t] = uint4{0u, 0u, 0u, 0u};
-  if (t == 0) res[0] = 0u;  // floor bin 0 unless the samples place it
   __syncthreads();
   // 2. q_low: one lane per output, a sequential fma chain over d
   if (t < 64) {
@@ -166,21 +162,6 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
   float t_lo = -INFINITY;
   if (k_rank > 0 && hi > lo) {
     const uint32_t cm = (uint32_t)(C - 1);
-    if (NPAIR > 0) {
-      // pair m: entry c0 + 64 c1 = T_{2m}[c0] + T_{2m+1}[c1]; thread t writes
-      // entries t + NT r, whose c0 = t & 63 is its own and c1 = t / 64 + (NT / 64) r
-#pragma unroll
-      for (int m = 0; m < NPAIR; ++m) {
-        const float a0 = tab[2 * m * C + min((uint32_t)(t & 63), cm)];
-        float b[4096 / NT];
-#pragma unroll
-        for (int r = 0; r < 4096 / NT; ++r)
-          b[r] = tab[(2 * m + 1) * C + min((uint32_t)((t >> 6) + (NT / 64) * r), cm)];
-#pragma unroll
-        for (int r = 0; r < 4096 / NT; ++r) pairs[m * 4096 + t + NT * r] = a0 + b[r];
-      }
-      __syncthreads();
-    }
     // 4. sampled sums, kept in registers
     float sums[QW * KPW];
 #pragma unroll
@@ -189,22 +170,11 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
 #pragma unroll
       for (int q = 0; q < KPW; ++q) {
         float acc = 0.0f;
-        if (NPAIR > 0) {
 #pragma unroll
-          for (int m = 0; m < NPAIR; ++m) {
-            const int j = q * S + 2 * m;  // byte of subspace 2m
-            const uint32_t x = words[i][j >> 2] >> (8 * (j & 3));
-            const uint32_t c0 = min(x & 0xFFu, cm), c1 = min((x >> 8) & 0xFFu, cm);
-            const float v = pairs[m * 4096 + (c0 | (c1 << 6))];
-            acc = m == 0 ? v : acc + v;
-          }
-        } else {
-#pragma unroll
-          for (int s2 = 0; s2 < S; ++s2) {
-            const int j = q * S + s2;
-            const uint32_t c = min((words[i][j >> 2] >> (8 * (j & 3))) & 0xFFu, cm);
-            acc = acc + tab[s2 * C + c];
-          }
+        for (int s2 = 0; s2 < S; ++s2) {
+          const int j = q * S + s2;
+          const uint32_t c = min((words[i][j >> 2] >> (8 * (j & 3))) & 0xFFu, cm);
+          acc = acc + tab[s2 * C + c];
         }
         sums[i * KPW + q] = valid ? acc : -INFINITY;
       }
@@ -222,23 +192,36 @@ SVA_DEV void query_decode_item(const LutParams& p, int h) {
       }
     }
     __syncthreads();
-    // 5. the bin of the k-th largest sampled sum: thread t < 256 owns bins 1023 - 4 t - j
-    const uint4 hv = t < SAMPLE_BINS / 4 ? reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - t]
-                                         : uint4{0u, 0u, 0u, 0u};
-    const uint32_t c[4] = {hv.w, hv.z, hv.y, hv.x};
-    const uint32_t mine = c[0] + c[1] + c[2] + c[3];
-    const uint32_t incl = wave_incl_scan(mine);
-    if (lane == WAVE - 1) wsum[wid] = incl;
-    __syncthreads();
-    uint32_t a = incl - mine;
-    for (int v = 0; v < wid; ++v) a += wsum[v];
+    // 5. the bin of the k-th largest sampled sum, found by wave 0 alone:
+    // lane l owns bins SAMPLE_BINS - 1 - BPL l - j (j = 0 .. BPL - 1, in
+    // descending order); the lane whose bins cross k holds it (bin 0 when
+    // fewer than k sums were sampled)
+    if (wid == 0) {
+      constexpr int BPL = SAMPLE_BINS / WAVE;
+      static_assert(BPL % 4 == 0, "whole uint4s of bins per lane");
+      uint32_t c[BPL];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (a < (uint32_t)k_rank && a + c[j] >= (uint32_t)k_rank) res[0] = (uint32_t)(SAMPLE_BINS - 1 - 4 * t - j);
-      a += c[j];
+      for (int u = 0; u < BPL / 4; ++u) {
+        const uint4 hv = reinterpret_cast<const uint4*>(hist)[SAMPLE_BINS / 4 - 1 - (lane * (BPL / 4) + u)];
+        c[4 * u + 0] = hv.w;
+        c[4 * u + 1] = hv.z;
+        c[4 * u + 2] = hv.y;
+        c[4 * u + 3] = hv.x;
+      }
+      uint32_t mine = 0;
+#pragma unroll
+      for (int j = 0; j < BPL; ++j) mine += c[j];
+      uint32_t a = wave_incl_scan(mine) - mine;
+      int found = -1;
+#pragma unroll
+      for (int j = 0; j < BPL; ++j) {
+        if (a < (uint32_t)k_rank && a + c[j] >= (uint32_t)k_rank) found = SAMPLE_BINS - 1 - BPL * lane - j;
+        a += c[j];
+      }
+      const uint64_t m = __builtin_amdgcn_ballot_w64(found >= 0);
+      const int bin = m != 0ull ? __builtin_amdgcn_readlane(found, __builtin_ctzll(m)) : 0;
+      t_lo = base + (float)bin / inv_w;
     }
-    __syncthreads();
-    t_lo = base + (float)res[0] / inv_w;
   }
   if (t == 0) {
     float* rg = p.range + (int64_t)h * 4;

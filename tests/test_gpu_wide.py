@@ -368,9 +368,9 @@ def _check_decode_step(plan, codes, k_low, qb, keys, values, out, L, B, scaling=
     (300001, 2, 256, 1024, 256),   # a partial last word with eight keys per word
 ])
 def test_decode_step_at_a_million_keys_matches_oracle(device, N, S, C, L, B):
-    """The one-call decode step (sva_lookup_verify: the query inside the persistent scan, then the finish with
-    the verifier) on caches of up to a million keys, seeded, against the oracle's shortlist, budget and fp64
-    verifier for every head."""
+    """The one-call decode step (sva_lookup_verify: the query, the scan, then the finish with the verifier) on
+    caches of up to a million keys, seeded, against the oracle's shortlist, budget and fp64 verifier for every
+    head."""
     from sva_amd import kernels
 
     H = 9
