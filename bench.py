@@ -315,8 +315,11 @@ REF_US_BY_CONFIG = {("4x64", 2048, 512): REF_US_PER_QUERY, ("1x256", 2048, 512):
 REF_MODEL_TOK_S = 8.05     # the reference's SmolLM2-135M 30-layer SVA decode at 8192 context (H100)
 
 
+READ_KERNEL = "stream_read_kernel"  # the plain read of the codes the scan is priced against
+
+
 def _kernel_key(name):
-    for k in PATH_KERNELS + ("__amd_rocclr_copyBuffer",):
+    for k in PATH_KERNELS + ("__amd_rocclr_copyBuffer", READ_KERNEL):
         if k in name:
             return k
     return None
@@ -384,7 +387,7 @@ def write_profiles(args):
     with open(stats_csv) as f:
         for r in csv.DictReader(f):
             k = _kernel_key(r["Name"])
-            if k in PATH_KERNELS:
+            if k in PATH_KERNELS or k == READ_KERNEL:
                 rows[k] = (int(r["Calls"]), float(r["AverageNs"]), float(r["MinNs"]), float(r["MaxNs"]))
     counters = {}
     for path in (fetch_csv, write_csv):
@@ -416,6 +419,12 @@ def write_profiles(args):
             total += a
             lines.append(f"| {k} | {c} | {a / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |")
     lines += [f"| **sum per decode step** | | {total / 1e3:.2f} | | |", ""]
+    if READ_KERNEL in rows:
+        c, a, mn, mx = rows[READ_KERNEL]
+        lines += ["Not part of the step: the same codes read on their own by a plain streaming kernel in the "
+                  "scan's access pattern (`roofline.read_floor`).", "",
+                  "| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|",
+                  f"| {READ_KERNEL} | {c} | {a / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} |", ""]
     (out_dir / f"{stem}_kernel_trace.md").write_text("\n".join(lines))
     summon_bytes = 0.0
     lines = [f"# HBM traffic per dispatch: decode step (sva_lookup_verify) at 1M keys, {args.layout} codes, L/B "
@@ -436,6 +445,11 @@ def write_profiles(args):
     entry = "sva_lookup_verify"
     lines += ["", f"{entry} (query table, scan, finish with the verifier): {summon_bytes:,.0f} bytes per decode "
                   f"step.", ""]
+    fr, wr = avg.get((READ_KERNEL, "FETCH_SIZE")), avg.get((READ_KERNEL, "WRITE_SIZE"))
+    if fr is not None and wr is not None:
+        lines += [f"Not part of the step: {READ_KERNEL}, the plain read of the same codes, FETCH_SIZE {fr:.1f} KiB, "
+                  f"WRITE_SIZE {wr:.1f} KiB, {1024.0 * (fr * fetch_scale + wr * write_scale):,.0f} bytes "
+                  f"(scaled).", ""]
     (out_dir / f"{stem}_pmc.md").write_text("\n".join(lines))
     (out_dir / f"{stem}_traffic.json").write_text(json.dumps(
         {"entry_point": entry, "kernels": list(SUMMON_KERNELS), "hbm_bytes_per_launch": round(summon_bytes),
