@@ -7,6 +7,7 @@
 #include <new>
 
 #include "capi_internal.h"
+#include "summon.h"
 
 struct sva_decode_layer {
   int64_t H, G, D, R, S, C, L, B;
@@ -132,15 +133,17 @@ extern "C" int sva_decode_layer_step(sva_decode_layer* h, const void* q, int q_d
   const int64_t H = h->H;
   const int strategy = sva_summon_strategy(1, H, 1, n_keys, h->R, h->S, h->C, h->L, h->code_type, 0);
   const bool with_floor = strategy == 1 || strategy == 2;
-  rc = sva_lookup_verify(q, q_dtype, q_head_stride, H, h->D, h->R, h->S, h->C, h->q_proj, h->scale, h->codebooks,
-                         h->codes, h->code_type, h->code_hs, h->k_low, h->klow_hs, n_keys, h->L, nullptr, 0, 0,
-                         h->q_low, h->lut, h->range, h->sl_idx, h->sl_rank, h->counts, h->B, h->fin_idx,
-                         h->counts + H, h->ws, h->ws_bytes, keys, values, kv_dtype, kv_head_stride, kv_row_stride,
-                         h->G, h->scaling, out, out_dtype, out_head_stride, h->vws, h->vws_bytes,
-                         with_floor ? h->counts + 2 * H : nullptr, stream);
+  // the per-item register path adds the statistics itself (one launch fewer)
+  unsigned long long* fused_stats = strategy == 3 ? (unsigned long long*)h->stats : nullptr;
+  rc = sva::lookup_verify_impl(q, q_dtype, q_head_stride, H, h->D, h->R, h->S, h->C, h->q_proj, h->scale,
+                               h->codebooks, h->codes, h->code_type, h->code_hs, h->k_low, h->klow_hs, n_keys, h->L,
+                               nullptr, 0, 0, h->q_low, h->lut, h->range, h->sl_idx, h->sl_rank, h->counts, h->B,
+                               h->fin_idx, h->counts + H, h->ws, h->ws_bytes, keys, values, kv_dtype, kv_head_stride,
+                               kv_row_stride, h->G, h->scaling, out, out_dtype, out_head_stride, h->vws, h->vws_bytes,
+                               with_floor ? h->counts + 2 * H : nullptr, stream, fused_stats);
   if (rc != SVA_OK) return rc;
   // the step's statistics (sva/llama.py:319-326), summed on the device
-  if (h->stats != nullptr) {
+  if (h->stats != nullptr && fused_stats == nullptr) {
     hipLaunchKernelGGL(decode_stats_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, h->counts, (int)H, with_floor,
                        h->stats);
     SVA_CHECK_LAUNCH("decode_stats_kernel");

@@ -75,6 +75,9 @@ struct SummonParams {
   int B;
   int32_t* fin_idx;
   int32_t* fin_count;
+  // optional int64 [4] statistics row the per-item path adds each item's
+  // counts to (summoned, verified, -, queries); nullptr: none
+  unsigned long long* stats;
 };
 
 // The exact verifier run by the wide path's finish kernel right after each
@@ -100,6 +103,21 @@ struct FusedVerify {
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
+// sva_lookup_verify, adding each query head's counts to `stats` (an int64 [4]
+// row: summoned, verified, -, queries) when it is not null: only where the
+// per-item register path serves the shape (sva_summon_strategy 3).  The caller
+// clears the error state.
+int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
+                       int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
+                       const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
+                       int64_t k_low_head_stride, int64_t n_keys, int64_t L, const void* mask, int mask_type,
+                       int64_t mask_tok_stride, float* q_low, float* lut, float* score_range,
+                       int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx,
+                       int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
+                       const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                       int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
+                       void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
+                       void* stream, unsigned long long* stats);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);

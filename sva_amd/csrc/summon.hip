@@ -471,6 +471,11 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   if (threadIdx.x == 0) {
     p.sl_count[item] = leff;
     p.fin_count[item] = beff;
+    if (p.stats != nullptr) {  // a decode step's statistics, without a launch of their own
+      atomicAdd(&p.stats[0], (unsigned long long)leff);
+      atomicAdd(&p.stats[1], (unsigned long long)beff);
+      atomicAdd(&p.stats[3], 1ull);
+    }
   }
   if (leff == 0) return;
   // the shortlist: keys above T, then the first need keys at T in key order
@@ -480,7 +485,6 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
   if (leff < (int)allowed_total) select_key_regs<ITEM_BLOCK, NPT>(e, NPT, leff, kor, kand, tl, &T, &need);
 
   // shortlist in ascending key order: slot-major (i, wave, lane) is key order
-  const int lane = lane_id(), wid = (int)threadIdx.x / WAVE;
   compact_selected<ITEM_BLOCK, NPT>(e, NPT, T, need, wbase, tl.scratch, [&](int i, uint32_t pos) {
     if (pos < (uint32_t)leff) slidx[pos] = i * ITEM_BLOCK + (int)threadIdx.x;
   });
@@ -633,7 +637,7 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
                 int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
                 const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr,
-                const sva::QueryLaunch* query = nullptr) {
+                const sva::QueryLaunch* query = nullptr, unsigned long long* stats = nullptr) {
   if (fused != nullptr) *fused = false;
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((sl_idx == nullptr) == (sl_rank == nullptr), "%s: shortlist indices and ranks go together", fn);
@@ -679,10 +683,14 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   p.B = (int)B;
   p.fin_idx = fin_idx;
   p.fin_count = fin_count;
+  p.stats = stats;
   // a prepared query launch (the tables this call reads): the code-class
   // path runs its decode form in one grid with the code counts; every other
   // path launches it first
   const bool class_path = n_keys > 0 && sva::summon_class_eligible(p, items);
+  SVA_REQUIRE(stats == nullptr || (n_keys > 0 && !class_path && !sva::summon_wide_eligible(p, items) &&
+                                   sva::summon_regs_eligible(p)),
+              "%s: a statistics row is added on the per-item register path only", fn);
   // without shortlist outputs only the fused per-item path (strategy 3) runs
   SVA_UNSUPPORTED(sl_idx != nullptr || n_keys == 0 ||
                       (B > 0 && !class_path && !sva::summon_wide_eligible(p, items) && sva::summon_regs_eligible(p)),
@@ -776,18 +784,21 @@ extern "C" int sva_lookup_select(const void* q, int q_dtype, int64_t q_head_stri
                      stream, nullptr, nullptr, nullptr, &ql);
 }
 
-extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
-                                 int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
-                                 const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
-                                 int64_t k_low_head_stride, int64_t n_keys, int64_t L, const void* mask, int mask_type,
-                                 int64_t mask_tok_stride, float* q_low, float* lut, float* score_range,
-                                 int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx,
-                                 int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
-                                 const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
-                                 int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
-                                 void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
-                                 void* stream) {
-  sva::clear_error();
+namespace sva {
+
+// sva_lookup_verify with an optional statistics row (see SummonParams::stats;
+// the per-item register path only).  The caller clears the error state.
+int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
+                       int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
+                       const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
+                       int64_t k_low_head_stride, int64_t n_keys, int64_t L, const void* mask, int mask_type,
+                       int64_t mask_tok_stride, float* q_low, float* lut, float* score_range,
+                       int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx,
+                       int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
+                       const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                       int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
+                       void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
+                       void* stream, unsigned long long* stats) {
   SVA_REQUIRE(q && q_proj && scale && codebooks && codes && q_low && lut && score_range,
               "sva_lookup_verify: null pointer");
   SVA_REQUIRE(fin_idx && fin_count && keys && values && out, "sva_lookup_verify: null pointer");
@@ -821,9 +832,31 @@ extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stri
   rc = summon_impl("sva_lookup_verify", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
                    k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride,
                    sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused,
-                   floor_overshoot, &ql);
+                   floor_overshoot, &ql, stats);
   if (rc != SVA_OK || fused) return rc;
   return sva_verify(q, q_dtype, 0, q_head_stride, 0, keys, values, kv_dtype, kv_head_stride, kv_row_stride, nullptr,
                     nullptr, n_keys, fin_idx, fin_count, 1, H, G, 1, D, B, scaling, out, out_dtype, 0, out_head_stride,
                     0, verify_workspace, verify_workspace_bytes, stream);
+}
+
+}  // namespace sva
+
+extern "C" int sva_lookup_verify(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
+                                 int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
+                                 const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
+                                 int64_t k_low_head_stride, int64_t n_keys, int64_t L, const void* mask, int mask_type,
+                                 int64_t mask_tok_stride, float* q_low, float* lut, float* score_range,
+                                 int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B, int32_t* fin_idx,
+                                 int32_t* fin_count, void* workspace, size_t workspace_bytes, const void* keys,
+                                 const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                                 int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
+                                 void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
+                                 void* stream) {
+  sva::clear_error();
+  return sva::lookup_verify_impl(q, q_dtype, q_head_stride, H, D, R, S, C, q_proj, scale, codebooks, codes, code_type,
+                                 code_head_stride, k_low, k_low_head_stride, n_keys, L, mask, mask_type,
+                                 mask_tok_stride, q_low, lut, score_range, sl_idx, sl_rank, sl_count, B, fin_idx,
+                                 fin_count, workspace, workspace_bytes, keys, values, kv_dtype, kv_head_stride,
+                                 kv_row_stride, G, scaling, out, out_dtype, out_head_stride, verify_workspace,
+                                 verify_workspace_bytes, floor_overshoot, stream, nullptr);
 }

@@ -14,7 +14,7 @@ import math
 import torch
 
 from . import _lib
-from ._lib import check, code_type, dtype_code, lib, ptr, require_device, stream_handle
+from ._lib import DTYPE_CODES, check, code_type, dtype_code, lib, ptr, require_device, stream_handle
 
 
 _workspaces: dict[tuple[torch.device, str, int], torch.Tensor] = {}
@@ -662,6 +662,30 @@ class DecodeLayer:
                                               values.data_ptr(), dtype_code(keys), keys.stride(-3), keys.stride(-2),
                                               row_begin, n_keys, out.data_ptr(), dtype_code(out), out.stride(1),
                                               stream), "sva_decode_layer_step")
+        return out
+
+
+    def step_next(self, q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, kst: tuple, k_low: torch.Tensor,
+                  codes: torch.Tensor, row_begin: int, n_keys: int) -> torch.Tensor | None:
+        """step() for the next token of a caller that compared q [1, H, 1, D]
+        and the cache [1, G, rows, D] (strides `kst`, contiguous rows, K and V
+        alike, one dtype, this device) with the ones a step() call accepted:
+        those checks are not repeated.  None when the layer must bind its
+        buffers again or its output buffer does not fit (take step())."""
+        plan = self.plan
+        stream = stream_handle(self.device)
+        ws = plan._summon_ws(n_keys, stream)
+        vws, kv = plan._vws.get(stream, (None, -1))
+        b = self._bound
+        out = self._out
+        if (b is None or b[0] is not k_low or b[1] is not codes or b[2] is not ws or b[3] is not vws
+                or kv != self._kv_heads or keys.shape[1] != self._kv_heads or out is None or out.dtype is not q.dtype):
+            return None
+        codes_ = DTYPE_CODES
+        check(self._lib.sva_decode_layer_step(self._handle, q.data_ptr(), codes_[q.dtype], q.stride(1), keys.data_ptr(),
+                                              values.data_ptr(), codes_[keys.dtype], kst[1], kst[2], row_begin,
+                                              n_keys, out.data_ptr(), codes_[out.dtype], out.stride(1), stream),
+              "sva_decode_layer_step")
         return out
 
 

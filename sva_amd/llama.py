@@ -125,6 +125,7 @@ class SVALlamaAttention(nn.Module):
         self._postings: inverted.Postings | None = None
         self._decode_plan: kernels.ScanDecodePlan | None = None  # q = 1 buffers, kept across steps
         self._decode_layer: kernels.DecodeLayer | None = None    # the native decode step over those buffers
+        self._fast: tuple | None = None  # what the last native step checked, for the next token's lean path
 
     # ------------------------------------------------------------------
     def forward(self, hidden_states: torch.Tensor, position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
@@ -157,6 +158,10 @@ class SVALlamaAttention(nn.Module):
         # one scan-mode decode token of one sequence with no mask (the token
         # sees every key): the native step, behind checks kept lean because
         # they run for every layer and token
+        if attention_mask is None and self._fast is not None:
+            out = self._decode_next(query, key, value)
+            if out is not None:
+                return out
         if attention_mask is None and query.shape[2] == 1 and query.shape[0] == 1 and \
                 self.serving.summon_mode == "scan" and query.is_cuda and key.is_cuda and value.is_cuda and \
                 key.stride(-1) == 1 and value.stride() == key.stride() and value.shape == key.shape:
@@ -231,6 +236,37 @@ class SVALlamaAttention(nn.Module):
         self._key_len = self._codes_len = k_len
         self._postings = None
         self._signature = sig
+        # the next token takes _decode_next while nothing but the key count
+        # moves on (the plan's shortlist and budget are final from L keys on)
+        self._fast = None
+        if k_len >= self.serving.coarse_shortlist:
+            self._fast = (layer, sig, query.shape, key.shape[1], key.shape[3], key.dtype, query.dtype,
+                          key.get_device())
+        return out
+
+    def _decode_next(self, query, key, value):
+        """The native decode step for the token after one _native_decode set
+        up: the cache grew by one row and its shapes, strides pattern, dtypes
+        and device, the query's shape and the catalog are as checked then, so
+        only those are compared again (a few attribute reads instead of the
+        full checks).  None when anything differs: the caller takes the full
+        path."""
+        layer, sig, qshape, kv_heads, head_dim, kv_dtype, q_dtype, dev = self._fast
+        ks = key.shape
+        n = ks[2]
+        if (n != self._key_len + 1 or self._codes_len != self._key_len or self._signature is not sig
+                or self._k_low is None or n > self._k_low.shape[1] or query.shape != qshape
+                or ks[0] != 1 or ks[1] != kv_heads or ks[3] != head_dim or key.dtype is not kv_dtype
+                or value.dtype is not kv_dtype or query.dtype is not q_dtype
+                or self.serving.summon_mode != "scan"):
+            return None
+        kst = key.stride()
+        if (kst[3] != 1 or value.shape != ks or value.stride() != kst or query.stride(3) != 1
+                or key.get_device() != dev or value.get_device() != dev or query.get_device() != dev):
+            return None
+        out = layer.step_next(query, key, value, kst, self._k_low, self._codes, n - 1, n)
+        if out is not None:
+            self._key_len = self._codes_len = n
         return out
 
     def _scan_attention(self, query, keys, values, k_low, codes, k_len, mask, shortlist, budget):
