@@ -241,7 +241,7 @@ class SVALlamaAttention(nn.Module):
         self._fast = None
         if k_len >= self.serving.coarse_shortlist:
             self._fast = (layer, sig, query.shape, key.shape[1], key.shape[3], key.dtype, query.dtype,
-                          key.get_device())
+                          key.get_device(), self.serving.coarse_shortlist, self.serving.budget)
         return out
 
     def _decode_next(self, query, key, value):
@@ -251,14 +251,15 @@ class SVALlamaAttention(nn.Module):
         only those are compared again (a few attribute reads instead of the
         full checks).  None when anything differs: the caller takes the full
         path."""
-        layer, sig, qshape, kv_heads, head_dim, kv_dtype, q_dtype, dev = self._fast
+        layer, sig, qshape, kv_heads, head_dim, kv_dtype, q_dtype, dev, shortlist, budget = self._fast
+        serving = self.serving
         ks = key.shape
         n = ks[2]
         if (n != self._key_len + 1 or self._codes_len != self._key_len or self._signature is not sig
                 or self._k_low is None or n > self._k_low.shape[1] or query.shape != qshape
                 or ks[0] != 1 or ks[1] != kv_heads or ks[3] != head_dim or key.dtype is not kv_dtype
-                or value.dtype is not kv_dtype or query.dtype is not q_dtype
-                or self.serving.summon_mode != "scan"):
+                or value.dtype is not kv_dtype or query.dtype is not q_dtype or serving.summon_mode != "scan"
+                or serving.coarse_shortlist != shortlist or serving.budget != budget):
             return None
         kst = key.stride()
         if (kst[3] != 1 or value.shape != ks or value.stride() != kst or query.stride(3) != 1

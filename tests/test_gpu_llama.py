@@ -300,3 +300,50 @@ def test_per_head_mask(device):
         differ[0, 2, 0, 30] = fmin
         with pytest.raises(ValueError, match="leading"):
             attn.sva_attention(q, k, v, differ)
+
+
+def test_decode_next_token_path_equals_full_checks(device):
+    # after one native decode step, the next tokens take the lean path (only
+    # what moves is compared again); its logits and statistics equal those of
+    # the full path token by token
+    heads, kv_heads, head_dim = 4, 2, 64
+    model = make_tiny_model(device, hidden=heads * head_dim, heads=heads, kv_heads=kv_heads, seed=7)
+    bundle = make_tiny_bundle(heads=heads, head_dim=head_dim, rank=64, subspaces=2, codewords=16, shortlist=24,
+                              budget=8)
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, 64, (1, 48), generator=g).to(device)
+    steps = torch.randint(0, 64, (1, 6), generator=g).to(device)
+
+    def run(lean):
+        taken = []
+        with torch.no_grad(), patch_llama_attention(model, bundle, summon_mode="scan") as handle:
+            for layer in model.model.layers:
+                attn = layer.self_attn
+                if lean:
+                    orig = attn._decode_next
+
+                    def counted(q, k, v, _orig=orig):
+                        out = _orig(q, k, v)
+                        taken.append(out is not None)
+                        return out
+
+                    attn._decode_next = counted
+                else:
+                    attn._decode_next = lambda q, k, v: None
+            out = model(input_ids=prompt, use_cache=True)
+            logits, past = [out.logits], out.past_key_values
+            for j in range(steps.shape[1]):
+                out = model(input_ids=steps[:, j:j + 1], use_cache=True, past_key_values=past)
+                logits.append(out.logits)
+                past = out.past_key_values
+            torch.cuda.synchronize()
+            totals = dict(handle.stats.totals)
+        return logits, totals, taken
+
+    lean_logits, lean_totals, taken = run(True)
+    full_logits, full_totals, _ = run(False)
+    # two layers x six tokens; the first decode token of each layer sets the lean path up
+    assert sum(taken) == 2 * (steps.shape[1] - 1), taken
+    for a, b in zip(lean_logits, full_logits):
+        assert torch.equal(a, b)
+    assert lean_totals == full_totals and lean_totals["queries"] > 0
