@@ -495,15 +495,18 @@ __global__ void __launch_bounds__(ITEM_BLOCK, NPT <= 8 ? 8 : 4) summon_regs_kern
     const int oct = (int)threadIdx.x >> 3, c = (int)threadIdx.x & 7;
     const float4* q4 = reinterpret_cast<const float4*>(p.q_low + (int64_t)item * 64);
     const float4 q0 = q4[c], q1 = q4[8 + c];
-    const float4* kl4 = reinterpret_cast<const float4*>(p.k_low + (int64_t)h * p.klow_hs + off * 64);
+    // a row is 256 bytes (R = 64 floats) and N <= 16 * ITEM_BLOCK keys, so a
+    // row's byte offset fits 32 bits: one shift-add per row, the base uniform
+    const char* klb = reinterpret_cast<const char*>(p.k_low + (int64_t)h * p.klow_hs + off * 64);
+    const uint32_t lane_b = 16u * (uint32_t)c;
     for (int j0 = 0; j0 < leff; j0 += REG_OCT * (ITEM_BLOCK / 8)) {
       float4 r0[REG_OCT], r1[REG_OCT];
 #pragma unroll
       for (int u = 0; u < REG_OCT; ++u) {
         const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
-        const int64_t n = slidx[j < leff ? j : 0];
-        r0[u] = kl4[n * 16 + c];
-        r1[u] = kl4[n * 16 + 8 + c];
+        const uint32_t o = ((uint32_t)slidx[j < leff ? j : 0] << 8) + lane_b;
+        r0[u] = *reinterpret_cast<const float4*>(klb + o);
+        r1[u] = *reinterpret_cast<const float4*>(klb + o + 128);
       }
 #pragma unroll
       for (int u = 0; u < REG_OCT; ++u) {
