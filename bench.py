@@ -1004,7 +1004,7 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode path shards by KV-head group or "
-                                   "sequence (see DESIGN.md) but no multi-GPU figure is produced",
+                                   "sequence, but no multi-GPU figure is produced",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import numpy as np

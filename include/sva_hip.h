@@ -4,7 +4,7 @@
  * The reference (asystemoffields/sva) is pure Python on PyTorch and has no FFI;
  * each entry point below replaces the torch ops of one stage of its decode
  * path, cited as file:line.  A ctypes binding (sva_amd/_lib.py) is the host
- * side; INTEGRATION.md shows how a reference-side caller would bind it.
+ * side.
  *
  * Conventions
  *  - Pointers are device pointers unless stated.  Nothing here allocates,

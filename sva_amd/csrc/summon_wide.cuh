@@ -295,7 +295,7 @@ SVA_DEV void append_round(const SummonParams& p, const bool (&c)[KPT], const flo
 // (one 16-byte word of codes) is examined key by key only when its largest
 // sum reaches the floor.  Full chunks of up to four subspaces score every
 // round before any append, so the rounds' table reads are in flight
-// together rather than each behind the previous round's branch (eight
+// together rather than each behind the branch of the round before (eight
 // subspaces keep the per-round order: holding every round's sums would cost
 // them a wave per SIMD).
 template <int S, bool SMALLC, bool CHECK, bool MASKED>

@@ -66,7 +66,7 @@ def make_case(H=9, G=3, N=8192, D=64, R=64, S=2, C=256, Q=1, dtype=torch.float32
     return Case(H, G, N, D, R, S, C, q, keys, values, k_low, q_proj, k_proj, scale, codebooks, codes, dtype)
 
 
-def config1_inputs(seed: int = 20260514):
+def lookup8192_inputs(seed: int = 20260514):
     """The single-layer decode lookup of the reference's CPU-runnable case:
     8192 cached keys, head_dim 64, 9 query heads over 3 KV heads, K/V/q iid
     N(0, 1) fp32, learned maps N(0, 1/64) of rank 64, 2 x 256 PQ codebooks of

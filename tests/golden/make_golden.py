@@ -1,5 +1,5 @@
-"""Writes tests/golden/config1_reference.npz: outputs of the reference
-package's own functions on tests/cases.py:config1_inputs().
+"""Writes tests/golden/lookup8192_reference.npz: outputs of the reference
+package's own functions on tests/cases.py:lookup8192_inputs().
 
 Run once, in a container that holds the reference at /root/reference
 (``python tests/golden/make_golden.py``).  Nothing on the GPU side runs this
@@ -24,12 +24,12 @@ sys.path.insert(1, str(ROOT))
 
 from sva.ops import encode_product_keys, product_quantized_scores  # noqa: E402
 
-from tests.cases import config1_inputs  # noqa: E402
+from tests.cases import lookup8192_inputs  # noqa: E402
 
 
 def main() -> None:
     torch.set_num_threads(1)
-    inp = config1_inputs()
+    inp = lookup8192_inputs()
     H, _, D = inp["q"].shape
     G = inp["keys"].shape[0]
     R = inp["q_proj"].shape[2]
@@ -62,7 +62,7 @@ def main() -> None:
         w = torch.softmax(att, dim=-1, dtype=torch.float32)
         out = (w[..., None] * sel_v).sum(-2)
     np.savez_compressed(
-        Path(__file__).with_name("config1_reference.npz"),
+        Path(__file__).with_name("lookup8192_reference.npz"),
         q_low=q_low[0, :, 0].numpy(),
         lut=lut.numpy(),
         k_low_head_sums=k_low[0].double().sum(dim=(1, 2)).numpy(),
@@ -75,7 +75,7 @@ def main() -> None:
         out=out[0, :, 0].numpy(),
         torch_version=np.array(torch.__version__),
     )
-    print("wrote", Path(__file__).with_name("config1_reference.npz"))
+    print("wrote", Path(__file__).with_name("lookup8192_reference.npz"))
 
 
 if __name__ == "__main__":

@@ -1,5 +1,5 @@
 """Comparison of a full decode lookup against the reference's own outputs on
-config 1 (tests/golden/config1_reference.npz, written by
+the 8192-key single-layer lookup (tests/golden/lookup8192_reference.npz, written by
 tests/golden/make_golden.py).  Shared by the oracle test (CPU) and the GPU
 test: each passes the pieces it computed."""
 
@@ -11,7 +11,7 @@ import numpy as np
 
 import oracle
 
-GOLDEN = Path(__file__).resolve().parent / "golden" / "config1_reference.npz"
+GOLDEN = Path(__file__).resolve().parent / "golden" / "lookup8192_reference.npz"
 
 
 def load():

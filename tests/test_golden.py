@@ -1,5 +1,5 @@
-"""The CPU oracle against the reference's own outputs on config 1
-(tests/golden/config1_reference.npz)."""
+"""The CPU oracle against the reference's own outputs on the 8192-key lookup
+(tests/golden/lookup8192_reference.npz)."""
 
 from __future__ import annotations
 
@@ -7,12 +7,12 @@ import numpy as np
 
 import oracle
 from tests import golden_check
-from tests.cases import config1_inputs
+from tests.cases import lookup8192_inputs
 
 
 def test_oracle_matches_reference_outputs():
     ref = golden_check.load()
-    inp = config1_inputs()
+    inp = lookup8192_inputs()
     H, G = inp["q"].shape[0], inp["keys"].shape[0]
     scale = np.exp(inp["logit_scale"]).clip(0.01, 100.0).astype(np.float32)
     q_low = oracle.query_low(inp["q"], inp["q_proj"], scale)[:, 0]

@@ -127,10 +127,10 @@ def test_smollm2_layer_prefill_8192(device):
 
 
 def test_smollm2_30_layer_decode_steps(device):
-    """Config 2's model: 30 SVA-patched layers, an 8192-token prefill, then greedy decode steps through the native
-    decode step (catalog append, lookup, verifier and statistics in one call per layer).  Layers 0 and 29's
-    decode outputs equal the oracle's scan attention over their own catalogs; every step appends one catalog row;
-    the statistics count 9 queries, 2048 summoned and 512 verified keys per head per layer and step."""
+    """The SmolLM2-135M-shape model with 30 SVA-patched layers: an 8192-token prefill, then greedy decode steps
+    through the native decode step (catalog append, lookup, verifier and statistics in one call per layer).  Layers 0
+    and 29's decode outputs equal the oracle's scan attention over their own catalogs; every step appends one catalog
+    row; the statistics count 9 queries, 2048 summoned and 512 verified keys per head per layer and step."""
     from sva import patch_llama_attention
 
     n, steps, layers = 8192, 3, 30

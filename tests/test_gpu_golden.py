@@ -1,6 +1,6 @@
 """The whole GPU path (write encode -> query LUT -> summon -> budget ->
-verify) against the reference's own outputs on config 1
-(tests/golden/config1_reference.npz)."""
+verify) against the reference's own outputs on the 8192-key lookup
+(tests/golden/lookup8192_reference.npz)."""
 
 from __future__ import annotations
 
@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from tests import golden_check
-from tests.cases import config1_inputs
+from tests.cases import lookup8192_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -18,7 +18,7 @@ def test_gpu_path_matches_reference_outputs(device):
     from sva_amd import kernels
 
     ref = golden_check.load()
-    inp = config1_inputs()
+    inp = lookup8192_inputs()
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
     H, N = inp["q"].shape[0], inp["keys"].shape[1]
     S = inp["codebooks"].shape[1]

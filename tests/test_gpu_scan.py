@@ -79,7 +79,7 @@ def _check_case(case, res, shortlist, budget, allowed=None, tol=1e-5):
 
 
 @pytest.mark.parametrize("S,C", [(2, 256), (4, 64), (1, 256)])
-def test_scan_decode_fp32_config1(device, S, C):
+def test_scan_decode_fp32_8192_keys(device, S, C):
     case = make_case(N=8192, S=S, C=C, seed=11 + S)
     res = _run_scan(case, device, 2048, 512)
     _check_case(case, res, 2048, 512)
