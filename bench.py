@@ -157,6 +157,9 @@ def parse_args():
     ap.add_argument("--decode-steps", type=int, default=256, help="model suite: timed greedy decode steps")
     ap.add_argument("--write-profiles", nargs=3, metavar=("STATS_CSV", "FETCH_CSV", "WRITE_CSV"),
                     help="summarize rocprofv3 outputs of this benchmark into profiles/ and exit")
+    ap.add_argument("--write-graph-profile", metavar="TRACE_CSV",
+                    help="summarize the graph-replayed dispatches of a --kernel-trace run of the decode step (per "
+                         "dispatch file) into profiles/<layout>_graph_kernel_trace.md and exit")
     ap.add_argument("--write-trace-profile", nargs=2, metavar=("STATS_CSV", "NAME"),
                     help="summarize a --kernel-trace --stats file into profiles/NAME.md and exit")
     ap.add_argument("--profile-title", default="Kernel durations")
@@ -337,6 +340,52 @@ def _short_kernel_name(name: str) -> str:
         out.append(ch)
     short = "".join(out).strip()
     return short[5:] if short.startswith("void ") else short
+
+
+def write_graph_profile(args):
+    """Per-kernel durations of the dispatches the HIP graph launched in a
+    rocprofv3 --kernel-trace run of the decode step (graph_replay: one
+    checked replay, warm-up replays, the wall-timed and the event-timed ones,
+    all after the eager steps), from the per-dispatch trace file."""
+
+    import csv
+
+    import numpy as np
+
+    n_layers = args.layers
+    reps = max(1, args.steps // n_layers)
+    replays = 1 + max(1, args.warmup // n_layers) + reps + min(reps, 100)
+    last = replays * n_layers
+    durs = {}
+    with open(args.write_graph_profile) as f:
+        for r in csv.DictReader(f):
+            k = _kernel_key(r["Kernel_Name"])
+            if k in PATH_KERNELS:
+                durs.setdefault(k, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    cfg = f"--layout {args.layout} --shortlist {args.shortlist} --budget {args.budget}"
+    cmd = (f"rocprofv3 --kernel-trace --output-format csv -d OUT -o kt -- python bench.py --steps {args.steps} "
+           f"--warmup {args.warmup} --no-cpu-baseline --no-decode --no-extra {cfg}")
+    lines = [f"# Kernel durations inside the HIP-graph replay: decode step (sva_lookup_verify) at 1M keys, "
+             f"{args.layout} codes, L/B {args.shortlist}/{args.budget}", "",
+             f"Command: `{cmd}` (file `kt_kernel_trace.csv`).", "",
+             f"The bench's eager passes come first; it then captures the {n_layers} rotated layers' lookups in one "
+             f"graph and replays it {replays} times (1 checked against the eager outputs, "
+             f"{max(1, args.warmup // n_layers)} warm-up, {reps} wall-timed, {min(reps, 100)} event-timed). The "
+             f"table covers the last {last} dispatches of each kernel ({replays} replays x {n_layers} lookups), "
+             "those the graph launched.", "",
+             "| kernel | graph dispatches | avg us | p50 us | min us | max us |", "|---|---:|---:|---:|---:|---:|"]
+    total = 0.0
+    for k in PATH_KERNELS:
+        if k not in durs:
+            continue
+        d = np.array([(e - b) / 1e3 for b, e in sorted(durs[k])[-last:]])
+        total += d.mean()
+        lines.append(f"| {k} | {len(d)} | {d.mean():.2f} | {np.percentile(d, 50):.2f} | {d.min():.2f} | "
+                     f"{d.max():.2f} |")
+    lines += [f"| **sum per lookup** | | {total:.2f} | | | |", ""]
+    out = ROOT / "profiles" / f"{profile_stem(args)}_graph_kernel_trace.md"
+    out.write_text("\n".join(lines))
+    print(f"wrote {out}")
 
 
 def write_trace_profile(args):
@@ -995,6 +1044,9 @@ def main():
         return
     if args.write_trace_profile:
         write_trace_profile(args)
+        return
+    if args.write_graph_profile:
+        write_graph_profile(args)
         return
     if args.suite in ("write", "model", "ragged", "socket", "overshoot", "verify"):
         if args.gpus != 1:
