@@ -1,0 +1,14 @@
+// The fused one-token lookup of the per-item register path with its
+// verifier: head_dim 64, float32 K / V.
+#include "lookup_item.cuh"
+
+namespace sva {
+namespace item_lookup {
+
+int launch_v64_f32(const LutParams& lp, const SummonParams& p, const FusedVerify& fv, int32_t* overshoot,
+                   hipStream_t st) {
+  return launch<64, F32>(lp, p, fv, overshoot, st);
+}
+
+}  // namespace item_lookup
+}  // namespace sva

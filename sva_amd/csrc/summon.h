@@ -103,6 +103,13 @@ struct FusedVerify {
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
+// One token of one sequence on the per-item register path with the verifier
+// (lookup_item.hip): the prepared decode query, the summon and the verifier
+// in one launch when item_fused_eligible holds for the prepared query `ql`.
+bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const FusedVerify& fv);
+// overshoot (optional, [H]) is cleared: the per-item path has no sampled floor.
+int item_lookup_verify_path(const QueryLaunch& ql, const SummonParams& p, const FusedVerify& fv, int32_t* overshoot,
+                            hipStream_t stream);
 // sva_lookup_verify, adding each query head's counts to `stats` (an int64 [4]
 // row: summoned, verified, -, queries) when it is not null: only where the
 // per-item register path serves the shape (sva_summon_strategy 3).  The caller
