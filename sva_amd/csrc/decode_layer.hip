@@ -8,6 +8,7 @@
 
 #include "capi_internal.h"
 #include "summon.h"
+#include "write_few.cuh"
 
 struct sva_decode_layer {
   int64_t H, G, D, R, S, C, L, B;
@@ -119,13 +120,23 @@ extern "C" int sva_decode_layer_step(sva_decode_layer* h, const void* q, int q_d
               (long long)n_keys, (long long)h->capacity);
   SVA_REQUIRE(row_begin >= 0 && row_begin <= n_keys, "sva_decode_layer_step: rows from %lld of %lld",
               (long long)row_begin, (long long)n_keys);
-  // the catalog rows the cache gained since the last step (sva/llama.py:597-616)
+  // the catalog rows the cache gained since the last step (sva/llama.py:597-616):
+  // a few rows go with the lookup (inside its kernel on the one-launch path),
+  // more are encoded first
   int rc = SVA_OK;
+  sva::WriteParams wp;
+  const sva::WriteParams* append = nullptr;
   if (n_keys > row_begin) {
-    rc = sva_write_encode(keys, kv_dtype, kv_head_stride, kv_row_stride, row_begin, n_keys - row_begin, h->H, h->G,
-                          h->D, h->R, h->S, h->C, h->k_proj, h->codebooks, h->k_low, h->klow_hs, h->codes,
-                          h->code_type, h->code_hs, stream);
+    rc = sva::write_encode_setup(keys, kv_dtype, kv_head_stride, kv_row_stride, row_begin, n_keys - row_begin, h->H,
+                                 h->G, h->D, h->R, h->S, h->C, h->k_proj, h->codebooks, h->k_low, h->klow_hs,
+                                 h->codes, h->code_type, h->code_hs, &wp);
     if (rc != SVA_OK) return rc;
+    if (sva::write_few_form(wp) >= 0) {
+      append = &wp;
+    } else {
+      rc = sva::write_encode_launch(wp, (hipStream_t)stream);
+      if (rc != SVA_OK) return rc;
+    }
   }
   // the lookup and the verifier (sva/llama.py:211-317); only the paths with a
   // sampled floor (strategy 1 and 2) report overshoots, so the per-item path
@@ -140,7 +151,7 @@ extern "C" int sva_decode_layer_step(sva_decode_layer* h, const void* q, int q_d
                                nullptr, 0, 0, h->q_low, h->lut, h->range, h->sl_idx, h->sl_rank, h->counts, h->B,
                                h->fin_idx, h->counts + H, h->ws, h->ws_bytes, keys, values, kv_dtype, kv_head_stride,
                                kv_row_stride, h->G, h->scaling, out, out_dtype, out_head_stride, h->vws, h->vws_bytes,
-                               with_floor ? h->counts + 2 * H : nullptr, stream, fused_stats);
+                               with_floor ? h->counts + 2 * H : nullptr, stream, fused_stats, append);
   if (rc != SVA_OK) return rc;
   // the step's statistics (sva/llama.py:319-326), summed on the device
   if (h->stats != nullptr && fused_stats == nullptr) {

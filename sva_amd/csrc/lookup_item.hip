@@ -4,7 +4,8 @@
 
 namespace sva {
 
-bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const FusedVerify& fv) {
+bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const FusedVerify& fv,
+                         const WriteParams* append) {
   const int form_s = ql.form == QUERY_DECODE_4_64    ? 4
                      : ql.form == QUERY_DECODE_2_256 ? 2
                      : ql.form == QUERY_DECODE_1_256 ? 1
@@ -18,16 +19,28 @@ bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const Fus
   if (fv.out == nullptr || fv.D != 64 || fv.G <= 0 || p.H % fv.G != 0) return false;
   if (fv.q_dtype < 0 || fv.q_dtype > 2 || fv.kv_dtype < 0 || fv.kv_dtype > 2 || fv.out_dtype < 0 || fv.out_dtype > 2)
     return false;
+  if (append != nullptr) {  // the append writes this lookup's catalog, in the form compiled in
+    if (fv.kv_dtype == F32) return false;  // the fp32 K / V variants carry no append
+    const WriteParams& w = *append;
+    const int form = write_few_form(w);
+    if (form < 0 || (p.S > 1 && form != 64 / p.S) || w.codes == nullptr || w.codes != p.codes || w.k_low != p.k_low ||
+        w.code_hs != p.code_hs || w.klow_hs != p.klow_hs || w.ctype != p.ctype || w.H != p.H || w.G != fv.G ||
+        w.R != p.R || w.S != p.S || w.C != p.C || w.D != fv.D || w.row0 + w.n_rows > p.N)
+      return false;
+  }
   return item_lookup::item_lds(p, fv.D) <= item_lookup::kDynLds;
 }
 
-int item_lookup_verify_path(const QueryLaunch& ql, const SummonParams& p, const FusedVerify& fv, int32_t* overshoot,
-                            hipStream_t stream) {
+int item_lookup_verify_path(const QueryLaunch& ql, const SummonParams& p, const FusedVerify& fv,
+                            const WriteParams* append, int32_t* overshoot, hipStream_t stream) {
   using namespace item_lookup;
   SVA_REQUIRE(fv.D == 64, "item_lookup_verify: head_dim %d", fv.D);
-  if (fv.kv_dtype == BF16) return launch_v64_bf16(ql.p, p, fv, overshoot, stream);
-  if (fv.kv_dtype == F16) return launch_v64_f16(ql.p, p, fv, overshoot, stream);
-  return launch_v64_f32(ql.p, p, fv, overshoot, stream);
+  WriteParams none{};
+  none.n_rows = 0;
+  const WriteParams& wp = append != nullptr ? *append : none;
+  if (fv.kv_dtype == BF16) return launch_v64_bf16(ql.p, p, fv, wp, overshoot, stream);
+  if (fv.kv_dtype == F16) return launch_v64_f16(ql.p, p, fv, wp, overshoot, stream);
+  return launch_v64_f32(ql.p, p, fv, wp, overshoot, stream);
 }
 
 }  // namespace sva

@@ -5,9 +5,9 @@
 namespace sva {
 namespace item_lookup {
 
-int launch_v64_f32(const LutParams& lp, const SummonParams& p, const FusedVerify& fv, int32_t* overshoot,
-                   hipStream_t st) {
-  return launch<64, F32>(lp, p, fv, overshoot, st);
+int launch_v64_f32(const LutParams& lp, const SummonParams& p, const FusedVerify& fv, const WriteParams& wp,
+                   int32_t* overshoot, hipStream_t st) {
+  return launch<64, F32>(lp, p, fv, wp, overshoot, st);
 }
 
 }  // namespace item_lookup

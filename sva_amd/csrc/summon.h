@@ -49,6 +49,7 @@ __host__ __device__ inline int sample_floor_rank(int64_t L, int64_t n_keys, int 
 }
 
 struct QueryLaunch;  // query.h: a prepared query launch the class path may fuse
+struct WriteParams;  // write_few.cuh: a prepared catalog append of a few rows
 
 struct SummonParams {
   const float* lut;    // [items, S*C]
@@ -104,16 +105,21 @@ int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream);
 bool summon_regs_eligible(const SummonParams& p);
 int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream);
 // One token of one sequence on the per-item register path with the verifier
-// (lookup_item.hip): the prepared decode query, the summon and the verifier
-// in one launch when item_fused_eligible holds for the prepared query `ql`.
-bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const FusedVerify& fv);
-// overshoot (optional, [H]) is cleared: the per-item path has no sampled floor.
-int item_lookup_verify_path(const QueryLaunch& ql, const SummonParams& p, const FusedVerify& fv, int32_t* overshoot,
-                            hipStream_t stream);
+// (lookup_item.hip): the prepared catalog append of a few rows (optional),
+// the prepared decode query, the summon and the verifier in one launch when
+// item_fused_eligible holds for them.  overshoot (optional, [H]) is cleared:
+// the per-item path has no sampled floor.
+bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const FusedVerify& fv,
+                         const WriteParams* append);
+int item_lookup_verify_path(const QueryLaunch& ql, const SummonParams& p, const FusedVerify& fv,
+                            const WriteParams* append, int32_t* overshoot, hipStream_t stream);
 // sva_lookup_verify, adding each query head's counts to `stats` (an int64 [4]
 // row: summoned, verified, -, queries) when it is not null: only where the
-// per-item register path serves the shape (sva_summon_strategy 3).  The caller
-// clears the error state.
+// per-item register path serves the shape (sva_summon_strategy 3).  append
+// (optional): a prepared few-row catalog append (write_encode_setup) that
+// must land before the lookup reads the catalog; it runs inside the lookup's
+// kernel where the one-launch path serves the shape, else first on its own.
+// The caller clears the error state.
 int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_t H, int64_t D, int64_t R,
                        int64_t S, int64_t C, const float* q_proj, const float* scale, const float* codebooks,
                        const void* codes, int code_type, int64_t code_head_stride, const float* k_low,
@@ -124,7 +130,7 @@ int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_
                        const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                        int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
                        void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
-                       void* stream, unsigned long long* stats);
+                       void* stream, unsigned long long* stats, const WriteParams* append = nullptr);
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
                          int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);

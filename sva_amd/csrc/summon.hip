@@ -21,6 +21,7 @@
 #include "query.h"
 #include "summon.h"
 #include "summon_regs.cuh"
+#include "write_few.cuh"
 
 using namespace sva;
 
@@ -254,7 +255,8 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                 int64_t mask_tok_stride, int32_t* sl_idx, float* sl_rank, int32_t* sl_count, int64_t B,
                 int32_t* fin_idx, int32_t* fin_count, void* workspace, size_t workspace_bytes, void* stream,
                 const sva::FusedVerify* fv = nullptr, bool* fused = nullptr, int32_t* overshoot = nullptr,
-                const sva::QueryLaunch* query = nullptr, unsigned long long* stats = nullptr) {
+                const sva::QueryLaunch* query = nullptr, unsigned long long* stats = nullptr,
+                const sva::WriteParams* append = nullptr) {
   if (fused != nullptr) *fused = false;
   SVA_REQUIRE(lut && score_range && q_low && codes && k_low && sl_count, "%s: null pointer", fn);
   SVA_REQUIRE((sl_idx == nullptr) == (sl_rank == nullptr), "%s: shortlist indices and ranks go together", fn);
@@ -315,10 +317,14 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   // one token of one sequence on the per-item register path with the
   // verifier: the query, the summon and the verifier in one launch
   if (fv != nullptr && fused != nullptr && query != nullptr && n_keys > 0 && !class_path &&
-      !sva::summon_wide_eligible(p, items) && sva::item_fused_eligible(p, *query, *fv)) {
-    const int rc = sva::item_lookup_verify_path(*query, p, *fv, overshoot, (hipStream_t)stream);
+      !sva::summon_wide_eligible(p, items) && sva::item_fused_eligible(p, *query, *fv, append)) {
+    const int rc = sva::item_lookup_verify_path(*query, p, *fv, append, overshoot, (hipStream_t)stream);
     if (rc == SVA_OK) *fused = true;
     return rc;
+  }
+  if (append != nullptr) {  // the catalog's new rows before anything reads them
+    const int rc = sva::write_encode_launch(*append, (hipStream_t)stream);
+    if (rc != SVA_OK) return rc;
   }
   if (query != nullptr && !(class_path && query->form == sva::QUERY_DECODE_1_256)) {
     const int rc = sva::query_lut_launch(*query, (hipStream_t)stream);
@@ -423,7 +429,7 @@ int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_
                        const void* values, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                        int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
                        void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
-                       void* stream, unsigned long long* stats) {
+                       void* stream, unsigned long long* stats, const WriteParams* append) {
   SVA_REQUIRE(q && q_proj && scale && codebooks && codes && q_low && lut && score_range,
               "sva_lookup_verify: null pointer");
   SVA_REQUIRE(fin_idx && fin_count && keys && values && out, "sva_lookup_verify: null pointer");
@@ -457,7 +463,7 @@ int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_
   rc = summon_impl("sva_lookup_verify", lut, score_range, q_low, codes, code_type, code_head_stride, k_low,
                    k_low_head_stride, nullptr, nullptr, 1, H, 1, n_keys, R, S, C, L, mask, mask_type, mask_tok_stride,
                    sl_idx, sl_rank, sl_count, B, fin_idx, fin_count, workspace, workspace_bytes, stream, &fv, &fused,
-                   floor_overshoot, &ql, stats);
+                   floor_overshoot, &ql, stats, append);
   if (rc != SVA_OK || fused) return rc;
   return sva_verify(q, q_dtype, 0, q_head_stride, 0, keys, values, kv_dtype, kv_head_stride, kv_row_stride, nullptr,
                     nullptr, n_keys, fin_idx, fin_count, 1, H, G, 1, D, B, scaling, out, out_dtype, 0, out_head_stride,

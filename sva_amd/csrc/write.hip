@@ -17,6 +17,7 @@
 #include "capi_internal.h"
 #include "common.cuh"
 #include "summon.h"
+#include "write_few.cuh"
 
 using namespace sva;
 
@@ -26,20 +27,6 @@ constexpr int WT = 256;  // threads per workgroup
 constexpr int KT = 64;   // rows per workgroup
 constexpr int CB_PAD = 4;
 
-struct WriteParams {
-  const void* keys;
-  int kv_dtype;
-  int64_t kv_hs, kv_rs;
-  int64_t row0, n_rows;
-  int H, G, D, R, S, C;
-  const float* k_proj;     // [H, D, R]
-  const float* codebooks;  // [H, S, C, sub]
-  float* k_low;            // [H, rows, R] (head stride klow_hs)
-  int64_t klow_hs;
-  void* codes;             // [H, rows, S] (head stride code_hs)
-  int ctype;
-  int64_t code_hs;
-};
 
 // SUB: compile-time subspace width (0: runtime, x read from LDS).
 template <int SUB>
@@ -556,125 +543,11 @@ __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p)
   }
 }
 
-// A decode step's append (at most FEW_ROWS rows): one workgroup per head,
-// the same arithmetic as the kernels above with the work spread over the
-// threads instead of over a tile of rows: thread (row, r) forms k_low[row][r]
-// by the fma chain over d, then, per subspace and row, thread c the distance
-// to codeword c, and the workgroup the first index of the least distance.
-// The bulk kernels stage a 64-row tile's map and codebooks for one row.
-constexpr int FEW_ROWS = 4;
-constexpr int FEW_MAP = 64 * 64;  // map floats staged in LDS
-
+// A decode step's append (at most FEW_ROWS rows): few_append (write_few.cuh)
+// with one 256-thread workgroup per head.
 template <int SUB>
 __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
-#pragma clang fp contract(off)
-  __shared__ float kr[FEW_ROWS][256];  // the new K rows (D <= 256)
-  __shared__ float xl[FEW_ROWS][256];  // their k_low rows (R <= 256)
-  __shared__ __align__(16) float ws[FEW_MAP];  // the head's map when D * R <= FEW_MAP
-  __shared__ float rbest[WT / WAVE];
-  __shared__ int rarg[WT / WAVE];
-  const int D = p.D, R = p.R, S = p.S, C = p.C;
-  const int sub = SUB > 0 ? SUB : R / S;
-  const int h = blockIdx.x;
-  const int g = h / (p.H / p.G);
-  const int nr = (int)p.n_rows;  // <= FEW_ROWS
-  const int t = threadIdx.x, lane = lane_id(), wid = t / WAVE;
-  const float* W = p.k_proj + (int64_t)h * D * R;
-  const bool map_in_lds = D * R <= FEW_MAP && (D * R) % 4 == 0 && ((uintptr_t)W & 15u) == 0;  // uniform
-  // thread c < C holds codeword c's row of the current subspace (SUB > 0, C <= WT), requested for
-  // subspace 0 before the projection so that both loads overlap
-  const bool rows_in_regs = SUB > 0 && C <= WT;
-  float crow[SUB > 0 ? SUB : 1];
-  auto load_row = [&](int s) {
-    if constexpr (SUB > 0) {
-      const float4* src = reinterpret_cast<const float4*>(p.codebooks + (((int64_t)h * S + s) * C + min(t, C - 1)) * SUB);
-#pragma unroll
-      for (int k = 0; k < SUB / 4; ++k) {
-        const float4 v = src[k];
-        crow[4 * k] = v.x, crow[4 * k + 1] = v.y, crow[4 * k + 2] = v.z, crow[4 * k + 3] = v.w;
-      }
-    }
-  };
-  if (rows_in_regs && p.codes != nullptr) load_row(0);
-  if (map_in_lds)
-    for (int i = t; i < D * R / 4; i += WT) reinterpret_cast<float4*>(ws)[i] = reinterpret_cast<const float4*>(W)[i];
-  for (int e = t; e < nr * D; e += WT) {
-    const int j = e / D, d = e - j * D;
-    kr[j][d] = load_elem(p.keys, (int64_t)g * p.kv_hs + (p.row0 + j) * p.kv_rs + d, p.kv_dtype);
-  }
-  __syncthreads();
-  const float* Wm = map_in_lds ? ws : W;
-  for (int e = t; e < nr * R; e += WT) {
-    const int j = e / R, r = e - j * R;
-    float acc = 0.0f;
-    for (int d = 0; d < D; ++d) acc = __builtin_fmaf(kr[j][d], Wm[d * R + r], acc);
-    xl[j][r] = acc;
-    p.k_low[(int64_t)h * p.klow_hs + (p.row0 + j) * R + r] = acc;
-  }
-  if (p.codes == nullptr) return;  // uniform
-  __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const float* cbs = p.codebooks + ((int64_t)h * S + s) * C * sub;
-    if (rows_in_regs && s > 0) load_row(s);
-    float cn = 0.0f;  // the codeword's squared norm in torch's sum order (rows held in registers)
-    if constexpr (SUB > 0) {
-      if (rows_in_regs) cn = torch_order_dot(crow, crow, SUB);
-    }
-    for (int j = 0; j < nr; ++j) {
-      const float* xs = &xl[j][s * sub];
-      const float xx = torch_order_dot(xs, xs, sub);
-      // this thread's codewords in ascending order: the least distance, its
-      // first index; NaN never wins, and none at all is index INT_MAX
-      float best = INFINITY;
-      int arg = 0x7FFFFFFF;
-      if (rows_in_regs) {
-        if (t < C) {
-          float xc = 0.0f;
-#pragma unroll
-          for (int k = 0; k < (SUB > 0 ? SUB : 1); ++k) xc = __builtin_fmaf(xs[k], crow[k], xc);
-          const float dist = (xx - 2.0f * xc) + cn;
-          if (dist < best) {
-            best = dist;
-            arg = t;
-          }
-        }
-      } else {
-        for (int c = t; c < C; c += WT) {
-          const float* cr = cbs + (int64_t)c * sub;
-          float xc = 0.0f;
-          for (int k = 0; k < sub; ++k) xc = __builtin_fmaf(xs[k], cr[k], xc);
-          const float dist = (xx - 2.0f * xc) + torch_order_dot(cr, cr, sub);
-          if (dist < best) {
-            best = dist;
-            arg = c;
-          }
-        }
-      }
-      // (best, arg) ordered by distance, then index: across the wave, then the waves
-      for (int o = 1; o < WAVE; o <<= 1) {
-        const float b2 = __shfl_xor(best, o, WAVE);
-        const int a2 = __shfl_xor(arg, o, WAVE);
-        if (b2 < best || (b2 == best && a2 < arg)) {
-          best = b2;
-          arg = a2;
-        }
-      }
-      if (lane == 0) {
-        rbest[wid] = best;
-        rarg[wid] = arg;
-      }
-      __syncthreads();
-      if (t == 0) {
-        for (int w = 1; w < WT / WAVE; ++w)
-          if (rbest[w] < best || (rbest[w] == best && rarg[w] < arg)) {
-            best = rbest[w];
-            arg = rarg[w];
-          }
-        store_code(p.codes, (int64_t)h * p.code_hs + (p.row0 + j) * S + s, p.ctype, arg == 0x7FFFFFFF ? 0 : arg);
-      }
-      __syncthreads();
-    }
-  }
+  few_append<SUB, WT>(p, (int)blockIdx.x);
 }
 
 template <int SUB>
@@ -699,12 +572,13 @@ int launch_write(const WriteParams& p, dim3 grid, size_t lds, hipStream_t stream
 
 }  // namespace
 
-extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
-                                int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R,
-                                int64_t S, int64_t C, const float* k_proj, const float* codebooks, float* k_low,
-                                int64_t k_low_head_stride, void* codes, int code_type, int64_t code_head_stride,
-                                void* stream) {
-  sva::clear_error();
+namespace sva {
+
+int write_encode_setup(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                       int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R, int64_t S,
+                       int64_t C, const float* k_proj, const float* codebooks, float* k_low,
+                       int64_t k_low_head_stride, void* codes, int code_type, int64_t code_head_stride,
+                       WriteParams* out) {
   SVA_REQUIRE(keys && k_proj && codebooks && k_low, "sva_write_encode: null pointer");
   SVA_REQUIRE(row_begin >= 0 && n_rows >= 0, "sva_write_encode: bad row range");
   SVA_REQUIRE(H > 0 && G > 0 && H % G == 0, "sva_write_encode: %lld query heads over %lld KV heads", (long long)H,
@@ -717,14 +591,8 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   SVA_REQUIRE(kv_dtype >= 0 && kv_dtype <= 2 && code_type >= 0 && code_type <= 3, "sva_write_encode: bad dtype");
   const int64_t code_max = code_type == 0 ? 256 : code_type == 1 ? 32768 : (1ll << 31);
   SVA_REQUIRE(C <= code_max, "sva_write_encode: %lld codewords do not fit the code type", (long long)C);
-  const size_t lds = write_lds_bytes(D, R, S, C);
-  const bool tiled = R % 4 == 0 && (R / S) % 4 == 0 && k_low_head_stride % 4 == 0 &&
-                     (((uintptr_t)k_proj | (uintptr_t)codebooks | (uintptr_t)k_low) & 15u) == 0 &&
-                     lds <= (size_t)sva::kMaxLds;
-  if (n_rows == 0) return SVA_OK;
-  const int64_t tiles = (n_rows + KT - 1) / KT;
-  SVA_REQUIRE(tiles < (1ll << 31) && H <= 65535, "sva_write_encode: too many rows or heads");
-  WriteParams p;
+  SVA_REQUIRE((n_rows + KT - 1) / KT < (1ll << 31) && H <= 65535, "sva_write_encode: too many rows or heads");
+  WriteParams& p = *out;
   p.keys = keys;
   p.kv_dtype = kv_dtype;
   p.kv_hs = kv_head_stride;
@@ -744,42 +612,74 @@ extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_
   p.codes = codes;
   p.ctype = code_type;
   p.code_hs = code_head_stride;
-  const dim3 grid((unsigned)tiles, (unsigned)H);
-  if (n_rows <= FEW_ROWS) {  // a decode step's append (codeword rows as float4 where aligned)
-    if (((uintptr_t)codebooks & 15u) != 0) return launch_few<0>(p, (hipStream_t)stream);
-    switch (R / S) {
-      case 16: return launch_few<16>(p, (hipStream_t)stream);
-      case 32: return launch_few<32>(p, (hipStream_t)stream);
-      case 64: return launch_few<64>(p, (hipStream_t)stream);
-      default: return launch_few<0>(p, (hipStream_t)stream);
-    }
+  return SVA_OK;
+}
+
+int write_few_form(const WriteParams& p) {
+  if (p.n_rows <= 0 || p.n_rows > FEW_ROWS) return -1;
+  if (((uintptr_t)p.codebooks & 15u) != 0) return 0;  // codeword rows as float4 where aligned
+  const int sub = p.R / p.S;
+  return sub == 16 || sub == 32 || sub == 64 ? sub : 0;
+}
+
+int write_encode_launch(const WriteParams& p, hipStream_t stream) {
+  if (p.n_rows == 0) return SVA_OK;
+  switch (write_few_form(p)) {  // a decode step's append
+    case 0: return launch_few<0>(p, stream);
+    case 16: return launch_few<16>(p, stream);
+    case 32: return launch_few<32>(p, stream);
+    case 64: return launch_few<64>(p, stream);
+    default: break;
   }
+  const int64_t D = p.D, R = p.R, S = p.S, C = p.C;
+  const size_t lds = write_lds_bytes(D, R, S, C);
+  const bool tiled = R % 4 == 0 && (R / S) % 4 == 0 && p.klow_hs % 4 == 0 &&
+                     (((uintptr_t)p.k_proj | (uintptr_t)p.codebooks | (uintptr_t)p.k_low) & 15u) == 0 &&
+                     lds <= (size_t)sva::kMaxLds;
+  const int64_t tiles = (p.n_rows + KT - 1) / KT;
+  const dim3 grid((unsigned)tiles, (unsigned)p.H);
   if (!tiled) {
-    hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(write_encode_rowwise_kernel, grid, dim3(64), 0, stream, p);
     SVA_CHECK_LAUNCH("write_encode_rowwise_kernel");
     return SVA_OK;
   }
-  const int64_t es = kv_dtype == 0 ? 4 : 2;
-  const bool rows_aligned = ((uintptr_t)keys & 15u) == 0 && (kv_head_stride * es) % 16 == 0 &&
-                            (kv_row_stride * es) % 16 == 0;
+  const int64_t es = p.kv_dtype == 0 ? 4 : 2;
+  const bool rows_aligned = ((uintptr_t)p.keys & 15u) == 0 && (p.kv_hs * es) % 16 == 0 && (p.kv_rs * es) % 16 == 0;
   if (rows_aligned && R == 64 && (D == 64 || D == 128)) {
-    const hipStream_t st = (hipStream_t)stream;
     if (S == 2 && C == 256)
-      return D == 64 ? launch_persistent<64, 2, 32, 256>(p, tiles, st) : launch_persistent<128, 2, 32, 256>(p, tiles, st);
+      return D == 64 ? launch_persistent<64, 2, 32, 256>(p, tiles, stream)
+                     : launch_persistent<128, 2, 32, 256>(p, tiles, stream);
     if (S == 4 && C == 64)
-      return D == 64 ? launch_persistent<64, 4, 16, 64>(p, tiles, st) : launch_persistent<128, 4, 16, 64>(p, tiles, st);
+      return D == 64 ? launch_persistent<64, 4, 16, 64>(p, tiles, stream)
+                     : launch_persistent<128, 4, 16, 64>(p, tiles, stream);
   }
   if (R % 16 == 0 && C % 16 == 0 && D % 4 == 0) {
     SVA_SET_MAX_LDS_ONCE(write_encode_mfma_kernel, sva::kMaxLds, "hipFuncSetAttribute(write_encode_mfma_kernel)");
-    hipLaunchKernelGGL(write_encode_mfma_kernel, grid, dim3(WT), lds, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(write_encode_mfma_kernel, grid, dim3(WT), lds, stream, p);
     SVA_CHECK_LAUNCH("write_encode_mfma_kernel");
     return SVA_OK;
   }
   switch (R / S) {
-    case 8: return launch_write<8>(p, grid, lds, (hipStream_t)stream);
-    case 16: return launch_write<16>(p, grid, lds, (hipStream_t)stream);
-    case 32: return launch_write<32>(p, grid, lds, (hipStream_t)stream);
-    case 64: return launch_write<64>(p, grid, lds, (hipStream_t)stream);
-    default: return launch_write<0>(p, grid, lds, (hipStream_t)stream);
+    case 8: return launch_write<8>(p, grid, lds, stream);
+    case 16: return launch_write<16>(p, grid, lds, stream);
+    case 32: return launch_write<32>(p, grid, lds, stream);
+    case 64: return launch_write<64>(p, grid, lds, stream);
+    default: return launch_write<0>(p, grid, lds, stream);
   }
+}
+
+}  // namespace sva
+
+extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
+                                int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R,
+                                int64_t S, int64_t C, const float* k_proj, const float* codebooks, float* k_low,
+                                int64_t k_low_head_stride, void* codes, int code_type, int64_t code_head_stride,
+                                void* stream) {
+  sva::clear_error();
+  sva::WriteParams p;
+  const int rc = sva::write_encode_setup(keys, kv_dtype, kv_head_stride, kv_row_stride, row_begin, n_rows, H, G, D,
+                                         R, S, C, k_proj, codebooks, k_low, k_low_head_stride, codes, code_type,
+                                         code_head_stride, &p);
+  if (rc != SVA_OK) return rc;
+  return sva::write_encode_launch(p, (hipStream_t)stream);
 }

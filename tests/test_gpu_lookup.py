@@ -276,22 +276,30 @@ def test_lookup_verify_matches_oracle(G, D, kv_dtype, L, B, masked):
             assert err <= 1e-5, f"head {h}: rel err {err}"
 
 
-def test_decode_layer_steps_equal_plan():
-    """The native decode step (sva_decode_layer_step) over three appended rows and one rebuild equals, bit for
-    bit, the catalog encoded whole by sva_write_encode followed by the plan's sva_lookup_verify; its device
-    statistics count every head's shortlist and budget sizes and the queries."""
+@pytest.mark.parametrize("N0,S,C,kv_dtype", [
+    (40000, 2, 256, torch.bfloat16),  # the wide scan: the append on its own, then the lookup
+    (8000, 2, 256, torch.bfloat16),   # the per-item path: the append inside the one-launch lookup
+    (12000, 4, 64, torch.float16),    # 4x64, 16 keys a thread
+    (3000, 1, 256, torch.bfloat16),   # 1x256: the append reads codeword rows in place
+    (8000, 2, 256, torch.float32),    # fp32 K / V: the per-item path with the append on its own
+])
+def test_decode_layer_steps_equal_plan(N0, S, C, kv_dtype):
+    """The native decode step (sva_decode_layer_step) over appends of one and two rows and one rebuild equals,
+    bit for bit, the catalog encoded whole by sva_write_encode followed by the plan's sva_lookup_verify; its
+    device statistics count every head's shortlist and budget sizes and the queries."""
     from sva_amd import kernels
 
     device = torch.device("cuda:0")
-    H, G, D, R, S, C, L, B, N0 = 9, 3, 64, 64, 2, 256, 2048, 512, 40000
+    H, G, D, R, L, B = 9, 3, 64, 64, 2048, 512
+    print(f"case N0={N0} S={S} C={C} kv={kv_dtype}", flush=True)
     g = torch.Generator(device=device).manual_seed(61)
     q_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
     k_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
     scale = torch.rand(H, device=device, generator=g) + 0.5
     cb = torch.randn(H, S, C, R // S, device=device, generator=g)
     cap = 65536
-    keys = torch.randn(G, cap, D, device=device, generator=g).to(torch.bfloat16)
-    values = torch.randn(G, cap, D, device=device, generator=g).to(torch.bfloat16)
+    keys = torch.randn(G, cap, D, device=device, generator=g).to(kv_dtype)
+    values = torch.randn(G, cap, D, device=device, generator=g).to(kv_dtype)
     k_low = torch.empty(H, cap, R, device=device)
     codes = torch.empty(H, cap, S, device=device, dtype=torch.uint8)
     kernels.write_encode(keys, k_proj, cb, k_low, codes, 0, N0)
@@ -301,7 +309,7 @@ def test_decode_layer_steps_equal_plan():
     ref_low = torch.empty_like(k_low)
     ref_codes = torch.empty_like(codes)
     summoned = verified = 0
-    for step, (row_begin, n) in enumerate([(N0, N0 + 1), (N0 + 1, N0 + 2), (N0 + 2, N0 + 3), (0, N0 + 3)]):
+    for step, (row_begin, n) in enumerate([(N0, N0 + 1), (N0 + 1, N0 + 3), (N0 + 3, N0 + 4), (0, N0 + 4)]):
         q = torch.randn(1, H, 1, D, device=device, generator=g).to(torch.bfloat16)
         out = torch.empty(1, H, 1, D, device=device, dtype=torch.bfloat16)
         layer.step(q, keys, values, k_low, codes, row_begin, n, out)
