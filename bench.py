@@ -836,6 +836,48 @@ def cpu_decode_baseline(torch, model, past, tok, steps: int, warmups: int = 3):
             "busy_threads": round(cpu_s / wall, 2), "ms_per_token": round(1e3 * wall / steps, 1)}
 
 
+def attention_host_us(torch, model, past, tok, modules, steps: int = 32):
+    """Host time of one attention call of the model's decode, in µs: `steps`
+    greedy decode steps continued from (past, tok) after the timed ones,
+    with perf_counter around every call of each module's attention (the
+    patched modules' sva_attention, or the model's sdpa attention function
+    when `modules` is None).  Mean and p50 over the calls."""
+
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    times = []
+
+    def timed(f):
+        def call(*a, **k):
+            t0 = time.perf_counter()
+            r = f(*a, **k)
+            times.append(time.perf_counter() - t0)
+            return r
+        return call
+
+    sdpa = ALL_ATTENTION_FUNCTIONS["sdpa"]
+    if modules is None:
+        ALL_ATTENTION_FUNCTIONS["sdpa"] = timed(sdpa)
+    else:
+        for m in modules:
+            m.sva_attention = timed(m.sva_attention)
+    try:
+        with torch.no_grad():
+            for _ in range(steps):
+                out = model(input_ids=tok, past_key_values=past, use_cache=True)
+                past, tok = out.past_key_values, out.logits[:, -1:].argmax(-1)
+            torch.cuda.synchronize()
+    finally:
+        if modules is None:
+            ALL_ATTENTION_FUNCTIONS["sdpa"] = sdpa
+        else:
+            for m in modules:
+                del m.sva_attention  # the instance attribute: the class method again
+    times.sort()
+    return {"mean_us": round(1e6 * sum(times) / len(times), 2), "p50_us": round(1e6 * times[len(times) // 2], 2),
+            "calls": len(times)}
+
+
 def model_decode(args, with_cpu: bool):
     """Decode tokens/s of a SmolLM2-135M-architecture decoder (random init,
     bf16, 30 layers, 9 q-heads / 3 KV heads, head_dim 64, RoPE theta 1e5)
@@ -894,7 +936,8 @@ def model_decode(args, with_cpu: bool):
             torch.cuda.synchronize()
             return prefill_s, time.perf_counter() - t0, past, tok
 
-    dense_prefill, dense_decode, past, _ = run()
+    dense_prefill, dense_decode, past, tok = run()
+    dense_call = attention_host_us(torch, model, past, tok, None)
     del past
     cpu = None
     with patch_llama_attention(model, bundle, shortlist=2048, budget=512, summon_mode="scan") as handle:
@@ -903,6 +946,8 @@ def model_decode(args, with_cpu: bool):
         summary["floor_overshoots"] = handle.stats.floor_overshoots()
         if with_cpu:
             cpu = cpu_decode_baseline(torch, model, past, tok, args.cpu_decode_steps)
+        sva_call = attention_host_us(torch, model, past, tok,
+                                     [m for m in model.modules() if hasattr(m, "_decode_next")])
     del past
     tok_s = args.decode_steps / sva_decode
     return {
@@ -913,7 +958,9 @@ def model_decode(args, with_cpu: bool):
                    "shortlist": 2048, "budget": 512, "summon_mode": "scan", "intermediate_size": 1536},
         "prefill_s": round(sva_prefill, 3), "prefill_tok_s": round(args.prefill / sva_prefill, 1),
         "dense_attention": {"tok_s": round(args.decode_steps / dense_decode, 1), "prefill_s": round(dense_prefill, 3),
-                            "prefill_tok_s": round(args.prefill / dense_prefill, 1), "attention": "torch sdpa, bf16"},
+                            "prefill_tok_s": round(args.prefill / dense_prefill, 1), "attention": "torch sdpa, bf16",
+                            "attention_call_host": dense_call},
+        "attention_call_host": sva_call,
         "sva_stats": {k: round(v, 3) for k, v in summary.items() if isinstance(v, float) and v == v},
         "cpu_baseline": cpu,
     }
@@ -984,7 +1031,8 @@ def model_suite(args):
         "dtype": "bf16 (fp32 scores)",
         "data": "synthetic (random-init weights, uniform random prompt, synthetic 2x256 artifacts)",
         "config": res["config"], "prefill_s": res["prefill_s"], "prefill_tok_s": res["prefill_tok_s"],
-        "dense_attention": res["dense_attention"], "sva_stats": res["sva_stats"], "cpu_baseline": res["cpu_baseline"],
+        "dense_attention": res["dense_attention"], "attention_call_host": res["attention_call_host"],
+        "sva_stats": res["sva_stats"], "cpu_baseline": res["cpu_baseline"],
     }), flush=True)
 
 
