@@ -315,16 +315,20 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
                       (B > 0 && !class_path && !sva::summon_wide_eligible(p, items) && sva::summon_regs_eligible(p)),
                   "%s: these shapes keep the shortlist in memory; pass shortlist outputs", fn);
   // one token of one sequence on the per-item register path with the
-  // verifier: the query, the summon and the verifier in one launch
-  if (fv != nullptr && fused != nullptr && query != nullptr && n_keys > 0 && !class_path &&
-      !sva::summon_wide_eligible(p, items) && sva::item_fused_eligible(p, *query, *fv, append)) {
+  // verifier: the query, the summon and the verifier in one launch, with a
+  // decode step's catalog append in front where that launch can take it
+  const bool item_one_launch = fv != nullptr && fused != nullptr && query != nullptr && n_keys > 0 && !class_path &&
+                               !sva::summon_wide_eligible(p, items);
+  if (append != nullptr && !(item_one_launch && sva::item_fused_eligible(p, *query, *fv, append))) {
+    // the catalog's new rows on their own, before anything reads them
+    const int rc = sva::write_encode_launch(*append, (hipStream_t)stream);
+    if (rc != SVA_OK) return rc;
+    append = nullptr;
+  }
+  if (item_one_launch && sva::item_fused_eligible(p, *query, *fv, append)) {
     const int rc = sva::item_lookup_verify_path(*query, p, *fv, append, overshoot, (hipStream_t)stream);
     if (rc == SVA_OK) *fused = true;
     return rc;
-  }
-  if (append != nullptr) {  // the catalog's new rows before anything reads them
-    const int rc = sva::write_encode_launch(*append, (hipStream_t)stream);
-    if (rc != SVA_OK) return rc;
   }
   if (query != nullptr && !(class_path && query->form == sva::QUERY_DECODE_1_256)) {
     const int rc = sva::query_lut_launch(*query, (hipStream_t)stream);
