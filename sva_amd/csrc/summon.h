@@ -131,8 +131,11 @@ int lookup_verify_impl(const void* q, int q_dtype, int64_t q_head_stride, int64_
                        int64_t G, float scaling, void* out, int out_dtype, int64_t out_head_stride,
                        void* verify_workspace, size_t verify_workspace_bytes, int32_t* floor_overshoot,
                        void* stream, unsigned long long* stats, const WriteParams* append = nullptr);
+// ordered: every shortlist is in ascending key order (the per-item summon's),
+// so the budget is compacted in slot order rather than sorted.
 int budget_select_launch(const int32_t* sl_idx, const float* sl_rank, const int32_t* sl_count, int64_t n_items,
-                         int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, hipStream_t stream);
+                         int64_t L, int64_t B, int32_t* fin_idx, int32_t* fin_count, bool ordered,
+                         hipStream_t stream);
 bool summon_wide_eligible(const SummonParams& p, int64_t items);
 // overshoot (optional, [items]): 1 where the sampled floor overshot and the
 // finish selected over every key, else 0.

@@ -32,7 +32,10 @@ struct ItemLds {
   int tab, ql, hist, scratch, shared, slidx, keys, total;
 };
 
-__host__ __device__ inline ItemLds item_lds_layout(int S, int C, int R, int L, int64_t N, bool keys_in_lds) {
+// idx16: shortlist slots as uint16 (every key index below 65536), which
+// leaves room for the keys of caches of about 35K keys at L = 8192.
+__host__ __device__ inline ItemLds item_lds_layout(int S, int C, int R, int L, int64_t N, bool keys_in_lds,
+                                                   bool idx16) {
   ItemLds l;
   int o = 0;
   l.tab = o;
@@ -46,14 +49,16 @@ __host__ __device__ inline ItemLds item_lds_layout(int S, int C, int R, int L, i
   l.shared = o;
   o = align16(o + 4 * 4);
   l.slidx = o;
-  o = align16(o + 4 * L);
+  o = align16(o + (idx16 ? 2 : 4) * L);
   l.keys = o;
   if (keys_in_lds) o = align16(o + (int)(4 * N));
   l.total = o;
   return l;
 }
 
-__global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p, int keys_in_lds) {
+// flags: bit 0 the keys sit in LDS, bit 1 the shortlist slots are uint16
+// (item_lds_layout's idx16; the host sets both from the largest length).
+__global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p, int flags) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char lds[];
   const int item = blockIdx.x;
@@ -62,13 +67,20 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   const int b = item / (p.Q * p.H);
   const int64_t len = p.lens ? p.lens[b] : p.N;
   const int64_t off = p.offs ? p.offs[b] : 0;
-  const ItemLds L = item_lds_layout(p.S, p.C, p.R, p.L, len, keys_in_lds != 0);
+  const bool keys_in_lds = (flags & 1) != 0, idx16 = (flags & 2) != 0;
+  const ItemLds L = item_lds_layout(p.S, p.C, p.R, p.L, len, keys_in_lds, idx16);
   float* tab = (float*)(lds + L.tab);
   float* ql = (float*)(lds + L.ql);
   uint32_t* hist = (uint32_t*)(lds + L.hist);
   uint32_t* scratch = (uint32_t*)(lds + L.scratch);
   uint32_t* shared = (uint32_t*)(lds + L.shared);
-  int32_t* slidx = (int32_t*)(lds + L.slidx);
+  int32_t* slidx32 = (int32_t*)(lds + L.slidx);
+  uint16_t* slidx16 = (uint16_t*)(lds + L.slidx);
+  auto set_slot = [&](uint32_t j, int64_t n) {
+    if (idx16) slidx16[j] = (uint16_t)n;
+    else slidx32[j] = (int32_t)n;
+  };
+  auto slot = [&](int j) -> int64_t { return idx16 ? (int64_t)slidx16[j] : (int64_t)slidx32[j]; };
   uint32_t* keys = (uint32_t*)(lds + L.keys);
 
   const int SC = p.S * p.C;
@@ -83,6 +95,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   const char* mrow = p.mask ? (const char*)p.mask : nullptr;
   const int S = p.S, C = p.C;
   const float sqrt_r = p.sqrt_r;
+  const bool r64 = p.R == 64;  // x / 8 is x * 0.125 exactly
 
   auto compute_key = [&](int64_t n) -> uint32_t {
     const bool allowed =
@@ -95,7 +108,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
       c = c < 0 ? 0 : (c >= C ? C - 1 : c);
       acc = acc + tab[s * C + c];
     }
-    return f2key(acc / sqrt_r);
+    return f2key(r64 ? acc * 0.125f : acc / sqrt_r);
   };
 
   uint32_t cnt = 0;
@@ -135,9 +148,9 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   for (int64_t n = lo; n < hi; ++n) {
     const uint32_t k = get_key(n);
     if (k > T) {
-      slidx[pos++] = (int32_t)n;
+      set_slot(pos++, n);
     } else if (k == T && taken < take_eq) {
-      slidx[pos++] = (int32_t)n;
+      set_slot(pos++, n);
       ++taken;
     }
   }
@@ -147,12 +160,38 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   const float* kl = p.k_low + (int64_t)h * p.klow_hs + off * p.R;
   int32_t* out_idx = p.sl_idx + (int64_t)item * p.L;
   float* out_rank = p.sl_rank + (int64_t)item * p.L;
-  for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
-    const int64_t n = slidx[j];
-    const float* row = kl + n * p.R;
-    const float dot = p.R == 64 ? torch_order_dot64(row, ql) : torch_order_dot(row, ql, p.R);
-    out_idx[j] = (int32_t)n;
-    out_rank[j] = dot / sqrt_r;
+  if (r64 && ((uintptr_t)kl & 15u) == 0) {  // block-uniform
+    // lane octet o takes shortlist entries o, o + 128, ...: eight lanes per
+    // row, two 16-byte loads each (a row's two 128-byte lines), REG_OCT
+    // rows in flight; rank_dot64_oct8 sums in torch_order_dot64's order
+    const int oct = (int)threadIdx.x >> 3, c = (int)threadIdx.x & 7;
+    const float4 q0 = reinterpret_cast<const float4*>(ql)[c], q1 = reinterpret_cast<const float4*>(ql)[8 + c];
+    const float4* kl4 = reinterpret_cast<const float4*>(kl);
+    for (int j0 = 0; j0 < leff; j0 += REG_OCT * (ITEM_BLOCK / 8)) {
+      float4 r0[REG_OCT], r1[REG_OCT];
+#pragma unroll
+      for (int u = 0; u < REG_OCT; ++u) {
+        const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
+        const int64_t n = slot(j < leff ? j : 0);
+        r0[u] = kl4[n * 16 + c];
+        r1[u] = kl4[n * 16 + 8 + c];
+      }
+#pragma unroll
+      for (int u = 0; u < REG_OCT; ++u) {
+        const int j = j0 + u * (ITEM_BLOCK / 8) + oct;
+        const float dot = rank_dot64_oct8(r0[u], r1[u], q0, q1);
+        if (c == 0 && j < leff) out_rank[j] = dot * 0.125f;
+      }
+    }
+    for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) out_idx[j] = (int32_t)slot(j);
+  } else {
+    for (int j = threadIdx.x; j < leff; j += ITEM_BLOCK) {
+      const int64_t n = slot(j);
+      const float* row = kl + n * p.R;
+      const float dot = p.R == 64 ? torch_order_dot64(row, ql) : torch_order_dot(row, ql, p.R);
+      out_idx[j] = (int32_t)n;
+      out_rank[j] = r64 ? dot * 0.125f : dot / sqrt_r;
+    }
   }
   if (threadIdx.x == 0) p.sl_count[item] = leff;
 }
@@ -207,12 +246,13 @@ int summon_regs_path(const SummonParams& p, int64_t items, hipStream_t stream) {
 }
 
 int summon_item_path(const SummonParams& p, int64_t items, hipStream_t stream) {
-  const bool keys_fit = item_lds_layout(p.S, p.C, p.R, p.L, p.N, true).total <= kMaxLds;
-  const ItemLds layout = item_lds_layout(p.S, p.C, p.R, p.L, p.N, keys_fit);
+  const bool idx16 = p.N <= 65536;  // every sequence's length is at most N
+  const bool keys_fit = item_lds_layout(p.S, p.C, p.R, p.L, p.N, true, idx16).total <= kMaxLds;
+  const ItemLds layout = item_lds_layout(p.S, p.C, p.R, p.L, p.N, keys_fit, idx16);
   SVA_UNSUPPORTED(layout.total <= kMaxLds, "sva_summon: shortlist %d with %dx%d codes exceeds LDS", p.L, p.S, p.C);
   SVA_SET_MAX_LDS_ONCE(summon_item_kernel, kMaxLds, "hipFuncSetAttribute(summon_item_kernel)");
   hipLaunchKernelGGL(summon_item_kernel, dim3((unsigned)items), dim3(ITEM_BLOCK), (size_t)layout.total, stream, p,
-                     keys_fit ? 1 : 0);
+                     (keys_fit ? 1 : 0) | (idx16 ? 2 : 0));
   SVA_CHECK_LAUNCH("summon_item_kernel");
   return SVA_OK;
 }
@@ -361,7 +401,8 @@ int summon_impl(const char* fn, const float* lut, const float* score_range, cons
   if (sva::summon_regs_eligible(p)) return sva::summon_regs_path(p, items, (hipStream_t)stream);
   int rc = sva::summon_item_path(p, items, (hipStream_t)stream);
   if (rc == SVA_OK && B > 0)
-    rc = sva::budget_select_launch(sl_idx, sl_rank, sl_count, items, L, B, fin_idx, fin_count, (hipStream_t)stream);
+    rc = sva::budget_select_launch(sl_idx, sl_rank, sl_count, items, L, B, fin_idx, fin_count, true,
+                                   (hipStream_t)stream);  // the item kernel's shortlists ascend
   return rc;
 }
 

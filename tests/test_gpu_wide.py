@@ -238,11 +238,13 @@ def test_summon_select_fallbacks_and_mask(device):
     _check_fused(codes, k_low, fused, split, q_low, lut, 1024, 256, allowed=mask[0, 0, 0] > -1e4)
 
 
-def test_summon_select_per_item_path(device):
-    # q = 2 takes the one-workgroup-per-item summon, then the budget kernel
+@pytest.mark.parametrize("L,B", [(1024, 300), (4096, 2048), (8192, 2048)])
+def test_summon_select_per_item_path(device, L, B):
+    # q = 2 takes the one-workgroup-per-item summon, then the budget kernel (the item kernel's shortlists ascend,
+    # so the budget is compacted in slot order; sva_budget_select sorts whatever order it is given)
     from sva_amd import kernels
 
-    N, S, C, L, B = 40000, 4, 64, 1024, 300
+    N, S, C = 40000, 4, 64
     codes, k_low, q, q_proj, scale, cb = _setup(device, N, S, C, seed=11)
     q2 = np.concatenate([q, q[:, :, ::-1].copy()], axis=1)
     codes_t = torch.from_numpy(codes).to(device)
