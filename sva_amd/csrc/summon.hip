@@ -112,10 +112,49 @@ __global__ void __launch_bounds__(ITEM_BLOCK) summon_item_kernel(SummonParams p,
   };
 
   uint32_t cnt = 0;
-  for (int64_t n = threadIdx.x; n < len; n += ITEM_BLOCK) {
-    const uint32_t k = compute_key(n);
-    cnt += k != 0u;
-    if (keys_in_lds) keys[n] = k;
+  const bool u8w = p.ctype == CODE_U8 && (S == 1 || S == 2 || S == 4) && code_base % S == 0 &&
+                   ((uintptr_t)p.codes % (uintptr_t)S) == 0;
+  if (keys_in_lds && u8w) {
+    // uint8 codes of 1, 2 or 4 subspaces: one load per key, U keys' loads
+    // issued (clamped to the last key) before any is used; the same sums as
+    // compute_key
+    constexpr int U = 8;
+    const uint8_t* c8 = (const uint8_t*)p.codes + code_base;
+    for (int64_t n0 = threadIdx.x; n0 < len; n0 += (int64_t)U * ITEM_BLOCK) {
+      uint32_t w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t n = min(n0 + (int64_t)u * ITEM_BLOCK, len - 1);
+        w[u] = S == 4   ? *reinterpret_cast<const uint32_t*>(c8 + n * 4)
+               : S == 2 ? (uint32_t)*reinterpret_cast<const uint16_t*>(c8 + n * 2)
+                        : (uint32_t)c8[n];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t n = n0 + (int64_t)u * ITEM_BLOCK;
+        if (n < len) {
+          const bool allowed = p.mask_type == MASK_NONE ? n <= causal_last
+                                                        : mask_allows(mrow, (int64_t)t * p.mask_ts + n, p.mask_type);
+          uint32_t k = 0u;
+          if (allowed) {
+            float acc = 0.0f;
+            for (int s = 0; s < S; ++s) {
+              const int c = (int)((w[u] >> (8 * s)) & 0xFFu);
+              acc = acc + tab[s * C + (c >= C ? C - 1 : c)];
+            }
+            k = f2key(r64 ? acc * 0.125f : acc / sqrt_r);
+          }
+          cnt += k != 0u;
+          keys[n] = k;
+        }
+      }
+    }
+  } else {
+    for (int64_t n = threadIdx.x; n < len; n += ITEM_BLOCK) {
+      const uint32_t k = compute_key(n);
+      cnt += k != 0u;
+      if (keys_in_lds) keys[n] = k;
+    }
   }
   uint32_t allowed_total;
   block_excl_scan<ITEM_BLOCK>(cnt, scratch, &allowed_total);
