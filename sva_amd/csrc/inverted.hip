@@ -629,8 +629,8 @@ __global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  //
   extern __shared__ __align__(16) unsigned char lds[];
   const int HASH = p.hash;
   uint64_t* hcomp = (uint64_t*)lds;                        // [HASH] best composite per key
-  uint64_t* sel = hcomp + HASH;                            // [max(B, sel_cap)] chosen composites
-  uint64_t* shared64 = sel + max(p.B, p.sel_cap);          // [4]
+  uint64_t* sel = hcomp + HASH;                            // [max(B, sel_cap), even] chosen composites
+  uint64_t* shared64 = sel + ((max(p.B, p.sel_cap) + 1) & ~1);  // [4]; whist after it 16-byte aligned
   uint32_t(*whist)[256] = (uint32_t(*)[256])(shared64 + 4);  // [UNW][256]
   uint32_t* hkey = (uint32_t*)(whist + UNW);               // [HASH]
   uint32_t* hpos = hkey + HASH;                            // [HASH] first window position of the best
@@ -770,10 +770,40 @@ __global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  //
     const uint32_t slot = slot_of(composite_index(c));
     return hcomp[slot] == c && hpos[slot] == (uint32_t)i && composite_key(c) != f2key(-FLT_MAX);
   };
+  // a domain of at most UR * UB entries (the usual one) puts U's elements in
+  // registers, slot j of thread t holding entry t + j UB, and selects over
+  // them with 12-bit passes that rank the last bucket directly
+  // (select_top_regs), instead of 8-bit passes that probe the key table for
+  // every element; the selections are the same (unique composites)
+  constexpr int UR = 2;
+  const bool regs = ndom <= UR * UB;  // block-uniform
+  const int uslots = (ndom + UB - 1) / UB;
+  uint64_t ue[UR];
+  uint64_t uor = 0ull, uand = ~0ull;
   uint32_t ucount = 0;
-  for (int i = threadIdx.x; i < ndom; i += UB) ucount += in_u(i, dom(i));
+  if (regs) {
+#pragma unroll
+    for (int j = 0; j < UR; ++j) {
+      const int i = (int)threadIdx.x + j * UB;
+      ue[j] = 0ull;
+      if (i < ndom) {
+        const uint64_t c = dom(i);
+        if (in_u(i, c)) {
+          ue[j] = c;
+          uor |= c;
+          uand &= c;
+          ++ucount;
+        }
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < ndom; i += UB) ucount += in_u(i, dom(i));
+  }
   uint32_t U;
   block_excl_scan<UB>(ucount, scratch, &U);
+  // the register selects' LDS: the wave histograms as one 4096-bin histogram,
+  // the key table's composites (no longer probed) as the last bucket
+  const TopLds tl{&whist[0][0], hcomp, scratch, shared, shared64};
   // rank count (selected slots) and the budget
   const int64_t rank_count = p.mode == 1 ? min((int64_t)Bi, (int64_t)U) : min((int64_t)Bi, refill);
   auto visit_u = [&](auto&& f) {
@@ -788,7 +818,12 @@ __global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  //
     // U hold the masked minimum
     const int mref = (int)min((int64_t)min_b, rank_count) - 1;
     uint64_t best = 0ull;
-    visit_u([&](uint64_t c) { best = c > best ? c : best; });
+    if (regs) {
+#pragma unroll
+      for (int j = 0; j < UR; ++j) best = ue[j] > best ? ue[j] : best;
+    } else {
+      visit_u([&](uint64_t c) { best = c > best ? c : best; });
+    }
     for (int off = 1; off < WAVE; off <<= 1) {
       const uint64_t o = __shfl_xor(best, off, WAVE);
       best = o > best ? o : best;
@@ -803,10 +838,16 @@ __global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  //
     const float s0 = U > 0 ? key2f(composite_key(shared64[2])) : -FLT_MAX;
     float sref = -FLT_MAX;
     if ((int64_t)U > mref) {
-      const uint64_t Xr = select_largest<UB>(visit_u, mref + 1, whist, scratch, shared64, shared);
+      const uint64_t Xr = regs ? select_top_regs<UB, UR>(ue, mref + 1, uor, uand, tl, uslots)
+                               : select_largest<UB>(visit_u, mref + 1, whist, scratch, shared64, shared);
       // the (mref+1)-th largest element is the smallest one >= Xr
       uint64_t mn = ~0ull;
-      visit_u([&](uint64_t c) { mn = (c >= Xr && c < mn) ? c : mn; });
+      if (regs) {
+#pragma unroll
+        for (int j = 0; j < UR; ++j) mn = (ue[j] != 0ull && ue[j] >= Xr && ue[j] < mn) ? ue[j] : mn;
+      } else {
+        visit_u([&](uint64_t c) { mn = (c >= Xr && c < mn) ? c : mn; });
+      }
       for (int off = 1; off < WAVE; off <<= 1) {
         const uint64_t o = __shfl_xor(mn, off, WAVE);
         mn = o < mn ? o : mn;
@@ -829,9 +870,27 @@ __global__ void __launch_bounds__(UB, 8) unique_select_kernel(SelParams p) {  //
   }
   const int k3 = (int)min((int64_t)budget, (int64_t)U);
   uint64_t X3 = 1ull;
-  if (k3 > 0 && (int)U > k3) X3 = select_largest<UB>(visit_u, k3, whist, scratch, shared64, shared);
-  // chosen keys (composites) in window order
-  if (k3 > 0) {
+  if (k3 > 0 && (int)U > k3)
+    X3 = regs ? select_top_regs<UB, UR>(ue, k3, uor, uand, tl, uslots)
+              : select_largest<UB>(visit_u, k3, whist, scratch, shared64, shared);
+  // chosen keys (composites): any order, the outputs below order them
+  if (k3 > 0 && regs) {
+    if (threadIdx.x == 0) shared[5] = 0u;
+    __syncthreads();
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < UR; ++j) {
+      const bool take = ue[j] != 0ull && ue[j] >= X3;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(take);
+      if (m != 0ull) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&shared[5], (uint32_t)__popcll(m));
+        base = __shfl(base, 0, WAVE);
+        const uint32_t o = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (take && o < (uint32_t)k3) sel[o] = ue[j];
+      }
+    }
+  } else if (k3 > 0) {  // in window order
     const int per = (ndom + UB - 1) / UB;
     const int i0 = min(ndom, (int)threadIdx.x * per), i1 = min(ndom, i0 + per);
     uint32_t cnt = 0;
@@ -911,7 +970,8 @@ __global__ void pack_entries_kernel(const int64_t* __restrict__ idx, const float
 }
 
 size_t select_lds_bytes(int64_t B, int64_t hash) {
-  return sizeof(uint64_t) * (size_t)(hash + B + 4) + sizeof(uint32_t) * (size_t)(UNW * 256 + 2 * hash + UNW + 1 + 8);
+  return sizeof(uint64_t) * (size_t)(hash + ((B + 1) & ~1ll) + 4) +
+         sizeof(uint32_t) * (size_t)(UNW * 256 + 2 * hash + UNW + 1 + 8);
 }
 
 int hash_slots(int win_cap) {
