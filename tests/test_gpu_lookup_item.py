@@ -32,6 +32,8 @@ CASES = [
     (5000, 1, 256, 64, F32, BF16, 1024, 256, False),     # 1x256
     (8192, 2, 256, 64, BF16, BF16, 2048, 512, True),     # a mask allowing every 37th key
     (100, 2, 256, 64, BF16, F16, 2048, 512, False),      # fewer keys than the shortlist
+    (1, 4, 64, 64, BF16, BF16, 2048, 512, False),        # a single key
+    (16384, 2, 256, 64, BF16, BF16, 512, 512, False),    # the largest cache, budget equal to the shortlist
     (8192, 2, 256, 128, BF16, BF16, 2048, 512, False),   # head_dim 128: the separate launches
 ]
 
