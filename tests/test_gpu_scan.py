@@ -117,6 +117,15 @@ def test_scan_prefill_causal(device):
     _check_case(case, res, 64, 16, allowed=allowed)
 
 
+@pytest.mark.parametrize("N,L,B", [(33000, 8192, 2048), (70000, 2048, 512)])
+def test_scan_two_tokens_long_cache(device, N, L, B):
+    # q_len 2 keeps long caches on the one-workgroup-per-item summon: 33000 keys stay in LDS beside uint16
+    # shortlist slots (the batch-8 socket shape's 8192 / 2048), 70000 keys are recomputed per pass with int32 slots
+    case = make_case(N=N, S=2, C=256, Q=2, seed=23 + N % 7)
+    res = _run_scan(case, device, L, B)
+    _check_case(case, res, L, B, allowed=oracle.allowed_mask(2, N))
+
+
 def test_scan_additive_mask(device):
     q_len, n = 4, 900
     case = make_case(N=n, S=2, C=32, Q=q_len, seed=22)
