@@ -74,6 +74,19 @@ int sva_write_encode(const void *keys, int kv_dtype, int64_t kv_head_stride, int
                      void *codes, int code_type, int64_t code_head_stride, void *stream);
 
 /*
+ * sva_write_encode for a batch of n_seq equal-layout caches (sva/llama.py:597-616
+ * per sequence of a batch; the reference decodes batch 1): sequence b's K rows
+ * start kv_seq_stride elements after sequence b - 1's, its catalog rows
+ * catalog_seq_rows rows after (k_low row b * catalog_seq_rows + row of head h).
+ * An append of at most four rows per sequence is one launch for the batch.
+ */
+int sva_write_encode_batch(const void *keys, int kv_dtype, int64_t kv_seq_stride, int64_t kv_head_stride,
+                           int64_t kv_row_stride, int64_t n_seq, int64_t row_begin, int64_t n_rows, int64_t H,
+                           int64_t G, int64_t D, int64_t R, int64_t S, int64_t C, const float *k_proj,
+                           const float *codebooks, float *k_low, int64_t k_low_head_stride, int64_t catalog_seq_rows,
+                           void *codes, int code_type, int64_t code_head_stride, void *stream);
+
+/*
  * Learned query map and per-query PQ lookup table.
  * Replaces sva/llama.py:211 (q_low = einsum(q, q_proj) * scale) and the table
  * of sva/ops.py:66-68.

@@ -31,6 +31,8 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
     "sva_last_error": (ctypes.c_char_p, []),
     "sva_write_encode": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64,
                               _P, _I, _I64, _P]),
+    "sva_write_encode_batch": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                    _P, _P, _P, _I64, _I64, _P, _I, _I64, _P]),
     "sva_query_lut": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I,
                            _I64, _I64, _I64, _P, _P, _P, _P]),
     "sva_pq_scores": (_I, [_P, _P, _I, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P]),

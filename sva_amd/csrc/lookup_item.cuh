@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(ITEM_BLOCK) item_lookup_verify_kernel(LutParam
   // would spill here; fp32 K / V: no append, its verifier needs the registers)
   if constexpr (kAppends<VKV>) {
     if (wp.n_rows > 0) {  // uniform
-      few_append<S == 1 ? 0 : 64 / S, ITEM_BLOCK>(wp, h);
+      few_append<S == 1 ? 0 : 64 / S, ITEM_BLOCK>(wp, h, 0);
       __syncthreads();
     }
   }

@@ -23,7 +23,7 @@ bool item_fused_eligible(const SummonParams& p, const QueryLaunch& ql, const Fus
     if (fv.kv_dtype == F32) return false;  // the fp32 K / V variants carry no append
     const WriteParams& w = *append;
     const int form = write_few_form(w);
-    if (form < 0 || (p.S > 1 && form != 64 / p.S) || w.codes == nullptr || w.codes != p.codes || w.k_low != p.k_low ||
+    if (form < 0 || (p.S > 1 && form != 64 / p.S) || w.n_seq != 1 || w.codes == nullptr || w.codes != p.codes || w.k_low != p.k_low ||
         w.code_hs != p.code_hs || w.klow_hs != p.klow_hs || w.ctype != p.ctype || w.H != p.H || w.G != fv.G ||
         w.R != p.R || w.S != p.S || w.C != p.C || w.D != fv.D || w.row0 + w.n_rows > p.N)
       return false;

@@ -547,12 +547,12 @@ __global__ void __launch_bounds__(64) write_encode_rowwise_kernel(WriteParams p)
 // with one 256-thread workgroup per head.
 template <int SUB>
 __global__ void __launch_bounds__(WT) write_encode_few_kernel(WriteParams p) {
-  few_append<SUB, WT>(p, (int)blockIdx.x);
+  few_append<SUB, WT>(p, (int)blockIdx.x, (int)blockIdx.y);
 }
 
 template <int SUB>
 int launch_few(const WriteParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((write_encode_few_kernel<SUB>), dim3((unsigned)p.H), dim3(WT), 0, stream, p);
+  hipLaunchKernelGGL((write_encode_few_kernel<SUB>), dim3((unsigned)p.H, (unsigned)p.n_seq), dim3(WT), 0, stream, p);
   SVA_CHECK_LAUNCH("write_encode_few_kernel");
   return SVA_OK;
 }
@@ -612,6 +612,9 @@ int write_encode_setup(const void* keys, int kv_dtype, int64_t kv_head_stride, i
   p.codes = codes;
   p.ctype = code_type;
   p.code_hs = code_head_stride;
+  p.n_seq = 1;
+  p.seq_kv = 0;
+  p.seq_rows = 0;
   return SVA_OK;
 }
 
@@ -623,13 +626,28 @@ int write_few_form(const WriteParams& p) {
 }
 
 int write_encode_launch(const WriteParams& p, hipStream_t stream) {
-  if (p.n_rows == 0) return SVA_OK;
-  switch (write_few_form(p)) {  // a decode step's append
+  if (p.n_rows == 0 || p.n_seq <= 0) return SVA_OK;
+  switch (write_few_form(p)) {  // a decode step's append, every sequence in one launch
     case 0: return launch_few<0>(p, stream);
     case 16: return launch_few<16>(p, stream);
     case 32: return launch_few<32>(p, stream);
     case 64: return launch_few<64>(p, stream);
     default: break;
+  }
+  if (p.n_seq > 1) {  // the tiled forms take one sequence a launch
+    const int64_t kv_es = p.kv_dtype == 0 ? 4 : 2;
+    const int64_t code_es = p.ctype == 0 ? 1 : p.ctype == 1 ? 2 : p.ctype == 2 ? 4 : 8;
+    for (int64_t b = 0; b < p.n_seq; ++b) {
+      WriteParams q = p;
+      q.n_seq = 1;
+      q.seq_kv = q.seq_rows = 0;
+      q.keys = (const char*)p.keys + b * p.seq_kv * kv_es;
+      q.k_low = p.k_low + b * p.seq_rows * p.R;
+      q.codes = p.codes != nullptr ? (void*)((char*)p.codes + b * p.seq_rows * p.S * code_es) : nullptr;
+      const int rc = write_encode_launch(q, stream);
+      if (rc != SVA_OK) return rc;
+    }
+    return SVA_OK;
   }
   const int64_t D = p.D, R = p.R, S = p.S, C = p.C;
   const size_t lds = write_lds_bytes(D, R, S, C);
@@ -669,6 +687,28 @@ int write_encode_launch(const WriteParams& p, hipStream_t stream) {
 }
 
 }  // namespace sva
+
+extern "C" int sva_write_encode_batch(const void* keys, int kv_dtype, int64_t kv_seq_stride, int64_t kv_head_stride,
+                                      int64_t kv_row_stride, int64_t n_seq, int64_t row_begin, int64_t n_rows,
+                                      int64_t H, int64_t G, int64_t D, int64_t R, int64_t S, int64_t C,
+                                      const float* k_proj, const float* codebooks, float* k_low,
+                                      int64_t k_low_head_stride, int64_t catalog_seq_rows, void* codes, int code_type,
+                                      int64_t code_head_stride, void* stream) {
+  sva::clear_error();
+  SVA_REQUIRE(n_seq > 0 && n_seq <= 65535, "sva_write_encode_batch: %lld sequences", (long long)n_seq);
+  SVA_REQUIRE(kv_seq_stride >= 0 && catalog_seq_rows >= row_begin + n_rows,
+              "sva_write_encode_batch: sequences overlap (catalog rows per sequence %lld, rows up to %lld)",
+              (long long)catalog_seq_rows, (long long)(row_begin + n_rows));
+  sva::WriteParams p;
+  const int rc = sva::write_encode_setup(keys, kv_dtype, kv_head_stride, kv_row_stride, row_begin, n_rows, H, G, D,
+                                         R, S, C, k_proj, codebooks, k_low, k_low_head_stride, codes, code_type,
+                                         code_head_stride, &p);
+  if (rc != SVA_OK) return rc;
+  p.n_seq = (int)n_seq;
+  p.seq_kv = kv_seq_stride;
+  p.seq_rows = catalog_seq_rows;
+  return sva::write_encode_launch(p, (hipStream_t)stream);
+}
 
 extern "C" int sva_write_encode(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                                 int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R,

@@ -20,6 +20,11 @@ struct WriteParams {
   void* codes;             // [H, rows, S] (head stride code_hs)
   int ctype;
   int64_t code_hs;
+  // a batch of equal-layout caches (sva_write_encode_batch): sequence b's K
+  // rows start seq_kv elements after sequence b - 1's, its catalog rows
+  // seq_rows rows after; one sequence: n_seq 1, both 0
+  int n_seq;
+  int64_t seq_kv, seq_rows;
 };
 
 // A decode step's append (at most FEW_ROWS rows): one workgroup per head,
@@ -32,10 +37,11 @@ struct WriteParams {
 constexpr int FEW_ROWS = 4;
 constexpr int FEW_MAP = 64 * 64;  // map floats staged in LDS
 
-// Head h's rows [row0, row0 + n_rows) of p (n_rows <= FEW_ROWS) on this
-// workgroup of NT threads (NT a multiple of WAVE); every thread must call it.
+// Head h's rows [row0, row0 + n_rows) of sequence b of p (n_rows <=
+// FEW_ROWS) on this workgroup of NT threads (NT a multiple of WAVE); every
+// thread must call it.
 template <int SUB, int NT>
-SVA_DEV void few_append(const WriteParams& p, int h) {
+SVA_DEV void few_append(const WriteParams& p, int h, int b) {
 #pragma clang fp contract(off)
   __shared__ float kr[FEW_ROWS][256];  // the new K rows (D <= 256)
   __shared__ float xl[FEW_ROWS][256];  // their k_low rows (R <= 256)
@@ -68,7 +74,7 @@ SVA_DEV void few_append(const WriteParams& p, int h) {
     for (int i = t; i < D * R / 4; i += NT) reinterpret_cast<float4*>(ws)[i] = reinterpret_cast<const float4*>(W)[i];
   for (int e = t; e < nr * D; e += NT) {
     const int j = e / D, d = e - j * D;
-    kr[j][d] = load_elem(p.keys, (int64_t)g * p.kv_hs + (p.row0 + j) * p.kv_rs + d, p.kv_dtype);
+    kr[j][d] = load_elem(p.keys, (int64_t)b * p.seq_kv + (int64_t)g * p.kv_hs + (p.row0 + j) * p.kv_rs + d, p.kv_dtype);
   }
   __syncthreads();
   const float* Wm = map_in_lds ? ws : W;
@@ -77,7 +83,7 @@ SVA_DEV void few_append(const WriteParams& p, int h) {
     float acc = 0.0f;
     for (int d = 0; d < D; ++d) acc = __builtin_fmaf(kr[j][d], Wm[d * R + r], acc);
     xl[j][r] = acc;
-    p.k_low[(int64_t)h * p.klow_hs + (p.row0 + j) * R + r] = acc;
+    p.k_low[(int64_t)h * p.klow_hs + ((int64_t)b * p.seq_rows + p.row0 + j) * R + r] = acc;
   }
   if (p.codes == nullptr) return;  // uniform
   __syncthreads();
@@ -138,16 +144,17 @@ SVA_DEV void few_append(const WriteParams& p, int h) {
             best = rbest[w];
             arg = rarg[w];
           }
-        store_code(p.codes, (int64_t)h * p.code_hs + (p.row0 + j) * S + s, p.ctype, arg == 0x7FFFFFFF ? 0 : arg);
+        store_code(p.codes, (int64_t)h * p.code_hs + ((int64_t)b * p.seq_rows + p.row0 + j) * S + s, p.ctype,
+                   arg == 0x7FFFFFFF ? 0 : arg);
       }
       __syncthreads();
     }
   }
 }
 
-// sva_write_encode split into the validation (filling the parameters) and
-// the launch, so that a decode step can run its few-row append inside
-// another kernel (write.hip).
+// sva_write_encode split into the validation (filling the parameters, one
+// sequence) and the launch, so that a decode step can run its few-row append
+// inside another kernel (write.hip).  The launch takes p.n_seq sequences.
 int write_encode_setup(const void* keys, int kv_dtype, int64_t kv_head_stride, int64_t kv_row_stride,
                        int64_t row_begin, int64_t n_rows, int64_t H, int64_t G, int64_t D, int64_t R, int64_t S,
                        int64_t C, const float* k_proj, const float* codebooks, float* k_low,

@@ -88,6 +88,38 @@ def write_encode(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tens
     )
 
 
+def write_encode_batch(keys: torch.Tensor, k_proj: torch.Tensor, codebooks: torch.Tensor, k_low: torch.Tensor,
+                       codes: torch.Tensor, seq_rows: int, row_begin: int, n_rows: int) -> None:
+    """write_encode for every sequence of a batch of caches keys [B, G, rows, D]
+    (sva/llama.py:597-616 per sequence): sequence b's catalog rows are
+    [b * seq_rows, (b + 1) * seq_rows) of k_low [H, B * seq_rows, R] and codes
+    [H, B * seq_rows, S]; cache rows [row_begin, row_begin + n_rows) of each
+    sequence are encoded, an append of a few rows in one launch for the batch."""
+
+    if keys.dim() != 4 or keys.stride(-1) != 1:
+        raise ValueError("keys must be [B, G, rows, D] with contiguous rows")
+    batch, kv_heads, rows, dim = keys.shape
+    heads, _, rank = k_proj.shape
+    subspaces, codewords = codebooks.shape[1], codebooks.shape[2]
+    if k_low.dim() != 3 or k_low.shape[0] != heads or k_low.shape[2] != rank or k_low.stride(1) != rank \
+            or k_low.stride(2) != 1 or k_low.dtype != torch.float32 or k_low.shape[1] < batch * seq_rows:
+        raise ValueError("k_low must be fp32 [H, B * seq_rows, R] with contiguous rows")
+    if codes.dim() != 3 or codes.shape[0] != heads or codes.shape[2] != subspaces or codes.stride(1) != subspaces \
+            or codes.stride(2) != 1 or codes.shape[1] < batch * seq_rows:
+        raise ValueError("codes must be [H, B * seq_rows, S] with contiguous rows")
+    if row_begin < 0 or n_rows < 0 or row_begin + n_rows > min(rows, seq_rows):
+        raise ValueError("row range outside the catalog")
+    device = require_device(keys, k_proj, codebooks, k_low, codes)
+    check(
+        lib().sva_write_encode_batch(
+            ptr(keys), dtype_code(keys), keys.stride(0), keys.stride(1), keys.stride(2), batch, row_begin, n_rows,
+            heads, kv_heads, dim, rank, subspaces, codewords, ptr(_f32c(k_proj)), ptr(_f32c(codebooks)), ptr(k_low),
+            k_low.stride(0), seq_rows, ptr(codes), code_type(codes), codes.stride(0), stream_handle(device),
+        ),
+        "sva_write_encode_batch",
+    )
+
+
 def query_lut(q: torch.Tensor, q_proj: torch.Tensor, scale: torch.Tensor, codebooks: torch.Tensor,
               codes: torch.Tensor | None = None, n_keys: int = 0, shortlist: int = 0):
     """q_low [n_seq,H,Q,R], lut [n_seq,H,Q,S,C], score_range [n_seq,H,Q,4] (sva/llama.py:211, sva/ops.py:66-68).

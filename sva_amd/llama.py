@@ -396,10 +396,14 @@ class SVALlamaAttention(nn.Module):
                         self._codes[:, b * cap:b * cap + self._key_len])
             self._k_low, self._codes, cap = k_low, codes, new_cap
         start = self._key_len if can_append else 0
-        for b in range(batch):
-            kernels.write_encode(key[b], self.sva_k_proj, self.sva_coarse_codebooks,
-                                 self._k_low[:, b * cap:(b + 1) * cap], self._codes[:, b * cap:(b + 1) * cap], start,
-                                 k_len - start)
+        if key.stride(-1) == 1:  # every sequence in one call (one launch for a decode step's rows)
+            kernels.write_encode_batch(key, self.sva_k_proj, self.sva_coarse_codebooks, self._k_low, self._codes, cap,
+                                       start, k_len - start)
+        else:
+            for b in range(batch):
+                kernels.write_encode(key[b], self.sva_k_proj, self.sva_coarse_codebooks,
+                                     self._k_low[:, b * cap:(b + 1) * cap], self._codes[:, b * cap:(b + 1) * cap],
+                                     start, k_len - start)
         self._key_len = self._codes_len = k_len
         self._postings = None
         self._signature = sig

@@ -120,3 +120,31 @@ def test_decode_append_ties_take_first_centroid(device):
     k_low, codes = _encode(device, kt, k_proj, cb, torch.uint8, [(a, a + 1) for a in range(N)])
     assert codes.max() < 128
     np.testing.assert_array_equal(codes, oracle.encode_product_keys(k_low, cb))
+
+
+@pytest.mark.parametrize("S,C,kv_dtype,n_rows", [
+    (2, 256, torch.bfloat16, 1),    # a decode step's append: every sequence in one launch
+    (4, 64, torch.float32, 3),
+    (2, 256, torch.float16, 100),   # more rows: the tiled encoder, one sequence a launch
+])
+def test_batch_encode_equals_each_sequence(device, S, C, kv_dtype, n_rows):
+    """sva_write_encode_batch over a batch of 5 caches [B, G, rows, D] equals sva_write_encode run on each
+    sequence's cache and catalog slice, bit for bit, and leaves every other catalog row untouched."""
+    from sva_amd import kernels
+
+    B, G, H, D, R, rows, cap, row0 = 5, 3, 9, 64, 64, 300, 320, 150
+    g = torch.Generator(device=device).manual_seed(71 + n_rows)
+    keys = torch.randn(B, G, rows, D, device=device, generator=g).to(kv_dtype)
+    k_proj = torch.randn(H, D, R, device=device, generator=g) / 8.0
+    cb = torch.randn(H, S, C, R // S, device=device, generator=g)
+    k_low = torch.full((H, B * cap, R), 7.0, device=device)
+    codes = torch.full((H, B * cap, S), 9, device=device, dtype=torch.uint8)
+    ref_low, ref_codes = k_low.clone(), codes.clone()
+    kernels.write_encode_batch(keys, k_proj, cb, k_low, codes, cap, row0, n_rows)
+    for b in range(B):
+        kernels.write_encode(keys[b], k_proj, cb, ref_low[:, b * cap:(b + 1) * cap], ref_codes[:, b * cap:(b + 1) * cap],
+                             row0, n_rows)
+    torch.cuda.synchronize()
+    assert torch.equal(k_low, ref_low), "k_low differs"
+    assert torch.equal(codes, ref_codes), "codes differ"
+    assert bool((k_low[:, :row0] == 7.0).all()) and bool((codes[:, cap - 1] == 9).all()), "rows outside the range written"
