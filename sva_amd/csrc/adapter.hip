@@ -9,6 +9,10 @@
 // fp32, each thread forms down-projection outputs (token, o) as a
 // sequential fma chain over the 2 * hidden inputs, the GELU values go to
 // LDS, then each output (token, j) is a sequential chain over the rank.
+// Consecutive threads take consecutive tokens of one output, so a wave's
+// weight loads read a few rows (the same address across a row's tokens)
+// rather than one row per lane; the staged rows are padded by a float so
+// that the tokens' reads of one column fall in different LDS banks.
 #include <cmath>
 
 #include "capi_internal.h"
@@ -54,34 +58,98 @@ SVA_DEV float round_to(float v, int dtype) {
 
 __global__ void __launch_bounds__(AB) residual_adapter_kernel(AdapterParams p) {
 #pragma clang fp contract(off)
-  extern __shared__ __align__(16) float xs[];  // [tok][2 * H], then z [tok][rank]
+  extern __shared__ __align__(16) float xs[];  // [tok][2 * H + 1], then z [tok][rank + 1]
   const int H2 = 2 * p.H;
-  float* z = xs + p.tok * H2;
+  const int XS = H2 + 1, ZS = p.rank + 1;  // padded row strides
+  float* z = xs + p.tok * XS;
   const int64_t t0 = (int64_t)blockIdx.x * p.tok;
   const int nt = (int)min((int64_t)p.tok, p.T - t0);
-  for (int e = threadIdx.x; e < nt * H2; e += AB) {
-    const int t = e / H2, k = e - t * H2;
-    xs[e] = k < p.H ? load_elem(p.hidden, (t0 + t) * p.h_rs + k, p.h_dtype)
-                    : load_elem(p.attn, (t0 + t) * p.a_rs + (k - p.H), p.a_dtype);
+  {
+    // the inputs, SU elements a thread per batch: raw bits requested first
+    // (indices clamped, every load unconditional), converted at the store
+    constexpr int SU = 8;
+    const int total = nt * H2;
+    for (int e0 = threadIdx.x; e0 < total; e0 += SU * AB) {
+      uint32_t bits[SU];
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int e = min(e0 + u * AB, total - 1);
+        const int t = e / H2, k = e - t * H2;
+        const bool hid = k < p.H;
+        bits[u] = load_elem_bits(hid ? p.hidden : p.attn, hid ? (t0 + t) * p.h_rs + k : (t0 + t) * p.a_rs + (k - p.H),
+                                 hid ? p.h_dtype : p.a_dtype);
+      }
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int e = e0 + u * AB;
+        if (e < total) {
+          const int t = e / H2, k = e - t * H2;
+          xs[t * XS + k] = elem_from_bits(bits[u], k < p.H ? p.h_dtype : p.a_dtype);
+        }
+      }
+    }
   }
   __syncthreads();
+  // the weight rows as float4 where aligned: a chain of 2H steps is bound by
+  // its loads unless the next 32 weights are in flight while the current 32
+  // are used (the same fma chain, in k order)
+  constexpr int V = 8;  // float4s per batch
+  const bool vec = ((uintptr_t)p.down & 15u) == 0 && ((uintptr_t)p.up & 15u) == 0 && H2 % (4 * V) == 0 &&
+                   p.rank % 4 == 0;
   for (int e = threadIdx.x; e < nt * p.rank; e += AB) {
-    const int t = e / p.rank, o = e - t * p.rank;
-    const float* x = xs + t * H2;
+    const int o = e / nt, t = e - o * nt;
+    const float* x = xs + t * XS;
     const float* w = p.down + (int64_t)o * H2;
     float acc = 0.0f;
-    for (int k = 0; k < H2; ++k) acc = __builtin_fmaf(x[k], w[k], acc);
-    z[e] = 0.5f * acc * (1.0f + erff(acc * 0.70710678118654752f));  // F.gelu (erf form)
+    if (vec) {
+      const float4* w4 = reinterpret_cast<const float4*>(w);
+      const int nb = H2 / (4 * V);
+      float4 cur[V], nxt[V];
+#pragma unroll
+      for (int u = 0; u < V; ++u) cur[u] = w4[u];
+      for (int b = 0; b < nb; ++b) {
+        const int bn = min(b + 1, nb - 1);  // the last batch loads itself again: every load unconditional
+#pragma unroll
+        for (int u = 0; u < V; ++u) nxt[u] = w4[bn * V + u];
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+          const float* xk = x + (b * V + u) * 4;
+          acc = __builtin_fmaf(xk[0], cur[u].x, acc);
+          acc = __builtin_fmaf(xk[1], cur[u].y, acc);
+          acc = __builtin_fmaf(xk[2], cur[u].z, acc);
+          acc = __builtin_fmaf(xk[3], cur[u].w, acc);
+        }
+#pragma unroll
+        for (int u = 0; u < V; ++u) cur[u] = nxt[u];
+      }
+    } else {
+      for (int k = 0; k < H2; ++k) acc = __builtin_fmaf(x[k], w[k], acc);
+    }
+    z[t * ZS + o] = 0.5f * acc * (1.0f + erff(acc * 0.70710678118654752f));  // F.gelu (erf form)
   }
   __syncthreads();
   for (int e = threadIdx.x; e < nt * p.H; e += AB) {
-    const int t = e / p.H, j = e - t * p.H;
-    const float* zz = z + t * p.rank;
+    const int j = e / nt, t = e - j * nt;
+    const float* zz = z + t * ZS;
     const float* w = p.up + (int64_t)j * p.rank;
     float acc = 0.0f;
-    for (int o = 0; o < p.rank; ++o) acc = __builtin_fmaf(zz[o], w[o], acc);
+    if (vec && p.rank == MAX_RANK) {  // the row's 64 weights requested at once
+      const float4* w4 = reinterpret_cast<const float4*>(w);
+      float4 wv[MAX_RANK / 4];
+#pragma unroll
+      for (int u = 0; u < MAX_RANK / 4; ++u) wv[u] = w4[u];
+#pragma unroll
+      for (int u = 0; u < MAX_RANK / 4; ++u) {
+        acc = __builtin_fmaf(zz[4 * u], wv[u].x, acc);
+        acc = __builtin_fmaf(zz[4 * u + 1], wv[u].y, acc);
+        acc = __builtin_fmaf(zz[4 * u + 2], wv[u].z, acc);
+        acc = __builtin_fmaf(zz[4 * u + 3], wv[u].w, acc);
+      }
+    } else {
+      for (int o = 0; o < p.rank; ++o) acc = __builtin_fmaf(zz[o], w[o], acc);
+    }
     const float corr = round_to(acc * p.scale, p.a_dtype);
-    const float a = xs[t * H2 + p.H + j];
+    const float a = xs[t * XS + p.H + j];
     store_elem(p.out, (t0 + t) * p.o_rs + j, p.o_dtype, a + corr);
   }
 }
@@ -101,8 +169,8 @@ extern "C" int sva_residual_adapter(const void* hidden, int hidden_dtype, int64_
                   out_dtype <= 2,
               "sva_residual_adapter: bad dtype");
   if (n_tokens == 0) return SVA_OK;
-  // tokens per workgroup: as many as fit 64 KB of staged fp32 inputs, at most MAX_TOK
-  const int64_t per_tok = sizeof(float) * (2 * hidden_size + rank);
+  // tokens per workgroup: as many as fit 64 KB of staged fp32 inputs (rows padded by a float), at most MAX_TOK
+  const int64_t per_tok = sizeof(float) * (2 * hidden_size + 1 + rank + 1);
   const int tok = (int)std::max<int64_t>(1, std::min<int64_t>(MAX_TOK, (64 * 1024) / per_tok));
   const size_t lds = (size_t)tok * (size_t)per_tok;
   SVA_UNSUPPORTED(lds <= (size_t)sva::kMaxLds, "sva_residual_adapter: hidden size %lld needs %zu bytes of LDS",
