@@ -64,6 +64,23 @@ __global__ void __launch_bounds__(AB) residual_adapter_kernel(AdapterParams p) {
   float* z = xs + p.tok * XS;
   const int64_t t0 = (int64_t)blockIdx.x * p.tok;
   const int nt = (int)min((int64_t)p.tok, p.T - t0);
+  // Both weight matrices requested by every thread at entry, one float per
+  // 128-byte line: they miss the L2 at every call (the layer runs once a
+  // step), and the chains below would otherwise wait on one miss after
+  // another.  The values are folded into a word that is stored only in a case
+  // that cannot occur (a negative token count), so the loads are kept.
+  float touch = 0.0f;
+  {
+    const int64_t nd = (int64_t)p.rank * H2, nall = nd + (int64_t)p.H * p.rank;  // floats
+    auto at = [&](int64_t f) { return f < nd ? p.down[f] : p.up[f - nd]; };
+    constexpr int TU = 16;  // the first TU lines a thread, requested together (indices clamped)
+    float v[TU];
+#pragma unroll
+    for (int u = 0; u < TU; ++u) v[u] = at(min(((int64_t)threadIdx.x + (int64_t)u * AB) * 32, nall - 1));
+#pragma unroll
+    for (int u = 0; u < TU; ++u) touch += v[u];
+    for (int64_t f = ((int64_t)threadIdx.x + (int64_t)TU * AB) * 32; f < nall; f += (int64_t)AB * 32) touch += at(f);
+  }
   {
     // the inputs, SU elements a thread per batch: raw bits requested first
     // (indices clamped, every load unconditional), converted at the store
@@ -152,6 +169,7 @@ __global__ void __launch_bounds__(AB) residual_adapter_kernel(AdapterParams p) {
     const float a = xs[t * XS + p.H + j];
     store_elem(p.out, (t0 + t) * p.o_rs + j, p.o_dtype, a + corr);
   }
+  if (p.T < 0) store_elem(p.out, threadIdx.x, p.o_dtype, touch);  // never: keeps the requests above
 }
 
 }  // namespace
